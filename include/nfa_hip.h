@@ -1,0 +1,185 @@
+/*
+ * nfa_hip.h -- C ABI of libnfa_hip.so, the MI355X (gfx950) implementation of
+ * the NFA / LoDA-SA two-level sparse-attention decode path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * (passed as void*), launches asynchronously on that stream, allocates no
+ * memory and never synchronises, so calls can be captured into a hipGraph.
+ * Outputs and persistent state live in caller-owned buffers.
+ *
+ * Return value: 0 on success, a negative NFA_E* code on a rejected argument
+ * or a failed launch; nfa_last_error() then describes the problem.  Argument
+ * checks run before any launch or KV mutation, as the reference's host checks
+ * do before its kernels run.
+ *
+ * Reference interfaces replaced (Chosen-David/two-level-attention):
+ *   nfa_select_layer        <- sparse_attn/indexer/nfa_layer_batch_selector.py:2649-2720
+ *                              (select_topk_for_layer_batched; kernels :29-2028)
+ *   nfa_sparse_attn_decode  <- sparse_attn/ops/paged_region_kernels.py:800-1006
+ *                              (sparse_paged_attention_gather; kernel :251-363)
+ *   nfa_paged_write_decode  <- sparse_attn/ops/paged_region_kernels.py:665-724
+ *   nfa_paged_write_prefill <- sparse_attn/ops/paged_region_kernels.py:610-662
+ */
+#ifndef NFA_HIP_H
+#define NFA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NFA_ABI_VERSION 1
+
+/* error codes */
+#define NFA_OK 0
+#define NFA_EINVAL (-1)    /* bad geometry / flags / pointer */
+#define NFA_ELAUNCH (-2)   /* hipLaunch failed */
+#define NFA_EWORKSPACE (-3) /* workspace too small */
+
+/* dtypes of KV pools, queries and outputs */
+#define NFA_DTYPE_BF16 0
+#define NFA_DTYPE_F32 1
+
+/* L1 score sources (--nfa_far_method / --nfa_near_method) */
+#define NFA_METHOD_MINMAX 0
+#define NFA_METHOD_AVG 1
+
+/*
+ * One selector call over B batch rows for one layer.  Mirrors the arguments
+ * of select_topk_for_layer_batched after its host-side geometry resolution
+ * (selector:2762-2832).  Pointers with a _l suffix point at this layer's slice.
+ */
+typedef struct NfaSelectParams {
+  int32_t abi_version;        /* = NFA_ABI_VERSION */
+  int32_t struct_size;        /* = sizeof(NfaSelectParams) */
+
+  /* geometry */
+  int32_t batch;              /* B selector rows (visible bucket rows) */
+  int32_t hq, hkv;            /* query heads, kv heads */
+  int32_t head_dim, head_dim_v;
+  int32_t bs;                 /* --tia_block_size (L1 statistics block) */
+  int32_t page;               /* physical KV page size */
+  int32_t max_blocks;         /* block-table width = kt_cap */
+  int32_t max_req;            /* request slots */
+  int32_t geo_sink, geo_near, geo_window;   /* RegionGeometry */
+  int32_t sink_tokens, swa;   /* --nfa_sink_tokens, --nfa_swa_size */
+  int32_t near_len;           /* --nfa_near_len */
+  int32_t k_f, k_n;           /* far / near L1 page budgets */
+  int32_t k2;                 /* --tia_level2_topk */
+  int32_t near_tokens;        /* --nfa_near_tokens, -1 == off */
+  int32_t far_method, near_method;
+  int32_t dsub, fine_dsub;    /* number of L1 / L2 dims */
+  int32_t kv_dtype, q_dtype;
+  int32_t max_vis;            /* gather row width */
+  int32_t middle_only;        /* write only the middle selection */
+  int32_t pool_pages;         /* pages in the KV arena (P + 1); block-table
+                                 entries outside [0, pool_pages) read the
+                                 last (PAD) page */
+  int32_t protected_only;     /* sink/SWA union with an empty middle only
+                                 (both regions skipped); no statistics */
+  float scale;                /* attention.scaling */
+  float pad1;
+
+  /* cache state (device pointers) */
+  void *k_pool_l, *v_pool_l;          /* [P+1,1,hkv,page,D] of this layer */
+  const int32_t *block_table_l;       /* [max_req, max_blocks] */
+  const int32_t *lengths;             /* [batch] planned lengths */
+  const int64_t *active_req;          /* [batch] request id or -1 */
+  const int64_t *valid_req;           /* [batch] request id (PAD rows -> 0) */
+  const int32_t *skip_far_l;          /* [max_req] */
+  const int32_t *skip_near_l;         /* [max_req] */
+  const int32_t *dims;                /* [dsub] */
+  const int32_t *fine_dims;           /* [fine_dsub] */
+  const void *q;                      /* [batch, hq, head_dim] rows */
+  int64_t q_stride_b, q_stride_h;     /* element strides */
+
+  /* decode write fused into the selector; k_new == NULL disables it */
+  const void *k_new, *v_new;          /* [batch, hkv, 1, D] contiguous */
+  const int32_t *slots;               /* [batch] physical slot or -1 */
+
+  /* persistent page statistics of this layer, KV dtype,
+     [max_req, hkv, dsub/chunk, max_blocks, chunk] with chunk = 16B/elem */
+  void *stat_min_l, *stat_max_l, *stat_sum_l;
+  int32_t *stats_len_l;               /* [max_req] */
+
+  /* outputs */
+  int32_t *gather;                    /* [rows >= batch, hkv, max_vis] */
+  int32_t *vis_lens;                  /* [rows >= batch, hkv] */
+
+  /* scratch: nfa_select_workspace_bytes() bytes, zero-filled once */
+  void *workspace;
+  int64_t workspace_bytes;
+
+  /* optional intermediate outputs for parity tests (NULL = off) */
+  uint16_t *dbg_far, *dbg_near;       /* [batch, hkv, max_blocks] bf16 bits */
+  int32_t *dbg_i_f, *dbg_i_n;         /* [batch, hkv, k_f] / [.., k_n] */
+  int32_t *dbg_middle, *dbg_counts;   /* [batch, hkv, k2] / [batch, hkv] */
+  int64_t *dbg_bounds;                /* [batch, 3] lower, upper, quota */
+  int32_t *dbg_cand_tok;              /* [batch, hkv, dbg_cand_cap] scored tokens */
+  uint16_t *dbg_cand_logit;           /* their bf16 logit bits */
+  int32_t *dbg_cand_count;            /* [batch, hkv] */
+  int64_t dbg_cand_cap;
+} NfaSelectParams;
+
+typedef struct NfaAttnParams {
+  int32_t abi_version;
+  int32_t struct_size;
+  int32_t total_q;            /* T query rows */
+  int32_t hq, hkv, head_dim, head_dim_v, page;
+  int32_t gather_rows;        /* rows of gather / vis_lens */
+  int32_t max_vis;
+  int32_t kv_dtype, q_dtype;  /* output dtype == q dtype */
+  int32_t tokens_per_split;   /* 0 = automatic */
+  int32_t pool_pages;         /* pages in the KV arena; slots beyond are
+                                 skipped like negative slots */
+  float scale;
+  float pad1;
+  const void *q;              /* [T, hq, head_dim] contiguous */
+  const void *k_pool, *v_pool;
+  const int32_t *gather;      /* [gather_rows, hkv, max_vis] physical slots */
+  const int32_t *vis_lens;    /* [gather_rows, hkv] */
+  const int32_t *query_to_req;/* [T] */
+  void *out;                  /* [T, hq, head_dim_v] */
+  void *workspace;
+  int64_t workspace_bytes;
+} NfaAttnParams;
+
+/* ABI / diagnostics */
+int32_t nfa_abi_version(void);
+int32_t nfa_select_params_size(void);
+int32_t nfa_attn_params_size(void);
+const char *nfa_last_error(void);
+
+/* Scratch bytes a call with these parameters needs (0 on bad params). */
+int64_t nfa_select_workspace_bytes(const NfaSelectParams *p);
+int64_t nfa_attn_workspace_bytes(const NfaAttnParams *p);
+
+/* A1-A9: decode write + page statistics + L1 + L2 + union for one layer. */
+int32_t nfa_select_layer(const NfaSelectParams *p, void *stream);
+
+/* A10: sparse gather attention, out[t,h] = softmax(scale q k^T) v. */
+int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream);
+
+/* A11: one decode token per row; slot < 0 writes nothing. */
+int32_t nfa_paged_write_decode(const void *keys, const void *values,
+                               const int32_t *slots, int32_t batch,
+                               int32_t hkv, int32_t head_dim,
+                               int32_t head_dim_v, int32_t page,
+                               int32_t kv_dtype, void *k_pool, void *v_pool,
+                               void *stream);
+
+/* K13: prefill of n tokens of one request through its block-table row. */
+int32_t nfa_paged_write_prefill(const void *keys, const void *values,
+                                int64_t n, const int32_t *block_table_row,
+                                int32_t hkv, int32_t head_dim,
+                                int32_t head_dim_v, int32_t page,
+                                int32_t kv_dtype, void *k_pool, void *v_pool,
+                                void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NFA_HIP_H */

@@ -1,0 +1,75 @@
+"""The C ABI of libnfa_hip.so: exported symbols, struct layout, host checks.
+
+Runs without a GPU: only entry points that reject their arguments before
+any HIP call are invoked.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'nfa_hip.h')
+
+
+@pytest.fixture(scope='module')
+def lib():
+    import torch  # noqa: F401  (bind to torch's HIP runtime first)
+    from sparse_attn import _native
+    if not os.path.exists(_native.LIB_PATH):
+        from sparse_attn import _build
+        _build.build()
+    return _native.load_library()
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r'\b(nfa_[a-z0-9_]+)\s*\(', text)))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = _declared()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_struct_layout_matches(lib):
+    from sparse_attn import _native
+    assert lib.nfa_select_params_size() == ctypes.sizeof(_native.NfaSelectParams)
+    assert lib.nfa_attn_params_size() == ctypes.sizeof(_native.NfaAttnParams)
+    assert lib.nfa_abi_version() == _native.ABI_VERSION
+
+
+def test_null_and_bad_params_are_rejected_before_launch(lib):
+    from sparse_attn import _native
+    assert lib.nfa_select_layer(None, None) == -1
+    assert b'null params' in lib.nfa_last_error()
+    p = _native.NfaSelectParams()
+    p.abi_version = 99
+    p.struct_size = ctypes.sizeof(p)
+    assert lib.nfa_select_layer(ctypes.byref(p), None) == -1
+    assert b'ABI mismatch' in lib.nfa_last_error()
+    p.abi_version = _native.ABI_VERSION
+    p.batch, p.hq, p.hkv = 1, 32, 8
+    p.dsub = 48
+    assert lib.nfa_select_layer(ctypes.byref(p), None) == -1
+    assert b'L1 dim' in lib.nfa_last_error()
+
+
+def test_workspace_size_is_host_computed(lib):
+    from sparse_attn import _native
+    p = _native.NfaSelectParams()
+    p.abi_version = _native.ABI_VERSION
+    p.struct_size = ctypes.sizeof(p)
+    p.batch, p.hq, p.hkv, p.bs, p.max_blocks = 1, 32, 8, 16, 8216
+    p.k_f, p.k_n, p.k2, p.dsub, p.fine_dsub = 96, 32, 1024, 32, 32
+    need = lib.nfa_select_workspace_bytes(ctypes.byref(p))
+    tiles = (8216 + 255) // 256
+    assert need >= 8 * 8 * tiles * (96 + 32)
+    a = _native.NfaAttnParams()
+    a.abi_version = _native.ABI_VERSION
+    a.struct_size = ctypes.sizeof(a)
+    a.total_q, a.hq, a.hkv, a.head_dim_v, a.max_vis = 1, 32, 8, 128, 1024
+    assert lib.nfa_attn_workspace_bytes(ctypes.byref(a)) > 0

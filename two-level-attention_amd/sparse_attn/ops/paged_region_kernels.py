@@ -1,0 +1,181 @@
+"""Paged KV writes and sparse gather attention on the graph-ready arena.
+
+Drop-in for the reference's ``sparse_attn/ops/paged_region_kernels.py``:
+``paged_write_prefill`` (:610-662), ``paged_write_decode`` (:665-724) and
+``sparse_paged_attention_gather`` (:800-1006).  Device work runs in
+libnfa_hip.so; CPU tensors are accepted only by the two write helpers (a plain
+copy, as the reference's CPU branch), never by the attention.
+"""
+import ctypes
+
+import torch
+
+from .. import _native as nat
+
+
+def _kv_contiguous(x):
+    return x if x.is_contiguous() else x.contiguous()
+
+
+def paged_write_prefill(cache_layer, key_states, value_states, block_table, *,
+                        workspace=None):
+    """Scatter an unpadded ``[1, HK, N, D]`` prefill through ``block_table``."""
+    if key_states.ndim != 4 or key_states.shape[0] != 1 or key_states.shape[2] < 1:
+        raise ValueError('paged write prefill expects [1,HK,N,D] keys')
+    if value_states.ndim != 4 or value_states.shape[:3] != key_states.shape[:3]:
+        raise ValueError('paged write prefill expects [1,HK,N,DV] values')
+    if key_states.shape[1] != cache_layer.num_kv_heads:
+        raise ValueError('KV head count does not match arena')
+    if key_states.shape[-1] != cache_layer.head_dim_k:
+        raise ValueError('key head dimension does not match arena')
+    if value_states.shape[-1] != cache_layer.head_dim_v:
+        raise ValueError('value head dimension does not match arena')
+    if block_table.ndim != 1 or block_table.device != key_states.device:
+        raise ValueError('prefill block table must be a device-matched 1D row')
+    n = key_states.shape[2]
+    page = cache_layer.geometry.page
+    if n > block_table.numel() * page:
+        raise ValueError('prefill length exceeds block-table capacity')
+    if key_states.dtype != cache_layer.kv_pool_k.dtype:
+        raise ValueError('KV dtype does not match arena')
+    if not key_states.is_cuda:
+        for lp in range((n + page - 1) // page):
+            pid = int(block_table[lp])
+            lo, hi = lp * page, min(lp * page + page, n)
+            cache_layer.kv_pool_k[pid, 0, :, :hi - lo].copy_(key_states[0, :, lo:hi])
+            cache_layer.kv_pool_v[pid, 0, :, :hi - lo].copy_(value_states[0, :, lo:hi])
+        return key_states, value_states
+    lib = nat.load_library()
+    keys = _kv_contiguous(key_states)
+    values = _kv_contiguous(value_states)
+    table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
+    table = _kv_contiguous(table)
+    rc = lib.nfa_paged_write_prefill(
+        keys.data_ptr(), values.data_ptr(), n, table.data_ptr(),
+        cache_layer.num_kv_heads, cache_layer.head_dim_k, cache_layer.head_dim_v,
+        page, nat.dtype_code(keys.dtype), cache_layer.kv_pool_k.data_ptr(),
+        cache_layer.kv_pool_v.data_ptr(), nat.stream_handle())
+    nat.check(rc, 'paged_write_prefill')
+    return key_states, value_states
+
+
+def paged_write_decode(cache_layer, key_states, value_states, slot_mapping, *,
+                       workspace=None):
+    """Write ``[B, HK, 1, D]`` decode keys/values at ``slot_mapping`` [B]."""
+    if key_states.ndim != 4 or key_states.shape[-2] != 1:
+        raise ValueError('paged write decode expects [B,HK,1,D] keys')
+    if value_states.ndim != 4 or value_states.shape[-2] != 1:
+        raise ValueError('paged write decode expects [B,HK,1,DV] values')
+    if key_states.shape[0] != slot_mapping.shape[0]:
+        raise ValueError('slot mapping batch must match KV batch')
+    if key_states.shape[1] != cache_layer.num_kv_heads:
+        raise ValueError('KV head count does not match arena')
+    if key_states.device != slot_mapping.device:
+        slot_mapping = slot_mapping.to(key_states.device)
+    batch = key_states.shape[0]
+    page = cache_layer.geometry.page
+    if not key_states.is_cuda:
+        pad_slot = cache_layer.PAD_PAGE_ID * page
+        for b in range(batch):
+            slot = int(slot_mapping[b])
+            pid, off = divmod(slot if slot >= 0 else pad_slot, page)
+            cache_layer.kv_pool_k[pid, 0, :, off] = key_states[b, :, 0]
+            cache_layer.kv_pool_v[pid, 0, :, off] = value_states[b, :, 0]
+        return key_states, value_states
+    lib = nat.load_library()
+    keys = _kv_contiguous(key_states.to(cache_layer.kv_pool_k.dtype))
+    values = _kv_contiguous(value_states.to(cache_layer.kv_pool_v.dtype))
+    slots = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
+    slots = _kv_contiguous(slots)
+    rc = lib.nfa_paged_write_decode(
+        keys.data_ptr(), values.data_ptr(), slots.data_ptr(), batch,
+        cache_layer.num_kv_heads, cache_layer.head_dim_k, cache_layer.head_dim_v,
+        page, nat.dtype_code(keys.dtype), cache_layer.kv_pool_k.data_ptr(),
+        cache_layer.kv_pool_v.data_ptr(), nat.stream_handle())
+    nat.check(rc, 'paged_write_decode')
+    return key_states, value_states
+
+
+def _scratch(workspace, key, nbytes, device):
+    """Zero-initialised byte scratch, cached in ``workspace`` when given."""
+    if workspace is None:
+        return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    buf = workspace.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f'scratch {key!r} must be allocated before capture')
+        buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        workspace[key] = buf
+    return buf
+
+
+def sparse_paged_attention_gather(cache_layer, q, gather_indices, visible_lens,
+                                  query_to_req, *, scale, workspace=None,
+                                  split_kv=False, tokens_per_split=0):
+    """Attention of each query head over its kv group's selected slots.
+
+    ``q`` is ``[T, HQ, D]``; ``gather_indices`` ``[B, HK, MAX_VISIBLE]`` holds
+    absolute physical slots, ``visible_lens`` ``[B, HK]`` their counts and
+    ``query_to_req`` ``[T]`` the gather row of each query row (-1 = padding,
+    output zero).  Softmax in fp32; output in the dtype of ``q``.
+    ``split_kv`` is accepted for compatibility; the kernel always splits the
+    selected slots across workgroups and merges the partial softmax states.
+    """
+    if q.ndim != 3 or q.shape[-1] != cache_layer.head_dim_k:
+        raise ValueError('sparse gather attention expects flat [T,HQ,D] query')
+    hq = q.shape[1]
+    hk = cache_layer.num_kv_heads
+    if hq % hk != 0:
+        raise ValueError('GQA requires HQ % HK == 0')
+    if (gather_indices.ndim != 3 or gather_indices.shape[1] != hk
+            or visible_lens.shape != gather_indices.shape[:2]):
+        raise ValueError('gather attention expects indices [B,HK,K] and lens [B,HK]')
+    page = cache_layer.geometry.page
+    if page & (page - 1):
+        raise ValueError('sparse gather attention requires power-of-two page size')
+    nat.require_hip(q, 'sparse_paged_attention_gather')
+    lib = nat.load_library()
+    total_q = q.shape[0]
+    out = q.new_empty((total_q, hq, cache_layer.head_dim_v))
+    if total_q == 0:
+        return out
+    qc = q if q.is_contiguous() else q.contiguous()
+    gather = gather_indices
+    if gather.dtype != torch.int32 or not gather.is_contiguous():
+        raise ValueError('gather indices must be contiguous int32')
+    lens = visible_lens
+    if lens.dtype != torch.int32 or not lens.is_contiguous():
+        raise ValueError('visible lens must be contiguous int32')
+    q2r = query_to_req
+    if q2r.dtype != torch.int32:
+        q2r = q2r.to(torch.int32)
+    q2r = q2r.contiguous()
+    p = nat.NfaAttnParams()
+    p.abi_version = nat.ABI_VERSION
+    p.struct_size = ctypes.sizeof(nat.NfaAttnParams)
+    p.total_q = total_q
+    p.hq, p.hkv = hq, hk
+    p.head_dim, p.head_dim_v = cache_layer.head_dim_k, cache_layer.head_dim_v
+    p.page = page
+    p.gather_rows = gather.shape[0]
+    p.max_vis = gather.shape[-1]
+    p.kv_dtype = nat.dtype_code(cache_layer.kv_pool_k.dtype)
+    p.q_dtype = nat.dtype_code(q.dtype)
+    p.tokens_per_split = int(tokens_per_split)
+    p.pool_pages = cache_layer.kv_pool_k.shape[0]
+    p.scale = float(scale)
+    p.q = qc.data_ptr()
+    p.k_pool = cache_layer.kv_pool_k.data_ptr()
+    p.v_pool = cache_layer.kv_pool_v.data_ptr()
+    p.gather = gather.data_ptr()
+    p.vis_lens = lens.data_ptr()
+    p.query_to_req = q2r.data_ptr()
+    p.out = out.data_ptr()
+    need = lib.nfa_attn_workspace_bytes(ctypes.byref(p))
+    ws = _scratch(workspace, ('nfa_attn_scratch', total_q, hk, p.max_vis, hq,
+                              p.head_dim_v, p.tokens_per_split), need, q.device)
+    p.workspace = ws.data_ptr()
+    p.workspace_bytes = ws.numel()
+    nat.check(lib.nfa_sparse_attn_decode(ctypes.byref(p), nat.stream_handle()),
+              'sparse_paged_attention_gather')
+    return out
