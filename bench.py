@@ -1,0 +1,431 @@
+#!/usr/bin/env python
+"""NFA two-level sparse-attention decode at 128K context on one MI355X.
+
+Workload (Qwen3-8B attention geometry): 36 layers, 32 query / 8 KV heads,
+head_dim 128, batch 1, 131072-token context, paged bf16 KV with page = block
+= 16, production NFA flags (far minmax, near avg, 32 near pages of 128 L1
+pages, near_len 4096, tail subspace at cmp_ratio 4, sink 4, SWA 128, L2
+top-1024).  Each layer owns its own 128K paged cache (18 GiB of KV in total,
+far beyond the 256 MiB Infinity Cache).  Synthetic keys follow the
+outlier-channel recipe: N(0,1) per channel times a per-channel
+LogNormal(0,1) scale, RoPE theta 1e6 at positions 0..L-1; values and queries
+N(0,1).
+
+One step = one decode token through the hot path of all 36 layers: the
+selector (fused decode K/V write, page statistics, L1, L2, union) and the
+sparse gather attention, captured once into a hipGraph and replayed, with
+the host-side step planning (plan_common / commit_step) in the timed loop.
+Dense projections and the MLP are outside this hot path.
+
+Prints one JSON line (see ``_result``); ``--gpus`` above 1 is refused: this
+path runs on one GPU.
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, 'two-level-attention_amd')):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=200)
+    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--ctx', type=int, default=131072)
+    ap.add_argument('--layers', type=int, default=36)
+    ap.add_argument('--kernel-rounds', type=int, default=20)
+    ap.add_argument('--cpu-seconds', type=float, default=15.0,
+                    help='budget of the CPU oracle baseline sample')
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--seed', type=int, default=20261201)
+    ap.add_argument('--timeline', type=int, default=0,
+                    help='print selector phase timings of N extra decode steps')
+    return ap.parse_args()
+
+
+def synthetic_keys(torch, n, hkv, d, gen, device, theta=1e6):
+    """N(0,1) x per-channel LogNormal(0,1) scale, RoPE (half-split) applied."""
+    scale = torch.exp(torch.randn(hkv, 1, d, generator=gen, device=device))
+    k = torch.randn(hkv, n, d, generator=gen, device=device) * scale
+    half = d // 2
+    inv = theta ** (-torch.arange(0, half, device=device, dtype=torch.float32) / half)
+    pos = torch.arange(n, device=device, dtype=torch.float32)
+    ang = pos[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    x1, x2 = k[..., :half], k[..., half:]
+    out = torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1)
+    return out.to(torch.bfloat16).unsqueeze(0)
+
+
+def build_workload(torch, args, device):
+    from types import SimpleNamespace
+    from sparse_attn.cache import GraphReadyPagedRegionCache
+    from sparse_attn.indexer.nfa_indexer import NFAIndexer
+    from sparse_attn.ops.paged_region_kernels_nfa import nfa_args
+    from sparse_attn.policies.region_geometry import RegionGeometry
+
+    hkv, hq, d, page = 8, 32, 128, 16
+    new_tokens = args.warmup + args.steps + args.kernel_rounds + args.timeline + 8
+    geo = RegionGeometry(sink=4, near=4096, window=128, page=page,
+                         max_new_tokens=new_tokens)
+    pages = (args.ctx + new_tokens + page - 1) // page
+    cache = GraphReadyPagedRegionCache(
+        args.layers, geo, max_requests=1, max_physical_pages=pages + 1,
+        max_blocks=pages + 8, max_visible_len=1024, max_query_tokens=1,
+        num_kv_heads=hkv, num_query_heads=hq, head_dim_k=d, head_dim_v=d,
+        dtype=torch.bfloat16, device=device)
+    fargs = nfa_args('tail')
+    fargs.tia_block_size = page
+    indexer = NFAIndexer(fargs)
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    cache.add_request(0)
+    for layer in range(args.layers):
+        keys = synthetic_keys(torch, args.ctx, hkv, d, gen, device)
+        values = torch.randn(1, hkv, args.ctx, d, generator=gen,
+                             device=device).to(torch.bfloat16)
+        cache.write_prefill(layer, 0, keys, values)
+        del keys, values
+    cache.freeze(0, [False] * args.layers, [False] * args.layers)
+    attn = [SimpleNamespace(indexer=indexer, scaling=d ** -0.5, layer_idx=l)
+            for l in range(args.layers)]
+    q = [torch.randn(1, hq, d, generator=gen, device=device).to(torch.bfloat16)
+         for _ in range(args.layers)]
+    kn = [torch.randn(1, hkv, 1, d, generator=gen, device=device).to(torch.bfloat16)
+          for _ in range(args.layers)]
+    vn = [torch.randn(1, hkv, 1, d, generator=gen, device=device).to(torch.bfloat16)
+          for _ in range(args.layers)]
+    torch.cuda.synchronize()
+    return SimpleNamespace(cache=cache, indexer=indexer, attn=attn, q=q, kn=kn,
+                           vn=vn, hkv=hkv, hq=hq, d=d, page=page)
+
+
+def run_layer(w, layer, outs):
+    from sparse_attn.indexer.nfa_layer_batch_selector import \
+        select_topk_for_layer_batched
+    from sparse_attn.ops.paged_region_kernels_nfa import decode_graph_ready
+    cache = w.cache
+    select_topk_for_layer_batched(
+        cache, layer, [0], w.q[layer], attention=w.attn[layer],
+        decode_write=(w.kn[layer], w.vn[layer],
+                      cache.slot_mapping_for_layer(layer)[:1]))
+    outs[layer] = decode_graph_ready(w.attn[layer], w.q[layer], cache)
+
+
+def algorithmic_bytes(w, length, bs=16, window=128, near_len=4096, sink=4,
+                      k_far=96, k_near=32, k2=1024, dsub=32):
+    """Bytes one selector launch and one attention launch must move.
+
+    Selector: L1 reads min+max (far pool, minmax score) or sum (near pool,
+    avg score) of the 32 tail dims per page and KV head; L2 reads the 32 tail
+    dims (64 B) of every candidate token; plus the decode K/V write, the
+    latest page's statistics update, the query and the gather row.
+    Attention: K and V rows of every selected slot plus query, output and
+    gather row.  Pool sizes follow the selector's region formulas.
+    """
+    hkv, hq, d = w.hkv, w.hq, w.d
+    kt_eff = (length + bs - 1) // bs
+    spl = sink // bs
+    near_start = max((length - window - near_len) // bs, spl)
+    swa_lo_blk = max(near_start, kt_eff - max(1, window // bs))
+    p_far = max(0, near_start - spl) - (1 if sink % bs and near_start > spl else 0)
+    p_near = max(0, swa_lo_blk - near_start)
+    byp = max(length - window, 0)
+    if byp % bs and byp // bs >= near_start and byp // bs < swa_lo_blk:
+        p_near -= 1
+    # candidate tokens: full far/near pages, the sink page past the sink
+    # tokens and the part of the SWA boundary page before the window
+    t_c = (k_far + k_near) * bs + (bs - sink % bs if sink % bs else 0) + byp % bs
+    l1 = hkv * (2 * p_far * dsub * 2 + p_near * dsub * 2)
+    l2 = hkv * t_c * dsub * 2
+    misc = (2 * hkv * d * 2 * 2        # decode K/V write (read + write)
+            + 3 * hkv * dsub * 2       # latest page statistics
+            + bs * hkv * dsub * 2      # latest page keys
+            + hq * d * 2               # query
+            + hkv * k2 * 4)            # gather row
+    sel = l1 + l2 + misc
+    att = hkv * k2 * (d + d) * 2 + hkv * k2 * 4 + 2 * hq * d * 2
+    return dict(select=sel, attention=att, l1=l1, l2=l2, p_far=p_far,
+                p_near=p_near, t_c=t_c)
+
+
+def _oracle_cfg(w):
+    """Oracle configuration of the workload (CPU baseline leg only)."""
+    from oracle import nfa_oracle as orc
+    import numpy as np
+    import torch
+    cache = w.cache
+    dims = w.indexer._subspace_indices(torch.device('cpu')).numpy()
+    return orc.NfaConfig(
+        hq=w.hq, hkv=w.hkv, head_dim=w.d, head_dim_v=w.d, bs=16, page=w.page,
+        max_blocks=cache.max_blocks, geo_sink=4, geo_near=4096, geo_window=128,
+        sink_tokens=4, swa=128, near_len=4096, k1=128, near_pages=32, k2=1024,
+        dims=np.asarray(dims), fine_dims=np.asarray(dims), scale=w.d ** -0.5)
+
+
+def time_kernels(torch, w, rounds, plan):
+    """Per-launch durations of the selector and attention kernels, from HIP
+    events recorded around each launch on the launching stream, over
+    ``rounds`` eager decode steps of all layers."""
+    from sparse_attn.indexer.nfa_layer_batch_selector import \
+        select_topk_for_layer_batched
+    from sparse_attn.ops.paged_region_kernels_nfa import decode_graph_ready
+    cache = w.cache
+    layers = len(w.q)
+    sel_ev, att_ev = [], []
+    length = 0
+    for _ in range(rounds):
+        plan()
+        length = int(cache.pending_lengths[0])
+        for layer in range(layers):
+            a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            a.record()
+            select_topk_for_layer_batched(
+                cache, layer, [0], w.q[layer], attention=w.attn[layer],
+                decode_write=(w.kn[layer], w.vn[layer],
+                              cache.slot_mapping_for_layer(layer)[:1]))
+            b.record()
+            decode_graph_ready(w.attn[layer], w.q[layer], cache)
+            c.record()
+            sel_ev.append((a, b))
+            att_ev.append((b, c))
+        cache.commit_step()
+    torch.cuda.synchronize()
+    sel = sorted(x.elapsed_time(y) * 1000.0 for x, y in sel_ev)
+    att = sorted(x.elapsed_time(y) * 1000.0 for x, y in att_ev)
+    mean = lambda v: sum(v) / len(v)
+    return dict(select_us=mean(sel), attention_us=mean(att),
+                select_us_median=sel[len(sel) // 2],
+                attention_us_median=att[len(att) // 2], length=length)
+
+
+def selector_timeline(torch, w, steps, plan):
+    """Phase durations (µs) of the selector kernel from its in-kernel wall
+    clock marks, over ``steps`` eager decode steps of every layer."""
+    from sparse_attn import _native
+    from sparse_attn.indexer.nfa_layer_batch_selector import \
+        select_topk_for_layer_batched
+    rate_khz = _native.load_library().nfa_wall_clock_khz() or 100000
+    cache = w.cache
+    tiles, tails = [], []
+    for _ in range(steps):
+        plan()
+        for layer in range(len(w.q)):
+            dbg = {'want_clock': True}
+            select_topk_for_layer_batched(
+                cache, layer, [0], w.q[layer], attention=w.attn[layer],
+                decode_write=(w.kn[layer], w.vn[layer],
+                              cache.slot_mapping_for_layer(layer)[:1]),
+                _debug=dbg)
+            tiles.append(dbg['clock'])
+        cache.commit_step()
+    torch.cuda.synchronize()
+    us = 1000.0 / rate_khz
+    import numpy as np
+    acc = {}
+    for clk in tiles:
+        c = clk.cpu().numpy().astype(np.int64)
+        tile, tail = c[:, :-1, :], c[:, -1, :]
+        start = tile[:, :, 0][tile[:, :, 0] > 0].min()
+        ends = tail[:, 6]
+        acc.setdefault('kernel span', []).append((ends.max() - start) * us)
+        acc.setdefault('last tile arrives', []).append(
+            (tile[:, :, 5].max() - start) * us)
+        names = ['write+dims', 'page stats', 'q prep', 'L1 scores', 'tile top-k']
+        for k, name in enumerate(names):
+            d = (tile[:, :, k + 1] - tile[:, :, k]) * us
+            acc.setdefault(f'tile {name} (max)', []).append(d.max())
+        tnames = ['L1 merge', 'cand pages', 'q grouped', 'L2 logits', 'L2 top-k',
+                  'union']
+        for k, name in enumerate(tnames):
+            d = (tail[:, k + 1] - tail[:, k]) * us
+            acc.setdefault(f'tail {name} (max)', []).append(d.max())
+    for name, vals in acc.items():
+        print(f'# timeline {name:28s} median {np.median(vals):8.2f} us',
+              file=sys.stderr, flush=True)
+
+
+def cpu_baseline(torch, w, seconds):
+    """The CPU oracle on a bounded sample: layer-0 decode steps at the same
+    128K context, single-threaded numpy."""
+    import numpy as np
+    from oracle import nfa_oracle as orc
+    try:
+        from threadpoolctl import threadpool_limits
+    except Exception:  # pragma: no cover
+        threadpool_limits = None
+    cache = w.cache
+    cfg = _oracle_cfg(w)
+    layer = cache.layers[0]
+    k_pool = layer.kv_pool_k.float().cpu().numpy()
+    v_pool = layer.kv_pool_v.float().cpu().numpy()
+    bt = cache.block_table_buf[0].cpu().numpy().astype(np.int64)
+    length = int(cache.states[0].logical_length) + 1
+    q = w.q[0].float().cpu().numpy()
+    q2r = np.zeros(1, dtype=np.int64)
+    ctx = threadpool_limits(1) if threadpool_limits else None
+    if ctx is not None:
+        ctx.__enter__()
+    try:
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            res = orc.select_layer(cfg, k_pool, bt, np.array([length]),
+                                   np.array([0]), np.array([True]), np.zeros(1),
+                                   np.zeros(1), q, 1024)
+            gather = np.zeros((1, w.hkv, 1024), dtype=np.int64)
+            vis = np.zeros((1, w.hkv), dtype=np.int64)
+            for kv in range(w.hkv):
+                r = res[0][kv]
+                gather[0, kv, :len(r.gather)] = r.gather
+                vis[0, kv] = r.vis_len
+            orc.sparse_attention(k_pool, v_pool, q, gather, vis, q2r,
+                                 cfg.scale, w.page)
+            n += 1
+            elapsed = time.perf_counter() - t0
+            if elapsed >= seconds or n >= 100:
+                break
+    finally:
+        if ctx is not None:
+            ctx.__exit__(None, None, None)
+    layer_s = elapsed / n
+    return dict(value=1.0 / (layer_s * len(w.q)), unit='tok/s', cores=1,
+                kind='port',
+                sample=f'{n} single-layer decode steps (selector + attention) '
+                       f'of the same 128K workload on the numpy oracle, '
+                       f'{layer_s * 1e3:.1f} ms per layer, scaled to '
+                       f'{len(w.q)} layers per token')
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({'error': 'this hot path runs on one GPU; '
+                                   f'--gpus {args.gpus} is not supported'}))
+        sys.exit(2)
+    import torch
+    from sparse_attn import _native
+    if not os.path.exists(_native.LIB_PATH):
+        import __graft_entry__
+        __graft_entry__.build()
+    device = torch.device('cuda:0')
+    torch.cuda.set_device(device)
+    t_setup = time.perf_counter()
+    w = build_workload(torch, args, device)
+    cache = w.cache
+    outs = [None] * args.layers
+    print(f'# workload ready in {time.perf_counter() - t_setup:.1f}s', file=sys.stderr,
+          flush=True)
+
+    def plan():
+        cache.new_step([0])
+        cache.plan_common([0])
+
+    # warm-up: first step rebuilds page statistics, later ones are incremental
+    for _ in range(args.warmup):
+        plan()
+        for layer in range(args.layers):
+            run_layer(w, layer, outs)
+        cache.commit_step()
+    torch.cuda.synchronize()
+
+    # capture one decode step of all layers
+    plan()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        for layer in range(args.layers):  # warm the capture stream
+            run_layer(w, layer, outs)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        for layer in range(args.layers):
+            run_layer(w, layer, outs)
+    cache.commit_step()
+    torch.cuda.synchronize()
+    print('# graph captured', file=sys.stderr, flush=True)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        plan()
+        graph.replay()
+        cache.commit_step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    print(f'# timed {args.steps} steps: {ms_per_step:.3f} ms/step', file=sys.stderr,
+          flush=True)
+
+    if args.timeline:
+        selector_timeline(torch, w, args.timeline, plan)
+    # per-kernel durations (events around each launch), same stream
+    kt = time_kernels(torch, w, args.kernel_rounds, plan)
+    nbytes = algorithmic_bytes(w, kt['length'])
+    sel_gbs = nbytes['select'] / (kt['select_us'] * 1e-6) / 1e9
+    att_gbs = nbytes['attention'] / (kt['attention_us'] * 1e-6) / 1e9
+    layer_us = ms_per_step * 1e3 / args.layers
+    layer_gbs = (nbytes['select'] + nbytes['attention']) / (layer_us * 1e-6) / 1e9
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print('# cpu baseline ...', file=sys.stderr, flush=True)
+        cpu = cpu_baseline(torch, w, args.cpu_seconds)
+
+    result = {
+        'metric': 'sparse-attn decode layer µs + e2e decode tok/s at 128K '
+                  'ctx; % of HBM peak',
+        'value': round(1e3 / ms_per_step, 2),
+        'unit': 'tok/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(ms_per_step, 4),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'bf16',
+        'data': 'synthetic',
+        'config': {
+            'workload': 'NFA sparse-attention decode hot path (selector + '
+                        'attention) of all 36 layers, Qwen3-8B attention '
+                        'geometry, batch 1, 128K context, page 16, hipGraph',
+            'layers': args.layers, 'context': args.ctx, 'batch': 1,
+            'heads': [w.hq, w.hkv], 'head_dim': w.d, 'page': w.page,
+            'nfa': 'far minmax / near avg, K1 128 (32 near), near_len 4096, '
+                   'tail dims cmp 4, sink 4, SWA 128, K2 1024',
+            'layer_us': round(layer_us, 3),
+            'layer_hbm_frac': round(layer_gbs / HBM_PEAK_GBS, 4),
+            'select_us': round(kt['select_us'], 3),
+            'attention_us': round(kt['attention_us'], 3),
+            'select_bytes': nbytes['select'],
+            'attention_bytes': nbytes['attention'],
+            'attention_gbs': round(att_gbs, 1),
+            'parallelism': 'single GPU',
+        },
+        'roofline': {
+            'bound': 'hbm',
+            'kernel': 'nfa_select_kernel',
+            'achieved': round(sel_gbs, 1),
+            'peak': HBM_PEAK_GBS,
+            'unit': 'GB/s',
+            'frac': round(sel_gbs / HBM_PEAK_GBS, 4),
+            'traffic': None,
+        },
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -121,6 +121,8 @@ typedef struct NfaSelectParams {
   uint16_t *dbg_cand_logit;           /* their bf16 logit bits */
   int32_t *dbg_cand_count;            /* [batch, hkv] */
   int64_t dbg_cand_cap;
+  int64_t *dbg_clock;                 /* [batch*hkv, ntiles + 1, 16] phase
+                                         timestamps (wall clock), or NULL */
 } NfaSelectParams;
 
 typedef struct NfaAttnParams {
@@ -148,6 +150,7 @@ typedef struct NfaAttnParams {
 
 /* ABI / diagnostics */
 int32_t nfa_abi_version(void);
+int32_t nfa_wall_clock_khz(void);   /* rate of the dbg_clock timestamps */
 int32_t nfa_select_params_size(void);
 int32_t nfa_attn_params_size(void);
 const char *nfa_last_error(void);

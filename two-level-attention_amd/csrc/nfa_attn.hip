@@ -17,6 +17,28 @@ namespace nfa {
 
 constexpr int AGMAX = 8;     // query heads per kv head
 constexpr int ADMAX = 256;   // head dim
+constexpr int kSplitMax = 64;                    // tokens per workgroup
+constexpr int kTpw = kSplitMax / NFA_WAVES;      // tokens per wave
+constexpr int kMaxSplits = 256;                  // splits merged in LDS
+
+// Two adjacent elements of a K/V row as one load.
+template <typename T> struct PairOf;
+template <> struct PairOf<uint16_t> {
+  using type = uint32_t;
+  static __device__ __forceinline__ type zero() { return 0u; }
+  static __device__ __forceinline__ void unpack(type v, float *a, float *b) {
+    *a = __uint_as_float(v << 16);
+    *b = __uint_as_float(v & 0xFFFF0000u);
+  }
+};
+template <> struct PairOf<float> {
+  using type = float2;
+  static __device__ __forceinline__ type zero() { return make_float2(0.f, 0.f); }
+  static __device__ __forceinline__ void unpack(type v, float *a, float *b) {
+    *a = v.x;
+    *b = v.y;
+  }
+};
 
 struct AttnDims {
   int split;    // tokens per split
@@ -30,7 +52,7 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p) {
   AttnDims a;
   a.rows = p.total_q * p.hkv;
   int split = p.tokens_per_split;
-  if (split <= 0) split = a.rows <= 16 ? 32 : (a.rows <= 64 ? 64 : 128);
+  if (split <= 0) split = a.rows <= 16 ? 32 : 64;
   a.split = split;
   a.nsplit = (p.max_vis + split - 1) / split;
   if (a.nsplit < 1) a.nsplit = 1;
@@ -59,8 +81,8 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int DV = p.head_dim_v;
 
   __shared__ float s_q[AGMAX * ADMAX];
-  __shared__ float s_p[AGMAX * 128];          // probabilities [G][split<=128]
-  __shared__ int s_slot[128];
+  __shared__ float s_p[AGMAX * kSplitMax];    // probabilities [G][split]
+  __shared__ int s_slot[kSplitMax];
   __shared__ float s_red[NFA_WAVES * AGMAX * ADMAX];
   __shared__ float s_m[AGMAX], s_z[AGMAX];
   __shared__ int s_last;
@@ -100,18 +122,41 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 
   const KV *kpool = (const KV *)p.k_pool;
   const KV *vpool = (const KV *)p.v_pool;
-  // scores: wave w takes tokens w, w+4, ...; lane holds dims 2*lane + 128*k
-  for (int i = w; i < cn; i += NFA_WAVES) {
+  // Raw row pieces: lane holds dims 2*lane + 128*h (h < 2); every row this
+  // wave needs is requested before the first one is used.
+  using Pair = typename PairOf<KV>::type;
+  constexpr int H = ADMAX / 128;
+  // scores: wave w takes tokens w, w+4, ... (at most kTpw of them)
+  Pair kraw[kTpw][H];
+#pragma unroll
+  for (int t = 0; t < kTpw; ++t) {
+    const int i = w + t * NFA_WAVES;
+    const int slot = i < cn ? s_slot[i] : -1;
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      kraw[t][h] = PairOf<KV>::zero();
+      const int d = 2 * lane + 128 * h;
+      if (slot >= 0 && d < D) {
+        const int phys = slot / p.page, off = slot % p.page;
+        kraw[t][h] = *reinterpret_cast<const Pair *>(
+            kpool + (((int64_t)phys * p.hkv + kh) * p.page + off) * D + d);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kTpw; ++t) {
+    const int i = w + t * NFA_WAVES;
+    if (i >= cn) break;
     const int slot = s_slot[i];
     float part_s[AGMAX];
 #pragma unroll
     for (int g = 0; g < AGMAX; ++g) part_s[g] = 0.0f;
-    if (slot >= 0) {
-      const int phys = slot / p.page, off = slot % p.page;
-      const KV *kr = kpool + (((int64_t)phys * p.hkv + kh) * p.page + off) * D;
-      for (int d = 2 * lane; d < D; d += 128) {
-        const float k0 = Elem<KV>::load(kr + d);
-        const float k1 = Elem<KV>::load(kr + d + 1);
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const int d = 2 * lane + 128 * h;
+      if (d < D) {
+        float k0, k1;
+        PairOf<KV>::unpack(kraw[t][h], &k0, &k1);
 #pragma unroll
         for (int g = 0; g < AGMAX; ++g) {
           if (g < G) {
@@ -128,7 +173,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
         if (lane == 0)
-          s_p[g * 128 + i] =
+          s_p[g * kSplitMax + i] =
               slot >= 0 ? x * p.scale : __uint_as_float(0xFF800000u);
       }
     }
@@ -138,14 +183,14 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   // softmax partial per head (one wave per head)
   for (int g = w; g < G; g += NFA_WAVES) {
     float m = __uint_as_float(0xFF800000u);
-    for (int i = lane; i < cn; i += 64) m = fmaxf(m, s_p[g * 128 + i]);
+    for (int i = lane; i < cn; i += 64) m = fmaxf(m, s_p[g * kSplitMax + i]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     float z = 0.0f;
     for (int i = lane; i < cn; i += 64) {
-      const float s = s_p[g * 128 + i];
-      const float e = (m == __uint_as_float(0xFF800000u)) ? 0.0f : __expf(s - m);
-      s_p[g * 128 + i] = e;
+      const float sc = s_p[g * kSplitMax + i];
+      const float e = (m == __uint_as_float(0xFF800000u)) ? 0.0f : __expf(sc - m);
+      s_p[g * kSplitMax + i] = e;
       z += e;
     }
 #pragma unroll
@@ -157,29 +202,45 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   __syncthreads();
 
-  // P V: wave w accumulates tokens w, w+4, ...; lane holds dims 2*lane+128*k
-  float acc[AGMAX][ADMAX / 128 * 2];
+  // P V with the same token assignment; V rows requested up front
+  Pair vraw[kTpw][H];
+#pragma unroll
+  for (int t = 0; t < kTpw; ++t) {
+    const int i = w + t * NFA_WAVES;
+    const int slot = i < cn ? s_slot[i] : -1;
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      vraw[t][h] = PairOf<KV>::zero();
+      const int d = 2 * lane + 128 * h;
+      if (slot >= 0 && d < DV) {
+        const int phys = slot / p.page, off = slot % p.page;
+        vraw[t][h] = *reinterpret_cast<const Pair *>(
+            vpool + (((int64_t)phys * p.hkv + kh) * p.page + off) * DV + d);
+      }
+    }
+  }
+  float acc[AGMAX][H * 2];
 #pragma unroll
   for (int g = 0; g < AGMAX; ++g)
 #pragma unroll
-    for (int e = 0; e < ADMAX / 128 * 2; ++e) acc[g][e] = 0.0f;
-  for (int i = w; i < cn; i += NFA_WAVES) {
-    const int slot = s_slot[i];
-    if (slot < 0) continue;
-    const int phys = slot / p.page, off = slot % p.page;
-    const KV *vr = vpool + (((int64_t)phys * p.hkv + kh) * p.page + off) * DV;
+    for (int e = 0; e < H * 2; ++e) acc[g][e] = 0.0f;
 #pragma unroll
-    for (int k = 0; k < ADMAX / 128; ++k) {
-      const int d = 2 * lane + 128 * k;
+  for (int t = 0; t < kTpw; ++t) {
+    const int i = w + t * NFA_WAVES;
+    if (i >= cn) break;
+    if (s_slot[i] < 0) continue;
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      const int d = 2 * lane + 128 * h;
       if (d < DV) {
-        const float v0 = Elem<KV>::load(vr + d);
-        const float v1 = Elem<KV>::load(vr + d + 1);
+        float v0, v1;
+        PairOf<KV>::unpack(vraw[t][h], &v0, &v1);
 #pragma unroll
         for (int g = 0; g < AGMAX; ++g) {
           if (g < G) {
-            const float pr = s_p[g * 128 + i];
-            acc[g][2 * k] = fmaf(pr, v0, acc[g][2 * k]);
-            acc[g][2 * k + 1] = fmaf(pr, v1, acc[g][2 * k + 1]);
+            const float pr = s_p[g * kSplitMax + i];
+            acc[g][2 * h] = fmaf(pr, v0, acc[g][2 * h]);
+            acc[g][2 * h + 1] = fmaf(pr, v1, acc[g][2 * h + 1]);
           }
         }
       }
@@ -225,20 +286,41 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 
   const float *base = (const float *)(ws + ad.w_part) +
                       (int64_t)row * ad.nsplit * ad.part_stride;
+  // split maxima and denominators -> LDS (one round of loads)
+  float *s_ms = s_red;                         // [G][kMaxSplits]
+  float *s_zs = s_red + AGMAX * kMaxSplits;    // [G][kMaxSplits]
+  for (int i = tid; i < G * ad.nsplit; i += NFA_BLOCK) {
+    const int g = i / ad.nsplit, sp = i % ad.nsplit;
+    const float *ps = base + (int64_t)sp * ad.part_stride + g * (DV + 2);
+    s_ms[g * kMaxSplits + sp] = ps[0];
+    s_zs[g * kMaxSplits + sp] = ps[1];
+  }
+  __syncthreads();
   for (int i = tid; i < G * DV; i += NFA_BLOCK) {
     const int g = i / DV, d = i % DV;
     float M = __uint_as_float(0xFF800000u);
-    for (int s = 0; s < ad.nsplit; ++s)
-      M = fmaxf(M, base[(int64_t)s * ad.part_stride + g * (DV + 2)]);
+    for (int sp = 0; sp < ad.nsplit; ++sp) M = fmaxf(M, s_ms[g * kMaxSplits + sp]);
     float Z = 0.0f, O = 0.0f;
     if (M != __uint_as_float(0xFF800000u)) {
-      for (int s = 0; s < ad.nsplit; ++s) {
-        const float *ps = base + (int64_t)s * ad.part_stride + g * (DV + 2);
-        const float ms = ps[0];
-        if (ms == __uint_as_float(0xFF800000u)) continue;
-        const float f = __expf(ms - M);
-        Z += ps[1] * f;
-        O += ps[2 + d] * f;
+      for (int s0 = 0; s0 < ad.nsplit; s0 += 8) {
+        float a[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int sp = s0 + u;
+          a[u] = sp < ad.nsplit
+                     ? base[(int64_t)sp * ad.part_stride + g * (DV + 2) + 2 + d]
+                     : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int sp = s0 + u;
+          if (sp >= ad.nsplit) break;
+          const float ms = s_ms[g * kMaxSplits + sp];
+          if (ms == __uint_as_float(0xFF800000u)) continue;
+          const float f = __expf(ms - M);
+          Z += s_zs[g * kMaxSplits + sp] * f;
+          O += a[u] * f;
+        }
       }
     }
     const float o = Z == 0.0f ? 0.0f : O / Z;
@@ -280,8 +362,13 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
     nfa_set_error("nfa_sparse_attn_decode: bad max_vis/page/pool/rows");
     return NFA_EINVAL;
   }
-  if (p->tokens_per_split < 0 || p->tokens_per_split > 128) {
-    nfa_set_error("nfa_sparse_attn_decode: tokens_per_split must be in [0,128]");
+  if (p->tokens_per_split < 0 || p->tokens_per_split > nfa::kSplitMax) {
+    nfa_set_error("nfa_sparse_attn_decode: tokens_per_split must be in [0,64]");
+    return NFA_EINVAL;
+  }
+  if (nfa::attn_dims(*p).nsplit > nfa::kMaxSplits) {
+    nfa_set_error("nfa_sparse_attn_decode: %d splits exceed %d",
+                  nfa::attn_dims(*p).nsplit, nfa::kMaxSplits);
     return NFA_EINVAL;
   }
   if (!p->q || !p->k_pool || !p->v_pool || !p->gather || !p->vis_lens ||

@@ -35,15 +35,22 @@ struct SelDims {
   int np;          // candidate page slots = k_f + k_n + 2
   int cand_cap;    // np * bs
   int prot;        // protected width = min(s_cap, sink + swa)
+  int n_merge;     // keys merged per L1 pool: ntiles * max(k_f, k_n)
+  bool merge_lds;  // merge keys fit the LDS union
   int lds_bytes;   // dynamic LDS of the launch
-  // LDS byte offsets
-  int o_qf, o_hist, o_tmp, o_key, o_pages, o_pgoff, o_cand, o_l0, o_l1, o_mid,
-      o_sel, o_fp, o_np, o_qg, o_sp, o_rank;
+  // LDS byte offsets: common part, then the tile and tail parts overlap
+  int o_hist, o_tmp;
+  int o_qf, o_key, o_dims, o_stage;                       // tile stage
+  int o_fp, o_np, o_sel, o_qg, o_choff, o_fdims, o_pages, o_pgoff, o_pphys,
+      o_sp, o_rank, o_union, o_cand, o_l0, o_l1, o_mid;  // tail stage
   // global workspace byte offsets
   int64_t w_rowcnt, w_reqcnt, w_far, w_near, w_total;
 };
 
 __host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
+
+// Tokens per staging sub-batch of the page-statistics pass.
+constexpr int kStatTokens = 16;
 
 __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p) {
   SelDims s;
@@ -54,24 +61,41 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p) {
   const int s_cap = p.max_blocks * p.bs;
   s.prot = p.sink_tokens + p.swa < s_cap ? p.sink_tokens + p.swa : s_cap;
   const int kmax = p.k_f > p.k_n ? p.k_f : p.k_n;
+  s.n_merge = s.ntiles * (kmax > 0 ? kmax : 1);
   int o = 0;
-  s.o_qf = o;    o += align16(4 * group * p.dsub);
   s.o_hist = o;  o += align16(4 * 256);
   s.o_tmp = o;   o += align16(4 * 32);
+  const int base = o;
+  // tile stage
+  s.o_qf = o;    o += align16(4 * group * p.dsub);
   s.o_key = o;   o += align16(4 * NFA_BLOCK);
+  s.o_dims = o;  o += align16(4 * p.dsub);
+  s.o_stage = o; o += align16(4 * NFA_BLOCK * kStatTokens);
+  const int tile_end = o;
+  // tail stage
+  o = base;
+  s.o_fp = o;    o += align16(4 * (p.k_f > 0 ? p.k_f : 1));
+  s.o_np = o;    o += align16(4 * (p.k_n > 0 ? p.k_n : 1));
+  s.o_sel = o;   o += align16(8 * (kmax > 0 ? kmax : 1));
+  s.o_qg = o;    o += align16(4 * p.fine_dsub);
+  s.o_choff = o; o += align16(4 * 64);
+  s.o_fdims = o; o += align16(4 * p.fine_dsub);
   s.o_pages = o; o += align16(4 * s.np);
   s.o_pgoff = o; o += align16(4 * (s.np + 1));
+  s.o_pphys = o; o += align16(4 * s.np);
+  s.o_sp = o;    o += align16(4 * s.np);
+  s.o_rank = o;  o += align16(4 * s.np);
+  s.o_union = o;
+  // union: merge keys (u16) | candidates + lists
   s.o_cand = o;  o += align16(2 * s.cand_cap);
   s.o_l0 = o;    o += align16(4 * p.k2);
   s.o_l1 = o;    o += align16(4 * p.k2);
   s.o_mid = o;   o += align16(4 * p.k2);
-  s.o_sel = o;   o += align16(8 * (kmax > 0 ? kmax : 1));
-  s.o_fp = o;    o += align16(4 * (p.k_f > 0 ? p.k_f : 1));
-  s.o_np = o;    o += align16(4 * (p.k_n > 0 ? p.k_n : 1));
-  s.o_qg = o;    o += align16(4 * p.fine_dsub);
-  s.o_sp = o;    o += align16(4 * s.np);
-  s.o_rank = o;  o += align16(4 * s.np);
-  s.lds_bytes = o;
+  int tail_end = o;
+  const int merge_end = s.o_union + align16(2 * s.n_merge);
+  s.merge_lds = merge_end <= 60 * 1024;
+  if (s.merge_lds && merge_end > tail_end) tail_end = merge_end;
+  s.lds_bytes = tile_end > tail_end ? tile_end : tail_end;
   const int rows = p.batch * p.hkv;
   int64_t w = 0;
   s.w_rowcnt = w; w += ((int64_t)4 * rows + 255) & ~(int64_t)255;
@@ -199,37 +223,133 @@ __device__ __forceinline__ int64_t kv_offset(const NfaSelectParams &p,
 // page statistics of pages [pg_lo, pg_hi) for one (request, kv)
 // ---------------------------------------------------------------------------
 
+// The page's tokens are staged through LDS in sub-batches of kStatTokens
+// (all loads of a sub-batch in flight at once); each (page, dim) thread then
+// scans its tokens in ascending order: v < min, v > max, sum + v.
 template <int DSUB, typename KV>
 __device__ void compute_stats(const NfaSelectParams &p, int64_t req, int kv,
-                              int L, int pg_lo, int pg_hi) {
+                              int L, int pg_lo, int pg_hi, float *s_stage,
+                              const int *s_dims) {
   const KV *kpool = (const KV *)p.k_pool_l;
   const int32_t *bt = p.block_table_l + req * p.max_blocks;
-  constexpr int PER = NFA_BLOCK / DSUB;  // pages in flight
-  const int d = threadIdx.x % DSUB;
-  const int slot = threadIdx.x / DSUB;
-  const int dim = p.dims[d];
+  constexpr int PER = NFA_BLOCK / DSUB;  // pages per pass
+  const int tid = threadIdx.x;
+  const int d = tid % DSUB;
+  const int slot = tid / DSUB;
   KV *smin = (KV *)p.stat_min_l;
   KV *smax = (KV *)p.stat_max_l;
   KV *ssum = (KV *)p.stat_sum_l;
-  for (int pg = pg_lo + slot; pg < pg_hi; pg += PER) {
+  for (int pg0 = pg_lo; pg0 < pg_hi; pg0 += PER) {
+    const int pg = pg0 + slot;
     float mn = __uint_as_float(0x7F800000u);
     float mx = __uint_as_float(0xFF800000u);
     float sm = 0.0f;
-    for (int i = 0; i < p.bs; ++i) {
-      const int tok = pg * p.bs + i;
-      if (tok >= L) break;
-      const int lp = tok / p.page;
-      if (lp >= p.max_blocks) break;
-      const int phys = safe_page(p, bt[lp]);
-      const float v = Elem<KV>::load(kpool + kv_offset(p, phys, kv, tok % p.page) + dim);
-      mn = (v < mn) ? v : mn;
-      mx = (v > mx) ? v : mx;
-      sm = sm + v;
+    for (int i0 = 0; i0 < p.bs; i0 += kStatTokens) {
+#pragma unroll
+      for (int k = 0; k < kStatTokens; ++k) {
+        const int e = tid + k * NFA_BLOCK;  // [page slot][token][dim]
+        const int dd = e % DSUB;
+        const int ti = (e / DSUB) % kStatTokens;
+        const int ps = e / (DSUB * kStatTokens);
+        const int px = pg0 + ps;
+        const int tok = px * p.bs + i0 + ti;
+        const int lp = tok / p.page;
+        float v = 0.0f;
+        if (px < pg_hi && i0 + ti < p.bs && tok < L && lp < p.max_blocks) {
+          const int phys = safe_page(p, bt[lp]);
+          v = Elem<KV>::load(kpool + kv_offset(p, phys, kv, tok % p.page) +
+                             s_dims[dd]);
+        }
+        s_stage[e] = v;
+      }
+      __syncthreads();
+      if (pg < pg_hi) {
+        for (int ti = 0; ti < kStatTokens && i0 + ti < p.bs; ++ti) {
+          const int tok = pg * p.bs + i0 + ti;
+          if (tok >= L || tok / p.page >= p.max_blocks) break;
+          const float v = s_stage[(slot * kStatTokens + ti) * DSUB + d];
+          mn = (v < mn) ? v : mn;
+          mx = (v > mx) ? v : mx;
+          sm = sm + v;
+        }
+      }
+      __syncthreads();
     }
-    const int64_t si = stat_index<KV>(p, req, kv, d, pg, DSUB);
-    smin[si] = (KV)Elem<KV>::from_f32(mn);
-    smax[si] = (KV)Elem<KV>::from_f32(mx);
-    ssum[si] = (KV)Elem<KV>::from_f32(sm);
+    if (pg < pg_hi) {
+      const int64_t si = stat_index<KV>(p, req, kv, d, pg, DSUB);
+      smin[si] = (KV)Elem<KV>::from_f32(mn);
+      smax[si] = (KV)Elem<KV>::from_f32(mx);
+      ssum[si] = (KV)Elem<KV>::from_f32(sm);
+    }
+  }
+}
+
+// Vector form for L1 dims made of aligned 16-byte runs: one item = (page,
+// 16-byte chunk of dims); the chunk of 16 tokens is requested at once and
+// each dim is then scanned over the tokens in ascending order.  ``s_coff``
+// holds the element offset of every chunk, ``s_tphys`` (or NULL) the
+// physical page of every page of the range when a page never straddles two
+// physical pages.
+template <int DSUB, typename KV>
+__device__ void compute_stats_vec(const NfaSelectParams &p, int64_t req, int kv,
+                                  int L, int pg_lo, int pg_hi,
+                                  const int *s_coff, const int *s_tphys) {
+  constexpr int CH = Elem<KV>::kChunk;
+  constexpr int NCH1 = DSUB / CH;
+  constexpr int TG = 16;
+  const KV *kpool = (const KV *)p.k_pool_l;
+  const int32_t *bt = p.block_table_l + req * p.max_blocks;
+  KV *smin = (KV *)p.stat_min_l;
+  KV *smax = (KV *)p.stat_max_l;
+  KV *ssum = (KV *)p.stat_sum_l;
+  const int n_items = (pg_hi - pg_lo) * NCH1;
+  for (int it = threadIdx.x; it < n_items; it += NFA_BLOCK) {
+    const int pg = pg_lo + it / NCH1;
+    const int c = it % NCH1;
+    float mn[CH], mx[CH], sm[CH];
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+      mn[e] = __uint_as_float(0x7F800000u);
+      mx[e] = __uint_as_float(0xFF800000u);
+      sm[e] = 0.0f;
+    }
+    for (int i0 = 0; i0 < p.bs; i0 += TG) {
+      uint4 raw[TG];
+      bool ok[TG];
+#pragma unroll
+      for (int k = 0; k < TG; ++k) {
+        const int i = i0 + k;
+        const int tok = pg * p.bs + i;
+        const int lp = tok / p.page;
+        ok[k] = i < p.bs && tok < L && lp < p.max_blocks;
+        raw[k] = make_uint4(0u, 0u, 0u, 0u);
+        if (ok[k]) {
+          const int phys = s_tphys != nullptr ? s_tphys[pg - pg_lo]
+                                              : safe_page(p, bt[lp]);
+          raw[k] = *reinterpret_cast<const uint4 *>(
+              kpool + kv_offset(p, phys, kv, tok % p.page) + s_coff[c]);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < TG; ++k) {
+        if (!ok[k]) continue;
+        float x[CH];
+        load_chunk<KV>(reinterpret_cast<const KV *>(&raw[k]), x);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+          mn[e] = (x[e] < mn[e]) ? x[e] : mn[e];
+          mx[e] = (x[e] > mx[e]) ? x[e] : mx[e];
+          sm[e] = sm[e] + x[e];
+        }
+      }
+    }
+    const int64_t si = stat_index<KV>(p, req, kv, c * CH, pg, DSUB);
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+      smin[si + e] = (KV)Elem<KV>::from_f32(mn[e]);
+      smax[si + e] = (KV)Elem<KV>::from_f32(mx[e]);
+      ssum[si + e] = (KV)Elem<KV>::from_f32(sm[e]);
+    }
   }
 }
 
@@ -339,29 +459,72 @@ __device__ void tile_topk(uint32_t key, int t, int K, uint64_t *out,
 // ---------------------------------------------------------------------------
 
 __device__ int merge_l1(const uint64_t *part, int n, int K, int *out_pages,
-                        uint64_t *s_sel, int *hist, int *tmp) {
+                        uint64_t *s_sel, uint16_t *s_m16, int *hist,
+                        int *tmp) {
   const int tid = threadIdx.x;
   int *thr = tmp + 16;
-  topk_threshold16([&](int i) { return (uint32_t)(part[i] >> 32); }, n, K,
-                   hist, tmp, thr);
+  if (s_m16 != nullptr) {
+    // stage the 16-bit score keys, four loads in flight per thread
+    for (int i0 = tid; i0 < n; i0 += 4 * NFA_BLOCK) {
+      uint64_t k[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * NFA_BLOCK;
+        k[u] = i < n ? part[i] : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * NFA_BLOCK;
+        if (i < n) s_m16[i] = (uint16_t)(k[u] >> 32);
+      }
+    }
+    __syncthreads();
+    topk_threshold16([&](int i) { return (uint32_t)s_m16[i]; }, n, K, hist,
+                     tmp, thr);
+  } else {
+    topk_threshold16([&](int i) { return (uint32_t)(part[i] >> 32); }, n, K,
+                     hist, tmp, thr);
+  }
   const uint32_t T = (uint32_t)thr[0];
   const int need = thr[1];
   const int nvalid = thr[2] < K ? thr[2] : K;
   int carry_eq = 0, carry_sel = 0;
   for (int base = 0; base < n; base += NFA_BLOCK) {
     const int i = base + tid;
-    const uint64_t key = i < n ? part[i] : 0ull;
-    const uint32_t v = (uint32_t)(key >> 32);
+    uint32_t v = 0;
+    if (i < n) v = s_m16 != nullptr ? (uint32_t)s_m16[i] : (uint32_t)(part[i] >> 32);
     const bool eq = v != 0 && v == T;
     int tot_eq, tot_sel;
     const int r_eq = block_count_exclusive(eq, tmp, &tot_eq) + carry_eq;
     const bool sel = v > T || (eq && r_eq < need);
     const int pos = block_count_exclusive(sel, tmp, &tot_sel) + carry_sel;
-    if (sel && pos < K) s_sel[pos] = key;
+    if (sel && pos < K) ((int *)s_sel)[pos] = i;  // index now, key below
     carry_eq += tot_eq;
     carry_sel += tot_sel;
   }
   __syncthreads();
+  {
+    // fetch the selected keys: all loads in flight, no barrier in between
+    int idx[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int pos = tid + u * NFA_BLOCK;
+      idx[u] = pos < nvalid ? ((const int *)s_sel)[pos] : 0;
+    }
+    uint64_t key[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int pos = tid + u * NFA_BLOCK;
+      key[u] = pos < nvalid ? part[idx[u]] : 0ull;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int pos = tid + u * NFA_BLOCK;
+      if (pos < nvalid) s_sel[pos] = key[u];
+    }
+    __syncthreads();
+  }
   // order the selection by (score desc, page asc)
   for (int i = tid; i < nvalid; i += NFA_BLOCK) {
     const uint64_t ki = s_sel[i];
@@ -413,8 +576,10 @@ __device__ int merge_l1(const uint64_t *part, int n, int K, int *out_pages,
 }
 
 // ---------------------------------------------------------------------------
-// tail: one L2 region -- top-quota of the candidates in index range [ia, ib),
-// hole fill inside [rlo, rhi), sink filter; appended to s_mid at *mid_count.
+// tail: L2 logits of the candidate tokens (selector:459-516).  One token per
+// thread, the fp32 dot product runs over the L2 dims in order.  When the L2
+// dims form aligned 16-byte runs (tail, rope, nope, full) each token's keys
+// come in NCH vector loads with U tokens in flight per thread.
 // ---------------------------------------------------------------------------
 
 struct CandView {
@@ -423,13 +588,115 @@ struct CandView {
   int np_u;
   int tok_lo;         // first token of every page is max(page*bs, tok_lo)
   int bs;
-  __device__ __forceinline__ int token(int i) const {
-    const int pi = upper_bound_i32(pgoff, np_u + 1, i) - 1;
-    const int pg = pages[pi];
-    const int first = imax(pg * bs, tok_lo);
+  __device__ __forceinline__ int page_index(int i) const {
+    return upper_bound_i32(pgoff, np_u + 1, i) - 1;
+  }
+  __device__ __forceinline__ int token_at(int pi, int i) const {
+    const int first = pages[pi] * bs > tok_lo ? pages[pi] * bs : tok_lo;
     return first + (i - pgoff[pi]);
   }
+  __device__ __forceinline__ int token(int i) const {
+    return token_at(page_index(i), i);
+  }
 };
+
+template <typename KV>
+__device__ __forceinline__ uint16_t logit_key(const NfaSelectParams &p,
+                                              float acc, int row, int i,
+                                              int tok) {
+  const uint16_t bits = bf16_bits(acc);
+  if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
+    p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tok;
+    p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
+        bits == kNanBits ? kNegInfBits : bits;
+  }
+  return bits == kNanBits ? 0 : (uint16_t)score_key(bits);
+}
+
+template <typename KV, int NCH>
+__device__ void l2_logits_vec(const NfaSelectParams &p, const CandView &cv,
+                              int n_cand, int kv, int row, const int *s_pphys,
+                              const int *s_choff, const float *s_qg,
+                              uint16_t *s_cand) {
+  constexpr int CH = Elem<KV>::kChunk;
+  constexpr int U = NCH <= 4 ? 4 : (NCH <= 8 ? 2 : 1);
+  const KV *kpool = (const KV *)p.k_pool_l;
+  const int32_t *bt = p.block_table_l + p.valid_req[row / p.hkv] * p.max_blocks;
+  const bool page_phys = (p.page % p.bs) == 0;
+  for (int i0 = threadIdx.x; i0 < n_cand; i0 += U * NFA_BLOCK) {
+    uint4 raw[U][NCH];
+    int tok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * NFA_BLOCK;
+      tok[u] = 0;
+      if (i < n_cand) {
+        const int pi = cv.page_index(i);
+        tok[u] = cv.token_at(pi, i);
+        const int phys =
+            page_phys ? s_pphys[pi] : safe_page(p, bt[tok[u] / p.page]);
+        const KV *kr = kpool + kv_offset(p, phys, kv, tok[u] % p.page);
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          raw[u][c] = *reinterpret_cast<const uint4 *>(kr + s_choff[c]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * NFA_BLOCK;
+      if (i < n_cand) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          float x[CH];
+          load_chunk<KV>(reinterpret_cast<const KV *>(&raw[u][c]), x);
+#pragma unroll
+          for (int e = 0; e < CH; ++e) {
+            const float prod = x[e] * s_qg[c * CH + e];
+            acc = acc + prod;
+          }
+        }
+        s_cand[i] = logit_key<KV>(p, acc, row, i, tok[u]);
+      }
+    }
+  }
+}
+
+template <typename KV>
+__device__ void l2_logits_scalar(const NfaSelectParams &p, const CandView &cv,
+                                 int n_cand, int kv, int row,
+                                 const int *s_pphys, const int *s_fdims,
+                                 const float *s_qg, uint16_t *s_cand) {
+  const KV *kpool = (const KV *)p.k_pool_l;
+  const int32_t *bt = p.block_table_l + p.valid_req[row / p.hkv] * p.max_blocks;
+  const bool page_phys = (p.page % p.bs) == 0;
+  for (int i = threadIdx.x; i < n_cand; i += NFA_BLOCK) {
+    const int pi = cv.page_index(i);
+    const int tok = cv.token_at(pi, i);
+    const int phys = page_phys ? s_pphys[pi] : safe_page(p, bt[tok / p.page]);
+    const KV *kr = kpool + kv_offset(p, phys, kv, tok % p.page);
+    float acc = 0.0f;
+    for (int d0 = 0; d0 < p.fine_dsub; d0 += 8) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        x[e] = d0 + e < p.fine_dsub ? Elem<KV>::load(kr + s_fdims[d0 + e]) : 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (d0 + e < p.fine_dsub) {
+          const float prod = x[e] * s_qg[d0 + e];
+          acc = acc + prod;
+        }
+      }
+    }
+    s_cand[i] = logit_key<KV>(p, acc, row, i, tok);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// tail: one L2 region -- top-quota of the candidates in index range [ia, ib),
+// hole fill inside [rlo, rhi), sink filter; appended to s_mid at *mid_count.
+// ---------------------------------------------------------------------------
 
 __device__ void l2_region(const CandView &cv, const uint16_t *s_cand, int ia,
                           int ib, int rlo, int rhi, int quota, int sink,
@@ -602,15 +869,27 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 // the kernel
 // ---------------------------------------------------------------------------
 
+// Phase timestamp (debug timeline): completes the phase for the whole
+// workgroup, then thread 0 stores the wall clock.  Uniform condition.
+#define NFA_MARK(slot_base, k)                                        \
+  do {                                                                \
+    if (p.dbg_clock != nullptr) {                                     \
+      __syncthreads();                                                \
+      if (threadIdx.x == 0) p.dbg_clock[(slot_base) + (k)] = wall_clock64(); \
+    }                                                                 \
+  } while (0)
+
 template <int DSUB, typename KV>
 __global__ void __launch_bounds__(NFA_BLOCK)
     nfa_select_kernel(const NfaSelectParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   const SelDims sd = sel_dims(p);
-  float *s_qf = (float *)(smem + sd.o_qf);
   int *s_hist = (int *)(smem + sd.o_hist);
   int *s_tmp = (int *)(smem + sd.o_tmp);
+  float *s_qf = (float *)(smem + sd.o_qf);
   uint32_t *s_key = (uint32_t *)(smem + sd.o_key);
+  int *s_dims = (int *)(smem + sd.o_dims);
+  float *s_stage = (float *)(smem + sd.o_stage);
 
   const int tid = threadIdx.x;
   const int tile = blockIdx.x;
@@ -632,6 +911,9 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const bool owns_last = last_blk >= t0 && last_blk < t0 + NFA_BLOCK &&
                          last_blk < p.max_blocks;
 
+  const int64_t clk_tile = ((int64_t)row * (ntiles + 1) + tile) * 16;
+  const int64_t clk_tail = ((int64_t)row * (ntiles + 1) + ntiles) * 16;
+  NFA_MARK(clk_tile, 0);
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
   unsigned int *req_cnt = (unsigned int *)(ws + sd.w_reqcnt);
@@ -640,30 +922,62 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 
   // 1. decode write of the current token (selector:1030-1061)
   if (p.k_new != nullptr && active && owns_last) decode_write<KV>(p, b, kv);
+  for (int i = tid; i < DSUB; i += NFA_BLOCK) s_dims[i] = p.dims[i];
   __syncthreads();
 
+  NFA_MARK(clk_tile, 1);
   // 2. page statistics: latest page, or the whole tile on a rebuild
   const int prev = p.stats_len_l[req];
   const bool do_stats = active && L > 0 && !(skip_far && skip_near);
   const bool incremental = prev > 0 && L == prev + 1;
-  if (do_stats) {
-    if (incremental) {
-      if (owns_last) compute_stats<DSUB, KV>(p, req, kv, L, last_blk, last_blk + 1);
+  if (do_stats && (!incremental || owns_last)) {
+    const int pg_lo = incremental ? last_blk : t0;
+    const int pg_hi = incremental ? last_blk + 1 : imin(t0 + NFA_BLOCK, kt_eff);
+    // aligned 16-byte runs of L1 dims -> vector path
+    constexpr int CH = Elem<KV>::kChunk;
+    int *s_coff = (int *)s_stage;              // DSUB / CH chunk offsets
+    int *s_tphys = s_coff + 32;                // physical page per page
+    __shared__ int s_vec;
+    if (tid == 0) {
+      bool vec = true;
+      for (int c = 0; vec && c < DSUB / CH; ++c) {
+        const int first = s_dims[c * CH];
+        vec = (first % CH) == 0;
+        for (int e = 1; vec && e < CH; ++e) vec = s_dims[c * CH + e] == first + e;
+        s_coff[c] = first;
+      }
+      s_vec = vec;
+    }
+    const bool page_phys = (p.page % bs) == 0;
+    if (page_phys) {
+      const int32_t *btr = p.block_table_l + req * p.max_blocks;
+      for (int i = tid; i < pg_hi - pg_lo; i += NFA_BLOCK) {
+        const int lp = imin(((pg_lo + i) * bs) / p.page, p.max_blocks - 1);
+        s_tphys[i] = safe_page(p, btr[lp]);
+      }
+    }
+    __syncthreads();
+    if (s_vec) {
+      compute_stats_vec<DSUB, KV>(p, req, kv, L, pg_lo, pg_hi, s_coff,
+                                  page_phys ? s_tphys : nullptr);
     } else {
-      compute_stats<DSUB, KV>(p, req, kv, L, t0, imin(t0 + NFA_BLOCK, kt_eff));
+      __syncthreads();
+      compute_stats<DSUB, KV>(p, req, kv, L, pg_lo, pg_hi, s_stage, s_dims);
     }
   }
+  NFA_MARK(clk_tile, 2);
 
   // 3. scaled, bf16-rounded query rows of this kv group (selector:943-963)
   for (int i = tid; i < G * DSUB; i += NFA_BLOCK) {
     const int j = i / DSUB;
     const int d = i % DSUB;
     const int64_t qi = (int64_t)b * p.q_stride_b +
-                       (int64_t)(kv * G + j) * p.q_stride_h + p.dims[d];
+                       (int64_t)(kv * G + j) * p.q_stride_h + s_dims[d];
     const float qv = load_any(p.q, qi, p.q_dtype);
     s_qf[i] = bf16r(qv * p.scale);
   }
   __syncthreads();
+  NFA_MARK(clk_tile, 3);
 
   // 4. L1 scores, one page per thread
   const RowGeo geo = row_geo(p, L, skip_far, skip_near);
@@ -689,6 +1003,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     p.dbg_near[(int64_t)row * p.max_blocks + t] = near_bits;
   }
 
+  NFA_MARK(clk_tile, 4);
   // 5. exact top-k of this tile
   tile_topk(score_key(far_bits), t, p.k_f,
             part_far + ((int64_t)row * ntiles + tile) * p.k_f, s_key, s_hist,
@@ -697,6 +1012,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
             part_near + ((int64_t)row * ntiles + tile) * p.k_n, s_key, s_hist,
             s_tmp);
 
+  NFA_MARK(clk_tile, 5);
   // 6. arrival; the last workgroup of the row runs the tail
   __syncthreads();
   if (tid == 0) {
@@ -716,8 +1032,10 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   if (tid == 0) atomicExch(&row_cnt[row], 0u);
 
   // =========================== tail stage ================================
+  // (its LDS overlaps the tile stage's, which is no longer used)
   int *s_pages = (int *)(smem + sd.o_pages);
   int *s_pgoff = (int *)(smem + sd.o_pgoff);
+  int *s_pphys = (int *)(smem + sd.o_pphys);
   uint16_t *s_cand = (uint16_t *)(smem + sd.o_cand);
   int *s_l0 = (int *)(smem + sd.o_l0);
   int *s_l1 = (int *)(smem + sd.o_l1);
@@ -726,7 +1044,12 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   int *s_fp = (int *)(smem + sd.o_fp);
   int *s_np = (int *)(smem + sd.o_np);
   float *s_qg = (float *)(smem + sd.o_qg);
+  int *s_choff = (int *)(smem + sd.o_choff);
+  int *s_fdims = (int *)(smem + sd.o_fdims);
+  uint16_t *s_m16 = sd.merge_lds ? (uint16_t *)(smem + sd.o_union) : nullptr;
   __shared__ int s_misc[8];
+  __syncthreads();
+  NFA_MARK(clk_tail, 0);
 
   const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
   if (p.dbg_bounds != nullptr && kv == 0 && tid == 0) {
@@ -739,10 +1062,12 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   int nfv = 0, nnv = 0;
   if (p.k_f > 0)
     nfv = merge_l1(part_far + (int64_t)row * ntiles * p.k_f, ntiles * p.k_f,
-                   p.k_f, s_fp, s_sel, s_hist, s_tmp);
+                   p.k_f, s_fp, s_sel, s_m16, s_hist, s_tmp);
   if (p.k_n > 0)
     nnv = merge_l1(part_near + (int64_t)row * ntiles * p.k_n, ntiles * p.k_n,
-                   p.k_n, s_np, s_sel, s_hist, s_tmp);
+                   p.k_n, s_np, s_sel, s_m16, s_hist, s_tmp);
+  __syncthreads();
+  NFA_MARK(clk_tail, 1);
   if (p.dbg_i_f != nullptr) {
     for (int i = tid; i < p.k_f; i += NFA_BLOCK)
       p.dbg_i_f[(int64_t)row * p.k_f + i] = s_fp[i];
@@ -821,46 +1146,61 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   // pages that contribute no token keep offset == next offset; harmless
   __syncthreads();
 
+  NFA_MARK(clk_tail, 2);
+  // physical page of every candidate page (one lookup per page when a
+  // statistics block never straddles a physical page)
+  {
+    const int32_t *btr = p.block_table_l + req * p.max_blocks;
+    for (int i = tid; i < np_u; i += NFA_BLOCK) {
+      const int lp = imin((s_pages[i] * bs) / p.page, p.max_blocks - 1);
+      s_pphys[i] = safe_page(p, btr[lp]);
+    }
+  }
   // grouped query over the L2 dims (selector:979-1002)
   for (int d = tid; d < p.fine_dsub; d += NFA_BLOCK) {
+    const int dim = p.fine_dims[d];
+    s_fdims[d] = dim;
     float acc = 0.0f;
     for (int j = 0; j < G; ++j) {
       const int64_t qi = (int64_t)b * p.q_stride_b +
-                         (int64_t)(kv * G + j) * p.q_stride_h + p.fine_dims[d];
+                         (int64_t)(kv * G + j) * p.q_stride_h + dim;
       acc = acc + bf16r(load_any(p.q, qi, p.q_dtype) * p.scale);
     }
     s_qg[d] = acc;
   }
   __syncthreads();
-
-  // L2 logits (selector:459-516)
-  CandView cv{s_pages, s_pgoff, np_u, tok_lo, bs};
-  {
-    const KV *kpool = (const KV *)p.k_pool_l;
-    const int32_t *bt = p.block_table_l + req * p.max_blocks;
-    for (int i = tid; i < n_cand; i += NFA_BLOCK) {
-      const int tok = cv.token(i);
-      const int phys = safe_page(p, bt[tok / p.page]);
-      const KV *kr = kpool + kv_offset(p, phys, kv, tok % p.page);
-      float acc = 0.0f;
-      for (int d = 0; d < p.fine_dsub; ++d) {
-        const float x = Elem<KV>::load(kr + p.fine_dims[d]);
-        const float prod = x * s_qg[d];
-        acc = acc + prod;
-      }
-      const uint16_t bits = bf16_bits(acc);
-      s_cand[i] = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
-      if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
-        p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tok;
-        p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
-            bits == kNanBits ? kNegInfBits : bits;
-      }
+  // vector path when the L2 dims are aligned runs of 16 bytes
+  constexpr int CH = Elem<KV>::kChunk;
+  const int nch = p.fine_dsub / CH;
+  if (tid == 0) {
+    bool vec = (p.fine_dsub % CH == 0) && (nch == 4 || nch == 8 || nch == 16);
+    for (int c = 0; vec && c < nch; ++c) {
+      const int first = s_fdims[c * CH];
+      vec = (first % CH) == 0;
+      for (int e = 1; vec && e < CH; ++e) vec = s_fdims[c * CH + e] == first + e;
+      s_choff[c] = first;
     }
-    if (p.dbg_cand_count != nullptr && tid == 0)
-      p.dbg_cand_count[row] = n_cand;
+    s_misc[1] = vec;
   }
   __syncthreads();
 
+  NFA_MARK(clk_tail, 3);
+  // L2 logits (selector:459-516)
+  CandView cv{s_pages, s_pgoff, np_u, tok_lo, bs};
+  if (s_misc[1]) {
+    if (nch == 4)
+      l2_logits_vec<KV, 4>(p, cv, n_cand, kv, row, s_pphys, s_choff, s_qg, s_cand);
+    else if (nch == 8)
+      l2_logits_vec<KV, 8>(p, cv, n_cand, kv, row, s_pphys, s_choff, s_qg, s_cand);
+    else
+      l2_logits_vec<KV, 16>(p, cv, n_cand, kv, row, s_pphys, s_choff, s_qg, s_cand);
+  } else {
+    l2_logits_scalar<KV>(p, cv, n_cand, kv, row, s_pphys, s_fdims, s_qg, s_cand);
+  }
+  if (p.dbg_cand_count != nullptr && tid == 0) p.dbg_cand_count[row] = n_cand;
+  __syncthreads();
+
+  NFA_MARK(clk_tail, 4);
   // L2 top-quota + hole fill (+ fixed near quota), selector:519-566, 873-940
   if (tid == 0) s_misc[0] = 0;
   __syncthreads();
@@ -903,6 +1243,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     }
   }
   __syncthreads();
+  NFA_MARK(clk_tail, 5);
   int mcount = s_misc[0];
   if (mcount > p.k2) mcount = p.k2;
   if (p.dbg_middle != nullptr) {
@@ -915,7 +1256,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int32_t *bt = p.block_table_l + req * p.max_blocks;
   int32_t *grow = p.gather + ((int64_t)b * p.hkv + kv) * p.max_vis;
   auto phys_slot = [&](int id) {
-    return bt[id / p.page] * p.page + id % p.page;
+    return bt[imin(id / p.page, p.max_blocks - 1)] * p.page + id % p.page;
   };
   if (p.middle_only) {
     const int n = imin(mcount, p.max_vis);
@@ -930,7 +1271,8 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     return imax(0, imin(x, u1) - u0) + imax(0, imin(x, u3) - u2);
   };
   const int nu = (u1 - u0) + (u3 - u2);
-  // middle entries inside U are duplicates; the rest keep their order
+  // middle entries inside U are duplicates; the rest keep their order.
+  // Destinations first (barrier loop, LDS only), then one mapping pass.
   int carry = 0;
   for (int base = 0; base < mcount; base += NFA_BLOCK) {
     const int i = base + tid;
@@ -938,14 +1280,15 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     const bool keep = i < mcount && !in_u(x);
     int tot;
     const int r = block_count_exclusive(keep, s_tmp, &tot) + carry;
-    if (keep) {
-      const int dest = r + below_u(x);
-      if (dest < p.max_vis) grow[dest] = phys_slot(x);
-    }
+    if (i < mcount) s_l0[i] = keep ? r + below_u(x) : -1;
     carry += tot;
   }
   const int nkeep = carry;
   __syncthreads();
+  for (int i = tid; i < mcount; i += NFA_BLOCK) {
+    const int dest = s_l0[i];
+    if (dest >= 0 && dest < p.max_vis) grow[dest] = phys_slot(s_mid[i]);
+  }
   // kept-middle entries below x: lower_bound over s_mid minus duplicates
   auto kept_below = [&](int x) {
     const int lbx = lower_bound_i32(s_mid, mcount, x);
@@ -961,6 +1304,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     if (dest < p.max_vis) grow[dest] = phys_slot(x);
   }
   if (tid == 0) p.vis_lens[b * p.hkv + kv] = nkeep + nu;
+  NFA_MARK(clk_tail, 6);
 }
 
 }  // namespace nfa

@@ -78,6 +78,13 @@ extern "C" void nfa_set_error(const char *fmt, ...) {
 
 extern "C" const char *nfa_last_error(void) { return g_err; }
 extern "C" int32_t nfa_abi_version(void) { return NFA_ABI_VERSION; }
+extern "C" int32_t nfa_wall_clock_khz(void) {
+  int dev = 0, rate = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    return 0;
+  return rate;
+}
 extern "C" int32_t nfa_select_params_size(void) {
   return (int32_t)sizeof(NfaSelectParams);
 }

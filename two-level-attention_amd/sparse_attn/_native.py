@@ -58,6 +58,7 @@ class NfaSelectParams(ctypes.Structure):
         ('dbg_middle', _ptr), ('dbg_counts', _ptr), ('dbg_bounds', _ptr),
         ('dbg_cand_tok', _ptr), ('dbg_cand_logit', _ptr),
         ('dbg_cand_count', _ptr), ('dbg_cand_cap', _i64),
+        ('dbg_clock', _ptr),
     ]
 
 
@@ -77,7 +78,7 @@ class NfaAttnParams(ctypes.Structure):
 
 
 EXPORTS = (
-    'nfa_abi_version', 'nfa_select_params_size', 'nfa_attn_params_size',
+    'nfa_abi_version', 'nfa_wall_clock_khz', 'nfa_select_params_size', 'nfa_attn_params_size',
     'nfa_last_error', 'nfa_select_workspace_bytes', 'nfa_attn_workspace_bytes',
     'nfa_select_layer', 'nfa_sparse_attn_decode', 'nfa_paged_write_decode',
     'nfa_paged_write_prefill',
@@ -106,6 +107,7 @@ def load_library(path: str = None):
                 '(hipcc --offload-arch=gfx950)')
         lib = ctypes.CDLL(lib_path)
         lib.nfa_abi_version.restype = _i32
+        lib.nfa_wall_clock_khz.restype = _i32
         lib.nfa_select_params_size.restype = _i32
         lib.nfa_attn_params_size.restype = _i32
         lib.nfa_last_error.restype = ctypes.c_char_p

@@ -272,6 +272,9 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
     p.workspace = scratch.data_ptr()
     p.workspace_bytes = scratch.numel()
     if _debug is not None:
+        want_clock = _debug.get('want_clock', False)
+        _debug.clear()
+        _debug['want_clock'] = want_clock
         cand_cap = (k_f + k_n + 2) * bs
         _alloc_debug(_debug, b, hkv, cache.max_blocks, k_f, k_n, k2, cand_cap,
                      device)
@@ -287,6 +290,11 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
         p.dbg_cand_count = _debug['cand_count'].data_ptr()
         p.dbg_cand_cap = cand_cap
         _debug['region_mode'] = region_mode
+        if _debug.get('want_clock'):
+            ntiles = (cache.max_blocks + 255) // 256
+            _debug['clock'] = torch.zeros((b * hkv, ntiles + 1, 16),
+                                          dtype=torch.int64, device=device)
+            p.dbg_clock = _debug['clock'].data_ptr()
     rc = lib.nfa_select_layer(ctypes.byref(p), nat.stream_handle())
     if rc == -1 and 'LDS' in lib.nfa_last_error().decode():
         raise FallbackRequired(lib.nfa_last_error().decode())
