@@ -220,7 +220,7 @@ def selector_timeline(torch, w, steps, plan):
     for _ in range(steps):
         plan()
         for layer in range(len(w.q)):
-            dbg = {'want_clock': True}
+            dbg = {'clock_only': True}
             select_topk_for_layer_batched(
                 cache, layer, [0], w.q[layer], attention=w.attn[layer],
                 decode_write=(w.kn[layer], w.vn[layer],
@@ -236,19 +236,20 @@ def selector_timeline(torch, w, steps, plan):
         c = clk.cpu().numpy().astype(np.int64)
         tile, tail = c[:, :-1, :], c[:, -1, :]
         start = tile[:, :, 0][tile[:, :, 0] > 0].min()
-        ends = tail[:, 6]
-        acc.setdefault('kernel span', []).append((ends.max() - start) * us)
+        acc.setdefault('kernel span (A+B)', []).append((tail[:, 12].max() - start) * us)
         acc.setdefault('last tile arrives', []).append(
-            (tile[:, :, 5].max() - start) * us)
-        names = ['write+dims', 'page stats', 'q prep', 'L1 scores', 'tile top-k']
+            (tile[:, :, 4].max() - start) * us)
+        names = ['row scalars', 'q prep', 'page stats', 'L1 scores+publish']
         for k, name in enumerate(names):
             d = (tile[:, :, k + 1] - tile[:, :, k]) * us
-            acc.setdefault(f'tile {name} (max)', []).append(d.max())
-        tnames = ['L1 merge', 'cand pages', 'q grouped', 'L2 logits', 'L2 top-k',
-                  'union']
-        for k, name in enumerate(tnames):
-            d = (tail[:, k + 1] - tail[:, k]) * us
-            acc.setdefault(f'tail {name} (max)', []).append(d.max())
+            acc.setdefault(f'A tile {name} (max)', []).append(d.max())
+        spans = [('A tail L1 threshold', 0, 1), ('A tail cand pages', 1, 2),
+                 ('A end -> B start', 2, 8), ('B chunk0 L2 logits', 8, 9),
+                 ('B last arrival', 9, 10), ('B L2 top-k', 10, 11),
+                 ('B union', 11, 12)]
+        for name, a, b in spans:
+            d = (tail[:, b] - tail[:, a]) * us
+            acc.setdefault(f'{name} (max)', []).append(d.max())
     for name, vals in acc.items():
         print(f'# timeline {name:28s} median {np.median(vals):8.2f} us',
               file=sys.stderr, flush=True)

@@ -102,6 +102,9 @@ def run_and_compare(cache, indexer, req_ids, q, decode, *, scaling=1.0,
             nc = int(dbg['cand_count'][row_b, kv])
             tok = dbg['cand_tok'][row_b, kv, :nc].cpu().numpy()
             logit = _u16(dbg['cand_logit'][row_b, kv, :nc])
+            # dense page-major layout: slots outside the candidate range are -1
+            scored = tok >= 0
+            tok, logit = tok[scored], logit[scored]
             order = np.argsort(r.cand_tokens, kind='stable')
             np.testing.assert_array_equal(tok, r.cand_tokens[order], err_msg=tag)
             np.testing.assert_array_equal(logit, r.cand_logits[order].astype(np.int64),

@@ -4,41 +4,26 @@
 // sparse_attn/ops/paged_region_kernels.py:251-363 and :800-1006.
 //
 // Grid (nsplit, T * hkv), 256 threads.  Each workgroup owns one (query row,
-// kv head) and a contiguous chunk of the selected slots, handles the G query
-// heads of the group together (K/V rows are read once per group, not once per
-// query head), and writes an online-softmax partial (m, z, acc).  The last
-// workgroup of the (row, kv) to arrive -- device-scope atomic counter, no
-// waiting -- merges the partials and writes the output in the query dtype.
-// Selected rows are 256-byte K/V rows: each wave reads a whole row per
-// instruction (lane = 2 dims), the 4 waves stream different rows.
+// kv head) and a contiguous chunk of at most 64 selected slots, handles the
+// G query heads of the group together (K/V rows are read once per group),
+// and writes an online-softmax partial (m, z, acc).  The last workgroup of
+// the (row, kv) to arrive -- device-scope atomic counter, no waiting --
+// merges the partials and writes the output in the query dtype.
+//
+// Row layout: TPR threads share a K/V row, one 16-byte chunk each, so a pass
+// of the 256 threads covers 256 / TPR rows and every K and V chunk of the
+// split is requested before the first one is used.  Scores reduce over the
+// TPR threads with lane shuffles; V rows are staged in LDS and P.V runs with
+// one thread per (head, dim pair).  All loops are rolled or short: the code
+// a workgroup executes stays a few KB, so instruction fetch does not become
+// the latency of the launch.
 #include "nfa_common.h"
 
 namespace nfa {
 
-constexpr int AGMAX = 8;     // query heads per kv head
-constexpr int ADMAX = 256;   // head dim
-constexpr int kSplitMax = 64;                    // tokens per workgroup
-constexpr int kTpw = kSplitMax / NFA_WAVES;      // tokens per wave
-constexpr int kMaxSplits = 256;                  // splits merged in LDS
-
-// Two adjacent elements of a K/V row as one load.
-template <typename T> struct PairOf;
-template <> struct PairOf<uint16_t> {
-  using type = uint32_t;
-  static __device__ __forceinline__ type zero() { return 0u; }
-  static __device__ __forceinline__ void unpack(type v, float *a, float *b) {
-    *a = __uint_as_float(v << 16);
-    *b = __uint_as_float(v & 0xFFFF0000u);
-  }
-};
-template <> struct PairOf<float> {
-  using type = float2;
-  static __device__ __forceinline__ type zero() { return make_float2(0.f, 0.f); }
-  static __device__ __forceinline__ void unpack(type v, float *a, float *b) {
-    *a = v.x;
-    *b = v.y;
-  }
-};
+constexpr int AGMAX = 8;         // query heads per kv head
+constexpr int kSplitMax = 64;    // tokens per workgroup
+constexpr int kMaxSplits = 256;  // splits merged in LDS
 
 struct AttnDims {
   int split;    // tokens per split
@@ -52,7 +37,7 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p) {
   AttnDims a;
   a.rows = p.total_q * p.hkv;
   int split = p.tokens_per_split;
-  if (split <= 0) split = a.rows <= 16 ? 32 : 64;
+  if (split <= 0) split = 32;
   a.split = split;
   a.nsplit = (p.max_vis + split - 1) / split;
   if (a.nsplit < 1) a.nsplit = 1;
@@ -65,9 +50,27 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p) {
   return a;
 }
 
-template <typename KV>
+// Two adjacent KV elements of an LDS row as floats.
+__device__ __forceinline__ void lds_pair(const uint16_t *v, int d, float *a,
+                                         float *b) {
+  const uint32_t x = *reinterpret_cast<const uint32_t *>(v + d);
+  *a = __uint_as_float(x << 16);
+  *b = __uint_as_float(x & 0xFFFF0000u);
+}
+__device__ __forceinline__ void lds_pair(const float *v, int d, float *a,
+                                         float *b) {
+  const float2 x = *reinterpret_cast<const float2 *>(v + d);
+  *a = x.x;
+  *b = x.y;
+}
+
+template <typename KV, int TPR>
 __global__ void __launch_bounds__(NFA_BLOCK)
     nfa_attn_kernel(const NfaAttnParams p) {
+  constexpr int CH = Elem<KV>::kChunk;  // dims per 16-byte chunk
+  constexpr int D = TPR * CH;           // head dim (K and V)
+  constexpr int RPP = NFA_BLOCK / TPR;  // rows per pass
+  constexpr int PMAX = kSplitMax / RPP; // passes per split
   const AttnDims ad = attn_dims(p);
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -77,13 +80,12 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int t = row / p.hkv;
   const int kh = row % p.hkv;
   const int G = p.hq / p.hkv;
-  const int D = p.head_dim;
-  const int DV = p.head_dim_v;
+  const float kNegInf = __uint_as_float(0xFF800000u);
 
-  __shared__ float s_q[AGMAX * ADMAX];
-  __shared__ float s_p[AGMAX * kSplitMax];    // probabilities [G][split]
+  __shared__ __align__(16) float s_q[AGMAX * D];
+  __shared__ float s_p[AGMAX * kSplitMax];  // scores, then exp weights
   __shared__ int s_slot[kSplitMax];
-  __shared__ float s_red[NFA_WAVES * AGMAX * ADMAX];
+  __shared__ __align__(16) KV s_v[kSplitMax * D];
   __shared__ float s_m[AGMAX], s_z[AGMAX];
   __shared__ int s_last;
 
@@ -105,11 +107,8 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int cn = c1 > c0 ? c1 - c0 : 0;
 
   if (cn > 0) {
-    for (int i = tid; i < G * D; i += NFA_BLOCK) {
-      const int g = i / D, d = i % D;
-      s_q[g * ADMAX + d] =
-          load_any(p.q, ((int64_t)t * p.hq + kh * G + g) * D + d, p.q_dtype);
-    }
+    for (int i = tid; i < G * D; i += NFA_BLOCK)
+      s_q[i] = load_any(p.q, ((int64_t)t * p.hq + kh * G) * D + i, p.q_dtype);
     const int32_t *grow = p.gather + ((int64_t)req * p.hkv + kh) * p.max_vis;
     // slots outside the arena are skipped like negative ones
     const int max_slot = p.pool_pages * p.page;
@@ -120,76 +119,64 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   __syncthreads();
 
+  // every K and V chunk of the split in flight at once
+  const int sc = tid % TPR;  // chunk of the row
+  const int rr = tid / TPR;  // row within a pass
   const KV *kpool = (const KV *)p.k_pool;
   const KV *vpool = (const KV *)p.v_pool;
-  // Raw row pieces: lane holds dims 2*lane + 128*h (h < 2); every row this
-  // wave needs is requested before the first one is used.
-  using Pair = typename PairOf<KV>::type;
-  constexpr int H = ADMAX / 128;
-  // scores: wave w takes tokens w, w+4, ... (at most kTpw of them)
-  Pair kraw[kTpw][H];
+  uint4 kr[PMAX], vr[PMAX];
 #pragma unroll
-  for (int t = 0; t < kTpw; ++t) {
-    const int i = w + t * NFA_WAVES;
-    const int slot = i < cn ? s_slot[i] : -1;
-#pragma unroll
-    for (int h = 0; h < H; ++h) {
-      kraw[t][h] = PairOf<KV>::zero();
-      const int d = 2 * lane + 128 * h;
-      if (slot >= 0 && d < D) {
-        const int phys = slot / p.page, off = slot % p.page;
-        kraw[t][h] = *reinterpret_cast<const Pair *>(
-            kpool + (((int64_t)phys * p.hkv + kh) * p.page + off) * D + d);
-      }
+  for (int pp = 0; pp < PMAX; ++pp) {
+    const int j = pp * RPP + rr;
+    const int slot = j < cn ? s_slot[j] : -1;
+    kr[pp] = make_uint4(0u, 0u, 0u, 0u);
+    vr[pp] = make_uint4(0u, 0u, 0u, 0u);
+    if (slot >= 0) {
+      const int64_t base =
+          (((int64_t)(slot / p.page) * p.hkv + kh) * p.page + slot % p.page) * D +
+          sc * CH;
+      kr[pp] = *reinterpret_cast<const uint4 *>(kpool + base);
+      vr[pp] = *reinterpret_cast<const uint4 *>(vpool + base);
     }
   }
+  // scores: partial dot over the chunk, then a shuffle reduction over the
+  // TPR threads of the row
 #pragma unroll
-  for (int t = 0; t < kTpw; ++t) {
-    const int i = w + t * NFA_WAVES;
-    if (i >= cn) break;
-    const int slot = s_slot[i];
-    float part_s[AGMAX];
+  for (int pp = 0; pp < PMAX; ++pp) {
+    if (pp * RPP >= cn) break;
+    const int j = pp * RPP + rr;
+    float x[CH];
+    unpack_chunk<KV>(kr[pp], x);
+    for (int g = 0; g < G; ++g) {
+      const float *q = s_q + g * D + sc * CH;
+      float part_s = 0.0f;
 #pragma unroll
-    for (int g = 0; g < AGMAX; ++g) part_s[g] = 0.0f;
+      for (int e = 0; e < CH; ++e) part_s = fmaf(q[e], x[e], part_s);
 #pragma unroll
-    for (int h = 0; h < H; ++h) {
-      const int d = 2 * lane + 128 * h;
-      if (d < D) {
-        float k0, k1;
-        PairOf<KV>::unpack(kraw[t][h], &k0, &k1);
-#pragma unroll
-        for (int g = 0; g < AGMAX; ++g) {
-          if (g < G) {
-            part_s[g] = fmaf(s_q[g * ADMAX + d], k0, part_s[g]);
-            part_s[g] = fmaf(s_q[g * ADMAX + d + 1], k1, part_s[g]);
-          }
-        }
-      }
+      for (int off = 1; off < TPR; off <<= 1)
+        part_s += __shfl_xor(part_s, off, 64);
+      if (sc == 0 && j < cn)
+        s_p[g * kSplitMax + j] = s_slot[j] >= 0 ? part_s * p.scale : kNegInf;
     }
+  }
+  // stage V rows for P.V
 #pragma unroll
-    for (int g = 0; g < AGMAX; ++g) {
-      if (g < G) {
-        float x = part_s[g];
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
-        if (lane == 0)
-          s_p[g * kSplitMax + i] =
-              slot >= 0 ? x * p.scale : __uint_as_float(0xFF800000u);
-      }
-    }
+  for (int pp = 0; pp < PMAX; ++pp) {
+    const int j = pp * RPP + rr;
+    if (j < cn) *reinterpret_cast<uint4 *>(s_v + j * D + sc * CH) = vr[pp];
   }
   __syncthreads();
 
   // softmax partial per head (one wave per head)
   for (int g = w; g < G; g += NFA_WAVES) {
-    float m = __uint_as_float(0xFF800000u);
+    float m = kNegInf;
     for (int i = lane; i < cn; i += 64) m = fmaxf(m, s_p[g * kSplitMax + i]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     float z = 0.0f;
     for (int i = lane; i < cn; i += 64) {
-      const float sc = s_p[g * kSplitMax + i];
-      const float e = (m == __uint_as_float(0xFF800000u)) ? 0.0f : __expf(sc - m);
+      const float sc2 = s_p[g * kSplitMax + i];
+      const float e = (m == kNegInf) ? 0.0f : __expf(sc2 - m);
       s_p[g * kSplitMax + i] = e;
       z += e;
     }
@@ -202,129 +189,59 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   __syncthreads();
 
-  // P V with the same token assignment; V rows requested up front
-  Pair vraw[kTpw][H];
-#pragma unroll
-  for (int t = 0; t < kTpw; ++t) {
-    const int i = w + t * NFA_WAVES;
-    const int slot = i < cn ? s_slot[i] : -1;
-#pragma unroll
-    for (int h = 0; h < H; ++h) {
-      vraw[t][h] = PairOf<KV>::zero();
-      const int d = 2 * lane + 128 * h;
-      if (slot >= 0 && d < DV) {
-        const int phys = slot / p.page, off = slot % p.page;
-        vraw[t][h] = *reinterpret_cast<const Pair *>(
-            vpool + (((int64_t)phys * p.hkv + kh) * p.page + off) * DV + d);
-      }
+  // P.V, one thread per (head, dim pair)
+  for (int o = tid; o < G * (D / 2); o += NFA_BLOCK) {
+    const int g = o / (D / 2);
+    const int d = 2 * (o % (D / 2));
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 4
+    for (int j = 0; j < cn; ++j) {
+      const float pr = s_p[g * kSplitMax + j];
+      float v0, v1;
+      lds_pair(s_v + j * D, d, &v0, &v1);
+      a0 = fmaf(pr, v0, a0);
+      a1 = fmaf(pr, v1, a1);
     }
-  }
-  float acc[AGMAX][H * 2];
-#pragma unroll
-  for (int g = 0; g < AGMAX; ++g)
-#pragma unroll
-    for (int e = 0; e < H * 2; ++e) acc[g][e] = 0.0f;
-#pragma unroll
-  for (int t = 0; t < kTpw; ++t) {
-    const int i = w + t * NFA_WAVES;
-    if (i >= cn) break;
-    if (s_slot[i] < 0) continue;
-#pragma unroll
-    for (int h = 0; h < H; ++h) {
-      const int d = 2 * lane + 128 * h;
-      if (d < DV) {
-        float v0, v1;
-        PairOf<KV>::unpack(vraw[t][h], &v0, &v1);
-#pragma unroll
-        for (int g = 0; g < AGMAX; ++g) {
-          if (g < G) {
-            const float pr = s_p[g * kSplitMax + i];
-            acc[g][2 * h] = fmaf(pr, v0, acc[g][2 * h]);
-            acc[g][2 * h + 1] = fmaf(pr, v1, acc[g][2 * h + 1]);
-          }
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < AGMAX; ++g) {
-    if (g < G) {
-#pragma unroll
-      for (int k = 0; k < ADMAX / 128; ++k) {
-        const int d = 2 * lane + 128 * k;
-        if (d < DV) {
-          s_red[(w * AGMAX + g) * ADMAX + d] = acc[g][2 * k];
-          s_red[(w * AGMAX + g) * ADMAX + d + 1] = acc[g][2 * k + 1];
-        }
-      }
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < G * DV; i += NFA_BLOCK) {
-    const int g = i / DV, d = i % DV;
-    float s = 0.0f;
-#pragma unroll
-    for (int ww = 0; ww < NFA_WAVES; ++ww) s += s_red[(ww * AGMAX + g) * ADMAX + d];
-    part[g * (DV + 2) + 2 + d] = s;
+    part[g * (D + 2) + 2 + d] = a0;
+    part[g * (D + 2) + 3 + d] = a1;
   }
   if (tid < G) {
-    part[tid * (DV + 2) + 0] = cn > 0 ? s_m[tid] : __uint_as_float(0xFF800000u);
-    part[tid * (DV + 2) + 1] = cn > 0 ? s_z[tid] : 0.0f;
+    part[tid * (D + 2) + 0] = cn > 0 ? s_m[tid] : kNegInf;
+    part[tid * (D + 2) + 1] = cn > 0 ? s_z[tid] : 0.0f;
   }
 
   // arrival; the last split of the (row, kv) merges
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    const unsigned int before = atomicAdd(&cnt[row], 1u);
-    s_last = before == (unsigned int)(ad.nsplit - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  if (tid == 0) atomicExch(&cnt[row], 0u);
+  if (!arrive_last(&cnt[row], (unsigned int)ad.nsplit, &s_last)) return;
 
   const float *base = (const float *)(ws + ad.w_part) +
                       (int64_t)row * ad.nsplit * ad.part_stride;
   // split maxima and denominators -> LDS (one round of loads)
-  float *s_ms = s_red;                         // [G][kMaxSplits]
-  float *s_zs = s_red + AGMAX * kMaxSplits;    // [G][kMaxSplits]
+  float *s_ms = reinterpret_cast<float *>(s_v);  // [G][kMaxSplits]
+  float *s_zs = s_ms + AGMAX * kMaxSplits;        // [G][kMaxSplits]
   for (int i = tid; i < G * ad.nsplit; i += NFA_BLOCK) {
     const int g = i / ad.nsplit, sp = i % ad.nsplit;
-    const float *ps = base + (int64_t)sp * ad.part_stride + g * (DV + 2);
+    const float *ps = base + (int64_t)sp * ad.part_stride + g * (D + 2);
     s_ms[g * kMaxSplits + sp] = ps[0];
     s_zs[g * kMaxSplits + sp] = ps[1];
   }
   __syncthreads();
-  for (int i = tid; i < G * DV; i += NFA_BLOCK) {
-    const int g = i / DV, d = i % DV;
-    float M = __uint_as_float(0xFF800000u);
+  for (int i = tid; i < G * D; i += NFA_BLOCK) {
+    const int g = i / D, d = i % D;
+    float M = kNegInf;
     for (int sp = 0; sp < ad.nsplit; ++sp) M = fmaxf(M, s_ms[g * kMaxSplits + sp]);
     float Z = 0.0f, O = 0.0f;
-    if (M != __uint_as_float(0xFF800000u)) {
-      for (int s0 = 0; s0 < ad.nsplit; s0 += 8) {
-        float a[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int sp = s0 + u;
-          a[u] = sp < ad.nsplit
-                     ? base[(int64_t)sp * ad.part_stride + g * (DV + 2) + 2 + d]
-                     : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int sp = s0 + u;
-          if (sp >= ad.nsplit) break;
-          const float ms = s_ms[g * kMaxSplits + sp];
-          if (ms == __uint_as_float(0xFF800000u)) continue;
-          const float f = __expf(ms - M);
-          Z += s_zs[g * kMaxSplits + sp] * f;
-          O += a[u] * f;
-        }
+    if (M != kNegInf) {
+#pragma unroll 8
+      for (int sp = 0; sp < ad.nsplit; ++sp) {
+        const float ms = s_ms[g * kMaxSplits + sp];
+        const float a = base[(int64_t)sp * ad.part_stride + g * (D + 2) + 2 + d];
+        const float f = ms == kNegInf ? 0.0f : __expf(ms - M);
+        Z += s_zs[g * kMaxSplits + sp] * f;
+        O += a * f;
       }
     }
     const float o = Z == 0.0f ? 0.0f : O / Z;
-    const int64_t oi = ((int64_t)t * p.hq + kh * G + g) * DV + d;
+    const int64_t oi = ((int64_t)t * p.hq + kh * G + g) * D + d;
     if (p.q_dtype == NFA_DTYPE_BF16)
       ((uint16_t *)p.out)[oi] = bf16_bits(o);
     else
@@ -351,10 +268,17 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
                   p->hq, p->hkv);
     return NFA_EINVAL;
   }
-  if (p->head_dim <= 0 || p->head_dim > nfa::ADMAX || (p->head_dim & 1) ||
-      p->head_dim_v <= 0 || p->head_dim_v > nfa::ADMAX || (p->head_dim_v & 1)) {
-    nfa_set_error("nfa_sparse_attn_decode: unsupported head dims %d/%d",
+  const int chunk = p->kv_dtype == NFA_DTYPE_BF16 ? 8 : 4;
+  const int tpr = p->head_dim / chunk;
+  if (p->head_dim != p->head_dim_v || p->head_dim % chunk != 0 ||
+      !(tpr == 8 || tpr == 16 || tpr == 32)) {
+    nfa_set_error("nfa_sparse_attn_decode: unsupported head dims %d/%d "
+                  "(K and V dims must match and span 8, 16 or 32 chunks of 16 bytes)",
                   p->head_dim, p->head_dim_v);
+    return NFA_EINVAL;
+  }
+  if (p->kv_dtype != NFA_DTYPE_BF16 && p->kv_dtype != NFA_DTYPE_F32) {
+    nfa_set_error("nfa_sparse_attn_decode: unsupported kv dtype %d", p->kv_dtype);
     return NFA_EINVAL;
   }
   if (p->max_vis <= 0 || p->page <= 0 || p->pool_pages <= 0 ||
@@ -384,10 +308,17 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
   }
   dim3 grid(ad.nsplit, ad.rows);
   hipStream_t s = (hipStream_t)stream;
-  if (p->kv_dtype == NFA_DTYPE_BF16)
-    hipLaunchKernelGGL(nfa::nfa_attn_kernel<uint16_t>, grid, dim3(NFA_BLOCK), 0, s, *p);
-  else
-    hipLaunchKernelGGL(nfa::nfa_attn_kernel<float>, grid, dim3(NFA_BLOCK), 0, s, *p);
+  const bool bf = p->kv_dtype == NFA_DTYPE_BF16;
+#define NFA_ATTN_LAUNCH(KV, TPR) \
+  hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR>), grid, dim3(NFA_BLOCK), 0, s, *p)
+  if (tpr == 8) {
+    if (bf) NFA_ATTN_LAUNCH(uint16_t, 8); else NFA_ATTN_LAUNCH(float, 8);
+  } else if (tpr == 16) {
+    if (bf) NFA_ATTN_LAUNCH(uint16_t, 16); else NFA_ATTN_LAUNCH(float, 16);
+  } else {
+    if (bf) NFA_ATTN_LAUNCH(uint16_t, 32); else NFA_ATTN_LAUNCH(float, 32);
+  }
+#undef NFA_ATTN_LAUNCH
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     nfa_set_error("nfa_sparse_attn_decode: launch failed: %s", hipGetErrorString(err));

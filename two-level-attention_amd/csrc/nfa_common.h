@@ -95,35 +95,49 @@ __device__ __forceinline__ void load_chunk(const T *p, float *out) {
   }
 }
 
+// 16 bytes of KV elements (already in registers) as floats.
+template <typename KV>
+__device__ __forceinline__ void unpack_chunk(const uint4 &raw, float *out) {
+  load_chunk<KV>(reinterpret_cast<const KV *>(&raw), out);
+}
+
+// ---------------------------------------------------------------------------
+// cross-workgroup publication ("last arriving workgroup" pattern)
+// ---------------------------------------------------------------------------
+
+// Every wave completes its own global stores, the workgroup meets at a
+// barrier, then one wave makes them visible device-wide (one agent-scope
+// release for the whole workgroup, not one per wave) and takes a ticket from
+// the device-scope counter.  Returns true in every thread of the workgroup
+// that arrives last of `n`; that workgroup has acquired (one agent-scope
+// acquire, then a barrier) and resets the counter, so no memset is needed
+// between launches.  `s_flag` is one int of LDS.
+__device__ __forceinline__ bool arrive_last(unsigned int *counter,
+                                            unsigned int n, int *s_flag) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const unsigned int before =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = before == n - 1;
+    if (last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *s_flag = last;
+  }
+  __syncthreads();
+  return *s_flag != 0;
+}
+
 // ---------------------------------------------------------------------------
 // block-level (256 threads) scans and reductions
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
-
-// Exclusive count of `pred` over the block in thread order; *total receives
-// the block total.  `scratch` needs NFA_WAVES ints.  Contains two barriers.
-__device__ __forceinline__ int block_count_exclusive(bool pred, int *scratch,
-                                                     int *total) {
-  const unsigned long long mask = __ballot(pred);
-  const int lane = lane_id();
-  const int w = wave_id();
-  const unsigned long long below = lane ? (mask & ((1ull << lane) - 1ull)) : 0ull;
-  const int in_wave = __popcll(below);
-  if (lane == 0) scratch[w] = __popcll(mask);
-  __syncthreads();
-  int before = 0, sum = 0;
-#pragma unroll
-  for (int i = 0; i < NFA_WAVES; ++i) {
-    const int c = scratch[i];
-    if (i < w) before += c;
-    sum += c;
-  }
-  __syncthreads();
-  *total = sum;
-  return before + in_wave;
-}
 
 // Exclusive prefix sum of an int over the block; two barriers.
 __device__ __forceinline__ int block_scan_exclusive(int v, int *scratch,
@@ -150,26 +164,72 @@ __device__ __forceinline__ int block_scan_exclusive(int v, int *scratch,
   return before + x - v;
 }
 
-// Given a 256-bin histogram in LDS and K >= 1, find the bin b with
-// above(b) < K <= above(b) + hist[b], where above(b) counts entries in bins
-// greater than b.  Executed by wave 0; results land in out[0] (bin) and
-// out[1] (above).  Requires K <= total count.  Caller syncs afterwards.
-__device__ __forceinline__ void find_threshold_bin(const int *hist, int K,
+// Exclusive prefix sums of N ints at once (one pair of barriers for all N);
+// v is replaced by its exclusive prefix, total receives the block totals.
+// `scratch` needs NFA_WAVES * N ints.
+template <int N>
+__device__ __forceinline__ void block_scan_n(int (&v)[N], int *scratch,
+                                             int (&total)[N]) {
+  const int lane = lane_id();
+  const int w = wave_id();
+  int x[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) x[k] = v[k];
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      const int y = __shfl_up(x[k], off, 64);
+      if (lane >= off) x[k] += y;
+    }
+  }
+  if (lane == 63) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) scratch[w * N + k] = x[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    int before = 0, sum = 0;
+#pragma unroll
+    for (int i = 0; i < NFA_WAVES; ++i) {
+      const int c = scratch[i * N + k];
+      if (i < w) before += c;
+      sum += c;
+    }
+    total[k] = sum;
+    v[k] = before + x[k] - v[k];
+  }
+  __syncthreads();
+}
+
+// One wave: threshold bin of the top-K over a 256-bin histogram (bin = high
+// byte of a 16-bit key, higher is better).  out[0] = bin b with
+// above(b) < K <= above(b) + hist[b], or -1 when every counted entry fits
+// (total <= K, or K <= 0); out[1] = above(b); out[2] = total.  Must be
+// called by all 64 lanes of one wave.
+__device__ __forceinline__ void wave_threshold_bin(const int *hist, int K,
                                                    int *out) {
-  if (wave_id() != 0) return;
   const int lane = lane_id();
   const int h0 = hist[4 * lane + 0], h1 = hist[4 * lane + 1];
   const int h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
   const int s = h0 + h1 + h2 + h3;
-  // inclusive suffix sum over lanes (lane l sums lanes l..63)
   int x = s;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const int y = __shfl_down(x, off, 64);
     if (lane + off < 64) x += y;
   }
-  int above = x - s;  // entries in lanes > lane
-  // bins in descending order within the lane: 3, 2, 1, 0
+  const int total = __shfl(x, 0, 64);
+  if (total <= K || K <= 0) {
+    if (lane == 0) {
+      out[0] = -1;
+      out[1] = 0;
+      out[2] = total;
+    }
+    return;
+  }
+  int above = x - s;
   const int hb[4] = {h3, h2, h1, h0};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -179,73 +239,7 @@ __device__ __forceinline__ void find_threshold_bin(const int *hist, int K,
     }
     above += hb[i];
   }
-}
-
-// Threshold of the top-K among `n` 16-bit keys (0 = invalid) supplied by
-// `get(i)`.  Returns via out: out[0] = threshold key T, out[1] = number of
-// entries equal to T that are selected (the lowest-index ones), out[2] =
-// number of valid entries.  If valid <= K every valid entry is selected and
-// out[0] = 1, out[1] = large.  `hist` needs 256 ints, `tmp` 8 ints.
-template <typename Get>
-__device__ void topk_threshold16(Get get, int n, int K, int *hist, int *tmp,
-                                 int *out) {
-  const int tid = threadIdx.x;
-  for (int i = tid; i < 256; i += NFA_BLOCK) hist[i] = 0;
-  __syncthreads();
-  int local_valid = 0;
-  for (int i = tid; i < n; i += NFA_BLOCK) {
-    const uint32_t v = get(i);
-    if (v) {
-      atomicAdd(&hist[v >> 8], 1);
-      ++local_valid;
-    }
-  }
-  int total_valid;
-  block_scan_exclusive(local_valid, tmp, &total_valid);
-  if (total_valid <= K) {
-    if (tid == 0) {
-      out[0] = 1;
-      out[1] = 1 << 30;
-      out[2] = total_valid;
-    }
-    __syncthreads();
-    return;
-  }
-  find_threshold_bin(hist, K, tmp + 4);
-  __syncthreads();
-  const int hb = tmp[4];
-  const int above_hb = tmp[5];
-  __syncthreads();
-  for (int i = tid; i < 256; i += NFA_BLOCK) hist[i] = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += NFA_BLOCK) {
-    const uint32_t v = get(i);
-    if (v && (int)(v >> 8) == hb) atomicAdd(&hist[v & 255u], 1);
-  }
-  __syncthreads();
-  find_threshold_bin(hist, K - above_hb, tmp + 4);
-  __syncthreads();
-  if (tid == 0) {
-    const int lb = tmp[4];
-    const int above_lb = tmp[5];
-    out[0] = (hb << 8) | lb;
-    out[1] = K - above_hb - above_lb;
-    out[2] = total_valid;
-  }
-  __syncthreads();
-}
-
-// Upper bound: first index in sorted a[0..n) with a[idx] > x.
-__device__ __forceinline__ int upper_bound_i32(const int *a, int n, int x) {
-  int lo = 0, hi = n;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (a[mid] <= x)
-      lo = mid + 1;
-    else
-      hi = mid;
-  }
-  return lo;
+  if (lane == 0) out[2] = total;
 }
 
 // Lower bound: first index with a[idx] >= x.

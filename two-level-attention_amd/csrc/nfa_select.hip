@@ -1,24 +1,38 @@
-// NFA two-level selector for one decode layer on gfx950.
+// NFA two-level selector for one decode layer on gfx950: two launches.
 //
-// One launch, grid (ntiles, batch * hkv), 256 threads per workgroup:
-//
+// Kernel A, grid (ntiles, batch * hkv), 256 threads per workgroup:
 //   tile stage (every workgroup, 256 pages = one page per thread):
-//     decode K/V write of the current token (owner of the last page),
-//     page min/max/sum statistics (latest page, or every page of the tile on
-//     a rebuild), L1 far/near page scores, and the exact top-K_F / top-K_N
-//     of the tile written to scratch in page order.
-//   tail stage (the last workgroup of each (row, kv) to arrive, found with a
+//     decode K/V write of the current token (owner of the last page), page
+//     min/max/sum statistics (the latest page, or every page of the tile on
+//     a rebuild), L1 far/near page scores.  One 16-bit score key per page
+//     (far and near pools are disjoint page ranges) goes to the workspace,
+//     the high bytes of the keys into a per-row, per-pool histogram (one
+//     global atomic per non-empty bin and workgroup).
+//   tail (the last workgroup of each (row, kv) to arrive, found with a
 //     device-scope atomic counter; no workgroup ever waits on another):
-//     merge of the tile top-k lists into I_F / I_N, candidate pages, L2
-//     logits over the L2 dims, top-quota selection with lowest-token
-//     tie-break, hole fill, sink/SWA union and the physical gather rows.
+//     exact top-K_F / top-K_N thresholds from the histogram plus one
+//     refinement pass over the keys staged in LDS, the selected pages and
+//     the sink/SWA bypass pages as an LDS bitmap (sorted and de-duplicated
+//     by construction), compacted into the candidate page list with its
+//     physical pages.
+// Kernel B, grid (ceil(dense slots / 64), batch * hkv), 256 threads:
+//     L2 logits of the candidate tokens in a dense page-major layout, 64
+//     tokens per workgroup and 4 threads per token; the last workgroup of the
+//     row to arrive runs the top-quota selection with the lowest-token
+//     tie-break, hole fill, the sink/SWA union and the physical gather rows.
+//
+// Every loop a workgroup executes on the steady decode path is rolled or
+// short: the code of a phase is fetched cold by nearly every workgroup, so
+// executed code size is latency.
 //
 // Reference semantics: sparse_attn/indexer/nfa_layer_batch_selector.py
 // (selector:32-131 stats, :175-354 L1, :1473-1863 L1 top-k, :1081-1251
 // candidates/owners, :423-516 L2 logits, :519-848 L2 top-k, :873-940 fixed
 // quota, :1337-1470 union).  Owner tags of the reference reduce to "each
-// candidate token is scored once", which the sorted, de-duplicated candidate
-// page list gives directly.
+// candidate token is scored once", which the candidate page bitmap gives
+// directly.  Only pages with a finite L1 score become candidates
+// (selector:1195-1251); the -inf fillers of I_F / I_N matter for the debug
+// outputs only.
 #include "nfa_common.h"
 
 #include <stdarg.h>
@@ -27,81 +41,113 @@
 namespace nfa {
 
 // ---------------------------------------------------------------------------
-// scratch layouts (shared by host and device)
+// LDS and workspace layouts (shared by host and device)
 // ---------------------------------------------------------------------------
 
+constexpr int kL2Slots = 64;     // dense candidate slots per kernel-B workgroup
+constexpr int kStatTokens = 16;  // tokens per staging round of the stats pass
+
 struct SelDims {
-  int ntiles;      // L1 tiles per row
-  int np;          // candidate page slots = k_f + k_n + 2
-  int cand_cap;    // np * bs
-  int prot;        // protected width = min(s_cap, sink + swa)
-  int n_merge;     // keys merged per L1 pool: ntiles * max(k_f, k_n)
-  bool merge_lds;  // merge keys fit the LDS union
-  int lds_bytes;   // dynamic LDS of the launch
-  // LDS byte offsets: common part, then the tile and tail parts overlap
-  int o_hist, o_tmp;
-  int o_qf, o_key, o_dims, o_stage;                       // tile stage
-  int o_fp, o_np, o_sel, o_qg, o_choff, o_fdims, o_pages, o_pgoff, o_pphys,
-      o_sp, o_rank, o_union, o_cand, o_l0, o_l1, o_mid;  // tail stage
-  // global workspace byte offsets
-  int64_t w_rowcnt, w_reqcnt, w_far, w_near, w_total;
+  int ntiles;     // L1 tiles per row (kernel A grid.x)
+  int segc;       // pages per tail thread and key segment (multiple of 8)
+  int nseg;       // key segments per row
+  int kstride;    // keys per row in the workspace = nseg * 256 * segc
+  int words;      // candidate bitmap words = kstride / 32
+  int np;         // candidate page capacity = k_f + k_n + 2
+  int dense;      // dense candidate slots = np * bs
+  int dstride;    // dense keys per row in the workspace (multiple of 8)
+  int nchunk;     // kernel B grid.x
+  int prot;       // protected width = min(s_cap, sink + swa)
+  int lds_a, lds_b;
+  // kernel A LDS: common part, then the tile and tail parts overlap
+  int a_hist, a_tmp, a_misc, a_qf, a_fdims;
+  int a_dims, a_last, a_tphys, a_stage;                 // tile
+  int a_keys, a_pages, a_cbits, a_dbf, a_dbn, a_dsel;   // tail
+  // kernel B LDS: common part, then the scoring and tail parts overlap
+  int b_hist, b_tmp, b_misc, b_qg, b_fdims;
+  int b_tok, b_stage;                                   // scoring
+  int b_dk, b_pages, b_pphys, b_l0, b_l0x, b_l1, b_l1x, b_mid, b_mslot;  // tail
+  // global workspace byte offsets; counters and histograms first (they must
+  // start at zero and are reset by the kernels themselves)
+  int64_t w_rowcnt, w_reqcnt, w_bcnt, w_hist, w_keys, w_pages, w_pphys, w_npu,
+      w_l2vec, w_dk, w_total;
 };
 
 __host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
-
-// Tokens per staging sub-batch of the page-statistics pass.
-constexpr int kStatTokens = 16;
 
 __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p) {
   SelDims s;
   const int group = p.hq / p.hkv;
   s.ntiles = (p.max_blocks + NFA_BLOCK - 1) / NFA_BLOCK;
+  const int cpt = s.ntiles;  // pages per thread when one segment covers the row
+  int segc = (cpt + 7) & ~7;
+  if (segc > 64) segc = 64;
+  s.segc = segc;
+  s.nseg = (cpt + segc - 1) / segc;
+  s.kstride = s.nseg * NFA_BLOCK * segc;
+  s.words = s.kstride / 32;
   s.np = p.k_f + p.k_n + 2;
-  s.cand_cap = s.np * p.bs;
+  s.dense = s.np * p.bs;
+  s.dstride = (s.dense + 7) & ~7;
+  s.nchunk = (s.dense + kL2Slots - 1) / kL2Slots;
   const int s_cap = p.max_blocks * p.bs;
   s.prot = p.sink_tokens + p.swa < s_cap ? p.sink_tokens + p.swa : s_cap;
-  const int kmax = p.k_f > p.k_n ? p.k_f : p.k_n;
-  s.n_merge = s.ntiles * (kmax > 0 ? kmax : 1);
+  // kernel A
   int o = 0;
-  s.o_hist = o;  o += align16(4 * 256);
-  s.o_tmp = o;   o += align16(4 * 32);
-  const int base = o;
-  // tile stage
-  s.o_qf = o;    o += align16(4 * group * p.dsub);
-  s.o_key = o;   o += align16(4 * NFA_BLOCK);
-  s.o_dims = o;  o += align16(4 * p.dsub);
-  s.o_stage = o; o += align16(4 * NFA_BLOCK * kStatTokens);
-  const int tile_end = o;
-  // tail stage
-  o = base;
-  s.o_fp = o;    o += align16(4 * (p.k_f > 0 ? p.k_f : 1));
-  s.o_np = o;    o += align16(4 * (p.k_n > 0 ? p.k_n : 1));
-  s.o_sel = o;   o += align16(8 * (kmax > 0 ? kmax : 1));
-  s.o_qg = o;    o += align16(4 * p.fine_dsub);
-  s.o_choff = o; o += align16(4 * 64);
-  s.o_fdims = o; o += align16(4 * p.fine_dsub);
-  s.o_pages = o; o += align16(4 * s.np);
-  s.o_pgoff = o; o += align16(4 * (s.np + 1));
-  s.o_pphys = o; o += align16(4 * s.np);
-  s.o_sp = o;    o += align16(4 * s.np);
-  s.o_rank = o;  o += align16(4 * s.np);
-  s.o_union = o;
-  // union: merge keys (u16) | candidates + lists
-  s.o_cand = o;  o += align16(2 * s.cand_cap);
-  s.o_l0 = o;    o += align16(4 * p.k2);
-  s.o_l1 = o;    o += align16(4 * p.k2);
-  s.o_mid = o;   o += align16(4 * p.k2);
-  int tail_end = o;
-  const int merge_end = s.o_union + align16(2 * s.n_merge);
-  s.merge_lds = merge_end <= 60 * 1024;
-  if (s.merge_lds && merge_end > tail_end) tail_end = merge_end;
-  s.lds_bytes = tile_end > tail_end ? tile_end : tail_end;
+  s.a_hist = o;  o += align16(4 * 4 * 256);
+  s.a_tmp = o;   o += align16(4 * 64);
+  s.a_misc = o;  o += align16(4 * 32);
+  s.a_qf = o;    o += align16(4 * group * p.dsub);
+  s.a_fdims = o; o += align16(4 * p.fine_dsub);
+  const int a_base = o;
+  s.a_dims = o;  o += align16(4 * p.dsub);
+  s.a_last = o;  o += align16(4 * 3 * p.dsub);
+  s.a_tphys = o; o += align16(4 * NFA_BLOCK);
+  s.a_stage = o; o += align16(4 * NFA_BLOCK * kStatTokens);
+  const int a_tile = o;
+  o = a_base;
+  s.a_keys = o;  o += align16(2 * NFA_BLOCK * s.segc);
+  s.a_pages = o; o += align16(4 * s.np);
+  s.a_cbits = o; o += align16(4 * s.words);
+  s.a_dbf = o;   o += align16(4 * s.words);
+  s.a_dbn = o;   o += align16(4 * s.words);
+  s.a_dsel = o;  o += align16(8 * (p.k_f + p.k_n + 1));
+  s.lds_a = a_tile > o ? a_tile : o;
+  // kernel B
+  o = 0;
+  s.b_hist = o;  o += align16(4 * 2 * 256);
+  s.b_tmp = o;   o += align16(4 * 64);
+  s.b_misc = o;  o += align16(4 * 32);
+  s.b_qg = o;    o += align16(4 * p.fine_dsub);
+  s.b_fdims = o; o += align16(4 * p.fine_dsub);
+  const int b_base = o;
+  s.b_tok = o;   o += align16(4 * kL2Slots);
+  s.b_stage = o; o += align16(4 * kL2Slots * p.fine_dsub);
+  const int b_score = o;
+  o = b_base;
+  s.b_dk = o;    o += align16(2 * s.dstride);
+  s.b_pages = o; o += align16(4 * s.np);
+  s.b_pphys = o; o += align16(4 * s.np);
+  s.b_l0 = o;    o += align16(4 * p.k2);
+  s.b_l0x = o;   o += align16(4 * p.k2);
+  s.b_l1 = o;    o += align16(4 * p.k2);
+  s.b_l1x = o;   o += align16(4 * p.k2);
+  s.b_mid = o;   o += align16(4 * p.k2);
+  s.b_mslot = o; o += align16(4 * p.k2);
+  s.lds_b = b_score > o ? b_score : o;
+  // workspace
   const int rows = p.batch * p.hkv;
   int64_t w = 0;
   s.w_rowcnt = w; w += ((int64_t)4 * rows + 255) & ~(int64_t)255;
   s.w_reqcnt = w; w += ((int64_t)4 * p.batch + 255) & ~(int64_t)255;
-  s.w_far = w;    w += (int64_t)8 * rows * s.ntiles * (p.k_f > 0 ? p.k_f : 1);
-  s.w_near = w;   w += (int64_t)8 * rows * s.ntiles * (p.k_n > 0 ? p.k_n : 1);
+  s.w_bcnt = w;   w += ((int64_t)4 * rows + 255) & ~(int64_t)255;
+  s.w_hist = w;   w += (int64_t)4 * rows * 512;
+  s.w_keys = w;   w += (((int64_t)2 * rows * s.kstride) + 255) & ~(int64_t)255;
+  s.w_pages = w;  w += (((int64_t)4 * rows * s.np) + 255) & ~(int64_t)255;
+  s.w_pphys = w;  w += (((int64_t)4 * rows * s.np) + 255) & ~(int64_t)255;
+  s.w_npu = w;    w += ((int64_t)4 * rows + 255) & ~(int64_t)255;
+  s.w_l2vec = w;  w += ((int64_t)4 * 2 + 255) & ~(int64_t)255;
+  s.w_dk = w;     w += (int64_t)2 * rows * s.dstride;
   s.w_total = w;
   return s;
 }
@@ -146,6 +192,8 @@ __device__ __forceinline__ RowGeo row_geo(const NfaSelectParams &p, int L,
   return g;
 }
 
+// Pool membership of page t.  Monotone in the skip flags: a page in a pool
+// with skips applied is also in it without them.
 __device__ __forceinline__ void pools(const NfaSelectParams &p, const RowGeo &g,
                                       int t, bool *far_pool, bool *near_pool) {
   const int bs = p.bs;
@@ -223,13 +271,23 @@ __device__ __forceinline__ int64_t kv_offset(const NfaSelectParams &p,
 // page statistics of pages [pg_lo, pg_hi) for one (request, kv)
 // ---------------------------------------------------------------------------
 
+// The key row of token `new_tok` comes from `new_row` when it is non-null
+// (the decode token, whose pool write is issued by this same workgroup).
+__device__ __forceinline__ bool is_new(int tok, int new_tok, const void *row) {
+  return row != nullptr && tok == new_tok;
+}
+
 // The page's tokens are staged through LDS in sub-batches of kStatTokens
 // (all loads of a sub-batch in flight at once); each (page, dim) thread then
-// scans its tokens in ascending order: v < min, v > max, sum + v.
+// scans its tokens in ascending order: v < min, v > max, sum + v.  Compact
+// code: this is the path of the incremental (latest page) update.  ``s_tphys``
+// (or NULL) holds the physical page of every page of the range when a page
+// never straddles two physical pages.
 template <int DSUB, typename KV>
-__device__ void compute_stats(const NfaSelectParams &p, int64_t req, int kv,
+__device__ __forceinline__ void compute_stats(const NfaSelectParams &p, int64_t req, int kv,
                               int L, int pg_lo, int pg_hi, float *s_stage,
-                              const int *s_dims) {
+                              const int *s_dims, const int *s_tphys,
+                              const KV *new_row, int new_tok, float *s_last) {
   const KV *kpool = (const KV *)p.k_pool_l;
   const int32_t *bt = p.block_table_l + req * p.max_blocks;
   constexpr int PER = NFA_BLOCK / DSUB;  // pages per pass
@@ -256,9 +314,14 @@ __device__ void compute_stats(const NfaSelectParams &p, int64_t req, int kv,
         const int lp = tok / p.page;
         float v = 0.0f;
         if (px < pg_hi && i0 + ti < p.bs && tok < L && lp < p.max_blocks) {
-          const int phys = safe_page(p, bt[lp]);
-          v = Elem<KV>::load(kpool + kv_offset(p, phys, kv, tok % p.page) +
-                             s_dims[dd]);
+          if (is_new(tok, new_tok, new_row)) {
+            v = Elem<KV>::load(new_row + s_dims[dd]);
+          } else {
+            const int phys = s_tphys != nullptr ? s_tphys[px - pg_lo]
+                                                : safe_page(p, bt[lp]);
+            v = Elem<KV>::load(kpool + kv_offset(p, phys, kv, tok % p.page) +
+                               s_dims[dd]);
+          }
         }
         s_stage[e] = v;
       }
@@ -277,9 +340,17 @@ __device__ void compute_stats(const NfaSelectParams &p, int64_t req, int kv,
     }
     if (pg < pg_hi) {
       const int64_t si = stat_index<KV>(p, req, kv, d, pg, DSUB);
-      smin[si] = (KV)Elem<KV>::from_f32(mn);
-      smax[si] = (KV)Elem<KV>::from_f32(mx);
-      ssum[si] = (KV)Elem<KV>::from_f32(sm);
+      const KV a = (KV)Elem<KV>::from_f32(mn);
+      const KV c = (KV)Elem<KV>::from_f32(mx);
+      const KV s = (KV)Elem<KV>::from_f32(sm);
+      smin[si] = a;
+      smax[si] = c;
+      ssum[si] = s;
+      if (s_last != nullptr) {
+        s_last[d] = Elem<KV>::load(&a);
+        s_last[DSUB + d] = Elem<KV>::load(&c);
+        s_last[2 * DSUB + d] = Elem<KV>::load(&s);
+      }
     }
   }
 }
@@ -289,11 +360,14 @@ __device__ void compute_stats(const NfaSelectParams &p, int64_t req, int kv,
 // each dim is then scanned over the tokens in ascending order.  ``s_coff``
 // holds the element offset of every chunk, ``s_tphys`` (or NULL) the
 // physical page of every page of the range when a page never straddles two
-// physical pages.
+// physical pages.  ``s_last`` (or NULL) receives the stored statistics of a
+// single-page range as floats.
 template <int DSUB, typename KV>
-__device__ void compute_stats_vec(const NfaSelectParams &p, int64_t req, int kv,
+__device__ __forceinline__ void compute_stats_vec(const NfaSelectParams &p, int64_t req, int kv,
                                   int L, int pg_lo, int pg_hi,
-                                  const int *s_coff, const int *s_tphys) {
+                                  const int *s_coff, const int *s_tphys,
+                                  const KV *new_row, int new_tok,
+                                  float *s_last) {
   constexpr int CH = Elem<KV>::kChunk;
   constexpr int NCH1 = DSUB / CH;
   constexpr int TG = 16;
@@ -324,17 +398,22 @@ __device__ void compute_stats_vec(const NfaSelectParams &p, int64_t req, int kv,
         ok[k] = i < p.bs && tok < L && lp < p.max_blocks;
         raw[k] = make_uint4(0u, 0u, 0u, 0u);
         if (ok[k]) {
-          const int phys = s_tphys != nullptr ? s_tphys[pg - pg_lo]
-                                              : safe_page(p, bt[lp]);
-          raw[k] = *reinterpret_cast<const uint4 *>(
-              kpool + kv_offset(p, phys, kv, tok % p.page) + s_coff[c]);
+          const KV *src;
+          if (is_new(tok, new_tok, new_row)) {
+            src = new_row;
+          } else {
+            const int phys = s_tphys != nullptr ? s_tphys[pg - pg_lo]
+                                                : safe_page(p, bt[lp]);
+            src = kpool + kv_offset(p, phys, kv, tok % p.page);
+          }
+          raw[k] = *reinterpret_cast<const uint4 *>(src + s_coff[c]);
         }
       }
 #pragma unroll
       for (int k = 0; k < TG; ++k) {
         if (!ok[k]) continue;
         float x[CH];
-        load_chunk<KV>(reinterpret_cast<const KV *>(&raw[k]), x);
+        unpack_chunk<KV>(raw[k], x);
 #pragma unroll
         for (int e = 0; e < CH; ++e) {
           mn[e] = (x[e] < mn[e]) ? x[e] : mn[e];
@@ -346,10 +425,89 @@ __device__ void compute_stats_vec(const NfaSelectParams &p, int64_t req, int kv,
     const int64_t si = stat_index<KV>(p, req, kv, c * CH, pg, DSUB);
 #pragma unroll
     for (int e = 0; e < CH; ++e) {
-      smin[si + e] = (KV)Elem<KV>::from_f32(mn[e]);
-      smax[si + e] = (KV)Elem<KV>::from_f32(mx[e]);
-      ssum[si + e] = (KV)Elem<KV>::from_f32(sm[e]);
+      const KV a = (KV)Elem<KV>::from_f32(mn[e]);
+      const KV b = (KV)Elem<KV>::from_f32(mx[e]);
+      const KV s = (KV)Elem<KV>::from_f32(sm[e]);
+      smin[si + e] = a;
+      smax[si + e] = b;
+      ssum[si + e] = s;
+      if (s_last != nullptr) {
+        s_last[c * CH + e] = Elem<KV>::load(&a);
+        s_last[DSUB + c * CH + e] = Elem<KV>::load(&b);
+        s_last[2 * DSUB + c * CH + e] = Elem<KV>::load(&s);
+      }
     }
+  }
+}
+
+// Statistics of the latest page (the incremental update of every decode
+// step), compact: rounds of 4 * (256 / DSUB) tokens are staged through LDS by
+// (token, dim) threads, four loads in flight each; thread d < DSUB then scans
+// the round's tokens in ascending order.  `phys_first` is the physical page
+// of the page's first token (used when a page never straddles two physical
+// pages).
+template <int DSUB, typename KV>
+__device__ __forceinline__ void stats_latest_page(
+    const NfaSelectParams &p, int64_t req, int kv, int L, int pg,
+    int phys_first, const int *s_dims, float *s_stage, const KV *new_row,
+    float *s_last) {
+  constexpr int R = NFA_BLOCK / DSUB;
+  constexpr int RT = 4 * R;  // tokens per round
+  const int tid = threadIdx.x;
+  const int d = tid % DSUB;
+  const int r = tid / DSUB;
+  const int tok0 = pg * p.bs;
+  const int nt = imin(p.bs, L - tok0);
+  const bool one_phys = (p.page % p.bs) == 0;
+  const int32_t *bt = p.block_table_l + req * p.max_blocks;
+  const KV *kpool = (const KV *)p.k_pool_l;
+  const int dim = s_dims[d];
+  float mn = __uint_as_float(0x7F800000u);
+  float mx = __uint_as_float(0xFF800000u);
+  float sm = 0.0f;
+  for (int i0 = 0; i0 < nt; i0 += RT) {
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = i0 + r + k * R;
+      v[k] = 0.0f;
+      if (i < nt) {
+        const int tok = tok0 + i;
+        if (new_row != nullptr && tok == L - 1) {
+          v[k] = Elem<KV>::load(new_row + dim);
+        } else {
+          const int phys =
+              one_phys ? phys_first
+                       : safe_page(p, bt[imin(tok / p.page, p.max_blocks - 1)]);
+          v[k] = Elem<KV>::load(kpool + kv_offset(p, phys, kv, tok % p.page) + dim);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s_stage[(r + k * R) * DSUB + d] = v[k];
+    __syncthreads();
+    if (tid < DSUB) {
+      const int n = imin(RT, nt - i0);
+      for (int i = 0; i < n; ++i) {
+        const float x = s_stage[i * DSUB + d];
+        mn = (x < mn) ? x : mn;
+        mx = (x > mx) ? x : mx;
+        sm = sm + x;
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < DSUB) {
+    const int64_t si = stat_index<KV>(p, req, kv, d, pg, DSUB);
+    const KV a = (KV)Elem<KV>::from_f32(mn);
+    const KV c = (KV)Elem<KV>::from_f32(mx);
+    const KV s = (KV)Elem<KV>::from_f32(sm);
+    ((KV *)p.stat_min_l)[si] = a;
+    ((KV *)p.stat_max_l)[si] = c;
+    ((KV *)p.stat_sum_l)[si] = s;
+    s_last[d] = Elem<KV>::load(&a);
+    s_last[DSUB + d] = Elem<KV>::load(&c);
+    s_last[2 * DSUB + d] = Elem<KV>::load(&s);
   }
 }
 
@@ -359,423 +517,164 @@ __device__ void compute_stats_vec(const NfaSelectParams &p, int64_t req, int kv,
 
 constexpr int GMAX = 8;
 
-template <int DSUB, typename KV>
-__device__ __forceinline__ void l1_page_scores(const NfaSelectParams &p,
-                                               int64_t req, int kv, int t,
-                                               int G, const float *qf,
+// Head-major: for each query head j (rolled loop) the dims run in order, so
+// sneg_j / spos_j / savg_j accumulate exactly as Σ_d in ascending d; the
+// group mean then sums bf16(per-head score) over j in order.  kmin / kmax /
+// kavg hold the page statistics as floats (kavg = bf16(sum / bs)).
+template <int DSUB>
+__device__ __forceinline__ void l1_scores_regs(const float *kmin,
+                                               const float *kmax,
+                                               const float *kavg,
+                                               const float *s_qf, int G,
                                                bool need_mm, bool need_avg,
                                                uint16_t *mm_bits,
                                                uint16_t *avg_bits) {
-  constexpr int CH = Elem<KV>::kChunk;
-  const KV *smin = (const KV *)p.stat_min_l;
-  const KV *smax = (const KV *)p.stat_max_l;
-  const KV *ssum = (const KV *)p.stat_sum_l;
-  float sneg[GMAX], spos[GMAX], savg[GMAX];
-#pragma unroll
-  for (int j = 0; j < GMAX; ++j) {
-    sneg[j] = 0.0f;
-    spos[j] = 0.0f;
-    savg[j] = 0.0f;
-  }
-  const float inv_bs = (float)p.bs;
-#pragma unroll
-  for (int c = 0; c < DSUB / CH; ++c) {
-    const int64_t base = stat_index<KV>(p, req, kv, c * CH, t, DSUB);
-    float kmin[CH], kmax[CH], kavg[CH];
+  float mm_acc = 0.0f, avg_acc = 0.0f;
+  for (int j = 0; j < G; ++j) {
+    const float *q = s_qf + j * DSUB;
     if (need_mm) {
-      load_chunk<KV>(smin + base, kmin);
-      load_chunk<KV>(smax + base, kmax);
+      float sn = 0.0f, sp = 0.0f;
+#pragma unroll
+      for (int d = 0; d < DSUB; ++d) {
+        const float qd = q[d];
+        const float ql = qd < 0.0f ? qd : 0.0f;
+        const float qh = qd > 0.0f ? qd : 0.0f;
+        const float a = kmin[d] * ql;
+        const float b = kmax[d] * qh;
+        sn = sn + a;
+        sp = sp + b;
+      }
+      mm_acc = mm_acc + bf16r(sn + sp);
     }
     if (need_avg) {
-      float ks[CH];
-      load_chunk<KV>(ssum + base, ks);
+      float sa = 0.0f;
 #pragma unroll
-      for (int e = 0; e < CH; ++e) kavg[e] = bf16r(ks[e] / inv_bs);
-    }
-#pragma unroll
-    for (int e = 0; e < CH; ++e) {
-      const int d = c * CH + e;
-#pragma unroll
-      for (int j = 0; j < GMAX; ++j) {
-        if (j < G) {
-          const float q = qf[j * DSUB + d];
-          if (need_mm) {
-            const float ql = q < 0.0f ? q : 0.0f;
-            const float qh = q > 0.0f ? q : 0.0f;
-            const float a = kmin[e] * ql;
-            const float b = kmax[e] * qh;
-            sneg[j] = sneg[j] + a;
-            spos[j] = spos[j] + b;
-          }
-          if (need_avg) {
-            const float a = kavg[e] * q;
-            savg[j] = savg[j] + a;
-          }
-        }
+      for (int d = 0; d < DSUB; ++d) {
+        const float a = kavg[d] * q[d];
+        sa = sa + a;
       }
-    }
-  }
-  float mm_acc = 0.0f, avg_acc = 0.0f;
-#pragma unroll
-  for (int j = 0; j < GMAX; ++j) {
-    if (j < G) {
-      mm_acc = mm_acc + bf16r(sneg[j] + spos[j]);
-      avg_acc = avg_acc + bf16r(savg[j]);
+      avg_acc = avg_acc + bf16r(sa);
     }
   }
   *mm_bits = bf16_bits(mm_acc / (float)G);
   *avg_bits = bf16_bits(avg_acc / (float)G);
 }
 
-// ---------------------------------------------------------------------------
-// tile top-k: select the best K of the block's 256 keys (one per thread,
-// 0 = invalid) and write them in thread (= page) order, padded with zeros.
-// ---------------------------------------------------------------------------
-
-__device__ void tile_topk(uint32_t key, int t, int K, uint64_t *out,
-                          uint32_t *s_key, int *hist, int *tmp) {
-  if (K <= 0) return;
-  const int tid = threadIdx.x;
-  s_key[tid] = key;
-  __syncthreads();
-  int *thr = tmp + 16;
-  topk_threshold16([&](int i) { return s_key[i]; }, NFA_BLOCK, K, hist, tmp,
-                   thr);
-  const uint32_t T = (uint32_t)thr[0];
-  const int need = thr[1];
-  int tot;
-  const bool eq = key != 0 && key == T;
-  const int r_eq = block_count_exclusive(eq, tmp, &tot);
-  const bool sel = key > T || (eq && r_eq < need);
-  const int pos = block_count_exclusive(sel, tmp, &tot);
-  if (sel && pos < K) out[pos] = ((uint64_t)key << 32) | (uint32_t)t;
-  for (int i = tot + tid; i < K; i += NFA_BLOCK) out[i] = 0;
+// Same arithmetic with the statistics read chunk by chunk from memory (L1
+// dim counts above 32: rope / full subspaces).
+template <int DSUB, typename KV>
+__device__ __forceinline__ void l1_scores_mem(const NfaSelectParams &p,
+                                              int64_t req, int kv, int t,
+                                              const float *s_qf, int G,
+                                              bool need_mm, bool need_avg,
+                                              const float *s_last,
+                                              uint16_t *mm_bits,
+                                              uint16_t *avg_bits) {
+  constexpr int CH = Elem<KV>::kChunk;
+  const KV *smin = (const KV *)p.stat_min_l;
+  const KV *smax = (const KV *)p.stat_max_l;
+  const KV *ssum = (const KV *)p.stat_sum_l;
+  const float bsf = (float)p.bs;
+  float mm_acc = 0.0f, avg_acc = 0.0f;
+  for (int j = 0; j < G; ++j) {
+    const float *q = s_qf + j * DSUB;
+    float sn = 0.0f, sp = 0.0f, sa = 0.0f;
+    for (int c = 0; c < DSUB / CH; ++c) {
+      float kmin[CH], kmax[CH], ks[CH];
+      if (s_last != nullptr) {
+#pragma unroll
+        for (int e = 0; e < CH; ++e) {
+          kmin[e] = s_last[c * CH + e];
+          kmax[e] = s_last[DSUB + c * CH + e];
+          ks[e] = s_last[2 * DSUB + c * CH + e];
+        }
+      } else {
+        const int64_t base = stat_index<KV>(p, req, kv, c * CH, t, DSUB);
+        if (need_mm) {
+          load_chunk<KV>(smin + base, kmin);
+          load_chunk<KV>(smax + base, kmax);
+        }
+        if (need_avg) load_chunk<KV>(ssum + base, ks);
+      }
+#pragma unroll
+      for (int e = 0; e < CH; ++e) {
+        const float qd = q[c * CH + e];
+        if (need_mm) {
+          const float ql = qd < 0.0f ? qd : 0.0f;
+          const float qh = qd > 0.0f ? qd : 0.0f;
+          const float a = kmin[e] * ql;
+          const float b = kmax[e] * qh;
+          sn = sn + a;
+          sp = sp + b;
+        }
+        if (need_avg) {
+          const float a = bf16r(ks[e] / bsf) * qd;
+          sa = sa + a;
+        }
+      }
+    }
+    if (need_mm) mm_acc = mm_acc + bf16r(sn + sp);
+    if (need_avg) avg_acc = avg_acc + bf16r(sa);
+  }
+  *mm_bits = bf16_bits(mm_acc / (float)G);
+  *avg_bits = bf16_bits(avg_acc / (float)G);
 }
 
 // ---------------------------------------------------------------------------
-// tail: merge of tile lists into the sorted L1 top-K page list
-// (selector:1766-1803 contract: valid pages by (score desc, page asc), then
-// -inf pages by ascending index)
+// tail helpers
 // ---------------------------------------------------------------------------
 
-__device__ int merge_l1(const uint64_t *part, int n, int K, int *out_pages,
-                        uint64_t *s_sel, uint16_t *s_m16, int *hist,
-                        int *tmp) {
-  const int tid = threadIdx.x;
-  int *thr = tmp + 16;
-  if (s_m16 != nullptr) {
-    // stage the 16-bit score keys, four loads in flight per thread
-    for (int i0 = tid; i0 < n; i0 += 4 * NFA_BLOCK) {
-      uint64_t k[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * NFA_BLOCK;
-        k[u] = i < n ? part[i] : 0ull;
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * NFA_BLOCK;
-        if (i < n) s_m16[i] = (uint16_t)(k[u] >> 32);
-      }
-    }
-    __syncthreads();
-    topk_threshold16([&](int i) { return (uint32_t)s_m16[i]; }, n, K, hist,
-                     tmp, thr);
-  } else {
-    topk_threshold16([&](int i) { return (uint32_t)(part[i] >> 32); }, n, K,
-                     hist, tmp, thr);
-  }
-  const uint32_t T = (uint32_t)thr[0];
-  const int need = thr[1];
-  const int nvalid = thr[2] < K ? thr[2] : K;
-  int carry_eq = 0, carry_sel = 0;
-  for (int base = 0; base < n; base += NFA_BLOCK) {
-    const int i = base + tid;
-    uint32_t v = 0;
-    if (i < n) v = s_m16 != nullptr ? (uint32_t)s_m16[i] : (uint32_t)(part[i] >> 32);
-    const bool eq = v != 0 && v == T;
-    int tot_eq, tot_sel;
-    const int r_eq = block_count_exclusive(eq, tmp, &tot_eq) + carry_eq;
-    const bool sel = v > T || (eq && r_eq < need);
-    const int pos = block_count_exclusive(sel, tmp, &tot_sel) + carry_sel;
-    if (sel && pos < K) ((int *)s_sel)[pos] = i;  // index now, key below
-    carry_eq += tot_eq;
-    carry_sel += tot_sel;
-  }
-  __syncthreads();
-  {
-    // fetch the selected keys: all loads in flight, no barrier in between
-    int idx[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int pos = tid + u * NFA_BLOCK;
-      idx[u] = pos < nvalid ? ((const int *)s_sel)[pos] : 0;
-    }
-    uint64_t key[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int pos = tid + u * NFA_BLOCK;
-      key[u] = pos < nvalid ? part[idx[u]] : 0ull;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int pos = tid + u * NFA_BLOCK;
-      if (pos < nvalid) s_sel[pos] = key[u];
-    }
-    __syncthreads();
-  }
-  // order the selection by (score desc, page asc)
-  for (int i = tid; i < nvalid; i += NFA_BLOCK) {
-    const uint64_t ki = s_sel[i];
-    const uint32_t vi = (uint32_t)(ki >> 32);
-    const uint32_t ti = (uint32_t)ki;
-    int rank = 0;
-    for (int j = 0; j < nvalid; ++j) {
-      const uint64_t kj = s_sel[j];
-      const uint32_t vj = (uint32_t)(kj >> 32);
-      const uint32_t tj = (uint32_t)kj;
-      rank += (vj > vi) || (vj == vi && tj < ti);
-    }
-    out_pages[rank] = (int)ti;
-  }
-  __syncthreads();
-  if (nvalid < K) {
-    // -inf fillers: the lowest page indices that are not valid pages.
-    // s_sel is reused to hold the valid pages sorted ascending as ints.
-    int *vt = (int *)s_sel;
-    int vtmp[4];
-    int cnt = 0;
-    for (int i = tid; i < nvalid && cnt < 4; i += NFA_BLOCK) {
-      const int ti = out_pages[i];
-      int rank = 0;
-      for (int j = 0; j < nvalid; ++j) rank += out_pages[j] < ti;
-      vtmp[cnt++] = rank;
-    }
-    __syncthreads();
-    cnt = 0;
-    for (int i = tid; i < nvalid && cnt < 4; i += NFA_BLOCK) {
-      vt[vtmp[cnt++]] = out_pages[i];
-    }
-    __syncthreads();
-    // boundary b[j] = vt[j] - j counts non-valid pages below vt[j]
-    for (int i = tid; i < K - nvalid; i += NFA_BLOCK) {
-      int lo = 0, hi = nvalid;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (vt[mid] - mid <= i)
-          lo = mid + 1;
-        else
-          hi = mid;
-      }
-      out_pages[nvalid + i] = i + lo;
-    }
-    __syncthreads();
-  }
-  return nvalid;
-}
-
-// ---------------------------------------------------------------------------
-// tail: L2 logits of the candidate tokens (selector:459-516).  One token per
-// thread, the fp32 dot product runs over the L2 dims in order.  When the L2
-// dims form aligned 16-byte runs (tail, rope, nope, full) each token's keys
-// come in NCH vector loads with U tokens in flight per thread.
-// ---------------------------------------------------------------------------
-
-struct CandView {
-  const int *pages;   // sorted unique candidate pages
-  const int *pgoff;   // exclusive offsets, np_u + 1 entries
-  int np_u;
-  int tok_lo;         // first token of every page is max(page*bs, tok_lo)
-  int bs;
-  __device__ __forceinline__ int page_index(int i) const {
-    return upper_bound_i32(pgoff, np_u + 1, i) - 1;
-  }
-  __device__ __forceinline__ int token_at(int pi, int i) const {
-    const int first = pages[pi] * bs > tok_lo ? pages[pi] * bs : tok_lo;
-    return first + (i - pgoff[pi]);
-  }
-  __device__ __forceinline__ int token(int i) const {
-    return token_at(page_index(i), i);
-  }
+// Final top-K rule of one pool: a key k is selected when k > T, or when
+// k == T != 0 and fewer than `need` equal keys precede it in page order.
+struct PoolThr {
+  int T, need, nsel;
 };
 
-template <typename KV>
-__device__ __forceinline__ uint16_t logit_key(const NfaSelectParams &p,
-                                              float acc, int row, int i,
-                                              int tok) {
-  const uint16_t bits = bf16_bits(acc);
-  if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
-    p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tok;
-    p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
-        bits == kNanBits ? kNegInfBits : bits;
+__device__ __forceinline__ PoolThr pool_threshold(int K, const int *coarse,
+                                                  const int *fine,
+                                                  const int *fine_hist) {
+  PoolThr r;
+  const int hb = coarse[0];
+  if (K <= 0) {
+    r.T = 0x10000;  // nothing
+    r.need = 0;
+    r.nsel = 0;
+  } else if (hb < 0) {  // every valid key
+    r.T = 0;
+    r.need = 0;
+    r.nsel = coarse[2];
+  } else {
+    r.T = (hb << 8) | fine[0];
+    r.need = K - coarse[1] - fine[1];
+    r.nsel = K;
+    if (fine_hist[fine[0]] == r.need) r.need = 1 << 30;  // no tie cut
   }
-  return bits == kNanBits ? 0 : (uint16_t)score_key(bits);
+  return r;
 }
 
-template <typename KV, int NCH>
-__device__ void l2_logits_vec(const NfaSelectParams &p, const CandView &cv,
-                              int n_cand, int kv, int row, const int *s_pphys,
-                              const int *s_choff, const float *s_qg,
-                              uint16_t *s_cand) {
-  constexpr int CH = Elem<KV>::kChunk;
-  constexpr int U = NCH <= 4 ? 4 : (NCH <= 8 ? 2 : 1);
-  const KV *kpool = (const KV *)p.k_pool_l;
-  const int32_t *bt = p.block_table_l + p.valid_req[row / p.hkv] * p.max_blocks;
-  const bool page_phys = (p.page % p.bs) == 0;
-  for (int i0 = threadIdx.x; i0 < n_cand; i0 += U * NFA_BLOCK) {
-    uint4 raw[U][NCH];
-    int tok[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + u * NFA_BLOCK;
-      tok[u] = 0;
-      if (i < n_cand) {
-        const int pi = cv.page_index(i);
-        tok[u] = cv.token_at(pi, i);
-        const int phys =
-            page_phys ? s_pphys[pi] : safe_page(p, bt[tok[u] / p.page]);
-        const KV *kr = kpool + kv_offset(p, phys, kv, tok[u] % p.page);
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-          raw[u][c] = *reinterpret_cast<const uint4 *>(kr + s_choff[c]);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + u * NFA_BLOCK;
-      if (i < n_cand) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-          float x[CH];
-          load_chunk<KV>(reinterpret_cast<const KV *>(&raw[u][c]), x);
-#pragma unroll
-          for (int e = 0; e < CH; ++e) {
-            const float prod = x[e] * s_qg[c * CH + e];
-            acc = acc + prod;
-          }
-        }
-        s_cand[i] = logit_key<KV>(p, acc, row, i, tok[u]);
-      }
-    }
-  }
+__device__ __forceinline__ bool tie_cut(const PoolThr &t) {
+  return t.need < (1 << 30) && t.T > 0 && t.T < 0x10000;
 }
 
-template <typename KV>
-__device__ void l2_logits_scalar(const NfaSelectParams &p, const CandView &cv,
-                                 int n_cand, int kv, int row,
-                                 const int *s_pphys, const int *s_fdims,
-                                 const float *s_qg, uint16_t *s_cand) {
-  const KV *kpool = (const KV *)p.k_pool_l;
-  const int32_t *bt = p.block_table_l + p.valid_req[row / p.hkv] * p.max_blocks;
-  const bool page_phys = (p.page % p.bs) == 0;
-  for (int i = threadIdx.x; i < n_cand; i += NFA_BLOCK) {
-    const int pi = cv.page_index(i);
-    const int tok = cv.token_at(pi, i);
-    const int phys = page_phys ? s_pphys[pi] : safe_page(p, bt[tok / p.page]);
-    const KV *kr = kpool + kv_offset(p, phys, kv, tok % p.page);
-    float acc = 0.0f;
-    for (int d0 = 0; d0 < p.fine_dsub; d0 += 8) {
-      float x[8];
+// Stage keys [seg_base, seg_base + 256 * segc) of a row into LDS with 16-byte
+// loads, every load of the segment in flight at once.
+__device__ __forceinline__ void stage_keys(const uint16_t *g_keys, int seg_base,
+                                           int segc, uint16_t *s_keys) {
+  const int n16 = NFA_BLOCK * segc / 8;
+  const uint4 *src = reinterpret_cast<const uint4 *>(g_keys + seg_base);
+  uint4 *dst = reinterpret_cast<uint4 *>(s_keys);
+  uint4 r[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        x[e] = d0 + e < p.fine_dsub ? Elem<KV>::load(kr + s_fdims[d0 + e]) : 0.0f;
+  for (int k = 0; k < 8; ++k) {
+    const int u = threadIdx.x + k * NFA_BLOCK;
+    r[k] = u < n16 ? src[u] : make_uint4(0u, 0u, 0u, 0u);
+  }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (d0 + e < p.fine_dsub) {
-          const float prod = x[e] * s_qg[d0 + e];
-          acc = acc + prod;
-        }
-      }
-    }
-    s_cand[i] = logit_key<KV>(p, acc, row, i, tok);
+  for (int k = 0; k < 8; ++k) {
+    const int u = threadIdx.x + k * NFA_BLOCK;
+    if (u < n16) dst[u] = r[k];
   }
 }
-
-// ---------------------------------------------------------------------------
-// tail: one L2 region -- top-quota of the candidates in index range [ia, ib),
-// hole fill inside [rlo, rhi), sink filter; appended to s_mid at *mid_count.
-// ---------------------------------------------------------------------------
-
-__device__ void l2_region(const CandView &cv, const uint16_t *s_cand, int ia,
-                          int ib, int rlo, int rhi, int quota, int sink,
-                          int *s_l0, int *s_l1, int *s_mid, int *mid_count,
-                          int *hist, int *tmp) {
-  const int tid = threadIdx.x;
-  if (quota <= 0) return;
-  const int n = ib > ia ? ib - ia : 0;
-  int *thr = tmp + 16;
-  topk_threshold16([&](int i) { return (uint32_t)s_cand[ia + i]; }, n, quota,
-                   hist, tmp, thr);
-  const uint32_t T = (uint32_t)thr[0];
-  const int need = thr[1];
-  const int nvalid = thr[2];
-  const int nch = nvalid < quota ? nvalid : quota;
-  int carry_eq = 0, carry_sel = 0;
-  for (int base = 0; base < n; base += NFA_BLOCK) {
-    const int i = base + tid;
-    const uint32_t v = i < n ? (uint32_t)s_cand[ia + i] : 0u;
-    const bool eq = v != 0 && v == T;
-    int tot_eq, tot_sel;
-    const int r_eq = block_count_exclusive(eq, tmp, &tot_eq) + carry_eq;
-    const bool sel = v > T || (eq && r_eq < need);
-    const int pos = block_count_exclusive(sel, tmp, &tot_sel) + carry_sel;
-    if (sel && pos < quota) s_l0[pos] = cv.token(ia + i);
-    carry_eq += tot_eq;
-    carry_sel += tot_sel;
-  }
-  __syncthreads();
-  // hole fill: the (quota - nch) smallest ids of [rlo, rhi) not chosen
-  const int nfill_req = quota - nch;
-  for (int i = tid; i < nfill_req; i += NFA_BLOCK) {
-    int lo = 0, hi = nch;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (s_l0[mid] - rlo - mid <= i)
-        lo = mid + 1;
-      else
-        hi = mid;
-    }
-    const int id = rlo + i + lo;
-    s_l1[i] = id < rhi ? id : 0x7FFFFFFF;
-  }
-  __syncthreads();
-  // fill ids increase with i, so the valid ones form a prefix
-  int nfill = 0;
-  {
-    int lo = 0, hi = nfill_req;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (s_l1[mid] != 0x7FFFFFFF)
-        lo = mid + 1;
-      else
-        hi = mid;
-    }
-    nfill = lo;
-  }
-  const int drop = lower_bound_i32(s_l0, nch, sink) +
-                   lower_bound_i32(s_l1, nfill, sink);
-  const int base_out = *mid_count;
-  for (int j = tid; j < nch; j += NFA_BLOCK) {
-    const int v = s_l0[j];
-    if (v >= sink) {
-      const int pos = j + lower_bound_i32(s_l1, nfill, v) - drop;
-      s_mid[base_out + pos] = v;
-    }
-  }
-  for (int j = tid; j < nfill; j += NFA_BLOCK) {
-    const int v = s_l1[j];
-    if (v >= sink) {
-      const int pos = j + lower_bound_i32(s_l0, nch, v) - drop;
-      s_mid[base_out + pos] = v;
-    }
-  }
-  __syncthreads();
-  if (tid == 0) *mid_count = base_out + nch + nfill - drop;
-  __syncthreads();
-}
-
 
 // Protected sink/SWA ids as up to two disjoint intervals [u0,u1) [u2,u3),
 // exactly the ids of _final_union_protected_sort_kernel (selector:1337-1360):
@@ -865,8 +764,9 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   if (p.dbg_counts != nullptr && threadIdx.x == 0) p.dbg_counts[row] = 0;
 }
 
+
 // ---------------------------------------------------------------------------
-// the kernel
+// kernel A: L1 tiles and candidate pages
 // ---------------------------------------------------------------------------
 
 // Phase timestamp (debug timeline): completes the phase for the whole
@@ -881,15 +781,20 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 
 template <int DSUB, typename KV>
 __global__ void __launch_bounds__(NFA_BLOCK)
-    nfa_select_kernel(const NfaSelectParams p) {
+    nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
   extern __shared__ __align__(16) unsigned char smem[];
-  const SelDims sd = sel_dims(p);
-  int *s_hist = (int *)(smem + sd.o_hist);
-  int *s_tmp = (int *)(smem + sd.o_tmp);
-  float *s_qf = (float *)(smem + sd.o_qf);
-  uint32_t *s_key = (uint32_t *)(smem + sd.o_key);
-  int *s_dims = (int *)(smem + sd.o_dims);
-  float *s_stage = (float *)(smem + sd.o_stage);
+  constexpr int CH = Elem<KV>::kChunk;
+  constexpr int NC = DSUB / CH;
+  constexpr bool REG = DSUB == 32;  // page statistics held in registers
+  int *s_hist = (int *)(smem + sd.a_hist);  // far hi | near hi | far lo | near lo
+  int *s_tmp = (int *)(smem + sd.a_tmp);
+  int *s_misc = (int *)(smem + sd.a_misc);
+  float *s_qf = (float *)(smem + sd.a_qf);
+  int *s_fdims = (int *)(smem + sd.a_fdims);
+  int *s_dims = (int *)(smem + sd.a_dims);
+  float *s_last = (float *)(smem + sd.a_last);
+  int *s_tphys = (int *)(smem + sd.a_tphys);
+  float *s_stage = (float *)(smem + sd.a_stage);
 
   const int tid = threadIdx.x;
   const int tile = blockIdx.x;
@@ -898,18 +803,10 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int b = row / p.hkv;
   const int kv = row % p.hkv;
   const int G = p.hq / p.hkv;
-  const int L = p.lengths[b];
-  const bool active = p.active_req[b] >= 0;
-  const int64_t req = p.valid_req[b];
-  const bool skip_far = p.skip_far_l[req] != 0;
-  const bool skip_near = p.skip_near_l[req] != 0;
   const int bs = p.bs;
+  const int mb = p.max_blocks;
   const int t0 = tile * NFA_BLOCK;
-  // pages past the block-table width are never scored (selector:205-206)
-  const int kt_eff = imin(L > 0 ? (L + bs - 1) / bs : 0, p.max_blocks);
-  const int last_blk = L > 0 ? (L - 1) / bs : -1;
-  const bool owns_last = last_blk >= t0 && last_blk < t0 + NFA_BLOCK &&
-                         last_blk < p.max_blocks;
+  const int t = t0 + tid;
 
   const int64_t clk_tile = ((int64_t)row * (ntiles + 1) + tile) * 16;
   const int64_t clk_tail = ((int64_t)row * (ntiles + 1) + ntiles) * 16;
@@ -917,138 +814,230 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
   unsigned int *req_cnt = (unsigned int *)(ws + sd.w_reqcnt);
-  uint64_t *part_far = (uint64_t *)(ws + sd.w_far);
-  uint64_t *part_near = (uint64_t *)(ws + sd.w_near);
+  int *g_hist = (int *)(ws + sd.w_hist) + (int64_t)row * 512;
+  uint16_t *g_keys = (uint16_t *)(ws + sd.w_keys) + (int64_t)row * sd.kstride;
 
-  // 1. decode write of the current token (selector:1030-1061)
-  if (p.k_new != nullptr && active && owns_last) decode_write<KV>(p, b, kv);
-  for (int i = tid; i < DSUB; i += NFA_BLOCK) s_dims[i] = p.dims[i];
-  __syncthreads();
+  // ---- first round trip: row scalars, dims -------------------------------
+  const int L = p.lengths[b];
+  const bool active = p.active_req[b] >= 0;
+  const int64_t req = p.valid_req[b];
+  const int32_t *btr = p.block_table_l + req * mb;
+  if (tid < DSUB) s_dims[tid] = p.dims[tid];
+  for (int d = tid; d < p.fine_dsub; d += NFA_BLOCK) s_fdims[d] = p.fine_dims[d];
+  s_hist[tid] = 0;
+  s_hist[NFA_BLOCK + tid] = 0;
+  // pages past the block-table width are never scored (selector:205-206)
+  const int kt_eff = imin(L > 0 ? (L + bs - 1) / bs : 0, mb);
+  const int last_blk = L > 0 ? (L - 1) / bs : -1;
+  const bool owns_last =
+      last_blk >= t0 && last_blk < t0 + NFA_BLOCK && last_blk < mb;
 
-  NFA_MARK(clk_tile, 1);
-  // 2. page statistics: latest page, or the whole tile on a rebuild
+  // ---- second round trip: request state, statistics (speculative) -------
   const int prev = p.stats_len_l[req];
+  const bool skip_far = p.skip_far_l[req] != 0;
+  const bool skip_near = p.skip_near_l[req] != 0;
+  const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
+  const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
+  bool fp0 = false, np0 = false;
+  if (t < kt_eff) {
+    const RowGeo g0 = row_geo(p, L, false, false);
+    pools(p, g0, t, &fp0, &np0);
+  }
+  const bool want_mm = (fp0 && far_mm) || (np0 && near_mm);
+  const bool want_sum = (fp0 && !far_mm) || (np0 && !near_mm);
+  uint4 rmn[REG ? NC : 1], rmx[REG ? NC : 1], rsm[REG ? NC : 1];
+  auto load_regs = [&]() {
+    if constexpr (REG) {
+      const KV *smin = (const KV *)p.stat_min_l;
+      const KV *smax = (const KV *)p.stat_max_l;
+      const KV *ssum = (const KV *)p.stat_sum_l;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int64_t base = stat_index<KV>(p, req, kv, c * CH, t, DSUB);
+        rmn[c] = rmx[c] = rsm[c] = make_uint4(0u, 0u, 0u, 0u);
+        if (want_mm) {
+          rmn[c] = *reinterpret_cast<const uint4 *>(smin + base);
+          rmx[c] = *reinterpret_cast<const uint4 *>(smax + base);
+        }
+        if (want_sum) rsm[c] = *reinterpret_cast<const uint4 *>(ssum + base);
+      }
+    }
+  };
+  load_regs();
+  // the decode token's key row is read from k_new for the statistics when
+  // the fused write targets the slot of token L-1
+  const KV *new_row = nullptr;
+  int last_phys = 0;
+  if (owns_last && active) {
+    const int ph = btr[imin((L - 1) / p.page, mb - 1)];
+    last_phys = safe_page(p, ph);
+    if (p.k_new != nullptr) {
+      const int slot = p.slots[b];
+      if (slot >= 0 && slot / p.page < p.pool_pages &&
+          slot == ph * p.page + (L - 1) % p.page)
+        new_row = (const KV *)p.k_new + ((int64_t)b * p.hkv + kv) * p.head_dim;
+    }
+  }
+  __syncthreads();
+  NFA_MARK(clk_tile, 1);
+
+  // decode write of the current token (selector:1030-1061), fire and forget
+  if (p.k_new != nullptr && active && owns_last) decode_write<KV>(p, b, kv);
+
+  // scaled, bf16-rounded query rows of this kv group (selector:943-963)
+  const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kv * G * p.q_stride_h;
+  for (int i = tid; i < G * DSUB; i += NFA_BLOCK) {
+    const int j = i / DSUB;
+    const int d = i % DSUB;
+    const float qv = load_any(p.q, qrow + (int64_t)j * p.q_stride_h + s_dims[d],
+                              p.q_dtype);
+    s_qf[i] = bf16r(qv * p.scale);
+  }
+  NFA_MARK(clk_tile, 2);
+
+  // ---- page statistics: latest page, or the whole tile on a rebuild -----
   const bool do_stats = active && L > 0 && !(skip_far && skip_near);
   const bool incremental = prev > 0 && L == prev + 1;
-  if (do_stats && (!incremental || owns_last)) {
-    const int pg_lo = incremental ? last_blk : t0;
-    const int pg_hi = incremental ? last_blk + 1 : imin(t0 + NFA_BLOCK, kt_eff);
-    // aligned 16-byte runs of L1 dims -> vector path
-    constexpr int CH = Elem<KV>::kChunk;
-    int *s_coff = (int *)s_stage;              // DSUB / CH chunk offsets
-    int *s_tphys = s_coff + 32;                // physical page per page
-    __shared__ int s_vec;
+  const bool page_phys = (p.page % bs) == 0;
+  if (do_stats && incremental && owns_last) {
+    stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims,
+                                s_stage, new_row, s_last);
+  } else if (do_stats && !incremental) {
+    const int pg_lo = t0;
+    const int pg_hi = imin(t0 + NFA_BLOCK, kt_eff);
+    int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
     if (tid == 0) {
       bool vec = true;
-      for (int c = 0; vec && c < DSUB / CH; ++c) {
+      for (int c = 0; vec && c < NC; ++c) {
         const int first = s_dims[c * CH];
         vec = (first % CH) == 0;
         for (int e = 1; vec && e < CH; ++e) vec = s_dims[c * CH + e] == first + e;
         s_coff[c] = first;
       }
-      s_vec = vec;
+      s_misc[1] = vec;
     }
-    const bool page_phys = (p.page % bs) == 0;
     if (page_phys) {
-      const int32_t *btr = p.block_table_l + req * p.max_blocks;
       for (int i = tid; i < pg_hi - pg_lo; i += NFA_BLOCK) {
-        const int lp = imin(((pg_lo + i) * bs) / p.page, p.max_blocks - 1);
+        const int lp = imin(((pg_lo + i) * bs) / p.page, mb - 1);
         s_tphys[i] = safe_page(p, btr[lp]);
       }
     }
     __syncthreads();
-    if (s_vec) {
+    if (s_misc[1]) {
       compute_stats_vec<DSUB, KV>(p, req, kv, L, pg_lo, pg_hi, s_coff,
-                                  page_phys ? s_tphys : nullptr);
+                                  page_phys ? s_tphys : nullptr, new_row, L - 1,
+                                  nullptr);
     } else {
       __syncthreads();
-      compute_stats<DSUB, KV>(p, req, kv, L, pg_lo, pg_hi, s_stage, s_dims);
+      compute_stats<DSUB, KV>(p, req, kv, L, pg_lo, pg_hi, s_stage, s_dims,
+                              page_phys ? s_tphys : nullptr, new_row, L - 1,
+                              nullptr);
     }
-  }
-  NFA_MARK(clk_tile, 2);
-
-  // 3. scaled, bf16-rounded query rows of this kv group (selector:943-963)
-  for (int i = tid; i < G * DSUB; i += NFA_BLOCK) {
-    const int j = i / DSUB;
-    const int d = i % DSUB;
-    const int64_t qi = (int64_t)b * p.q_stride_b +
-                       (int64_t)(kv * G + j) * p.q_stride_h + s_dims[d];
-    const float qv = load_any(p.q, qi, p.q_dtype);
-    s_qf[i] = bf16r(qv * p.scale);
+    // rebuilt statistics: complete the stores, drop cached lines, read back
+    __threadfence();
   }
   __syncthreads();
+  if (do_stats && !incremental) {
+    __threadfence();
+    load_regs();
+  }
   NFA_MARK(clk_tile, 3);
 
-  // 4. L1 scores, one page per thread
+  // ---- L1 scores, one page per thread ------------------------------------
   const RowGeo geo = row_geo(p, L, skip_far, skip_near);
-  const int t = t0 + tid;
   uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
   if (do_stats && t < kt_eff) {
     bool fp, np;
     pools(p, geo, t, &fp, &np);
     if (fp || np) {
-      const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
-      const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
       const bool need_mm = (fp && far_mm) || (np && near_mm);
       const bool need_avg = (fp && !far_mm) || (np && !near_mm);
+      const bool from_lds = incremental && t == last_blk;
       uint16_t mm, avg;
-      l1_page_scores<DSUB, KV>(p, req, kv, t, G, s_qf, need_mm, need_avg, &mm,
-                               &avg);
+      if constexpr (REG) {
+        float kmin[DSUB], kmax[DSUB], kavg[DSUB];
+        if (from_lds) {
+#pragma unroll
+          for (int d = 0; d < DSUB; ++d) {
+            kmin[d] = s_last[d];
+            kmax[d] = s_last[DSUB + d];
+            kavg[d] = s_last[2 * DSUB + d];
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            unpack_chunk<KV>(rmn[c], kmin + c * CH);
+            unpack_chunk<KV>(rmx[c], kmax + c * CH);
+            unpack_chunk<KV>(rsm[c], kavg + c * CH);
+          }
+        }
+        if (need_avg) {
+          // x / bs == x * (1 / bs) exactly when bs is a power of two
+          const float bsf = (float)bs;
+          if ((bs & (bs - 1)) == 0) {
+            const float inv = 1.0f / bsf;
+#pragma unroll
+            for (int d = 0; d < DSUB; ++d) kavg[d] = bf16r(kavg[d] * inv);
+          } else {
+#pragma unroll
+            for (int d = 0; d < DSUB; ++d) kavg[d] = bf16r(kavg[d] / bsf);
+          }
+        }
+        l1_scores_regs<DSUB>(kmin, kmax, kavg, s_qf, G, need_mm, need_avg, &mm,
+                             &avg);
+      } else {
+        l1_scores_mem<DSUB, KV>(p, req, kv, t, s_qf, G, need_mm, need_avg,
+                                from_lds ? s_last : nullptr, &mm, &avg);
+      }
       if (fp) far_bits = far_mm ? mm : avg;
       if (np) near_bits = near_mm ? mm : avg;
     }
   }
   if (p.dbg_far != nullptr && t < kt_eff) {
-    p.dbg_far[(int64_t)row * p.max_blocks + t] = far_bits;
-    p.dbg_near[(int64_t)row * p.max_blocks + t] = near_bits;
+    p.dbg_far[(int64_t)row * mb + t] = far_bits;
+    p.dbg_near[(int64_t)row * mb + t] = near_bits;
   }
 
-  NFA_MARK(clk_tile, 4);
-  // 5. exact top-k of this tile
-  tile_topk(score_key(far_bits), t, p.k_f,
-            part_far + ((int64_t)row * ntiles + tile) * p.k_f, s_key, s_hist,
-            s_tmp);
-  tile_topk(score_key(near_bits), t, p.k_n,
-            part_near + ((int64_t)row * ntiles + tile) * p.k_n, s_key, s_hist,
-            s_tmp);
-
-  NFA_MARK(clk_tile, 5);
-  // 6. arrival; the last workgroup of the row runs the tail
+  // ---- publish keys and the high-byte histograms ------------------------
+  {
+    // a page belongs to at most one pool: far pages lie below near_start,
+    // near pages at or above it
+    const uint32_t fk = score_key(far_bits);
+    const uint32_t nk = score_key(near_bits);
+    g_keys[t] = (uint16_t)(fk ? fk : nk);
+    if (fk) atomicAdd(&s_hist[fk >> 8], 1);
+    if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
+  }
   __syncthreads();
+  {
+    const int hf = s_hist[tid];
+    const int hn = s_hist[256 + tid];
+    if (hf) atomicAdd(&g_hist[tid], hf);
+    if (hn) atomicAdd(&g_hist[256 + tid], hn);
+  }
+  NFA_MARK(clk_tile, 4);
+
+  // ---- arrival; the last workgroup of the row runs the tail --------------
   if (tid == 0) {
-    __threadfence();
-    const unsigned int before = atomicAdd(&row_cnt[row], 1u);
-    s_tmp[0] = before == (unsigned int)(ntiles - 1);
-    const unsigned int rb = atomicAdd(&req_cnt[b], 1u);
+    // every workgroup of the request has read stats_len once all arrived
+    const unsigned int rb = __hip_atomic_fetch_add(
+        &req_cnt[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (rb == (unsigned int)(ntiles * p.hkv - 1)) {
-      // every workgroup of this request has read stats_len
       if (do_stats) p.stats_len_l[req] = L;
-      atomicExch(&req_cnt[b], 0u);
+      __hip_atomic_store(&req_cnt[b], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  __syncthreads();
-  if (!s_tmp[0]) return;
-  __threadfence();
-  if (tid == 0) atomicExch(&row_cnt[row], 0u);
+  if (!arrive_last(&row_cnt[row], (unsigned int)ntiles, &s_misc[0])) return;
 
-  // =========================== tail stage ================================
-  // (its LDS overlaps the tile stage's, which is no longer used)
-  int *s_pages = (int *)(smem + sd.o_pages);
-  int *s_pgoff = (int *)(smem + sd.o_pgoff);
-  int *s_pphys = (int *)(smem + sd.o_pphys);
-  uint16_t *s_cand = (uint16_t *)(smem + sd.o_cand);
-  int *s_l0 = (int *)(smem + sd.o_l0);
-  int *s_l1 = (int *)(smem + sd.o_l1);
-  int *s_mid = (int *)(smem + sd.o_mid);
-  uint64_t *s_sel = (uint64_t *)(smem + sd.o_sel);
-  int *s_fp = (int *)(smem + sd.o_fp);
-  int *s_np = (int *)(smem + sd.o_np);
-  float *s_qg = (float *)(smem + sd.o_qg);
-  int *s_choff = (int *)(smem + sd.o_choff);
-  int *s_fdims = (int *)(smem + sd.o_fdims);
-  uint16_t *s_m16 = sd.merge_lds ? (uint16_t *)(smem + sd.o_union) : nullptr;
-  __shared__ int s_misc[8];
-  __syncthreads();
+  // =========================== tail ======================================
+  // (its LDS overlaps the tile stage's private part, no longer used)
+  uint16_t *s_keys = (uint16_t *)(smem + sd.a_keys);
+  uint32_t *s_cbits = (uint32_t *)(smem + sd.a_cbits);
+  const bool dbg = p.dbg_i_f != nullptr;
+  uint32_t *s_dbf = (uint32_t *)(smem + sd.a_dbf);
+  uint32_t *s_dbn = (uint32_t *)(smem + sd.a_dbn);
+  uint64_t *s_dsel = (uint64_t *)(smem + sd.a_dsel);
   NFA_MARK(clk_tail, 0);
 
   const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
@@ -1057,169 +1046,600 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     p.dbg_bounds[b * 3 + 1] = lb.upper;
     p.dbg_bounds[b * 3 + 2] = lb.quota;
   }
-
-  // L1 merge (skipped pools give 0..K-1, which the filler rule reproduces)
-  int nfv = 0, nnv = 0;
-  if (p.k_f > 0)
-    nfv = merge_l1(part_far + (int64_t)row * ntiles * p.k_f, ntiles * p.k_f,
-                   p.k_f, s_fp, s_sel, s_m16, s_hist, s_tmp);
-  if (p.k_n > 0)
-    nnv = merge_l1(part_near + (int64_t)row * ntiles * p.k_n, ntiles * p.k_n,
-                   p.k_n, s_np, s_sel, s_m16, s_hist, s_tmp);
-  __syncthreads();
-  NFA_MARK(clk_tail, 1);
-  if (p.dbg_i_f != nullptr) {
-    for (int i = tid; i < p.k_f; i += NFA_BLOCK)
-      p.dbg_i_f[(int64_t)row * p.k_f + i] = s_fp[i];
-    for (int i = tid; i < p.k_n; i += NFA_BLOCK)
-      p.dbg_i_n[(int64_t)row * p.k_n + i] = s_np[i];
-  }
-
-  // candidate pages in slot order: far | near | sink bypass | SWA bypass
-  const int spl = p.sink_tokens / bs;
-  const bool byp0_keep = (p.sink_tokens % bs) != 0;
-  bool byp1_keep = (lb.lo % bs != 0) && (lb.lo / bs >= spl);
-  if (p.sink_tokens % bs != 0) byp1_keep = byp1_keep && (lb.lo / bs != spl);
-  const int np_all = sd.np;
-  auto slot_page = [&](int s) -> int {
-    if (s < p.k_f) return s < nfv ? s_fp[s] : -1;
-    s -= p.k_f;
-    if (s < p.k_n) return s < nnv ? s_np[s] : -1;
-    s -= p.k_n;
-    if (s == 0) return byp0_keep ? spl : -1;
-    return byp1_keep ? lb.lo / bs : -1;
-  };
-  // unique pages sorted ascending; candidates only exist when quota > 0
+  // candidate tokens lie in [tok_lo, tok_hi) and exist only when quota > 0
   const int tok_lo = imax(p.sink_tokens, lb.lower);
   const int tok_hi = imin(imin(lb.lo, L), lb.upper);
-  int *s_sp = (int *)(smem + sd.o_sp);
-  int *s_rank = (int *)(smem + sd.o_rank);
-  for (int s = tid; s < np_all; s += NFA_BLOCK)
-    s_sp[s] = lb.quota > 0 ? slot_page(s) : -1;
+  const bool any_cand = lb.quota > 0 && tok_hi > tok_lo;
+  const int near_start = geo.near_start;
+
+  // row histograms into LDS, reset for the next launch
+  {
+    const int hf = atomicExch(&g_hist[tid], 0);
+    const int hn = atomicExch(&g_hist[256 + tid], 0);
+    s_hist[tid] = hf;
+    s_hist[256 + tid] = hn;
+    s_hist[512 + tid] = 0;
+    s_hist[768 + tid] = 0;
+  }
+  for (int w = tid; w < sd.words; w += NFA_BLOCK) {
+    s_cbits[w] = 0u;
+    if (dbg) {
+      s_dbf[w] = 0u;
+      s_dbn[w] = 0u;
+    }
+  }
+  if (sd.nseg == 1) stage_keys(g_keys, 0, sd.segc, s_keys);
   __syncthreads();
-  for (int s = tid; s < np_all; s += NFA_BLOCK) {
-    const int pg = s_sp[s];
-    bool first = pg >= 0;
-    for (int j = 0; j < s && first; ++j) first = s_sp[j] != pg;
-    s_rank[s] = first ? 0 : -1;
+  // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
+  if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 8);
+  if (wave_id() == 1) wave_threshold_bin(s_hist + 256, p.k_n, s_tmp + 12);
+  __syncthreads();
+  const int hbf = s_tmp[8], hbn = s_tmp[12];
+  const int seg_pages = NFA_BLOCK * sd.segc;
+  const int my0 = tid * sd.segc;  // first page of this thread in a segment
+  if (hbf >= 0 || hbn >= 0) {
+    // refinement: low-byte histograms of the keys in the threshold bins
+    for (int sg = 0; sg < sd.nseg; ++sg) {
+      const int seg_base = sg * seg_pages;
+      if (sd.nseg > 1) {
+        __syncthreads();
+        stage_keys(g_keys, seg_base, sd.segc, s_keys);
+        __syncthreads();
+      }
+      const int n = imin(sd.segc, kt_eff - seg_base - my0);
+      for (int i = 0; i < n; ++i) {
+        const uint32_t k = s_keys[my0 + i];
+        const bool near = seg_base + my0 + i >= near_start;
+        const int hb = near ? hbn : hbf;
+        if (k != 0u && (int)(k >> 8) == hb)
+          atomicAdd(&s_hist[(near ? 768 : 512) + (k & 255u)], 1);
+      }
+    }
+    __syncthreads();
+    if (wave_id() == 0 && hbf >= 0)
+      wave_threshold_bin(s_hist + 512, p.k_f - s_tmp[9], s_tmp + 16);
+    if (wave_id() == 1 && hbn >= 0)
+      wave_threshold_bin(s_hist + 768, p.k_n - s_tmp[13], s_tmp + 20);
+    __syncthreads();
+  }
+  const PoolThr tf = pool_threshold(p.k_f, s_tmp + 8, s_tmp + 16, s_hist + 512);
+  const PoolThr tn = pool_threshold(p.k_n, s_tmp + 12, s_tmp + 20, s_hist + 768);
+  NFA_MARK(clk_tail, 1);
+
+  // ---- selected pages -> candidate page bitmap ---------------------------
+  const bool ordered = tie_cut(tf) || tie_cut(tn) || dbg;
+  int carry[4] = {0, 0, 0, 0};  // far >T, far ==T, near >T, near ==T
+  for (int sg = 0; sg < sd.nseg; ++sg) {
+    const int seg_base = sg * seg_pages;
+    if (sd.nseg > 1) {
+      __syncthreads();
+      stage_keys(g_keys, seg_base, sd.segc, s_keys);
+      __syncthreads();
+    }
+    const int n = imin(sd.segc, kt_eff - seg_base - my0);
+    int cnt[4] = {0, 0, 0, 0};
+    if (ordered) {
+      for (int i = 0; i < n; ++i) {
+        const uint32_t k = s_keys[my0 + i];
+        const int o = seg_base + my0 + i >= near_start ? 2 : 0;
+        const uint32_t T = o ? (uint32_t)tn.T : (uint32_t)tf.T;
+        cnt[o] += k > T;
+        cnt[o + 1] += (k == T && k != 0u);
+      }
+      int tot4[4];
+      block_scan_n<4>(cnt, s_tmp + 32, tot4);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        cnt[q] += carry[q];
+        carry[q] += tot4[q];
+      }
+    }
+    int eqf = cnt[1], eqn = cnt[3];
+    int posf = cnt[0] + imin(cnt[1], tf.need);
+    int posn = cnt[2] + imin(cnt[3], tn.need);
+    for (int i = 0; i < n; ++i) {
+      const uint32_t k = s_keys[my0 + i];
+      if (k == 0u) continue;
+      const int page = seg_base + my0 + i;
+      const bool near = page >= near_start;
+      bool sel;
+      if (!near) {
+        sel = k > (uint32_t)tf.T;
+        if (k == (uint32_t)tf.T) {
+          sel = eqf < tf.need;
+          ++eqf;
+        }
+      } else {
+        sel = k > (uint32_t)tn.T;
+        if (k == (uint32_t)tn.T) {
+          sel = eqn < tn.need;
+          ++eqn;
+        }
+      }
+      if (!sel) continue;
+      const uint32_t bit = 1u << (page & 31);
+      if (any_cand && page * bs < tok_hi && page * bs + bs > tok_lo)
+        atomicOr(&s_cbits[page >> 5], bit);
+      if (dbg) {
+        if (!near) {
+          s_dsel[posf++] = ((uint64_t)k << 32) | (uint32_t)page;
+          atomicOr(&s_dbf[page >> 5], bit);
+        } else {
+          s_dsel[p.k_f + posn++] = ((uint64_t)k << 32) | (uint32_t)page;
+          atomicOr(&s_dbn[page >> 5], bit);
+        }
+      }
+    }
   }
   __syncthreads();
+  if (tid == 0 && any_cand) {
+    // sink and SWA bypass pages (selector:1195-1251)
+    const int spl = p.sink_tokens / bs;
+    const bool byp0_keep = (p.sink_tokens % bs) != 0;
+    bool byp1_keep = (lb.lo % bs != 0) && (lb.lo / bs >= spl);
+    if (p.sink_tokens % bs != 0) byp1_keep = byp1_keep && (lb.lo / bs != spl);
+    const int bp0 = byp0_keep ? spl : -1;
+    const int bp1 = byp1_keep ? lb.lo / bs : -1;
+    if (bp0 >= 0 && bp0 < sd.kstride && bp0 * bs < tok_hi && bp0 * bs + bs > tok_lo)
+      s_cbits[bp0 >> 5] |= 1u << (bp0 & 31);
+    if (bp1 >= 0 && bp1 < sd.kstride && bp1 * bs < tok_hi && bp1 * bs + bs > tok_lo)
+      s_cbits[bp1 >> 5] |= 1u << (bp1 & 31);
+  }
+  __syncthreads();
+  // compaction: sorted unique candidate pages, then their physical pages
+  const int wpt = (sd.words + NFA_BLOCK - 1) / NFA_BLOCK;
+  const int w0 = tid * wpt;
+  const int w1 = imin(w0 + wpt, sd.words);
+  int *s_pages = (int *)(smem + sd.a_pages);
   int np_u;
   {
-    int cnt = 0;
-    for (int s = tid; s < np_all; s += NFA_BLOCK) {
-      if (s_rank[s] < 0) continue;
-      ++cnt;
-    }
-    block_scan_exclusive(cnt, s_tmp, &np_u);
-  }
-  for (int s = tid; s < np_all; s += NFA_BLOCK) {
-    if (s_rank[s] < 0) continue;
-    const int pg = s_sp[s];
-    int r = 0;
-    for (int j = 0; j < np_all; ++j) r += (s_rank[j] >= 0) && (s_sp[j] < pg);
-    s_pages[r] = pg;
-  }
-  __syncthreads();
-  // token counts per page and exclusive offsets
-  int n_cand;
-  {
-    // np_u <= np_all; process in chunks of the block
-    int carry = 0;
-    for (int base = 0; base < np_u; base += NFA_BLOCK) {
-      const int i = base + tid;
-      int c = 0;
-      if (i < np_u) {
-        const int pg = s_pages[i];
-        const int a = imax(pg * bs, tok_lo);
-        const int e = imin(pg * bs + bs, tok_hi);
-        c = e > a ? e - a : 0;
+    int c1 = 0;
+    for (int w = w0; w < w1; ++w) c1 += __popc(s_cbits[w]);
+    int pos = block_scan_exclusive(c1, s_tmp, &np_u);
+    for (int w = w0; w < w1; ++w) {
+      uint32_t bits = s_cbits[w];
+      while (bits) {
+        if (pos < sd.np) s_pages[pos] = w * 32 + __ffs(bits) - 1;
+        ++pos;
+        bits &= bits - 1u;
       }
-      int tot;
-      const int ex = block_scan_exclusive(c, s_tmp, &tot);
-      if (i < np_u) s_pgoff[i] = carry + ex;
-      carry += tot;
     }
-    if (tid == 0) s_pgoff[np_u] = carry;
-    n_cand = carry;
   }
-  // pages that contribute no token keep offset == next offset; harmless
   __syncthreads();
-
-  NFA_MARK(clk_tail, 2);
-  // physical page of every candidate page (one lookup per page when a
-  // statistics block never straddles a physical page)
+  np_u = imin(np_u, sd.np);
   {
-    const int32_t *btr = p.block_table_l + req * p.max_blocks;
+    int *g_pages = (int *)(ws + sd.w_pages) + (int64_t)row * sd.np;
+    int *g_pphys = (int *)(ws + sd.w_pphys) + (int64_t)row * sd.np;
     for (int i = tid; i < np_u; i += NFA_BLOCK) {
-      const int lp = imin((s_pages[i] * bs) / p.page, p.max_blocks - 1);
-      s_pphys[i] = safe_page(p, btr[lp]);
+      const int pg = s_pages[i];
+      g_pages[i] = pg;
+      g_pphys[i] = btr[imin((pg * bs) / p.page, mb - 1)];
+    }
+    if (tid == 0) {
+      ((int *)(ws + sd.w_npu))[row] = np_u;
+      if (p.dbg_cand_count != nullptr)
+        p.dbg_cand_count[row] = imin(np_u * bs, p.dbg_cand_cap);
+    }
+    if (tid == 1 && row == 0) {
+      // the L2 dims as aligned 16-byte runs (the vector path of kernel B)
+      const int nch = p.fine_dsub / CH;
+      bool vec = (p.fine_dsub % CH == 0) && nch <= 16;
+      for (int c = 0; vec && c < nch; ++c) {
+        const int first = s_fdims[c * CH];
+        vec = (first % CH) == 0;
+        for (int e = 1; vec && e < CH; ++e) vec = s_fdims[c * CH + e] == first + e;
+      }
+      int *g_vec = (int *)(ws + sd.w_l2vec);
+      g_vec[0] = vec ? nch : 0;
     }
   }
-  // grouped query over the L2 dims (selector:979-1002)
-  for (int d = tid; d < p.fine_dsub; d += NFA_BLOCK) {
-    const int dim = p.fine_dims[d];
-    s_fdims[d] = dim;
-    float acc = 0.0f;
-    for (int j = 0; j < G; ++j) {
-      const int64_t qi = (int64_t)b * p.q_stride_b +
-                         (int64_t)(kv * G + j) * p.q_stride_h + dim;
-      acc = acc + bf16r(load_any(p.q, qi, p.q_dtype) * p.scale);
+  // L1 debug outputs: I_F / I_N (selector:1766-1803 order: valid pages by
+  // (score desc, page asc), then -inf fillers by ascending page)
+  if (dbg) {
+    for (int pool = 0; pool < 2; ++pool) {
+      const int K = pool == 0 ? p.k_f : p.k_n;
+      const int nsel = pool == 0 ? tf.nsel : tn.nsel;
+      const uint64_t *sel = s_dsel + (pool == 0 ? 0 : p.k_f);
+      const uint32_t *bm = pool == 0 ? s_dbf : s_dbn;
+      int32_t *out = (pool == 0 ? p.dbg_i_f + (int64_t)row * p.k_f
+                                : p.dbg_i_n + (int64_t)row * p.k_n);
+      for (int i = tid; i < nsel; i += NFA_BLOCK) {
+        const uint64_t ki = sel[i];
+        const uint32_t vi = (uint32_t)(ki >> 32), ti = (uint32_t)ki;
+        int rank = 0;
+        for (int j = 0; j < nsel; ++j) {
+          const uint64_t kj = sel[j];
+          const uint32_t vj = (uint32_t)(kj >> 32), tj = (uint32_t)kj;
+          rank += (vj > vi) || (vj == vi && tj < ti);
+        }
+        out[rank] = (int)ti;
+      }
+      const int nfill = K - nsel;  // uniform
+      if (nfill > 0) {
+        int z = 0;
+        for (int w = w0; w < w1; ++w) z += 32 - __popc(bm[w]);
+        int tz;
+        int r = block_scan_exclusive(z, s_tmp, &tz);
+        for (int w = w0; w < w1 && r < nfill; ++w) {
+          uint32_t zeros = ~bm[w];
+          while (zeros && r < nfill) {
+            out[nsel + r++] = w * 32 + __ffs(zeros) - 1;
+            zeros &= zeros - 1u;
+          }
+        }
+      }
     }
-    s_qg[d] = acc;
   }
-  __syncthreads();
-  // vector path when the L2 dims are aligned runs of 16 bytes
-  constexpr int CH = Elem<KV>::kChunk;
-  const int nch = p.fine_dsub / CH;
-  if (tid == 0) {
-    bool vec = (p.fine_dsub % CH == 0) && (nch == 4 || nch == 8 || nch == 16);
-    for (int c = 0; vec && c < nch; ++c) {
-      const int first = s_fdims[c * CH];
-      vec = (first % CH) == 0;
-      for (int e = 1; vec && e < CH; ++e) vec = s_fdims[c * CH + e] == first + e;
-      s_choff[c] = first;
-    }
-    s_misc[1] = vec;
-  }
-  __syncthreads();
+  NFA_MARK(clk_tail, 2);
+}
 
-  NFA_MARK(clk_tail, 3);
-  // L2 logits (selector:459-516)
-  CandView cv{s_pages, s_pgoff, np_u, tok_lo, bs};
-  if (s_misc[1]) {
-    if (nch == 4)
-      l2_logits_vec<KV, 4>(p, cv, n_cand, kv, row, s_pphys, s_choff, s_qg, s_cand);
-    else if (nch == 8)
-      l2_logits_vec<KV, 8>(p, cv, n_cand, kv, row, s_pphys, s_choff, s_qg, s_cand);
-    else
-      l2_logits_vec<KV, 16>(p, cv, n_cand, kv, row, s_pphys, s_choff, s_qg, s_cand);
-  } else {
-    l2_logits_scalar<KV>(p, cv, n_cand, kv, row, s_pphys, s_fdims, s_qg, s_cand);
-  }
-  if (p.dbg_cand_count != nullptr && tid == 0) p.dbg_cand_count[row] = n_cand;
-  __syncthreads();
+// ---------------------------------------------------------------------------
+// kernel B: L2 logits, top-quota selection and union
+// ---------------------------------------------------------------------------
 
-  NFA_MARK(clk_tail, 4);
-  // L2 top-quota + hole fill (+ fixed near quota), selector:519-566, 873-940
-  if (tid == 0) s_misc[0] = 0;
+// Candidate tokens in the dense page-major layout: slot i belongs to page
+// pages[i / bs], token pages[i / bs] * bs + i % bs.
+struct DenseView {
+  const uint16_t *keys;
+  const int *pages;
+  const int *pphys;  // raw block-table entry of every page (page_phys mode)
+  const int32_t *bt;
+  int n, bs, page, mb;
+  bool page_phys;
+  __device__ __forceinline__ int tok(int i) const {
+    const int pi = i / bs;
+    return pages[pi] * bs + (i - pi * bs);
+  }
+  __device__ __forceinline__ int slot_of(int i, int t) const {
+    const int ph = page_phys ? pphys[i / bs] : bt[imin(t / page, mb - 1)];
+    return ph * page + t % page;
+  }
+  __device__ __forceinline__ int slot_of_token(int t) const {
+    return bt[imin(t / page, mb - 1)] * page + t % page;
+  }
+};
+
+struct RegionLists {
+  int *l0, *l0x, *l1, *l1x, *mid, *mslot;
+};
+
+// One L2 region (selector:519-566): top-quota of the dense candidates whose
+// token lies in [rlo, rhi) (every candidate when !masked), ties to the lower
+// token, then hole fill with the smallest ids of [rlo, rhi) not chosen and
+// the sink filter; appended in ascending order to mid / mslot at *mid_count.
+// `hist` needs 512 ints, `tmp` 48.
+__device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked,
+                                                int rlo, int rhi, int quota,
+                                                int sink, const RegionLists &rl,
+                                                int *mid_count, int *hist,
+                                                int *tmp) {
+  if (quota <= 0) return;
+  const int tid = threadIdx.x;
+  const int n = dv.n;
+  auto key = [&](int i) -> uint32_t {
+    uint32_t v = dv.keys[i];
+    if (masked && v != 0u) {
+      const int t = dv.tok(i);
+      if (t < rlo || t >= rhi) v = 0u;
+    }
+    return v;
+  };
+  hist[tid] = 0;
+  hist[NFA_BLOCK + tid] = 0;
   __syncthreads();
-  auto index_of_token = [&](int x) {  // first candidate index with token >= x
-    int lo = 0, hi = n_cand;
+  for (int i = tid; i < n; i += NFA_BLOCK) {
+    const uint32_t v = key(i);
+    if (v) atomicAdd(&hist[v >> 8], 1);
+  }
+  __syncthreads();
+  if (wave_id() == 0) wave_threshold_bin(hist, quota, tmp + 8);
+  __syncthreads();
+  const int hb = tmp[8];
+  const int above = tmp[9];
+  const int total = tmp[10];
+  uint32_t T = 0u;
+  int need = 0;
+  if (hb >= 0) {
+    for (int i = tid; i < n; i += NFA_BLOCK) {
+      const uint32_t v = key(i);
+      if (v != 0u && (int)(v >> 8) == hb) atomicAdd(&hist[256 + (v & 255u)], 1);
+    }
+    __syncthreads();
+    if (wave_id() == 0) wave_threshold_bin(hist + 256, quota - above, tmp + 12);
+    __syncthreads();
+    T = ((uint32_t)hb << 8) | (uint32_t)tmp[12];
+    need = quota - above - tmp[13];
+  }
+  const int nch = total < quota ? total : quota;
+  // ordered emission, one contiguous run of slots per thread
+  const int per = (n + NFA_BLOCK - 1) / NFA_BLOCK;
+  const int ia = tid * per;
+  const int ib = imin(n, ia + per);
+  int c[2] = {0, 0};
+  for (int i = ia; i < ib; ++i) {
+    const uint32_t v = key(i);
+    c[0] += v > T;
+    c[1] += (v == T && v != 0u);
+  }
+  int tot2[2];
+  block_scan_n<2>(c, tmp + 32, tot2);
+  {
+    int eq = c[1];
+    int pos = c[0] + (c[1] < need ? c[1] : need);
+    for (int i = ia; i < ib; ++i) {
+      const uint32_t v = key(i);
+      bool sel = v > T;
+      if (v == T && v != 0u) {
+        sel = eq < need;
+        ++eq;
+      }
+      if (sel) {
+        const int t = dv.tok(i);
+        rl.l0[pos] = t;
+        rl.l0x[pos] = dv.slot_of(i, t);
+        ++pos;
+      }
+    }
+  }
+  __syncthreads();
+  // hole fill: the (quota - nch) smallest ids of [rlo, rhi) not chosen
+  const int nfill_req = quota - nch;
+  for (int i = tid; i < nfill_req; i += NFA_BLOCK) {
+    int lo = 0, hi = nch;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      if (cv.token(mid) < x)
+      if (rl.l0[mid] - rlo - mid <= i)
         lo = mid + 1;
       else
         hi = mid;
     }
-    return lo;
-  };
+    const int id = rlo + i + lo;
+    rl.l1[i] = id < rhi ? id : 0x7FFFFFFF;
+    rl.l1x[i] = id < rhi ? dv.slot_of_token(id) : 0;
+  }
+  __syncthreads();
+  // fill ids increase with i, so the valid ones form a prefix
+  int nfill = 0;
+  {
+    int lo = 0, hi = nfill_req;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (rl.l1[mid] != 0x7FFFFFFF)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    nfill = lo;
+  }
+  const int drop = lower_bound_i32(rl.l0, nch, sink) +
+                   lower_bound_i32(rl.l1, nfill, sink);
+  const int base_out = *mid_count;
+  for (int j = tid; j < nch; j += NFA_BLOCK) {
+    const int v = rl.l0[j];
+    if (v >= sink) {
+      const int pos = base_out + j + lower_bound_i32(rl.l1, nfill, v) - drop;
+      rl.mid[pos] = v;
+      rl.mslot[pos] = rl.l0x[j];
+    }
+  }
+  for (int j = tid; j < nfill; j += NFA_BLOCK) {
+    const int v = rl.l1[j];
+    if (v >= sink) {
+      const int pos = base_out + j + lower_bound_i32(rl.l0, nch, v) - drop;
+      rl.mid[pos] = v;
+      rl.mslot[pos] = rl.l1x[j];
+    }
+  }
+  __syncthreads();
+  if (tid == 0) *mid_count = base_out + nch + nfill - drop;
+  __syncthreads();
+}
+
+template <typename KV>
+__global__ void __launch_bounds__(NFA_BLOCK)
+    nfa_l2_kernel(const NfaSelectParams p, const SelDims sd) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int CH = Elem<KV>::kChunk;
+  constexpr int TPS = NFA_BLOCK / kL2Slots;  // threads per dense slot
+  int *s_hist = (int *)(smem + sd.b_hist);
+  int *s_tmp = (int *)(smem + sd.b_tmp);
+  int *s_misc = (int *)(smem + sd.b_misc);
+  float *s_qg = (float *)(smem + sd.b_qg);
+  int *s_fdims = (int *)(smem + sd.b_fdims);
+  int *s_tok = (int *)(smem + sd.b_tok);
+
+  const int tid = threadIdx.x;
+  const int chunk = blockIdx.x;
+  const int row = blockIdx.y;
+  const int b = row / p.hkv;
+  const int kv = row % p.hkv;
+  const int G = p.hq / p.hkv;
+  const int bs = p.bs;
+  const int mb = p.max_blocks;
+  const int ntiles = sd.ntiles;
+  const int64_t clk_b = ((int64_t)row * (ntiles + 1) + ntiles) * 16 + 8;
+  if (chunk == 0) NFA_MARK(clk_b, 0);
+  unsigned char *ws = (unsigned char *)p.workspace;
+  unsigned int *bcnt = (unsigned int *)(ws + sd.w_bcnt);
+  const int *g_pages = (const int *)(ws + sd.w_pages) + (int64_t)row * sd.np;
+  const int *g_pphys = (const int *)(ws + sd.w_pphys) + (int64_t)row * sd.np;
+  uint16_t *g_dk = (uint16_t *)(ws + sd.w_dk) + (int64_t)row * sd.dstride;
+
+  // ---- first round trip: row scalars, candidate pages, L2 dims -----------
+  const int L = p.lengths[b];
+  const int64_t req = p.valid_req[b];
+  const int32_t *btr = p.block_table_l + req * mb;
+  const int np_u = ((const int *)(ws + sd.w_npu))[row];
+  const int nch = ((const int *)(ws + sd.w_l2vec))[0];  // 0: scalar L2 dims
+  const int n_dense = np_u * bs;
+  for (int d = tid; d < p.fine_dsub; d += NFA_BLOCK) s_fdims[d] = p.fine_dims[d];
+  const int sl = tid / TPS;   // dense slot of this thread within the chunk
+  const int part = tid % TPS; // which quarter of the slot's L2 dims it loads
+  const int i = chunk * kL2Slots + sl;
+  int tok = -1, phys = 0, pgphys = 0;
+  {
+    const int pi = i / bs;
+    if (pi < sd.np) {
+      const int pg = g_pages[pi];
+      pgphys = g_pphys[pi];
+      tok = pg * bs + (i - pi * bs);
+    }
+  }
+  // chunk offsets of this thread's part of the L2 dims
+  int coff[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int c = part + TPS * k;
+    if (c * CH < p.fine_dsub) coff[k] = imin(p.fine_dims[c * CH], p.head_dim - CH);
+  }
+  const bool scored = i < n_dense;  // uniform per slot
+  // ---- second round trip: the key rows of the slots, the query ----------
+  const bool skip_far = p.skip_far_l[req] != 0;
+  const bool skip_near = p.skip_near_l[req] != 0;
+  const bool page_phys = (p.page % bs) == 0;
+  const KV *kpool = (const KV *)p.k_pool_l;
+  uint4 *s_st4 = (uint4 *)(smem + sd.b_stage);
+  float *s_stf = (float *)(smem + sd.b_stage);
+  if (scored) {
+    phys = safe_page(p, page_phys ? pgphys : btr[imin(tok / p.page, mb - 1)]);
+    const KV *kr = kpool + kv_offset(p, phys, kv, tok % p.page);
+    if (nch > 0) {
+      uint4 r[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int c = part + TPS * k;
+        r[k] = c < nch ? *reinterpret_cast<const uint4 *>(kr + coff[k])
+                       : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int c = part + TPS * k;
+        if (c < nch) s_st4[sl * nch + c] = r[k];
+      }
+    }
+  }
+  if (part == 0) s_tok[sl] = scored ? tok : -1;
+  __syncthreads();  // s_fdims
+  if (scored && nch == 0) {
+    // L2 dims not in 16-byte runs: element loads, TPS threads per slot
+    const KV *kr = kpool + kv_offset(p, phys, kv, tok % p.page);
+    for (int d = part; d < p.fine_dsub; d += TPS)
+      s_stf[sl * p.fine_dsub + d] = Elem<KV>::load(kr + s_fdims[d]);
+  }
+  // grouped L2 query (selector:979-1002)
+  const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kv * G * p.q_stride_h;
+  for (int d = tid; d < p.fine_dsub; d += NFA_BLOCK) {
+    const int dim = s_fdims[d];
+    float qv[GMAX];
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j)
+      qv[j] = j < G ? load_any(p.q, qrow + (int64_t)j * p.q_stride_h + dim,
+                               p.q_dtype)
+                    : 0.0f;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j)
+      if (j < G) acc = acc + bf16r(qv[j] * p.scale);
+    s_qg[d] = acc;
+  }
+  __syncthreads();
+
+  // ---- L2 logits (selector:459-516): fp32 dot over the L2 dims in order --
+  const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
+  const int tok_lo = imax(p.sink_tokens, lb.lower);
+  const int tok_hi = imin(imin(lb.lo, L), lb.upper);
+  if (tid < kL2Slots) {
+    const int ii = chunk * kL2Slots + tid;
+    const int tk = s_tok[tid];
+    if (tk >= 0) {
+      uint16_t key = 0;
+      if (tk >= tok_lo && tk < tok_hi) {
+        float acc = 0.0f;
+        if (nch > 0) {
+          for (int c = 0; c < nch; ++c) {
+            float x[CH];
+            unpack_chunk<KV>(s_st4[tid * nch + c], x);
+#pragma unroll
+            for (int e = 0; e < CH; ++e) {
+              const float prod = x[e] * s_qg[c * CH + e];
+              acc = acc + prod;
+            }
+          }
+        } else {
+          for (int d = 0; d < p.fine_dsub; ++d) {
+            const float prod = s_stf[tid * p.fine_dsub + d] * s_qg[d];
+            acc = acc + prod;
+          }
+        }
+        const uint16_t bits = bf16_bits(acc);
+        key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
+        if (p.dbg_cand_tok != nullptr && ii < p.dbg_cand_cap) {
+          p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + ii] = tk;
+          p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + ii] =
+              bits == kNanBits ? kNegInfBits : bits;
+        }
+      } else if (p.dbg_cand_tok != nullptr && ii < p.dbg_cand_cap) {
+        p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + ii] = -1;
+      }
+      g_dk[ii] = key;
+    }
+  }
+  if (chunk == 0) NFA_MARK(clk_b, 1);
+
+  // ---- arrival; the last workgroup of the row selects ---------------------
+  if (!arrive_last(&bcnt[row], gridDim.x, &s_misc[0])) return;
+  NFA_MARK(clk_b, 2);
+
+  uint16_t *s_dk = (uint16_t *)(smem + sd.b_dk);
+  int *s_pages = (int *)(smem + sd.b_pages);
+  int *s_pphys = (int *)(smem + sd.b_pphys);
+  const RegionLists rl{(int *)(smem + sd.b_l0), (int *)(smem + sd.b_l0x),
+                       (int *)(smem + sd.b_l1), (int *)(smem + sd.b_l1x),
+                       (int *)(smem + sd.b_mid), (int *)(smem + sd.b_mslot)};
+  // protected ids; the gather slots of the first 256 are fetched now
+  int u0, u1, u2, u3;
+  protected_intervals(p, L, sd.prot, &u0, &u1, &u2, &u3);
+  const int nu = (u1 - u0) + (u3 - u2);
+  int pre_slot = 0;
+  if (!p.middle_only && tid < nu) {
+    const int x = tid < (u1 - u0) ? u0 + tid : u2 + (tid - (u1 - u0));
+    pre_slot = btr[imin(x / p.page, mb - 1)] * p.page + x % p.page;
+  }
+  // dense keys and candidate pages into LDS
+  {
+    const int n16 = (n_dense + 7) / 8;
+    const uint4 *src = reinterpret_cast<const uint4 *>(g_dk);
+    uint4 *dst = reinterpret_cast<uint4 *>(s_dk);
+    for (int u0 = 0; u0 < n16; u0 += 4 * NFA_BLOCK) {
+      uint4 r[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int u = u0 + tid + k * NFA_BLOCK;
+        r[k] = u < n16 ? src[u] : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int u = u0 + tid + k * NFA_BLOCK;
+        if (u < n16) dst[u] = r[k];
+      }
+    }
+    for (int k = tid; k < np_u; k += NFA_BLOCK) {
+      s_pages[k] = g_pages[k];
+      s_pphys[k] = g_pphys[k];
+    }
+    if (tid == 0) s_misc[2] = 0;  // middle count
+  }
+  __syncthreads();
+
+  // ---- L2 top-quota + hole fill (+ fixed near quota), selector:519-566,
+  //      873-940 -------------------------------------------------------------
+  const DenseView dv{s_dk, s_pages, s_pphys, btr, n_dense, bs, p.page, mb,
+                     page_phys};
   if (lb.quota > 0) {
-    if (p.near_tokens < 0) {
-      l2_region(cv, s_cand, 0, n_cand, lb.lower, lb.upper, lb.quota,
-                p.sink_tokens, s_l0, s_l1, s_mid, &s_misc[0], s_hist, s_tmp);
-    } else {
+    int nreg = 1;
+    bool masked = false;
+    int r_lo[2] = {lb.lower, 0}, r_hi[2] = {lb.upper, 0}, r_q[2] = {lb.quota, 0};
+    if (p.near_tokens >= 0) {
       // far quota first, the remainder goes to near (selector:873-920)
       const L2Bounds fb = l2_bounds(p, L, false, false, p.near_len);
       const int base = imax(imin(L, p.k2) - p.sink_tokens - (L - fb.lo), 0);
@@ -1234,60 +1654,60 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       const int near_low = fb.far_hi;
       const int near_high = skip_near ? fb.far_hi : upper0;
       near_quota = imin(near_quota, imax(near_high - near_low, 0));
-      const int fa = index_of_token(far_low), fz = index_of_token(far_high);
-      l2_region(cv, s_cand, fa, imax(fa, fz), far_low, far_high, far_quota,
-                p.sink_tokens, s_l0, s_l1, s_mid, &s_misc[0], s_hist, s_tmp);
-      const int na = index_of_token(near_low), nz = index_of_token(near_high);
-      l2_region(cv, s_cand, na, imax(na, nz), near_low, near_high, near_quota,
-                p.sink_tokens, s_l0, s_l1, s_mid, &s_misc[0], s_hist, s_tmp);
+      nreg = 2;
+      masked = true;
+      r_lo[0] = far_low;
+      r_hi[0] = imax(far_low, far_high);
+      r_q[0] = far_quota;
+      r_lo[1] = near_low;
+      r_hi[1] = imax(near_low, near_high);
+      r_q[1] = near_quota;
     }
+    for (int r = 0; r < nreg; ++r)
+      l2_region_dense(dv, masked, r_lo[r], r_hi[r], r_q[r], p.sink_tokens, rl,
+                      &s_misc[2], s_hist, s_tmp);
   }
   __syncthreads();
-  NFA_MARK(clk_tail, 5);
-  int mcount = s_misc[0];
+  NFA_MARK(clk_b, 3);
+  int mcount = s_misc[2];
   if (mcount > p.k2) mcount = p.k2;
+  const int *s_mid = rl.mid;
+  const int *s_mslot = rl.mslot;
   if (p.dbg_middle != nullptr) {
-    for (int i = tid; i < p.k2; i += NFA_BLOCK)
-      p.dbg_middle[(int64_t)row * p.k2 + i] = i < mcount ? s_mid[i] : 0;
+    for (int k = tid; k < p.k2; k += NFA_BLOCK)
+      p.dbg_middle[(int64_t)row * p.k2 + k] = k < mcount ? s_mid[k] : 0;
     if (tid == 0) p.dbg_counts[row] = mcount;
   }
 
-  // final union with the protected sink/SWA ids (selector:1337-1437)
-  const int32_t *bt = p.block_table_l + req * p.max_blocks;
+  // ---- final union with the protected sink/SWA ids (selector:1337-1437) --
   int32_t *grow = p.gather + ((int64_t)b * p.hkv + kv) * p.max_vis;
-  auto phys_slot = [&](int id) {
-    return bt[imin(id / p.page, p.max_blocks - 1)] * p.page + id % p.page;
-  };
   if (p.middle_only) {
     const int n = imin(mcount, p.max_vis);
-    for (int i = tid; i < n; i += NFA_BLOCK) grow[i] = phys_slot(s_mid[i]);
+    for (int k = tid; k < n; k += NFA_BLOCK) grow[k] = s_mslot[k];
     if (tid == 0) p.vis_lens[b * p.hkv + kv] = n;
+    NFA_MARK(clk_b, 4);
     return;
   }
-  int u0, u1, u2, u3;
-  protected_intervals(p, L, sd.prot, &u0, &u1, &u2, &u3);
   auto in_u = [&](int x) { return (x >= u0 && x < u1) || (x >= u2 && x < u3); };
   auto below_u = [&](int x) {  // |U ∩ [0, x)|
     return imax(0, imin(x, u1) - u0) + imax(0, imin(x, u3) - u2);
   };
-  const int nu = (u1 - u0) + (u3 - u2);
-  // middle entries inside U are duplicates; the rest keep their order.
-  // Destinations first (barrier loop, LDS only), then one mapping pass.
-  int carry = 0;
-  for (int base = 0; base < mcount; base += NFA_BLOCK) {
-    const int i = base + tid;
-    const int x = i < mcount ? s_mid[i] : 0;
-    const bool keep = i < mcount && !in_u(x);
-    int tot;
-    const int r = block_count_exclusive(keep, s_tmp, &tot) + carry;
-    if (i < mcount) s_l0[i] = keep ? r + below_u(x) : -1;
-    carry += tot;
-  }
-  const int nkeep = carry;
-  __syncthreads();
-  for (int i = tid; i < mcount; i += NFA_BLOCK) {
-    const int dest = s_l0[i];
-    if (dest >= 0 && dest < p.max_vis) grow[dest] = phys_slot(s_mid[i]);
+  // middle entries inside U are duplicates; the rest keep their order
+  int nkeep;
+  {
+    const int per = (mcount + NFA_BLOCK - 1) / NFA_BLOCK;
+    const int ia = tid * per;
+    const int ib = imin(mcount, ia + per);
+    int c = 0;
+    for (int k = ia; k < ib; ++k) c += !in_u(s_mid[k]);
+    int r = block_scan_exclusive(c, s_tmp, &nkeep);
+    for (int k = ia; k < ib; ++k) {
+      const int x = s_mid[k];
+      if (in_u(x)) continue;
+      const int dest = r + below_u(x);
+      if (dest < p.max_vis) grow[dest] = s_mslot[k];
+      ++r;
+    }
   }
   // kept-middle entries below x: lower_bound over s_mid minus duplicates
   auto kept_below = [&](int x) {
@@ -1301,10 +1721,12 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   for (int k = tid; k < nu; k += NFA_BLOCK) {
     const int x = k < (u1 - u0) ? u0 + k : u2 + (k - (u1 - u0));
     const int dest = k + kept_below(x);
-    if (dest < p.max_vis) grow[dest] = phys_slot(x);
+    const int slot = k == tid ? pre_slot
+                              : btr[imin(x / p.page, mb - 1)] * p.page + x % p.page;
+    if (dest < p.max_vis) grow[dest] = slot;
   }
   if (tid == 0) p.vis_lens[b * p.hkv + kv] = nkeep + nu;
-  NFA_MARK(clk_tail, 6);
+  NFA_MARK(clk_b, 4);
 }
 
 }  // namespace nfa
@@ -1360,9 +1782,9 @@ static int select_check(const NfaSelectParams *p) {
     return NFA_EINVAL;
   }
   const SelDims sd = nfa::sel_dims(*p);
-  if (sd.lds_bytes > 64 * 1024) {
-    nfa_set_error("nfa_select_layer: geometry needs %d bytes of LDS (> 64 KiB)",
-                  sd.lds_bytes);
+  if (sd.lds_a > 64 * 1024 || sd.lds_b > 64 * 1024) {
+    nfa_set_error("nfa_select_layer: geometry needs %d / %d bytes of LDS (> 64 KiB)",
+                  sd.lds_a, sd.lds_b);
     return NFA_EINVAL;
   }
   if (p->workspace == nullptr || p->workspace_bytes < sd.w_total) {
@@ -1399,9 +1821,13 @@ extern "C" int64_t nfa_select_workspace_bytes(const NfaSelectParams *p) {
 template <int DSUB, typename KV>
 static hipError_t launch_select(const NfaSelectParams &p, hipStream_t stream) {
   const SelDims sd = nfa::sel_dims(p);
-  dim3 grid(sd.ntiles, p.batch * p.hkv);
-  hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV>), grid, dim3(NFA_BLOCK),
-                     sd.lds_bytes, stream, p);
+  const int rows = p.batch * p.hkv;
+  hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV>), dim3(sd.ntiles, rows),
+                     dim3(NFA_BLOCK), sd.lds_a, stream, p, sd);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((nfa::nfa_l2_kernel<KV>), dim3(sd.nchunk, rows),
+                     dim3(NFA_BLOCK), sd.lds_b, stream, p, sd);
   return hipGetLastError();
 }
 

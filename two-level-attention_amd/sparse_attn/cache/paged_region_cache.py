@@ -178,6 +178,10 @@ class GraphReadyPagedRegionCache:
             (n_layers, max_requests), dtype=i32, device=device)
 
         pin = device.type == 'cuda'
+        # pinned staging buffers feed asynchronous copies; a buffer is only
+        # rewritten once the device has executed the last copy out of it
+        self._pinned_staging = pin
+        self._staging_event = None
 
         def staging(shape, fill, dtype):
             t = torch.full(shape, fill, dtype=dtype, device='cpu')
@@ -295,6 +299,21 @@ class GraphReadyPagedRegionCache:
     def _alloc_pages(self, layer_idx, count):
         return self.layers[layer_idx].alloc_pages(count)
 
+    def _staging_wait(self):
+        """Block until the device has executed the last asynchronous copy
+        out of the pinned staging buffers, so that they can be rewritten."""
+        ev = self._staging_event
+        if ev is not None:
+            self._staging_event = None
+            ev.synchronize()
+
+    def _staging_mark(self):
+        """Mark the copies just enqueued out of the staging buffers."""
+        if self._pinned_staging and not torch.cuda.is_current_stream_capturing():
+            ev = torch.cuda.Event()
+            ev.record()
+            self._staging_event = ev
+
     def add_request(self, request_id=None):
         if request_id is None:
             request_id = self._next_free_slot()
@@ -305,6 +324,7 @@ class GraphReadyPagedRegionCache:
         self.states[request_id] = RequestState(
             block_tables=[{} for _ in range(self.n_layers)])
         self.request_phases[request_id] = RequestPhase.PREFILL
+        self._staging_wait()
         self._cpu_block_table_staging[:, request_id].fill_(self.layers[0].PAD_PAGE_ID)
         return request_id
 
@@ -334,6 +354,7 @@ class GraphReadyPagedRegionCache:
         if state is None:
             return
         freed = [set(state.block_tables[l].values()) for l in range(self.n_layers)]
+        self._staging_wait()
         self._cpu_block_table_staging[:, request_id].fill_(self.layers[0].PAD_PAGE_ID)
         if self.layers[0].kv_pool_k.is_cuda:
             # pages may still be read by queued kernels; return them only
@@ -379,12 +400,14 @@ class GraphReadyPagedRegionCache:
             state.logical_length = n
         elif n != state.prompt_length:
             raise ValueError('prefill length diverged across layers')
+        self._staging_wait()
         row = self._cpu_block_table_staging[layer_idx, request_id]
         row.fill_(self.layers[0].PAD_PAGE_ID)
         for lp, pid in table.items():
             if 0 <= lp < self.max_blocks:
                 row[lp] = pid
         self.block_table_buf[layer_idx, request_id].copy_(row, non_blocking=keys.is_cuda)
+        self._staging_mark()
         from ..ops.paged_region_kernels import paged_write_prefill
         return paged_write_prefill(
             layer, keys, values, self.block_table_buf[layer_idx, request_id],
@@ -399,6 +422,7 @@ class GraphReadyPagedRegionCache:
         state.skip_far_by_layer = [bool(x) for x in skip_far_list]
         state.skip_near_by_layer = [bool(x) for x in skip_near_list]
         state.skip_policy_groups = self._build_skip_policy_groups(state)
+        self._staging_wait()
         self._cpu_skip_far_layer_staging[:, request_id] = torch.as_tensor(
             state.skip_far_by_layer, dtype=torch.int32)
         self._cpu_skip_near_layer_staging[:, request_id] = torch.as_tensor(
@@ -420,6 +444,7 @@ class GraphReadyPagedRegionCache:
         self._write_block_table_row(request_id, state)
         self.block_table_buf[:, request_id].copy_(
             self._cpu_block_table_staging[:, request_id], non_blocking=nb)
+        self._staging_mark()
         self.common_dirty = True
         self.request_layout_revision += 1
         self._layout_source = None
@@ -618,6 +643,7 @@ class GraphReadyPagedRegionCache:
         # same physical page as the previous step: valid slots move by one
         slots = self.slot_mapping_buf[:, :batch]
         slots.add_(slots >= 0)
+        self._staging_wait()
         self.pending_lengths.clear()
         for row, (rid, state) in enumerate(zip(req_ids, refs)):
             self._cpu_planned_lengths_staging[row] = planned[row]
@@ -625,11 +651,13 @@ class GraphReadyPagedRegionCache:
                 self.pending_lengths[rid] = planned[row]
         self.planned_lengths_buf[:batch].copy_(
             self._cpu_planned_lengths_staging[:batch], non_blocking=True)
+        self._staging_mark()
         return True
 
     def _prepare_common(self, req_ids, query_lengths):
         page = self.geometry.page
         batch = len(req_ids)
+        self._staging_wait()
         self._cpu_slot_mapping_staging[:, :batch].fill_(PAD_SLOT)
         self._cpu_active_req_ids_staging[:batch].fill_(self.INVALID_REQ_ID)
         self._cpu_valid_req_ids_staging[:batch].zero_()
@@ -674,6 +702,7 @@ class GraphReadyPagedRegionCache:
         self.valid_req_ids_buf.copy_(self._cpu_valid_req_ids_staging, non_blocking=True)
         self.planned_lengths_buf.copy_(
             self._cpu_planned_lengths_staging, non_blocking=True)
+        self._staging_mark()
         self._common_active_req_ids = tuple(req_ids)
         self._common_state_refs = tuple(
             self.states.get(r) if r is not None and r >= 0 else None for r in req_ids)

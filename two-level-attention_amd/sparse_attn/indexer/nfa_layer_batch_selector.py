@@ -271,7 +271,13 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
                                                 device=device)
     p.workspace = scratch.data_ptr()
     p.workspace_bytes = scratch.numel()
-    if _debug is not None:
+    if _debug is not None and _debug.get('clock_only'):
+        # phase timeline only: the production path plus wall-clock marks
+        ntiles = (cache.max_blocks + 255) // 256
+        _debug['clock'] = torch.zeros((b * hkv, ntiles + 1, 16),
+                                      dtype=torch.int64, device=device)
+        p.dbg_clock = _debug['clock'].data_ptr()
+    elif _debug is not None:
         want_clock = _debug.get('want_clock', False)
         _debug.clear()
         _debug['want_clock'] = want_clock
