@@ -236,17 +236,19 @@ def selector_timeline(torch, w, steps, plan):
         c = clk.cpu().numpy().astype(np.int64)
         tile, tail = c[:, :-1, :], c[:, -1, :]
         start = tile[:, :, 0][tile[:, :, 0] > 0].min()
-        acc.setdefault('kernel span (A+B)', []).append((tail[:, 12].max() - start) * us)
+        acc.setdefault('kernel span (A+B)', []).append((tail[:, 13].max() - start) * us)
         acc.setdefault('last tile arrives', []).append(
             (tile[:, :, 4].max() - start) * us)
         names = ['row scalars', 'q prep', 'page stats', 'L1 scores+publish']
         for k, name in enumerate(names):
             d = (tile[:, :, k + 1] - tile[:, :, k]) * us
             acc.setdefault(f'A tile {name} (max)', []).append(d.max())
-        spans = [('A tail L1 threshold', 0, 1), ('A tail cand pages', 1, 2),
-                 ('A end -> B start', 2, 8), ('B chunk0 L2 logits', 8, 9),
-                 ('B last arrival', 9, 10), ('B L2 top-k', 10, 11),
-                 ('B union', 11, 12)]
+        spans = [('A tail L1 threshold', 0, 1), ('A tail selection pass', 1, 2),
+                 ('A tail bitmap compaction', 2, 3), ('A tail publish pages', 3, 4),
+                 ('A tail end', 4, 6),
+                 ('A end -> B start', 6, 8), ('B chunk0 L2 logits', 8, 9),
+                 ('B last arrival', 9, 10), ('B tail staging', 10, 11),
+                 ('B L2 top-k', 11, 12), ('B union', 12, 13)]
         for name, a, b in spans:
             d = (tail[:, b] - tail[:, a]) * us
             acc.setdefault(f'{name} (max)', []).append(d.max())

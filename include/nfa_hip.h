@@ -32,6 +32,9 @@ extern "C" {
 
 #define NFA_ABI_VERSION 1
 
+/* pages scored per selector workgroup; sizes the dbg_clock timeline */
+#define NFA_SELECT_TILE_PAGES 256
+
 /* error codes */
 #define NFA_OK 0
 #define NFA_EINVAL (-1)    /* bad geometry / flags / pointer */
@@ -122,7 +125,9 @@ typedef struct NfaSelectParams {
   int32_t *dbg_cand_count;            /* [batch, hkv] */
   int64_t dbg_cand_cap;
   int64_t *dbg_clock;                 /* [batch*hkv, ntiles + 1, 16] phase
-                                         timestamps (wall clock), or NULL */
+                                         timestamps (wall clock), or NULL;
+                                         ntiles = ceil(max_blocks /
+                                         NFA_SELECT_TILE_PAGES) */
 } NfaSelectParams;
 
 typedef struct NfaAttnParams {

@@ -101,6 +101,22 @@ __device__ __forceinline__ void unpack_chunk(const uint4 &raw, float *out) {
   load_chunk<KV>(reinterpret_cast<const KV *>(&raw), out);
 }
 
+// CH floats that are exact KV values back into 16 bytes of KV elements.
+template <typename KV>
+__device__ __forceinline__ uint4 pack_chunk(const float *x) {
+  if constexpr (sizeof(KV) == 2) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (__float_as_uint(x[2 * i]) >> 16) |
+             (__float_as_uint(x[2 * i + 1]) & 0xFFFF0000u);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    return make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]),
+                      __float_as_uint(x[2]), __float_as_uint(x[3]));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // cross-workgroup publication ("last arriving workgroup" pattern)
 // ---------------------------------------------------------------------------
@@ -139,7 +155,8 @@ __device__ __forceinline__ bool arrive_last(unsigned int *counter,
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
-// Exclusive prefix sum of an int over the block; two barriers.
+// Exclusive prefix sum of an int over a block of WAVES waves; two barriers.
+template <int WAVES = NFA_WAVES>
 __device__ __forceinline__ int block_scan_exclusive(int v, int *scratch,
                                                     int *total) {
   const int lane = lane_id();
@@ -154,7 +171,7 @@ __device__ __forceinline__ int block_scan_exclusive(int v, int *scratch,
   __syncthreads();
   int before = 0, sum = 0;
 #pragma unroll
-  for (int i = 0; i < NFA_WAVES; ++i) {
+  for (int i = 0; i < WAVES; ++i) {
     const int c = scratch[i];
     if (i < w) before += c;
     sum += c;
@@ -164,10 +181,10 @@ __device__ __forceinline__ int block_scan_exclusive(int v, int *scratch,
   return before + x - v;
 }
 
-// Exclusive prefix sums of N ints at once (one pair of barriers for all N);
-// v is replaced by its exclusive prefix, total receives the block totals.
-// `scratch` needs NFA_WAVES * N ints.
-template <int N>
+// Exclusive prefix sums of N ints at once over a block of WAVES waves (one
+// pair of barriers for all N); v is replaced by its exclusive prefix, total
+// receives the block totals.  `scratch` needs WAVES * N ints.
+template <int N, int WAVES = NFA_WAVES>
 __device__ __forceinline__ void block_scan_n(int (&v)[N], int *scratch,
                                              int (&total)[N]) {
   const int lane = lane_id();
@@ -192,7 +209,7 @@ __device__ __forceinline__ void block_scan_n(int (&v)[N], int *scratch,
   for (int k = 0; k < N; ++k) {
     int before = 0, sum = 0;
 #pragma unroll
-    for (int i = 0; i < NFA_WAVES; ++i) {
+    for (int i = 0; i < WAVES; ++i) {
       const int c = scratch[i * N + k];
       if (i < w) before += c;
       sum += c;

@@ -44,25 +44,32 @@ namespace nfa {
 // LDS and workspace layouts (shared by host and device)
 // ---------------------------------------------------------------------------
 
-constexpr int kL2Slots = 64;     // dense candidate slots per kernel-B workgroup
-constexpr int kStatTokens = 16;  // tokens per staging round of the stats pass
+constexpr int SB = 1024;         // threads per selector workgroup
+constexpr int SW = SB / 64;      // waves per selector workgroup
+constexpr int TPP = 4;           // threads per page in the tile stage
+constexpr int TP = NFA_SELECT_TILE_PAGES;  // pages per tile = SB / TPP
+static_assert(TP * TPP == SB, "tile geometry");
+constexpr int kL2SlotsMax = 256; // dense candidate slots per kernel-B workgroup
+constexpr int kStatTokens = 4;   // tokens per staging round of the stats pass
+constexpr int kSegMax = 16384;   // keys staged in LDS at once by the tail
 
 struct SelDims {
   int ntiles;     // L1 tiles per row (kernel A grid.x)
-  int segc;       // pages per tail thread and key segment (multiple of 8)
+  int seg;        // keys per segment staged in LDS by the tail
   int nseg;       // key segments per row
-  int kstride;    // keys per row in the workspace = nseg * 256 * segc
+  int kstride;    // keys per row in the workspace = nseg * seg
   int words;      // candidate bitmap words = kstride / 32
   int np;         // candidate page capacity = k_f + k_n + 2
   int dense;      // dense candidate slots = np * bs
   int dstride;    // dense keys per row in the workspace (multiple of 8)
+  int l2slots;    // dense slots per kernel-B workgroup (SB / l2slots threads each)
   int nchunk;     // kernel B grid.x
   int prot;       // protected width = min(s_cap, sink + swa)
   int lds_a, lds_b;
   // kernel A LDS: common part, then the tile and tail parts overlap
   int a_hist, a_tmp, a_misc, a_qf, a_fdims;
   int a_dims, a_last, a_tphys, a_stage;                 // tile
-  int a_keys, a_pages, a_cbits, a_dbf, a_dbn, a_dsel;   // tail
+  int a_keys, a_pages, a_cbits, a_eqb, a_dbf, a_dbn, a_dsel;  // tail
   // kernel B LDS: common part, then the scoring and tail parts overlap
   int b_hist, b_tmp, b_misc, b_qg, b_fdims;
   int b_tok, b_stage;                                   // scoring
@@ -78,37 +85,41 @@ __host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
 __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p) {
   SelDims s;
   const int group = p.hq / p.hkv;
-  s.ntiles = (p.max_blocks + NFA_BLOCK - 1) / NFA_BLOCK;
-  const int cpt = s.ntiles;  // pages per thread when one segment covers the row
-  int segc = (cpt + 7) & ~7;
-  if (segc > 64) segc = 64;
-  s.segc = segc;
-  s.nseg = (cpt + segc - 1) / segc;
-  s.kstride = s.nseg * NFA_BLOCK * segc;
+  s.ntiles = (p.max_blocks + TP - 1) / TP;
+  const int kpad = s.ntiles * TP;  // keys written by the tiles
+  s.seg = kpad < kSegMax ? kpad : kSegMax;
+  s.nseg = (kpad + s.seg - 1) / s.seg;
+  s.kstride = s.nseg * s.seg;
   s.words = s.kstride / 32;
   s.np = p.k_f + p.k_n + 2;
   s.dense = s.np * p.bs;
   s.dstride = (s.dense + 7) & ~7;
-  s.nchunk = (s.dense + kL2Slots - 1) / kL2Slots;
+  // staging of a slot's L2 dims is at most 4 * fine_dsub bytes; keep the
+  // chunk's staging within 32 KiB
+  int slots = kL2SlotsMax;
+  while (slots > 16 && slots * 4 * p.fine_dsub > 32 * 1024) slots /= 2;
+  s.l2slots = slots;
+  s.nchunk = (s.dense + slots - 1) / slots;
   const int s_cap = p.max_blocks * p.bs;
   s.prot = p.sink_tokens + p.swa < s_cap ? p.sink_tokens + p.swa : s_cap;
   // kernel A
   int o = 0;
   s.a_hist = o;  o += align16(4 * 4 * 256);
-  s.a_tmp = o;   o += align16(4 * 64);
+  s.a_tmp = o;   o += align16(4 * 128);
   s.a_misc = o;  o += align16(4 * 32);
   s.a_qf = o;    o += align16(4 * group * p.dsub);
   s.a_fdims = o; o += align16(4 * p.fine_dsub);
   const int a_base = o;
   s.a_dims = o;  o += align16(4 * p.dsub);
   s.a_last = o;  o += align16(4 * 3 * p.dsub);
-  s.a_tphys = o; o += align16(4 * NFA_BLOCK);
-  s.a_stage = o; o += align16(4 * NFA_BLOCK * kStatTokens);
+  s.a_tphys = o; o += align16(4 * SB);
+  s.a_stage = o; o += align16(4 * SB * kStatTokens);
   const int a_tile = o;
   o = a_base;
-  s.a_keys = o;  o += align16(2 * NFA_BLOCK * s.segc);
+  s.a_keys = o;  o += align16(2 * s.seg);
   s.a_pages = o; o += align16(4 * s.np);
   s.a_cbits = o; o += align16(4 * s.words);
+  s.a_eqb = o;   o += align16(4 * s.words);
   s.a_dbf = o;   o += align16(4 * s.words);
   s.a_dbn = o;   o += align16(4 * s.words);
   s.a_dsel = o;  o += align16(8 * (p.k_f + p.k_n + 1));
@@ -116,13 +127,13 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p) {
   // kernel B
   o = 0;
   s.b_hist = o;  o += align16(4 * 2 * 256);
-  s.b_tmp = o;   o += align16(4 * 64);
+  s.b_tmp = o;   o += align16(4 * 128);
   s.b_misc = o;  o += align16(4 * 32);
   s.b_qg = o;    o += align16(4 * p.fine_dsub);
   s.b_fdims = o; o += align16(4 * p.fine_dsub);
   const int b_base = o;
-  s.b_tok = o;   o += align16(4 * kL2Slots);
-  s.b_stage = o; o += align16(4 * kL2Slots * p.fine_dsub);
+  s.b_tok = o;   o += align16(4 * s.l2slots);
+  s.b_stage = o; o += align16(4 * s.l2slots * p.fine_dsub);
   const int b_score = o;
   o = b_base;
   s.b_dk = o;    o += align16(2 * s.dstride);
@@ -290,7 +301,7 @@ __device__ __forceinline__ void compute_stats(const NfaSelectParams &p, int64_t 
                               const KV *new_row, int new_tok, float *s_last) {
   const KV *kpool = (const KV *)p.k_pool_l;
   const int32_t *bt = p.block_table_l + req * p.max_blocks;
-  constexpr int PER = NFA_BLOCK / DSUB;  // pages per pass
+  constexpr int PER = SB / DSUB;  // pages per pass
   const int tid = threadIdx.x;
   const int d = tid % DSUB;
   const int slot = tid / DSUB;
@@ -305,7 +316,7 @@ __device__ __forceinline__ void compute_stats(const NfaSelectParams &p, int64_t 
     for (int i0 = 0; i0 < p.bs; i0 += kStatTokens) {
 #pragma unroll
       for (int k = 0; k < kStatTokens; ++k) {
-        const int e = tid + k * NFA_BLOCK;  // [page slot][token][dim]
+        const int e = tid + k * SB;  // [page slot][token][dim]
         const int dd = e % DSUB;
         const int ti = (e / DSUB) % kStatTokens;
         const int ps = e / (DSUB * kStatTokens);
@@ -370,14 +381,14 @@ __device__ __forceinline__ void compute_stats_vec(const NfaSelectParams &p, int6
                                   float *s_last) {
   constexpr int CH = Elem<KV>::kChunk;
   constexpr int NCH1 = DSUB / CH;
-  constexpr int TG = 16;
+  constexpr int TG = 4;
   const KV *kpool = (const KV *)p.k_pool_l;
   const int32_t *bt = p.block_table_l + req * p.max_blocks;
   KV *smin = (KV *)p.stat_min_l;
   KV *smax = (KV *)p.stat_max_l;
   KV *ssum = (KV *)p.stat_sum_l;
   const int n_items = (pg_hi - pg_lo) * NCH1;
-  for (int it = threadIdx.x; it < n_items; it += NFA_BLOCK) {
+  for (int it = threadIdx.x; it < n_items; it += SB) {
     const int pg = pg_lo + it / NCH1;
     const int c = it % NCH1;
     float mn[CH], mx[CH], sm[CH];
@@ -451,7 +462,7 @@ __device__ __forceinline__ void stats_latest_page(
     const NfaSelectParams &p, int64_t req, int kv, int L, int pg,
     int phys_first, const int *s_dims, float *s_stage, const KV *new_row,
     float *s_last) {
-  constexpr int R = NFA_BLOCK / DSUB;
+  constexpr int R = SB / DSUB;
   constexpr int RT = 4 * R;  // tokens per round
   const int tid = threadIdx.x;
   const int d = tid % DSUB;
@@ -517,107 +528,97 @@ __device__ __forceinline__ void stats_latest_page(
 
 constexpr int GMAX = 8;
 
-// Head-major: for each query head j (rolled loop) the dims run in order, so
-// sneg_j / spos_j / savg_j accumulate exactly as Σ_d in ascending d; the
-// group mean then sums bf16(per-head score) over j in order.  kmin / kmax /
-// kavg hold the page statistics as floats (kavg = bf16(sum / bs)).
-template <int DSUB>
-__device__ __forceinline__ void l1_scores_regs(const float *kmin,
-                                               const float *kmax,
-                                               const float *kavg,
-                                               const float *s_qf, int G,
-                                               bool need_mm, bool need_avg,
-                                               uint16_t *mm_bits,
-                                               uint16_t *avg_bits) {
-  float mm_acc = 0.0f, avg_acc = 0.0f;
-  for (int j = 0; j < G; ++j) {
-    const float *q = s_qf + j * DSUB;
-    if (need_mm) {
-      float sn = 0.0f, sp = 0.0f;
+// One query head: bf16(Σ_d kmin_d·min(q_d,0) + Σ_d kmax_d·max(q_d,0)) and
+// bf16(Σ_d kavg_d·q_d), every sum sequential in ascending d with separately
+// rounded products.  rmn / rmx hold the page's min / max statistics as stored
+// (16-byte chunks, unpacked on use), kavg = bf16(sum / bs) as floats.
+template <int DSUB, typename KV>
+__device__ __forceinline__ void l1_head_regs(const uint4 *rmn, const uint4 *rmx,
+                                             const float *kavg, const float *q,
+                                             bool need_mm, bool need_avg,
+                                             float *mm, float *avg) {
+  constexpr int CH = Elem<KV>::kChunk;
+  if (need_mm) {
+    float sn = 0.0f, sp = 0.0f;
 #pragma unroll
-      for (int d = 0; d < DSUB; ++d) {
-        const float qd = q[d];
+    for (int c = 0; c < DSUB / CH; ++c) {
+      float lo[CH], hi[CH];
+      unpack_chunk<KV>(rmn[c], lo);
+      unpack_chunk<KV>(rmx[c], hi);
+#pragma unroll
+      for (int e = 0; e < CH; ++e) {
+        const float qd = q[c * CH + e];
         const float ql = qd < 0.0f ? qd : 0.0f;
         const float qh = qd > 0.0f ? qd : 0.0f;
-        const float a = kmin[d] * ql;
-        const float b = kmax[d] * qh;
+        const float a = lo[e] * ql;
+        const float b = hi[e] * qh;
         sn = sn + a;
         sp = sp + b;
       }
-      mm_acc = mm_acc + bf16r(sn + sp);
     }
-    if (need_avg) {
-      float sa = 0.0f;
-#pragma unroll
-      for (int d = 0; d < DSUB; ++d) {
-        const float a = kavg[d] * q[d];
-        sa = sa + a;
-      }
-      avg_acc = avg_acc + bf16r(sa);
-    }
+    *mm = bf16r(sn + sp);
   }
-  *mm_bits = bf16_bits(mm_acc / (float)G);
-  *avg_bits = bf16_bits(avg_acc / (float)G);
+  if (need_avg) {
+    float sa = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DSUB; ++d) {
+      const float a = kavg[d] * q[d];
+      sa = sa + a;
+    }
+    *avg = bf16r(sa);
+  }
 }
 
 // Same arithmetic with the statistics read chunk by chunk from memory (L1
-// dim counts above 32: rope / full subspaces).
+// dim counts above 32, fp32 statistics) or from `s_last` (the latest page).
 template <int DSUB, typename KV>
-__device__ __forceinline__ void l1_scores_mem(const NfaSelectParams &p,
-                                              int64_t req, int kv, int t,
-                                              const float *s_qf, int G,
-                                              bool need_mm, bool need_avg,
-                                              const float *s_last,
-                                              uint16_t *mm_bits,
-                                              uint16_t *avg_bits) {
+__device__ __forceinline__ void l1_head_mem(const NfaSelectParams &p,
+                                            int64_t req, int kv, int t,
+                                            const float *q, bool need_mm,
+                                            bool need_avg, const float *s_last,
+                                            float *mm, float *avg) {
   constexpr int CH = Elem<KV>::kChunk;
   const KV *smin = (const KV *)p.stat_min_l;
   const KV *smax = (const KV *)p.stat_max_l;
   const KV *ssum = (const KV *)p.stat_sum_l;
   const float bsf = (float)p.bs;
-  float mm_acc = 0.0f, avg_acc = 0.0f;
-  for (int j = 0; j < G; ++j) {
-    const float *q = s_qf + j * DSUB;
-    float sn = 0.0f, sp = 0.0f, sa = 0.0f;
-    for (int c = 0; c < DSUB / CH; ++c) {
-      float kmin[CH], kmax[CH], ks[CH];
-      if (s_last != nullptr) {
-#pragma unroll
-        for (int e = 0; e < CH; ++e) {
-          kmin[e] = s_last[c * CH + e];
-          kmax[e] = s_last[DSUB + c * CH + e];
-          ks[e] = s_last[2 * DSUB + c * CH + e];
-        }
-      } else {
-        const int64_t base = stat_index<KV>(p, req, kv, c * CH, t, DSUB);
-        if (need_mm) {
-          load_chunk<KV>(smin + base, kmin);
-          load_chunk<KV>(smax + base, kmax);
-        }
-        if (need_avg) load_chunk<KV>(ssum + base, ks);
-      }
+  float sn = 0.0f, sp = 0.0f, sa = 0.0f;
+  for (int c = 0; c < DSUB / CH; ++c) {
+    float kmin[CH], kmax[CH], ks[CH];
+    if (s_last != nullptr) {
 #pragma unroll
       for (int e = 0; e < CH; ++e) {
-        const float qd = q[c * CH + e];
-        if (need_mm) {
-          const float ql = qd < 0.0f ? qd : 0.0f;
-          const float qh = qd > 0.0f ? qd : 0.0f;
-          const float a = kmin[e] * ql;
-          const float b = kmax[e] * qh;
-          sn = sn + a;
-          sp = sp + b;
-        }
-        if (need_avg) {
-          const float a = bf16r(ks[e] / bsf) * qd;
-          sa = sa + a;
-        }
+        kmin[e] = s_last[c * CH + e];
+        kmax[e] = s_last[DSUB + c * CH + e];
+        ks[e] = s_last[2 * DSUB + c * CH + e];
+      }
+    } else {
+      const int64_t base = stat_index<KV>(p, req, kv, c * CH, t, DSUB);
+      if (need_mm) {
+        load_chunk<KV>(smin + base, kmin);
+        load_chunk<KV>(smax + base, kmax);
+      }
+      if (need_avg) load_chunk<KV>(ssum + base, ks);
+    }
+#pragma unroll
+    for (int e = 0; e < CH; ++e) {
+      const float qd = q[c * CH + e];
+      if (need_mm) {
+        const float ql = qd < 0.0f ? qd : 0.0f;
+        const float qh = qd > 0.0f ? qd : 0.0f;
+        const float a = kmin[e] * ql;
+        const float b = kmax[e] * qh;
+        sn = sn + a;
+        sp = sp + b;
+      }
+      if (need_avg) {
+        const float a = bf16r(ks[e] / bsf) * qd;
+        sa = sa + a;
       }
     }
-    if (need_mm) mm_acc = mm_acc + bf16r(sn + sp);
-    if (need_avg) avg_acc = avg_acc + bf16r(sa);
   }
-  *mm_bits = bf16_bits(mm_acc / (float)G);
-  *avg_bits = bf16_bits(avg_acc / (float)G);
+  if (need_mm) *mm = bf16r(sn + sp);
+  if (need_avg) *avg = bf16r(sa);
 }
 
 // ---------------------------------------------------------------------------
@@ -656,22 +657,23 @@ __device__ __forceinline__ bool tie_cut(const PoolThr &t) {
   return t.need < (1 << 30) && t.T > 0 && t.T < 0x10000;
 }
 
-// Stage keys [seg_base, seg_base + 256 * segc) of a row into LDS with 16-byte
-// loads, every load of the segment in flight at once.
+// Stage keys [seg_base, seg_base + seg) of a row into LDS with 16-byte
+// loads, every load of the segment in flight at once (seg <= kSegMax).
 __device__ __forceinline__ void stage_keys(const uint16_t *g_keys, int seg_base,
-                                           int segc, uint16_t *s_keys) {
-  const int n16 = NFA_BLOCK * segc / 8;
+                                           int seg, uint16_t *s_keys) {
+  constexpr int R = kSegMax / 8 / SB;
+  const int n16 = seg / 8;
   const uint4 *src = reinterpret_cast<const uint4 *>(g_keys + seg_base);
   uint4 *dst = reinterpret_cast<uint4 *>(s_keys);
-  uint4 r[8];
+  uint4 r[R];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int u = threadIdx.x + k * NFA_BLOCK;
+  for (int k = 0; k < R; ++k) {
+    const int u = threadIdx.x + k * SB;
     r[k] = u < n16 ? src[u] : make_uint4(0u, 0u, 0u, 0u);
   }
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int u = threadIdx.x + k * NFA_BLOCK;
+  for (int k = 0; k < R; ++k) {
+    const int u = threadIdx.x + k * SB;
     if (u < n16) dst[u] = r[k];
   }
 }
@@ -725,10 +727,10 @@ __device__ __forceinline__ void decode_write(const NfaSelectParams &p, int b,
   KV *vp = (KV *)p.v_pool_l;
   const KV *kn = (const KV *)p.k_new;
   const KV *vn = (const KV *)p.v_new;
-  for (int d = threadIdx.x; d < p.head_dim; d += NFA_BLOCK)
+  for (int d = threadIdx.x; d < p.head_dim; d += SB)
     kp[kv_offset(p, phys, kv, off) + d] =
         kn[((int64_t)b * p.hkv + kv) * p.head_dim + d];
-  for (int d = threadIdx.x; d < p.head_dim_v; d += NFA_BLOCK)
+  for (int d = threadIdx.x; d < p.head_dim_v; d += SB)
     vp[(((int64_t)phys * p.hkv + kv) * p.page + off) * p.head_dim_v + d] =
         vn[((int64_t)b * p.hkv + kv) * p.head_dim_v + d];
 }
@@ -736,7 +738,7 @@ __device__ __forceinline__ void decode_write(const NfaSelectParams &p, int b,
 // Both regions skipped (region mode 3 / disjoint protected gather): decode
 // write plus the union with an empty middle; no statistics are touched.
 template <typename KV>
-__global__ void __launch_bounds__(NFA_BLOCK)
+__global__ void __launch_bounds__(SB)
     nfa_protected_kernel(const NfaSelectParams p) {
   const int row = blockIdx.x;
   const int b = row / p.hkv;
@@ -756,7 +758,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int nu = (u1 - u0) + (u3 - u2);
   const int32_t *bt = p.block_table_l + req * p.max_blocks;
   int32_t *grow = p.gather + ((int64_t)b * p.hkv + kv) * p.max_vis;
-  for (int k = threadIdx.x; k < nu && k < p.max_vis; k += NFA_BLOCK) {
+  for (int k = threadIdx.x; k < nu && k < p.max_vis; k += SB) {
     const int x = k < (u1 - u0) ? u0 + k : u2 + (k - (u1 - u0));
     grow[k] = bt[x / p.page] * p.page + x % p.page;
   }
@@ -780,12 +782,12 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   } while (0)
 
 template <int DSUB, typename KV>
-__global__ void __launch_bounds__(NFA_BLOCK)
+__global__ void __launch_bounds__(SB)
     nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int CH = Elem<KV>::kChunk;
   constexpr int NC = DSUB / CH;
-  constexpr bool REG = DSUB == 32;  // page statistics held in registers
+  constexpr bool REG = DSUB == 32 && sizeof(KV) == 2;  // stats in registers
   int *s_hist = (int *)(smem + sd.a_hist);  // far hi | near hi | far lo | near lo
   int *s_tmp = (int *)(smem + sd.a_tmp);
   int *s_misc = (int *)(smem + sd.a_misc);
@@ -805,8 +807,9 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int G = p.hq / p.hkv;
   const int bs = p.bs;
   const int mb = p.max_blocks;
-  const int t0 = tile * NFA_BLOCK;
-  const int t = t0 + tid;
+  const int t0 = tile * TP;
+  const int hp = tid % TPP;       // query heads hp, hp + TPP, ... of page t
+  const int t = t0 + tid / TPP;
 
   const int64_t clk_tile = ((int64_t)row * (ntiles + 1) + tile) * 16;
   const int64_t clk_tail = ((int64_t)row * (ntiles + 1) + ntiles) * 16;
@@ -823,14 +826,13 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int64_t req = p.valid_req[b];
   const int32_t *btr = p.block_table_l + req * mb;
   if (tid < DSUB) s_dims[tid] = p.dims[tid];
-  for (int d = tid; d < p.fine_dsub; d += NFA_BLOCK) s_fdims[d] = p.fine_dims[d];
-  s_hist[tid] = 0;
-  s_hist[NFA_BLOCK + tid] = 0;
+  for (int d = tid; d < p.fine_dsub; d += SB) s_fdims[d] = p.fine_dims[d];
+  if (tid < 512) s_hist[tid] = 0;
   // pages past the block-table width are never scored (selector:205-206)
   const int kt_eff = imin(L > 0 ? (L + bs - 1) / bs : 0, mb);
   const int last_blk = L > 0 ? (L - 1) / bs : -1;
   const bool owns_last =
-      last_blk >= t0 && last_blk < t0 + NFA_BLOCK && last_blk < mb;
+      last_blk >= t0 && last_blk < t0 + TP && last_blk < mb;
 
   // ---- second round trip: request state, statistics (speculative) -------
   const int prev = p.stats_len_l[req];
@@ -886,7 +888,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 
   // scaled, bf16-rounded query rows of this kv group (selector:943-963)
   const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kv * G * p.q_stride_h;
-  for (int i = tid; i < G * DSUB; i += NFA_BLOCK) {
+  for (int i = tid; i < G * DSUB; i += SB) {
     const int j = i / DSUB;
     const int d = i % DSUB;
     const float qv = load_any(p.q, qrow + (int64_t)j * p.q_stride_h + s_dims[d],
@@ -904,7 +906,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
                                 s_stage, new_row, s_last);
   } else if (do_stats && !incremental) {
     const int pg_lo = t0;
-    const int pg_hi = imin(t0 + NFA_BLOCK, kt_eff);
+    const int pg_hi = imin(t0 + TP, kt_eff);
     int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
     if (tid == 0) {
       bool vec = true;
@@ -917,7 +919,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       s_misc[1] = vec;
     }
     if (page_phys) {
-      for (int i = tid; i < pg_hi - pg_lo; i += NFA_BLOCK) {
+      for (int i = tid; i < pg_hi - pg_lo; i += SB) {
         const int lp = imin(((pg_lo + i) * bs) / p.page, mb - 1);
         s_tphys[i] = safe_page(p, btr[lp]);
       }
@@ -935,65 +937,84 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     }
     // rebuilt statistics: complete the stores, drop cached lines, read back
     __threadfence();
-  }
-  __syncthreads();
-  if (do_stats && !incremental) {
+    __syncthreads();
     __threadfence();
     load_regs();
   }
+  __syncthreads();
   NFA_MARK(clk_tile, 3);
 
-  // ---- L1 scores, one page per thread ------------------------------------
+  // ---- L1 scores: four threads per page, one query head each ------------
   const RowGeo geo = row_geo(p, L, skip_far, skip_near);
-  uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
-  if (do_stats && t < kt_eff) {
-    bool fp, np;
-    pools(p, geo, t, &fp, &np);
-    if (fp || np) {
-      const bool need_mm = (fp && far_mm) || (np && near_mm);
-      const bool need_avg = (fp && !far_mm) || (np && !near_mm);
-      const bool from_lds = incremental && t == last_blk;
-      uint16_t mm, avg;
-      if constexpr (REG) {
-        float kmin[DSUB], kmax[DSUB], kavg[DSUB];
-        if (from_lds) {
+  bool fp = false, np = false;
+  if (do_stats && t < kt_eff) pools(p, geo, t, &fp, &np);
+  const bool need_mm = (fp && far_mm) || (np && near_mm);
+  const bool need_avg = (fp && !far_mm) || (np && !near_mm);
+  float hm[2] = {0.0f, 0.0f}, ha[2] = {0.0f, 0.0f};  // heads hp, hp + 4
+  if (fp || np) {
+    const bool from_lds = incremental && t == last_blk;
+    if constexpr (REG) {
+      if (from_lds) {
+        // the latest page's statistics, as stored, from LDS
 #pragma unroll
-          for (int d = 0; d < DSUB; ++d) {
-            kmin[d] = s_last[d];
-            kmax[d] = s_last[DSUB + d];
-            kavg[d] = s_last[2 * DSUB + d];
-          }
+        for (int c = 0; c < NC; ++c) {
+          rmn[c] = pack_chunk<KV>(s_last + c * CH);
+          rmx[c] = pack_chunk<KV>(s_last + DSUB + c * CH);
+          rsm[c] = pack_chunk<KV>(s_last + 2 * DSUB + c * CH);
+        }
+      }
+      float kavg[DSUB];
+      if (need_avg) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) unpack_chunk<KV>(rsm[c], kavg + c * CH);
+        // x / bs == x * (1 / bs) exactly when bs is a power of two
+        const float bsf = (float)bs;
+        if ((bs & (bs - 1)) == 0) {
+          const float inv = 1.0f / bsf;
+#pragma unroll
+          for (int d = 0; d < DSUB; ++d) kavg[d] = bf16r(kavg[d] * inv);
         } else {
 #pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            unpack_chunk<KV>(rmn[c], kmin + c * CH);
-            unpack_chunk<KV>(rmx[c], kmax + c * CH);
-            unpack_chunk<KV>(rsm[c], kavg + c * CH);
-          }
+          for (int d = 0; d < DSUB; ++d) kavg[d] = bf16r(kavg[d] / bsf);
         }
-        if (need_avg) {
-          // x / bs == x * (1 / bs) exactly when bs is a power of two
-          const float bsf = (float)bs;
-          if ((bs & (bs - 1)) == 0) {
-            const float inv = 1.0f / bsf;
-#pragma unroll
-            for (int d = 0; d < DSUB; ++d) kavg[d] = bf16r(kavg[d] * inv);
-          } else {
-#pragma unroll
-            for (int d = 0; d < DSUB; ++d) kavg[d] = bf16r(kavg[d] / bsf);
-          }
-        }
-        l1_scores_regs<DSUB>(kmin, kmax, kavg, s_qf, G, need_mm, need_avg, &mm,
-                             &avg);
-      } else {
-        l1_scores_mem<DSUB, KV>(p, req, kv, t, s_qf, G, need_mm, need_avg,
-                                from_lds ? s_last : nullptr, &mm, &avg);
       }
-      if (fp) far_bits = far_mm ? mm : avg;
-      if (np) near_bits = near_mm ? mm : avg;
+      for (int r = 0; r < 2; ++r) {
+        const int j = hp + TPP * r;
+        if (j < G)
+          l1_head_regs<DSUB, KV>(rmn, rmx, kavg, s_qf + j * DSUB, need_mm,
+                                 need_avg, &hm[r], &ha[r]);
+      }
+    } else {
+      for (int r = 0; r < 2; ++r) {
+        const int j = hp + TPP * r;
+        if (j < G)
+          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j * DSUB, need_mm,
+                                need_avg, from_lds ? s_last : nullptr, &hm[r],
+                                &ha[r]);
+      }
     }
   }
-  if (p.dbg_far != nullptr && t < kt_eff) {
+  // group mean: bf16 per-head scores summed in head order, gathered from the
+  // page's four lanes (every lane takes part in the shuffles)
+  float mm_acc = 0.0f, avg_acc = 0.0f;
+  {
+    const int lane0 = lane_id() & ~(TPP - 1);
+    for (int j = 0; j < G; ++j) {
+      const int src = lane0 + (j % TPP);
+      const float vm = __shfl(j < TPP ? hm[0] : hm[1], src, 64);
+      const float va = __shfl(j < TPP ? ha[0] : ha[1], src, 64);
+      mm_acc = mm_acc + vm;
+      avg_acc = avg_acc + va;
+    }
+  }
+  uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
+  {
+    const uint16_t mm = bf16_bits(mm_acc / (float)G);
+    const uint16_t avg = bf16_bits(avg_acc / (float)G);
+    if (fp) far_bits = far_mm ? mm : avg;
+    if (np) near_bits = near_mm ? mm : avg;
+  }
+  if (p.dbg_far != nullptr && t < kt_eff && hp == 0) {
     p.dbg_far[(int64_t)row * mb + t] = far_bits;
     p.dbg_near[(int64_t)row * mb + t] = near_bits;
   }
@@ -1004,12 +1025,14 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     // near pages at or above it
     const uint32_t fk = score_key(far_bits);
     const uint32_t nk = score_key(near_bits);
-    g_keys[t] = (uint16_t)(fk ? fk : nk);
-    if (fk) atomicAdd(&s_hist[fk >> 8], 1);
-    if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
+    if (hp == 0) {
+      g_keys[t] = (uint16_t)(fk ? fk : nk);
+      if (fk) atomicAdd(&s_hist[fk >> 8], 1);
+      if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
+    }
   }
   __syncthreads();
-  {
+  if (tid < 256) {
     const int hf = s_hist[tid];
     const int hn = s_hist[256 + tid];
     if (hf) atomicAdd(&g_hist[tid], hf);
@@ -1053,43 +1076,43 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int near_start = geo.near_start;
 
   // row histograms into LDS, reset for the next launch
-  {
-    const int hf = atomicExch(&g_hist[tid], 0);
-    const int hn = atomicExch(&g_hist[256 + tid], 0);
-    s_hist[tid] = hf;
-    s_hist[256 + tid] = hn;
+  if (tid < 512) {
+    s_hist[tid] = atomicExch(&g_hist[tid], 0);
     s_hist[512 + tid] = 0;
-    s_hist[768 + tid] = 0;
   }
-  for (int w = tid; w < sd.words; w += NFA_BLOCK) {
+  uint32_t *s_eqb = (uint32_t *)(smem + sd.a_eqb);
+  for (int w = tid; w < sd.words; w += SB) {
     s_cbits[w] = 0u;
+    s_eqb[w] = 0u;
     if (dbg) {
       s_dbf[w] = 0u;
       s_dbn[w] = 0u;
     }
   }
-  if (sd.nseg == 1) stage_keys(g_keys, 0, sd.segc, s_keys);
+  if (tid == 0) {
+    s_misc[3] = 0;  // debug selection list lengths (far, near)
+    s_misc[4] = 0;
+  }
+  if (sd.nseg == 1) stage_keys(g_keys, 0, sd.seg, s_keys);
   __syncthreads();
   // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
   if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 8);
   if (wave_id() == 1) wave_threshold_bin(s_hist + 256, p.k_n, s_tmp + 12);
   __syncthreads();
   const int hbf = s_tmp[8], hbn = s_tmp[12];
-  const int seg_pages = NFA_BLOCK * sd.segc;
-  const int my0 = tid * sd.segc;  // first page of this thread in a segment
   if (hbf >= 0 || hbn >= 0) {
     // refinement: low-byte histograms of the keys in the threshold bins
     for (int sg = 0; sg < sd.nseg; ++sg) {
-      const int seg_base = sg * seg_pages;
+      const int seg_base = sg * sd.seg;
       if (sd.nseg > 1) {
         __syncthreads();
-        stage_keys(g_keys, seg_base, sd.segc, s_keys);
+        stage_keys(g_keys, seg_base, sd.seg, s_keys);
         __syncthreads();
       }
-      const int n = imin(sd.segc, kt_eff - seg_base - my0);
-      for (int i = 0; i < n; ++i) {
-        const uint32_t k = s_keys[my0 + i];
-        const bool near = seg_base + my0 + i >= near_start;
+      const int n = imin(sd.seg, kt_eff - seg_base);
+      for (int i = tid; i < n; i += SB) {
+        const uint32_t k = s_keys[i];
+        const bool near = seg_base + i >= near_start;
         const int hb = near ? hbn : hbf;
         if (k != 0u && (int)(k >> 8) == hb)
           atomicAdd(&s_hist[(near ? 768 : 512) + (k & 255u)], 1);
@@ -1107,70 +1130,72 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   NFA_MARK(clk_tail, 1);
 
   // ---- selected pages -> candidate page bitmap ---------------------------
-  const bool ordered = tie_cut(tf) || tie_cut(tn) || dbg;
-  int carry[4] = {0, 0, 0, 0};  // far >T, far ==T, near >T, near ==T
+  auto select_page = [&](int page, uint32_t k, bool near) {
+    const uint32_t bit = 1u << (page & 31);
+    if (any_cand && page * bs < tok_hi && page * bs + bs > tok_lo)
+      atomicOr(&s_cbits[page >> 5], bit);
+    if (dbg) {
+      const int pos = atomicAdd(&s_misc[near ? 4 : 3], 1);
+      s_dsel[(near ? p.k_f : 0) + pos] = ((uint64_t)k << 32) | (uint32_t)page;
+      atomicOr(near ? &s_dbn[page >> 5] : &s_dbf[page >> 5], bit);
+    }
+  };
+  // keys above the threshold are selected outright; keys equal to it too
+  // unless only some of them are, then they go to the tie bitmap
   for (int sg = 0; sg < sd.nseg; ++sg) {
-    const int seg_base = sg * seg_pages;
+    const int seg_base = sg * sd.seg;
     if (sd.nseg > 1) {
       __syncthreads();
-      stage_keys(g_keys, seg_base, sd.segc, s_keys);
+      stage_keys(g_keys, seg_base, sd.seg, s_keys);
       __syncthreads();
     }
-    const int n = imin(sd.segc, kt_eff - seg_base - my0);
-    int cnt[4] = {0, 0, 0, 0};
-    if (ordered) {
-      for (int i = 0; i < n; ++i) {
-        const uint32_t k = s_keys[my0 + i];
-        const int o = seg_base + my0 + i >= near_start ? 2 : 0;
-        const uint32_t T = o ? (uint32_t)tn.T : (uint32_t)tf.T;
-        cnt[o] += k > T;
-        cnt[o + 1] += (k == T && k != 0u);
-      }
-      int tot4[4];
-      block_scan_n<4>(cnt, s_tmp + 32, tot4);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        cnt[q] += carry[q];
-        carry[q] += tot4[q];
-      }
-    }
-    int eqf = cnt[1], eqn = cnt[3];
-    int posf = cnt[0] + imin(cnt[1], tf.need);
-    int posn = cnt[2] + imin(cnt[3], tn.need);
-    for (int i = 0; i < n; ++i) {
-      const uint32_t k = s_keys[my0 + i];
+    const int n = imin(sd.seg, kt_eff - seg_base);
+    for (int i = tid; i < n; i += SB) {
+      const uint32_t k = s_keys[i];
       if (k == 0u) continue;
-      const int page = seg_base + my0 + i;
+      const int page = seg_base + i;
       const bool near = page >= near_start;
-      bool sel;
-      if (!near) {
-        sel = k > (uint32_t)tf.T;
-        if (k == (uint32_t)tf.T) {
-          sel = eqf < tf.need;
-          ++eqf;
-        }
-      } else {
-        sel = k > (uint32_t)tn.T;
-        if (k == (uint32_t)tn.T) {
-          sel = eqn < tn.need;
-          ++eqn;
-        }
-      }
-      if (!sel) continue;
-      const uint32_t bit = 1u << (page & 31);
-      if (any_cand && page * bs < tok_hi && page * bs + bs > tok_lo)
-        atomicOr(&s_cbits[page >> 5], bit);
-      if (dbg) {
-        if (!near) {
-          s_dsel[posf++] = ((uint64_t)k << 32) | (uint32_t)page;
-          atomicOr(&s_dbf[page >> 5], bit);
-        } else {
-          s_dsel[p.k_f + posn++] = ((uint64_t)k << 32) | (uint32_t)page;
-          atomicOr(&s_dbn[page >> 5], bit);
-        }
+      const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
+      const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
+      if (k > T || (k == T && all_eq))
+        select_page(page, k, near);
+      else if (k == T)
+        atomicOr(&s_eqb[page >> 5], 1u << (page & 31));
+    }
+  }
+  __syncthreads();
+  if (tie_cut(tf) || tie_cut(tn)) {
+    // tied pages of each pool in page order: the first `need` are selected
+    const int wpt = (sd.words + SB - 1) / SB;
+    const int w0 = tid * wpt;
+    const int w1 = imin(w0 + wpt, sd.words);
+    auto far_mask = [&](int w) -> uint32_t {
+      const int d = near_start - w * 32;
+      return d >= 32 ? 0xFFFFFFFFu : (d <= 0 ? 0u : ((1u << d) - 1u));
+    };
+    int c[2] = {0, 0};
+    for (int w = w0; w < w1; ++w) {
+      const uint32_t bits = s_eqb[w];
+      const uint32_t fm = far_mask(w);
+      c[0] += __popc(bits & fm);
+      c[1] += __popc(bits & ~fm);
+    }
+    int tot2[2];
+    block_scan_n<2, SW>(c, s_tmp + 32, tot2);
+    for (int w = w0; w < w1; ++w) {
+      uint32_t bits = s_eqb[w];
+      const uint32_t fm = far_mask(w);
+      while (bits) {
+        const int bit = __ffs(bits) - 1;
+        bits &= bits - 1u;
+        const bool near = ((fm >> bit) & 1u) == 0u;
+        const int rank = near ? c[1]++ : c[0]++;
+        if (rank < (near ? tn.need : tf.need))
+          select_page(w * 32 + bit, (uint32_t)(near ? tn.T : tf.T), near);
       }
     }
   }
+  NFA_MARK(clk_tail, 2);
   __syncthreads();
   if (tid == 0 && any_cand) {
     // sink and SWA bypass pages (selector:1195-1251)
@@ -1187,7 +1212,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   __syncthreads();
   // compaction: sorted unique candidate pages, then their physical pages
-  const int wpt = (sd.words + NFA_BLOCK - 1) / NFA_BLOCK;
+  const int wpt = (sd.words + SB - 1) / SB;
   const int w0 = tid * wpt;
   const int w1 = imin(w0 + wpt, sd.words);
   int *s_pages = (int *)(smem + sd.a_pages);
@@ -1195,7 +1220,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   {
     int c1 = 0;
     for (int w = w0; w < w1; ++w) c1 += __popc(s_cbits[w]);
-    int pos = block_scan_exclusive(c1, s_tmp, &np_u);
+    int pos = block_scan_exclusive<SW>(c1, s_tmp, &np_u);
     for (int w = w0; w < w1; ++w) {
       uint32_t bits = s_cbits[w];
       while (bits) {
@@ -1205,12 +1230,13 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       }
     }
   }
+  NFA_MARK(clk_tail, 3);
   __syncthreads();
   np_u = imin(np_u, sd.np);
   {
     int *g_pages = (int *)(ws + sd.w_pages) + (int64_t)row * sd.np;
     int *g_pphys = (int *)(ws + sd.w_pphys) + (int64_t)row * sd.np;
-    for (int i = tid; i < np_u; i += NFA_BLOCK) {
+    for (int i = tid; i < np_u; i += SB) {
       const int pg = s_pages[i];
       g_pages[i] = pg;
       g_pphys[i] = btr[imin((pg * bs) / p.page, mb - 1)];
@@ -1233,6 +1259,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       g_vec[0] = vec ? nch : 0;
     }
   }
+  NFA_MARK(clk_tail, 4);
   // L1 debug outputs: I_F / I_N (selector:1766-1803 order: valid pages by
   // (score desc, page asc), then -inf fillers by ascending page)
   if (dbg) {
@@ -1243,7 +1270,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       const uint32_t *bm = pool == 0 ? s_dbf : s_dbn;
       int32_t *out = (pool == 0 ? p.dbg_i_f + (int64_t)row * p.k_f
                                 : p.dbg_i_n + (int64_t)row * p.k_n);
-      for (int i = tid; i < nsel; i += NFA_BLOCK) {
+      for (int i = tid; i < nsel; i += SB) {
         const uint64_t ki = sel[i];
         const uint32_t vi = (uint32_t)(ki >> 32), ti = (uint32_t)ki;
         int rank = 0;
@@ -1259,7 +1286,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
         int z = 0;
         for (int w = w0; w < w1; ++w) z += 32 - __popc(bm[w]);
         int tz;
-        int r = block_scan_exclusive(z, s_tmp, &tz);
+        int r = block_scan_exclusive<SW>(z, s_tmp, &tz);
         for (int w = w0; w < w1 && r < nfill; ++w) {
           uint32_t zeros = ~bm[w];
           while (zeros && r < nfill) {
@@ -1270,7 +1297,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       }
     }
   }
-  NFA_MARK(clk_tail, 2);
+  NFA_MARK(clk_tail, 6);
 }
 
 // ---------------------------------------------------------------------------
@@ -1324,10 +1351,9 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     }
     return v;
   };
-  hist[tid] = 0;
-  hist[NFA_BLOCK + tid] = 0;
+  if (tid < 512) hist[tid] = 0;
   __syncthreads();
-  for (int i = tid; i < n; i += NFA_BLOCK) {
+  for (int i = tid; i < n; i += SB) {
     const uint32_t v = key(i);
     if (v) atomicAdd(&hist[v >> 8], 1);
   }
@@ -1340,7 +1366,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
   uint32_t T = 0u;
   int need = 0;
   if (hb >= 0) {
-    for (int i = tid; i < n; i += NFA_BLOCK) {
+    for (int i = tid; i < n; i += SB) {
       const uint32_t v = key(i);
       if (v != 0u && (int)(v >> 8) == hb) atomicAdd(&hist[256 + (v & 255u)], 1);
     }
@@ -1352,7 +1378,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
   }
   const int nch = total < quota ? total : quota;
   // ordered emission, one contiguous run of slots per thread
-  const int per = (n + NFA_BLOCK - 1) / NFA_BLOCK;
+  const int per = (n + SB - 1) / SB;
   const int ia = tid * per;
   const int ib = imin(n, ia + per);
   int c[2] = {0, 0};
@@ -1362,7 +1388,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     c[1] += (v == T && v != 0u);
   }
   int tot2[2];
-  block_scan_n<2>(c, tmp + 32, tot2);
+  block_scan_n<2, SW>(c, tmp + 32, tot2);
   {
     int eq = c[1];
     int pos = c[0] + (c[1] < need ? c[1] : need);
@@ -1384,7 +1410,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
   __syncthreads();
   // hole fill: the (quota - nch) smallest ids of [rlo, rhi) not chosen
   const int nfill_req = quota - nch;
-  for (int i = tid; i < nfill_req; i += NFA_BLOCK) {
+  for (int i = tid; i < nfill_req; i += SB) {
     int lo = 0, hi = nch;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -1414,7 +1440,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
   const int drop = lower_bound_i32(rl.l0, nch, sink) +
                    lower_bound_i32(rl.l1, nfill, sink);
   const int base_out = *mid_count;
-  for (int j = tid; j < nch; j += NFA_BLOCK) {
+  for (int j = tid; j < nch; j += SB) {
     const int v = rl.l0[j];
     if (v >= sink) {
       const int pos = base_out + j + lower_bound_i32(rl.l1, nfill, v) - drop;
@@ -1422,7 +1448,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
       rl.mslot[pos] = rl.l0x[j];
     }
   }
-  for (int j = tid; j < nfill; j += NFA_BLOCK) {
+  for (int j = tid; j < nfill; j += SB) {
     const int v = rl.l1[j];
     if (v >= sink) {
       const int pos = base_out + j + lower_bound_i32(rl.l0, nch, v) - drop;
@@ -1436,11 +1462,11 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
 }
 
 template <typename KV>
-__global__ void __launch_bounds__(NFA_BLOCK)
+__global__ void __launch_bounds__(SB)
     nfa_l2_kernel(const NfaSelectParams p, const SelDims sd) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int CH = Elem<KV>::kChunk;
-  constexpr int TPS = NFA_BLOCK / kL2Slots;  // threads per dense slot
+  const int TPS = SB / sd.l2slots;  // threads per dense slot
   int *s_hist = (int *)(smem + sd.b_hist);
   int *s_tmp = (int *)(smem + sd.b_tmp);
   int *s_misc = (int *)(smem + sd.b_misc);
@@ -1472,10 +1498,10 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int np_u = ((const int *)(ws + sd.w_npu))[row];
   const int nch = ((const int *)(ws + sd.w_l2vec))[0];  // 0: scalar L2 dims
   const int n_dense = np_u * bs;
-  for (int d = tid; d < p.fine_dsub; d += NFA_BLOCK) s_fdims[d] = p.fine_dims[d];
+  for (int d = tid; d < p.fine_dsub; d += SB) s_fdims[d] = p.fine_dims[d];
   const int sl = tid / TPS;   // dense slot of this thread within the chunk
-  const int part = tid % TPS; // which quarter of the slot's L2 dims it loads
-  const int i = chunk * kL2Slots + sl;
+  const int part = tid % TPS; // which of the slot's 16-byte chunks it loads
+  const int i = chunk * sd.l2slots + sl;
   int tok = -1, phys = 0, pgphys = 0;
   {
     const int pi = i / bs;
@@ -1528,7 +1554,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   // grouped L2 query (selector:979-1002)
   const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kv * G * p.q_stride_h;
-  for (int d = tid; d < p.fine_dsub; d += NFA_BLOCK) {
+  for (int d = tid; d < p.fine_dsub; d += SB) {
     const int dim = s_fdims[d];
     float qv[GMAX];
 #pragma unroll
@@ -1548,8 +1574,8 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
   const int tok_lo = imax(p.sink_tokens, lb.lower);
   const int tok_hi = imin(imin(lb.lo, L), lb.upper);
-  if (tid < kL2Slots) {
-    const int ii = chunk * kL2Slots + tid;
+  if (tid < sd.l2slots) {
+    const int ii = chunk * sd.l2slots + tid;
     const int tk = s_tok[tid];
     if (tk >= 0) {
       uint16_t key = 0;
@@ -1610,26 +1636,27 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     const int n16 = (n_dense + 7) / 8;
     const uint4 *src = reinterpret_cast<const uint4 *>(g_dk);
     uint4 *dst = reinterpret_cast<uint4 *>(s_dk);
-    for (int u0 = 0; u0 < n16; u0 += 4 * NFA_BLOCK) {
+    for (int u0 = 0; u0 < n16; u0 += 4 * SB) {
       uint4 r[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int u = u0 + tid + k * NFA_BLOCK;
+        const int u = u0 + tid + k * SB;
         r[k] = u < n16 ? src[u] : make_uint4(0u, 0u, 0u, 0u);
       }
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int u = u0 + tid + k * NFA_BLOCK;
+        const int u = u0 + tid + k * SB;
         if (u < n16) dst[u] = r[k];
       }
     }
-    for (int k = tid; k < np_u; k += NFA_BLOCK) {
+    for (int k = tid; k < np_u; k += SB) {
       s_pages[k] = g_pages[k];
       s_pphys[k] = g_pphys[k];
     }
     if (tid == 0) s_misc[2] = 0;  // middle count
   }
   __syncthreads();
+  NFA_MARK(clk_b, 3);
 
   // ---- L2 top-quota + hole fill (+ fixed near quota), selector:519-566,
   //      873-940 -------------------------------------------------------------
@@ -1668,13 +1695,13 @@ __global__ void __launch_bounds__(NFA_BLOCK)
                       &s_misc[2], s_hist, s_tmp);
   }
   __syncthreads();
-  NFA_MARK(clk_b, 3);
+  NFA_MARK(clk_b, 4);
   int mcount = s_misc[2];
   if (mcount > p.k2) mcount = p.k2;
   const int *s_mid = rl.mid;
   const int *s_mslot = rl.mslot;
   if (p.dbg_middle != nullptr) {
-    for (int k = tid; k < p.k2; k += NFA_BLOCK)
+    for (int k = tid; k < p.k2; k += SB)
       p.dbg_middle[(int64_t)row * p.k2 + k] = k < mcount ? s_mid[k] : 0;
     if (tid == 0) p.dbg_counts[row] = mcount;
   }
@@ -1683,9 +1710,9 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   int32_t *grow = p.gather + ((int64_t)b * p.hkv + kv) * p.max_vis;
   if (p.middle_only) {
     const int n = imin(mcount, p.max_vis);
-    for (int k = tid; k < n; k += NFA_BLOCK) grow[k] = s_mslot[k];
+    for (int k = tid; k < n; k += SB) grow[k] = s_mslot[k];
     if (tid == 0) p.vis_lens[b * p.hkv + kv] = n;
-    NFA_MARK(clk_b, 4);
+    NFA_MARK(clk_b, 5);
     return;
   }
   auto in_u = [&](int x) { return (x >= u0 && x < u1) || (x >= u2 && x < u3); };
@@ -1695,12 +1722,12 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   // middle entries inside U are duplicates; the rest keep their order
   int nkeep;
   {
-    const int per = (mcount + NFA_BLOCK - 1) / NFA_BLOCK;
+    const int per = (mcount + SB - 1) / SB;
     const int ia = tid * per;
     const int ib = imin(mcount, ia + per);
     int c = 0;
     for (int k = ia; k < ib; ++k) c += !in_u(s_mid[k]);
-    int r = block_scan_exclusive(c, s_tmp, &nkeep);
+    int r = block_scan_exclusive<SW>(c, s_tmp, &nkeep);
     for (int k = ia; k < ib; ++k) {
       const int x = s_mid[k];
       if (in_u(x)) continue;
@@ -1718,7 +1745,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
                    lower_bound_i32(s_mid, mcount, u2);
     return lbx - d0 - d1;
   };
-  for (int k = tid; k < nu; k += NFA_BLOCK) {
+  for (int k = tid; k < nu; k += SB) {
     const int x = k < (u1 - u0) ? u0 + k : u2 + (k - (u1 - u0));
     const int dest = k + kept_below(x);
     const int slot = k == tid ? pre_slot
@@ -1726,7 +1753,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     if (dest < p.max_vis) grow[dest] = slot;
   }
   if (tid == 0) p.vis_lens[b * p.hkv + kv] = nkeep + nu;
-  NFA_MARK(clk_b, 4);
+  NFA_MARK(clk_b, 5);
 }
 
 }  // namespace nfa
@@ -1823,11 +1850,11 @@ static hipError_t launch_select(const NfaSelectParams &p, hipStream_t stream) {
   const SelDims sd = nfa::sel_dims(p);
   const int rows = p.batch * p.hkv;
   hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV>), dim3(sd.ntiles, rows),
-                     dim3(NFA_BLOCK), sd.lds_a, stream, p, sd);
+                     dim3(nfa::SB), sd.lds_a, stream, p, sd);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL((nfa::nfa_l2_kernel<KV>), dim3(sd.nchunk, rows),
-                     dim3(NFA_BLOCK), sd.lds_b, stream, p, sd);
+                     dim3(nfa::SB), sd.lds_b, stream, p, sd);
   return hipGetLastError();
 }
 
@@ -1841,9 +1868,9 @@ extern "C" int32_t nfa_select_layer(const NfaSelectParams *p, void *stream) {
     dim3 grid(p->batch * p->hkv);
     if (bf)
       hipLaunchKernelGGL(nfa::nfa_protected_kernel<uint16_t>, grid,
-                         dim3(NFA_BLOCK), 0, s, *p);
+                         dim3(nfa::SB), 0, s, *p);
     else
-      hipLaunchKernelGGL(nfa::nfa_protected_kernel<float>, grid, dim3(NFA_BLOCK),
+      hipLaunchKernelGGL(nfa::nfa_protected_kernel<float>, grid, dim3(nfa::SB),
                          0, s, *p);
     err = hipGetLastError();
     if (err != hipSuccess) {
