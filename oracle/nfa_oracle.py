@@ -28,12 +28,19 @@ the order is declared here and the HIP kernels follow it exactly):
   dtype (the reference packs them as 16-bit keys, ``selector:1482, 688``);
   page statistics are stored in the KV dtype (``selector:120-124``).
 
-Pinning.  Every function below is checked in ``tests/test_oracle_*.py``
-against closed forms, brute force on tiny inputs, torch library routines and
-the known answers of the reference's own tests (there are no golden vectors
-for this path in the reference).  L1 page indices above 65535 use exact
-(score, page) order; the reference packs the page into 16 bits
-(``selector:1481-1484``) and would alias there.
+Pinning (the reference holds no golden vectors for this path).
+``tests/test_oracle_pinning.py`` checks bf16 rounding against torch, the order
+key against the float order of all 65536 bf16 patterns, the declared fp32
+sum order with order- and FMA-sensitive closed forms, page statistics and
+query preparation against torch, L1 scores and L2 logits against exact
+integer arithmetic, L1 top-k, candidate expansion + owner tags, L2
+top-quota + hole fill and the final union against brute force, and the
+attention against torch softmax.  ``tests/test_oracle_known_answers.py``
+checks the region geometry, bounds and fixed quotas against the known
+answers of the reference's own tests.  ``fake_quant4`` (the optional 4-bit
+L2 keys, read by no selector code of the reference) is parity unpinned.
+L1 page indices above 65535 use exact (score, page) order; the reference
+packs the page into 16 bits (``selector:1481-1484``) and would alias there.
 """
 from __future__ import annotations
 
@@ -474,7 +481,10 @@ def owned_slots(cfg: NfaConfig, token, active, pack_r, lower, upper):
 # ---------------------------------------------------------------------------
 
 def fake_quant4(x):
-    """bf16 op-by-op ``min_max_per_token_quant`` over the last axis."""
+    """bf16 op-by-op ``min_max_per_token_quant`` over the last axis.
+
+    Parity unpinned: no selector code of the reference reads ``l2_quant``.
+    """
     x = bf16r(x)
     mx = x.max(axis=-1, keepdims=True)
     mn = x.min(axis=-1, keepdims=True)

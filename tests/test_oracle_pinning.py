@@ -1,0 +1,328 @@
+"""Pins every function of the CPU oracle against something independent of it.
+
+Each check is chosen so that a plausible slip in the oracle (a dropped term,
+a wrong sign or index, a transposed operand, a reordered sum) fails it:
+torch's own bf16 conversion and softmax, exact integer arithmetic where the
+inputs make every fp32 step exact, order-sensitive fp32 sums whose result
+is known in closed form, and brute force over small inputs (full sorts and
+set unions instead of the oracle's packed keys, owner tags and binary
+searches).  The reference holds no golden vectors for this path; its own
+tests' known answers are checked in test_oracle_known_answers.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import nfa_oracle as orc
+
+F32 = np.float32
+
+
+def _cfg(**kw):
+    base = dict(hq=8, hkv=2, head_dim=16, head_dim_v=16, bs=4, page=4,
+                max_blocks=64, geo_sink=4, geo_near=32, geo_window=16,
+                sink_tokens=4, swa=16, near_len=32, k1=6, near_pages=2, k2=64,
+                dims=np.arange(8), fine_dims=np.arange(8), scale=1.0)
+    base.update(kw)
+    return orc.NfaConfig(**base)
+
+
+def _torch_bf16_bits(x):
+    t = torch.from_numpy(np.asarray(x, dtype=np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().astype(np.int64) & 0xFFFF
+
+
+# ---------------------------------------------------------------------------
+# bf16 rounding and the order key
+# ---------------------------------------------------------------------------
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(20000).astype(F32) * F32(1e3)
+    # exact halfway cases (ties to even) and their neighbours
+    hi = rng.integers(0, 1 << 15, 4000, dtype=np.uint32) << 16
+    half = np.concatenate([hi | 0x8000, hi | 0x7FFF, hi | 0x8001]).view(F32)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, 1e-45, -1e-45, 3.4e38,
+                        -3.4e38, 1.0, -1.0], dtype=F32)
+    vals = np.concatenate([x, half[np.isfinite(half)], special])
+    np.testing.assert_array_equal(orc.bf16_bits(vals).astype(np.int64),
+                                  _torch_bf16_bits(vals))
+    nans = np.array([0x7FC00000, 0xFFC00000, 0x7F800001, 0xFF812345],
+                    dtype=np.uint32).view(F32)
+    assert (orc.bf16_bits(nans) == orc.NAN_BITS).all()
+
+
+def test_ord16u_orders_like_the_values():
+    bits = np.arange(1 << 16, dtype=np.int64)
+    vals = orc.bits_to_f32(bits.astype(np.uint16))
+    finite_or_inf = ~np.isnan(vals)
+    b = bits[finite_or_inf]
+    order = b[np.argsort(orc.ord16u(b), kind='stable')]
+    v = orc.bits_to_f32(order.astype(np.uint16))
+    assert (np.diff(v.astype(np.float64)) >= 0).all()
+    # -0 ranks just below +0, NaN (canonical) above +inf
+    assert orc.ord16u(0x8000) + 1 == orc.ord16u(0x0000)
+    assert orc.ord16u(orc.NAN_BITS) > orc.ord16u(0x7F80)
+    assert len(set(orc.ord16u(b).tolist())) == len(b)
+
+
+# ---------------------------------------------------------------------------
+# declared fp32 reduction order
+# ---------------------------------------------------------------------------
+
+def test_seq_dot_is_ascending_fp32_without_fma():
+    one = np.ones(3, dtype=F32)
+    # the 1 survives only if it is added after the large terms cancel
+    assert orc.seq_dot(np.array([1e8, -1e8, 1], dtype=F32), one) == F32(1)
+    assert orc.seq_dot(np.array([1e8, 1, -1e8], dtype=F32), one) == F32(0)
+    # product rounded before the add: (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24
+    a = F32(1 + 2.0 ** -12)
+    got = orc.seq_dot(np.array([-1, a], dtype=F32), np.array([1, a], dtype=F32))
+    assert got == F32(2.0 ** -11)   # a fused multiply-add would keep 2^-24
+    ints = np.random.default_rng(2).integers(-50, 50, (7, 33)).astype(F32)
+    w = np.random.default_rng(3).integers(-5, 5, (33,)).astype(F32)
+    np.testing.assert_array_equal(orc.seq_dot(ints, w),
+                                  (ints.astype(np.int64) @ w.astype(np.int64)).astype(F32))
+    np.testing.assert_array_equal(orc.seq_sum(ints), ints.astype(np.int64).sum(0).astype(F32))
+
+
+# ---------------------------------------------------------------------------
+# page statistics and query preparation
+# ---------------------------------------------------------------------------
+
+def _pool(rng, n_phys, hkv, page, d, integer=True):
+    if integer:
+        return rng.integers(-60, 60, (n_phys, 1, hkv, page, d)).astype(F32)
+    return orc.bf16r(rng.standard_normal((n_phys, 1, hkv, page, d)).astype(F32))
+
+
+@pytest.mark.parametrize('bs,page', [(4, 4), (4, 8), (8, 4)])
+def test_page_stats_against_torch(bs, page):
+    rng = np.random.default_rng(4 + bs + page)
+    cfg = _cfg(bs=bs, page=page, dims=np.array([1, 3, 4, 7, 9, 12]))
+    length = 37
+    n_phys = 20
+    k_pool = _pool(rng, n_phys, cfg.hkv, page, cfg.head_dim)
+    bt = rng.permutation(n_phys).astype(np.int64)
+    for kv in range(cfg.hkv):
+        kmin, kmax, ksum = orc.page_stats(cfg, k_pool, bt, length, kv)
+        tok = np.arange(length)
+        keys = torch.from_numpy(k_pool[bt[tok // page], 0, kv, tok % page][:, cfg.dims])
+        for p in range((length + bs - 1) // bs):
+            blk = keys[p * bs:min(length, p * bs + bs)]
+            exp_min = blk.amin(0).to(torch.bfloat16).float().numpy()
+            exp_max = blk.amax(0).to(torch.bfloat16).float().numpy()
+            exp_sum = blk.double().sum(0).float().to(torch.bfloat16).float().numpy()
+            np.testing.assert_array_equal(kmin[p], exp_min)
+            np.testing.assert_array_equal(kmax[p], exp_max)
+            np.testing.assert_array_equal(ksum[p], exp_sum)
+
+
+def test_page_stats_signed_zero_keeps_the_earlier_token():
+    cfg = _cfg(bs=4, page=4, dims=np.array([0]), hkv=1)
+    k_pool = np.zeros((1, 1, 1, 4, 16), dtype=F32)
+    k_pool[0, 0, 0, :, 0] = [0.0, -0.0, -0.0, 0.0]
+    kmin, kmax, _ = orc.page_stats(cfg, k_pool, np.array([0]), 4, 0)
+    assert not np.signbit(kmin[0, 0]) and not np.signbit(kmax[0, 0])
+    k_pool[0, 0, 0, :, 0] = [-0.0, 0.0, 0.0, -0.0]
+    kmin, kmax, _ = orc.page_stats(cfg, k_pool, np.array([0]), 4, 0)
+    assert np.signbit(kmin[0, 0]) and np.signbit(kmax[0, 0])
+
+
+def test_query_preparation_against_torch():
+    rng = np.random.default_rng(5)
+    cfg = _cfg(scale=0.125, dims=np.array([0, 5, 9]), fine_dims=np.array([2, 3, 15]))
+    q = rng.standard_normal((cfg.hq, cfg.head_dim)).astype(F32)
+    got = orc.prepare_q(cfg, q, cfg.dims)
+    exp = (torch.from_numpy(q[:, cfg.dims]) * 0.125).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(got, exp)
+    # grouped: exact small integers, head kv*G + j belongs to kv head kv
+    qi = rng.integers(-8, 8, (cfg.hq, cfg.head_dim)).astype(F32)
+    cfg1 = _cfg(scale=1.0, fine_dims=np.array([2, 3, 15]))
+    g = cfg1.group
+    exp_g = qi[:, cfg1.fine_dims].reshape(cfg1.hkv, g, -1).sum(1)
+    np.testing.assert_array_equal(orc.prepare_q_grouped(cfg1, qi), exp_g)
+
+
+# ---------------------------------------------------------------------------
+# L1 scores and top-k
+# ---------------------------------------------------------------------------
+
+def test_l1_page_scores_exact_integers():
+    rng = np.random.default_rng(6)
+    cfg = _cfg(bs=4, dims=np.arange(6))
+    g = cfg.group
+    n = 50
+    kmin = rng.integers(-4, 2, (n, 6)).astype(F32)
+    kmax = kmin + rng.integers(0, 4, (n, 6)).astype(F32)
+    ksum = (4 * rng.integers(-3, 3, (n, 6))).astype(F32)   # kavg = ksum / 4 exact
+    q = rng.integers(-3, 4, (g, 6)).astype(F32)
+    mm, avg = orc.l1_page_scores(cfg, kmin, kmax, ksum, q)
+    ql, qh = np.minimum(q, 0), np.maximum(q, 0)
+    per_head = (kmin.astype(np.int64) @ ql.T.astype(np.int64)
+                + kmax.astype(np.int64) @ qh.T.astype(np.int64))   # [n, g]
+    exp_mm = _torch_bf16_bits(per_head.sum(1) / g)
+    per_avg = (ksum.astype(np.int64) // 4) @ q.T.astype(np.int64)
+    exp_avg = _torch_bf16_bits(per_avg.sum(1) / g)
+    np.testing.assert_array_equal(mm.astype(np.int64), exp_mm)
+    np.testing.assert_array_equal(avg.astype(np.int64), exp_avg)
+
+
+def test_l1_topk_brute_force():
+    rng = np.random.default_rng(7)
+    for trial in range(200):
+        kt = int(rng.integers(1, 60))
+        pool = rng.integers(0, 6, kt)      # few distinct values -> many ties
+        bits = orc.bf16_bits(pool.astype(F32) - 2).astype(np.int64)
+        bits[rng.random(kt) < 0.1] = orc.NEG_INF_BITS
+        bits[rng.random(kt) < 0.05] = orc.NAN_BITS
+        lo = int(rng.integers(0, kt))
+        hi = int(rng.integers(lo, kt + 1))
+        k = int(rng.integers(0, kt + 1))
+        got = orc.l1_topk(bits, lo, hi, k, kt)
+        eff = [int(bits[t]) if lo <= t < hi else orc.NEG_INF_BITS for t in range(kt)]
+        exp = sorted(range(kt), key=lambda t: (-int(orc.ord16u(eff[t])), t))[:k]
+        assert got.tolist() == exp, trial
+
+
+# ---------------------------------------------------------------------------
+# candidates, L2 logits and L2 selection
+# ---------------------------------------------------------------------------
+
+def test_candidate_tokens_brute_force():
+    rng = np.random.default_rng(8)
+    for trial in range(60):
+        cfg = _cfg(bs=4, k1=6, near_pages=2, sink_tokens=int(rng.integers(0, 7)),
+                   swa=int(rng.choice([4, 6, 16])), max_blocks=64)
+        length = int(rng.integers(8, 200))
+        kt = (length + cfg.bs - 1) // cfg.bs
+        far = orc.bf16_bits(rng.standard_normal(kt).astype(F32)).astype(np.uint16)
+        near = far.copy()
+        far[rng.random(kt) < 0.5] = orc.NEG_INF_BITS
+        near[rng.random(kt) < 0.5] = orc.NEG_INF_BITS
+        i_f = orc.l1_topk(far, 0, kt, cfg.k_f, cfg.kt_cap)
+        i_n = orc.l1_topk(near, 0, kt, cfg.k_n, cfg.kt_cap)
+        skip = (bool(rng.random() < 0.2), bool(rng.random() < 0.2))
+        lower, upper, quota = orc.l2_bounds(cfg, length, *skip)
+        token, active, pack_r = orc.candidate_slots(cfg, i_f, i_n, far, near, length)
+        owned = orc.owned_slots(cfg, token, active, pack_r, lower, upper)
+        got = sorted(token[owned].tolist())
+        # brute force: tokens of the finite-score selected pages and of the
+        # kept bypass pages, inside [max(sink, lower), min(lo, L, upper))
+        lo = max(0, length - cfg.swa)
+        # (-inf fillers may point past kt; they never become candidates)
+        pages = {int(p) for p in i_f if p < kt and far[p] != orc.NEG_INF_BITS}
+        pages |= {int(p) for p in i_n if p < kt and near[p] != orc.NEG_INF_BITS}
+        spl = cfg.sink_tokens // cfg.bs
+        if cfg.sink_tokens % cfg.bs:
+            pages.add(spl)
+        byp1 = (lo % cfg.bs != 0) and (lo // cfg.bs >= spl)
+        if cfg.sink_tokens % cfg.bs:
+            byp1 = byp1 and lo // cfg.bs != spl
+        if byp1:
+            pages.add(lo // cfg.bs)
+        t_lo = max(cfg.sink_tokens, lower)
+        t_hi = min(lo, length, upper)
+        exp = sorted(t for p in pages for t in range(p * cfg.bs, p * cfg.bs + cfg.bs)
+                     if t_lo <= t < t_hi)
+        assert got == exp, trial
+
+
+def test_l2_logits_exact_integers():
+    rng = np.random.default_rng(9)
+    cfg = _cfg(fine_dims=np.array([1, 4, 6, 11]))
+    k_pool = _pool(rng, 12, cfg.hkv, cfg.page, cfg.head_dim)
+    bt = rng.permutation(12).astype(np.int64)
+    token = rng.permutation(40)[:20].astype(np.int64)
+    load = rng.random(20) < 0.7
+    q = rng.integers(-3, 4, 4).astype(F32)
+    for kv in range(cfg.hkv):
+        got = orc.l2_logits(cfg, k_pool, bt, token, load, q, kv, quota=5)
+        keys = k_pool[bt[token // cfg.page], 0, kv, token % cfg.page][:, cfg.fine_dims]
+        exp = _torch_bf16_bits(keys.astype(np.int64) @ q.astype(np.int64))
+        exp = np.where(load, exp, orc.NEG_INF_BITS)
+        np.testing.assert_array_equal(got.astype(np.int64), exp)
+        assert (orc.l2_logits(cfg, k_pool, bt, token, load, q, kv, quota=0)
+                == orc.NEG_INF_BITS).all()
+
+
+def test_l2_selection_brute_force():
+    rng = np.random.default_rng(10)
+    for trial in range(300):
+        cfg = _cfg(sink_tokens=int(rng.integers(0, 6)), k2=64, max_blocks=64)
+        # candidates always lie inside [low, high) (the selector builds them
+        # from [max(sink, lower), min(lo, L, upper)))
+        low = int(rng.integers(0, 100))
+        high = int(rng.integers(low, 220))
+        n = int(rng.integers(0, min(40, high - low) + 1))
+        token = (low + rng.permutation(high - low)[:n]).astype(np.int64)
+        bits = orc.bf16_bits(rng.integers(0, 5, n).astype(F32) - 2).astype(np.int64)
+        bits[rng.random(n) < 0.2] = orc.NEG_INF_BITS
+        bits[rng.random(n) < 0.05] = orc.NAN_BITS
+        quota = int(rng.integers(0, min(50, high - low) + 1))
+        mid, cnt = orc.l2_middle(cfg, bits.astype(np.uint16), token, 0, False, False,
+                                 low, high, quota)
+        valid = [i for i in range(n) if bits[i] not in (orc.NEG_INF_BITS, orc.NAN_BITS)]
+        ranked = sorted(valid, key=lambda i: (-int(orc.ord16u(bits[i])), token[i]))
+        chosen = [int(token[i]) for i in ranked[:quota]]
+        fill = [t for t in range(low, high) if t not in chosen][:max(0, quota - len(chosen))]
+        exp = sorted(t for t in chosen + fill if t >= cfg.sink_tokens)
+        assert mid[:cnt].tolist() == exp, trial
+
+
+# ---------------------------------------------------------------------------
+# protected set, union, attention
+# ---------------------------------------------------------------------------
+
+def test_protected_ids_closed_form_and_short_context_quirk():
+    cfg = _cfg(sink_tokens=4, swa=16, max_blocks=64)
+    for length in range(20, 120):
+        exp = list(range(4)) + list(range(length - 16, length))
+        assert orc.protected_ids(cfg, length).tolist() == exp
+    # below sink + swa the reference's SWA ids L - swa + aux - sink come out
+    # negative and are dropped (selector:1337-1360): only the sink survives
+    assert orc.protected_ids(cfg, 10).tolist() == [0, 1, 2, 3]
+    # L = 19: ids 19 - 16 + aux - 4 for aux in [4, 19) -> 3..17, sink 0..3
+    assert orc.protected_ids(cfg, 19).tolist() == [0, 1, 2, 3] + list(range(3, 18))
+
+
+def test_final_union_brute_force():
+    rng = np.random.default_rng(11)
+    cfg = _cfg(sink_tokens=4, swa=16, max_blocks=64, page=4)
+    for trial in range(50):
+        length = int(rng.integers(20, 250))
+        bt = rng.permutation(64).astype(np.int64)
+        cnt = int(rng.integers(0, 30))
+        middle = np.zeros(64, dtype=np.int64)
+        middle[:cnt] = np.sort(rng.choice(np.arange(4, length), cnt, replace=False))
+        slots, vis = orc.final_union(cfg, middle, cnt, length, bt, max_vis=40)
+        ids = sorted(set(middle[:cnt].tolist()) | set(orc.protected_ids(cfg, length).tolist()))
+        ids = [i for i in ids if i < cfg.s_cap]
+        assert vis == len(ids)
+        exp = [int(bt[i // 4]) * 4 + i % 4 for i in ids[:40]]
+        assert slots.tolist() == exp
+
+
+def test_sparse_attention_matches_torch_softmax():
+    rng = np.random.default_rng(12)
+    hkv, hq, d, page = 2, 8, 16, 4
+    k_pool = rng.standard_normal((10, 1, hkv, page, d)).astype(F32)
+    v_pool = rng.standard_normal((10, 1, hkv, page, d)).astype(F32)
+    q = rng.standard_normal((3, hq, d)).astype(F32)
+    gather = rng.integers(0, 40, (2, hkv, 12)).astype(np.int64)
+    vis = np.array([[12, 5], [0, 7]])
+    q2r = np.array([1, -1, 0])
+    out = orc.sparse_attention(k_pool, v_pool, q, gather, vis, q2r, 0.25, page)
+    kp = torch.from_numpy(k_pool).double()
+    vp = torch.from_numpy(v_pool).double()
+    for t, r in enumerate(q2r):
+        for h in range(hq):
+            kv = h // (hq // hkv)
+            if r < 0 or vis[r, kv] == 0:
+                assert (out[t, h] == 0).all()
+                continue
+            sl = torch.from_numpy(gather[r, kv, :vis[r, kv]])
+            kk = kp[sl // page, 0, kv, sl % page]
+            vv = vp[sl // page, 0, kv, sl % page]
+            w = torch.softmax(kk @ torch.from_numpy(q[t, h]).double() * 0.25, 0)
+            np.testing.assert_allclose(out[t, h], (w @ vv).numpy(), rtol=1e-9, atol=1e-12)
