@@ -25,6 +25,7 @@ import ctypes
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -160,6 +161,22 @@ def algorithmic_bytes(w, length, bs=16, window=128, near_len=4096, sink=4,
     att = hkv * k2 * (d + d) * 2 + hkv * k2 * 4 + 2 * hq * d * 2
     return dict(select=sel, attention=att, l1=l1, l2=l2, p_far=p_far,
                 p_near=p_near, t_c=t_c)
+
+
+def measured_traffic(args):
+    """HBM bytes per selector launch at this workload, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None when absent or when the
+    workload differs from the profiled one)."""
+    if args.ctx != 131072:
+        return None
+    path = os.path.join(ROOT, 'profiles', 'nfa_select_layer_128k_hbm_traffic.md')
+    try:
+        with open(path) as f:
+            text = f.read()
+    except OSError:
+        return None
+    m = re.search(r'traffic_bytes_per_launch: (\d+)', text)
+    return int(m.group(1)) if m else None
 
 
 def _oracle_cfg(w):
@@ -463,7 +480,7 @@ def main():
             'peak': HBM_PEAK_GBS,
             'unit': 'GB/s',
             'frac': round(sel_gbs / HBM_PEAK_GBS, 4),
-            'traffic': None,
+            'traffic': measured_traffic(args),
         },
         'cpu_baseline': cpu,
     }

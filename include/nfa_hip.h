@@ -111,7 +111,9 @@ typedef struct NfaSelectParams {
   int32_t *gather;                    /* [rows >= batch, hkv, max_vis] */
   int32_t *vis_lens;                  /* [rows >= batch, hkv] */
 
-  /* scratch: nfa_select_workspace_bytes() bytes, zero-filled once */
+  /* scratch: nfa_select_workspace_bytes() bytes, zero-filled once; the
+     kernels leave their counters and histograms at zero, so calls need no
+     clearing in between.  Calls that share a workspace must not overlap. */
   void *workspace;
   int64_t workspace_bytes;
 
@@ -134,7 +136,8 @@ typedef struct NfaAttnParams {
   int32_t abi_version;
   int32_t struct_size;
   int32_t total_q;            /* T query rows */
-  int32_t hq, hkv, head_dim, head_dim_v, page;
+  int32_t hq, hkv, head_dim, head_dim_v, page;  /* head_dim_v == head_dim,
+                                 spanning 8, 16 or 32 chunks of 16 bytes */
   int32_t gather_rows;        /* rows of gather / vis_lens */
   int32_t max_vis;
   int32_t kv_dtype, q_dtype;  /* output dtype == q dtype */
@@ -149,6 +152,8 @@ typedef struct NfaAttnParams {
   const int32_t *vis_lens;    /* [gather_rows, hkv] */
   const int32_t *query_to_req;/* [T] */
   void *out;                  /* [T, hq, head_dim_v] */
+  /* scratch: nfa_attn_workspace_bytes() bytes, zero-filled once; the kernel
+     leaves its counters at zero, so calls need no clearing in between */
   void *workspace;
   int64_t workspace_bytes;
 } NfaAttnParams;
