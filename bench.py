@@ -295,7 +295,11 @@ def selector_timeline(torch, w, steps, plan):
                  ('A tail end', 4, 6),
                  ('A end -> B start', 6, 8), ('B chunk0 L2 logits', 8, 9),
                  ('B last arrival', 9, 10), ('B tail staging', 10, 11),
-                 ('B L2 top-k', 11, 12), ('B union', 12, 13)]
+                 ('B L2 top-k', 11, 12), ('B union', 12, 13),
+                 ('  B top-k: coarse hist', 16, 17), ('  B top-k: coarse bin', 17, 18),
+                 ('  B top-k: fine pass+bin', 18, 19), ('  B top-k: count+scan', 19, 20),
+                 ('  B top-k: emit', 20, 21), ('  B top-k: hole fill', 21, 22),
+                 ('  B top-k: merge', 22, 23)]
         for name, a, b in spans:
             d = (tail[:, b] - tail[:, a]) * us
             acc.setdefault(f'{name} (max)', []).append(d.max())

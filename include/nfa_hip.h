@@ -126,7 +126,7 @@ typedef struct NfaSelectParams {
   uint16_t *dbg_cand_logit;           /* their bf16 logit bits */
   int32_t *dbg_cand_count;            /* [batch, hkv] */
   int64_t dbg_cand_cap;
-  int64_t *dbg_clock;                 /* [batch*hkv, ntiles + 1, 16] phase
+  int64_t *dbg_clock;                 /* [batch*hkv, ntiles + 1, 32] phase
                                          timestamps (wall clock), or NULL;
                                          ntiles = ceil(max_blocks /
                                          NFA_SELECT_TILE_PAGES) */

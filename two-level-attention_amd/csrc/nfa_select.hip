@@ -811,8 +811,8 @@ __global__ void __launch_bounds__(SB)
   const int hp = tid % TPP;       // query heads hp, hp + TPP, ... of page t
   const int t = t0 + tid / TPP;
 
-  const int64_t clk_tile = ((int64_t)row * (ntiles + 1) + tile) * 16;
-  const int64_t clk_tail = ((int64_t)row * (ntiles + 1) + ntiles) * 16;
+  const int64_t clk_tile = ((int64_t)row * (ntiles + 1) + tile) * 32;
+  const int64_t clk_tail = ((int64_t)row * (ntiles + 1) + ntiles) * 32;
   NFA_MARK(clk_tile, 0);
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
@@ -1339,9 +1339,13 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
                                                 int rlo, int rhi, int quota,
                                                 int sink, const RegionLists &rl,
                                                 int *mid_count, int *hist,
-                                                int *tmp) {
+                                                int *tmp, int64_t *clk) {
   if (quota <= 0) return;
   const int tid = threadIdx.x;
+  // optional phase timestamps, taken right after barriers the code has anyway
+  auto mark = [&](int k) {
+    if (clk != nullptr && tid == 0) clk[k] = wall_clock64();
+  };
   const int n = dv.n;
   auto key = [&](int i) -> uint32_t {
     uint32_t v = dv.keys[i];
@@ -1353,13 +1357,16 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
   };
   if (tid < 512) hist[tid] = 0;
   __syncthreads();
+  mark(0);
   for (int i = tid; i < n; i += SB) {
     const uint32_t v = key(i);
     if (v) atomicAdd(&hist[v >> 8], 1);
   }
   __syncthreads();
+  mark(1);
   if (wave_id() == 0) wave_threshold_bin(hist, quota, tmp + 8);
   __syncthreads();
+  mark(2);
   const int hb = tmp[8];
   const int above = tmp[9];
   const int total = tmp[10];
@@ -1376,6 +1383,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     T = ((uint32_t)hb << 8) | (uint32_t)tmp[12];
     need = quota - above - tmp[13];
   }
+  mark(3);
   const int nch = total < quota ? total : quota;
   // ordered emission, one contiguous run of slots per thread
   const int per = (n + SB - 1) / SB;
@@ -1389,6 +1397,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
   }
   int tot2[2];
   block_scan_n<2, SW>(c, tmp + 32, tot2);
+  mark(4);
   {
     int eq = c[1];
     int pos = c[0] + (c[1] < need ? c[1] : need);
@@ -1408,6 +1417,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     }
   }
   __syncthreads();
+  mark(5);
   // hole fill: the (quota - nch) smallest ids of [rlo, rhi) not chosen
   const int nfill_req = quota - nch;
   for (int i = tid; i < nfill_req; i += SB) {
@@ -1424,6 +1434,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     rl.l1x[i] = id < rhi ? dv.slot_of_token(id) : 0;
   }
   __syncthreads();
+  mark(6);
   // fill ids increase with i, so the valid ones form a prefix
   int nfill = 0;
   {
@@ -1457,6 +1468,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     }
   }
   __syncthreads();
+  mark(7);
   if (tid == 0) *mid_count = base_out + nch + nfill - drop;
   __syncthreads();
 }
@@ -1483,7 +1495,7 @@ __global__ void __launch_bounds__(SB)
   const int bs = p.bs;
   const int mb = p.max_blocks;
   const int ntiles = sd.ntiles;
-  const int64_t clk_b = ((int64_t)row * (ntiles + 1) + ntiles) * 16 + 8;
+  const int64_t clk_b = ((int64_t)row * (ntiles + 1) + ntiles) * 32 + 8;
   if (chunk == 0) NFA_MARK(clk_b, 0);
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *bcnt = (unsigned int *)(ws + sd.w_bcnt);
@@ -1690,9 +1702,10 @@ __global__ void __launch_bounds__(SB)
       r_hi[1] = imax(near_low, near_high);
       r_q[1] = near_quota;
     }
+    int64_t *rclk = p.dbg_clock != nullptr ? p.dbg_clock + clk_b + 8 : nullptr;
     for (int r = 0; r < nreg; ++r)
       l2_region_dense(dv, masked, r_lo[r], r_hi[r], r_q[r], p.sink_tokens, rl,
-                      &s_misc[2], s_hist, s_tmp);
+                      &s_misc[2], s_hist, s_tmp, rclk);
   }
   __syncthreads();
   NFA_MARK(clk_b, 4);
@@ -1712,6 +1725,23 @@ __global__ void __launch_bounds__(SB)
     const int n = imin(mcount, p.max_vis);
     for (int k = tid; k < n; k += SB) grow[k] = s_mslot[k];
     if (tid == 0) p.vis_lens[b * p.hkv + kv] = n;
+    NFA_MARK(clk_b, 5);
+    return;
+  }
+  const int n0 = u1 - u0;  // protected ids of the first interval
+  if (u0 == 0 && (mcount == 0 || (s_mid[0] >= u1 && s_mid[mcount - 1] < u2))) {
+    // the usual case: the middle lies between the sink and the SWA ids, so
+    // the union is [0, u1) ++ middle ++ [u2, u3) with no duplicates
+    for (int k = tid; k < mcount; k += SB)
+      if (n0 + k < p.max_vis) grow[n0 + k] = s_mslot[k];
+    for (int k = tid; k < nu; k += SB) {
+      const int x = k < n0 ? u0 + k : u2 + (k - n0);
+      const int dest = k < n0 ? k : k + mcount;
+      const int slot = k == tid ? pre_slot
+                                : btr[imin(x / p.page, mb - 1)] * p.page + x % p.page;
+      if (dest < p.max_vis) grow[dest] = slot;
+    }
+    if (tid == 0) p.vis_lens[b * p.hkv + kv] = mcount + nu;
     NFA_MARK(clk_b, 5);
     return;
   }

@@ -274,7 +274,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
     if _debug is not None and _debug.get('clock_only'):
         # phase timeline only: the production path plus wall-clock marks
         ntiles = -(-cache.max_blocks // nat.SELECT_TILE_PAGES)
-        _debug['clock'] = torch.zeros((b * hkv, ntiles + 1, 16),
+        _debug['clock'] = torch.zeros((b * hkv, ntiles + 1, 32),
                                       dtype=torch.int64, device=device)
         p.dbg_clock = _debug['clock'].data_ptr()
     elif _debug is not None:
@@ -298,7 +298,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
         _debug['region_mode'] = region_mode
         if _debug.get('want_clock'):
             ntiles = -(-cache.max_blocks // nat.SELECT_TILE_PAGES)
-            _debug['clock'] = torch.zeros((b * hkv, ntiles + 1, 16),
+            _debug['clock'] = torch.zeros((b * hkv, ntiles + 1, 32),
                                           dtype=torch.int64, device=device)
             p.dbg_clock = _debug['clock'].data_ptr()
     rc = lib.nfa_select_layer(ctypes.byref(p), nat.stream_handle())
