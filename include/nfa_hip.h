@@ -32,8 +32,9 @@ extern "C" {
 
 #define NFA_ABI_VERSION 1
 
-/* pages scored per selector workgroup; sizes the dbg_clock timeline */
-#define NFA_SELECT_TILE_PAGES 256
+/* sizes the dbg_clock timeline: a selector workgroup scores at least this
+   many pages, so a row has at most ceil(max_blocks / 64) tiles */
+#define NFA_SELECT_CLOCK_PAGES 64
 
 /* error codes */
 #define NFA_OK 0
@@ -129,7 +130,8 @@ typedef struct NfaSelectParams {
   int64_t *dbg_clock;                 /* [batch*hkv, ntiles + 1, 32] phase
                                          timestamps (wall clock), or NULL;
                                          ntiles = ceil(max_blocks /
-                                         NFA_SELECT_TILE_PAGES) */
+                                         NFA_SELECT_CLOCK_PAGES): tile rows,
+                                         then the tail row */
 } NfaSelectParams;
 
 typedef struct NfaAttnParams {

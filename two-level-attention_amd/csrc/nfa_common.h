@@ -153,7 +153,10 @@ __device__ __forceinline__ bool arrive_last(unsigned int *counter,
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+// wave index within the workgroup, as a scalar (uniform) value
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
 
 // Exclusive prefix sum of an int over a block of WAVES waves; two barriers.
 template <int WAVES = NFA_WAVES>

@@ -1,7 +1,8 @@
 // NFA two-level selector for one decode layer on gfx950: two launches.
 //
-// Kernel A, grid (ntiles, batch * hkv), 256 threads per workgroup:
-//   tile stage (every workgroup, 256 pages = one page per thread):
+// Kernel A, grid (batch * hkv, ntiles), 1024 threads per workgroup:
+//   tile stage (workgroups whose tile holds pages of the row; 256 pages per
+//   tile, four threads per page, one query head each):
 //     decode K/V write of the current token (owner of the last page), page
 //     min/max/sum statistics (the latest page, or every page of the tile on
 //     a rebuild), L1 far/near page scores.  One 16-bit score key per page
@@ -15,11 +16,12 @@
 //     the sink/SWA bypass pages as an LDS bitmap (sorted and de-duplicated
 //     by construction), compacted into the candidate page list with its
 //     physical pages.
-// Kernel B, grid (ceil(dense slots / 64), batch * hkv), 256 threads:
-//     L2 logits of the candidate tokens in a dense page-major layout, 64
-//     tokens per workgroup and 4 threads per token; the last workgroup of the
-//     row to arrive runs the top-quota selection with the lowest-token
-//     tie-break, hole fill, the sink/SWA union and the physical gather rows.
+// Kernel B, grid (batch * hkv, ceil(dense slots / l2slots)), 1024 threads:
+//     L2 logits of the candidate tokens in a dense page-major layout,
+//     l2slots tokens per workgroup, 1024 / l2slots threads loading each
+//     token's L2 dims; the last workgroup of the row to arrive runs the
+//     top-quota selection with the lowest-token tie-break, hole fill, the
+//     sink/SWA union and the physical gather rows.
 //
 // Every loop a workgroup executes on the steady decode path is rolled or
 // short: the code of a phase is fetched cold by nearly every workgroup, so
@@ -47,14 +49,18 @@ namespace nfa {
 constexpr int SB = 1024;         // threads per selector workgroup
 constexpr int SW = SB / 64;      // waves per selector workgroup
 constexpr int TPP = 4;           // threads per page in the tile stage
-constexpr int TP = NFA_SELECT_TILE_PAGES;  // pages per tile = SB / TPP
-static_assert(TP * TPP == SB, "tile geometry");
+constexpr int TP = SB / TPP;     // pages scored per pass of a workgroup
+constexpr int kSpanMin = NFA_SELECT_CLOCK_PAGES;  // pages per tile, at least
+constexpr int kSpanMax = 320;    // pages per tile, at most (staged in LDS)
+static_assert(kSpanMin == 64 && kSpanMax % 64 == 0, "tile geometry");
 constexpr int kL2SlotsMax = 256; // dense candidate slots per kernel-B workgroup
 constexpr int kStatTokens = 4;   // tokens per staging round of the stats pass
 constexpr int kSegMax = 16384;   // keys staged in LDS at once by the tail
 
 struct SelDims {
-  int ntiles;     // L1 tiles per row (kernel A grid.x)
+  int ntiles;     // L1 tiles per row at most (kernel A grid.y)
+  int tcap;       // tiles per row in one dispatch round (CUs / rows)
+  int clk_tiles;  // tile rows of the debug clock = ceil(max_blocks / 64)
   int seg;        // keys per segment staged in LDS by the tail
   int nseg;       // key segments per row
   int kstride;    // keys per row in the workspace = nseg * seg
@@ -68,7 +74,7 @@ struct SelDims {
   int lds_a, lds_b;
   // kernel A LDS: common part, then the tile and tail parts overlap
   int a_hist, a_tmp, a_misc, a_qf, a_fdims;
-  int a_dims, a_last, a_tphys, a_stage;                 // tile
+  int a_dims, a_last, a_tphys, a_stage, a_hs, a_st;    // tile
   int a_keys, a_pages, a_cbits, a_eqb, a_dbf, a_dbn, a_dsel;  // tail
   // kernel B LDS: common part, then the scoring and tail parts overlap
   int b_hist, b_tmp, b_misc, b_qg, b_fdims;
@@ -82,11 +88,49 @@ struct SelDims {
 
 __host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
 
-__host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p) {
+// bf16 statistics over 32 L1 dims are staged in LDS by asynchronous
+// global-to-LDS loads; other geometries are read from memory while scoring
+__host__ __device__ inline bool stats_staged(const NfaSelectParams &p) {
+  return p.dsub == 32 && p.kv_dtype == NFA_DTYPE_BF16;
+}
+
+struct TileSplit {
+  int span, tiles;  // pages per tile, tiles of the row
+};
+
+// The kt pages of a row in tiles of `span` pages: rounds of `tcap` tiles
+// (one workgroup per CU over all rows of the launch), as few rounds as keep
+// a tile within kSpanMax pages, the pages spread evenly over the tiles.
+__host__ __device__ inline TileSplit tile_split(int kt, int tcap) {
+  TileSplit s;
+  if (kt <= 0) {
+    s.span = kSpanMin;
+    s.tiles = 1;
+    return s;
+  }
+  const int per_round = tcap * kSpanMax;
+  const int k = (kt + per_round - 1) / per_round;
+  const int span = (kt + k * tcap - 1) / (k * tcap);
+  s.span = span < kSpanMin ? kSpanMin : span;
+  s.tiles = (kt + s.span - 1) / s.span;
+  return s;
+}
+
+// `cus`: compute units of the device (the tile split depends on it, the
+// workspace layout does not)
+__host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   SelDims s;
   const int group = p.hq / p.hkv;
-  s.ntiles = (p.max_blocks + TP - 1) / TP;
-  const int kpad = s.ntiles * TP;  // keys written by the tiles
+  const int nrows = p.batch * p.hkv;
+  s.tcap = cus / nrows > 1 ? cus / nrows : 1;
+  s.clk_tiles = (p.max_blocks + kSpanMin - 1) / kSpanMin;
+  {
+    // tile_split(kt).tiles <= k(kt) * tcap and <= ceil(kt / 64) for kt <= max_blocks
+    const int per_round = s.tcap * kSpanMax;
+    const int kmax = (p.max_blocks + per_round - 1) / per_round;
+    s.ntiles = kmax * s.tcap < s.clk_tiles ? kmax * s.tcap : s.clk_tiles;
+  }
+  const int kpad = ((p.max_blocks + TP - 1) / TP) * TP;  // keys per row
   s.seg = kpad < kSegMax ? kpad : kSegMax;
   s.nseg = (kpad + s.seg - 1) / s.seg;
   s.kstride = s.nseg * s.seg;
@@ -112,8 +156,11 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p) {
   const int a_base = o;
   s.a_dims = o;  o += align16(4 * p.dsub);
   s.a_last = o;  o += align16(4 * 3 * p.dsub);
-  s.a_tphys = o; o += align16(4 * SB);
+  s.a_tphys = o; o += align16(4 * kSpanMax);
   s.a_stage = o; o += align16(4 * SB * kStatTokens);
+  s.a_hs = s.a_stage;  // per-head page scores, after the statistics phase
+  s.a_st = o;          // bf16 32-dim statistics of the tile, staged
+  if (stats_staged(p)) o += 2 * (32 / 8) * kSpanMax * 16;
   const int a_tile = o;
   o = a_base;
   s.a_keys = o;  o += align16(2 * s.seg);
@@ -522,11 +569,106 @@ __device__ __forceinline__ void stats_latest_page(
   }
 }
 
+// Asynchronous global-to-LDS loads (gfx950 global_load_lds_dwordx4) of the
+// bf16 statistics of pages [t0, t1), 32 L1 dims:
+// s_st[slot][chunk][kSpanMax] 16-byte chunks, slot 0 the min (minmax pools)
+// or the sum (avg pools), slot 1 the max.  Lane i of a wave writes
+// base + 16 i, so a wave fills 64 consecutive pages of one (slot, chunk) row
+// per instruction; pages outside both pools are not loaded.  Completes at
+// the issuing wave's next vmcnt wait.
+__device__ __forceinline__ void stage_stats_async(const NfaSelectParams &p,
+                                                  const RowGeo &g, int64_t req,
+                                                  int kv, int t0, int t1,
+                                                  unsigned char *s_st) {
+  constexpr int NC = 32 / 8;
+  typedef __attribute__((address_space(3))) void lds_void;
+  const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
+  const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
+  const int nblk = (t1 - t0 + 63) / 64;
+  // units (chunk, 64-page block), both slots per unit
+  for (int u = wave_id(); u < NC * nblk; u += SW) {
+    const int c = u / nblk;
+    const int blk = u % nblk;
+    const int t = t0 + blk * 64 + lane_id();
+    bool fp = false, np = false;
+    if (t < t1) pools(p, g, t, &fp, &np);
+    const bool mm = (fp && far_mm) || (np && near_mm);
+    const bool avg = (fp && !far_mm) || (np && !near_mm);
+    const int64_t base = stat_index<uint16_t>(p, req, kv, c * 8, t, 32);
+    unsigned char *row0 = s_st + (c * kSpanMax + blk * 64) * 16;
+    if (mm || avg) {
+      const uint16_t *src = (const uint16_t *)(mm ? p.stat_min_l : p.stat_sum_l);
+      __builtin_amdgcn_global_load_lds((const void *)(src + base),
+                                       (lds_void *)row0, 16, 0, 0);
+    }
+    if (mm) {
+      const uint16_t *src = (const uint16_t *)p.stat_max_l;
+      __builtin_amdgcn_global_load_lds((const void *)(src + base),
+                                       (lds_void *)(row0 + NC * kSpanMax * 16),
+                                       16, 0, 0);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // L1 scores of one page for one kv group (selector:311-354)
 // ---------------------------------------------------------------------------
 
 constexpr int GMAX = 8;
+static_assert(GMAX * kSpanMax * 4 <= 4 * SB * kStatTokens,
+              "head scores fit the stage");
+
+// Two query heads q0, q1 (q1 null when absent) of one page from the staged
+// statistics st (chunk c at st[c * kSpanMax], the max slot at
+// st[4 * kSpanMax]):
+// bf16(Σ_d kmin_d·min(q_d,0) + Σ_d kmax_d·max(q_d,0)) for minmax pools,
+// bf16(Σ_d bf16(ksum_d / bs)·q_d) for avg pools, every sum sequential in
+// ascending d with separately rounded products.
+__device__ __forceinline__ void l1_heads_staged(const uint4 *st, const float *q0,
+                                                const float *q1, bool need_mm,
+                                                int bs, float *out0, float *out1) {
+  constexpr int NC = 32 / 8;
+  float sn0 = 0.0f, sp0 = 0.0f, sn1 = 0.0f, sp1 = 0.0f;
+  const float bsf = (float)bs;
+  const bool pow2 = (bs & (bs - 1)) == 0;
+  const float inv = 1.0f / bsf;
+  for (int c = 0; c < NC; ++c) {
+    float lo[8], hi[8];
+    unpack_chunk<uint16_t>(st[c * kSpanMax], lo);
+    if (need_mm) {
+      unpack_chunk<uint16_t>(st[(NC + c) * kSpanMax], hi);
+    } else if (pow2) {
+      // x / bs == x * (1 / bs) exactly when bs is a power of two
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lo[e] = bf16r(lo[e] * inv);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lo[e] = bf16r(lo[e] / bsf);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float qa = q0[c * 8 + e];
+      const float qb = q1 != nullptr ? q1[c * 8 + e] : 0.0f;
+      if (need_mm) {
+        const float a0 = lo[e] * (qa < 0.0f ? qa : 0.0f);
+        const float b0 = hi[e] * (qa > 0.0f ? qa : 0.0f);
+        const float a1 = lo[e] * (qb < 0.0f ? qb : 0.0f);
+        const float b1 = hi[e] * (qb > 0.0f ? qb : 0.0f);
+        sn0 = sn0 + a0;
+        sp0 = sp0 + b0;
+        sn1 = sn1 + a1;
+        sp1 = sp1 + b1;
+      } else {
+        const float a0 = lo[e] * qa;
+        const float a1 = lo[e] * qb;
+        sn0 = sn0 + a0;
+        sn1 = sn1 + a1;
+      }
+    }
+  }
+  *out0 = bf16r(need_mm ? sn0 + sp0 : sn0);
+  *out1 = bf16r(need_mm ? sn1 + sp1 : sn1);
+}
 
 // One query head: bf16(Σ_d kmin_d·min(q_d,0) + Σ_d kmax_d·max(q_d,0)) and
 // bf16(Σ_d kavg_d·q_d), every sum sequential in ascending d with separately
@@ -787,7 +929,7 @@ __global__ void __launch_bounds__(SB)
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int CH = Elem<KV>::kChunk;
   constexpr int NC = DSUB / CH;
-  constexpr bool REG = DSUB == 32 && sizeof(KV) == 2;  // stats in registers
+  constexpr bool STG = DSUB == 32 && sizeof(KV) == 2;  // stats staged in LDS
   int *s_hist = (int *)(smem + sd.a_hist);  // far hi | near hi | far lo | near lo
   int *s_tmp = (int *)(smem + sd.a_tmp);
   int *s_misc = (int *)(smem + sd.a_misc);
@@ -799,20 +941,24 @@ __global__ void __launch_bounds__(SB)
   float *s_stage = (float *)(smem + sd.a_stage);
 
   const int tid = threadIdx.x;
-  const int tile = blockIdx.x;
-  const int ntiles = gridDim.x;
-  const int row = blockIdx.y;
+  // tile-major grid: the first dispatch round holds the low tiles of every
+  // row, and a row's tiles share an XCD (workgroups go round-robin over XCDs)
+  const int row = blockIdx.x;
+  const int tile = blockIdx.y;
   const int b = row / p.hkv;
   const int kv = row % p.hkv;
   const int G = p.hq / p.hkv;
   const int bs = p.bs;
   const int mb = p.max_blocks;
-  const int t0 = tile * TP;
-  const int hp = tid % TPP;       // query heads hp, hp + TPP, ... of page t
-  const int t = t0 + tid / TPP;
+  // wave w scores query heads hp = w % TPP and hp + TPP of the pages of the
+  // 64-page groups w / TPP, w / TPP + SW / TPP, ...: query reads are uniform
+  // over the wave
+  const int hp = wave_id() % TPP;
+  const int grp0 = wave_id() / TPP;
+  constexpr int GSTEP = SW / TPP;
 
-  const int64_t clk_tile = ((int64_t)row * (ntiles + 1) + tile) * 32;
-  const int64_t clk_tail = ((int64_t)row * (ntiles + 1) + ntiles) * 32;
+  const int64_t clk_tile = ((int64_t)row * (sd.clk_tiles + 1) + tile) * 32;
+  const int64_t clk_tail = ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32;
   NFA_MARK(clk_tile, 0);
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
@@ -830,9 +976,15 @@ __global__ void __launch_bounds__(SB)
   if (tid < 512) s_hist[tid] = 0;
   // pages past the block-table width are never scored (selector:205-206)
   const int kt_eff = imin(L > 0 ? (L + bs - 1) / bs : 0, mb);
+  // this tile's pages [t0, t1); tiles past the row's pages take no part,
+  // neither scores nor arrival
+  const TileSplit split = tile_split(kt_eff, sd.tcap);
+  if (tile >= split.tiles) return;
+  const int t0 = tile * split.span;
+  const int t1 = imin(t0 + split.span, kt_eff);
+  const int ngrp = (t1 - t0 + 63) / 64;
   const int last_blk = L > 0 ? (L - 1) / bs : -1;
-  const bool owns_last =
-      last_blk >= t0 && last_blk < t0 + TP && last_blk < mb;
+  const bool owns_last = last_blk >= t0 && last_blk < t1;
 
   // ---- second round trip: request state, statistics (speculative) -------
   const int prev = p.stats_len_l[req];
@@ -840,32 +992,10 @@ __global__ void __launch_bounds__(SB)
   const bool skip_near = p.skip_near_l[req] != 0;
   const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
   const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
-  bool fp0 = false, np0 = false;
-  if (t < kt_eff) {
-    const RowGeo g0 = row_geo(p, L, false, false);
-    pools(p, g0, t, &fp0, &np0);
-  }
-  const bool want_mm = (fp0 && far_mm) || (np0 && near_mm);
-  const bool want_sum = (fp0 && !far_mm) || (np0 && !near_mm);
-  uint4 rmn[REG ? NC : 1], rmx[REG ? NC : 1], rsm[REG ? NC : 1];
-  auto load_regs = [&]() {
-    if constexpr (REG) {
-      const KV *smin = (const KV *)p.stat_min_l;
-      const KV *smax = (const KV *)p.stat_max_l;
-      const KV *ssum = (const KV *)p.stat_sum_l;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int64_t base = stat_index<KV>(p, req, kv, c * CH, t, DSUB);
-        rmn[c] = rmx[c] = rsm[c] = make_uint4(0u, 0u, 0u, 0u);
-        if (want_mm) {
-          rmn[c] = *reinterpret_cast<const uint4 *>(smin + base);
-          rmx[c] = *reinterpret_cast<const uint4 *>(smax + base);
-        }
-        if (want_sum) rsm[c] = *reinterpret_cast<const uint4 *>(ssum + base);
-      }
-    }
-  };
-  load_regs();
+  // speculative: the pools without skip flags contain the final ones
+  const RowGeo g0 = row_geo(p, L, false, false);
+  unsigned char *s_st = smem + sd.a_st;
+  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, t1, s_st);
   // the decode token's key row is read from k_new for the statistics when
   // the fused write targets the slot of token L-1
   const KV *new_row = nullptr;
@@ -905,8 +1035,6 @@ __global__ void __launch_bounds__(SB)
     stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims,
                                 s_stage, new_row, s_last);
   } else if (do_stats && !incremental) {
-    const int pg_lo = t0;
-    const int pg_hi = imin(t0 + TP, kt_eff);
     int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
     if (tid == 0) {
       bool vec = true;
@@ -919,19 +1047,19 @@ __global__ void __launch_bounds__(SB)
       s_misc[1] = vec;
     }
     if (page_phys) {
-      for (int i = tid; i < pg_hi - pg_lo; i += SB) {
-        const int lp = imin(((pg_lo + i) * bs) / p.page, mb - 1);
+      for (int i = tid; i < t1 - t0; i += SB) {
+        const int lp = imin(((t0 + i) * bs) / p.page, mb - 1);
         s_tphys[i] = safe_page(p, btr[lp]);
       }
     }
     __syncthreads();
     if (s_misc[1]) {
-      compute_stats_vec<DSUB, KV>(p, req, kv, L, pg_lo, pg_hi, s_coff,
+      compute_stats_vec<DSUB, KV>(p, req, kv, L, t0, t1, s_coff,
                                   page_phys ? s_tphys : nullptr, new_row, L - 1,
                                   nullptr);
     } else {
       __syncthreads();
-      compute_stats<DSUB, KV>(p, req, kv, L, pg_lo, pg_hi, s_stage, s_dims,
+      compute_stats<DSUB, KV>(p, req, kv, L, t0, t1, s_stage, s_dims,
                               page_phys ? s_tphys : nullptr, new_row, L - 1,
                               nullptr);
     }
@@ -939,93 +1067,91 @@ __global__ void __launch_bounds__(SB)
     __threadfence();
     __syncthreads();
     __threadfence();
-    load_regs();
+    if constexpr (STG) {
+      __builtin_amdgcn_s_waitcnt(0);  // the speculative loads have landed
+      // recomputed addresses: nothing of the first issue stays live across
+      // the rebuild
+      int t0r = t0;
+      asm volatile("" : "+s"(t0r));
+      stage_stats_async(p, g0, req, kv, t0r, t1, s_st);
+    }
+  }
+  if constexpr (STG) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's staged statistics
+    __syncthreads();
+    if (do_stats && incremental && owns_last && tid < 2 * NC) {
+      // the latest page's statistics, as stored, replace the staged ones
+      bool fpl = false, npl = false;
+      pools(p, g0, last_blk, &fpl, &npl);
+      const bool mml = (fpl && far_mm) || (npl && near_mm);
+      const int slot = tid / NC, c = tid % NC;
+      const float *src = s_last + (slot == 1 ? DSUB : (mml ? 0 : 2 * DSUB));
+      reinterpret_cast<uint4 *>(s_st)[(slot * NC + c) * kSpanMax + (last_blk - t0)] =
+          pack_chunk<KV>(src + c * CH);
+    }
   }
   __syncthreads();
   NFA_MARK(clk_tile, 3);
 
-  // ---- L1 scores: four threads per page, one query head each ------------
+  // ---- L1 scores: four waves per 64 pages, two query heads per thread -----
   const RowGeo geo = row_geo(p, L, skip_far, skip_near);
-  bool fp = false, np = false;
-  if (do_stats && t < kt_eff) pools(p, geo, t, &fp, &np);
-  const bool need_mm = (fp && far_mm) || (np && near_mm);
-  const bool need_avg = (fp && !far_mm) || (np && !near_mm);
-  float hm[2] = {0.0f, 0.0f}, ha[2] = {0.0f, 0.0f};  // heads hp, hp + 4
-  if (fp || np) {
-    const bool from_lds = incremental && t == last_blk;
-    if constexpr (REG) {
-      if (from_lds) {
-        // the latest page's statistics, as stored, from LDS
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          rmn[c] = pack_chunk<KV>(s_last + c * CH);
-          rmx[c] = pack_chunk<KV>(s_last + DSUB + c * CH);
-          rsm[c] = pack_chunk<KV>(s_last + 2 * DSUB + c * CH);
-        }
+  float *s_hs = (float *)(smem + sd.a_hs);  // [head][page] bf16 head scores
+  const int j0 = hp, j1 = hp + TPP;
+  if (do_stats && j0 < G) {
+    for (int grp = grp0; grp < ngrp; grp += GSTEP) {
+      const int lp = grp * 64 + lane_id();
+      const int t = t0 + lp;
+      bool fp = false, np = false;
+      if (t < t1) pools(p, geo, t, &fp, &np);
+      if (!(fp || np)) continue;
+      const bool need_mm = (fp && far_mm) || (np && near_mm);
+      const bool need_avg = !need_mm;
+      float h0 = 0.0f, h1 = 0.0f;
+      if constexpr (STG) {
+        l1_heads_staged(reinterpret_cast<const uint4 *>(s_st) + lp, s_qf + j0 * DSUB,
+                        j1 < G ? s_qf + j1 * DSUB : nullptr, need_mm, bs, &h0, &h1);
+      } else {
+        const bool from_lds = incremental && t == last_blk;
+        float m0 = 0.0f, a0 = 0.0f, m1 = 0.0f, a1 = 0.0f;
+        l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j0 * DSUB, need_mm, need_avg,
+                              from_lds ? s_last : nullptr, &m0, &a0);
+        if (j1 < G)
+          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j1 * DSUB, need_mm,
+                                need_avg, from_lds ? s_last : nullptr, &m1, &a1);
+        h0 = need_mm ? m0 : a0;
+        h1 = need_mm ? m1 : a1;
       }
-      float kavg[DSUB];
-      if (need_avg) {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) unpack_chunk<KV>(rsm[c], kavg + c * CH);
-        // x / bs == x * (1 / bs) exactly when bs is a power of two
-        const float bsf = (float)bs;
-        if ((bs & (bs - 1)) == 0) {
-          const float inv = 1.0f / bsf;
-#pragma unroll
-          for (int d = 0; d < DSUB; ++d) kavg[d] = bf16r(kavg[d] * inv);
-        } else {
-#pragma unroll
-          for (int d = 0; d < DSUB; ++d) kavg[d] = bf16r(kavg[d] / bsf);
-        }
-      }
-      for (int r = 0; r < 2; ++r) {
-        const int j = hp + TPP * r;
-        if (j < G)
-          l1_head_regs<DSUB, KV>(rmn, rmx, kavg, s_qf + j * DSUB, need_mm,
-                                 need_avg, &hm[r], &ha[r]);
-      }
-    } else {
-      for (int r = 0; r < 2; ++r) {
-        const int j = hp + TPP * r;
-        if (j < G)
-          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j * DSUB, need_mm,
-                                need_avg, from_lds ? s_last : nullptr, &hm[r],
-                                &ha[r]);
-      }
+      s_hs[j0 * kSpanMax + lp] = h0;
+      if (j1 < G) s_hs[j1 * kSpanMax + lp] = h1;
     }
   }
-  // group mean: bf16 per-head scores summed in head order, gathered from the
-  // page's four lanes (every lane takes part in the shuffles)
-  float mm_acc = 0.0f, avg_acc = 0.0f;
-  {
-    const int lane0 = lane_id() & ~(TPP - 1);
-    for (int j = 0; j < G; ++j) {
-      const int src = lane0 + (j % TPP);
-      const float vm = __shfl(j < TPP ? hm[0] : hm[1], src, 64);
-      const float va = __shfl(j < TPP ? ha[0] : ha[1], src, 64);
-      mm_acc = mm_acc + vm;
-      avg_acc = avg_acc + va;
-    }
-  }
-  uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
-  {
-    const uint16_t mm = bf16_bits(mm_acc / (float)G);
-    const uint16_t avg = bf16_bits(avg_acc / (float)G);
-    if (fp) far_bits = far_mm ? mm : avg;
-    if (np) near_bits = near_mm ? mm : avg;
-  }
-  if (p.dbg_far != nullptr && t < kt_eff && hp == 0) {
-    p.dbg_far[(int64_t)row * mb + t] = far_bits;
-    p.dbg_near[(int64_t)row * mb + t] = near_bits;
-  }
+  __syncthreads();
 
-  // ---- publish keys and the high-byte histograms ------------------------
-  {
-    // a page belongs to at most one pool: far pages lie below near_start,
-    // near pages at or above it
-    const uint32_t fk = score_key(far_bits);
-    const uint32_t nk = score_key(near_bits);
-    if (hp == 0) {
+  // ---- group mean, keys and high-byte histograms (the hp == 0 waves) -----
+  if (hp == 0) {
+    for (int grp = grp0; grp < ngrp; grp += GSTEP) {
+      const int lp = grp * 64 + lane_id();
+      const int t = t0 + lp;
+      if (t >= t1) continue;
+      bool fp = false, np = false;
+      if (do_stats) pools(p, geo, t, &fp, &np);
+      uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
+      if (fp || np) {
+        // bf16 head scores summed in head order
+        float acc = 0.0f;
+        for (int j = 0; j < G; ++j) acc = acc + s_hs[j * kSpanMax + lp];
+        const uint16_t mean = bf16_bits(acc / (float)G);
+        if (fp) far_bits = mean;
+        if (np) near_bits = mean;
+      }
+      if (p.dbg_far != nullptr) {
+        p.dbg_far[(int64_t)row * mb + t] = far_bits;
+        p.dbg_near[(int64_t)row * mb + t] = near_bits;
+      }
+      // a page belongs to at most one pool: far pages lie below near_start,
+      // near pages at or above it
+      const uint32_t fk = score_key(far_bits);
+      const uint32_t nk = score_key(near_bits);
       g_keys[t] = (uint16_t)(fk ? fk : nk);
       if (fk) atomicAdd(&s_hist[fk >> 8], 1);
       if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
@@ -1045,13 +1171,13 @@ __global__ void __launch_bounds__(SB)
     // every workgroup of the request has read stats_len once all arrived
     const unsigned int rb = __hip_atomic_fetch_add(
         &req_cnt[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (rb == (unsigned int)(ntiles * p.hkv - 1)) {
+    if (rb == (unsigned int)(split.tiles * p.hkv - 1)) {
       if (do_stats) p.stats_len_l[req] = L;
       __hip_atomic_store(&req_cnt[b], 0u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  if (!arrive_last(&row_cnt[row], (unsigned int)ntiles, &s_misc[0])) return;
+  if (!arrive_last(&row_cnt[row], (unsigned int)split.tiles, &s_misc[0])) return;
 
   // =========================== tail ======================================
   // (its LDS overlaps the tile stage's private part, no longer used)
@@ -1487,15 +1613,15 @@ __global__ void __launch_bounds__(SB)
   int *s_tok = (int *)(smem + sd.b_tok);
 
   const int tid = threadIdx.x;
-  const int chunk = blockIdx.x;
-  const int row = blockIdx.y;
+  const int row = blockIdx.x;  // chunk-major grid, as kernel A
+  const int chunk = blockIdx.y;
   const int b = row / p.hkv;
   const int kv = row % p.hkv;
   const int G = p.hq / p.hkv;
   const int bs = p.bs;
   const int mb = p.max_blocks;
-  const int ntiles = sd.ntiles;
-  const int64_t clk_b = ((int64_t)row * (ntiles + 1) + ntiles) * 32 + 8;
+  const int64_t clk_b =
+      ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32 + 8;
   if (chunk == 0) NFA_MARK(clk_b, 0);
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *bcnt = (unsigned int *)(ws + sd.w_bcnt);
@@ -1510,6 +1636,9 @@ __global__ void __launch_bounds__(SB)
   const int np_u = ((const int *)(ws + sd.w_npu))[row];
   const int nch = ((const int *)(ws + sd.w_l2vec))[0];  // 0: scalar L2 dims
   const int n_dense = np_u * bs;
+  // chunks past the row's dense slots take no part
+  const int nchk = imax(1, (n_dense + sd.l2slots - 1) / sd.l2slots);
+  if (chunk >= nchk) return;
   for (int d = tid; d < p.fine_dsub; d += SB) s_fdims[d] = p.fine_dims[d];
   const int sl = tid / TPS;   // dense slot of this thread within the chunk
   const int part = tid % TPS; // which of the slot's 16-byte chunks it loads
@@ -1625,7 +1754,7 @@ __global__ void __launch_bounds__(SB)
   if (chunk == 0) NFA_MARK(clk_b, 1);
 
   // ---- arrival; the last workgroup of the row selects ---------------------
-  if (!arrive_last(&bcnt[row], gridDim.x, &s_misc[0])) return;
+  if (!arrive_last(&bcnt[row], (unsigned int)nchk, &s_misc[0])) return;
   NFA_MARK(clk_b, 2);
 
   uint16_t *s_dk = (uint16_t *)(smem + sd.b_dk);
@@ -1794,6 +1923,22 @@ __global__ void __launch_bounds__(SB)
 
 using nfa::SelDims;
 
+// compute units of the current device, cached per device
+static int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess ||
+        v <= 0)
+      v = 256;
+    __atomic_store_n(&cached[dev], v, __ATOMIC_RELAXED);
+  }
+  return v;
+}
+
 static int select_check(const NfaSelectParams *p) {
   if (p == nullptr) {
     nfa_set_error("nfa_select_layer: null params");
@@ -1838,10 +1983,14 @@ static int select_check(const NfaSelectParams *p) {
     nfa_set_error("nfa_select_layer: pool_pages must be positive");
     return NFA_EINVAL;
   }
-  const SelDims sd = nfa::sel_dims(*p);
+  const SelDims sd = nfa::sel_dims(*p, device_cus());
   if (sd.lds_a > 64 * 1024 || sd.lds_b > 64 * 1024) {
     nfa_set_error("nfa_select_layer: geometry needs %d / %d bytes of LDS (> 64 KiB)",
                   sd.lds_a, sd.lds_b);
+    return NFA_EINVAL;
+  }
+  if (sd.ntiles > 65535 || sd.nchunk > 65535) {
+    nfa_set_error("nfa_select_layer: max_blocks %d exceeds the grid limit", p->max_blocks);
     return NFA_EINVAL;
   }
   if (p->workspace == nullptr || p->workspace_bytes < sd.w_total) {
@@ -1872,18 +2021,18 @@ static int select_check(const NfaSelectParams *p) {
 
 extern "C" int64_t nfa_select_workspace_bytes(const NfaSelectParams *p) {
   if (p == nullptr || p->batch <= 0 || p->hkv <= 0) return 0;
-  return nfa::sel_dims(*p).w_total;
+  return nfa::sel_dims(*p, 256).w_total;  // independent of the CU count
 }
 
 template <int DSUB, typename KV>
 static hipError_t launch_select(const NfaSelectParams &p, hipStream_t stream) {
-  const SelDims sd = nfa::sel_dims(p);
+  const SelDims sd = nfa::sel_dims(p, device_cus());
   const int rows = p.batch * p.hkv;
-  hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV>), dim3(sd.ntiles, rows),
+  hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV>), dim3(rows, sd.ntiles),
                      dim3(nfa::SB), sd.lds_a, stream, p, sd);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((nfa::nfa_l2_kernel<KV>), dim3(sd.nchunk, rows),
+  hipLaunchKernelGGL((nfa::nfa_l2_kernel<KV>), dim3(rows, sd.nchunk),
                      dim3(nfa::SB), sd.lds_b, stream, p, sd);
   return hipGetLastError();
 }

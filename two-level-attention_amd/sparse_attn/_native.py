@@ -18,7 +18,7 @@ _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG_ROOT, 'lib', _LIB_NAME)
 
 ABI_VERSION = 1
-SELECT_TILE_PAGES = 256  # NFA_SELECT_TILE_PAGES
+SELECT_CLOCK_PAGES = 64  # NFA_SELECT_CLOCK_PAGES
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
 METHOD_MINMAX = 0

@@ -273,7 +273,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
     p.workspace_bytes = scratch.numel()
     if _debug is not None and _debug.get('clock_only'):
         # phase timeline only: the production path plus wall-clock marks
-        ntiles = -(-cache.max_blocks // nat.SELECT_TILE_PAGES)
+        ntiles = -(-cache.max_blocks // nat.SELECT_CLOCK_PAGES)
         _debug['clock'] = torch.zeros((b * hkv, ntiles + 1, 32),
                                       dtype=torch.int64, device=device)
         p.dbg_clock = _debug['clock'].data_ptr()
@@ -297,7 +297,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
         p.dbg_cand_cap = cand_cap
         _debug['region_mode'] = region_mode
         if _debug.get('want_clock'):
-            ntiles = -(-cache.max_blocks // nat.SELECT_TILE_PAGES)
+            ntiles = -(-cache.max_blocks // nat.SELECT_CLOCK_PAGES)
             _debug['clock'] = torch.zeros((b * hkv, ntiles + 1, 32),
                                           dtype=torch.int64, device=device)
             p.dbg_clock = _debug['clock'].data_ptr()
