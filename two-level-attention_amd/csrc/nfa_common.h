@@ -101,6 +101,14 @@ __device__ __forceinline__ void unpack_chunk(const uint4 &raw, float *out) {
   load_chunk<KV>(reinterpret_cast<const KV *>(&raw), out);
 }
 
+// 8 floats from 16-byte aligned memory (LDS or global) as two 16-byte loads.
+__device__ __forceinline__ void load_f8(const float *src, float *out) {
+  const float4 a = reinterpret_cast<const float4 *>(src)[0];
+  const float4 b = reinterpret_cast<const float4 *>(src)[1];
+  out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+  out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+}
+
 // CH floats that are exact KV values back into 16 bytes of KV elements.
 template <typename KV>
 __device__ __forceinline__ uint4 pack_chunk(const float *x) {

@@ -51,8 +51,8 @@ constexpr int SW = SB / 64;      // waves per selector workgroup
 constexpr int TPP = 4;           // threads per page in the tile stage
 constexpr int TP = SB / TPP;     // pages scored per pass of a workgroup
 constexpr int kSpanMin = NFA_SELECT_CLOCK_PAGES;  // pages per tile, at least
-constexpr int kSpanMax = 320;    // pages per tile, at most (staged in LDS)
-static_assert(kSpanMin == 64 && kSpanMax % 64 == 0, "tile geometry");
+constexpr int kSpanMax = 288;    // pages per tile, at most (staged in LDS)
+static_assert(kSpanMin == 64 && kSpanMax >= TP, "tile geometry");
 constexpr int kL2SlotsMax = 256; // dense candidate slots per kernel-B workgroup
 constexpr int kStatTokens = 4;   // tokens per staging round of the stats pass
 constexpr int kSegMax = 16384;   // keys staged in LDS at once by the tail
@@ -73,7 +73,7 @@ struct SelDims {
   int prot;       // protected width = min(s_cap, sink + swa)
   int lds_a, lds_b;
   // kernel A LDS: common part, then the tile and tail parts overlap
-  int a_hist, a_tmp, a_misc, a_qf, a_fdims;
+  int a_hist, a_tmp, a_misc, a_qf, a_qs, a_fdims;
   int a_dims, a_last, a_tphys, a_stage, a_hs, a_st;    // tile
   int a_keys, a_pages, a_cbits, a_eqb, a_dbf, a_dbn, a_dsel;  // tail
   // kernel B LDS: common part, then the scoring and tail parts overlap
@@ -152,6 +152,7 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   s.a_tmp = o;   o += align16(4 * 128);
   s.a_misc = o;  o += align16(4 * 32);
   s.a_qf = o;    o += align16(4 * group * p.dsub);
+  s.a_qs = o;    o += align16(4 * group * 2 * p.dsub);  // min(q,0) | max(q,0)
   s.a_fdims = o; o += align16(4 * p.fine_dsub);
   const int a_base = o;
   s.a_dims = o;  o += align16(4 * p.dsub);
@@ -618,97 +619,75 @@ constexpr int GMAX = 8;
 static_assert(GMAX * kSpanMax * 4 <= 4 * SB * kStatTokens,
               "head scores fit the stage");
 
-// Two query heads q0, q1 (q1 null when absent) of one page from the staged
-// statistics st (chunk c at st[c * kSpanMax], the max slot at
-// st[4 * kSpanMax]):
-// bf16(Σ_d kmin_d·min(q_d,0) + Σ_d kmax_d·max(q_d,0)) for minmax pools,
-// bf16(Σ_d bf16(ksum_d / bs)·q_d) for avg pools, every sum sequential in
+// Two query heads of one page from the staged statistics st (chunk c at
+// st[c * kSpanMax], the max slot at st[4 * kSpanMax]):
+// bf16(Σ_d kmin_d·min(q_d,0) + Σ_d kmax_d·max(q_d,0)) for minmax pools, from
+// the split queries qs = [min(q,0) | max(q,0)], and bf16(Σ_d bf16(ksum_d /
+// bs)·q_d) for avg pools, from the queries qf; every sum sequential in
 // ascending d with separately rounded products.
-__device__ __forceinline__ void l1_heads_staged(const uint4 *st, const float *q0,
-                                                const float *q1, bool need_mm,
+__device__ __forceinline__ void l1_heads_staged(const uint4 *st, const float *qs0,
+                                                const float *qs1, const float *qf0,
+                                                const float *qf1, bool need_mm,
                                                 int bs, float *out0, float *out1) {
   constexpr int NC = 32 / 8;
-  float sn0 = 0.0f, sp0 = 0.0f, sn1 = 0.0f, sp1 = 0.0f;
-  const float bsf = (float)bs;
-  const bool pow2 = (bs & (bs - 1)) == 0;
-  const float inv = 1.0f / bsf;
-  for (int c = 0; c < NC; ++c) {
-    float lo[8], hi[8];
-    unpack_chunk<uint16_t>(st[c * kSpanMax], lo);
-    if (need_mm) {
+  float r0, r1;
+  if (need_mm) {
+    float sn0 = 0.0f, sp0 = 0.0f, sn1 = 0.0f, sp1 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float lo[8], hi[8], ln0[8], hp0[8], ln1[8], hp1[8];
+      unpack_chunk<uint16_t>(st[c * kSpanMax], lo);
       unpack_chunk<uint16_t>(st[(NC + c) * kSpanMax], hi);
-    } else if (pow2) {
-      // x / bs == x * (1 / bs) exactly when bs is a power of two
+      load_f8(qs0 + c * 8, ln0);
+      load_f8(qs0 + 32 + c * 8, hp0);
+      load_f8(qs1 + c * 8, ln1);
+      load_f8(qs1 + 32 + c * 8, hp1);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) lo[e] = bf16r(lo[e] * inv);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lo[e] = bf16r(lo[e] / bsf);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float qa = q0[c * 8 + e];
-      const float qb = q1 != nullptr ? q1[c * 8 + e] : 0.0f;
-      if (need_mm) {
-        const float a0 = lo[e] * (qa < 0.0f ? qa : 0.0f);
-        const float b0 = hi[e] * (qa > 0.0f ? qa : 0.0f);
-        const float a1 = lo[e] * (qb < 0.0f ? qb : 0.0f);
-        const float b1 = hi[e] * (qb > 0.0f ? qb : 0.0f);
+      for (int e = 0; e < 8; ++e) {
+        const float a0 = lo[e] * ln0[e];
+        const float b0 = hi[e] * hp0[e];
+        const float a1 = lo[e] * ln1[e];
+        const float b1 = hi[e] * hp1[e];
         sn0 = sn0 + a0;
         sp0 = sp0 + b0;
         sn1 = sn1 + a1;
         sp1 = sp1 + b1;
+      }
+    }
+    r0 = sn0 + sp0;
+    r1 = sn1 + sp1;
+  } else {
+    const float bsf = (float)bs;
+    const bool pow2 = (bs & (bs - 1)) == 0;
+    const float inv = 1.0f / bsf;
+    float sa0 = 0.0f, sa1 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float k[8], q0[8], q1[8];
+      unpack_chunk<uint16_t>(st[c * kSpanMax], k);
+      // x / bs == x * (1 / bs) exactly when bs is a power of two
+      if (pow2) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) k[e] = bf16r(k[e] * inv);
       } else {
-        const float a0 = lo[e] * qa;
-        const float a1 = lo[e] * qb;
-        sn0 = sn0 + a0;
-        sn1 = sn1 + a1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) k[e] = bf16r(k[e] / bsf);
+      }
+      load_f8(qf0 + c * 8, q0);
+      load_f8(qf1 + c * 8, q1);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a0 = k[e] * q0[e];
+        const float a1 = k[e] * q1[e];
+        sa0 = sa0 + a0;
+        sa1 = sa1 + a1;
       }
     }
+    r0 = sa0;
+    r1 = sa1;
   }
-  *out0 = bf16r(need_mm ? sn0 + sp0 : sn0);
-  *out1 = bf16r(need_mm ? sn1 + sp1 : sn1);
-}
-
-// One query head: bf16(Σ_d kmin_d·min(q_d,0) + Σ_d kmax_d·max(q_d,0)) and
-// bf16(Σ_d kavg_d·q_d), every sum sequential in ascending d with separately
-// rounded products.  rmn / rmx hold the page's min / max statistics as stored
-// (16-byte chunks, unpacked on use), kavg = bf16(sum / bs) as floats.
-template <int DSUB, typename KV>
-__device__ __forceinline__ void l1_head_regs(const uint4 *rmn, const uint4 *rmx,
-                                             const float *kavg, const float *q,
-                                             bool need_mm, bool need_avg,
-                                             float *mm, float *avg) {
-  constexpr int CH = Elem<KV>::kChunk;
-  if (need_mm) {
-    float sn = 0.0f, sp = 0.0f;
-#pragma unroll
-    for (int c = 0; c < DSUB / CH; ++c) {
-      float lo[CH], hi[CH];
-      unpack_chunk<KV>(rmn[c], lo);
-      unpack_chunk<KV>(rmx[c], hi);
-#pragma unroll
-      for (int e = 0; e < CH; ++e) {
-        const float qd = q[c * CH + e];
-        const float ql = qd < 0.0f ? qd : 0.0f;
-        const float qh = qd > 0.0f ? qd : 0.0f;
-        const float a = lo[e] * ql;
-        const float b = hi[e] * qh;
-        sn = sn + a;
-        sp = sp + b;
-      }
-    }
-    *mm = bf16r(sn + sp);
-  }
-  if (need_avg) {
-    float sa = 0.0f;
-#pragma unroll
-    for (int d = 0; d < DSUB; ++d) {
-      const float a = kavg[d] * q[d];
-      sa = sa + a;
-    }
-    *avg = bf16r(sa);
-  }
+  *out0 = bf16r(r0);
+  *out1 = bf16r(r1);
 }
 
 // Same arithmetic with the statistics read chunk by chunk from memory (L1
@@ -934,6 +913,7 @@ __global__ void __launch_bounds__(SB)
   int *s_tmp = (int *)(smem + sd.a_tmp);
   int *s_misc = (int *)(smem + sd.a_misc);
   float *s_qf = (float *)(smem + sd.a_qf);
+  float *s_qs = (float *)(smem + sd.a_qs);
   int *s_fdims = (int *)(smem + sd.a_fdims);
   int *s_dims = (int *)(smem + sd.a_dims);
   float *s_last = (float *)(smem + sd.a_last);
@@ -1023,7 +1003,10 @@ __global__ void __launch_bounds__(SB)
     const int d = i % DSUB;
     const float qv = load_any(p.q, qrow + (int64_t)j * p.q_stride_h + s_dims[d],
                               p.q_dtype);
-    s_qf[i] = bf16r(qv * p.scale);
+    const float qr = bf16r(qv * p.scale);
+    s_qf[i] = qr;
+    s_qs[j * 2 * DSUB + d] = qr < 0.0f ? qr : 0.0f;
+    s_qs[j * 2 * DSUB + DSUB + d] = qr > 0.0f ? qr : 0.0f;
   }
   NFA_MARK(clk_tile, 2);
 
@@ -1108,8 +1091,11 @@ __global__ void __launch_bounds__(SB)
       const bool need_avg = !need_mm;
       float h0 = 0.0f, h1 = 0.0f;
       if constexpr (STG) {
-        l1_heads_staged(reinterpret_cast<const uint4 *>(s_st) + lp, s_qf + j0 * DSUB,
-                        j1 < G ? s_qf + j1 * DSUB : nullptr, need_mm, bs, &h0, &h1);
+        // a missing second head scores the first one again, discarded
+        const int j1s = j1 < G ? j1 : j0;
+        l1_heads_staged(reinterpret_cast<const uint4 *>(s_st) + lp,
+                        s_qs + j0 * 2 * DSUB, s_qs + j1s * 2 * DSUB,
+                        s_qf + j0 * DSUB, s_qf + j1s * DSUB, need_mm, bs, &h0, &h1);
       } else {
         const bool from_lds = incremental && t == last_blk;
         float m0 = 0.0f, a0 = 0.0f, m1 = 0.0f, a1 = 0.0f;
