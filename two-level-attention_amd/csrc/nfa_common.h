@@ -101,6 +101,77 @@ __device__ __forceinline__ void unpack_chunk(const uint4 &raw, float *out) {
   load_chunk<KV>(reinterpret_cast<const KV *>(&raw), out);
 }
 
+// Touches the first 12 64-byte lines of the kernel arguments with
+// independent scalar loads and one wait: the compiler reads the arguments
+// where it needs them, one dependent scalar-cache miss per line, which at
+// kernel start costs several memory latencies in a row.  The loads and the
+// wait are one asm statement, so no load is in flight when it ends.  BYTES,
+// the explicit argument size, must end inside the 12th line.
+template <int BYTES>
+__device__ __forceinline__ void warm_kernargs() {
+  static_assert(BYTES >= 11 * 64 + 4 && BYTES <= 12 * 64,
+                "the arguments end in the 12th line");
+  auto k = __builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10, d11;
+  asm volatile(
+      "s_load_dword %0, %12, 0x0\n"
+      "s_load_dword %1, %12, 0x40\n"
+      "s_load_dword %2, %12, 0x80\n"
+      "s_load_dword %3, %12, 0xc0\n"
+      "s_load_dword %4, %12, 0x100\n"
+      "s_load_dword %5, %12, 0x140\n"
+      "s_load_dword %6, %12, 0x180\n"
+      "s_load_dword %7, %12, 0x1c0\n"
+      "s_load_dword %8, %12, 0x200\n"
+      "s_load_dword %9, %12, 0x240\n"
+      "s_load_dword %10, %12, 0x280\n"
+      "s_load_dword %11, %12, 0x2c0\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5),
+        "=&s"(d6), "=&s"(d7), "=&s"(d8), "=&s"(d9), "=&s"(d10), "=&s"(d11)
+      : "s"(k));
+}
+
+// Wave-uniform values read through the scalar cache, all loads issued
+// together and awaited once inside the asm statement (nothing is in flight
+// when it ends; vector loads issued before it stay in flight).  The data was
+// written before the kernel started or is not written by it.
+__device__ __forceinline__ void sload_i32x4(const int32_t *pa, const int32_t *pb,
+                                            const int32_t *pc, const int32_t *pd,
+                                            int32_t &a, int32_t &b, int32_t &c,
+                                            int32_t &d) {
+  asm volatile(
+      "s_load_dword %0, %4, 0x0\n"
+      "s_load_dword %1, %5, 0x0\n"
+      "s_load_dword %2, %6, 0x0\n"
+      "s_load_dword %3, %7, 0x0\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(a), "=&s"(b), "=&s"(c), "=&s"(d)
+      : "s"(pa), "s"(pb), "s"(pc), "s"(pd));
+}
+
+__device__ __forceinline__ void sload_row(const int32_t *pl, const int64_t *pa,
+                                          const int64_t *pr, const int32_t *ps,
+                                          int32_t &l, int64_t &a, int64_t &r,
+                                          int32_t &s) {
+  asm volatile(
+      "s_load_dword %0, %4, 0x0\n"
+      "s_load_dwordx2 %1, %5, 0x0\n"
+      "s_load_dwordx2 %2, %6, 0x0\n"
+      "s_load_dword %3, %7, 0x0\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(l), "=&s"(a), "=&s"(r), "=&s"(s)
+      : "s"(pl), "s"(pa), "s"(pr), "s"(ps));
+}
+
+// Workgroup barrier that orders the LDS instructions (ds_*) only: global
+// loads and stores and asynchronous global-to-LDS loads in flight stay in
+// flight (__syncthreads, and an LDS fence, wait for all of them).  The
+// memory clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // 8 floats from 16-byte aligned memory (LDS or global) as two 16-byte loads.
 __device__ __forceinline__ void load_f8(const float *src, float *out) {
   const float4 a = reinterpret_cast<const float4 *>(src)[0];

@@ -56,6 +56,7 @@ static_assert(kSpanMin == 64 && kSpanMax >= TP, "tile geometry");
 constexpr int kL2SlotsMax = 256; // dense candidate slots per kernel-B workgroup
 constexpr int kStatTokens = 4;   // tokens per staging round of the stats pass
 constexpr int kSegMax = 16384;   // keys staged in LDS at once by the tail
+constexpr int kQRawPerThread = 4;  // G * head_dim <= 4 * SB query elements
 
 struct SelDims {
   int ntiles;     // L1 tiles per row at most (kernel A grid.y)
@@ -892,12 +893,13 @@ __global__ void __launch_bounds__(SB)
 // kernel A: L1 tiles and candidate pages
 // ---------------------------------------------------------------------------
 
-// Phase timestamp (debug timeline): completes the phase for the whole
-// workgroup, then thread 0 stores the wall clock.  Uniform condition.
+// Phase timestamp (debug timeline): every wave of the workgroup has reached
+// it (memory accesses in flight stay in flight), then thread 0 stores the
+// wall clock.  Uniform condition.
 #define NFA_MARK(slot_base, k)                                        \
   do {                                                                \
     if (p.dbg_clock != nullptr) {                                     \
-      __syncthreads();                                                \
+      lds_barrier();                                                  \
       if (threadIdx.x == 0) p.dbg_clock[(slot_base) + (k)] = wall_clock64(); \
     }                                                                 \
   } while (0)
@@ -905,6 +907,7 @@ __global__ void __launch_bounds__(SB)
 template <int DSUB, typename KV>
 __global__ void __launch_bounds__(SB)
     nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
+  warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int CH = Elem<KV>::kChunk;
   constexpr int NC = DSUB / CH;
@@ -946,14 +949,34 @@ __global__ void __launch_bounds__(SB)
   int *g_hist = (int *)(ws + sd.w_hist) + (int64_t)row * 512;
   uint16_t *g_keys = (uint16_t *)(ws + sd.w_keys) + (int64_t)row * sd.kstride;
 
-  // ---- first round trip: row scalars, dims -------------------------------
-  const int L = p.lengths[b];
-  const bool active = p.active_req[b] >= 0;
-  const int64_t req = p.valid_req[b];
+  // ---- first round trip: every load that depends on no other ------------
+  // vector loads first (unconditional, clamped indices), then the row state
+  // through the scalar cache
+  const int dim_v = p.dims[imin(tid, DSUB - 1)];
+  const int fdim_v = p.fine_dims[imin(tid, p.fine_dsub - 1)];
+  // the kv group's query rows, whole (the L1 dims are gathered from LDS):
+  // the aligned 32-bit word holding each element, one load for either dtype
+  // (bf16 rows start at even elements, so the word stays inside the row)
+  const int hd = p.head_dim;
+  const int nq = G * hd;
+  const int qsh = p.q_dtype == NFA_DTYPE_BF16 ? 1 : 2;  // log2 element bytes
+  const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kv * G * p.q_stride_h;
+  uint32_t qbits[kQRawPerThread];
+  int qodd[kQRawPerThread];
+#pragma unroll
+  for (int k = 0; k < kQRawPerThread; ++k) {
+    const int i = imin(tid + k * SB, nq - 1);
+    const int64_t byte = (qrow + (int64_t)(i / hd) * p.q_stride_h + i % hd) << qsh;
+    qodd[k] = (int)(byte & 2);
+    qbits[k] = *(const uint32_t *)((const unsigned char *)p.q + (byte & ~(int64_t)3));
+  }
+  int32_t L, slot_b;
+  int64_t act64, req;
+  sload_row(p.lengths + b, p.active_req + b, p.valid_req + b,
+            p.k_new != nullptr ? p.slots + b : p.lengths + b, L, act64, req, slot_b);
+  const bool active = act64 >= 0;
+  if (p.k_new == nullptr) slot_b = -1;
   const int32_t *btr = p.block_table_l + req * mb;
-  if (tid < DSUB) s_dims[tid] = p.dims[tid];
-  for (int d = tid; d < p.fine_dsub; d += SB) s_fdims[d] = p.fine_dims[d];
-  if (tid < 512) s_hist[tid] = 0;
   // pages past the block-table width are never scored (selector:205-206)
   const int kt_eff = imin(L > 0 ? (L + bs - 1) / bs : 0, mb);
   // this tile's pages [t0, t1); tiles past the row's pages take no part,
@@ -965,50 +988,62 @@ __global__ void __launch_bounds__(SB)
   const int ngrp = (t1 - t0 + 63) / 64;
   const int last_blk = L > 0 ? (L - 1) / bs : -1;
   const bool owns_last = last_blk >= t0 && last_blk < t1;
+  // LDS: dims, fine dims, raw query rows, histogram
+  float *s_qraw = s_stage;  // until the statistics phase
+  if (tid < DSUB) s_dims[tid] = dim_v;
+  if (tid < p.fine_dsub) s_fdims[tid] = fdim_v;
+#pragma unroll
+  for (int k = 0; k < kQRawPerThread; ++k) {
+    if (tid + k * SB < nq) {
+      const uint32_t w = qbits[k];
+      s_qraw[tid + k * SB] = qsh == 1 ? __uint_as_float(qodd[k] ? (w & 0xFFFF0000u) : (w << 16))
+                                      : __uint_as_float(w);
+    }
+  }
+  if (tid < 512) s_hist[tid] = 0;
+  lds_barrier();
+  NFA_MARK(clk_tile, 1);
 
-  // ---- second round trip: request state, statistics (speculative) -------
-  const int prev = p.stats_len_l[req];
-  const bool skip_far = p.skip_far_l[req] != 0;
-  const bool skip_near = p.skip_near_l[req] != 0;
+  // scaled, bf16-rounded query rows of this kv group (selector:943-963), and
+  // their negative and positive parts
+  for (int i = tid; i < G * DSUB; i += SB) {
+    const int j = i / DSUB;
+    const int d = i % DSUB;
+    const float qr = bf16r(s_qraw[j * hd + s_dims[d]] * p.scale);
+    s_qf[i] = qr;
+    s_qs[j * 2 * DSUB + d] = qr < 0.0f ? qr : 0.0f;
+    s_qs[j * 2 * DSUB + DSUB + d] = qr > 0.0f ? qr : 0.0f;
+  }
+  lds_barrier();  // the query rows; the raw rows' LDS is free again
+  NFA_MARK(clk_tile, 2);
+
+  // ---- second round trip: statistics (asynchronous), request state -------
+  // (after every LDS read of the prologue: a read behind an asynchronous
+  // global-to-LDS load waits for it)
   const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
   const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
   // speculative: the pools without skip flags contain the final ones
   const RowGeo g0 = row_geo(p, L, false, false);
   unsigned char *s_st = smem + sd.a_st;
   if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, t1, s_st);
+  int32_t prev, skf, skn, ph_last;
+  sload_i32x4(p.stats_len_l + req, p.skip_far_l + req, p.skip_near_l + req,
+              btr + (owns_last ? imin((L - 1) / p.page, mb - 1) : 0), prev, skf,
+              skn, ph_last);
+  const bool skip_far = skf != 0;
+  const bool skip_near = skn != 0;
+  if (!(owns_last && active)) ph_last = 0;
   // the decode token's key row is read from k_new for the statistics when
   // the fused write targets the slot of token L-1
   const KV *new_row = nullptr;
-  int last_phys = 0;
-  if (owns_last && active) {
-    const int ph = btr[imin((L - 1) / p.page, mb - 1)];
-    last_phys = safe_page(p, ph);
-    if (p.k_new != nullptr) {
-      const int slot = p.slots[b];
-      if (slot >= 0 && slot / p.page < p.pool_pages &&
-          slot == ph * p.page + (L - 1) % p.page)
-        new_row = (const KV *)p.k_new + ((int64_t)b * p.hkv + kv) * p.head_dim;
-    }
+  const int last_phys = safe_page(p, ph_last);
+  if (owns_last && active && p.k_new != nullptr) {
+    if (slot_b >= 0 && slot_b / p.page < p.pool_pages &&
+        slot_b == ph_last * p.page + (L - 1) % p.page)
+      new_row = (const KV *)p.k_new + ((int64_t)b * p.hkv + kv) * p.head_dim;
   }
-  __syncthreads();
-  NFA_MARK(clk_tile, 1);
-
   // decode write of the current token (selector:1030-1061), fire and forget
   if (p.k_new != nullptr && active && owns_last) decode_write<KV>(p, b, kv);
-
-  // scaled, bf16-rounded query rows of this kv group (selector:943-963)
-  const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kv * G * p.q_stride_h;
-  for (int i = tid; i < G * DSUB; i += SB) {
-    const int j = i / DSUB;
-    const int d = i % DSUB;
-    const float qv = load_any(p.q, qrow + (int64_t)j * p.q_stride_h + s_dims[d],
-                              p.q_dtype);
-    const float qr = bf16r(qv * p.scale);
-    s_qf[i] = qr;
-    s_qs[j * 2 * DSUB + d] = qr < 0.0f ? qr : 0.0f;
-    s_qs[j * 2 * DSUB + DSUB + d] = qr > 0.0f ? qr : 0.0f;
-  }
-  NFA_MARK(clk_tile, 2);
 
   // ---- page statistics: latest page, or the whole tile on a rebuild -----
   const bool do_stats = active && L > 0 && !(skip_far && skip_near);
@@ -1073,7 +1108,7 @@ __global__ void __launch_bounds__(SB)
           pack_chunk<KV>(src + c * CH);
     }
   }
-  __syncthreads();
+  lds_barrier();
   NFA_MARK(clk_tile, 3);
 
   // ---- L1 scores: four waves per 64 pages, two query heads per thread -----
@@ -1111,7 +1146,7 @@ __global__ void __launch_bounds__(SB)
       if (j1 < G) s_hs[j1 * kSpanMax + lp] = h1;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- group mean, keys and high-byte histograms (the hp == 0 waves) -----
   if (hp == 0) {
@@ -1143,7 +1178,7 @@ __global__ void __launch_bounds__(SB)
       if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (tid < 256) {
     const int hf = s_hist[tid];
     const int hn = s_hist[256 + tid];
@@ -1588,6 +1623,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
 template <typename KV>
 __global__ void __launch_bounds__(SB)
     nfa_l2_kernel(const NfaSelectParams p, const SelDims sd) {
+  warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int CH = Elem<KV>::kChunk;
   const int TPS = SB / sd.l2slots;  // threads per dense slot
@@ -1973,6 +2009,11 @@ static int select_check(const NfaSelectParams *p) {
   if (sd.lds_a > 64 * 1024 || sd.lds_b > 64 * 1024) {
     nfa_set_error("nfa_select_layer: geometry needs %d / %d bytes of LDS (> 64 KiB)",
                   sd.lds_a, sd.lds_b);
+    return NFA_EINVAL;
+  }
+  if ((p->hq / p->hkv) * p->head_dim > nfa::kQRawPerThread * nfa::SB) {
+    nfa_set_error("nfa_select_layer: query group of %d x %d elements is too wide",
+                  p->hq / p->hkv, p->head_dim);
     return NFA_EINVAL;
   }
   if (sd.ntiles > 65535 || sd.nchunk > 65535) {
