@@ -283,23 +283,25 @@ def selector_timeline(torch, w, steps, plan):
         c = clk.cpu().numpy().astype(np.int64)
         tile, tail = c[:, :-1, :], c[:, -1, :]
         start = tile[:, :, 0][tile[:, :, 0] > 0].min()
-        acc.setdefault('kernel span (A+B)', []).append((tail[:, 13].max() - start) * us)
+        acc.setdefault('kernel span', []).append((tail[:, 13].max() - start) * us)
         acc.setdefault('last tile arrives', []).append(
             (tile[:, :, 4].max() - start) * us)
         names = ['row scalars', 'q prep', 'page stats', 'L1 scores+publish']
         for k, name in enumerate(names):
             d = (tile[:, :, k + 1] - tile[:, :, k]) * us
             acc.setdefault(f'A tile {name} (max)', []).append(d.max())
-        spans = [('A tail L1 threshold', 0, 1), ('A tail selection pass', 1, 2),
-                 ('A tail bitmap compaction', 2, 3), ('A tail publish pages', 3, 4),
-                 ('A tail end', 4, 6),
-                 ('A end -> B start', 6, 8), ('B chunk0 L2 logits', 8, 9),
-                 ('B last arrival', 9, 10), ('B tail staging', 10, 11),
-                 ('B L2 top-k', 11, 12), ('B union', 12, 13),
-                 ('  B top-k: coarse hist', 16, 17), ('  B top-k: coarse bin', 17, 18),
-                 ('  B top-k: fine pass+bin', 18, 19), ('  B top-k: count+scan', 19, 20),
-                 ('  B top-k: emit', 20, 21), ('  B top-k: hole fill', 21, 22),
-                 ('  B top-k: merge', 22, 23)]
+        spans = [('tail L1 threshold', 0, 1),
+                 ('  L1 thr: hist+keys load', 0, 24), ('  L1 thr: coarse bins', 24, 25),
+                 ('  L1 thr: refine pass', 25, 26), ('  L1 thr: fine bins', 26, 1),
+                 ('tail selection pass', 1, 2),
+                 ('  sel: main pass', 1, 27), ('  sel: ties', 27, 2),
+                 ('tail bitmap compaction', 2, 3), ('tail candidate pages', 3, 4),
+                 ('tail L1 end', 4, 6), ('tail L2 logits', 6, 9),
+                 ('tail L2 top-k', 9, 12), ('tail union', 12, 13),
+                 ('  L2 top-k: coarse hist', 16, 17), ('  L2 top-k: coarse bin', 17, 18),
+                 ('  L2 top-k: fine pass+bin', 18, 19), ('  L2 top-k: count+scan', 19, 20),
+                 ('  L2 top-k: emit', 20, 21), ('  L2 top-k: hole fill', 21, 22),
+                 ('  L2 top-k: merge', 22, 23)]
         for name, a, b in spans:
             d = (tail[:, b] - tail[:, a]) * us
             acc.setdefault(f'{name} (max)', []).append(d.max())
@@ -479,7 +481,7 @@ def main():
         },
         'roofline': {
             'bound': 'hbm',
-            'kernel': 'nfa_select_layer (nfa_select_kernel + nfa_l2_kernel)',
+            'kernel': 'nfa_select_layer (nfa_select_kernel)',
             'achieved': round(sel_gbs, 1),
             'peak': HBM_PEAK_GBS,
             'unit': 'GB/s',

@@ -107,6 +107,11 @@ typedef struct NfaSelectParams {
      [max_req, hkv, dsub/chunk, max_blocks, chunk] with chunk = 16B/elem */
   void *stat_min_l, *stat_max_l, *stat_sum_l;
   int32_t *stats_len_l;               /* [max_req] */
+  /* optional L2 side copy of this layer, KV dtype: the L2 dims of every
+     visible token in fine_dims order, [max_req, hkv, max_blocks * bs,
+     fine_dsub]; valid with the statistics (written by the same rebuild and
+     incremental update).  NULL: the L2 logits read the K pool. */
+  void *l2_keys_l;
 
   /* outputs */
   int32_t *gather;                    /* [rows >= batch, hkv, max_vis] */

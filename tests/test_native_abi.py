@@ -66,11 +66,10 @@ def test_workspace_size_is_host_computed(lib):
     p.batch, p.hq, p.hkv, p.bs, p.max_blocks = 1, 32, 8, 16, 8216
     p.k_f, p.k_n, p.k2, p.dsub, p.fine_dsub = 96, 32, 1024, 32, 32
     need = lib.nfa_select_workspace_bytes(ctypes.byref(p))
-    # per (row, kv head): a 16-bit key per page, two 256-bin histograms, the
-    # candidate pages with their physical pages and a 16-bit L2 key per
-    # dense candidate slot
-    rows, np_ = 8, 96 + 32 + 2
-    assert need >= rows * (2 * 8216 + 4 * 512 + np_ * (4 + 4 + 2 * 16))
+    # per (row, kv head): a 16-bit key per page and two 256-bin histograms
+    # (candidate pages and L2 keys stay in the tail workgroup's LDS)
+    rows = 8
+    assert need >= rows * (2 * 8216 + 4 * 512)
     a = _native.NfaAttnParams()
     a.abi_version = _native.ABI_VERSION
     a.struct_size = ctypes.sizeof(a)

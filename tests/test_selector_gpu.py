@@ -134,11 +134,13 @@ GEO16 = RegionGeometry(sink=4, near=4096, window=128, page=16, max_new_tokens=64
 
 
 def _prod_cache(lengths, *, hkv=2, hq=8, dtype=torch.bfloat16, max_req=4,
-                skips=None, req_ids=None, seed=20261201, zero_keys=False):
-    page = GEO16.page
-    max_blocks = (max(lengths) + 64 + page - 1) // page + 8
-    phys = sum((n + 64 + page - 1) // page for n in lengths) + 8
-    cache = make_cache(DEV, geometry=GEO16, max_blocks=max_blocks,
+                skips=None, req_ids=None, seed=20261201, zero_keys=False,
+                geometry=GEO16):
+    page = geometry.page
+    extra = geometry.max_new_tokens
+    max_blocks = (max(lengths) + extra + page - 1) // page + 8
+    phys = sum((n + extra + page - 1) // page for n in lengths) + 8
+    cache = make_cache(DEV, geometry=geometry, max_blocks=max_blocks,
                        max_physical_pages=phys, max_visible_len=1024, hkv=hkv,
                        hq=hq, dtype=dtype, max_requests=max_req)
     gen = torch.Generator(device=DEV).manual_seed(seed)
@@ -160,6 +162,40 @@ def test_production_flags_bit_exact(lengths):
     q = bf16_randn((b, cache.num_query_heads, 128), gen, DEV)
     decode = _decode_inputs(cache, b, gen, torch.bfloat16)
     run_and_compare(cache, indexer, req_ids, q, decode, scaling=0.08838834764831845)
+
+
+@pytest.mark.parametrize('side_copy', [True, False])
+def test_l2_from_side_copy_or_k_pool(side_copy):
+    # the L2 logits read the L2 side copy, or the K pool when it is off
+    cache, gen, req_ids = _prod_cache([9000, 20500])
+    cache.nfa_l2_side_copy = side_copy
+    indexer = make_indexer()
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = bf16_randn((2, cache.num_query_heads, 128), gen, DEV)
+    decode = _decode_inputs(cache, 2, gen, torch.bfloat16)
+    run_and_compare(cache, indexer, req_ids, q, decode, scaling=0.08838834764831845)
+
+
+def test_incremental_side_rows_become_candidates():
+    # tokens appended by incremental steps leave the 128-token window and
+    # are scored from the side rows those steps wrote
+    geo = RegionGeometry(sink=4, near=4096, window=128, page=16,
+                         max_new_tokens=256)
+    cache, gen, req_ids = _prod_cache([3000], geometry=geo)
+    indexer = make_indexer()
+    for step in range(150):
+        cache.new_step(req_ids)
+        cache.plan_common(req_ids)
+        q = bf16_randn((1, cache.num_query_heads, 128), gen, DEV)
+        decode = _decode_inputs(cache, 1, gen, torch.bfloat16)
+        if step < 149:
+            select_topk_for_layer_batched(cache, 0, req_ids, q,
+                                          attention=attention_ns(indexer, 1.0),
+                                          decode_write=decode)
+        else:
+            run_and_compare(cache, indexer, req_ids, q, decode)
+        cache.commit_step()
 
 
 def test_incremental_stats_over_decode_steps():

@@ -101,35 +101,40 @@ __device__ __forceinline__ void unpack_chunk(const uint4 &raw, float *out) {
   load_chunk<KV>(reinterpret_cast<const KV *>(&raw), out);
 }
 
-// Touches the first 12 64-byte lines of the kernel arguments with
-// independent scalar loads and one wait: the compiler reads the arguments
-// where it needs them, one dependent scalar-cache miss per line, which at
-// kernel start costs several memory latencies in a row.  The loads and the
-// wait are one asm statement, so no load is in flight when it ends.  BYTES,
-// the explicit argument size, must end inside the 12th line.
+// Touches every 64-byte line of the kernel arguments (BYTES explicit bytes,
+// at most 12 lines) with independent scalar loads and one wait: the compiler
+// reads the arguments where it needs them, one dependent scalar-cache miss
+// per line, which at kernel start costs several memory latencies in a row.
+// The loads and the wait are one asm statement, so no load is in flight when
+// it ends; lines past the last one repeat it.
 template <int BYTES>
 __device__ __forceinline__ void warm_kernargs() {
-  static_assert(BYTES >= 11 * 64 + 4 && BYTES <= 12 * 64,
-                "the arguments end in the 12th line");
+  static_assert(BYTES > 0 && BYTES <= 12 * 64, "at most 12 argument lines");
+  constexpr int last = (BYTES - 1) / 64;
   auto k = __builtin_amdgcn_kernarg_segment_ptr();
   uint32_t d0, d1, d2, d3, d4, d5, d6, d7, d8, d9, d10, d11;
   asm volatile(
-      "s_load_dword %0, %12, 0x0\n"
-      "s_load_dword %1, %12, 0x40\n"
-      "s_load_dword %2, %12, 0x80\n"
-      "s_load_dword %3, %12, 0xc0\n"
-      "s_load_dword %4, %12, 0x100\n"
-      "s_load_dword %5, %12, 0x140\n"
-      "s_load_dword %6, %12, 0x180\n"
-      "s_load_dword %7, %12, 0x1c0\n"
-      "s_load_dword %8, %12, 0x200\n"
-      "s_load_dword %9, %12, 0x240\n"
-      "s_load_dword %10, %12, 0x280\n"
-      "s_load_dword %11, %12, 0x2c0\n"
+      "s_load_dword %0, %12, %13\n"
+      "s_load_dword %1, %12, %14\n"
+      "s_load_dword %2, %12, %15\n"
+      "s_load_dword %3, %12, %16\n"
+      "s_load_dword %4, %12, %17\n"
+      "s_load_dword %5, %12, %18\n"
+      "s_load_dword %6, %12, %19\n"
+      "s_load_dword %7, %12, %20\n"
+      "s_load_dword %8, %12, %21\n"
+      "s_load_dword %9, %12, %22\n"
+      "s_load_dword %10, %12, %23\n"
+      "s_load_dword %11, %12, %24\n"
       "s_waitcnt lgkmcnt(0)"
       : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5),
         "=&s"(d6), "=&s"(d7), "=&s"(d8), "=&s"(d9), "=&s"(d10), "=&s"(d11)
-      : "s"(k));
+      : "s"(k), "i"(0), "i"((1 < last ? 1 : last) * 64),
+        "i"((2 < last ? 2 : last) * 64), "i"((3 < last ? 3 : last) * 64),
+        "i"((4 < last ? 4 : last) * 64), "i"((5 < last ? 5 : last) * 64),
+        "i"((6 < last ? 6 : last) * 64), "i"((7 < last ? 7 : last) * 64),
+        "i"((8 < last ? 8 : last) * 64), "i"((9 < last ? 9 : last) * 64),
+        "i"((10 < last ? 10 : last) * 64), "i"((11 < last ? 11 : last) * 64));
 }
 
 // Wave-uniform values read through the scalar cache, all loads issued

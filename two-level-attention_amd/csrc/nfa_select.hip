@@ -1,27 +1,25 @@
-// NFA two-level selector for one decode layer on gfx950: two launches.
+// NFA two-level selector for one decode layer on gfx950: one launch.
 //
-// Kernel A, grid (batch * hkv, ntiles), 1024 threads per workgroup:
-//   tile stage (workgroups whose tile holds pages of the row; 256 pages per
-//   tile, four threads per page, one query head each):
+// Grid (batch * hkv, ntiles), 1024 threads per workgroup.
+//   tile stage (workgroups whose tile holds pages of the row; a row's pages
+//   spread evenly over one dispatch round of tiles, four threads per page,
+//   one query head each):
 //     decode K/V write of the current token (owner of the last page), page
-//     min/max/sum statistics (the latest page, or every page of the tile on
-//     a rebuild), L1 far/near page scores.  One 16-bit score key per page
-//     (far and near pools are disjoint page ranges) goes to the workspace,
-//     the high bytes of the keys into a per-row, per-pool histogram (one
-//     global atomic per non-empty bin and workgroup).
+//     min/max/sum statistics and the L2 side rows (the latest page and token,
+//     or every page and token of the tile on a rebuild), L1 far/near page
+//     scores.  One 16-bit score key per page (far and near pools are
+//     disjoint page ranges) goes to the workspace, the high bytes of the keys
+//     into a per-row, per-pool histogram (one global atomic per non-empty bin
+//     and workgroup).
 //   tail (the last workgroup of each (row, kv) to arrive, found with a
 //     device-scope atomic counter; no workgroup ever waits on another):
 //     exact top-K_F / top-K_N thresholds from the histogram plus one
 //     refinement pass over the keys staged in LDS, the selected pages and
 //     the sink/SWA bypass pages as an LDS bitmap (sorted and de-duplicated
-//     by construction), compacted into the candidate page list with its
-//     physical pages.
-// Kernel B, grid (batch * hkv, ceil(dense slots / l2slots)), 1024 threads:
-//     L2 logits of the candidate tokens in a dense page-major layout,
-//     l2slots tokens per workgroup, 1024 / l2slots threads loading each
-//     token's L2 dims; the last workgroup of the row to arrive runs the
-//     top-quota selection with the lowest-token tie-break, hole fill, the
-//     sink/SWA union and the physical gather rows.
+//     by construction), compacted into the candidate page list; then the L2
+//     logits of the candidate tokens (dense page-major slots, read from the
+//     L2 side rows), the top-quota selection with the lowest-token tie-break,
+//     hole fill, the sink/SWA union and the physical gather rows.
 //
 // Every loop a workgroup executes on the steady decode path is rolled or
 // short: the code of a phase is fetched cold by nearly every workgroup, so
@@ -53,7 +51,6 @@ constexpr int TP = SB / TPP;     // pages scored per pass of a workgroup
 constexpr int kSpanMin = NFA_SELECT_CLOCK_PAGES;  // pages per tile, at least
 constexpr int kSpanMax = 288;    // pages per tile, at most (staged in LDS)
 static_assert(kSpanMin == 64 && kSpanMax >= TP, "tile geometry");
-constexpr int kL2SlotsMax = 256; // dense candidate slots per kernel-B workgroup
 constexpr int kStatTokens = 4;   // tokens per staging round of the stats pass
 constexpr int kSegMax = 16384;   // keys staged in LDS at once by the tail
 constexpr int kQRawPerThread = 4;  // G * head_dim <= 4 * SB query elements
@@ -68,23 +65,19 @@ struct SelDims {
   int words;      // candidate bitmap words = kstride / 32
   int np;         // candidate page capacity = k_f + k_n + 2
   int dense;      // dense candidate slots = np * bs
-  int dstride;    // dense keys per row in the workspace (multiple of 8)
-  int l2slots;    // dense slots per kernel-B workgroup (SB / l2slots threads each)
-  int nchunk;     // kernel B grid.x
+  int dstride;    // dense keys in LDS (multiple of 8)
   int prot;       // protected width = min(s_cap, sink + swa)
-  int lds_a, lds_b;
-  // kernel A LDS: common part, then the tile and tail parts overlap
-  int a_hist, a_tmp, a_misc, a_qf, a_qs, a_fdims;
+  int lds;        // LDS bytes per workgroup
+  // LDS: a common part, then the tile part, or the tail: its candidate pages,
+  // then its L1 part or (later) its L2 part
+  int a_hist, a_tmp, a_misc, a_qf, a_qs, a_qg, a_fdims;
   int a_dims, a_last, a_tphys, a_stage, a_hs, a_st;    // tile
-  int a_keys, a_pages, a_cbits, a_eqb, a_dbf, a_dbn, a_dsel;  // tail
-  // kernel B LDS: common part, then the scoring and tail parts overlap
-  int b_hist, b_tmp, b_misc, b_qg, b_fdims;
-  int b_tok, b_stage;                                   // scoring
-  int b_dk, b_pages, b_pphys, b_l0, b_l0x, b_l1, b_l1x, b_mid, b_mslot;  // tail
+  int a_pages, a_pphys;                                // tail
+  int a_keys, a_cbits, a_eqb, a_dbf, a_dbn, a_dsel;    // tail, L1
+  int a_dk, a_l0, a_l0x, a_l1, a_l1x, a_mid, a_mslot;  // tail, L2
   // global workspace byte offsets; counters and histograms first (they must
-  // start at zero and are reset by the kernels themselves)
-  int64_t w_rowcnt, w_reqcnt, w_bcnt, w_hist, w_keys, w_pages, w_pphys, w_npu,
-      w_l2vec, w_dk, w_total;
+  // start at zero and are reset by the kernel itself)
+  int64_t w_rowcnt, w_reqcnt, w_hist, w_keys, w_total;
 };
 
 __host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
@@ -139,21 +132,15 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   s.np = p.k_f + p.k_n + 2;
   s.dense = s.np * p.bs;
   s.dstride = (s.dense + 7) & ~7;
-  // staging of a slot's L2 dims is at most 4 * fine_dsub bytes; keep the
-  // chunk's staging within 32 KiB
-  int slots = kL2SlotsMax;
-  while (slots > 16 && slots * 4 * p.fine_dsub > 32 * 1024) slots /= 2;
-  s.l2slots = slots;
-  s.nchunk = (s.dense + slots - 1) / slots;
   const int s_cap = p.max_blocks * p.bs;
   s.prot = p.sink_tokens + p.swa < s_cap ? p.sink_tokens + p.swa : s_cap;
-  // kernel A
   int o = 0;
   s.a_hist = o;  o += align16(4 * 4 * 256);
   s.a_tmp = o;   o += align16(4 * 128);
   s.a_misc = o;  o += align16(4 * 32);
   s.a_qf = o;    o += align16(4 * group * p.dsub);
   s.a_qs = o;    o += align16(4 * group * 2 * p.dsub);  // min(q,0) | max(q,0)
+  s.a_qg = o;    o += align16(4 * p.fine_dsub);          // grouped L2 query
   s.a_fdims = o; o += align16(4 * p.fine_dsub);
   const int a_base = o;
   s.a_dims = o;  o += align16(4 * p.dsub);
@@ -165,49 +152,35 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   if (stats_staged(p)) o += 2 * (32 / 8) * kSpanMax * 16;
   const int a_tile = o;
   o = a_base;
-  s.a_keys = o;  o += align16(2 * s.seg);
   s.a_pages = o; o += align16(4 * s.np);
+  s.a_pphys = o; o += align16(4 * s.np);
+  const int a_l12 = o;
+  s.a_keys = o;  o += align16(2 * s.seg);
   s.a_cbits = o; o += align16(4 * s.words);
   s.a_eqb = o;   o += align16(4 * s.words);
   s.a_dbf = o;   o += align16(4 * s.words);
   s.a_dbn = o;   o += align16(4 * s.words);
   s.a_dsel = o;  o += align16(8 * (p.k_f + p.k_n + 1));
-  s.lds_a = a_tile > o ? a_tile : o;
-  // kernel B
-  o = 0;
-  s.b_hist = o;  o += align16(4 * 2 * 256);
-  s.b_tmp = o;   o += align16(4 * 128);
-  s.b_misc = o;  o += align16(4 * 32);
-  s.b_qg = o;    o += align16(4 * p.fine_dsub);
-  s.b_fdims = o; o += align16(4 * p.fine_dsub);
-  const int b_base = o;
-  s.b_tok = o;   o += align16(4 * s.l2slots);
-  s.b_stage = o; o += align16(4 * s.l2slots * p.fine_dsub);
-  const int b_score = o;
-  o = b_base;
-  s.b_dk = o;    o += align16(2 * s.dstride);
-  s.b_pages = o; o += align16(4 * s.np);
-  s.b_pphys = o; o += align16(4 * s.np);
-  s.b_l0 = o;    o += align16(4 * p.k2);
-  s.b_l0x = o;   o += align16(4 * p.k2);
-  s.b_l1 = o;    o += align16(4 * p.k2);
-  s.b_l1x = o;   o += align16(4 * p.k2);
-  s.b_mid = o;   o += align16(4 * p.k2);
-  s.b_mslot = o; o += align16(4 * p.k2);
-  s.lds_b = b_score > o ? b_score : o;
+  const int a_l1 = o;
+  o = a_l12;
+  s.a_dk = o;    o += align16(2 * s.dstride);
+  s.a_l0 = o;    o += align16(4 * p.k2);
+  s.a_l0x = o;   o += align16(4 * p.k2);
+  s.a_l1 = o;    o += align16(4 * p.k2);
+  s.a_l1x = o;   o += align16(4 * p.k2);
+  s.a_mid = o;   o += align16(4 * p.k2);
+  s.a_mslot = o; o += align16(4 * p.k2);
+  const int a_l2 = o;
+  s.lds = a_tile;
+  if (a_l1 > s.lds) s.lds = a_l1;
+  if (a_l2 > s.lds) s.lds = a_l2;
   // workspace
   const int rows = p.batch * p.hkv;
   int64_t w = 0;
   s.w_rowcnt = w; w += ((int64_t)4 * rows + 255) & ~(int64_t)255;
   s.w_reqcnt = w; w += ((int64_t)4 * p.batch + 255) & ~(int64_t)255;
-  s.w_bcnt = w;   w += ((int64_t)4 * rows + 255) & ~(int64_t)255;
   s.w_hist = w;   w += (int64_t)4 * rows * 512;
   s.w_keys = w;   w += (((int64_t)2 * rows * s.kstride) + 255) & ~(int64_t)255;
-  s.w_pages = w;  w += (((int64_t)4 * rows * s.np) + 255) & ~(int64_t)255;
-  s.w_pphys = w;  w += (((int64_t)4 * rows * s.np) + 255) & ~(int64_t)255;
-  s.w_npu = w;    w += ((int64_t)4 * rows + 255) & ~(int64_t)255;
-  s.w_l2vec = w;  w += ((int64_t)4 * 2 + 255) & ~(int64_t)255;
-  s.w_dk = w;     w += (int64_t)2 * rows * s.dstride;
   s.w_total = w;
   return s;
 }
@@ -325,6 +298,14 @@ __device__ __forceinline__ int safe_page(const NfaSelectParams &p, int phys) {
 __device__ __forceinline__ int64_t kv_offset(const NfaSelectParams &p,
                                              int phys, int kv, int off) {
   return (((int64_t)phys * p.hkv + kv) * p.page + off) * p.head_dim;
+}
+
+// L2 side row of token tok: its L2 dims, fine_dims order, KV dtype
+template <typename KV>
+__device__ __forceinline__ KV *l2_side_row(const NfaSelectParams &p, int64_t req,
+                                           int kv, int tok) {
+  return (KV *)p.l2_keys_l +
+         ((req * p.hkv + kv) * (int64_t)p.max_blocks * p.bs + tok) * p.fine_dsub;
 }
 
 // ---------------------------------------------------------------------------
@@ -890,565 +871,7 @@ __global__ void __launch_bounds__(SB)
 
 
 // ---------------------------------------------------------------------------
-// kernel A: L1 tiles and candidate pages
-// ---------------------------------------------------------------------------
-
-// Phase timestamp (debug timeline): every wave of the workgroup has reached
-// it (memory accesses in flight stay in flight), then thread 0 stores the
-// wall clock.  Uniform condition.
-#define NFA_MARK(slot_base, k)                                        \
-  do {                                                                \
-    if (p.dbg_clock != nullptr) {                                     \
-      lds_barrier();                                                  \
-      if (threadIdx.x == 0) p.dbg_clock[(slot_base) + (k)] = wall_clock64(); \
-    }                                                                 \
-  } while (0)
-
-template <int DSUB, typename KV>
-__global__ void __launch_bounds__(SB)
-    nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
-  warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
-  extern __shared__ __align__(16) unsigned char smem[];
-  constexpr int CH = Elem<KV>::kChunk;
-  constexpr int NC = DSUB / CH;
-  constexpr bool STG = DSUB == 32 && sizeof(KV) == 2;  // stats staged in LDS
-  int *s_hist = (int *)(smem + sd.a_hist);  // far hi | near hi | far lo | near lo
-  int *s_tmp = (int *)(smem + sd.a_tmp);
-  int *s_misc = (int *)(smem + sd.a_misc);
-  float *s_qf = (float *)(smem + sd.a_qf);
-  float *s_qs = (float *)(smem + sd.a_qs);
-  int *s_fdims = (int *)(smem + sd.a_fdims);
-  int *s_dims = (int *)(smem + sd.a_dims);
-  float *s_last = (float *)(smem + sd.a_last);
-  int *s_tphys = (int *)(smem + sd.a_tphys);
-  float *s_stage = (float *)(smem + sd.a_stage);
-
-  const int tid = threadIdx.x;
-  // tile-major grid: the first dispatch round holds the low tiles of every
-  // row, and a row's tiles share an XCD (workgroups go round-robin over XCDs)
-  const int row = blockIdx.x;
-  const int tile = blockIdx.y;
-  const int b = row / p.hkv;
-  const int kv = row % p.hkv;
-  const int G = p.hq / p.hkv;
-  const int bs = p.bs;
-  const int mb = p.max_blocks;
-  // wave w scores query heads hp = w % TPP and hp + TPP of the pages of the
-  // 64-page groups w / TPP, w / TPP + SW / TPP, ...: query reads are uniform
-  // over the wave
-  const int hp = wave_id() % TPP;
-  const int grp0 = wave_id() / TPP;
-  constexpr int GSTEP = SW / TPP;
-
-  const int64_t clk_tile = ((int64_t)row * (sd.clk_tiles + 1) + tile) * 32;
-  const int64_t clk_tail = ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32;
-  NFA_MARK(clk_tile, 0);
-  unsigned char *ws = (unsigned char *)p.workspace;
-  unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
-  unsigned int *req_cnt = (unsigned int *)(ws + sd.w_reqcnt);
-  int *g_hist = (int *)(ws + sd.w_hist) + (int64_t)row * 512;
-  uint16_t *g_keys = (uint16_t *)(ws + sd.w_keys) + (int64_t)row * sd.kstride;
-
-  // ---- first round trip: every load that depends on no other ------------
-  // vector loads first (unconditional, clamped indices), then the row state
-  // through the scalar cache
-  const int dim_v = p.dims[imin(tid, DSUB - 1)];
-  const int fdim_v = p.fine_dims[imin(tid, p.fine_dsub - 1)];
-  // the kv group's query rows, whole (the L1 dims are gathered from LDS):
-  // the aligned 32-bit word holding each element, one load for either dtype
-  // (bf16 rows start at even elements, so the word stays inside the row)
-  const int hd = p.head_dim;
-  const int nq = G * hd;
-  const int qsh = p.q_dtype == NFA_DTYPE_BF16 ? 1 : 2;  // log2 element bytes
-  const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kv * G * p.q_stride_h;
-  uint32_t qbits[kQRawPerThread];
-  int qodd[kQRawPerThread];
-#pragma unroll
-  for (int k = 0; k < kQRawPerThread; ++k) {
-    const int i = imin(tid + k * SB, nq - 1);
-    const int64_t byte = (qrow + (int64_t)(i / hd) * p.q_stride_h + i % hd) << qsh;
-    qodd[k] = (int)(byte & 2);
-    qbits[k] = *(const uint32_t *)((const unsigned char *)p.q + (byte & ~(int64_t)3));
-  }
-  int32_t L, slot_b;
-  int64_t act64, req;
-  sload_row(p.lengths + b, p.active_req + b, p.valid_req + b,
-            p.k_new != nullptr ? p.slots + b : p.lengths + b, L, act64, req, slot_b);
-  const bool active = act64 >= 0;
-  if (p.k_new == nullptr) slot_b = -1;
-  const int32_t *btr = p.block_table_l + req * mb;
-  // pages past the block-table width are never scored (selector:205-206)
-  const int kt_eff = imin(L > 0 ? (L + bs - 1) / bs : 0, mb);
-  // this tile's pages [t0, t1); tiles past the row's pages take no part,
-  // neither scores nor arrival
-  const TileSplit split = tile_split(kt_eff, sd.tcap);
-  if (tile >= split.tiles) return;
-  const int t0 = tile * split.span;
-  const int t1 = imin(t0 + split.span, kt_eff);
-  const int ngrp = (t1 - t0 + 63) / 64;
-  const int last_blk = L > 0 ? (L - 1) / bs : -1;
-  const bool owns_last = last_blk >= t0 && last_blk < t1;
-  // LDS: dims, fine dims, raw query rows, histogram
-  float *s_qraw = s_stage;  // until the statistics phase
-  if (tid < DSUB) s_dims[tid] = dim_v;
-  if (tid < p.fine_dsub) s_fdims[tid] = fdim_v;
-#pragma unroll
-  for (int k = 0; k < kQRawPerThread; ++k) {
-    if (tid + k * SB < nq) {
-      const uint32_t w = qbits[k];
-      s_qraw[tid + k * SB] = qsh == 1 ? __uint_as_float(qodd[k] ? (w & 0xFFFF0000u) : (w << 16))
-                                      : __uint_as_float(w);
-    }
-  }
-  if (tid < 512) s_hist[tid] = 0;
-  lds_barrier();
-  NFA_MARK(clk_tile, 1);
-
-  // scaled, bf16-rounded query rows of this kv group (selector:943-963), and
-  // their negative and positive parts
-  for (int i = tid; i < G * DSUB; i += SB) {
-    const int j = i / DSUB;
-    const int d = i % DSUB;
-    const float qr = bf16r(s_qraw[j * hd + s_dims[d]] * p.scale);
-    s_qf[i] = qr;
-    s_qs[j * 2 * DSUB + d] = qr < 0.0f ? qr : 0.0f;
-    s_qs[j * 2 * DSUB + DSUB + d] = qr > 0.0f ? qr : 0.0f;
-  }
-  lds_barrier();  // the query rows; the raw rows' LDS is free again
-  NFA_MARK(clk_tile, 2);
-
-  // ---- second round trip: statistics (asynchronous), request state -------
-  // (after every LDS read of the prologue: a read behind an asynchronous
-  // global-to-LDS load waits for it)
-  const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
-  const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
-  // speculative: the pools without skip flags contain the final ones
-  const RowGeo g0 = row_geo(p, L, false, false);
-  unsigned char *s_st = smem + sd.a_st;
-  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, t1, s_st);
-  int32_t prev, skf, skn, ph_last;
-  sload_i32x4(p.stats_len_l + req, p.skip_far_l + req, p.skip_near_l + req,
-              btr + (owns_last ? imin((L - 1) / p.page, mb - 1) : 0), prev, skf,
-              skn, ph_last);
-  const bool skip_far = skf != 0;
-  const bool skip_near = skn != 0;
-  if (!(owns_last && active)) ph_last = 0;
-  // the decode token's key row is read from k_new for the statistics when
-  // the fused write targets the slot of token L-1
-  const KV *new_row = nullptr;
-  const int last_phys = safe_page(p, ph_last);
-  if (owns_last && active && p.k_new != nullptr) {
-    if (slot_b >= 0 && slot_b / p.page < p.pool_pages &&
-        slot_b == ph_last * p.page + (L - 1) % p.page)
-      new_row = (const KV *)p.k_new + ((int64_t)b * p.hkv + kv) * p.head_dim;
-  }
-  // decode write of the current token (selector:1030-1061), fire and forget
-  if (p.k_new != nullptr && active && owns_last) decode_write<KV>(p, b, kv);
-
-  // ---- page statistics: latest page, or the whole tile on a rebuild -----
-  const bool do_stats = active && L > 0 && !(skip_far && skip_near);
-  const bool incremental = prev > 0 && L == prev + 1;
-  const bool page_phys = (p.page % bs) == 0;
-  if (do_stats && incremental && owns_last) {
-    stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims,
-                                s_stage, new_row, s_last);
-  } else if (do_stats && !incremental) {
-    int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
-    if (tid == 0) {
-      bool vec = true;
-      for (int c = 0; vec && c < NC; ++c) {
-        const int first = s_dims[c * CH];
-        vec = (first % CH) == 0;
-        for (int e = 1; vec && e < CH; ++e) vec = s_dims[c * CH + e] == first + e;
-        s_coff[c] = first;
-      }
-      s_misc[1] = vec;
-    }
-    if (page_phys) {
-      for (int i = tid; i < t1 - t0; i += SB) {
-        const int lp = imin(((t0 + i) * bs) / p.page, mb - 1);
-        s_tphys[i] = safe_page(p, btr[lp]);
-      }
-    }
-    __syncthreads();
-    if (s_misc[1]) {
-      compute_stats_vec<DSUB, KV>(p, req, kv, L, t0, t1, s_coff,
-                                  page_phys ? s_tphys : nullptr, new_row, L - 1,
-                                  nullptr);
-    } else {
-      __syncthreads();
-      compute_stats<DSUB, KV>(p, req, kv, L, t0, t1, s_stage, s_dims,
-                              page_phys ? s_tphys : nullptr, new_row, L - 1,
-                              nullptr);
-    }
-    // rebuilt statistics: complete the stores, drop cached lines, read back
-    __threadfence();
-    __syncthreads();
-    __threadfence();
-    if constexpr (STG) {
-      __builtin_amdgcn_s_waitcnt(0);  // the speculative loads have landed
-      // recomputed addresses: nothing of the first issue stays live across
-      // the rebuild
-      int t0r = t0;
-      asm volatile("" : "+s"(t0r));
-      stage_stats_async(p, g0, req, kv, t0r, t1, s_st);
-    }
-  }
-  if constexpr (STG) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's staged statistics
-    __syncthreads();
-    if (do_stats && incremental && owns_last && tid < 2 * NC) {
-      // the latest page's statistics, as stored, replace the staged ones
-      bool fpl = false, npl = false;
-      pools(p, g0, last_blk, &fpl, &npl);
-      const bool mml = (fpl && far_mm) || (npl && near_mm);
-      const int slot = tid / NC, c = tid % NC;
-      const float *src = s_last + (slot == 1 ? DSUB : (mml ? 0 : 2 * DSUB));
-      reinterpret_cast<uint4 *>(s_st)[(slot * NC + c) * kSpanMax + (last_blk - t0)] =
-          pack_chunk<KV>(src + c * CH);
-    }
-  }
-  lds_barrier();
-  NFA_MARK(clk_tile, 3);
-
-  // ---- L1 scores: four waves per 64 pages, two query heads per thread -----
-  const RowGeo geo = row_geo(p, L, skip_far, skip_near);
-  float *s_hs = (float *)(smem + sd.a_hs);  // [head][page] bf16 head scores
-  const int j0 = hp, j1 = hp + TPP;
-  if (do_stats && j0 < G) {
-    for (int grp = grp0; grp < ngrp; grp += GSTEP) {
-      const int lp = grp * 64 + lane_id();
-      const int t = t0 + lp;
-      bool fp = false, np = false;
-      if (t < t1) pools(p, geo, t, &fp, &np);
-      if (!(fp || np)) continue;
-      const bool need_mm = (fp && far_mm) || (np && near_mm);
-      const bool need_avg = !need_mm;
-      float h0 = 0.0f, h1 = 0.0f;
-      if constexpr (STG) {
-        // a missing second head scores the first one again, discarded
-        const int j1s = j1 < G ? j1 : j0;
-        l1_heads_staged(reinterpret_cast<const uint4 *>(s_st) + lp,
-                        s_qs + j0 * 2 * DSUB, s_qs + j1s * 2 * DSUB,
-                        s_qf + j0 * DSUB, s_qf + j1s * DSUB, need_mm, bs, &h0, &h1);
-      } else {
-        const bool from_lds = incremental && t == last_blk;
-        float m0 = 0.0f, a0 = 0.0f, m1 = 0.0f, a1 = 0.0f;
-        l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j0 * DSUB, need_mm, need_avg,
-                              from_lds ? s_last : nullptr, &m0, &a0);
-        if (j1 < G)
-          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j1 * DSUB, need_mm,
-                                need_avg, from_lds ? s_last : nullptr, &m1, &a1);
-        h0 = need_mm ? m0 : a0;
-        h1 = need_mm ? m1 : a1;
-      }
-      s_hs[j0 * kSpanMax + lp] = h0;
-      if (j1 < G) s_hs[j1 * kSpanMax + lp] = h1;
-    }
-  }
-  lds_barrier();
-
-  // ---- group mean, keys and high-byte histograms (the hp == 0 waves) -----
-  if (hp == 0) {
-    for (int grp = grp0; grp < ngrp; grp += GSTEP) {
-      const int lp = grp * 64 + lane_id();
-      const int t = t0 + lp;
-      if (t >= t1) continue;
-      bool fp = false, np = false;
-      if (do_stats) pools(p, geo, t, &fp, &np);
-      uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
-      if (fp || np) {
-        // bf16 head scores summed in head order
-        float acc = 0.0f;
-        for (int j = 0; j < G; ++j) acc = acc + s_hs[j * kSpanMax + lp];
-        const uint16_t mean = bf16_bits(acc / (float)G);
-        if (fp) far_bits = mean;
-        if (np) near_bits = mean;
-      }
-      if (p.dbg_far != nullptr) {
-        p.dbg_far[(int64_t)row * mb + t] = far_bits;
-        p.dbg_near[(int64_t)row * mb + t] = near_bits;
-      }
-      // a page belongs to at most one pool: far pages lie below near_start,
-      // near pages at or above it
-      const uint32_t fk = score_key(far_bits);
-      const uint32_t nk = score_key(near_bits);
-      g_keys[t] = (uint16_t)(fk ? fk : nk);
-      if (fk) atomicAdd(&s_hist[fk >> 8], 1);
-      if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
-    }
-  }
-  lds_barrier();
-  if (tid < 256) {
-    const int hf = s_hist[tid];
-    const int hn = s_hist[256 + tid];
-    if (hf) atomicAdd(&g_hist[tid], hf);
-    if (hn) atomicAdd(&g_hist[256 + tid], hn);
-  }
-  NFA_MARK(clk_tile, 4);
-
-  // ---- arrival; the last workgroup of the row runs the tail --------------
-  if (tid == 0) {
-    // every workgroup of the request has read stats_len once all arrived
-    const unsigned int rb = __hip_atomic_fetch_add(
-        &req_cnt[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (rb == (unsigned int)(split.tiles * p.hkv - 1)) {
-      if (do_stats) p.stats_len_l[req] = L;
-      __hip_atomic_store(&req_cnt[b], 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  if (!arrive_last(&row_cnt[row], (unsigned int)split.tiles, &s_misc[0])) return;
-
-  // =========================== tail ======================================
-  // (its LDS overlaps the tile stage's private part, no longer used)
-  uint16_t *s_keys = (uint16_t *)(smem + sd.a_keys);
-  uint32_t *s_cbits = (uint32_t *)(smem + sd.a_cbits);
-  const bool dbg = p.dbg_i_f != nullptr;
-  uint32_t *s_dbf = (uint32_t *)(smem + sd.a_dbf);
-  uint32_t *s_dbn = (uint32_t *)(smem + sd.a_dbn);
-  uint64_t *s_dsel = (uint64_t *)(smem + sd.a_dsel);
-  NFA_MARK(clk_tail, 0);
-
-  const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
-  if (p.dbg_bounds != nullptr && kv == 0 && tid == 0) {
-    p.dbg_bounds[b * 3 + 0] = lb.lower;
-    p.dbg_bounds[b * 3 + 1] = lb.upper;
-    p.dbg_bounds[b * 3 + 2] = lb.quota;
-  }
-  // candidate tokens lie in [tok_lo, tok_hi) and exist only when quota > 0
-  const int tok_lo = imax(p.sink_tokens, lb.lower);
-  const int tok_hi = imin(imin(lb.lo, L), lb.upper);
-  const bool any_cand = lb.quota > 0 && tok_hi > tok_lo;
-  const int near_start = geo.near_start;
-
-  // row histograms into LDS, reset for the next launch
-  if (tid < 512) {
-    s_hist[tid] = atomicExch(&g_hist[tid], 0);
-    s_hist[512 + tid] = 0;
-  }
-  uint32_t *s_eqb = (uint32_t *)(smem + sd.a_eqb);
-  for (int w = tid; w < sd.words; w += SB) {
-    s_cbits[w] = 0u;
-    s_eqb[w] = 0u;
-    if (dbg) {
-      s_dbf[w] = 0u;
-      s_dbn[w] = 0u;
-    }
-  }
-  if (tid == 0) {
-    s_misc[3] = 0;  // debug selection list lengths (far, near)
-    s_misc[4] = 0;
-  }
-  if (sd.nseg == 1) stage_keys(g_keys, 0, sd.seg, s_keys);
-  __syncthreads();
-  // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
-  if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 8);
-  if (wave_id() == 1) wave_threshold_bin(s_hist + 256, p.k_n, s_tmp + 12);
-  __syncthreads();
-  const int hbf = s_tmp[8], hbn = s_tmp[12];
-  if (hbf >= 0 || hbn >= 0) {
-    // refinement: low-byte histograms of the keys in the threshold bins
-    for (int sg = 0; sg < sd.nseg; ++sg) {
-      const int seg_base = sg * sd.seg;
-      if (sd.nseg > 1) {
-        __syncthreads();
-        stage_keys(g_keys, seg_base, sd.seg, s_keys);
-        __syncthreads();
-      }
-      const int n = imin(sd.seg, kt_eff - seg_base);
-      for (int i = tid; i < n; i += SB) {
-        const uint32_t k = s_keys[i];
-        const bool near = seg_base + i >= near_start;
-        const int hb = near ? hbn : hbf;
-        if (k != 0u && (int)(k >> 8) == hb)
-          atomicAdd(&s_hist[(near ? 768 : 512) + (k & 255u)], 1);
-      }
-    }
-    __syncthreads();
-    if (wave_id() == 0 && hbf >= 0)
-      wave_threshold_bin(s_hist + 512, p.k_f - s_tmp[9], s_tmp + 16);
-    if (wave_id() == 1 && hbn >= 0)
-      wave_threshold_bin(s_hist + 768, p.k_n - s_tmp[13], s_tmp + 20);
-    __syncthreads();
-  }
-  const PoolThr tf = pool_threshold(p.k_f, s_tmp + 8, s_tmp + 16, s_hist + 512);
-  const PoolThr tn = pool_threshold(p.k_n, s_tmp + 12, s_tmp + 20, s_hist + 768);
-  NFA_MARK(clk_tail, 1);
-
-  // ---- selected pages -> candidate page bitmap ---------------------------
-  auto select_page = [&](int page, uint32_t k, bool near) {
-    const uint32_t bit = 1u << (page & 31);
-    if (any_cand && page * bs < tok_hi && page * bs + bs > tok_lo)
-      atomicOr(&s_cbits[page >> 5], bit);
-    if (dbg) {
-      const int pos = atomicAdd(&s_misc[near ? 4 : 3], 1);
-      s_dsel[(near ? p.k_f : 0) + pos] = ((uint64_t)k << 32) | (uint32_t)page;
-      atomicOr(near ? &s_dbn[page >> 5] : &s_dbf[page >> 5], bit);
-    }
-  };
-  // keys above the threshold are selected outright; keys equal to it too
-  // unless only some of them are, then they go to the tie bitmap
-  for (int sg = 0; sg < sd.nseg; ++sg) {
-    const int seg_base = sg * sd.seg;
-    if (sd.nseg > 1) {
-      __syncthreads();
-      stage_keys(g_keys, seg_base, sd.seg, s_keys);
-      __syncthreads();
-    }
-    const int n = imin(sd.seg, kt_eff - seg_base);
-    for (int i = tid; i < n; i += SB) {
-      const uint32_t k = s_keys[i];
-      if (k == 0u) continue;
-      const int page = seg_base + i;
-      const bool near = page >= near_start;
-      const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
-      const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
-      if (k > T || (k == T && all_eq))
-        select_page(page, k, near);
-      else if (k == T)
-        atomicOr(&s_eqb[page >> 5], 1u << (page & 31));
-    }
-  }
-  __syncthreads();
-  if (tie_cut(tf) || tie_cut(tn)) {
-    // tied pages of each pool in page order: the first `need` are selected
-    const int wpt = (sd.words + SB - 1) / SB;
-    const int w0 = tid * wpt;
-    const int w1 = imin(w0 + wpt, sd.words);
-    auto far_mask = [&](int w) -> uint32_t {
-      const int d = near_start - w * 32;
-      return d >= 32 ? 0xFFFFFFFFu : (d <= 0 ? 0u : ((1u << d) - 1u));
-    };
-    int c[2] = {0, 0};
-    for (int w = w0; w < w1; ++w) {
-      const uint32_t bits = s_eqb[w];
-      const uint32_t fm = far_mask(w);
-      c[0] += __popc(bits & fm);
-      c[1] += __popc(bits & ~fm);
-    }
-    int tot2[2];
-    block_scan_n<2, SW>(c, s_tmp + 32, tot2);
-    for (int w = w0; w < w1; ++w) {
-      uint32_t bits = s_eqb[w];
-      const uint32_t fm = far_mask(w);
-      while (bits) {
-        const int bit = __ffs(bits) - 1;
-        bits &= bits - 1u;
-        const bool near = ((fm >> bit) & 1u) == 0u;
-        const int rank = near ? c[1]++ : c[0]++;
-        if (rank < (near ? tn.need : tf.need))
-          select_page(w * 32 + bit, (uint32_t)(near ? tn.T : tf.T), near);
-      }
-    }
-  }
-  NFA_MARK(clk_tail, 2);
-  __syncthreads();
-  if (tid == 0 && any_cand) {
-    // sink and SWA bypass pages (selector:1195-1251)
-    const int spl = p.sink_tokens / bs;
-    const bool byp0_keep = (p.sink_tokens % bs) != 0;
-    bool byp1_keep = (lb.lo % bs != 0) && (lb.lo / bs >= spl);
-    if (p.sink_tokens % bs != 0) byp1_keep = byp1_keep && (lb.lo / bs != spl);
-    const int bp0 = byp0_keep ? spl : -1;
-    const int bp1 = byp1_keep ? lb.lo / bs : -1;
-    if (bp0 >= 0 && bp0 < sd.kstride && bp0 * bs < tok_hi && bp0 * bs + bs > tok_lo)
-      s_cbits[bp0 >> 5] |= 1u << (bp0 & 31);
-    if (bp1 >= 0 && bp1 < sd.kstride && bp1 * bs < tok_hi && bp1 * bs + bs > tok_lo)
-      s_cbits[bp1 >> 5] |= 1u << (bp1 & 31);
-  }
-  __syncthreads();
-  // compaction: sorted unique candidate pages, then their physical pages
-  const int wpt = (sd.words + SB - 1) / SB;
-  const int w0 = tid * wpt;
-  const int w1 = imin(w0 + wpt, sd.words);
-  int *s_pages = (int *)(smem + sd.a_pages);
-  int np_u;
-  {
-    int c1 = 0;
-    for (int w = w0; w < w1; ++w) c1 += __popc(s_cbits[w]);
-    int pos = block_scan_exclusive<SW>(c1, s_tmp, &np_u);
-    for (int w = w0; w < w1; ++w) {
-      uint32_t bits = s_cbits[w];
-      while (bits) {
-        if (pos < sd.np) s_pages[pos] = w * 32 + __ffs(bits) - 1;
-        ++pos;
-        bits &= bits - 1u;
-      }
-    }
-  }
-  NFA_MARK(clk_tail, 3);
-  __syncthreads();
-  np_u = imin(np_u, sd.np);
-  {
-    int *g_pages = (int *)(ws + sd.w_pages) + (int64_t)row * sd.np;
-    int *g_pphys = (int *)(ws + sd.w_pphys) + (int64_t)row * sd.np;
-    for (int i = tid; i < np_u; i += SB) {
-      const int pg = s_pages[i];
-      g_pages[i] = pg;
-      g_pphys[i] = btr[imin((pg * bs) / p.page, mb - 1)];
-    }
-    if (tid == 0) {
-      ((int *)(ws + sd.w_npu))[row] = np_u;
-      if (p.dbg_cand_count != nullptr)
-        p.dbg_cand_count[row] = imin(np_u * bs, p.dbg_cand_cap);
-    }
-    if (tid == 1 && row == 0) {
-      // the L2 dims as aligned 16-byte runs (the vector path of kernel B)
-      const int nch = p.fine_dsub / CH;
-      bool vec = (p.fine_dsub % CH == 0) && nch <= 16;
-      for (int c = 0; vec && c < nch; ++c) {
-        const int first = s_fdims[c * CH];
-        vec = (first % CH) == 0;
-        for (int e = 1; vec && e < CH; ++e) vec = s_fdims[c * CH + e] == first + e;
-      }
-      int *g_vec = (int *)(ws + sd.w_l2vec);
-      g_vec[0] = vec ? nch : 0;
-    }
-  }
-  NFA_MARK(clk_tail, 4);
-  // L1 debug outputs: I_F / I_N (selector:1766-1803 order: valid pages by
-  // (score desc, page asc), then -inf fillers by ascending page)
-  if (dbg) {
-    for (int pool = 0; pool < 2; ++pool) {
-      const int K = pool == 0 ? p.k_f : p.k_n;
-      const int nsel = pool == 0 ? tf.nsel : tn.nsel;
-      const uint64_t *sel = s_dsel + (pool == 0 ? 0 : p.k_f);
-      const uint32_t *bm = pool == 0 ? s_dbf : s_dbn;
-      int32_t *out = (pool == 0 ? p.dbg_i_f + (int64_t)row * p.k_f
-                                : p.dbg_i_n + (int64_t)row * p.k_n);
-      for (int i = tid; i < nsel; i += SB) {
-        const uint64_t ki = sel[i];
-        const uint32_t vi = (uint32_t)(ki >> 32), ti = (uint32_t)ki;
-        int rank = 0;
-        for (int j = 0; j < nsel; ++j) {
-          const uint64_t kj = sel[j];
-          const uint32_t vj = (uint32_t)(kj >> 32), tj = (uint32_t)kj;
-          rank += (vj > vi) || (vj == vi && tj < ti);
-        }
-        out[rank] = (int)ti;
-      }
-      const int nfill = K - nsel;  // uniform
-      if (nfill > 0) {
-        int z = 0;
-        for (int w = w0; w < w1; ++w) z += 32 - __popc(bm[w]);
-        int tz;
-        int r = block_scan_exclusive<SW>(z, s_tmp, &tz);
-        for (int w = w0; w < w1 && r < nfill; ++w) {
-          uint32_t zeros = ~bm[w];
-          while (zeros && r < nfill) {
-            out[nsel + r++] = w * 32 + __ffs(zeros) - 1;
-            zeros &= zeros - 1u;
-          }
-        }
-      }
-    }
-  }
-  NFA_MARK(clk_tail, 6);
-}
-
-// ---------------------------------------------------------------------------
-// kernel B: L2 logits, top-quota selection and union
+// L2 top-quota selection over the dense candidate slots
 // ---------------------------------------------------------------------------
 
 // Candidate tokens in the dense page-major layout: slot i belongs to page
@@ -1620,172 +1043,554 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
   __syncthreads();
 }
 
-template <typename KV>
+// ---------------------------------------------------------------------------
+// the selector kernel: L1 tiles, then the tail (candidate pages, L2)
+// ---------------------------------------------------------------------------
+
+// Phase timestamp (debug timeline): every wave of the workgroup has reached
+// it (memory accesses in flight stay in flight), then thread 0 stores the
+// wall clock.  Uniform condition.
+#define NFA_MARK(slot_base, k)                                        \
+  do {                                                                \
+    if (p.dbg_clock != nullptr) {                                     \
+      lds_barrier();                                                  \
+      if (threadIdx.x == 0) p.dbg_clock[(slot_base) + (k)] = wall_clock64(); \
+    }                                                                 \
+  } while (0)
+
+template <int DSUB, typename KV>
 __global__ void __launch_bounds__(SB)
-    nfa_l2_kernel(const NfaSelectParams p, const SelDims sd) {
+    nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
   warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int CH = Elem<KV>::kChunk;
-  const int TPS = SB / sd.l2slots;  // threads per dense slot
-  int *s_hist = (int *)(smem + sd.b_hist);
-  int *s_tmp = (int *)(smem + sd.b_tmp);
-  int *s_misc = (int *)(smem + sd.b_misc);
-  float *s_qg = (float *)(smem + sd.b_qg);
-  int *s_fdims = (int *)(smem + sd.b_fdims);
-  int *s_tok = (int *)(smem + sd.b_tok);
+  constexpr int NC = DSUB / CH;
+  constexpr bool STG = DSUB == 32 && sizeof(KV) == 2;  // stats staged in LDS
+  int *s_hist = (int *)(smem + sd.a_hist);  // far hi | near hi | far lo | near lo
+  int *s_tmp = (int *)(smem + sd.a_tmp);
+  int *s_misc = (int *)(smem + sd.a_misc);
+  float *s_qf = (float *)(smem + sd.a_qf);
+  float *s_qs = (float *)(smem + sd.a_qs);
+  float *s_qg = (float *)(smem + sd.a_qg);
+  int *s_fdims = (int *)(smem + sd.a_fdims);
+  int *s_dims = (int *)(smem + sd.a_dims);
+  float *s_last = (float *)(smem + sd.a_last);
+  int *s_tphys = (int *)(smem + sd.a_tphys);
+  float *s_stage = (float *)(smem + sd.a_stage);
 
   const int tid = threadIdx.x;
-  const int row = blockIdx.x;  // chunk-major grid, as kernel A
-  const int chunk = blockIdx.y;
+  // tile-major grid: the first dispatch round holds the low tiles of every
+  // row, and a row's tiles share an XCD (workgroups go round-robin over XCDs)
+  const int row = blockIdx.x;
+  const int tile = blockIdx.y;
   const int b = row / p.hkv;
   const int kv = row % p.hkv;
   const int G = p.hq / p.hkv;
   const int bs = p.bs;
   const int mb = p.max_blocks;
-  const int64_t clk_b =
-      ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32 + 8;
-  if (chunk == 0) NFA_MARK(clk_b, 0);
-  unsigned char *ws = (unsigned char *)p.workspace;
-  unsigned int *bcnt = (unsigned int *)(ws + sd.w_bcnt);
-  const int *g_pages = (const int *)(ws + sd.w_pages) + (int64_t)row * sd.np;
-  const int *g_pphys = (const int *)(ws + sd.w_pphys) + (int64_t)row * sd.np;
-  uint16_t *g_dk = (uint16_t *)(ws + sd.w_dk) + (int64_t)row * sd.dstride;
+  // wave w scores query heads hp = w % TPP and hp + TPP of the pages of the
+  // 64-page groups w / TPP, w / TPP + SW / TPP, ...: query reads are uniform
+  // over the wave
+  const int hp = wave_id() % TPP;
+  const int grp0 = wave_id() / TPP;
+  constexpr int GSTEP = SW / TPP;
 
-  // ---- first round trip: row scalars, candidate pages, L2 dims -----------
-  const int L = p.lengths[b];
-  const int64_t req = p.valid_req[b];
-  const int32_t *btr = p.block_table_l + req * mb;
-  const int np_u = ((const int *)(ws + sd.w_npu))[row];
-  const int nch = ((const int *)(ws + sd.w_l2vec))[0];  // 0: scalar L2 dims
-  const int n_dense = np_u * bs;
-  // chunks past the row's dense slots take no part
-  const int nchk = imax(1, (n_dense + sd.l2slots - 1) / sd.l2slots);
-  if (chunk >= nchk) return;
-  for (int d = tid; d < p.fine_dsub; d += SB) s_fdims[d] = p.fine_dims[d];
-  const int sl = tid / TPS;   // dense slot of this thread within the chunk
-  const int part = tid % TPS; // which of the slot's 16-byte chunks it loads
-  const int i = chunk * sd.l2slots + sl;
-  int tok = -1, phys = 0, pgphys = 0;
-  {
-    const int pi = i / bs;
-    if (pi < sd.np) {
-      const int pg = g_pages[pi];
-      pgphys = g_pphys[pi];
-      tok = pg * bs + (i - pi * bs);
-    }
-  }
-  // chunk offsets of this thread's part of the L2 dims
-  int coff[4] = {0, 0, 0, 0};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int c = part + TPS * k;
-    if (c * CH < p.fine_dsub) coff[k] = imin(p.fine_dims[c * CH], p.head_dim - CH);
-  }
-  const bool scored = i < n_dense;  // uniform per slot
-  // ---- second round trip: the key rows of the slots, the query ----------
-  const bool skip_far = p.skip_far_l[req] != 0;
-  const bool skip_near = p.skip_near_l[req] != 0;
-  const bool page_phys = (p.page % bs) == 0;
-  const KV *kpool = (const KV *)p.k_pool_l;
-  uint4 *s_st4 = (uint4 *)(smem + sd.b_stage);
-  float *s_stf = (float *)(smem + sd.b_stage);
-  if (scored) {
-    phys = safe_page(p, page_phys ? pgphys : btr[imin(tok / p.page, mb - 1)]);
-    const KV *kr = kpool + kv_offset(p, phys, kv, tok % p.page);
-    if (nch > 0) {
-      uint4 r[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int c = part + TPS * k;
-        r[k] = c < nch ? *reinterpret_cast<const uint4 *>(kr + coff[k])
-                       : make_uint4(0u, 0u, 0u, 0u);
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int c = part + TPS * k;
-        if (c < nch) s_st4[sl * nch + c] = r[k];
-      }
-    }
-  }
-  if (part == 0) s_tok[sl] = scored ? tok : -1;
-  __syncthreads();  // s_fdims
-  if (scored && nch == 0) {
-    // L2 dims not in 16-byte runs: element loads, TPS threads per slot
-    const KV *kr = kpool + kv_offset(p, phys, kv, tok % p.page);
-    for (int d = part; d < p.fine_dsub; d += TPS)
-      s_stf[sl * p.fine_dsub + d] = Elem<KV>::load(kr + s_fdims[d]);
-  }
-  // grouped L2 query (selector:979-1002)
+  const int64_t clk_tile = ((int64_t)row * (sd.clk_tiles + 1) + tile) * 32;
+  const int64_t clk_tail = ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32;
+  NFA_MARK(clk_tile, 0);
+  unsigned char *ws = (unsigned char *)p.workspace;
+  unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
+  unsigned int *req_cnt = (unsigned int *)(ws + sd.w_reqcnt);
+  int *g_hist = (int *)(ws + sd.w_hist) + (int64_t)row * 512;
+  uint16_t *g_keys = (uint16_t *)(ws + sd.w_keys) + (int64_t)row * sd.kstride;
+
+  // ---- first round trip: every load that depends on no other ------------
+  // vector loads first (unconditional, clamped indices), then the row state
+  // through the scalar cache
+  const int dim_v = p.dims[imin(tid, DSUB - 1)];
+  const int fdim_v = p.fine_dims[imin(tid, p.fine_dsub - 1)];
+  // the kv group's query rows, whole (the L1 dims are gathered from LDS):
+  // the aligned 32-bit word holding each element, one load for either dtype
+  // (bf16 rows start at even elements, so the word stays inside the row)
+  const int hd = p.head_dim;
+  const int nq = G * hd;
+  const int qsh = p.q_dtype == NFA_DTYPE_BF16 ? 1 : 2;  // log2 element bytes
   const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kv * G * p.q_stride_h;
+  uint32_t qbits[kQRawPerThread];
+  int qodd[kQRawPerThread];
+#pragma unroll
+  for (int k = 0; k < kQRawPerThread; ++k) {
+    const int i = imin(tid + k * SB, nq - 1);
+    const int64_t byte = (qrow + (int64_t)(i / hd) * p.q_stride_h + i % hd) << qsh;
+    qodd[k] = (int)(byte & 2);
+    qbits[k] = *(const uint32_t *)((const unsigned char *)p.q + (byte & ~(int64_t)3));
+  }
+  int32_t L, slot_b;
+  int64_t act64, req;
+  sload_row(p.lengths + b, p.active_req + b, p.valid_req + b,
+            p.k_new != nullptr ? p.slots + b : p.lengths + b, L, act64, req, slot_b);
+  const bool active = act64 >= 0;
+  if (p.k_new == nullptr) slot_b = -1;
+  const int32_t *btr = p.block_table_l + req * mb;
+  // pages past the block-table width are never scored (selector:205-206)
+  const int kt_eff = imin(L > 0 ? (L + bs - 1) / bs : 0, mb);
+  // this tile's pages [t0, t1); tiles past the row's pages take no part,
+  // neither scores nor arrival
+  const TileSplit split = tile_split(kt_eff, sd.tcap);
+  if (tile >= split.tiles) return;
+  const int t0 = tile * split.span;
+  const int t1 = imin(t0 + split.span, kt_eff);
+  const int ngrp = (t1 - t0 + 63) / 64;
+  const int last_blk = L > 0 ? (L - 1) / bs : -1;
+  const bool owns_last = last_blk >= t0 && last_blk < t1;
+  // LDS: dims, fine dims, raw query rows, histogram
+  float *s_qraw = s_stage;  // until the statistics phase
+  if (tid < DSUB) s_dims[tid] = dim_v;
+  if (tid < p.fine_dsub) s_fdims[tid] = fdim_v;
+#pragma unroll
+  for (int k = 0; k < kQRawPerThread; ++k) {
+    if (tid + k * SB < nq) {
+      const uint32_t w = qbits[k];
+      s_qraw[tid + k * SB] = qsh == 1 ? __uint_as_float(qodd[k] ? (w & 0xFFFF0000u) : (w << 16))
+                                      : __uint_as_float(w);
+    }
+  }
+  if (tid < 512) s_hist[tid] = 0;
+  lds_barrier();
+  NFA_MARK(clk_tile, 1);
+
+  // scaled, bf16-rounded query rows of this kv group (selector:943-963), and
+  // their negative and positive parts
+  for (int i = tid; i < G * DSUB; i += SB) {
+    const int j = i / DSUB;
+    const int d = i % DSUB;
+    const float qr = bf16r(s_qraw[j * hd + s_dims[d]] * p.scale);
+    s_qf[i] = qr;
+    s_qs[j * 2 * DSUB + d] = qr < 0.0f ? qr : 0.0f;
+    s_qs[j * 2 * DSUB + DSUB + d] = qr > 0.0f ? qr : 0.0f;
+  }
+  // grouped L2 query (selector:979-1002): bf16 terms summed in head order
   for (int d = tid; d < p.fine_dsub; d += SB) {
     const int dim = s_fdims[d];
-    float qv[GMAX];
-#pragma unroll
-    for (int j = 0; j < GMAX; ++j)
-      qv[j] = j < G ? load_any(p.q, qrow + (int64_t)j * p.q_stride_h + dim,
-                               p.q_dtype)
-                    : 0.0f;
     float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < GMAX; ++j)
-      if (j < G) acc = acc + bf16r(qv[j] * p.scale);
+    for (int j = 0; j < G; ++j) acc = acc + bf16r(s_qraw[j * hd + dim] * p.scale);
     s_qg[d] = acc;
   }
-  __syncthreads();
+  if (wave_id() == 0) {
+    // the L2 dims as aligned 16-byte runs: their count, or 0 (element loads)
+    bool ok = p.fine_dsub % CH == 0;
+    for (int d = lane_id(); ok && d < p.fine_dsub; d += 64) {
+      const int first = s_fdims[d - d % CH];
+      ok = first % CH == 0 && first + CH <= p.head_dim && s_fdims[d] == first + d % CH;
+    }
+    const bool all = __ballot(!ok) == 0;
+    if (lane_id() == 0) s_misc[5] = all ? p.fine_dsub / CH : 0;
+  }
+  lds_barrier();  // the query rows; the raw rows' LDS is free again
+  NFA_MARK(clk_tile, 2);
 
-  // ---- L2 logits (selector:459-516): fp32 dot over the L2 dims in order --
-  const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
-  const int tok_lo = imax(p.sink_tokens, lb.lower);
-  const int tok_hi = imin(imin(lb.lo, L), lb.upper);
-  if (tid < sd.l2slots) {
-    const int ii = chunk * sd.l2slots + tid;
-    const int tk = s_tok[tid];
-    if (tk >= 0) {
-      uint16_t key = 0;
-      if (tk >= tok_lo && tk < tok_hi) {
-        float acc = 0.0f;
-        if (nch > 0) {
-          for (int c = 0; c < nch; ++c) {
-            float x[CH];
-            unpack_chunk<KV>(s_st4[tid * nch + c], x);
-#pragma unroll
-            for (int e = 0; e < CH; ++e) {
-              const float prod = x[e] * s_qg[c * CH + e];
-              acc = acc + prod;
-            }
-          }
-        } else {
-          for (int d = 0; d < p.fine_dsub; ++d) {
-            const float prod = s_stf[tid * p.fine_dsub + d] * s_qg[d];
-            acc = acc + prod;
-          }
-        }
-        const uint16_t bits = bf16_bits(acc);
-        key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
-        if (p.dbg_cand_tok != nullptr && ii < p.dbg_cand_cap) {
-          p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + ii] = tk;
-          p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + ii] =
-              bits == kNanBits ? kNegInfBits : bits;
-        }
-      } else if (p.dbg_cand_tok != nullptr && ii < p.dbg_cand_cap) {
-        p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + ii] = -1;
+  // ---- second round trip: statistics (asynchronous), request state -------
+  // (after every LDS read of the prologue: a read behind an asynchronous
+  // global-to-LDS load waits for it)
+  const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
+  const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
+  // speculative: the pools without skip flags contain the final ones
+  const RowGeo g0 = row_geo(p, L, false, false);
+  unsigned char *s_st = smem + sd.a_st;
+  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, t1, s_st);
+  int32_t prev, skf, skn, ph_last;
+  sload_i32x4(p.stats_len_l + req, p.skip_far_l + req, p.skip_near_l + req,
+              btr + (owns_last ? imin((L - 1) / p.page, mb - 1) : 0), prev, skf,
+              skn, ph_last);
+  const bool skip_far = skf != 0;
+  const bool skip_near = skn != 0;
+  if (!(owns_last && active)) ph_last = 0;
+  // the decode token's key row is read from k_new for the statistics when
+  // the fused write targets the slot of token L-1
+  const KV *new_row = nullptr;
+  const int last_phys = safe_page(p, ph_last);
+  if (owns_last && active && p.k_new != nullptr) {
+    if (slot_b >= 0 && slot_b / p.page < p.pool_pages &&
+        slot_b == ph_last * p.page + (L - 1) % p.page)
+      new_row = (const KV *)p.k_new + ((int64_t)b * p.hkv + kv) * p.head_dim;
+  }
+  // decode write of the current token (selector:1030-1061), fire and forget
+  if (p.k_new != nullptr && active && owns_last) decode_write<KV>(p, b, kv);
+
+  // ---- page statistics: latest page, or the whole tile on a rebuild -----
+  const bool do_stats = active && L > 0 && !(skip_far && skip_near);
+  const bool incremental = prev > 0 && L == prev + 1;
+  const bool page_phys = (p.page % bs) == 0;
+  const KV *kpool = (const KV *)p.k_pool_l;
+  if (do_stats && incremental && owns_last) {
+    stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims,
+                                s_stage, new_row, s_last);
+    if (p.l2_keys_l != nullptr && tid < p.fine_dsub) {
+      // the new token's L2 side row
+      const KV *src = new_row != nullptr
+                          ? new_row
+                          : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page);
+      l2_side_row<KV>(p, req, kv, L - 1)[tid] = src[s_fdims[tid]];
+    }
+  } else if (do_stats && !incremental) {
+    int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
+    if (tid == 0) {
+      bool vec = true;
+      for (int c = 0; vec && c < NC; ++c) {
+        const int first = s_dims[c * CH];
+        vec = (first % CH) == 0;
+        for (int e = 1; vec && e < CH; ++e) vec = s_dims[c * CH + e] == first + e;
+        s_coff[c] = first;
       }
-      g_dk[ii] = key;
+      s_misc[1] = vec;
+    }
+    if (page_phys) {
+      for (int i = tid; i < t1 - t0; i += SB) {
+        const int lp = imin(((t0 + i) * bs) / p.page, mb - 1);
+        s_tphys[i] = safe_page(p, btr[lp]);
+      }
+    }
+    __syncthreads();
+    if (s_misc[1]) {
+      compute_stats_vec<DSUB, KV>(p, req, kv, L, t0, t1, s_coff,
+                                  page_phys ? s_tphys : nullptr, new_row, L - 1,
+                                  nullptr);
+    } else {
+      __syncthreads();
+      compute_stats<DSUB, KV>(p, req, kv, L, t0, t1, s_stage, s_dims,
+                              page_phys ? s_tphys : nullptr, new_row, L - 1,
+                              nullptr);
+    }
+    if (p.l2_keys_l != nullptr) {
+      // L2 side rows of the tile's tokens
+      const int tlo = t0 * bs;
+      const int thi = imin(t1 * bs, L);
+      const int nchv = s_misc[5];  // 16-byte runs of the L2 dims, 0: elements
+      auto src_row = [&](int tok) -> const KV * {
+        if (new_row != nullptr && tok == L - 1) return new_row;
+        const int phys = page_phys ? s_tphys[tok / bs - t0]
+                                   : safe_page(p, btr[imin(tok / p.page, mb - 1)]);
+        return kpool + kv_offset(p, phys, kv, tok % p.page);
+      };
+      if (nchv > 0) {
+        for (int e = tid; e < (thi - tlo) * nchv; e += SB) {
+          const int tok = tlo + e / nchv;
+          const int c = e % nchv;
+          *reinterpret_cast<uint4 *>(l2_side_row<KV>(p, req, kv, tok) + c * CH) =
+              *reinterpret_cast<const uint4 *>(src_row(tok) + s_fdims[c * CH]);
+        }
+      } else {
+        for (int e = tid; e < (thi - tlo) * p.fine_dsub; e += SB) {
+          const int tok = tlo + e / p.fine_dsub;
+          const int d = e % p.fine_dsub;
+          l2_side_row<KV>(p, req, kv, tok)[d] = src_row(tok)[s_fdims[d]];
+        }
+      }
+    }
+    // rebuilt statistics: complete the stores, drop cached lines, read back
+    __threadfence();
+    __syncthreads();
+    __threadfence();
+    if constexpr (STG) {
+      __builtin_amdgcn_s_waitcnt(0);  // the speculative loads have landed
+      // recomputed addresses: nothing of the first issue stays live across
+      // the rebuild
+      int t0r = t0;
+      asm volatile("" : "+s"(t0r));
+      stage_stats_async(p, g0, req, kv, t0r, t1, s_st);
     }
   }
-  if (chunk == 0) NFA_MARK(clk_b, 1);
+  if constexpr (STG) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's staged statistics
+    __syncthreads();
+    if (do_stats && incremental && owns_last && tid < 2 * NC) {
+      // the latest page's statistics, as stored, replace the staged ones
+      bool fpl = false, npl = false;
+      pools(p, g0, last_blk, &fpl, &npl);
+      const bool mml = (fpl && far_mm) || (npl && near_mm);
+      const int slot = tid / NC, c = tid % NC;
+      const float *src = s_last + (slot == 1 ? DSUB : (mml ? 0 : 2 * DSUB));
+      reinterpret_cast<uint4 *>(s_st)[(slot * NC + c) * kSpanMax + (last_blk - t0)] =
+          pack_chunk<KV>(src + c * CH);
+    }
+  }
+  lds_barrier();
+  NFA_MARK(clk_tile, 3);
 
-  // ---- arrival; the last workgroup of the row selects ---------------------
-  if (!arrive_last(&bcnt[row], (unsigned int)nchk, &s_misc[0])) return;
-  NFA_MARK(clk_b, 2);
+  // ---- L1 scores: four waves per 64 pages, two query heads per thread -----
+  const RowGeo geo = row_geo(p, L, skip_far, skip_near);
+  float *s_hs = (float *)(smem + sd.a_hs);  // [head][page] bf16 head scores
+  const int j0 = hp, j1 = hp + TPP;
+  if (do_stats && j0 < G) {
+    for (int grp = grp0; grp < ngrp; grp += GSTEP) {
+      const int lp = grp * 64 + lane_id();
+      const int t = t0 + lp;
+      bool fp = false, np = false;
+      if (t < t1) pools(p, geo, t, &fp, &np);
+      if (!(fp || np)) continue;
+      const bool need_mm = (fp && far_mm) || (np && near_mm);
+      const bool need_avg = !need_mm;
+      float h0 = 0.0f, h1 = 0.0f;
+      if constexpr (STG) {
+        // a missing second head scores the first one again, discarded
+        const int j1s = j1 < G ? j1 : j0;
+        l1_heads_staged(reinterpret_cast<const uint4 *>(s_st) + lp,
+                        s_qs + j0 * 2 * DSUB, s_qs + j1s * 2 * DSUB,
+                        s_qf + j0 * DSUB, s_qf + j1s * DSUB, need_mm, bs, &h0, &h1);
+      } else {
+        const bool from_lds = incremental && t == last_blk;
+        float m0 = 0.0f, a0 = 0.0f, m1 = 0.0f, a1 = 0.0f;
+        l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j0 * DSUB, need_mm, need_avg,
+                              from_lds ? s_last : nullptr, &m0, &a0);
+        if (j1 < G)
+          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j1 * DSUB, need_mm,
+                                need_avg, from_lds ? s_last : nullptr, &m1, &a1);
+        h0 = need_mm ? m0 : a0;
+        h1 = need_mm ? m1 : a1;
+      }
+      s_hs[j0 * kSpanMax + lp] = h0;
+      if (j1 < G) s_hs[j1 * kSpanMax + lp] = h1;
+    }
+  }
+  lds_barrier();
 
-  uint16_t *s_dk = (uint16_t *)(smem + sd.b_dk);
-  int *s_pages = (int *)(smem + sd.b_pages);
-  int *s_pphys = (int *)(smem + sd.b_pphys);
-  const RegionLists rl{(int *)(smem + sd.b_l0), (int *)(smem + sd.b_l0x),
-                       (int *)(smem + sd.b_l1), (int *)(smem + sd.b_l1x),
-                       (int *)(smem + sd.b_mid), (int *)(smem + sd.b_mslot)};
-  // protected ids; the gather slots of the first 256 are fetched now
+  // ---- group mean, keys and high-byte histograms (the hp == 0 waves) -----
+  if (hp == 0) {
+    for (int grp = grp0; grp < ngrp; grp += GSTEP) {
+      const int lp = grp * 64 + lane_id();
+      const int t = t0 + lp;
+      if (t >= t1) continue;
+      bool fp = false, np = false;
+      if (do_stats) pools(p, geo, t, &fp, &np);
+      uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
+      if (fp || np) {
+        // bf16 head scores summed in head order
+        float acc = 0.0f;
+        for (int j = 0; j < G; ++j) acc = acc + s_hs[j * kSpanMax + lp];
+        const uint16_t mean = bf16_bits(acc / (float)G);
+        if (fp) far_bits = mean;
+        if (np) near_bits = mean;
+      }
+      if (p.dbg_far != nullptr) {
+        p.dbg_far[(int64_t)row * mb + t] = far_bits;
+        p.dbg_near[(int64_t)row * mb + t] = near_bits;
+      }
+      // a page belongs to at most one pool: far pages lie below near_start,
+      // near pages at or above it
+      const uint32_t fk = score_key(far_bits);
+      const uint32_t nk = score_key(near_bits);
+      g_keys[t] = (uint16_t)(fk ? fk : nk);
+      if (fk) atomicAdd(&s_hist[fk >> 8], 1);
+      if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
+    }
+  }
+  lds_barrier();
+  if (tid < 256) {
+    const int hf = s_hist[tid];
+    const int hn = s_hist[256 + tid];
+    if (hf) atomicAdd(&g_hist[tid], hf);
+    if (hn) atomicAdd(&g_hist[256 + tid], hn);
+  }
+  NFA_MARK(clk_tile, 4);
+
+  // ---- arrival; the last workgroup of the row runs the tail --------------
+  if (tid == 0) {
+    // every workgroup of the request has read stats_len once all arrived
+    const unsigned int rb = __hip_atomic_fetch_add(
+        &req_cnt[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (rb == (unsigned int)(split.tiles * p.hkv - 1)) {
+      if (do_stats) p.stats_len_l[req] = L;
+      __hip_atomic_store(&req_cnt[b], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  if (!arrive_last(&row_cnt[row], (unsigned int)split.tiles, &s_misc[0])) return;
+
+  // =========================== tail ======================================
+  // (its LDS overlaps the tile stage's private part, no longer used)
+  uint16_t *s_keys = (uint16_t *)(smem + sd.a_keys);
+  uint32_t *s_cbits = (uint32_t *)(smem + sd.a_cbits);
+  const bool dbg = p.dbg_i_f != nullptr;
+  uint32_t *s_dbf = (uint32_t *)(smem + sd.a_dbf);
+  uint32_t *s_dbn = (uint32_t *)(smem + sd.a_dbn);
+  uint64_t *s_dsel = (uint64_t *)(smem + sd.a_dsel);
+  NFA_MARK(clk_tail, 0);
+
+  const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
+  if (p.dbg_bounds != nullptr && kv == 0 && tid == 0) {
+    p.dbg_bounds[b * 3 + 0] = lb.lower;
+    p.dbg_bounds[b * 3 + 1] = lb.upper;
+    p.dbg_bounds[b * 3 + 2] = lb.quota;
+  }
+  // candidate tokens lie in [tok_lo, tok_hi) and exist only when quota > 0
+  const int tok_lo = imax(p.sink_tokens, lb.lower);
+  const int tok_hi = imin(imin(lb.lo, L), lb.upper);
+  const bool any_cand = lb.quota > 0 && tok_hi > tok_lo;
+  const int near_start = geo.near_start;
+
+  // row histograms into LDS, reset for the next launch
+  if (tid < 512) {
+    s_hist[tid] = atomicExch(&g_hist[tid], 0);
+    s_hist[512 + tid] = 0;
+  }
+  uint32_t *s_eqb = (uint32_t *)(smem + sd.a_eqb);
+  for (int w = tid; w < sd.words; w += SB) {
+    s_cbits[w] = 0u;
+    s_eqb[w] = 0u;
+    if (dbg) {
+      s_dbf[w] = 0u;
+      s_dbn[w] = 0u;
+    }
+  }
+  if (tid == 0) {
+    s_misc[3] = 0;  // debug selection list lengths (far, near)
+    s_misc[4] = 0;
+  }
+  if (sd.nseg == 1) stage_keys(g_keys, 0, sd.seg, s_keys);
+  __syncthreads();
+  NFA_MARK(clk_tail, 24);
+  // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
+  if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 8);
+  if (wave_id() == 1) wave_threshold_bin(s_hist + 256, p.k_n, s_tmp + 12);
+  __syncthreads();
+  NFA_MARK(clk_tail, 25);
+  const int hbf = s_tmp[8], hbn = s_tmp[12];
+  if (hbf >= 0 || hbn >= 0) {
+    // refinement: low-byte histograms of the keys in the threshold bins
+    for (int sg = 0; sg < sd.nseg; ++sg) {
+      const int seg_base = sg * sd.seg;
+      if (sd.nseg > 1) {
+        __syncthreads();
+        stage_keys(g_keys, seg_base, sd.seg, s_keys);
+        __syncthreads();
+      }
+      const int n = imin(sd.seg, kt_eff - seg_base);
+      for (int i = tid; i < n; i += SB) {
+        const uint32_t k = s_keys[i];
+        const bool near = seg_base + i >= near_start;
+        const int hb = near ? hbn : hbf;
+        if (k != 0u && (int)(k >> 8) == hb)
+          atomicAdd(&s_hist[(near ? 768 : 512) + (k & 255u)], 1);
+      }
+    }
+    __syncthreads();
+    NFA_MARK(clk_tail, 26);
+    if (wave_id() == 0 && hbf >= 0)
+      wave_threshold_bin(s_hist + 512, p.k_f - s_tmp[9], s_tmp + 16);
+    if (wave_id() == 1 && hbn >= 0)
+      wave_threshold_bin(s_hist + 768, p.k_n - s_tmp[13], s_tmp + 20);
+    __syncthreads();
+  }
+  const PoolThr tf = pool_threshold(p.k_f, s_tmp + 8, s_tmp + 16, s_hist + 512);
+  const PoolThr tn = pool_threshold(p.k_n, s_tmp + 12, s_tmp + 20, s_hist + 768);
+  NFA_MARK(clk_tail, 1);
+
+  // ---- selected pages -> candidate page bitmap ---------------------------
+  auto select_page = [&](int page, uint32_t k, bool near) {
+    const uint32_t bit = 1u << (page & 31);
+    if (any_cand && page * bs < tok_hi && page * bs + bs > tok_lo)
+      atomicOr(&s_cbits[page >> 5], bit);
+    if (dbg) {
+      const int pos = atomicAdd(&s_misc[near ? 4 : 3], 1);
+      s_dsel[(near ? p.k_f : 0) + pos] = ((uint64_t)k << 32) | (uint32_t)page;
+      atomicOr(near ? &s_dbn[page >> 5] : &s_dbf[page >> 5], bit);
+    }
+  };
+  // keys above the threshold are selected outright; keys equal to it too
+  // unless only some of them are, then they go to the tie bitmap
+  for (int sg = 0; sg < sd.nseg; ++sg) {
+    const int seg_base = sg * sd.seg;
+    if (sd.nseg > 1) {
+      __syncthreads();
+      stage_keys(g_keys, seg_base, sd.seg, s_keys);
+      __syncthreads();
+    }
+    const int n = imin(sd.seg, kt_eff - seg_base);
+    for (int i = tid; i < n; i += SB) {
+      const uint32_t k = s_keys[i];
+      if (k == 0u) continue;
+      const int page = seg_base + i;
+      const bool near = page >= near_start;
+      const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
+      const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
+      if (k > T || (k == T && all_eq))
+        select_page(page, k, near);
+      else if (k == T)
+        atomicOr(&s_eqb[page >> 5], 1u << (page & 31));
+    }
+  }
+  __syncthreads();
+  NFA_MARK(clk_tail, 27);
+  if (tie_cut(tf) || tie_cut(tn)) {
+    // tied pages of each pool in page order: the first `need` are selected
+    const int wpt = (sd.words + SB - 1) / SB;
+    const int w0 = tid * wpt;
+    const int w1 = imin(w0 + wpt, sd.words);
+    auto far_mask = [&](int w) -> uint32_t {
+      const int d = near_start - w * 32;
+      return d >= 32 ? 0xFFFFFFFFu : (d <= 0 ? 0u : ((1u << d) - 1u));
+    };
+    int c[2] = {0, 0};
+    for (int w = w0; w < w1; ++w) {
+      const uint32_t bits = s_eqb[w];
+      const uint32_t fm = far_mask(w);
+      c[0] += __popc(bits & fm);
+      c[1] += __popc(bits & ~fm);
+    }
+    int tot2[2];
+    block_scan_n<2, SW>(c, s_tmp + 32, tot2);
+    for (int w = w0; w < w1; ++w) {
+      uint32_t bits = s_eqb[w];
+      const uint32_t fm = far_mask(w);
+      while (bits) {
+        const int bit = __ffs(bits) - 1;
+        bits &= bits - 1u;
+        const bool near = ((fm >> bit) & 1u) == 0u;
+        const int rank = near ? c[1]++ : c[0]++;
+        if (rank < (near ? tn.need : tf.need))
+          select_page(w * 32 + bit, (uint32_t)(near ? tn.T : tf.T), near);
+      }
+    }
+  }
+  NFA_MARK(clk_tail, 2);
+  __syncthreads();
+  if (tid == 0 && any_cand) {
+    // sink and SWA bypass pages (selector:1195-1251)
+    const int spl = p.sink_tokens / bs;
+    const bool byp0_keep = (p.sink_tokens % bs) != 0;
+    bool byp1_keep = (lb.lo % bs != 0) && (lb.lo / bs >= spl);
+    if (p.sink_tokens % bs != 0) byp1_keep = byp1_keep && (lb.lo / bs != spl);
+    const int bp0 = byp0_keep ? spl : -1;
+    const int bp1 = byp1_keep ? lb.lo / bs : -1;
+    if (bp0 >= 0 && bp0 < sd.kstride && bp0 * bs < tok_hi && bp0 * bs + bs > tok_lo)
+      s_cbits[bp0 >> 5] |= 1u << (bp0 & 31);
+    if (bp1 >= 0 && bp1 < sd.kstride && bp1 * bs < tok_hi && bp1 * bs + bs > tok_lo)
+      s_cbits[bp1 >> 5] |= 1u << (bp1 & 31);
+  }
+  __syncthreads();
+  // compaction: sorted unique candidate pages, then their physical pages
+  const int wpt = (sd.words + SB - 1) / SB;
+  const int w0 = tid * wpt;
+  const int w1 = imin(w0 + wpt, sd.words);
+  int *s_pages = (int *)(smem + sd.a_pages);
+  int np_u;
+  {
+    int c1 = 0;
+    for (int w = w0; w < w1; ++w) c1 += __popc(s_cbits[w]);
+    int pos = block_scan_exclusive<SW>(c1, s_tmp, &np_u);
+    for (int w = w0; w < w1; ++w) {
+      uint32_t bits = s_cbits[w];
+      while (bits) {
+        if (pos < sd.np) s_pages[pos] = w * 32 + __ffs(bits) - 1;
+        ++pos;
+        bits &= bits - 1u;
+      }
+    }
+  }
+  NFA_MARK(clk_tail, 3);
+  __syncthreads();
+  np_u = imin(np_u, sd.np);
+  // protected ids; the gather slots of the first SB are fetched now
   int u0, u1, u2, u3;
   protected_intervals(p, L, sd.prot, &u0, &u1, &u2, &u3);
   const int nu = (u1 - u0) + (u3 - u2);
@@ -1794,35 +1599,165 @@ __global__ void __launch_bounds__(SB)
     const int x = tid < (u1 - u0) ? u0 + tid : u2 + (tid - (u1 - u0));
     pre_slot = btr[imin(x / p.page, mb - 1)] * p.page + x % p.page;
   }
-  // dense keys and candidate pages into LDS
+  // physical pages of the candidates
+  int *s_pphys = (int *)(smem + sd.a_pphys);
+  for (int i = tid; i < np_u; i += SB)
+    s_pphys[i] = btr[imin((s_pages[i] * bs) / p.page, mb - 1)];
+  if (tid == 0 && p.dbg_cand_count != nullptr)
+    p.dbg_cand_count[row] = imin(np_u * bs, p.dbg_cand_cap);
+  NFA_MARK(clk_tail, 4);
+  // L1 debug outputs: I_F / I_N (selector:1766-1803 order: valid pages by
+  // (score desc, page asc), then -inf fillers by ascending page)
+  if (dbg) {
+    for (int pool = 0; pool < 2; ++pool) {
+      const int K = pool == 0 ? p.k_f : p.k_n;
+      const int nsel = pool == 0 ? tf.nsel : tn.nsel;
+      const uint64_t *sel = s_dsel + (pool == 0 ? 0 : p.k_f);
+      const uint32_t *bm = pool == 0 ? s_dbf : s_dbn;
+      int32_t *out = (pool == 0 ? p.dbg_i_f + (int64_t)row * p.k_f
+                                : p.dbg_i_n + (int64_t)row * p.k_n);
+      for (int i = tid; i < nsel; i += SB) {
+        const uint64_t ki = sel[i];
+        const uint32_t vi = (uint32_t)(ki >> 32), ti = (uint32_t)ki;
+        int rank = 0;
+        for (int j = 0; j < nsel; ++j) {
+          const uint64_t kj = sel[j];
+          const uint32_t vj = (uint32_t)(kj >> 32), tj = (uint32_t)kj;
+          rank += (vj > vi) || (vj == vi && tj < ti);
+        }
+        out[rank] = (int)ti;
+      }
+      const int nfill = K - nsel;  // uniform
+      if (nfill > 0) {
+        int z = 0;
+        for (int w = w0; w < w1; ++w) z += 32 - __popc(bm[w]);
+        int tz;
+        int r = block_scan_exclusive<SW>(z, s_tmp, &tz);
+        for (int w = w0; w < w1 && r < nfill; ++w) {
+          uint32_t zeros = ~bm[w];
+          while (zeros && r < nfill) {
+            out[nsel + r++] = w * 32 + __ffs(zeros) - 1;
+            zeros &= zeros - 1u;
+          }
+        }
+      }
+    }
+  }
+  if (tid == 0) s_misc[2] = 0;  // middle count
+  __syncthreads();  // the L1 part of the tail LDS is dead from here
+  NFA_MARK(clk_tail, 6);
+
+  // ---- L2 logits (selector:423-516): fp32 dot over the L2 dims in order, --
+  //      the dense slots of the candidate pages, SPT per thread in flight
+  uint16_t *s_dk = (uint16_t *)(smem + sd.a_dk);
+  const int n_dense = np_u * bs;
   {
-    const int n16 = (n_dense + 7) / 8;
-    const uint4 *src = reinterpret_cast<const uint4 *>(g_dk);
-    uint4 *dst = reinterpret_cast<uint4 *>(s_dk);
-    for (int u0 = 0; u0 < n16; u0 += 4 * SB) {
-      uint4 r[4];
+    const float *s_qg = (const float *)(smem + sd.a_qg);
+    // the L2 dims of a slot: its side row (dense, in order) or its K row
+    const bool side = p.l2_keys_l != nullptr;
+    const int nch = side ? (p.fine_dsub % CH == 0 ? p.fine_dsub / CH : 0)
+                         : s_misc[5];  // 16-byte runs, 0: element loads
+    auto choff = [&](int c) { return side ? c * CH : s_fdims[c * CH]; };
+    auto eoff = [&](int d) { return side ? d : s_fdims[d]; };
+    constexpr int SPT = 3;
+    for (int i0 = 0; i0 < n_dense; i0 += SPT * SB) {
+      int tk[SPT];
+      const KV *kr[SPT];
+      bool on[SPT];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int u = u0 + tid + k * SB;
-        r[k] = u < n16 ? src[u] : make_uint4(0u, 0u, 0u, 0u);
+      for (int k = 0; k < SPT; ++k) {
+        const int i = i0 + tid + k * SB;
+        tk[k] = -1;
+        on[k] = false;
+        kr[k] = kpool;
+        if (i < n_dense) {
+          const int pi = i / bs;
+          tk[k] = s_pages[pi] * bs + (i - pi * bs);
+          on[k] = tk[k] >= tok_lo && tk[k] < tok_hi;
+          if (side) {
+            kr[k] = l2_side_row<KV>(p, req, kv, tk[k]);
+          } else {
+            const int phys = safe_page(
+                p, page_phys ? s_pphys[pi] : btr[imin(tk[k] / p.page, mb - 1)]);
+            kr[k] = kpool + kv_offset(p, phys, kv, tk[k] % p.page);
+          }
+        }
+      }
+      float acc[SPT];
+#pragma unroll
+      for (int k = 0; k < SPT; ++k) acc[k] = 0.0f;
+      if (nch > 0 && nch <= 4) {
+        // every run of every slot loaded before any is used
+        uint4 r[SPT][4];
+#pragma unroll
+        for (int k = 0; k < SPT; ++k)
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            r[k][c] = on[k] && c < nch
+                          ? *reinterpret_cast<const uint4 *>(kr[k] + choff(c))
+                          : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int k = 0; k < SPT; ++k)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            if (c >= nch) continue;
+            float x[CH];
+            unpack_chunk<KV>(r[k][c], x);
+#pragma unroll
+            for (int e = 0; e < CH; ++e) {
+              const float prod = x[e] * s_qg[c * CH + e];
+              acc[k] = acc[k] + prod;
+            }
+          }
+      } else {
+#pragma unroll
+        for (int k = 0; k < SPT; ++k) {
+          if (!on[k]) continue;
+          if (nch > 0) {
+            for (int c = 0; c < nch; ++c) {
+              float x[CH];
+              load_chunk<KV>(kr[k] + choff(c), x);
+              for (int e = 0; e < CH; ++e) {
+                const float prod = x[e] * s_qg[c * CH + e];
+                acc[k] = acc[k] + prod;
+              }
+            }
+          } else {
+            for (int d = 0; d < p.fine_dsub; ++d) {
+              const float prod = Elem<KV>::load(kr[k] + eoff(d)) * s_qg[d];
+              acc[k] = acc[k] + prod;
+            }
+          }
+        }
       }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int u = u0 + tid + k * SB;
-        if (u < n16) dst[u] = r[k];
+      for (int k = 0; k < SPT; ++k) {
+        const int i = i0 + tid + k * SB;
+        if (i >= n_dense) continue;
+        uint16_t key = 0;
+        if (on[k]) {
+          const uint16_t bits = bf16_bits(acc[k]);
+          key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
+          if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
+            p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tk[k];
+            p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
+                bits == kNanBits ? kNegInfBits : bits;
+          }
+        } else if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
+          p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = -1;
+        }
+        s_dk[i] = key;
       }
     }
-    for (int k = tid; k < np_u; k += SB) {
-      s_pages[k] = g_pages[k];
-      s_pphys[k] = g_pphys[k];
-    }
-    if (tid == 0) s_misc[2] = 0;  // middle count
   }
   __syncthreads();
-  NFA_MARK(clk_b, 3);
+  NFA_MARK(clk_tail, 9);
 
   // ---- L2 top-quota + hole fill (+ fixed near quota), selector:519-566,
   //      873-940 -------------------------------------------------------------
+  const RegionLists rl{(int *)(smem + sd.a_l0), (int *)(smem + sd.a_l0x),
+                       (int *)(smem + sd.a_l1), (int *)(smem + sd.a_l1x),
+                       (int *)(smem + sd.a_mid), (int *)(smem + sd.a_mslot)};
   const DenseView dv{s_dk, s_pages, s_pphys, btr, n_dense, bs, p.page, mb,
                      page_phys};
   if (lb.quota > 0) {
@@ -1853,13 +1788,13 @@ __global__ void __launch_bounds__(SB)
       r_hi[1] = imax(near_low, near_high);
       r_q[1] = near_quota;
     }
-    int64_t *rclk = p.dbg_clock != nullptr ? p.dbg_clock + clk_b + 8 : nullptr;
+    int64_t *rclk = p.dbg_clock != nullptr ? p.dbg_clock + clk_tail + 16 : nullptr;
     for (int r = 0; r < nreg; ++r)
       l2_region_dense(dv, masked, r_lo[r], r_hi[r], r_q[r], p.sink_tokens, rl,
                       &s_misc[2], s_hist, s_tmp, rclk);
   }
   __syncthreads();
-  NFA_MARK(clk_b, 4);
+  NFA_MARK(clk_tail, 12);
   int mcount = s_misc[2];
   if (mcount > p.k2) mcount = p.k2;
   const int *s_mid = rl.mid;
@@ -1876,7 +1811,7 @@ __global__ void __launch_bounds__(SB)
     const int n = imin(mcount, p.max_vis);
     for (int k = tid; k < n; k += SB) grow[k] = s_mslot[k];
     if (tid == 0) p.vis_lens[b * p.hkv + kv] = n;
-    NFA_MARK(clk_b, 5);
+    NFA_MARK(clk_tail, 13);
     return;
   }
   const int n0 = u1 - u0;  // protected ids of the first interval
@@ -1893,7 +1828,7 @@ __global__ void __launch_bounds__(SB)
       if (dest < p.max_vis) grow[dest] = slot;
     }
     if (tid == 0) p.vis_lens[b * p.hkv + kv] = mcount + nu;
-    NFA_MARK(clk_b, 5);
+    NFA_MARK(clk_tail, 13);
     return;
   }
   auto in_u = [&](int x) { return (x >= u0 && x < u1) || (x >= u2 && x < u3); };
@@ -1934,8 +1869,10 @@ __global__ void __launch_bounds__(SB)
     if (dest < p.max_vis) grow[dest] = slot;
   }
   if (tid == 0) p.vis_lens[b * p.hkv + kv] = nkeep + nu;
-  NFA_MARK(clk_b, 5);
+  NFA_MARK(clk_tail, 13);
 }
+
+
 
 }  // namespace nfa
 
@@ -2006,9 +1943,9 @@ static int select_check(const NfaSelectParams *p) {
     return NFA_EINVAL;
   }
   const SelDims sd = nfa::sel_dims(*p, device_cus());
-  if (sd.lds_a > 64 * 1024 || sd.lds_b > 64 * 1024) {
-    nfa_set_error("nfa_select_layer: geometry needs %d / %d bytes of LDS (> 64 KiB)",
-                  sd.lds_a, sd.lds_b);
+  if (sd.lds > 64 * 1024) {
+    nfa_set_error("nfa_select_layer: geometry needs %d bytes of LDS (> 64 KiB)",
+                  sd.lds);
     return NFA_EINVAL;
   }
   if ((p->hq / p->hkv) * p->head_dim > nfa::kQRawPerThread * nfa::SB) {
@@ -2016,7 +1953,7 @@ static int select_check(const NfaSelectParams *p) {
                   p->hq / p->hkv, p->head_dim);
     return NFA_EINVAL;
   }
-  if (sd.ntiles > 65535 || sd.nchunk > 65535) {
+  if (sd.ntiles > 65535) {
     nfa_set_error("nfa_select_layer: max_blocks %d exceeds the grid limit", p->max_blocks);
     return NFA_EINVAL;
   }
@@ -2056,11 +1993,7 @@ static hipError_t launch_select(const NfaSelectParams &p, hipStream_t stream) {
   const SelDims sd = nfa::sel_dims(p, device_cus());
   const int rows = p.batch * p.hkv;
   hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV>), dim3(rows, sd.ntiles),
-                     dim3(nfa::SB), sd.lds_a, stream, p, sd);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((nfa::nfa_l2_kernel<KV>), dim3(rows, sd.nchunk),
-                     dim3(nfa::SB), sd.lds_b, stream, p, sd);
+                     dim3(nfa::SB), sd.lds, stream, p, sd);
   return hipGetLastError();
 }
 

@@ -35,7 +35,7 @@ def _dims_for(indexer, device, head_dim):
     key = (str(device), head_dim, indexer.subspace, indexer.l2_subspace,
            indexer.cmp_ratio, indexer.enable_subspace)
     if cache is not None and cache[0] == key:
-        return cache[1], cache[2], cache[3]
+        return cache[1], cache[2], cache[3], cache[4]
     cpu = torch.device('cpu')
     full = torch.arange(head_dim, dtype=torch.int64)
     if indexer.enable_subspace:
@@ -49,10 +49,11 @@ def _dims_for(indexer, device, head_dim):
     else:
         fine = indexer._qat_indices(cpu).long()
     l1_key = tuple(l1.tolist())
+    fine_key = tuple(fine.tolist())
     l1 = l1.to(device=device, dtype=torch.int32).contiguous()
     fine = fine.to(device=device, dtype=torch.int32).contiguous()
-    indexer._nfa_hip_dims = (key, l1, fine, l1_key)
-    return l1, fine, l1_key
+    indexer._nfa_hip_dims = (key, l1, fine, l1_key, fine_key)
+    return l1, fine, l1_key, fine_key
 
 
 def _workspace(cache):
@@ -68,9 +69,13 @@ def _no_capture_alloc(what):
                            'graph capture')
 
 
-def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype):
+def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype, fine_key,
+                        head_dim, bs):
     """Persistent per-layer page statistics [max_req, hkv, dsub, max_blocks]
-    in the KV dtype, chunk-major; a new dims set for a layer forces rebuilds."""
+    in the KV dtype, chunk-major, and the L2 side copy [max_req, hkv,
+    max_blocks * bs, fine_dsub] of every visible token's L2 dims (None for a
+    full-width L2 subspace, or when ``cache.nfa_l2_side_copy`` is False); a new
+    dims set for a layer forces rebuilds of both."""
     layer0 = cache.layers[0]
     device = layer0.kv_pool_k.device
     lengths = getattr(cache, '_nfa_page_stats_lengths', None)
@@ -85,20 +90,28 @@ def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype):
     keys_by_layer = getattr(cache, '_nfa_stats_key_by_layer', None)
     if keys_by_layer is None:
         keys_by_layer = cache._nfa_stats_key_by_layer = {}
-    key = (layer_idx, 1, int(dims.numel()), dtype, dims_key)
+    want_side = (len(fine_key) < head_dim
+                 and getattr(cache, 'nfa_l2_side_copy', True))
+    key = (layer_idx, 1, int(dims.numel()), dtype, dims_key,
+           (fine_key, bs) if want_side else None)
     bufs = store.get(key)
     if bufs is None:
         _no_capture_alloc('page statistics')
         numel = (cache.max_requests * layer0.num_kv_heads * int(dims.numel())
                  * cache.max_blocks)
-        bufs = tuple(torch.empty(numel, dtype=dtype, device=device)
-                     for _ in range(3))
-        store[key] = bufs
+        stats = tuple(torch.empty(numel, dtype=dtype, device=device)
+                      for _ in range(3))
+        side = None
+        if want_side:
+            side = torch.empty(cache.max_requests * layer0.num_kv_heads
+                               * cache.max_blocks * bs * len(fine_key),
+                               dtype=dtype, device=device)
+        bufs = store[key] = (stats, side)
     if keys_by_layer.get(layer_idx) != key:
         _no_capture_alloc('page statistics')
         lengths[layer_idx].zero_()
         keys_by_layer[layer_idx] = key
-    return bufs, lengths[layer_idx]
+    return bufs[0], bufs[1], lengths[layer_idx]
 
 
 def _check_decode_write(decode_write, b, hkv, device):
@@ -183,7 +196,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
 
     bs = int(indexer.args.tia_block_size)
     geo = cache.geometry
-    l1_dims, fine_dims, l1_key = _dims_for(indexer, device, head_dim)
+    l1_dims, fine_dims, l1_key, fine_key = _dims_for(indexer, device, head_dim)
     if l1_dims.numel() not in (32, 64, 128):
         raise FallbackRequired(f'{l1_dims.numel()} L1 dims are not supported')
     nb_near = max(0, int(indexer.nt_near_pages))
@@ -206,8 +219,8 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
         raise ValueError('selection outputs must be contiguous int32')
 
     kv_dtype = layer0.kv_pool_k.dtype
-    (smin, smax, ssum), stats_len = _page_stats_buffers(
-        cache, layer_idx, l1_dims, l1_key, kv_dtype)
+    (smin, smax, ssum), l2_side, stats_len = _page_stats_buffers(
+        cache, layer_idx, l1_dims, l1_key, kv_dtype, fine_key, head_dim, bs)
     layer = cache.layers[layer_idx]
 
     p = nat.NfaSelectParams()
@@ -259,6 +272,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
     p.stat_min_l, p.stat_max_l, p.stat_sum_l = (
         smin.data_ptr(), smax.data_ptr(), ssum.data_ptr())
     p.stats_len_l = stats_len.data_ptr()
+    p.l2_keys_l = l2_side.data_ptr() if l2_side is not None else None
     p.gather = gather_out.data_ptr()
     p.vis_lens = vis_out.data_ptr()
     need = lib.nfa_select_workspace_bytes(ctypes.byref(p))
