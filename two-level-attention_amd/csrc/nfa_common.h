@@ -243,17 +243,33 @@ __device__ __forceinline__ int wave_id() {
 }
 
 // Exclusive prefix sum of an int over a block of WAVES waves; two barriers.
+// Wave-wide inclusive prefix sum in lane order with DPP moves (VALU, no LDS
+// round trips): shifts of 1, 2, 4, 8 within each 16-lane row, then the row
+// totals broadcast upward (row_bcast:15 into rows 1 and 3, row_bcast:31 into
+// rows 2 and 3).
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return x;
+}
+
+// Bitwise OR over each group of four consecutive lanes (DPP quad_perm).
+__device__ __forceinline__ uint32_t quad_or(uint32_t x) {
+  x |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);
+  x |= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);
+  return x;
+}
+
 template <int WAVES = NFA_WAVES>
 __device__ __forceinline__ int block_scan_exclusive(int v, int *scratch,
                                                     int *total) {
   const int lane = lane_id();
   const int w = wave_id();
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
+  const int x = wave_incl_sum(v);
   if (lane == 63) scratch[w] = x;
   __syncthreads();
   int before = 0, sum = 0;
@@ -278,15 +294,7 @@ __device__ __forceinline__ void block_scan_n(int (&v)[N], int *scratch,
   const int w = wave_id();
   int x[N];
 #pragma unroll
-  for (int k = 0; k < N; ++k) x[k] = v[k];
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-#pragma unroll
-    for (int k = 0; k < N; ++k) {
-      const int y = __shfl_up(x[k], off, 64);
-      if (lane >= off) x[k] += y;
-    }
-  }
+  for (int k = 0; k < N; ++k) x[k] = wave_incl_sum(v[k]);
   if (lane == 63) {
 #pragma unroll
     for (int k = 0; k < N; ++k) scratch[w * N + k] = x[k];
@@ -318,13 +326,9 @@ __device__ __forceinline__ void wave_threshold_bin(const int *hist, int K,
   const int h0 = hist[4 * lane + 0], h1 = hist[4 * lane + 1];
   const int h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
   const int s = h0 + h1 + h2 + h3;
-  int x = s;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_down(x, off, 64);
-    if (lane + off < 64) x += y;
-  }
-  const int total = __shfl(x, 0, 64);
+  const int pre = wave_incl_sum(s);
+  const int total = __builtin_amdgcn_readlane(pre, 63);
+  const int x = total - pre + s;  // lanes lane..63
   if (total <= K || K <= 0) {
     if (lane == 0) {
       out[0] = -1;
@@ -344,6 +348,13 @@ __device__ __forceinline__ void wave_threshold_bin(const int *hist, int K,
     above += hb[i];
   }
   if (lane == 0) out[2] = total;
+}
+
+// Wave-wide exclusive prefix sum of v in lane order, and the wave total.
+__device__ __forceinline__ int wave_scan_excl(int v, int *total) {
+  const int x = wave_incl_sum(v);
+  *total = __builtin_amdgcn_readlane(x, 63);
+  return x - v;
 }
 
 // Lower bound: first index with a[idx] >= x.

@@ -70,7 +70,7 @@ struct SelDims {
   int lds;        // LDS bytes per workgroup
   // LDS: a common part, then the tile part, or the tail: its candidate pages,
   // then its L1 part or (later) its L2 part
-  int a_hist, a_tmp, a_misc, a_qf, a_qs, a_qg, a_fdims;
+  int a_hist, a_tmp, a_misc, a_clk, a_qf, a_qs, a_qg, a_fdims;
   int a_dims, a_last, a_tphys, a_stage, a_hs, a_st;    // tile
   int a_pages, a_pphys;                                // tail
   int a_keys, a_cbits, a_eqb, a_dbf, a_dbn, a_dsel;    // tail, L1
@@ -138,6 +138,7 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   s.a_hist = o;  o += align16(4 * 4 * 256);
   s.a_tmp = o;   o += align16(4 * 128);
   s.a_misc = o;  o += align16(4 * 32);
+  s.a_clk = o;   o += 8 * 64;  // debug timeline: tile marks, tail marks
   s.a_qf = o;    o += align16(4 * group * p.dsub);
   s.a_qs = o;    o += align16(4 * group * 2 * p.dsub);  // min(q,0) | max(q,0)
   s.a_qg = o;    o += align16(4 * p.fine_dsub);          // grouped L2 query
@@ -1048,13 +1049,23 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
 // ---------------------------------------------------------------------------
 
 // Phase timestamp (debug timeline): every wave of the workgroup has reached
-// it (memory accesses in flight stay in flight), then thread 0 stores the
-// wall clock.  Uniform condition.
-#define NFA_MARK(slot_base, k)                                        \
+// it (memory accesses in flight stay in flight), then thread 0 keeps the
+// wall clock in LDS slot k of the tile (0) or tail (32) marks; NFA_FLUSH
+// copies them out at the end of the stage, so no global store of the
+// timeline sits inside a measured phase.  Uniform conditions.
+#define NFA_MARK(part, k)                                             \
   do {                                                                \
     if (p.dbg_clock != nullptr) {                                     \
       lds_barrier();                                                  \
-      if (threadIdx.x == 0) p.dbg_clock[(slot_base) + (k)] = wall_clock64(); \
+      if (threadIdx.x == 0) s_clk[(part) + (k)] = wall_clock64();     \
+    }                                                                 \
+  } while (0)
+#define NFA_FLUSH(part, slot_base)                                    \
+  do {                                                                \
+    if (p.dbg_clock != nullptr) {                                     \
+      lds_barrier();                                                  \
+      if (threadIdx.x < 32 && s_clk[(part) + threadIdx.x] != 0)       \
+        p.dbg_clock[(slot_base) + threadIdx.x] = s_clk[(part) + threadIdx.x]; \
     }                                                                 \
   } while (0)
 
@@ -1097,7 +1108,9 @@ __global__ void __launch_bounds__(SB)
 
   const int64_t clk_tile = ((int64_t)row * (sd.clk_tiles + 1) + tile) * 32;
   const int64_t clk_tail = ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32;
-  NFA_MARK(clk_tile, 0);
+  int64_t *s_clk = (int64_t *)(smem + sd.a_clk);
+  if (p.dbg_clock != nullptr && tid < 64) s_clk[tid] = 0;
+  NFA_MARK(0, 0);
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
   unsigned int *req_cnt = (unsigned int *)(ws + sd.w_reqcnt);
@@ -1157,7 +1170,7 @@ __global__ void __launch_bounds__(SB)
   }
   if (tid < 512) s_hist[tid] = 0;
   lds_barrier();
-  NFA_MARK(clk_tile, 1);
+  NFA_MARK(0, 1);
 
   // scaled, bf16-rounded query rows of this kv group (selector:943-963), and
   // their negative and positive parts
@@ -1187,7 +1200,7 @@ __global__ void __launch_bounds__(SB)
     if (lane_id() == 0) s_misc[5] = all ? p.fine_dsub / CH : 0;
   }
   lds_barrier();  // the query rows; the raw rows' LDS is free again
-  NFA_MARK(clk_tile, 2);
+  NFA_MARK(0, 2);
 
   // ---- second round trip: statistics (asynchronous), request state -------
   // (after every LDS read of the prologue: a read behind an asynchronous
@@ -1315,7 +1328,7 @@ __global__ void __launch_bounds__(SB)
     }
   }
   lds_barrier();
-  NFA_MARK(clk_tile, 3);
+  NFA_MARK(0, 3);
 
   // ---- L1 scores: four waves per 64 pages, two query heads per thread -----
   const RowGeo geo = row_geo(p, L, skip_far, skip_near);
@@ -1391,7 +1404,8 @@ __global__ void __launch_bounds__(SB)
     if (hf) atomicAdd(&g_hist[tid], hf);
     if (hn) atomicAdd(&g_hist[256 + tid], hn);
   }
-  NFA_MARK(clk_tile, 4);
+  NFA_MARK(0, 4);
+  NFA_FLUSH(0, clk_tile);
 
   // ---- arrival; the last workgroup of the row runs the tail --------------
   if (tid == 0) {
@@ -1414,7 +1428,7 @@ __global__ void __launch_bounds__(SB)
   uint32_t *s_dbf = (uint32_t *)(smem + sd.a_dbf);
   uint32_t *s_dbn = (uint32_t *)(smem + sd.a_dbn);
   uint64_t *s_dsel = (uint64_t *)(smem + sd.a_dsel);
-  NFA_MARK(clk_tail, 0);
+  NFA_MARK(32, 0);
 
   const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
   if (p.dbg_bounds != nullptr && kv == 0 && tid == 0) {
@@ -1448,12 +1462,12 @@ __global__ void __launch_bounds__(SB)
   }
   if (sd.nseg == 1) stage_keys(g_keys, 0, sd.seg, s_keys);
   __syncthreads();
-  NFA_MARK(clk_tail, 24);
+  NFA_MARK(32, 24);
   // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
   if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 8);
   if (wave_id() == 1) wave_threshold_bin(s_hist + 256, p.k_n, s_tmp + 12);
   __syncthreads();
-  NFA_MARK(clk_tail, 25);
+  NFA_MARK(32, 25);
   const int hbf = s_tmp[8], hbn = s_tmp[12];
   if (hbf >= 0 || hbn >= 0) {
     // refinement: low-byte histograms of the keys in the threshold bins
@@ -1465,16 +1479,23 @@ __global__ void __launch_bounds__(SB)
         __syncthreads();
       }
       const int n = imin(sd.seg, kt_eff - seg_base);
-      for (int i = tid; i < n; i += SB) {
-        const uint32_t k = s_keys[i];
-        const bool near = seg_base + i >= near_start;
-        const int hb = near ? hbn : hbf;
-        if (k != 0u && (int)(k >> 8) == hb)
-          atomicAdd(&s_hist[(near ? 768 : 512) + (k & 255u)], 1);
+      // eight keys per thread from one 16-byte read
+      for (int v = tid; v < (n + 7) / 8; v += SB) {
+        const uint4 w = reinterpret_cast<const uint4 *>(s_keys)[v];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t k = (ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+          const int i = v * 8 + j;
+          const bool near = seg_base + i >= near_start;
+          const int hb = near ? hbn : hbf;
+          if (i < n && k != 0u && (int)(k >> 8) == hb)
+            atomicAdd(&s_hist[(near ? 768 : 512) + (k & 255u)], 1);
+        }
       }
     }
     __syncthreads();
-    NFA_MARK(clk_tail, 26);
+    NFA_MARK(32, 26);
     if (wave_id() == 0 && hbf >= 0)
       wave_threshold_bin(s_hist + 512, p.k_f - s_tmp[9], s_tmp + 16);
     if (wave_id() == 1 && hbn >= 0)
@@ -1483,7 +1504,7 @@ __global__ void __launch_bounds__(SB)
   }
   const PoolThr tf = pool_threshold(p.k_f, s_tmp + 8, s_tmp + 16, s_hist + 512);
   const PoolThr tn = pool_threshold(p.k_n, s_tmp + 12, s_tmp + 20, s_hist + 768);
-  NFA_MARK(clk_tail, 1);
+  NFA_MARK(32, 1);
 
   // ---- selected pages -> candidate page bitmap ---------------------------
   auto select_page = [&](int page, uint32_t k, bool near) {
@@ -1498,87 +1519,126 @@ __global__ void __launch_bounds__(SB)
   };
   // keys above the threshold are selected outright; keys equal to it too
   // unless only some of them are, then they go to the tie bitmap
+  auto in_cand = [&](int page) {
+    return any_cand && page * bs < tok_hi && page * bs + bs > tok_lo;
+  };
   for (int sg = 0; sg < sd.nseg; ++sg) {
-    const int seg_base = sg * sd.seg;
+    const int seg_base = sg * sd.seg;  // a multiple of 32
     if (sd.nseg > 1) {
       __syncthreads();
       stage_keys(g_keys, seg_base, sd.seg, s_keys);
       __syncthreads();
     }
     const int n = imin(sd.seg, kt_eff - seg_base);
-    for (int i = tid; i < n; i += SB) {
-      const uint32_t k = s_keys[i];
-      if (k == 0u) continue;
-      const int page = seg_base + i;
-      const bool near = page >= near_start;
-      const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
-      const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
-      if (k > T || (k == T && all_eq))
-        select_page(page, k, near);
-      else if (k == T)
-        atomicOr(&s_eqb[page >> 5], 1u << (page & 31));
-    }
-  }
-  __syncthreads();
-  NFA_MARK(clk_tail, 27);
-  if (tie_cut(tf) || tie_cut(tn)) {
-    // tied pages of each pool in page order: the first `need` are selected
-    const int wpt = (sd.words + SB - 1) / SB;
-    const int w0 = tid * wpt;
-    const int w1 = imin(w0 + wpt, sd.words);
-    auto far_mask = [&](int w) -> uint32_t {
-      const int d = near_start - w * 32;
-      return d >= 32 ? 0xFFFFFFFFu : (d <= 0 ? 0u : ((1u << d) - 1u));
-    };
-    int c[2] = {0, 0};
-    for (int w = w0; w < w1; ++w) {
-      const uint32_t bits = s_eqb[w];
-      const uint32_t fm = far_mask(w);
-      c[0] += __popc(bits & fm);
-      c[1] += __popc(bits & ~fm);
-    }
-    int tot2[2];
-    block_scan_n<2, SW>(c, s_tmp + 32, tot2);
-    for (int w = w0; w < w1; ++w) {
-      uint32_t bits = s_eqb[w];
-      const uint32_t fm = far_mask(w);
-      while (bits) {
-        const int bit = __ffs(bits) - 1;
-        bits &= bits - 1u;
-        const bool near = ((fm >> bit) & 1u) == 0u;
-        const int rank = near ? c[1]++ : c[0]++;
-        if (rank < (near ? tn.need : tf.need))
-          select_page(w * 32 + bit, (uint32_t)(near ? tn.T : tf.T), near);
+    if (!dbg) {
+      // eight pages per thread from one 16-byte read; four lanes make one
+      // 32-page bitmap word
+      const int n8 = (n + 7) / 8;
+      for (int v0 = 0; v0 < n8; v0 += SB) {  // uniform trip count
+        const int v = v0 + tid;
+        uint32_t sel = 0u, tie = 0u;
+        if (v < n8) {
+          const uint4 w = reinterpret_cast<const uint4 *>(s_keys)[v];
+          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint32_t k = (ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+            const int i = v * 8 + j;
+            const int page = seg_base + i;
+            const bool near = page >= near_start;
+            const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
+            const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
+            if (i < n && k != 0u) {
+              if (k > T || (k == T && all_eq)) {
+                if (in_cand(page)) sel |= 1u << j;
+              } else if (k == T) {
+                tie |= 1u << j;
+              }
+            }
+          }
+        }
+        const int sh = 8 * (tid & 3);
+        sel <<= sh;
+        tie <<= sh;
+        sel = quad_or(sel);
+        tie = quad_or(tie);
+        if ((tid & 3) == 0 && v < n8) {
+          s_cbits[(seg_base >> 5) + (v >> 2)] = sel;
+          s_eqb[(seg_base >> 5) + (v >> 2)] = tie;
+        }
+      }
+    } else {
+      for (int i = tid; i < n; i += SB) {
+        const uint32_t k = s_keys[i];
+        if (k == 0u) continue;
+        const int page = seg_base + i;
+        const bool near = page >= near_start;
+        const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
+        const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
+        if (k > T || (k == T && all_eq))
+          select_page(page, k, near);
+        else if (k == T)
+          atomicOr(&s_eqb[page >> 5], 1u << (page & 31));
       }
     }
   }
-  NFA_MARK(clk_tail, 2);
   __syncthreads();
-  if (tid == 0 && any_cand) {
-    // sink and SWA bypass pages (selector:1195-1251)
-    const int spl = p.sink_tokens / bs;
-    const bool byp0_keep = (p.sink_tokens % bs) != 0;
-    bool byp1_keep = (lb.lo % bs != 0) && (lb.lo / bs >= spl);
-    if (p.sink_tokens % bs != 0) byp1_keep = byp1_keep && (lb.lo / bs != spl);
-    const int bp0 = byp0_keep ? spl : -1;
-    const int bp1 = byp1_keep ? lb.lo / bs : -1;
-    if (bp0 >= 0 && bp0 < sd.kstride && bp0 * bs < tok_hi && bp0 * bs + bs > tok_lo)
-      s_cbits[bp0 >> 5] |= 1u << (bp0 & 31);
-    if (bp1 >= 0 && bp1 < sd.kstride && bp1 * bs < tok_hi && bp1 * bs + bs > tok_lo)
-      s_cbits[bp1 >> 5] |= 1u << (bp1 & 31);
-  }
-  __syncthreads();
-  // compaction: sorted unique candidate pages, then their physical pages
-  const int wpt = (sd.words + SB - 1) / SB;
-  const int w0 = tid * wpt;
-  const int w1 = imin(w0 + wpt, sd.words);
+  NFA_MARK(32, 27);
+  // wave 0: tied pages, bypass pages, compaction (wave-level scans only)
   int *s_pages = (int *)(smem + sd.a_pages);
-  int np_u;
-  {
+  if (wave_id() == 0) {
+    const int lane = lane_id();
+    const int wl = (sd.words + 63) / 64;
+    const int wa = imin(lane * wl, sd.words);
+    const int wb = imin(wa + wl, sd.words);
+    if (tie_cut(tf) || tie_cut(tn)) {
+      // tied pages of each pool in page order: the first `need` are selected
+      auto far_mask = [&](int w) -> uint32_t {
+        const int d = near_start - w * 32;
+        return d >= 32 ? 0xFFFFFFFFu : (d <= 0 ? 0u : ((1u << d) - 1u));
+      };
+      int cf = 0, cn = 0;
+      for (int w = wa; w < wb; ++w) {
+        const uint32_t bits = s_eqb[w];
+        const uint32_t fm = far_mask(w);
+        cf += __popc(bits & fm);
+        cn += __popc(bits & ~fm);
+      }
+      int tot;
+      int rf = wave_scan_excl(cf, &tot);
+      int rn = wave_scan_excl(cn, &tot);
+      for (int w = wa; w < wb; ++w) {
+        uint32_t bits = s_eqb[w];
+        const uint32_t fm = far_mask(w);
+        while (bits) {
+          const int bit = __ffs(bits) - 1;
+          bits &= bits - 1u;
+          const bool near = ((fm >> bit) & 1u) == 0u;
+          const int rank = near ? rn++ : rf++;
+          if (rank < (near ? tn.need : tf.need))
+            select_page(w * 32 + bit, (uint32_t)(near ? tn.T : tf.T), near);
+        }
+      }
+    }
+    if (lane == 0 && any_cand) {
+      // sink and SWA bypass pages (selector:1195-1251)
+      const int spl = p.sink_tokens / bs;
+      const bool byp0_keep = (p.sink_tokens % bs) != 0;
+      bool byp1_keep = (lb.lo % bs != 0) && (lb.lo / bs >= spl);
+      if (p.sink_tokens % bs != 0) byp1_keep = byp1_keep && (lb.lo / bs != spl);
+      const int bp0 = byp0_keep ? spl : -1;
+      const int bp1 = byp1_keep ? lb.lo / bs : -1;
+      if (bp0 >= 0 && bp0 < sd.kstride && in_cand(bp0))
+        s_cbits[bp0 >> 5] |= 1u << (bp0 & 31);
+      if (bp1 >= 0 && bp1 < sd.kstride && in_cand(bp1))
+        s_cbits[bp1 >> 5] |= 1u << (bp1 & 31);
+    }
+    // compaction: sorted unique candidate pages
     int c1 = 0;
-    for (int w = w0; w < w1; ++w) c1 += __popc(s_cbits[w]);
-    int pos = block_scan_exclusive<SW>(c1, s_tmp, &np_u);
-    for (int w = w0; w < w1; ++w) {
+    for (int w = wa; w < wb; ++w) c1 += __popc(s_cbits[w]);
+    int total;
+    int pos = wave_scan_excl(c1, &total);
+    for (int w = wa; w < wb; ++w) {
       uint32_t bits = s_cbits[w];
       while (bits) {
         if (pos < sd.np) s_pages[pos] = w * 32 + __ffs(bits) - 1;
@@ -1586,8 +1646,16 @@ __global__ void __launch_bounds__(SB)
         bits &= bits - 1u;
       }
     }
+    if (lane == 0) s_misc[6] = total;
   }
-  NFA_MARK(clk_tail, 3);
+  NFA_MARK(32, 2);
+  __syncthreads();
+  int np_u = s_misc[6];
+  // word ranges of the debug outputs
+  const int wpt = (sd.words + SB - 1) / SB;
+  const int w0 = tid * wpt;
+  const int w1 = imin(w0 + wpt, sd.words);
+  NFA_MARK(32, 3);
   __syncthreads();
   np_u = imin(np_u, sd.np);
   // protected ids; the gather slots of the first SB are fetched now
@@ -1605,7 +1673,7 @@ __global__ void __launch_bounds__(SB)
     s_pphys[i] = btr[imin((s_pages[i] * bs) / p.page, mb - 1)];
   if (tid == 0 && p.dbg_cand_count != nullptr)
     p.dbg_cand_count[row] = imin(np_u * bs, p.dbg_cand_cap);
-  NFA_MARK(clk_tail, 4);
+  NFA_MARK(32, 4);
   // L1 debug outputs: I_F / I_N (selector:1766-1803 order: valid pages by
   // (score desc, page asc), then -inf fillers by ascending page)
   if (dbg) {
@@ -1645,7 +1713,7 @@ __global__ void __launch_bounds__(SB)
   }
   if (tid == 0) s_misc[2] = 0;  // middle count
   __syncthreads();  // the L1 part of the tail LDS is dead from here
-  NFA_MARK(clk_tail, 6);
+  NFA_MARK(32, 6);
 
   // ---- L2 logits (selector:423-516): fp32 dot over the L2 dims in order, --
   //      the dense slots of the candidate pages, SPT per thread in flight
@@ -1751,7 +1819,7 @@ __global__ void __launch_bounds__(SB)
     }
   }
   __syncthreads();
-  NFA_MARK(clk_tail, 9);
+  NFA_MARK(32, 9);
 
   // ---- L2 top-quota + hole fill (+ fixed near quota), selector:519-566,
   //      873-940 -------------------------------------------------------------
@@ -1788,13 +1856,13 @@ __global__ void __launch_bounds__(SB)
       r_hi[1] = imax(near_low, near_high);
       r_q[1] = near_quota;
     }
-    int64_t *rclk = p.dbg_clock != nullptr ? p.dbg_clock + clk_tail + 16 : nullptr;
+    int64_t *rclk = p.dbg_clock != nullptr ? s_clk + 32 + 16 : nullptr;
     for (int r = 0; r < nreg; ++r)
       l2_region_dense(dv, masked, r_lo[r], r_hi[r], r_q[r], p.sink_tokens, rl,
                       &s_misc[2], s_hist, s_tmp, rclk);
   }
   __syncthreads();
-  NFA_MARK(clk_tail, 12);
+  NFA_MARK(32, 12);
   int mcount = s_misc[2];
   if (mcount > p.k2) mcount = p.k2;
   const int *s_mid = rl.mid;
@@ -1811,7 +1879,8 @@ __global__ void __launch_bounds__(SB)
     const int n = imin(mcount, p.max_vis);
     for (int k = tid; k < n; k += SB) grow[k] = s_mslot[k];
     if (tid == 0) p.vis_lens[b * p.hkv + kv] = n;
-    NFA_MARK(clk_tail, 13);
+    NFA_MARK(32, 13);
+    NFA_FLUSH(32, clk_tail);
     return;
   }
   const int n0 = u1 - u0;  // protected ids of the first interval
@@ -1828,7 +1897,8 @@ __global__ void __launch_bounds__(SB)
       if (dest < p.max_vis) grow[dest] = slot;
     }
     if (tid == 0) p.vis_lens[b * p.hkv + kv] = mcount + nu;
-    NFA_MARK(clk_tail, 13);
+    NFA_MARK(32, 13);
+    NFA_FLUSH(32, clk_tail);
     return;
   }
   auto in_u = [&](int x) { return (x >= u0 && x < u1) || (x >= u2 && x < u3); };
@@ -1869,7 +1939,8 @@ __global__ void __launch_bounds__(SB)
     if (dest < p.max_vis) grow[dest] = slot;
   }
   if (tid == 0) p.vis_lens[b * p.hkv + kv] = nkeep + nu;
-  NFA_MARK(clk_tail, 13);
+  NFA_MARK(32, 13);
+  NFA_FLUSH(32, clk_tail);
 }
 
 
