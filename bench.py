@@ -294,7 +294,7 @@ def selector_timeline(torch, w, steps, plan):
                  ('  L1 thr: hist+keys load', 0, 24), ('  L1 thr: coarse bins', 24, 25),
                  ('  L1 thr: refine pass', 25, 26), ('  L1 thr: fine bins', 26, 1),
                  ('tail selection pass', 1, 2),
-                 ('  sel: main pass', 1, 27), ('  sel: ties+bypass+compaction', 27, 2),
+                 
                  ('tail bitmap compaction', 2, 3), ('tail candidate pages', 3, 4),
                  ('tail L1 end', 4, 6), ('tail L2 logits', 6, 9),
                  ('tail L2 top-k', 9, 12), ('tail union', 12, 13),

@@ -267,20 +267,17 @@ __device__ __forceinline__ uint32_t quad_or(uint32_t x) {
 template <int WAVES = NFA_WAVES>
 __device__ __forceinline__ int block_scan_exclusive(int v, int *scratch,
                                                     int *total) {
+  static_assert(WAVES <= 64, "one wave scans the wave totals");
   const int lane = lane_id();
   const int w = wave_id();
   const int x = wave_incl_sum(v);
   if (lane == 63) scratch[w] = x;
   __syncthreads();
-  int before = 0, sum = 0;
-#pragma unroll
-  for (int i = 0; i < WAVES; ++i) {
-    const int c = scratch[i];
-    if (i < w) before += c;
-    sum += c;
-  }
+  // every wave scans the wave totals itself (DPP), then picks its own
+  const int t = wave_incl_sum(lane < WAVES ? scratch[lane] : 0);
+  const int before = w > 0 ? __builtin_amdgcn_readlane(t, w - 1) : 0;
+  *total = __builtin_amdgcn_readlane(t, WAVES - 1);
   __syncthreads();
-  *total = sum;
   return before + x - v;
 }
 
@@ -292,6 +289,7 @@ __device__ __forceinline__ void block_scan_n(int (&v)[N], int *scratch,
                                              int (&total)[N]) {
   const int lane = lane_id();
   const int w = wave_id();
+  static_assert(WAVES <= 64, "one wave scans the wave totals");
   int x[N];
 #pragma unroll
   for (int k = 0; k < N; ++k) x[k] = wave_incl_sum(v[k]);
@@ -302,14 +300,9 @@ __device__ __forceinline__ void block_scan_n(int (&v)[N], int *scratch,
   __syncthreads();
 #pragma unroll
   for (int k = 0; k < N; ++k) {
-    int before = 0, sum = 0;
-#pragma unroll
-    for (int i = 0; i < WAVES; ++i) {
-      const int c = scratch[i * N + k];
-      if (i < w) before += c;
-      sum += c;
-    }
-    total[k] = sum;
+    const int t = wave_incl_sum(lane < WAVES ? scratch[lane * N + k] : 0);
+    const int before = w > 0 ? __builtin_amdgcn_readlane(t, w - 1) : 0;
+    total[k] = __builtin_amdgcn_readlane(t, WAVES - 1);
     v[k] = before + x[k] - v[k];
   }
   __syncthreads();

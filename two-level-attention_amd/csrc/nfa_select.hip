@@ -1423,7 +1423,6 @@ __global__ void __launch_bounds__(SB)
   // =========================== tail ======================================
   // (its LDS overlaps the tile stage's private part, no longer used)
   uint16_t *s_keys = (uint16_t *)(smem + sd.a_keys);
-  uint32_t *s_cbits = (uint32_t *)(smem + sd.a_cbits);
   const bool dbg = p.dbg_i_f != nullptr;
   uint32_t *s_dbf = (uint32_t *)(smem + sd.a_dbf);
   uint32_t *s_dbn = (uint32_t *)(smem + sd.a_dbn);
@@ -1447,11 +1446,8 @@ __global__ void __launch_bounds__(SB)
     s_hist[tid] = atomicExch(&g_hist[tid], 0);
     s_hist[512 + tid] = 0;
   }
-  uint32_t *s_eqb = (uint32_t *)(smem + sd.a_eqb);
-  for (int w = tid; w < sd.words; w += SB) {
-    s_cbits[w] = 0u;
-    s_eqb[w] = 0u;
-    if (dbg) {
+  if (dbg) {
+    for (int w = tid; w < sd.words; w += SB) {
       s_dbf[w] = 0u;
       s_dbn[w] = 0u;
     }
@@ -1506,151 +1502,100 @@ __global__ void __launch_bounds__(SB)
   const PoolThr tn = pool_threshold(p.k_n, s_tmp + 12, s_tmp + 20, s_hist + 768);
   NFA_MARK(32, 1);
 
-  // ---- selected pages -> candidate page bitmap ---------------------------
-  auto select_page = [&](int page, uint32_t k, bool near) {
-    const uint32_t bit = 1u << (page & 31);
-    if (any_cand && page * bs < tok_hi && page * bs + bs > tok_lo)
-      atomicOr(&s_cbits[page >> 5], bit);
-    if (dbg) {
-      const int pos = atomicAdd(&s_misc[near ? 4 : 3], 1);
-      s_dsel[(near ? p.k_f : 0) + pos] = ((uint64_t)k << 32) | (uint32_t)page;
-      atomicOr(near ? &s_dbn[page >> 5] : &s_dbf[page >> 5], bit);
-    }
+  // ---- selected pages -> sorted candidate page list ----------------------
+  // L1 selection of the debug outputs: per-pool lists and page bitmaps
+  auto dbg_select = [&](int page, uint32_t k, bool near) {
+    const int pos = atomicAdd(&s_misc[near ? 4 : 3], 1);
+    s_dsel[(near ? p.k_f : 0) + pos] = ((uint64_t)k << 32) | (uint32_t)page;
+    atomicOr(near ? &s_dbn[page >> 5] : &s_dbf[page >> 5], 1u << (page & 31));
   };
-  // keys above the threshold are selected outright; keys equal to it too
-  // unless only some of them are, then they go to the tie bitmap
   auto in_cand = [&](int page) {
     return any_cand && page * bs < tok_hi && page * bs + bs > tok_lo;
   };
+  // sink and SWA bypass pages (selector:1195-1251)
+  int bp0 = -1, bp1 = -1;
+  {
+    const int spl = p.sink_tokens / bs;
+    const bool byp0_keep = (p.sink_tokens % bs) != 0;
+    bool byp1_keep = (lb.lo % bs != 0) && (lb.lo / bs >= spl);
+    if (p.sink_tokens % bs != 0) byp1_keep = byp1_keep && (lb.lo / bs != spl);
+    if (byp0_keep && in_cand(spl)) bp0 = spl;
+    if (byp1_keep && in_cand(lb.lo / bs)) bp1 = lb.lo / bs;
+  }
+  // Eight pages per thread, in page order over the threads: keys above the
+  // threshold are selected, keys equal to it too unless only some of them
+  // are (then the first `need` tied pages of the pool in page order, ranked
+  // by a block scan); a second scan places the candidates, so the list is
+  // sorted and free of duplicates by construction.
+  int *s_pages = (int *)(smem + sd.a_pages);
+  int np_u = 0;          // candidates so far (uniform)
+  int tfb = 0, tnb = 0;  // tied far / near pages so far (uniform)
   for (int sg = 0; sg < sd.nseg; ++sg) {
-    const int seg_base = sg * sd.seg;  // a multiple of 32
+    const int seg_base = sg * sd.seg;
     if (sd.nseg > 1) {
       __syncthreads();
       stage_keys(g_keys, seg_base, sd.seg, s_keys);
       __syncthreads();
     }
     const int n = imin(sd.seg, kt_eff - seg_base);
-    if (!dbg) {
-      // eight pages per thread from one 16-byte read; four lanes make one
-      // 32-page bitmap word
-      const int n8 = (n + 7) / 8;
-      for (int v0 = 0; v0 < n8; v0 += SB) {  // uniform trip count
-        const int v = v0 + tid;
-        uint32_t sel = 0u, tie = 0u;
-        if (v < n8) {
-          const uint4 w = reinterpret_cast<const uint4 *>(s_keys)[v];
-          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const uint32_t k = (ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-            const int i = v * 8 + j;
-            const int page = seg_base + i;
-            const bool near = page >= near_start;
-            const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
-            const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
-            if (i < n && k != 0u) {
-              if (k > T || (k == T && all_eq)) {
-                if (in_cand(page)) sel |= 1u << j;
-              } else if (k == T) {
-                tie |= 1u << j;
-              }
-            }
+    const int n8 = (n + 7) / 8;
+    for (int v0 = 0; v0 < n8; v0 += SB) {  // uniform trip count
+      const int v = v0 + tid;
+      const int pg0 = seg_base + v * 8;
+      uint32_t cand = 0u, tief = 0u, tien = 0u;
+      if (v < n8) {
+        const uint4 w = reinterpret_cast<const uint4 *>(s_keys)[v];
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t k = (ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+          const int page = pg0 + j;
+          if (v * 8 + j >= n) break;
+          const bool near = page >= near_start;
+          const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
+          const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
+          if (k != 0u && (k > T || (k == T && all_eq))) {
+            if (in_cand(page)) cand |= 1u << j;
+            if (dbg) dbg_select(page, k, near);
+          } else if (k != 0u && k == T) {
+            if (near)
+              tien |= 1u << j;
+            else
+              tief |= 1u << j;
+          }
+          if (page == bp0 || page == bp1) cand |= 1u << j;
+        }
+      }
+      if (tie_cut(tf) || tie_cut(tn)) {
+        int c2[2] = {(int)__popc(tief), (int)__popc(tien)}, tot2[2];
+        block_scan_n<2, SW>(c2, s_tmp + 32, tot2);
+        int rf = tfb + c2[0], rn = tnb + c2[1];
+        for (uint32_t bits = tief; bits; bits &= bits - 1u) {
+          const int j = __ffs(bits) - 1;
+          if (rf++ < tf.need) {
+            if (in_cand(pg0 + j)) cand |= 1u << j;
+            if (dbg) dbg_select(pg0 + j, (uint32_t)tf.T, false);
           }
         }
-        const int sh = 8 * (tid & 3);
-        sel <<= sh;
-        tie <<= sh;
-        sel = quad_or(sel);
-        tie = quad_or(tie);
-        if ((tid & 3) == 0 && v < n8) {
-          s_cbits[(seg_base >> 5) + (v >> 2)] = sel;
-          s_eqb[(seg_base >> 5) + (v >> 2)] = tie;
+        for (uint32_t bits = tien; bits; bits &= bits - 1u) {
+          const int j = __ffs(bits) - 1;
+          if (rn++ < tn.need) {
+            if (in_cand(pg0 + j)) cand |= 1u << j;
+            if (dbg) dbg_select(pg0 + j, (uint32_t)tn.T, true);
+          }
         }
+        tfb += tot2[0];
+        tnb += tot2[1];
       }
-    } else {
-      for (int i = tid; i < n; i += SB) {
-        const uint32_t k = s_keys[i];
-        if (k == 0u) continue;
-        const int page = seg_base + i;
-        const bool near = page >= near_start;
-        const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
-        const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
-        if (k > T || (k == T && all_eq))
-          select_page(page, k, near);
-        else if (k == T)
-          atomicOr(&s_eqb[page >> 5], 1u << (page & 31));
-      }
-    }
-  }
-  __syncthreads();
-  NFA_MARK(32, 27);
-  // wave 0: tied pages, bypass pages, compaction (wave-level scans only)
-  int *s_pages = (int *)(smem + sd.a_pages);
-  if (wave_id() == 0) {
-    const int lane = lane_id();
-    const int wl = (sd.words + 63) / 64;
-    const int wa = imin(lane * wl, sd.words);
-    const int wb = imin(wa + wl, sd.words);
-    if (tie_cut(tf) || tie_cut(tn)) {
-      // tied pages of each pool in page order: the first `need` are selected
-      auto far_mask = [&](int w) -> uint32_t {
-        const int d = near_start - w * 32;
-        return d >= 32 ? 0xFFFFFFFFu : (d <= 0 ? 0u : ((1u << d) - 1u));
-      };
-      int cf = 0, cn = 0;
-      for (int w = wa; w < wb; ++w) {
-        const uint32_t bits = s_eqb[w];
-        const uint32_t fm = far_mask(w);
-        cf += __popc(bits & fm);
-        cn += __popc(bits & ~fm);
-      }
-      int tot;
-      int rf = wave_scan_excl(cf, &tot);
-      int rn = wave_scan_excl(cn, &tot);
-      for (int w = wa; w < wb; ++w) {
-        uint32_t bits = s_eqb[w];
-        const uint32_t fm = far_mask(w);
-        while (bits) {
-          const int bit = __ffs(bits) - 1;
-          bits &= bits - 1u;
-          const bool near = ((fm >> bit) & 1u) == 0u;
-          const int rank = near ? rn++ : rf++;
-          if (rank < (near ? tn.need : tf.need))
-            select_page(w * 32 + bit, (uint32_t)(near ? tn.T : tf.T), near);
-        }
-      }
-    }
-    if (lane == 0 && any_cand) {
-      // sink and SWA bypass pages (selector:1195-1251)
-      const int spl = p.sink_tokens / bs;
-      const bool byp0_keep = (p.sink_tokens % bs) != 0;
-      bool byp1_keep = (lb.lo % bs != 0) && (lb.lo / bs >= spl);
-      if (p.sink_tokens % bs != 0) byp1_keep = byp1_keep && (lb.lo / bs != spl);
-      const int bp0 = byp0_keep ? spl : -1;
-      const int bp1 = byp1_keep ? lb.lo / bs : -1;
-      if (bp0 >= 0 && bp0 < sd.kstride && in_cand(bp0))
-        s_cbits[bp0 >> 5] |= 1u << (bp0 & 31);
-      if (bp1 >= 0 && bp1 < sd.kstride && in_cand(bp1))
-        s_cbits[bp1 >> 5] |= 1u << (bp1 & 31);
-    }
-    // compaction: sorted unique candidate pages
-    int c1 = 0;
-    for (int w = wa; w < wb; ++w) c1 += __popc(s_cbits[w]);
-    int total;
-    int pos = wave_scan_excl(c1, &total);
-    for (int w = wa; w < wb; ++w) {
-      uint32_t bits = s_cbits[w];
-      while (bits) {
-        if (pos < sd.np) s_pages[pos] = w * 32 + __ffs(bits) - 1;
+      int ctot;
+      int pos = np_u + block_scan_exclusive<SW>(__popc(cand), s_tmp, &ctot);
+      for (uint32_t bits = cand; bits; bits &= bits - 1u) {
+        if (pos < sd.np) s_pages[pos] = pg0 + __ffs(bits) - 1;
         ++pos;
-        bits &= bits - 1u;
       }
+      np_u += ctot;
     }
-    if (lane == 0) s_misc[6] = total;
   }
   NFA_MARK(32, 2);
-  __syncthreads();
-  int np_u = s_misc[6];
   // word ranges of the debug outputs
   const int wpt = (sd.words + SB - 1) / SB;
   const int w0 = tid * wpt;
