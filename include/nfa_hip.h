@@ -112,6 +112,11 @@ typedef struct NfaSelectParams {
      fine_dsub]; valid with the statistics (written by the same rebuild and
      incremental update).  NULL: the L2 logits read the K pool. */
   void *l2_keys_l;
+  /* optional fp32 running sums of each request's last (partial) L1 page,
+     [max_req, hkv, dsub], valid with the statistics: with them a decode step
+     updates the last page's statistics from the new token alone.  NULL: the
+     last page is re-read. */
+  float *page_sum_l;
 
   /* outputs */
   int32_t *gather;                    /* [rows >= batch, hkv, max_vis] */

@@ -329,7 +329,8 @@ template <int DSUB, typename KV>
 __device__ __forceinline__ void compute_stats(const NfaSelectParams &p, int64_t req, int kv,
                               int L, int pg_lo, int pg_hi, float *s_stage,
                               const int *s_dims, const int *s_tphys,
-                              const KV *new_row, int new_tok, float *s_last) {
+                              const KV *new_row, int new_tok, float *page_sum,
+                              int sum_pg) {
   const KV *kpool = (const KV *)p.k_pool_l;
   const int32_t *bt = p.block_table_l + req * p.max_blocks;
   constexpr int PER = SB / DSUB;  // pages per pass
@@ -388,11 +389,7 @@ __device__ __forceinline__ void compute_stats(const NfaSelectParams &p, int64_t 
       smin[si] = a;
       smax[si] = c;
       ssum[si] = s;
-      if (s_last != nullptr) {
-        s_last[d] = Elem<KV>::load(&a);
-        s_last[DSUB + d] = Elem<KV>::load(&c);
-        s_last[2 * DSUB + d] = Elem<KV>::load(&s);
-      }
+      if (page_sum != nullptr && pg == sum_pg) page_sum[d] = sm;
     }
   }
 }
@@ -409,7 +406,7 @@ __device__ __forceinline__ void compute_stats_vec(const NfaSelectParams &p, int6
                                   int L, int pg_lo, int pg_hi,
                                   const int *s_coff, const int *s_tphys,
                                   const KV *new_row, int new_tok,
-                                  float *s_last) {
+                                  float *page_sum, int sum_pg) {
   constexpr int CH = Elem<KV>::kChunk;
   constexpr int NCH1 = DSUB / CH;
   constexpr int TG = 4;
@@ -473,11 +470,7 @@ __device__ __forceinline__ void compute_stats_vec(const NfaSelectParams &p, int6
       smin[si + e] = a;
       smax[si + e] = b;
       ssum[si + e] = s;
-      if (s_last != nullptr) {
-        s_last[c * CH + e] = Elem<KV>::load(&a);
-        s_last[DSUB + c * CH + e] = Elem<KV>::load(&b);
-        s_last[2 * DSUB + c * CH + e] = Elem<KV>::load(&s);
-      }
+      if (page_sum != nullptr && pg == sum_pg) page_sum[c * CH + e] = sm[e];
     }
   }
 }
@@ -551,6 +544,41 @@ __device__ __forceinline__ void stats_latest_page(
     s_last[DSUB + d] = Elem<KV>::load(&c);
     s_last[2 * DSUB + d] = Elem<KV>::load(&s);
   }
+}
+
+// Statistics of the latest page after appending token L-1, thread d < DSUB:
+// the sequential min / max / sum continue from the stored min and max (exact
+// KV values) and the fp32 running sum of the page (the stored sum is
+// rounded), or start over when the token opens a new page.  `row` is the
+// token's key row.
+template <int DSUB, typename KV>
+__device__ __forceinline__ void stats_append_token(const NfaSelectParams &p,
+                                                   int64_t req, int kv, int L,
+                                                   int pg, const KV *row,
+                                                   const int *s_dims) {
+  const int d = threadIdx.x;
+  const int64_t si = stat_index<KV>(p, req, kv, d, pg, DSUB);
+  float *psum = p.page_sum_l + (req * p.hkv + kv) * DSUB;
+  KV *smin = (KV *)p.stat_min_l;
+  KV *smax = (KV *)p.stat_max_l;
+  KV *ssum = (KV *)p.stat_sum_l;
+  const bool first = (L - 1) % p.bs == 0;
+  float mn = __uint_as_float(0x7F800000u);
+  float mx = __uint_as_float(0xFF800000u);
+  float sm = 0.0f;
+  if (!first) {
+    mn = Elem<KV>::load(smin + si);
+    mx = Elem<KV>::load(smax + si);
+    sm = psum[d];
+  }
+  const float x = Elem<KV>::load(row + s_dims[d]);
+  mn = (x < mn) ? x : mn;
+  mx = (x > mx) ? x : mx;
+  sm = sm + x;
+  smin[si] = (KV)Elem<KV>::from_f32(mn);
+  smax[si] = (KV)Elem<KV>::from_f32(mx);
+  ssum[si] = (KV)Elem<KV>::from_f32(sm);
+  psum[d] = sm;
 }
 
 // Asynchronous global-to-LDS loads (gfx950 global_load_lds_dwordx4) of the
@@ -1236,8 +1264,17 @@ __global__ void __launch_bounds__(SB)
   const bool page_phys = (p.page % bs) == 0;
   const KV *kpool = (const KV *)p.k_pool_l;
   if (do_stats && incremental && owns_last) {
-    stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims,
-                                s_stage, new_row, s_last);
+    if (p.page_sum_l != nullptr) {
+      if (tid < DSUB)
+        stats_append_token<DSUB, KV>(
+            p, req, kv, L, last_blk,
+            new_row != nullptr ? new_row
+                               : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page),
+            s_dims);
+    } else {
+      stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims,
+                                  s_stage, new_row, s_last);
+    }
     if (p.l2_keys_l != nullptr && tid < p.fine_dsub) {
       // the new token's L2 side row
       const KV *src = new_row != nullptr
@@ -1246,6 +1283,9 @@ __global__ void __launch_bounds__(SB)
       l2_side_row<KV>(p, req, kv, L - 1)[tid] = src[s_fdims[tid]];
     }
   } else if (do_stats && !incremental) {
+    float *psum_row = p.page_sum_l != nullptr
+                          ? p.page_sum_l + (req * p.hkv + kv) * DSUB
+                          : nullptr;
     int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
     if (tid == 0) {
       bool vec = true;
@@ -1267,12 +1307,12 @@ __global__ void __launch_bounds__(SB)
     if (s_misc[1]) {
       compute_stats_vec<DSUB, KV>(p, req, kv, L, t0, t1, s_coff,
                                   page_phys ? s_tphys : nullptr, new_row, L - 1,
-                                  nullptr);
+                                  psum_row, last_blk);
     } else {
       __syncthreads();
       compute_stats<DSUB, KV>(p, req, kv, L, t0, t1, s_stage, s_dims,
                               page_phys ? s_tphys : nullptr, new_row, L - 1,
-                              nullptr);
+                              psum_row, last_blk);
     }
     if (p.l2_keys_l != nullptr) {
       // L2 side rows of the tile's tokens
@@ -1316,16 +1356,6 @@ __global__ void __launch_bounds__(SB)
   if constexpr (STG) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's staged statistics
     __syncthreads();
-    if (do_stats && incremental && owns_last && tid < 2 * NC) {
-      // the latest page's statistics, as stored, replace the staged ones
-      bool fpl = false, npl = false;
-      pools(p, g0, last_blk, &fpl, &npl);
-      const bool mml = (fpl && far_mm) || (npl && near_mm);
-      const int slot = tid / NC, c = tid % NC;
-      const float *src = s_last + (slot == 1 ? DSUB : (mml ? 0 : 2 * DSUB));
-      reinterpret_cast<uint4 *>(s_st)[(slot * NC + c) * kSpanMax + (last_blk - t0)] =
-          pack_chunk<KV>(src + c * CH);
-    }
   }
   lds_barrier();
   NFA_MARK(0, 3);

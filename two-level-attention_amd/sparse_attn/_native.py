@@ -52,7 +52,7 @@ class NfaSelectParams(ctypes.Structure):
         ('k_new', _ptr), ('v_new', _ptr), ('slots', _ptr),
         ('stat_min_l', _ptr), ('stat_max_l', _ptr), ('stat_sum_l', _ptr),
         ('stats_len_l', _ptr),
-        ('l2_keys_l', _ptr),
+        ('l2_keys_l', _ptr), ('page_sum_l', _ptr),
         ('gather', _ptr), ('vis_lens', _ptr),
         ('workspace', _ptr), ('workspace_bytes', _i64),
         ('dbg_far', _ptr), ('dbg_near', _ptr),

@@ -72,7 +72,8 @@ def _no_capture_alloc(what):
 def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype, fine_key,
                         head_dim, bs):
     """Persistent per-layer page statistics [max_req, hkv, dsub, max_blocks]
-    in the KV dtype, chunk-major, and the L2 side copy [max_req, hkv,
+    in the KV dtype, chunk-major, the fp32 running sums of each request's last
+    page [max_req, hkv, dsub], and the L2 side copy [max_req, hkv,
     max_blocks * bs, fine_dsub] of every visible token's L2 dims (None for a
     full-width L2 subspace, or when ``cache.nfa_l2_side_copy`` is False); a new
     dims set for a layer forces rebuilds of both."""
@@ -101,6 +102,10 @@ def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype, fine_key,
                  * cache.max_blocks)
         stats = tuple(torch.empty(numel, dtype=dtype, device=device)
                       for _ in range(3))
+        # fp32 running sums of each request's last page
+        stats += (torch.zeros(cache.max_requests * layer0.num_kv_heads
+                              * int(dims.numel()), dtype=torch.float32,
+                              device=device),)
         side = None
         if want_side:
             side = torch.empty(cache.max_requests * layer0.num_kv_heads
@@ -219,7 +224,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
         raise ValueError('selection outputs must be contiguous int32')
 
     kv_dtype = layer0.kv_pool_k.dtype
-    (smin, smax, ssum), l2_side, stats_len = _page_stats_buffers(
+    (smin, smax, ssum, psum), l2_side, stats_len = _page_stats_buffers(
         cache, layer_idx, l1_dims, l1_key, kv_dtype, fine_key, head_dim, bs)
     layer = cache.layers[layer_idx]
 
@@ -273,6 +278,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
         smin.data_ptr(), smax.data_ptr(), ssum.data_ptr())
     p.stats_len_l = stats_len.data_ptr()
     p.l2_keys_l = l2_side.data_ptr() if l2_side is not None else None
+    p.page_sum_l = psum.data_ptr()
     p.gather = gather_out.data_ptr()
     p.vis_lens = vis_out.data_ptr()
     need = lib.nfa_select_workspace_bytes(ctypes.byref(p))
