@@ -296,7 +296,7 @@ def selector_timeline(torch, w, steps, plan):
                  ('tail selection pass', 1, 2),
                  
                  ('tail bitmap compaction', 2, 3), ('tail candidate pages', 3, 4),
-                 ('tail L1 end', 4, 6), ('tail L2 logits', 6, 9),
+                 ('tail L1 end', 4, 6), ('tail L2 logits', 6, 9), ('  L2 logits: loads', 6, 7), ('  L2 logits: dots', 7, 9),
                  ('tail L2 top-k', 9, 12), ('tail union', 12, 13),
                  ('  L2 top-k: coarse hist', 16, 17), ('  L2 top-k: coarse bin', 17, 18),
                  ('  L2 top-k: fine pass+bin', 18, 19), ('  L2 top-k: count+scan', 19, 20),

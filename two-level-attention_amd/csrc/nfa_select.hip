@@ -301,12 +301,21 @@ __device__ __forceinline__ int64_t kv_offset(const NfaSelectParams &p,
   return (((int64_t)phys * p.hkv + kv) * p.page + off) * p.head_dim;
 }
 
-// L2 side row of token tok: its L2 dims, fine_dims order, KV dtype
+// L2 side copy of one (request, kv head): per L1 page of bs tokens, when the
+// L2 dims split into 16-byte chunks, chunk-major [chunk][token][CH] (a wave
+// reading one chunk of consecutive tokens reads consecutive bytes), else
+// token-major [token][fine_dsub].  Element d of token tok:
 template <typename KV>
-__device__ __forceinline__ KV *l2_side_row(const NfaSelectParams &p, int64_t req,
-                                           int kv, int tok) {
-  return (KV *)p.l2_keys_l +
-         ((req * p.hkv + kv) * (int64_t)p.max_blocks * p.bs + tok) * p.fine_dsub;
+__device__ __forceinline__ int64_t l2_side_index(const NfaSelectParams &p,
+                                                 int64_t req, int kv, int tok,
+                                                 int d) {
+  constexpr int CH = Elem<KV>::kChunk;
+  const int64_t page = (req * p.hkv + kv) * (int64_t)p.max_blocks + tok / p.bs;
+  const int r = tok % p.bs;
+  const int64_t base = page * p.bs * p.fine_dsub;
+  return p.fine_dsub % CH == 0
+             ? base + ((int64_t)(d / CH) * p.bs + r) * CH + d % CH
+             : base + (int64_t)r * p.fine_dsub + d;
 }
 
 // ---------------------------------------------------------------------------
@@ -1280,7 +1289,7 @@ __global__ void __launch_bounds__(SB)
       const KV *src = new_row != nullptr
                           ? new_row
                           : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page);
-      l2_side_row<KV>(p, req, kv, L - 1)[tid] = src[s_fdims[tid]];
+      ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)] = src[s_fdims[tid]];
     }
   } else if (do_stats && !incremental) {
     float *psum_row = p.page_sum_l != nullptr
@@ -1329,14 +1338,16 @@ __global__ void __launch_bounds__(SB)
         for (int e = tid; e < (thi - tlo) * nchv; e += SB) {
           const int tok = tlo + e / nchv;
           const int c = e % nchv;
-          *reinterpret_cast<uint4 *>(l2_side_row<KV>(p, req, kv, tok) + c * CH) =
+          *reinterpret_cast<uint4 *>((KV *)p.l2_keys_l +
+                                     l2_side_index<KV>(p, req, kv, tok, c * CH)) =
               *reinterpret_cast<const uint4 *>(src_row(tok) + s_fdims[c * CH]);
         }
       } else {
         for (int e = tid; e < (thi - tlo) * p.fine_dsub; e += SB) {
           const int tok = tlo + e / p.fine_dsub;
           const int d = e % p.fine_dsub;
-          l2_side_row<KV>(p, req, kv, tok)[d] = src_row(tok)[s_fdims[d]];
+          ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, tok, d)] =
+              src_row(tok)[s_fdims[d]];
         }
       }
     }
@@ -1700,7 +1711,9 @@ __global__ void __launch_bounds__(SB)
     const bool side = p.l2_keys_l != nullptr;
     const int nch = side ? (p.fine_dsub % CH == 0 ? p.fine_dsub / CH : 0)
                          : s_misc[5];  // 16-byte runs, 0: element loads
-    auto choff = [&](int c) { return side ? c * CH : s_fdims[c * CH]; };
+    // side copy: kr = element 0 of the token, chunk c at c * bs * CH (chunk-
+    // major) or element d at d (token-major); K pool: the L2 dims' offsets
+    auto choff = [&](int c) { return side ? c * bs * CH : s_fdims[c * CH]; };
     auto eoff = [&](int d) { return side ? d : s_fdims[d]; };
     constexpr int SPT = 3;
     for (int i0 = 0; i0 < n_dense; i0 += SPT * SB) {
@@ -1718,7 +1731,7 @@ __global__ void __launch_bounds__(SB)
           tk[k] = s_pages[pi] * bs + (i - pi * bs);
           on[k] = tk[k] >= tok_lo && tk[k] < tok_hi;
           if (side) {
-            kr[k] = l2_side_row<KV>(p, req, kv, tk[k]);
+            kr[k] = (const KV *)p.l2_keys_l + l2_side_index<KV>(p, req, kv, tk[k], 0);
           } else {
             const int phys = safe_page(
                 p, page_phys ? s_pphys[pi] : btr[imin(tk[k] / p.page, mb - 1)]);
@@ -1739,6 +1752,10 @@ __global__ void __launch_bounds__(SB)
             r[k][c] = on[k] && c < nch
                           ? *reinterpret_cast<const uint4 *>(kr[k] + choff(c))
                           : make_uint4(0u, 0u, 0u, 0u);
+        if (p.dbg_clock != nullptr) {  // timeline only: the loads have landed
+          __builtin_amdgcn_s_waitcnt(0);
+          NFA_MARK(32, 7);
+        }
 #pragma unroll
         for (int k = 0; k < SPT; ++k)
 #pragma unroll
