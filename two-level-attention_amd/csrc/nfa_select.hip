@@ -1553,6 +1553,9 @@ __global__ void __launch_bounds__(SB)
   auto in_cand = [&](int page) {
     return any_cand && page * bs < tok_hi && page * bs + bs > tok_lo;
   };
+  // the same as a page range [cp_lo, cp_hi) (tok_lo >= 0)
+  const int cp_lo = any_cand ? tok_lo / bs : 0;
+  const int cp_hi = any_cand ? (tok_hi + bs - 1) / bs : 0;
   // sink and SWA bypass pages (selector:1195-1251)
   int bp0 = -1, bp1 = -1;
   {
@@ -1569,6 +1572,12 @@ __global__ void __launch_bounds__(SB)
   // by a block scan); a second scan places the candidates, so the list is
   // sorted and free of duplicates by construction.
   int *s_pages = (int *)(smem + sd.a_pages);
+  // bit j set for pages pg0 + j in [lo, hi), j < 8
+  auto range8 = [](int pg0, int lo, int hi) -> uint32_t {
+    const int a = imin(imax(lo - pg0, 0), 8);
+    const int b = imin(imax(hi - pg0, 0), 8);
+    return ((1u << b) - 1u) & ~((1u << a) - 1u);
+  };
   int np_u = 0;          // candidates so far (uniform)
   int tfb = 0, tnb = 0;  // tied far / near pages so far (uniform)
   for (int sg = 0; sg < sd.nseg; ++sg) {
@@ -1587,23 +1596,37 @@ __global__ void __launch_bounds__(SB)
       if (v < n8) {
         const uint4 w = reinterpret_cast<const uint4 *>(s_keys)[v];
         const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        // masks over the eight pages: in range, near pool, candidate range
+        const uint32_t valid = range8(pg0, pg0, seg_base + n);
+        const uint32_t nearm = range8(pg0, near_start, 0x7FFFFFFF);
+        const uint32_t candm = range8(pg0, cp_lo, cp_hi);
+        auto byp8 = [&](int bp) -> uint32_t {
+          return bp >= pg0 && bp < pg0 + 8 ? 1u << (bp - pg0) : 0u;
+        };
+        uint32_t gt = 0u, eq = 0u;
+#pragma unroll
         for (int j = 0; j < 8; ++j) {
           const uint32_t k = (ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-          const int page = pg0 + j;
-          if (v * 8 + j >= n) break;
-          const bool near = page >= near_start;
-          const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
-          const bool all_eq = (near ? tn.need : tf.need) == (1 << 30);
-          if (k != 0u && (k > T || (k == T && all_eq))) {
-            if (in_cand(page)) cand |= 1u << j;
-            if (dbg) dbg_select(page, k, near);
-          } else if (k != 0u && k == T) {
-            if (near)
-              tien |= 1u << j;
-            else
-              tief |= 1u << j;
+          const uint32_t T = ((nearm >> j) & 1u) ? (uint32_t)tn.T : (uint32_t)tf.T;
+          gt |= (k > T ? 1u : 0u) << j;
+          eq |= (k == T ? 1u : 0u) << j;
+        }
+        gt &= valid;
+        eq &= valid;
+        // keys equal to the threshold: all selected, or tied (zero keys equal
+        // a threshold of 0 only when every valid key is selected: no tie cut)
+        const uint32_t all_eq = (tf.need == (1 << 30) ? ~nearm : 0u) |
+                                (tn.need == (1 << 30) ? nearm : 0u);
+        const uint32_t sel = gt | (eq & all_eq);
+        tief = eq & ~all_eq & ~nearm;
+        tien = eq & ~all_eq & nearm;
+        cand = (sel & candm) | byp8(bp0) | byp8(bp1);
+        if (dbg) {
+          for (uint32_t bits = sel; bits; bits &= bits - 1u) {
+            const int j = __ffs(bits) - 1;
+            const uint32_t k = (ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+            dbg_select(pg0 + j, k, ((nearm >> j) & 1u) != 0u);
           }
-          if (page == bp0 || page == bp1) cand |= 1u << j;
         }
       }
       if (tie_cut(tf) || tie_cut(tn)) {
