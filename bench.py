@@ -296,15 +296,17 @@ def selector_timeline(torch, w, steps, plan):
                  ('tail selection pass', 1, 2),
                  
                  ('tail bitmap compaction', 2, 3), ('tail candidate pages', 3, 4),
-                 ('tail L1 end', 4, 6), ('tail L2 logits', 6, 9), ('  L2 logits: loads', 6, 7), ('  L2 logits: dots', 7, 9),
+                 ('tail L1 end', 4, 6), ('tail L2 logits', 6, 9),
                  ('tail L2 top-k', 9, 12), ('tail union', 12, 13),
                  ('  L2 top-k: coarse hist', 16, 17), ('  L2 top-k: coarse bin', 17, 18),
                  ('  L2 top-k: fine pass+bin', 18, 19), ('  L2 top-k: count+scan', 19, 20),
                  ('  L2 top-k: emit', 20, 21), ('  L2 top-k: hole fill', 21, 22),
                  ('  L2 top-k: merge', 22, 23)]
         for name, a, b in spans:
-            d = (tail[:, b] - tail[:, a]) * us
-            acc.setdefault(f'{name} (max)', []).append(d.max())
+            ok = (tail[:, a] > 0) & (tail[:, b] > 0)
+            if ok.any():
+                d = (tail[ok, b] - tail[ok, a]) * us
+                acc.setdefault(f'{name} (max)', []).append(d.max())
     for name, vals in acc.items():
         print(f'# timeline {name:28s} median {np.median(vals):8.2f} us',
               file=sys.stderr, flush=True)

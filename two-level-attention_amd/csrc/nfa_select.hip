@@ -1738,99 +1738,85 @@ __global__ void __launch_bounds__(SB)
     // major) or element d at d (token-major); K pool: the L2 dims' offsets
     auto choff = [&](int c) { return side ? c * bs * CH : s_fdims[c * CH]; };
     auto eoff = [&](int d) { return side ? d : s_fdims[d]; };
-    constexpr int SPT = 3;
-    for (int i0 = 0; i0 < n_dense; i0 += SPT * SB) {
-      int tk[SPT];
-      const KV *kr[SPT];
-      bool on[SPT];
+    // slot i: its token and L2 row (null outside the candidate range)
+    auto slot_row = [&](int i, int &tk) -> const KV * {
+      const int pi = i / bs;
+      tk = s_pages[pi] * bs + (i - pi * bs);
+      if (tk < tok_lo || tk >= tok_hi) return nullptr;
+      if (side) return (const KV *)p.l2_keys_l + l2_side_index<KV>(p, req, kv, tk, 0);
+      const int phys =
+          safe_page(p, page_phys ? s_pphys[pi] : btr[imin(tk / p.page, mb - 1)]);
+      return kpool + kv_offset(p, phys, kv, tk % p.page);
+    };
+    const bool vec4 = nch > 0 && nch <= 4;  // the L2 row in at most 4 loads
+    auto fetch = [&](const KV *kr, uint4 (&r)[4]) {
 #pragma unroll
-      for (int k = 0; k < SPT; ++k) {
-        const int i = i0 + tid + k * SB;
-        tk[k] = -1;
-        on[k] = false;
-        kr[k] = kpool;
-        if (i < n_dense) {
-          const int pi = i / bs;
-          tk[k] = s_pages[pi] * bs + (i - pi * bs);
-          on[k] = tk[k] >= tok_lo && tk[k] < tok_hi;
-          if (side) {
-            kr[k] = (const KV *)p.l2_keys_l + l2_side_index<KV>(p, req, kv, tk[k], 0);
-          } else {
-            const int phys = safe_page(
-                p, page_phys ? s_pphys[pi] : btr[imin(tk[k] / p.page, mb - 1)]);
-            kr[k] = kpool + kv_offset(p, phys, kv, tk[k] % p.page);
-          }
-        }
-      }
-      float acc[SPT];
-#pragma unroll
-      for (int k = 0; k < SPT; ++k) acc[k] = 0.0f;
-      if (nch > 0 && nch <= 4) {
-        // every run of every slot loaded before any is used
-        uint4 r[SPT][4];
-#pragma unroll
-        for (int k = 0; k < SPT; ++k)
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            r[k][c] = on[k] && c < nch
-                          ? *reinterpret_cast<const uint4 *>(kr[k] + choff(c))
-                          : make_uint4(0u, 0u, 0u, 0u);
-        if (p.dbg_clock != nullptr) {  // timeline only: the loads have landed
-          __builtin_amdgcn_s_waitcnt(0);
-          NFA_MARK(32, 7);
-        }
-#pragma unroll
-        for (int k = 0; k < SPT; ++k)
+      for (int c = 0; c < 4; ++c)
+        r[c] = kr != nullptr && c < nch
+                   ? *reinterpret_cast<const uint4 *>(kr + choff(c))
+                   : make_uint4(0u, 0u, 0u, 0u);
+    };
+    // slots tid, tid + SB, ...: the next slot's loads are in flight while
+    // the current slot's dot product runs (rolled: compact code)
+    int tk = -1;
+    const KV *kr = nullptr;
+    uint4 r[4];
+    if (tid < n_dense) kr = slot_row(tid, tk);
+    if (vec4) fetch(kr, r);
+#pragma unroll 1
+    for (int i = tid; i < n_dense; i += SB) {
+      int tkn = -1;
+      const KV *krn = nullptr;
+      uint4 rn[4];
+      if (i + SB < n_dense) krn = slot_row(i + SB, tkn);
+      if (vec4) fetch(krn, rn);
+      float acc = 0.0f;
+      if (kr != nullptr) {
+        if (vec4) {
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             if (c >= nch) continue;
             float x[CH];
-            unpack_chunk<KV>(r[k][c], x);
+            unpack_chunk<KV>(r[c], x);
 #pragma unroll
             for (int e = 0; e < CH; ++e) {
               const float prod = x[e] * s_qg[c * CH + e];
-              acc[k] = acc[k] + prod;
+              acc = acc + prod;
             }
           }
-      } else {
-#pragma unroll
-        for (int k = 0; k < SPT; ++k) {
-          if (!on[k]) continue;
-          if (nch > 0) {
-            for (int c = 0; c < nch; ++c) {
-              float x[CH];
-              load_chunk<KV>(kr[k] + choff(c), x);
-              for (int e = 0; e < CH; ++e) {
-                const float prod = x[e] * s_qg[c * CH + e];
-                acc[k] = acc[k] + prod;
-              }
+        } else if (nch > 0) {
+          for (int c = 0; c < nch; ++c) {
+            float x[CH];
+            load_chunk<KV>(kr + choff(c), x);
+            for (int e = 0; e < CH; ++e) {
+              const float prod = x[e] * s_qg[c * CH + e];
+              acc = acc + prod;
             }
-          } else {
-            for (int d = 0; d < p.fine_dsub; ++d) {
-              const float prod = Elem<KV>::load(kr[k] + eoff(d)) * s_qg[d];
-              acc[k] = acc[k] + prod;
-            }
+          }
+        } else {
+          for (int d = 0; d < p.fine_dsub; ++d) {
+            const float prod = Elem<KV>::load(kr + eoff(d)) * s_qg[d];
+            acc = acc + prod;
           }
         }
       }
-#pragma unroll
-      for (int k = 0; k < SPT; ++k) {
-        const int i = i0 + tid + k * SB;
-        if (i >= n_dense) continue;
-        uint16_t key = 0;
-        if (on[k]) {
-          const uint16_t bits = bf16_bits(acc[k]);
-          key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
-          if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
-            p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tk[k];
-            p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
-                bits == kNanBits ? kNegInfBits : bits;
-          }
-        } else if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
-          p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = -1;
+      uint16_t key = 0;
+      if (kr != nullptr) {
+        const uint16_t bits = bf16_bits(acc);
+        key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
+        if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
+          p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tk;
+          p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
+              bits == kNanBits ? kNegInfBits : bits;
         }
-        s_dk[i] = key;
+      } else if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
+        p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = -1;
       }
+      s_dk[i] = key;
+      tk = tkn;
+      kr = krn;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r[c] = rn[c];
     }
   }
   __syncthreads();
