@@ -12,6 +12,11 @@
 
 #include "../../include/nfa_hip.h"
 
+// Branch hint for paths the steady decode step does not take (debug
+// outputs, rebuilds, rare geometries): the compiler lays them out after the
+// hot code, which keeps the executed instruction stream contiguous.
+#define NFA_COLD(x) __builtin_expect(!!(x), 0)
+
 #define NFA_BLOCK 256
 #define NFA_WAVES (NFA_BLOCK / 64)
 

@@ -1092,14 +1092,14 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
 // timeline sits inside a measured phase.  Uniform conditions.
 #define NFA_MARK(part, k)                                             \
   do {                                                                \
-    if (p.dbg_clock != nullptr) {                                     \
+    if (NFA_COLD(p.dbg_clock != nullptr)) {                           \
       lds_barrier();                                                  \
       if (threadIdx.x == 0) s_clk[(part) + (k)] = wall_clock64();     \
     }                                                                 \
   } while (0)
 #define NFA_FLUSH(part, slot_base)                                    \
   do {                                                                \
-    if (p.dbg_clock != nullptr) {                                     \
+    if (NFA_COLD(p.dbg_clock != nullptr)) {                           \
       lds_barrier();                                                  \
       if (threadIdx.x < 32 && s_clk[(part) + threadIdx.x] != 0)       \
         p.dbg_clock[(slot_base) + threadIdx.x] = s_clk[(part) + threadIdx.x]; \
@@ -1146,7 +1146,7 @@ __global__ void __launch_bounds__(SB)
   const int64_t clk_tile = ((int64_t)row * (sd.clk_tiles + 1) + tile) * 32;
   const int64_t clk_tail = ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32;
   int64_t *s_clk = (int64_t *)(smem + sd.a_clk);
-  if (p.dbg_clock != nullptr && tid < 64) s_clk[tid] = 0;
+  if (NFA_COLD(p.dbg_clock != nullptr) && tid < 64) s_clk[tid] = 0;
   NFA_MARK(0, 0);
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
@@ -1273,7 +1273,7 @@ __global__ void __launch_bounds__(SB)
   const bool page_phys = (p.page % bs) == 0;
   const KV *kpool = (const KV *)p.k_pool_l;
   if (do_stats && incremental && owns_last) {
-    if (p.page_sum_l != nullptr) {
+    if (__builtin_expect(p.page_sum_l != nullptr, 1)) {
       if (tid < DSUB)
         stats_append_token<DSUB, KV>(
             p, req, kv, L, last_blk,
@@ -1291,7 +1291,7 @@ __global__ void __launch_bounds__(SB)
                           : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page);
       ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)] = src[s_fdims[tid]];
     }
-  } else if (do_stats && !incremental) {
+  } else if (NFA_COLD(do_stats && !incremental)) {
     float *psum_row = p.page_sum_l != nullptr
                           ? p.page_sum_l + (req * p.hkv + kv) * DSUB
                           : nullptr;
@@ -1425,7 +1425,7 @@ __global__ void __launch_bounds__(SB)
         if (fp) far_bits = mean;
         if (np) near_bits = mean;
       }
-      if (p.dbg_far != nullptr) {
+      if (NFA_COLD(p.dbg_far != nullptr)) {
         p.dbg_far[(int64_t)row * mb + t] = far_bits;
         p.dbg_near[(int64_t)row * mb + t] = near_bits;
       }
@@ -1471,7 +1471,7 @@ __global__ void __launch_bounds__(SB)
   NFA_MARK(32, 0);
 
   const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
-  if (p.dbg_bounds != nullptr && kv == 0 && tid == 0) {
+  if (NFA_COLD(p.dbg_bounds != nullptr) && kv == 0 && tid == 0) {
     p.dbg_bounds[b * 3 + 0] = lb.lower;
     p.dbg_bounds[b * 3 + 1] = lb.upper;
     p.dbg_bounds[b * 3 + 2] = lb.quota;
@@ -1487,7 +1487,7 @@ __global__ void __launch_bounds__(SB)
     s_hist[tid] = atomicExch(&g_hist[tid], 0);
     s_hist[512 + tid] = 0;
   }
-  if (dbg) {
+  if (NFA_COLD(dbg)) {
     for (int w = tid; w < sd.words; w += SB) {
       s_dbf[w] = 0u;
       s_dbn[w] = 0u;
@@ -1510,7 +1510,7 @@ __global__ void __launch_bounds__(SB)
     // refinement: low-byte histograms of the keys in the threshold bins
     for (int sg = 0; sg < sd.nseg; ++sg) {
       const int seg_base = sg * sd.seg;
-      if (sd.nseg > 1) {
+      if (NFA_COLD(sd.nseg > 1)) {
         __syncthreads();
         stage_keys(g_keys, seg_base, sd.seg, s_keys);
         __syncthreads();
@@ -1582,7 +1582,7 @@ __global__ void __launch_bounds__(SB)
   int tfb = 0, tnb = 0;  // tied far / near pages so far (uniform)
   for (int sg = 0; sg < sd.nseg; ++sg) {
     const int seg_base = sg * sd.seg;
-    if (sd.nseg > 1) {
+    if (NFA_COLD(sd.nseg > 1)) {
       __syncthreads();
       stage_keys(g_keys, seg_base, sd.seg, s_keys);
       __syncthreads();
@@ -1621,7 +1621,7 @@ __global__ void __launch_bounds__(SB)
         tief = eq & ~all_eq & ~nearm;
         tien = eq & ~all_eq & nearm;
         cand = (sel & candm) | byp8(bp0) | byp8(bp1);
-        if (dbg) {
+        if (NFA_COLD(dbg)) {
           for (uint32_t bits = sel; bits; bits &= bits - 1u) {
             const int j = __ffs(bits) - 1;
             const uint32_t k = (ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
@@ -1637,14 +1637,14 @@ __global__ void __launch_bounds__(SB)
           const int j = __ffs(bits) - 1;
           if (rf++ < tf.need) {
             if (in_cand(pg0 + j)) cand |= 1u << j;
-            if (dbg) dbg_select(pg0 + j, (uint32_t)tf.T, false);
+            if (NFA_COLD(dbg)) dbg_select(pg0 + j, (uint32_t)tf.T, false);
           }
         }
         for (uint32_t bits = tien; bits; bits &= bits - 1u) {
           const int j = __ffs(bits) - 1;
           if (rn++ < tn.need) {
             if (in_cand(pg0 + j)) cand |= 1u << j;
-            if (dbg) dbg_select(pg0 + j, (uint32_t)tn.T, true);
+            if (NFA_COLD(dbg)) dbg_select(pg0 + j, (uint32_t)tn.T, true);
           }
         }
         tfb += tot2[0];
@@ -1685,7 +1685,7 @@ __global__ void __launch_bounds__(SB)
   NFA_MARK(32, 4);
   // L1 debug outputs: I_F / I_N (selector:1766-1803 order: valid pages by
   // (score desc, page asc), then -inf fillers by ascending page)
-  if (dbg) {
+  if (NFA_COLD(dbg)) {
     for (int pool = 0; pool < 2; ++pool) {
       const int K = pool == 0 ? p.k_f : p.k_n;
       const int nsel = pool == 0 ? tf.nsel : tn.nsel;
@@ -1804,12 +1804,12 @@ __global__ void __launch_bounds__(SB)
       if (kr != nullptr) {
         const uint16_t bits = bf16_bits(acc);
         key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
-        if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
+        if (NFA_COLD(p.dbg_cand_tok != nullptr) && i < p.dbg_cand_cap) {
           p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tk;
           p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
               bits == kNanBits ? kNegInfBits : bits;
         }
-      } else if (p.dbg_cand_tok != nullptr && i < p.dbg_cand_cap) {
+      } else if (NFA_COLD(p.dbg_cand_tok != nullptr) && i < p.dbg_cand_cap) {
         p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = -1;
       }
       s_dk[i] = key;
@@ -1833,7 +1833,7 @@ __global__ void __launch_bounds__(SB)
     int nreg = 1;
     bool masked = false;
     int r_lo[2] = {lb.lower, 0}, r_hi[2] = {lb.upper, 0}, r_q[2] = {lb.quota, 0};
-    if (p.near_tokens >= 0) {
+    if (NFA_COLD(p.near_tokens >= 0)) {
       // far quota first, the remainder goes to near (selector:873-920)
       const L2Bounds fb = l2_bounds(p, L, false, false, p.near_len);
       const int base = imax(imin(L, p.k2) - p.sink_tokens - (L - fb.lo), 0);
@@ -1868,7 +1868,7 @@ __global__ void __launch_bounds__(SB)
   if (mcount > p.k2) mcount = p.k2;
   const int *s_mid = rl.mid;
   const int *s_mslot = rl.mslot;
-  if (p.dbg_middle != nullptr) {
+  if (NFA_COLD(p.dbg_middle != nullptr)) {
     for (int k = tid; k < p.k2; k += SB)
       p.dbg_middle[(int64_t)row * p.k2 + k] = k < mcount ? s_mid[k] : 0;
     if (tid == 0) p.dbg_counts[row] = mcount;
@@ -1876,7 +1876,7 @@ __global__ void __launch_bounds__(SB)
 
   // ---- final union with the protected sink/SWA ids (selector:1337-1437) --
   int32_t *grow = p.gather + ((int64_t)b * p.hkv + kv) * p.max_vis;
-  if (p.middle_only) {
+  if (NFA_COLD(p.middle_only)) {
     const int n = imin(mcount, p.max_vis);
     for (int k = tid; k < n; k += SB) grow[k] = s_mslot[k];
     if (tid == 0) p.vis_lens[b * p.hkv + kv] = n;
@@ -1885,7 +1885,7 @@ __global__ void __launch_bounds__(SB)
     return;
   }
   const int n0 = u1 - u0;  // protected ids of the first interval
-  if (u0 == 0 && (mcount == 0 || (s_mid[0] >= u1 && s_mid[mcount - 1] < u2))) {
+  if (__builtin_expect(u0 == 0 && (mcount == 0 || (s_mid[0] >= u1 && s_mid[mcount - 1] < u2)), 1)) {
     // the usual case: the middle lies between the sink and the SWA ids, so
     // the union is [0, u1) ++ middle ++ [u2, u3) with no duplicates
     for (int k = tid; k < mcount; k += SB)
