@@ -51,6 +51,12 @@ def parse():
     ap.add_argument('--seed', type=int, default=20261201)
     ap.add_argument('--timeline', type=int, default=0,
                     help='print selector phase timings of N extra decode steps')
+    ap.add_argument('--e2e-steps', type=int, default=0,
+                    help='also run the whole Qwen3-8B-geometry model (random-init '
+                         'bf16): dense prefill of --ctx tokens, then this many '
+                         'greedy decode steps replayed from a hipGraph; 0 = off')
+    ap.add_argument('--e2e-only', action='store_true',
+                    help='run only the end-to-end model decode')
     ap.add_argument('--copy-calibration', type=int, default=0, metavar='MIB',
                     help='only copy a MIB-MiB device buffer three times (the '
                          'known-size kernel that scales rocprofv3 FETCH_SIZE '
@@ -312,6 +318,117 @@ def selector_timeline(torch, w, steps, plan):
               file=sys.stderr, flush=True)
 
 
+def qwen3_8b_config(ctx, new_tokens):
+    """Qwen3-8B architecture (36 layers, hidden 4096, MLP 12288, 32/8 heads,
+    head_dim 128, vocab 151936, RoPE theta 1e6)."""
+    from transformers import Qwen3Config
+    cfg = Qwen3Config(vocab_size=151936, hidden_size=4096, intermediate_size=12288,
+                      num_hidden_layers=36, num_attention_heads=32,
+                      num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6,
+                      rope_theta=1e6, tie_word_embeddings=False,
+                      max_position_embeddings=ctx + new_tokens + 64)
+    cfg._attn_implementation = 'sdpa'
+    return cfg
+
+
+def end_to_end(torch, args, device):
+    """Whole-model decode: random-init bf16 Qwen3-8B, dense prefill of
+    ``args.ctx`` seeded uniform token ids into the paged cache, 3 warm-up
+    steps, then ``args.e2e_steps`` greedy steps replayed from one captured
+    hipGraph each; HIP events around every ``GraphRunner.step``, median
+    TPOT (the steady-state time per output token)."""
+    from transformers import Qwen3ForCausalLM
+    from sparse_attn.engine.frozen_runner import (build_frozen_cache,
+                                                  prefill_frozen_request)
+    from sparse_attn.engine.graph_runner import GraphRunner
+    from sparse_attn.ops.paged_region_kernels_nfa import nfa_args
+    from sparse_attn.patches.patch import register_patch
+    from sparse_attn.policies.region_geometry import RegionGeometry
+    from sparse_attn.scheduler.scheduler import ContinuousBatchScheduler
+
+    warm = 3
+    new_tokens = warm + args.e2e_steps + 8
+    cfg = qwen3_8b_config(args.ctx, new_tokens)
+    t0 = time.perf_counter()
+    torch.manual_seed(args.seed)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            model = Qwen3ForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    fargs = nfa_args('tail')
+    fargs.tia_block_size = 16
+    n_patched = register_patch(model, fargs)
+    params = sum(p.numel() for p in model.parameters())
+    torch.cuda.synchronize()
+    print(f'# e2e model ready ({params / 1e9:.2f} B params) in '
+          f'{time.perf_counter() - t0:.1f}s', file=sys.stderr, flush=True)
+
+    geo = RegionGeometry(sink=4, near=4096, window=128, page=16,
+                         max_new_tokens=new_tokens)
+    cache = build_frozen_cache(model, geo, args.ctx, max_visible_len=1024)
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    ids = torch.randint(0, cfg.vocab_size, (1, args.ctx), generator=gen,
+                        device=device)
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    t0 = time.perf_counter()
+    with torch.no_grad(), sdpa_kernel([SDPBackend.FLASH_ATTENTION,
+                                       SDPBackend.EFFICIENT_ATTENTION]):
+        out, audit = prefill_frozen_request(model, ids, None, geo, cache=cache)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    print(f'# e2e prefill of {args.ctx} tokens: {prefill_s:.1f}s', file=sys.stderr,
+          flush=True)
+    rid = audit['request_id']
+    del ids
+    sched = ContinuousBatchScheduler(cache=cache, max_batch=1, eos_ids=(),
+                                     pad_token_id=0)
+    sched.add_request(rid)
+    sched.next_tokens[rid] = int(out.logits[0, -1].argmax())
+    del out
+    runner = GraphRunner(scheduler=sched, buckets=(1,), visible_buckets=(),
+                         device=device)
+    with torch.no_grad():
+        runner.capture_all(model, cache)
+        for i in range(warm):
+            runner.step(model, cache, generated_counts=i + 1)
+        torch.cuda.synchronize()
+        events = [(torch.cuda.Event(enable_timing=True),
+                   torch.cuda.Event(enable_timing=True))
+                  for _ in range(args.e2e_steps)]
+        t0 = time.perf_counter()
+        for i, (a, b) in enumerate(events):
+            a.record()
+            runner.step(model, cache, generated_counts=warm + i + 1)
+            b.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / args.e2e_steps
+    tpot = sorted(a.elapsed_time(b) for a, b in events)
+    med = tpot[len(tpot) // 2]
+    tokens = len(sched.flush_ready_receipts())
+    print(f'# e2e decode: median TPOT {med:.3f} ms, wall {wall_ms:.3f} ms/token',
+          file=sys.stderr, flush=True)
+    res = {
+        'model': 'Qwen3-8B architecture, random-init bf16 weights',
+        'params': params, 'patched_attention_layers': n_patched,
+        'prompt_tokens': args.ctx, 'prefill_s': round(prefill_s, 2),
+        'decode_steps': args.e2e_steps, 'warmup_steps': warm,
+        'tpot_ms_median': round(med, 4),
+        'tpot_ms_p10_p90': [round(tpot[len(tpot) // 10], 4),
+                            round(tpot[(len(tpot) * 9) // 10], 4)],
+        'wall_ms_per_token': round(wall_ms, 4),
+        'tok_s': round(1e3 / med, 2),
+        'graph_replays': runner.replay_count,
+        'graph_eager_fallbacks': runner.eager_fallback_count,
+        'receipts': tokens,
+    }
+    del runner, sched, model, cache
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(torch, w, seconds):
     """The CPU oracle on a bounded sample: layer-0 decode steps at the same
     128K context, single-threaded numpy."""
@@ -387,6 +504,18 @@ def main():
         print(json.dumps({'copy_bytes_read': n, 'copy_bytes_written': n,
                           'launches': 3}), flush=True)
         return
+    if args.e2e_only:
+        steps = args.e2e_steps or 256
+        args.e2e_steps = steps
+        e2e = end_to_end(torch, args, device)
+        print(json.dumps({
+            'metric': 'e2e decode tok/s at 128K ctx', 'value': e2e['tok_s'],
+            'unit': 'tok/s', 'n_gpus': 1, 'steps': steps, 'warmup': 3,
+            'ms_per_step': e2e['tpot_ms_median'], 'higher_is_better': True,
+            'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16',
+            'data': 'synthetic', 'config': {'workload': 'whole-model decode', **e2e},
+        }), flush=True)
+        return
     t_setup = time.perf_counter()
     w = build_workload(torch, args, device)
     cache = w.cache
@@ -449,6 +578,12 @@ def main():
     if not args.no_cpu_baseline:
         print('# cpu baseline ...', file=sys.stderr, flush=True)
         cpu = cpu_baseline(torch, w, args.cpu_seconds)
+    e2e = None
+    if args.e2e_steps > 0:
+        del graph, w, cache, outs
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        e2e = end_to_end(torch, args, device)
 
     result = {
         'metric': 'sparse-attn decode layer µs + e2e decode tok/s at 128K '
@@ -491,6 +626,7 @@ def main():
             'traffic': measured_traffic(args),
         },
         'cpu_baseline': cpu,
+        'e2e': e2e,
     }
     print(json.dumps(result), flush=True)
 

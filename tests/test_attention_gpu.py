@@ -17,10 +17,11 @@ DEV = 'cuda'
 GEO = RegionGeometry(sink=4, near=4096, window=128, page=16, max_new_tokens=64)
 
 
-def _setup(dtype, hkv=8, hq=32, max_vis=1024, rows=3, pages=400, seed=7):
+def _setup(dtype, hkv=8, hq=32, max_vis=1024, rows=3, pages=400, seed=7,
+           head_dim=128):
     cache = make_cache(DEV, geometry=GEO, max_blocks=64, max_physical_pages=pages,
                        max_visible_len=max_vis, hkv=hkv, hq=hq, dtype=dtype,
-                       max_requests=rows)
+                       max_requests=rows, head_dim=head_dim)
     gen = torch.Generator(device=DEV).manual_seed(seed)
     layer = cache.layers[0]
     layer.kv_pool_k.copy_(bf16_randn(layer.kv_pool_k.shape, gen, DEV).to(dtype))
@@ -79,3 +80,28 @@ def test_split_sizes_agree(split):
     q = bf16_randn((2, 8, 128), gen, DEV)
     q2r = torch.tensor([0, 1], dtype=torch.int32, device=DEV)
     _check(cache, q, gather, lens, q2r, 0.125, dtype, tokens_per_split=split)
+
+
+def test_wide_rows_take_several_chunks_per_workgroup():
+    """20000-slot rows: 625 chunks of 32 over at most 256 workgroups per row,
+    so each workgroup carries its running softmax over several chunks."""
+    dtype = torch.bfloat16
+    cache, gen, gather = _setup(dtype, rows=2, hkv=2, hq=8, max_vis=20000, pages=1400)
+    lens = torch.tensor([[20000, 8193], [12345, 0]], dtype=torch.int32, device=DEV)
+    gather[1, 0, 100:3000] = -1
+    q = bf16_randn((2, 8, 128), gen, DEV)
+    q2r = torch.tensor([0, 1], dtype=torch.int32, device=DEV)
+    got = _check(cache, q, gather, lens, q2r, 0.09, dtype)
+    assert np.all(got[1, 4:] == 0)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+def test_head_dim_64_group_8(dtype):
+    """head_dim 64 with 8 query heads per kv head: the merge stages fewer
+    splits in LDS (128 for bf16), so 5000-slot rows loop over chunks."""
+    cache, gen, gather = _setup(dtype, rows=2, hkv=2, hq=16, max_vis=5000,
+                                pages=400, head_dim=64)
+    lens = torch.tensor([[5000, 1000], [4097, 31]], dtype=torch.int32, device=DEV)
+    q = bf16_randn((2, 16, 64), gen, DEV).to(dtype)
+    q2r = torch.tensor([0, 1], dtype=torch.int32, device=DEV)
+    _check(cache, q, gather, lens, q2r, 64 ** -0.5, dtype)

@@ -4,9 +4,11 @@
 // sparse_attn/ops/paged_region_kernels.py:251-363 and :800-1006.
 //
 // Grid (nsplit, T * hkv), 256 threads.  Each workgroup owns one (query row,
-// kv head) and a contiguous chunk of at most 64 selected slots, handles the
-// G query heads of the group together (K/V rows are read once per group),
-// and writes an online-softmax partial (m, z, acc).  The last workgroup of
+// kv head) and the chunks split, split + nsplit, ... of at most 64 selected
+// slots (one chunk per workgroup at decode widths; any visible width is
+// covered with at most 256 workgroups per row), handles the G query heads of
+// the group together (K/V rows are read once per group), and writes an
+// online-softmax partial (m, z, acc).  The last workgroup of
 // the (row, kv) to arrive -- device-scope atomic counter, no waiting --
 // merges the partials and writes the output in the query dtype.
 //
@@ -39,9 +41,19 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p) {
   int split = p.tokens_per_split;
   if (split <= 0) split = 32;
   a.split = split;
-  a.nsplit = (p.max_vis + split - 1) / split;
-  if (a.nsplit < 1) a.nsplit = 1;
   const int G = p.hq / p.hkv;
+  // at most kMaxSplits workgroups per row, and no more than the merge can
+  // stage in the V tile's LDS (a maximum and a denominator per head and
+  // split); a workgroup takes every nsplit-th chunk of the row
+  int cap = kMaxSplits;
+  if (G > 0) {
+    const int kvb = p.kv_dtype == NFA_DTYPE_BF16 ? 2 : 4;
+    const int lds_cap = kSplitMax * p.head_dim_v * kvb / (8 * G);
+    if (lds_cap < cap) cap = lds_cap;
+  }
+  a.nsplit = (p.max_vis + split - 1) / split;
+  if (a.nsplit > cap) a.nsplit = cap;
+  if (a.nsplit < 1) a.nsplit = 1;
   a.part_stride = G * (p.head_dim_v + 2);
   int64_t w = 0;
   a.w_cnt = w;  w += ((int64_t)4 * a.rows + 255) & ~(int64_t)255;
@@ -86,7 +98,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   __shared__ float s_p[AGMAX * kSplitMax];  // scores, then exp weights
   __shared__ int s_slot[kSplitMax];
   __shared__ __align__(16) KV s_v[kSplitMax * D];
-  __shared__ float s_m[AGMAX], s_z[AGMAX];
+  __shared__ float s_m[AGMAX], s_z[AGMAX], s_f[AGMAX];
   __shared__ int s_last;
 
   unsigned char *ws = (unsigned char *)p.workspace;
@@ -101,113 +113,145 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     n = p.vis_lens[req * p.hkv + kh];
     if (n > p.max_vis) n = p.max_vis;
   }
-  const int c0 = split * ad.split;
-  int c1 = c0 + ad.split;
-  if (c1 > n) c1 = n;
-  const int cn = c1 > c0 ? c1 - c0 : 0;
-
-  if (cn > 0) {
+  // chunks split, split + nsplit, ... of ad.split slots each; the running
+  // (max, denominator, P.V) of the workgroup carries from chunk to chunk
+  const int c_first = split * ad.split;
+  const int c_step = ad.nsplit * ad.split;
+  if (c_first < n) {
     for (int i = tid; i < G * D; i += NFA_BLOCK)
       s_q[i] = load_any(p.q, ((int64_t)t * p.hq + kh * G) * D + i, p.q_dtype);
-    const int32_t *grow = p.gather + ((int64_t)req * p.hkv + kh) * p.max_vis;
-    // slots outside the arena are skipped like negative ones
-    const int max_slot = p.pool_pages * p.page;
-    for (int i = tid; i < cn; i += NFA_BLOCK) {
-      const int sl = grow[c0 + i];
-      s_slot[i] = sl < max_slot ? sl : -1;
-    }
   }
-  __syncthreads();
+  if (tid < G) {
+    s_m[tid] = kNegInf;
+    s_z[tid] = 0.0f;
+  }
+  constexpr int OPT = (AGMAX * (D / 2) + NFA_BLOCK - 1) / NFA_BLOCK;  // outputs per thread
+  float acc0[OPT], acc1[OPT];
+#pragma unroll
+  for (int k = 0; k < OPT; ++k) acc0[k] = acc1[k] = 0.0f;
 
-  // every K and V chunk of the split in flight at once
+  const int32_t *grow = req >= 0 ? p.gather + ((int64_t)req * p.hkv + kh) * p.max_vis
+                                 : nullptr;
+  // slots outside the arena are skipped like negative ones
+  const int max_slot = p.pool_pages * p.page;
   const int sc = tid % TPR;  // chunk of the row
   const int rr = tid / TPR;  // row within a pass
   const KV *kpool = (const KV *)p.k_pool;
   const KV *vpool = (const KV *)p.v_pool;
-  uint4 kr[PMAX], vr[PMAX];
-#pragma unroll
-  for (int pp = 0; pp < PMAX; ++pp) {
-    const int j = pp * RPP + rr;
-    const int slot = j < cn ? s_slot[j] : -1;
-    kr[pp] = make_uint4(0u, 0u, 0u, 0u);
-    vr[pp] = make_uint4(0u, 0u, 0u, 0u);
-    if (slot >= 0) {
-      const int64_t base =
-          (((int64_t)(slot / p.page) * p.hkv + kh) * p.page + slot % p.page) * D +
-          sc * CH;
-      kr[pp] = *reinterpret_cast<const uint4 *>(kpool + base);
-      vr[pp] = *reinterpret_cast<const uint4 *>(vpool + base);
+  for (int c0 = c_first; c0 < n; c0 += c_step) {
+    const int cn = n - c0 < ad.split ? n - c0 : ad.split;
+    __syncthreads();  // the previous chunk's LDS readers are done
+    for (int i = tid; i < cn; i += NFA_BLOCK) {
+      const int sl = grow[c0 + i];
+      s_slot[i] = sl < max_slot ? sl : -1;
     }
-  }
-  // scores: partial dot over the chunk, then a shuffle reduction over the
-  // TPR threads of the row
+    __syncthreads();
+
+    // every K and V chunk of the split in flight at once
+    uint4 kr[PMAX], vr[PMAX];
 #pragma unroll
-  for (int pp = 0; pp < PMAX; ++pp) {
-    if (pp * RPP >= cn) break;
-    const int j = pp * RPP + rr;
-    float x[CH];
-    unpack_chunk<KV>(kr[pp], x);
-    for (int g = 0; g < G; ++g) {
-      const float *q = s_q + g * D + sc * CH;
-      float part_s = 0.0f;
-#pragma unroll
-      for (int e = 0; e < CH; ++e) part_s = fmaf(q[e], x[e], part_s);
-#pragma unroll
-      for (int off = 1; off < TPR; off <<= 1)
-        part_s += __shfl_xor(part_s, off, 64);
-      if (sc == 0 && j < cn)
-        s_p[g * kSplitMax + j] = s_slot[j] >= 0 ? part_s * p.scale : kNegInf;
+    for (int pp = 0; pp < PMAX; ++pp) {
+      const int j = pp * RPP + rr;
+      const int slot = j < cn ? s_slot[j] : -1;
+      kr[pp] = make_uint4(0u, 0u, 0u, 0u);
+      vr[pp] = make_uint4(0u, 0u, 0u, 0u);
+      if (slot >= 0) {
+        const int64_t base =
+            (((int64_t)(slot / p.page) * p.hkv + kh) * p.page + slot % p.page) * D +
+            sc * CH;
+        kr[pp] = *reinterpret_cast<const uint4 *>(kpool + base);
+        vr[pp] = *reinterpret_cast<const uint4 *>(vpool + base);
+      }
     }
-  }
-  // stage V rows for P.V
+    // scores: partial dot over the chunk, then a shuffle reduction over the
+    // TPR threads of the row
 #pragma unroll
-  for (int pp = 0; pp < PMAX; ++pp) {
-    const int j = pp * RPP + rr;
-    if (j < cn) *reinterpret_cast<uint4 *>(s_v + j * D + sc * CH) = vr[pp];
+    for (int pp = 0; pp < PMAX; ++pp) {
+      if (pp * RPP >= cn) break;
+      const int j = pp * RPP + rr;
+      float x[CH];
+      unpack_chunk<KV>(kr[pp], x);
+      for (int g = 0; g < G; ++g) {
+        const float *q = s_q + g * D + sc * CH;
+        float part_s = 0.0f;
+#pragma unroll
+        for (int e = 0; e < CH; ++e) part_s = fmaf(q[e], x[e], part_s);
+#pragma unroll
+        for (int off = 1; off < TPR; off <<= 1)
+          part_s += __shfl_xor(part_s, off, 64);
+        if (sc == 0 && j < cn)
+          s_p[g * kSplitMax + j] = s_slot[j] >= 0 ? part_s * p.scale : kNegInf;
+      }
+    }
+    // stage V rows for P.V
+#pragma unroll
+    for (int pp = 0; pp < PMAX; ++pp) {
+      const int j = pp * RPP + rr;
+      if (j < cn) *reinterpret_cast<uint4 *>(s_v + j * D + sc * CH) = vr[pp];
+    }
+    __syncthreads();
+
+    // online softmax per head (one wave per head): new running max, the
+    // factor for what was accumulated so far, weights of this chunk
+    for (int g = w; g < G; g += NFA_WAVES) {
+      float m = kNegInf;
+      for (int i = lane; i < cn; i += 64) m = fmaxf(m, s_p[g * kSplitMax + i]);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+      const float m_old = s_m[g];
+      const float m_new = fmaxf(m_old, m);
+      float z = 0.0f;
+      for (int i = lane; i < cn; i += 64) {
+        const float sc2 = s_p[g * kSplitMax + i];
+        const float e = (m_new == kNegInf) ? 0.0f : __expf(sc2 - m_new);
+        s_p[g * kSplitMax + i] = e;
+        z += e;
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) z += __shfl_xor(z, off, 64);
+      if (lane == 0) {
+        const float f = m_old == kNegInf ? 0.0f : __expf(m_old - m_new);
+        s_f[g] = f;
+        s_m[g] = m_new;
+        s_z[g] = s_z[g] * f + z;
+      }
+    }
+    __syncthreads();
+
+    // P.V, one thread per (head, dim pair)
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+      const int o = tid + k * NFA_BLOCK;
+      if (o >= G * (D / 2)) break;
+      const int g = o / (D / 2);
+      const int d = 2 * (o % (D / 2));
+      const float f = s_f[g];
+      float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 4
+      for (int j = 0; j < cn; ++j) {
+        const float pr = s_p[g * kSplitMax + j];
+        float v0, v1;
+        lds_pair(s_v + j * D, d, &v0, &v1);
+        a0 = fmaf(pr, v0, a0);
+        a1 = fmaf(pr, v1, a1);
+      }
+      acc0[k] = acc0[k] * f + a0;
+      acc1[k] = acc1[k] * f + a1;
+    }
   }
   __syncthreads();
-
-  // softmax partial per head (one wave per head)
-  for (int g = w; g < G; g += NFA_WAVES) {
-    float m = kNegInf;
-    for (int i = lane; i < cn; i += 64) m = fmaxf(m, s_p[g * kSplitMax + i]);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    float z = 0.0f;
-    for (int i = lane; i < cn; i += 64) {
-      const float sc2 = s_p[g * kSplitMax + i];
-      const float e = (m == kNegInf) ? 0.0f : __expf(sc2 - m);
-      s_p[g * kSplitMax + i] = e;
-      z += e;
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) z += __shfl_xor(z, off, 64);
-    if (lane == 0) {
-      s_m[g] = m;
-      s_z[g] = z;
-    }
-  }
-  __syncthreads();
-
-  // P.V, one thread per (head, dim pair)
-  for (int o = tid; o < G * (D / 2); o += NFA_BLOCK) {
+  for (int k = 0; k < OPT; ++k) {
+    const int o = tid + k * NFA_BLOCK;
+    if (o >= G * (D / 2)) break;
     const int g = o / (D / 2);
     const int d = 2 * (o % (D / 2));
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll 4
-    for (int j = 0; j < cn; ++j) {
-      const float pr = s_p[g * kSplitMax + j];
-      float v0, v1;
-      lds_pair(s_v + j * D, d, &v0, &v1);
-      a0 = fmaf(pr, v0, a0);
-      a1 = fmaf(pr, v1, a1);
-    }
-    part[g * (D + 2) + 2 + d] = a0;
-    part[g * (D + 2) + 3 + d] = a1;
+    part[g * (D + 2) + 2 + d] = acc0[k];
+    part[g * (D + 2) + 3 + d] = acc1[k];
   }
   if (tid < G) {
-    part[tid * (D + 2) + 0] = cn > 0 ? s_m[tid] : kNegInf;
-    part[tid * (D + 2) + 1] = cn > 0 ? s_z[tid] : 0.0f;
+    part[tid * (D + 2) + 0] = s_m[tid];
+    part[tid * (D + 2) + 1] = s_z[tid];
   }
 
   // arrival; the last split of the (row, kv) merges
@@ -216,27 +260,28 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const float *base = (const float *)(ws + ad.w_part) +
                       (int64_t)row * ad.nsplit * ad.part_stride;
   // split maxima and denominators -> LDS (one round of loads)
-  float *s_ms = reinterpret_cast<float *>(s_v);  // [G][kMaxSplits]
-  float *s_zs = s_ms + AGMAX * kMaxSplits;        // [G][kMaxSplits]
-  for (int i = tid; i < G * ad.nsplit; i += NFA_BLOCK) {
-    const int g = i / ad.nsplit, sp = i % ad.nsplit;
+  const int ns = ad.nsplit;
+  float *s_ms = reinterpret_cast<float *>(s_v);  // [G][ns]
+  float *s_zs = s_ms + G * ns;                    // [G][ns]
+  for (int i = tid; i < G * ns; i += NFA_BLOCK) {
+    const int g = i / ns, sp = i % ns;
     const float *ps = base + (int64_t)sp * ad.part_stride + g * (D + 2);
-    s_ms[g * kMaxSplits + sp] = ps[0];
-    s_zs[g * kMaxSplits + sp] = ps[1];
+    s_ms[g * ns + sp] = ps[0];
+    s_zs[g * ns + sp] = ps[1];
   }
   __syncthreads();
   for (int i = tid; i < G * D; i += NFA_BLOCK) {
     const int g = i / D, d = i % D;
     float M = kNegInf;
-    for (int sp = 0; sp < ad.nsplit; ++sp) M = fmaxf(M, s_ms[g * kMaxSplits + sp]);
+    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, s_ms[g * ns + sp]);
     float Z = 0.0f, O = 0.0f;
     if (M != kNegInf) {
 #pragma unroll 8
-      for (int sp = 0; sp < ad.nsplit; ++sp) {
-        const float ms = s_ms[g * kMaxSplits + sp];
+      for (int sp = 0; sp < ns; ++sp) {
+        const float ms = s_ms[g * ns + sp];
         const float a = base[(int64_t)sp * ad.part_stride + g * (D + 2) + 2 + d];
         const float f = ms == kNegInf ? 0.0f : __expf(ms - M);
-        Z += s_zs[g * kMaxSplits + sp] * f;
+        Z += s_zs[g * ns + sp] * f;
         O += a * f;
       }
     }
@@ -288,11 +333,6 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
   }
   if (p->tokens_per_split < 0 || p->tokens_per_split > nfa::kSplitMax) {
     nfa_set_error("nfa_sparse_attn_decode: tokens_per_split must be in [0,64]");
-    return NFA_EINVAL;
-  }
-  if (nfa::attn_dims(*p).nsplit > nfa::kMaxSplits) {
-    nfa_set_error("nfa_sparse_attn_decode: %d splits exceed %d",
-                  nfa::attn_dims(*p).nsplit, nfa::kMaxSplits);
     return NFA_EINVAL;
   }
   if (!p->q || !p->k_pool || !p->v_pool || !p->gather || !p->vis_lens ||

@@ -659,6 +659,7 @@ class GraphReadyPagedRegionCache:
         batch = len(req_ids)
         self._staging_wait()
         self._cpu_slot_mapping_staging[:, :batch].fill_(PAD_SLOT)
+        self._cpu_query_to_req_staging.fill_(-1)  # tokens of padding rows
         self._cpu_active_req_ids_staging[:batch].fill_(self.INVALID_REQ_ID)
         self._cpu_valid_req_ids_staging[:batch].zero_()
         self._cpu_planned_lengths_staging[:batch].zero_()
@@ -839,6 +840,10 @@ class GraphReadyPagedRegionCache:
         if self.states:
             return max(s.logical_length for s in self.states.values())
         return 0
+
+    def get_query_offset(self, layer_idx=0):
+        """Position of the first query token: the tokens already cached."""
+        return self.get_seq_length(layer_idx)
 
     def get_mask_sizes(self, cache_position, layer_idx=0):
         query_len = (cache_position if isinstance(cache_position, int)

@@ -1,0 +1,103 @@
+"""Attach the NFA indexer and the paged-cache attention forward to a model.
+
+Reference: sparse_attn/patches/patch.py:28-132 (``register_patch``).  Same
+contract: every Qwen3 attention module (and, as in the reference's v1 tree,
+every Llama attention module) gets ``module.indexer`` built from ``args`` and
+its ``forward`` replaced on the instance (the original is kept in
+``_nfa_original_forward``); the number of patched modules is returned, and a
+sparse method that matches no module raises instead of silently running dense
+attention.  GLM-4.7 (absorbed latent attention) is not built here.
+"""
+from types import MethodType
+
+import torch.nn as nn
+
+from ..indexer import indexer_type_dict
+from ..indexer.nfa_indexer import NFAIndexer
+
+
+def _reject_removed_cache_args(args):
+    backend = getattr(args, 'nfa_far_skip_backend', 'legacy')
+    cache = getattr(args, 'nfa_far_skip_cache', 'retain')
+    if backend != 'legacy' or cache != 'retain':
+        raise ValueError(
+            'far-skip/static/batch cache paths have been removed; '
+            'only GraphReadyPagedRegionCache is supported '
+            '(nfa_far_skip_backend=legacy, nfa_far_skip_cache=retain)')
+
+
+def _attention_classes():
+    """(class, forward) pairs of the attention modules this build patches."""
+    from transformers.models.llama.modeling_llama import LlamaAttention
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3Attention
+    from .llama3_attn_patch import llama3_attn_forward
+    from .qwen3_attn_patch import qwen3_attn_forward
+    return ((Qwen3Attention, qwen3_attn_forward),
+            (LlamaAttention, llama3_attn_forward))
+
+
+def register_patch(model: nn.Module, args, snapshot=None,
+                   rmsnorm_decode: bool = False,
+                   mlp_silu_decode: bool = False) -> int:
+    """Patch the model's attention modules; returns how many were patched.
+
+    ``rmsnorm_decode`` / ``mlp_silu_decode`` also replace the decode-step
+    RMSNorm and SiLU-gate kernels of a Qwen3 model with fused HIP kernels.
+    """
+    _reject_removed_cache_args(args)
+    indexer_type = indexer_type_dict.get(args.method, None)
+    if args.method != 'none' and indexer_type is None:
+        raise ValueError(f'not support {args.method}')
+    if args.method != 'none' and any(
+            type(m).__name__ == 'Glm4MoeLiteAttention' for m in model.modules()):
+        raise ValueError('GLM-4.7 latent attention is not built in this package')
+
+    n_patched = 0
+    if indexer_type is not None:
+        classes = _attention_classes()
+        for name, module in model.named_modules():
+            forward = next((f for c, f in classes if isinstance(module, c)), None)
+            if forward is None:
+                continue
+            if snapshot is not None and indexer_type is NFAIndexer:
+                module.indexer = indexer_type(args, snapshot=snapshot)
+            else:
+                module.indexer = indexer_type(args)
+            module.indexer.head_dim = module.head_dim
+            if hasattr(module, 'layer_idx'):
+                module.indexer.layer_idx = module.layer_idx
+            if not hasattr(module, '_nfa_original_forward'):
+                module._nfa_original_forward = module.forward
+            module.forward = MethodType(forward, module)
+            n_patched += 1
+    model_type = getattr(getattr(model, 'config', None), 'model_type', None)
+    if (rmsnorm_decode or mlp_silu_decode) and n_patched:
+        if model_type != 'qwen3':
+            raise ValueError('fused decode RMSNorm / SiLU patches are Qwen3 only')
+        layers = model.config.num_hidden_layers
+        if rmsnorm_decode:
+            from .qwen3_rmsnorm_patch import register_rmsnorm_patch
+            register_rmsnorm_patch(model, expected=layers * 4 + 1)
+        if mlp_silu_decode:
+            from .qwen3_mlp_silu_patch import register_mlp_silu_patch
+            register_mlp_silu_patch(model, expected=layers)
+    if args.method != 'none' and n_patched == 0:
+        kinds = sorted({type(m).__name__ for _, m in model.named_modules()})
+        raise RuntimeError(
+            f'method={args.method!r} but the model has no Qwen3Attention or '
+            f'LlamaAttention module to patch (patched=0); running on would '
+            f'label dense output as sparse. Module types: {kinds[:8]}')
+    return n_patched
+
+
+def unregister_patch(model: nn.Module) -> int:
+    """Restore the original attention forwards; returns how many."""
+    n = 0
+    for module in model.modules():
+        original = getattr(module, '_nfa_original_forward', None)
+        if original is None:
+            continue
+        module.forward = original
+        del module._nfa_original_forward
+        n += 1
+    return n

@@ -1,0 +1,120 @@
+"""Qwen3 attention forward on the graph-ready paged cache.
+
+Reference: sparse_attn/patches/qwen3_attn_patch.py:22-196 (``qwen3_attn_forward``).
+Same contract: a prompt (more than one token per row) is written into the
+paged arena with ``write_prefill`` and attended densely by the model's own
+attention implementation; a decode step (one token per row) selects this
+layer's tokens from the current post-RoPE query with
+``select_topk_for_layer_batched`` — which also writes the current K/V — and
+attends to them with the sparse gather attention.  Both device steps are HIP
+kernels with fixed buffers, so the decode forward can be captured into a
+hipGraph.  Operator modes other than ``'off'`` (protected-set attention beside
+the middle selection) are not built and raise ``ValueError``.
+"""
+from typing import Optional
+
+import torch
+
+
+def _attention_interface(module):
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    from transformers.models.qwen3.modeling_qwen3 import eager_attention_forward
+    impl = module.config._attn_implementation
+    getter = getattr(ALL_ATTENTION_FUNCTIONS, 'get_interface', None)
+    if getter is not None:
+        return getter(impl, eager_attention_forward)
+    return ALL_ATTENTION_FUNCTIONS.get(impl, eager_attention_forward)
+
+
+def _check_cache(module, cache):
+    from ..cache import GraphReadyPagedRegionCache
+    from ..ops.selector_options import validate_selector_options
+    if getattr(module, 'layer_idx', 0) == 0:
+        capacity = cache.get_max_cache_shape() if cache is not None else None
+        validate_selector_options(
+            capacity if isinstance(capacity, int) and capacity > 0 else None)
+    if not isinstance(cache, GraphReadyPagedRegionCache):
+        raise ValueError(
+            'NFA requires GraphReadyPagedRegionCache; use prefill_frozen_request')
+
+
+def paged_prefill_attention(module, query_states, key_states, value_states,
+                            attention_mask, cache, input_shape, **kwargs):
+    """Write the prompt K/V into the arena, then dense causal attention."""
+    request_id = cache.active_request_id
+    if request_id is None:
+        raise ValueError('GraphReady prefill requires an active request id')
+    cache.write_prefill(module.layer_idx, request_id, key_states, value_states)
+    attention = _attention_interface(module)
+    attn_output, attn_weights = attention(
+        module, query_states, key_states, value_states, attention_mask,
+        dropout=0.0 if not module.training else module.attention_dropout,
+        scaling=module.scaling,
+        sliding_window=getattr(module, 'sliding_window', None),
+        **kwargs)
+    return module.o_proj(attn_output.reshape(*input_shape, -1).contiguous()), attn_weights
+
+
+def nfa_decode_attention(module, query_states, key_states, value_states, cache,
+                         input_shape):
+    """One decode token per row: select, write the current K/V, attend.
+
+    ``query_states`` ``[B, HQ, 1, D]`` and ``key_states`` / ``value_states``
+    ``[B, HKV, 1, D]`` are post-RoPE.  Returns the o_proj output
+    ``[B, 1, hidden]``.
+    """
+    from ..indexer.nfa_layer_batch_selector import select_topk_for_layer_batched
+    from ..ops.paged_region_kernels_nfa import decode_graph_ready
+
+    operator_mode = getattr(module.indexer.args, 'nfa_operator_mode', 'off')
+    if operator_mode != 'off':
+        raise ValueError(
+            f'NFA operator mode {operator_mode!r} is not built; use "off"')
+    batch = input_shape[0]
+    layer_idx = module.layer_idx
+    slot_mapping = cache.slot_mapping_for_layer(layer_idx)[:batch]
+    q_flat = query_states[:, :, 0]
+    select_topk_for_layer_batched(
+        cache, layer_idx, cache.active_req_ids, q_flat, attention=module,
+        decode_write=(key_states, value_states, slot_mapping))
+    result = decode_graph_ready(
+        module, q_flat, cache,
+        gather_indices=cache.gather_indices_for_layer(layer_idx),
+        visible_lens=cache.visible_lens_for_layer(layer_idx),
+        query_to_req=cache.query_to_req_buf)
+    return module.o_proj(result.reshape(*input_shape, -1).contiguous())
+
+
+def _rope(module, query_states, key_states, cos, sin):
+    from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb
+    return apply_rotary_pos_emb(query_states, key_states, cos, sin)
+
+
+def qwen3_attn_forward(
+    self,
+    hidden_states: torch.Tensor,
+    position_embeddings,
+    attention_mask: Optional[torch.Tensor],
+    past_key_values=None,
+    cache_position=None,
+    **kwargs,
+):
+    """Qwen3 attention with the single GraphReadyPagedRegionCache path."""
+    _check_cache(self, past_key_values)
+    input_shape = hidden_states.shape[:-1]
+    hidden_shape = (*input_shape, -1, self.head_dim)
+    query_states = self.q_norm(
+        self.q_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
+    key_states = self.k_norm(
+        self.k_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
+    value_states = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+    cos, sin = position_embeddings
+    query_states, key_states = _rope(self, query_states, key_states, cos, sin)
+
+    if input_shape[1] != 1:
+        return paged_prefill_attention(
+            self, query_states, key_states, value_states, attention_mask,
+            past_key_values, input_shape, **kwargs)
+    return nfa_decode_attention(
+        self, query_states, key_states, value_states, past_key_values,
+        input_shape), None
