@@ -55,6 +55,9 @@ def parse():
                     help='also run the whole Qwen3-8B-geometry model (random-init '
                          'bf16): dense prefill of --ctx tokens, then this many '
                          'greedy decode steps replayed from a hipGraph; 0 = off')
+    ap.add_argument('--e2e-unfused', action='store_true',
+                    help='end-to-end decode with HF\'s own dense layers (only the '
+                         'attention patched)')
     ap.add_argument('--e2e-only', action='store_true',
                     help='run only the end-to-end model decode')
     ap.add_argument('--copy-calibration', type=int, default=0, metavar='MIB',
@@ -360,7 +363,9 @@ def end_to_end(torch, args, device):
         torch.set_default_dtype(prev)
     fargs = nfa_args('tail')
     fargs.tia_block_size = 16
-    n_patched = register_patch(model, fargs)
+    fused = not args.e2e_unfused
+    n_patched = register_patch(model, fargs, rmsnorm_decode=fused,
+                               decode_layers=fused)
     params = sum(p.numel() for p in model.parameters())
     torch.cuda.synchronize()
     print(f'# e2e model ready ({params / 1e9:.2f} B params) in '
@@ -412,6 +417,7 @@ def end_to_end(torch, args, device):
           file=sys.stderr, flush=True)
     res = {
         'model': 'Qwen3-8B architecture, random-init bf16 weights',
+        'dense_layers': 'fused HIP decode layers' if fused else 'HF modules',
         'params': params, 'patched_attention_layers': n_patched,
         'prompt_tokens': args.ctx, 'prefill_s': round(prefill_s, 2),
         'decode_steps': args.e2e_steps, 'warmup_steps': warm,

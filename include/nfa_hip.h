@@ -170,8 +170,56 @@ typedef struct NfaAttnParams {
   int64_t workspace_bytes;
 } NfaAttnParams;
 
+/* Decode-step dense layers around the sparse attention (bf16 only). */
+#define NFA_EPI_PLAIN 0      /* y_s = x W_s^T for each segment s */
+#define NFA_EPI_RESIDUAL 1   /* y = residual + x W^T (one segment) */
+#define NFA_EPI_SILU_GATE 2  /* y = silu(x W_gate^T) * (x W_up^T), segments
+                                gate (0) and up (1) of equal rows */
+
+typedef struct NfaLinearParams {
+  int32_t abi_version;
+  int32_t struct_size;
+  int32_t m;                  /* activation rows (decode batch), 1..4 */
+  int32_t k;                  /* input features, multiple of 8; m*k*2 <= 48 KiB */
+  int32_t nseg;               /* weight segments sharing x, 1..3 */
+  int32_t epilogue;           /* NFA_EPI_* */
+  const void *x;              /* [m, k] bf16, rows x_stride elements apart */
+  int64_t x_stride;
+  const void *norm_weight;    /* [k] bf16, or NULL: when set, x is first
+                                 RMS-normalised as HF's RMSNorm */
+  float norm_eps;
+  float pad0;
+  const void *w[3];           /* [n_s, k] bf16 row-major (nn.Linear weight) */
+  int32_t n[3];
+  int32_t pad1;
+  void *y[3];                 /* [m, n_s] bf16, rows y_stride[s] apart */
+  int64_t y_stride[3];
+  const void *residual;       /* [m, n_0] bf16 (NFA_EPI_RESIDUAL) */
+  int64_t residual_stride;
+} NfaLinearParams;
+
+typedef struct NfaRopeParams {
+  int32_t abi_version;
+  int32_t struct_size;
+  int32_t batch, hq, hkv, head_dim;
+  const void *q;              /* [batch, hq*head_dim] bf16 rows (projection out) */
+  int64_t q_stride_b;
+  const void *k;              /* [batch, hkv*head_dim] bf16 rows */
+  int64_t k_stride_b;
+  const void *q_weight;       /* [head_dim] bf16 per-head RMSNorm weights, or */
+  const void *k_weight;       /*   both NULL (no q/k norm, e.g. Llama) */
+  float eps;
+  float pad0;
+  const void *cos, *sin;      /* [batch, head_dim] bf16 */
+  int64_t cs_stride_b;
+  void *q_out;                /* [batch, hq, head_dim] bf16 */
+  void *k_out;                /* [batch, hkv, head_dim] bf16 */
+} NfaRopeParams;
+
 /* ABI / diagnostics */
 int32_t nfa_abi_version(void);
+int32_t nfa_linear_params_size(void);
+int32_t nfa_rope_params_size(void);
 int32_t nfa_wall_clock_khz(void);   /* rate of the dbg_clock timestamps */
 int32_t nfa_select_params_size(void);
 int32_t nfa_attn_params_size(void);
@@ -202,6 +250,27 @@ int32_t nfa_paged_write_prefill(const void *keys, const void *values,
                                 int32_t head_dim_v, int32_t page,
                                 int32_t kv_dtype, void *k_pool, void *v_pool,
                                 void *stream);
+
+/* Decode linear layer (batch <= 4) with optional RMSNorm prologue and a
+   residual or SiLU-gate epilogue.  Replaces the decode-step projection
+   chain of HF's Qwen3/Llama decoder layer that the reference runs as vendor
+   GEMMs plus the fused RMSNorm of sparse_attn/ops/qwen3_rmsnorm_triton.py:
+   240-300 and the SiLU*up of sparse_attn/ops/qwen3_mlp_silu_triton.py:
+   102-130 (wired in by patches/qwen3_rmsnorm_patch.py:48 and
+   patches/qwen3_mlp_silu_patch.py:59). */
+int32_t nfa_decode_linear(const NfaLinearParams *p, void *stream);
+
+/* Per-head q/k RMSNorm (optional) and rotate-half RoPE of one decode token
+   per row.  Replaces qwen3_decode_rope, sparse_attn/ops/qwen3_rope_triton.py:
+   118-160, together with the q_norm/k_norm calls before it
+   (patches/qwen3_attn_patch.py:46-50). */
+int32_t nfa_qk_norm_rope_decode(const NfaRopeParams *p, void *stream);
+
+/* HF RMSNorm of `rows` rows of `dim` bf16 elements.  Replaces
+   fused_rmsnorm_decode, sparse_attn/ops/qwen3_rmsnorm_triton.py:240-300. */
+int32_t nfa_rmsnorm_decode(const void *x, int64_t x_stride, const void *weight,
+                           void *out, int64_t out_stride, int32_t rows,
+                           int32_t dim, float eps, void *stream);
 
 #ifdef __cplusplus
 }

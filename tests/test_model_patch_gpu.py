@@ -139,8 +139,9 @@ def _arena_rows(cache, layer_idx, rid, n):
     return k, v
 
 
-def _prefill(model, ids):
-    register_patch(model, _args())
+def _prefill(model, ids, fused=False):
+    register_patch(model, _args(), rmsnorm_decode=fused, mlp_silu_decode=fused,
+                   decode_layers=fused)
     with torch.no_grad():
         out, audit = prefill_frozen_request(model, ids, None, GEO)
     return out, out.past_key_values, audit['request_id']
@@ -232,15 +233,46 @@ def test_decode_step_selection_attention_and_logits(kind):
 
 
 @pytest.mark.parametrize('kind', ['qwen3', 'llama'])
-def test_graph_replay_matches_eager_steps(kind):
+def test_fused_decode_layers_match_unfused(kind):
+    """Seven-launch decoder layers against the layer-by-layer HF modules
+    (with the patched attention), fed the same tokens for three steps."""
+    fused = _tiny_model(kind)
+    plain = copy.deepcopy(fused)
+    gen = torch.Generator(device='cpu').manual_seed(17)
+    ids = torch.randint(0, 1024, (1, PROMPT), generator=gen).to(DEV)
+    out_f, cache_f, rid_f = _prefill(fused, ids, fused=True)
+    out_p, cache_p, rid_p = _prefill(plain, ids)
+    assert torch.equal(out_f.logits, out_p.logits)  # prefill is not fused
+    token = out_p.logits[:, -1].argmax(-1, keepdim=True)
+    for step in range(3):
+        print(f'# {kind} fused vs plain decode step {step}', flush=True)
+        pos = torch.full((1, 1), PROMPT + step, dtype=torch.long, device=DEV)
+        logits = []
+        for model, cache, rid in ((fused, cache_f, rid_f), (plain, cache_p, rid_p)):
+            cache.new_step([rid])
+            cache.plan_common([rid])
+            with torch.no_grad():
+                logits.append(model(input_ids=token, position_ids=pos,
+                                    past_key_values=cache, use_cache=True,
+                                    attention_mask=_mask_arg(model)).logits.float())
+            cache.commit_step()
+        diff = (logits[0] - logits[1]).abs().max().item()
+        scale = logits[1].abs().max().item()
+        assert diff <= 3e-2 * scale, (step, diff, scale)
+        token = logits[1][:, -1].argmax(-1, keepdim=True)
+
+
+@pytest.mark.parametrize('fused', [False, True])
+@pytest.mark.parametrize('kind', ['qwen3', 'llama'])
+def test_graph_replay_matches_eager_steps(kind, fused):
     steps = 6
     model = _tiny_model(kind)
     gen = torch.Generator(device='cpu').manual_seed(13)
     ids = torch.randint(0, 1024, (1, PROMPT), generator=gen).to(DEV)
     runs = {}
     for mode in ('eager', 'graph'):
-        print(f'# {kind} {mode} decode {steps} steps', flush=True)
-        out, cache, rid = _prefill(model, ids)
+        print(f'# {kind} fused={fused} {mode} decode {steps} steps', flush=True)
+        out, cache, rid = _prefill(model, ids, fused=fused)
         sched = ContinuousBatchScheduler(cache=cache, max_batch=1, eos_ids=(),
                                          pad_token_id=0, track_receipts=True)
         sched.add_request(rid)

@@ -79,11 +79,40 @@ class NfaAttnParams(ctypes.Structure):
     ]
 
 
+EPI_PLAIN = 0
+EPI_RESIDUAL = 1
+EPI_SILU_GATE = 2
+
+
+class NfaLinearParams(ctypes.Structure):
+    _fields_ = [
+        ('abi_version', _i32), ('struct_size', _i32),
+        ('m', _i32), ('k', _i32), ('nseg', _i32), ('epilogue', _i32),
+        ('x', _ptr), ('x_stride', _i64),
+        ('norm_weight', _ptr), ('norm_eps', _f32), ('pad0', _f32),
+        ('w', _ptr * 3), ('n', _i32 * 3), ('pad1', _i32),
+        ('y', _ptr * 3), ('y_stride', _i64 * 3),
+        ('residual', _ptr), ('residual_stride', _i64),
+    ]
+
+
+class NfaRopeParams(ctypes.Structure):
+    _fields_ = [
+        ('abi_version', _i32), ('struct_size', _i32),
+        ('batch', _i32), ('hq', _i32), ('hkv', _i32), ('head_dim', _i32),
+        ('q', _ptr), ('q_stride_b', _i64), ('k', _ptr), ('k_stride_b', _i64),
+        ('q_weight', _ptr), ('k_weight', _ptr), ('eps', _f32), ('pad0', _f32),
+        ('cos', _ptr), ('sin', _ptr), ('cs_stride_b', _i64),
+        ('q_out', _ptr), ('k_out', _ptr),
+    ]
+
+
 EXPORTS = (
     'nfa_abi_version', 'nfa_wall_clock_khz', 'nfa_select_params_size', 'nfa_attn_params_size',
     'nfa_last_error', 'nfa_select_workspace_bytes', 'nfa_attn_workspace_bytes',
     'nfa_select_layer', 'nfa_sparse_attn_decode', 'nfa_paged_write_decode',
-    'nfa_paged_write_prefill',
+    'nfa_paged_write_prefill', 'nfa_linear_params_size', 'nfa_rope_params_size',
+    'nfa_decode_linear', 'nfa_qk_norm_rope_decode', 'nfa_rmsnorm_decode',
 )
 
 _lib = None
@@ -127,12 +156,25 @@ def load_library(path: str = None):
         lib.nfa_paged_write_prefill.restype = _i32
         lib.nfa_paged_write_prefill.argtypes = [
             _ptr, _ptr, _i64, _ptr, _i32, _i32, _i32, _i32, _i32, _ptr, _ptr, _ptr]
+        lib.nfa_linear_params_size.restype = _i32
+        lib.nfa_rope_params_size.restype = _i32
+        lib.nfa_decode_linear.restype = _i32
+        lib.nfa_decode_linear.argtypes = [ctypes.POINTER(NfaLinearParams), _ptr]
+        lib.nfa_qk_norm_rope_decode.restype = _i32
+        lib.nfa_qk_norm_rope_decode.argtypes = [ctypes.POINTER(NfaRopeParams), _ptr]
+        lib.nfa_rmsnorm_decode.restype = _i32
+        lib.nfa_rmsnorm_decode.argtypes = [
+            _ptr, _i64, _ptr, _ptr, _i64, _i32, _i32, _f32, _ptr]
         if lib.nfa_abi_version() != ABI_VERSION:
             raise NativeError('libnfa_hip ABI version mismatch')
         if lib.nfa_select_params_size() != ctypes.sizeof(NfaSelectParams):
             raise NativeError('NfaSelectParams layout mismatch')
         if lib.nfa_attn_params_size() != ctypes.sizeof(NfaAttnParams):
             raise NativeError('NfaAttnParams layout mismatch')
+        if lib.nfa_linear_params_size() != ctypes.sizeof(NfaLinearParams):
+            raise NativeError('NfaLinearParams layout mismatch')
+        if lib.nfa_rope_params_size() != ctypes.sizeof(NfaRopeParams):
+            raise NativeError('NfaRopeParams layout mismatch')
         if path is None:
             _lib = lib
         return lib

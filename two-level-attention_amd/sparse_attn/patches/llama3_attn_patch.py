@@ -9,8 +9,8 @@ from typing import Optional
 
 import torch
 
-from .qwen3_attn_patch import (_check_cache, _rope, nfa_decode_attention,
-                               paged_prefill_attention)
+from .qwen3_attn_patch import (_check_cache, _decode_fusable, _rope, decode_qkv,
+                               nfa_decode_attention, paged_prefill_attention)
 
 
 def llama3_attn_forward(
@@ -25,6 +25,9 @@ def llama3_attn_forward(
     """Llama attention with the single GraphReadyPagedRegionCache path."""
     _check_cache(self, past_key_values)
     input_shape = hidden_states.shape[:-1]
+    if _decode_fusable(hidden_states):
+        q, k, v = decode_qkv(self, hidden_states, position_embeddings)
+        return nfa_decode_attention(self, q, k, v, past_key_values, input_shape), None
     hidden_shape = (*input_shape, -1, self.head_dim)
     query_states = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
     key_states = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)

@@ -38,11 +38,13 @@ def _attention_classes():
 
 def register_patch(model: nn.Module, args, snapshot=None,
                    rmsnorm_decode: bool = False,
-                   mlp_silu_decode: bool = False) -> int:
+                   mlp_silu_decode: bool = False,
+                   decode_layers: bool = False) -> int:
     """Patch the model's attention modules; returns how many were patched.
 
-    ``rmsnorm_decode`` / ``mlp_silu_decode`` also replace the decode-step
-    RMSNorm and SiLU-gate kernels of a Qwen3 model with fused HIP kernels.
+    ``rmsnorm_decode`` / ``mlp_silu_decode`` also move the decode-step
+    RMSNorm and MLP onto fused HIP kernels; ``decode_layers`` runs the whole
+    decoder layer's decode step as seven fused launches.
     """
     _reject_removed_cache_args(args)
     indexer_type = indexer_type_dict.get(args.method, None)
@@ -71,16 +73,20 @@ def register_patch(model: nn.Module, args, snapshot=None,
             module.forward = MethodType(forward, module)
             n_patched += 1
     model_type = getattr(getattr(model, 'config', None), 'model_type', None)
-    if (rmsnorm_decode or mlp_silu_decode) and n_patched:
-        if model_type != 'qwen3':
-            raise ValueError('fused decode RMSNorm / SiLU patches are Qwen3 only')
+    if (rmsnorm_decode or mlp_silu_decode or decode_layers) and n_patched:
+        if model_type not in ('qwen3', 'llama'):
+            raise ValueError('fused decode patches cover Qwen3 and Llama models')
         layers = model.config.num_hidden_layers
+        norms_per_layer = 4 if model_type == 'qwen3' else 2
         if rmsnorm_decode:
             from .qwen3_rmsnorm_patch import register_rmsnorm_patch
-            register_rmsnorm_patch(model, expected=layers * 4 + 1)
+            register_rmsnorm_patch(model, expected=layers * norms_per_layer + 1)
         if mlp_silu_decode:
             from .qwen3_mlp_silu_patch import register_mlp_silu_patch
             register_mlp_silu_patch(model, expected=layers)
+        if decode_layers:
+            from .decode_layer_patch import register_decode_layer_patch
+            register_decode_layer_patch(model, expected=layers)
     if args.method != 'none' and n_patched == 0:
         kinds = sorted({type(m).__name__ for _, m in model.named_modules()})
         raise RuntimeError(
@@ -91,7 +97,14 @@ def register_patch(model: nn.Module, args, snapshot=None,
 
 
 def unregister_patch(model: nn.Module) -> int:
-    """Restore the original attention forwards; returns how many."""
+    """Restore the original attention forwards (and undo the fused decode
+    patches); returns how many attention modules were restored."""
+    from .decode_layer_patch import unregister_decode_layer_patch
+    from .qwen3_mlp_silu_patch import unregister_mlp_silu_patch
+    from .qwen3_rmsnorm_patch import unregister_rmsnorm_patch
+    unregister_decode_layer_patch(model)
+    unregister_mlp_silu_patch(model)
+    unregister_rmsnorm_patch(model)
     n = 0
     for module in model.modules():
         original = getattr(module, '_nfa_original_forward', None)

@@ -6,8 +6,10 @@ paged arena with ``write_prefill`` and attended densely by the model's own
 attention implementation; a decode step (one token per row) selects this
 layer's tokens from the current post-RoPE query with
 ``select_topk_for_layer_batched`` — which also writes the current K/V — and
-attends to them with the sparse gather attention.  Both device steps are HIP
-kernels with fixed buffers, so the decode forward can be captured into a
+attends to them with the sparse gather attention.  For bf16 decode the q/k
+RMSNorm and RoPE run as one launch (the reference's qwen3_decode_rope,
+ops/qwen3_rope_triton.py:118, plus the two norms).  Every device step is a
+HIP kernel with fixed buffers, so the decode forward can be captured into a
 hipGraph.  Operator modes other than ``'off'`` (protected-set attention beside
 the middle selection) are not built and raise ``ValueError``.
 """
@@ -90,6 +92,33 @@ def _rope(module, query_states, key_states, cos, sin):
     return apply_rotary_pos_emb(query_states, key_states, cos, sin)
 
 
+def decode_qkv(module, hidden_states, position_embeddings):
+    """q/k/v of one decode token per row: projections, then per-head q/k
+    RMSNorm (when the module has q_norm/k_norm) and RoPE in one launch.
+    Returns ``q`` [B, HQ, 1, D], ``k``/``v`` [B, HKV, 1, D], post-RoPE."""
+    from ..ops.decode_fused import qk_norm_rope_decode
+    b = hidden_states.shape[0]
+    d = module.head_dim
+    q = module.q_proj(hidden_states).view(b, -1)
+    k = module.k_proj(hidden_states).view(b, -1)
+    v = module.v_proj(hidden_states).view(b, -1, 1, d)
+    hq, hkv = q.shape[1] // d, k.shape[1] // d
+    q_norm = getattr(module, 'q_norm', None)
+    k_norm = getattr(module, 'k_norm', None)
+    cos, sin = position_embeddings
+    q, k = qk_norm_rope_decode(
+        q, k, None if q_norm is None else q_norm.weight,
+        None if k_norm is None else k_norm.weight, cos, sin,
+        0.0 if q_norm is None else q_norm.variance_epsilon,
+        hq=hq, hkv=hkv, head_dim=d)
+    return q.view(b, hq, 1, d), k.view(b, hkv, 1, d), v
+
+
+def _decode_fusable(hidden_states):
+    return (hidden_states.dim() == 3 and hidden_states.shape[1] == 1
+            and hidden_states.dtype == torch.bfloat16 and hidden_states.is_cuda)
+
+
 def qwen3_attn_forward(
     self,
     hidden_states: torch.Tensor,
@@ -102,6 +131,9 @@ def qwen3_attn_forward(
     """Qwen3 attention with the single GraphReadyPagedRegionCache path."""
     _check_cache(self, past_key_values)
     input_shape = hidden_states.shape[:-1]
+    if _decode_fusable(hidden_states):
+        q, k, v = decode_qkv(self, hidden_states, position_embeddings)
+        return nfa_decode_attention(self, q, k, v, past_key_values, input_shape), None
     hidden_shape = (*input_shape, -1, self.head_dim)
     query_states = self.q_norm(
         self.q_proj(hidden_states).view(hidden_shape)).transpose(1, 2)
