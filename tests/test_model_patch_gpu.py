@@ -260,6 +260,9 @@ def test_fused_decode_layers_match_unfused(kind):
         scale = logits[1].abs().max().item()
         assert diff <= 3e-2 * scale, (step, diff, scale)
         token = logits[1][:, -1].argmax(-1, keepdim=True)
+    layers = fused.model.layers
+    assert all(getattr(l, '_nfa_fused_calls', 0) == 3 for l in layers)
+    assert not any(hasattr(l, '_nfa_fused_calls') for l in plain.model.layers)
 
 
 @pytest.mark.parametrize('fused', [False, True])
@@ -291,6 +294,8 @@ def test_graph_replay_matches_eager_steps(kind, fused):
             assert runner.replay_count == steps and runner.eager_fallback_count == 0
         else:
             assert runner.eager_fallback_count == steps
+        calls = [getattr(l, '_nfa_fused_calls', 0) for l in model.model.layers]
+        assert all(c > 0 for c in calls) == fused, calls
         assert cache.states[rid].logical_length == PROMPT + steps
         runs[mode] = (tokens, torch.stack(logits))
     assert runs['graph'][0] == runs['eager'][0]

@@ -31,6 +31,12 @@ def _decoder_layer_classes():
     return (Qwen3DecoderLayer, LlamaDecoderLayer)
 
 
+def is_silu(act):
+    """HF's SiLU activation module (``SiLUActivation``) or torch's."""
+    return (isinstance(act, torch.nn.SiLU) or type(act).__name__ == 'SiLUActivation') \
+        and not getattr(act, 'inplace', False)
+
+
 def _fusable(layer, hidden_states, cache):
     from ..cache import GraphReadyPagedRegionCache
     from ..ops.decode_fused import LINEAR_MAX_ROWS
@@ -44,7 +50,7 @@ def _fusable(layer, hidden_states, cache):
             and hidden_states.is_contiguous()
             and attn.q_proj.bias is None and attn.k_proj.bias is None
             and attn.v_proj.bias is None and attn.o_proj.bias is None
-            and isinstance(layer.mlp.act_fn, torch.nn.SiLU)
+            and is_silu(layer.mlp.act_fn)
             and layer.mlp.gate_proj.bias is None and layer.mlp.down_proj.bias is None)
 
 
@@ -62,6 +68,7 @@ def nfa_decode_layer_forward(self, hidden_states, attention_mask=None,
     from ..ops.decode_fused import decode_linear, qk_norm_rope_decode
     from ..ops.paged_region_kernels_nfa import decode_graph_ready
 
+    self._nfa_fused_calls = getattr(self, '_nfa_fused_calls', 0) + 1
     attn, mlp, cache = self.self_attn, self.mlp, past_key_values
     b, _, hidden = hidden_states.shape
     d = attn.head_dim

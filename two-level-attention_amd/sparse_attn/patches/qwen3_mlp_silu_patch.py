@@ -22,10 +22,12 @@ def _mlp_classes():
 
 def _mlp_forward(self, x):
     from ..ops.decode_fused import LINEAR_MAX_ROWS, decode_linear
-    if (isinstance(self.act_fn, torch.nn.SiLU) and x.dim() == 3 and x.shape[1] == 1
+    from .decode_layer_patch import is_silu
+    if (is_silu(self.act_fn) and x.dim() == 3 and x.shape[1] == 1
             and x.shape[0] <= LINEAR_MAX_ROWS and x.dtype == torch.bfloat16
             and x.is_cuda and x.is_contiguous() and self.gate_proj.bias is None
             and self.up_proj.bias is None and self.down_proj.bias is None):
+        self._nfa_fused_calls = getattr(self, '_nfa_fused_calls', 0) + 1
         b, _, h = x.shape
         a, = decode_linear(x.view(b, h), (self.gate_proj.weight, self.up_proj.weight),
                            silu_gate=True)
