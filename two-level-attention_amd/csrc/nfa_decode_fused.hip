@@ -134,33 +134,52 @@ __device__ __forceinline__ const uint4 *seg_row(const NfaLinearParams &p, int ro
   return nullptr;
 }
 
-// Dot products of two weight rows with every x row: acc[r][m] per lane.
-template <int MM>
-__device__ __forceinline__ void rows_dot(const uint4 *w0, const uint4 *w1, int nch,
-                                         const uint4 *s_x, float (&acc)[2][LIN_MMAX]) {
+// v when keep, else zeros (component-wise selects: a select of the whole
+// vector is lowered through scratch memory)
+__device__ __forceinline__ uint4 keep4(bool keep, const uint4 &v) {
+  return make_uint4(keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u);
+}
+
+// One iteration's weight chunks of two rows: chunk base + 64 j + lane of
+// each row, zeros past the row end or for a missing second row.  The loads
+// themselves are unconditional (clamped to the row's last chunk) so that all
+// of them are in flight before the first is waited for.  w0 is not null.
+__device__ __forceinline__ void load_iter(const uint4 *w0, const uint4 *w1, int base,
+                                          int nch, uint4 (&a)[LIN_CPI],
+                                          uint4 (&b)[LIN_CPI]) {
   const int lane = threadIdx.x & 63;
-  for (int base = 0; base < nch; base += LIN_ITER_CHUNKS) {
-    uint4 a[LIN_CPI], b[LIN_CPI];
+  const uint4 *p1 = w1 ? w1 : w0;
 #pragma unroll
-    for (int j = 0; j < LIN_CPI; ++j) {
-      const int c = base + j * 64 + lane;
-      a[j] = make_uint4(0u, 0u, 0u, 0u);
-      b[j] = make_uint4(0u, 0u, 0u, 0u);
-      if (c < nch) {
-        if (w0) a[j] = w0[c];
-        if (w1) b[j] = w1[c];
-      }
-    }
+  for (int j = 0; j < LIN_CPI; ++j) {
+    const int c = base + j * 64 + lane;
+    const int cc = c < nch ? c : nch - 1;
+    a[j] = w0[cc];
+    b[j] = p1[cc];
+  }
 #pragma unroll
-    for (int j = 0; j < LIN_CPI; ++j) {
-      const int c = base + j * 64 + lane;
-      if (c >= nch) break;
+  for (int j = 0; j < LIN_CPI; ++j) {
+    const bool in = base + j * 64 + lane < nch;
+    a[j] = keep4(in, a[j]);
+    b[j] = keep4(in && w1, b[j]);
+  }
+}
+
+// Multiply-add one iteration's chunks with every x row: acc[r][m] per lane.
+template <int MM>
+__device__ __forceinline__ void dot_iter(const uint4 (&a)[LIN_CPI],
+                                         const uint4 (&b)[LIN_CPI], int base, int nch,
+                                         const uint4 *s_x,
+                                         float (&acc)[2][LIN_MMAX]) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-      for (int m = 0; m < MM; ++m) {
-        const uint4 xv = s_x[m * nch + c];
-        acc[0][m] = dot8(a[j], xv, acc[0][m]);
-        acc[1][m] = dot8(b[j], xv, acc[1][m]);
-      }
+  for (int j = 0; j < LIN_CPI; ++j) {
+    const int c = base + j * 64 + lane;
+    if (c >= nch) break;
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      const uint4 xv = s_x[m * nch + c];
+      acc[0][m] = dot8(a[j], xv, acc[0][m]);
+      acc[1][m] = dot8(b[j], xv, acc[1][m]);
     }
   }
 }
@@ -175,44 +194,54 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   extern __shared__ uint4 s_x[];
   __shared__ float s_red[NFA_WAVES];
   const int nch = p.k / 8;
-  stage_x<NORM>(p, nch, s_x, s_red);
-
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int unit = blockIdx.x * LIN_WAVES + wv;  // wave's unit of work
+  const int unit = blockIdx.x * LIN_WAVES + (threadIdx.x >> 6);  // wave's work
+
+  // the wave's two weight rows: gate and up row `unit` (SiLU gate), else rows
+  // 2 unit and 2 unit + 1 of the concatenated segments
+  const uint4 *w0 = nullptr, *w1 = nullptr;
+  int seg[2] = {-1, -1}, loc[2] = {0, 0};
+  if (EPI == NFA_EPI_SILU_GATE) {
+    if (unit < p.n[0]) {
+      w0 = reinterpret_cast<const uint4 *>((const uint16_t *)p.w[0] + (int64_t)unit * p.k);
+      w1 = reinterpret_cast<const uint4 *>((const uint16_t *)p.w[1] + (int64_t)unit * p.k);
+    }
+  } else {
+    w0 = seg_row(p, unit * 2, &seg[0], &loc[0]);
+    w1 = seg_row(p, unit * 2 + 1, &seg[1], &loc[1]);
+  }
+  // Without a norm prologue the first weight chunks are in flight while the
+  // activations are staged; with one, the registers they would hold through
+  // the norm cost more occupancy than the overlap gains.
+  uint4 a[LIN_CPI], b[LIN_CPI];
+  if (!NORM && w0) load_iter(w0, w1, 0, nch, a, b);
+  stage_x<NORM>(p, nch, s_x, s_red);
+  if (!w0) return;
+  if (NORM) load_iter(w0, w1, 0, nch, a, b);
+
   float acc[2][LIN_MMAX];
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int m = 0; m < LIN_MMAX; ++m) acc[r][m] = 0.0f;
+  dot_iter<MM>(a, b, 0, nch, s_x, acc);
+  for (int base = LIN_ITER_CHUNKS; base < nch; base += LIN_ITER_CHUNKS) {
+    load_iter(w0, w1, base, nch, a, b);
+    dot_iter<MM>(a, b, base, nch, s_x, acc);
+  }
 
   if (EPI == NFA_EPI_SILU_GATE) {
-    // one output row per wave: row `unit` of the gate and of the up weight
-    const int row = unit;
-    if (row >= p.n[0]) return;
-    const uint4 *wg = reinterpret_cast<const uint4 *>((const uint16_t *)p.w[0] +
-                                                      (int64_t)row * p.k);
-    const uint4 *wu = reinterpret_cast<const uint4 *>((const uint16_t *)p.w[1] +
-                                                      (int64_t)row * p.k);
-    rows_dot<MM>(wg, wu, nch, s_x, acc);
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
       const float g = bf16r(wave_sum(acc[0][m]));
       const float u = bf16r(wave_sum(acc[1][m]));
       if (lane == m) {
         const float act = bf16r(g / (1.0f + expf(-g)));
-        ((uint16_t *)p.y[0])[(int64_t)m * p.y_stride[0] + row] = bf16_bits(act * u);
+        ((uint16_t *)p.y[0])[(int64_t)m * p.y_stride[0] + unit] = bf16_bits(act * u);
       }
     }
     return;
   }
-  // two output rows per wave, anywhere in the concatenated segments
-  const int row0 = unit * 2;
-  int seg[2], loc[2];
-  const uint4 *w0 = seg_row(p, row0, &seg[0], &loc[0]);
-  const uint4 *w1 = seg_row(p, row0 + 1, &seg[1], &loc[1]);
-  if (!w0) return;
-  rows_dot<MM>(w0, w1, nch, s_x, acc);
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     if (seg[r] < 0) break;
