@@ -51,7 +51,7 @@ def parse():
     ap.add_argument('--seed', type=int, default=20261201)
     ap.add_argument('--timeline', type=int, default=0,
                     help='print selector phase timings of N extra decode steps')
-    ap.add_argument('--e2e-steps', type=int, default=0,
+    ap.add_argument('--e2e-steps', type=int, default=256,
                     help='also run the whole Qwen3-8B-geometry model (random-init '
                          'bf16): dense prefill of --ctx tokens, then this many '
                          'greedy decode steps replayed from a hipGraph; 0 = off')
