@@ -76,7 +76,9 @@ __device__ __forceinline__ void lds_pair(const float *v, int d, float *a,
   *b = x.y;
 }
 
-template <typename KV, int TPR>
+// LOOP: a workgroup may own several chunks (rows wider than nsplit chunks);
+// without it every workgroup owns at most one and nothing is carried.
+template <typename KV, int TPR, bool LOOP>
 __global__ void __launch_bounds__(NFA_BLOCK)
     nfa_attn_kernel(const NfaAttnParams p) {
   constexpr int CH = Elem<KV>::kChunk;  // dims per 16-byte chunk
@@ -140,7 +142,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const KV *vpool = (const KV *)p.v_pool;
   for (int c0 = c_first; c0 < n; c0 += c_step) {
     const int cn = n - c0 < ad.split ? n - c0 : ad.split;
-    __syncthreads();  // the previous chunk's LDS readers are done
+    if (LOOP && c0 != c_first) __syncthreads();  // the previous chunk's readers are done
     for (int i = tid; i < cn; i += NFA_BLOCK) {
       const int sl = grow[c0 + i];
       s_slot[i] = sl < max_slot ? sl : -1;
@@ -225,7 +227,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       if (o >= G * (D / 2)) break;
       const int g = o / (D / 2);
       const int d = 2 * (o % (D / 2));
-      const float f = s_f[g];
+      const float f = LOOP ? s_f[g] : 0.0f;
       float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll 4
       for (int j = 0; j < cn; ++j) {
@@ -235,15 +237,25 @@ __global__ void __launch_bounds__(NFA_BLOCK)
         a0 = fmaf(pr, v0, a0);
         a1 = fmaf(pr, v1, a1);
       }
-      acc0[k] = acc0[k] * f + a0;
-      acc1[k] = acc1[k] * f + a1;
+      if (LOOP) {
+        acc0[k] = acc0[k] * f + a0;
+        acc1[k] = acc1[k] * f + a1;
+      } else {
+        part[g * (D + 2) + 2 + d] = a0;
+        part[g * (D + 2) + 3 + d] = a1;
+      }
     }
+    if (!LOOP) break;
   }
-  __syncthreads();
+  // s_m / s_z of a head were last written before the barrier that precedes
+  // the P.V step (or, with no chunk, by the same thread that reads them)
+  // (a single-chunk workgroup stored its P.V above; one with no chunk
+  // stores zeros here)
+  const bool store_acc = LOOP || c_first >= n;
 #pragma unroll
   for (int k = 0; k < OPT; ++k) {
     const int o = tid + k * NFA_BLOCK;
-    if (o >= G * (D / 2)) break;
+    if (!store_acc || o >= G * (D / 2)) break;
     const int g = o / (D / 2);
     const int d = 2 * (o % (D / 2));
     part[g * (D + 2) + 2 + d] = acc0[k];
@@ -349,8 +361,16 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
   dim3 grid(ad.nsplit, ad.rows);
   hipStream_t s = (hipStream_t)stream;
   const bool bf = p->kv_dtype == NFA_DTYPE_BF16;
-#define NFA_ATTN_LAUNCH(KV, TPR) \
-  hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR>), grid, dim3(NFA_BLOCK), 0, s, *p)
+  const bool loop = (int64_t)ad.nsplit * ad.split < p->max_vis;
+#define NFA_ATTN_LAUNCH(KV, TPR)                                                       \
+  do {                                                                               \
+    if (loop)                                                                        \
+      hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, true>), grid,                \
+                         dim3(NFA_BLOCK), 0, s, *p);                                 \
+    else                                                                             \
+      hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, false>), grid,               \
+                         dim3(NFA_BLOCK), 0, s, *p);                                 \
+  } while (0)
   if (tpr == 8) {
     if (bf) NFA_ATTN_LAUNCH(uint16_t, 8); else NFA_ATTN_LAUNCH(float, 8);
   } else if (tpr == 16) {
