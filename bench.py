@@ -43,6 +43,11 @@ def parse():
     ap.add_argument('--steps', type=int, default=200)
     ap.add_argument('--warmup', type=int, default=5)
     ap.add_argument('--ctx', type=int, default=131072)
+    ap.add_argument('--batch', type=int, default=1,
+                    help='decode rows (requests) sharing one cache per layer')
+    ap.add_argument('--ragged', type=int, nargs=2, metavar=('LO', 'HI'),
+                    help='request lengths drawn uniformly from [LO, HI] (seeded) '
+                         'instead of --ctx for every request')
     ap.add_argument('--layers', type=int, default=36)
     ap.add_argument('--kernel-rounds', type=int, default=20)
     ap.add_argument('--cpu-seconds', type=float, default=15.0,
@@ -92,35 +97,45 @@ def build_workload(torch, args, device):
     new_tokens = args.warmup + args.steps + args.kernel_rounds + args.timeline + 8
     geo = RegionGeometry(sink=4, near=4096, window=128, page=page,
                          max_new_tokens=new_tokens)
-    pages = (args.ctx + new_tokens + page - 1) // page
+    b = args.batch
+    if args.ragged:
+        lo, hi = args.ragged
+        g = torch.Generator().manual_seed(args.seed)
+        lengths = torch.randint(lo, hi + 1, (b,), generator=g).tolist()
+    else:
+        lengths = [args.ctx] * b
+    pages = [(n + new_tokens + page - 1) // page for n in lengths]
     cache = GraphReadyPagedRegionCache(
-        args.layers, geo, max_requests=1, max_physical_pages=pages + 1,
-        max_blocks=pages + 8, max_visible_len=1024, max_query_tokens=1,
+        args.layers, geo, max_requests=b, max_physical_pages=sum(pages) + 1,
+        max_blocks=max(pages) + 8, max_visible_len=1024, max_query_tokens=b,
         num_kv_heads=hkv, num_query_heads=hq, head_dim_k=d, head_dim_v=d,
         dtype=torch.bfloat16, device=device)
     fargs = nfa_args('tail')
     fargs.tia_block_size = page
     indexer = NFAIndexer(fargs)
     gen = torch.Generator(device=device).manual_seed(args.seed)
-    cache.add_request(0)
-    for layer in range(args.layers):
-        keys = synthetic_keys(torch, args.ctx, hkv, d, gen, device)
-        values = torch.randn(1, hkv, args.ctx, d, generator=gen,
-                             device=device).to(torch.bfloat16)
-        cache.write_prefill(layer, 0, keys, values)
-        del keys, values
-    cache.freeze(0, [False] * args.layers, [False] * args.layers)
+    req_ids = list(range(b))
+    for rid, n in zip(req_ids, lengths):
+        cache.add_request(rid)
+        for layer in range(args.layers):
+            keys = synthetic_keys(torch, n, hkv, d, gen, device)
+            values = torch.randn(1, hkv, n, d, generator=gen,
+                                 device=device).to(torch.bfloat16)
+            cache.write_prefill(layer, rid, keys, values)
+            del keys, values
+        cache.freeze(rid, [False] * args.layers, [False] * args.layers)
     attn = [SimpleNamespace(indexer=indexer, scaling=d ** -0.5, layer_idx=l)
             for l in range(args.layers)]
-    q = [torch.randn(1, hq, d, generator=gen, device=device).to(torch.bfloat16)
+    q = [torch.randn(b, hq, d, generator=gen, device=device).to(torch.bfloat16)
          for _ in range(args.layers)]
-    kn = [torch.randn(1, hkv, 1, d, generator=gen, device=device).to(torch.bfloat16)
+    kn = [torch.randn(b, hkv, 1, d, generator=gen, device=device).to(torch.bfloat16)
           for _ in range(args.layers)]
-    vn = [torch.randn(1, hkv, 1, d, generator=gen, device=device).to(torch.bfloat16)
+    vn = [torch.randn(b, hkv, 1, d, generator=gen, device=device).to(torch.bfloat16)
           for _ in range(args.layers)]
     torch.cuda.synchronize()
     return SimpleNamespace(cache=cache, indexer=indexer, attn=attn, q=q, kn=kn,
-                           vn=vn, hkv=hkv, hq=hq, d=d, page=page)
+                           vn=vn, hkv=hkv, hq=hq, d=d, page=page, req_ids=req_ids,
+                           lengths=lengths)
 
 
 def run_layer(w, layer, outs):
@@ -129,9 +144,9 @@ def run_layer(w, layer, outs):
     from sparse_attn.ops.paged_region_kernels_nfa import decode_graph_ready
     cache = w.cache
     select_topk_for_layer_batched(
-        cache, layer, [0], w.q[layer], attention=w.attn[layer],
+        cache, layer, w.req_ids, w.q[layer], attention=w.attn[layer],
         decode_write=(w.kn[layer], w.vn[layer],
-                      cache.slot_mapping_for_layer(layer)[:1]))
+                      cache.slot_mapping_for_layer(layer)[:len(w.req_ids)]))
     outs[layer] = decode_graph_ready(w.attn[layer], w.q[layer], cache)
 
 
@@ -176,7 +191,7 @@ def measured_traffic(args):
     """HBM bytes per selector launch at this workload, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None when absent or when the
     workload differs from the profiled one)."""
-    if args.ctx != 131072:
+    if args.ctx != 131072 or args.batch != 1 or args.ragged:
         return None
     path = os.path.join(ROOT, 'profiles', 'nfa_select_layer_128k_hbm_traffic.md')
     try:
@@ -218,9 +233,9 @@ def time_kernels(torch, w, rounds, plan):
     def sel_all():
         for layer in range(layers):
             select_topk_for_layer_batched(
-                cache, layer, [0], w.q[layer], attention=w.attn[layer],
+                cache, layer, w.req_ids, w.q[layer], attention=w.attn[layer],
                 decode_write=(w.kn[layer], w.vn[layer],
-                              cache.slot_mapping_for_layer(layer)[:1]))
+                              cache.slot_mapping_for_layer(layer)[:len(w.req_ids)]))
 
     def att_all():
         for layer in range(layers):
@@ -242,10 +257,10 @@ def time_kernels(torch, w, rounds, plan):
     cache.commit_step()
     torch.cuda.synchronize()
     sel, att = [], []
-    length = 0
+    lengths = []
     for _ in range(rounds):
         plan()
-        length = int(cache.pending_lengths[0])
+        lengths = [int(cache.pending_lengths[r]) for r in w.req_ids]
         a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
         a.record()
         g_sel.replay()
@@ -261,7 +276,7 @@ def time_kernels(torch, w, rounds, plan):
     mean = lambda v: sum(v) / len(v)
     return dict(select_us=mean(sel), attention_us=mean(att),
                 select_us_median=sel[len(sel) // 2],
-                attention_us_median=att[len(att) // 2], length=length)
+                attention_us_median=att[len(att) // 2], lengths=lengths)
 
 
 def selector_timeline(torch, w, steps, plan):
@@ -278,9 +293,9 @@ def selector_timeline(torch, w, steps, plan):
         for layer in range(len(w.q)):
             dbg = {'clock_only': True}
             select_topk_for_layer_batched(
-                cache, layer, [0], w.q[layer], attention=w.attn[layer],
+                cache, layer, w.req_ids, w.q[layer], attention=w.attn[layer],
                 decode_write=(w.kn[layer], w.vn[layer],
-                              cache.slot_mapping_for_layer(layer)[:1]),
+                              cache.slot_mapping_for_layer(layer)[:len(w.req_ids)]),
                 _debug=dbg)
             tiles.append(dbg['clock'])
         cache.commit_step()
@@ -530,8 +545,8 @@ def main():
           flush=True)
 
     def plan():
-        cache.new_step([0])
-        cache.plan_common([0])
+        cache.new_step(w.req_ids)
+        cache.plan_common(w.req_ids)
 
     # warm-up: first step rebuilds page statistics, later ones are incremental
     for _ in range(args.warmup):
@@ -574,18 +589,22 @@ def main():
         selector_timeline(torch, w, args.timeline, plan)
     # per-kernel durations (events around each launch), same stream
     kt = time_kernels(torch, w, args.kernel_rounds, plan)
-    nbytes = algorithmic_bytes(w, kt['length'])
+    per_req = [algorithmic_bytes(w, n) for n in kt['lengths']]
+    nbytes = {k: sum(b[k] for b in per_req) for k in ('select', 'attention')}
     sel_gbs = nbytes['select'] / (kt['select_us'] * 1e-6) / 1e9
     att_gbs = nbytes['attention'] / (kt['attention_us'] * 1e-6) / 1e9
     layer_us = ms_per_step * 1e3 / args.layers
     layer_gbs = (nbytes['select'] + nbytes['attention']) / (layer_us * 1e-6) / 1e9
 
+    single = args.batch == 1 and not args.ragged
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and single:
         print('# cpu baseline ...', file=sys.stderr, flush=True)
         cpu = cpu_baseline(torch, w, args.cpu_seconds)
+    geometry = {'heads': [w.hq, w.hkv], 'head_dim': w.d, 'page': w.page}
+    lengths = list(w.lengths)
     e2e = None
-    if args.e2e_steps > 0:
+    if args.e2e_steps > 0 and single:
         del graph, w, cache, outs
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
@@ -594,7 +613,7 @@ def main():
     result = {
         'metric': 'sparse-attn decode layer µs + e2e decode tok/s at 128K '
                   'ctx; % of HBM peak',
-        'value': round(1e3 / ms_per_step, 2),
+        'value': round(args.batch * 1e3 / ms_per_step, 2),
         'unit': 'tok/s',
         'n_gpus': 1,
         'steps': args.steps,
@@ -606,11 +625,15 @@ def main():
         'dtype': 'bf16',
         'data': 'synthetic',
         'config': {
-            'workload': 'NFA sparse-attention decode hot path (selector + '
-                        'attention) of all 36 layers, Qwen3-8B attention '
-                        'geometry, batch 1, 128K context, page 16, hipGraph',
-            'layers': args.layers, 'context': args.ctx, 'batch': 1,
-            'heads': [w.hq, w.hkv], 'head_dim': w.d, 'page': w.page,
+            'workload': f'NFA sparse-attention decode hot path (selector + '
+                        f'attention) of {args.layers} layers, Qwen3-8B attention '
+                        f'geometry, batch {args.batch}, '
+                        + (f'contexts U({args.ragged[0]}, {args.ragged[1]})'
+                           if args.ragged else f'{args.ctx // 1024}K context')
+                        + ', page 16, hipGraph',
+            'layers': args.layers, 'batch': args.batch,
+            'context': (lengths if args.ragged else args.ctx),
+            **geometry,
             'nfa': 'far minmax / near avg, K1 128 (32 near), near_len 4096, '
                    'tail dims cmp 4, sink 4, SWA 128, K2 1024',
             'layer_us': round(layer_us, 3),

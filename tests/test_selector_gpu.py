@@ -142,7 +142,8 @@ def _prod_cache(lengths, *, hkv=2, hq=8, dtype=torch.bfloat16, max_req=4,
     phys = sum((n + extra + page - 1) // page for n in lengths) + 8
     cache = make_cache(DEV, geometry=geometry, max_blocks=max_blocks,
                        max_physical_pages=phys, max_visible_len=1024, hkv=hkv,
-                       hq=hq, dtype=dtype, max_requests=max_req)
+                       hq=hq, dtype=dtype, max_requests=max_req,
+                       max_query_tokens=max(8, max_req))
     gen = torch.Generator(device=DEV).manual_seed(seed)
     req_ids = req_ids or list(range(len(lengths)))
     skips = skips or [(False, False)] * len(lengths)
@@ -162,6 +163,36 @@ def test_production_flags_bit_exact(lengths):
     q = bf16_randn((b, cache.num_query_heads, 128), gen, DEV)
     decode = _decode_inputs(cache, b, gen, torch.bfloat16)
     run_and_compare(cache, indexer, req_ids, q, decode, scaling=0.08838834764831845)
+
+
+def test_sixteen_ragged_requests():
+    """The batched decode shape: 16 requests of ragged lengths in one cache."""
+    lengths = torch.randint(3000, 24001, (16,),
+                            generator=torch.Generator().manual_seed(16)).tolist()
+    cache, gen, req_ids = _prod_cache(lengths, max_req=16)
+    indexer = make_indexer()
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = bf16_randn((16, cache.num_query_heads, 128), gen, DEV)
+    decode = _decode_inputs(cache, 16, gen, torch.bfloat16)
+    run_and_compare(cache, indexer, req_ids, q, decode, scaling=0.08838834764831845)
+
+
+def test_one_million_token_context():
+    """1M-token row (plus 8192, so that the near pool's pages have ids past
+    16 bits): 66048 pages over several dispatch rounds of tiles, the L1
+    top-k over every page."""
+    cache, gen, req_ids = _prod_cache([(1 << 20) + 8192], hkv=1, hq=4, max_req=1)
+    indexer = make_indexer()
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = bf16_randn((1, 4, 128), gen, DEV)
+    decode = _decode_inputs(cache, 1, gen, torch.bfloat16)
+    print('# 1M context: selector + oracle', flush=True)
+    res = run_and_compare(cache, indexer, req_ids, q, decode,
+                          scaling=0.08838834764831845)
+    assert res[0][0].vis_len == 1024
+    assert int(res[0][0].i_n.min()) > 65535  # near pages past 16-bit ids
 
 
 @pytest.mark.parametrize('side_copy', [True, False])

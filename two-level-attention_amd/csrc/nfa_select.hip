@@ -73,7 +73,7 @@ struct SelDims {
   int a_hist, a_tmp, a_misc, a_clk, a_qf, a_qs, a_qg, a_fdims;
   int a_dims, a_last, a_tphys, a_stage, a_hs, a_st;    // tile
   int a_pages, a_pphys;                                // tail
-  int a_keys, a_cbits, a_eqb, a_dbf, a_dbn, a_dsel;    // tail, L1
+  int a_keys, a_dbf, a_dbn, a_dsel;                    // tail, L1
   int a_dk, a_l0, a_l0x, a_l1, a_l1x, a_mid, a_mslot;  // tail, L2
   // global workspace byte offsets; counters and histograms first (they must
   // start at zero and are reset by the kernel itself)
@@ -110,26 +110,9 @@ __host__ __device__ inline TileSplit tile_split(int kt, int tcap) {
   return s;
 }
 
-// `cus`: compute units of the device (the tile split depends on it, the
-// workspace layout does not)
-__host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
-  SelDims s;
+// LDS layout of the selector and its workspace for s.seg / s.words / s.np.
+__host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s) {
   const int group = p.hq / p.hkv;
-  const int nrows = p.batch * p.hkv;
-  s.tcap = cus / nrows > 1 ? cus / nrows : 1;
-  s.clk_tiles = (p.max_blocks + kSpanMin - 1) / kSpanMin;
-  {
-    // tile_split(kt).tiles <= k(kt) * tcap and <= ceil(kt / 64) for kt <= max_blocks
-    const int per_round = s.tcap * kSpanMax;
-    const int kmax = (p.max_blocks + per_round - 1) / per_round;
-    s.ntiles = kmax * s.tcap < s.clk_tiles ? kmax * s.tcap : s.clk_tiles;
-  }
-  const int kpad = ((p.max_blocks + TP - 1) / TP) * TP;  // keys per row
-  s.seg = kpad < kSegMax ? kpad : kSegMax;
-  s.nseg = (kpad + s.seg - 1) / s.seg;
-  s.kstride = s.nseg * s.seg;
-  s.words = s.kstride / 32;
-  s.np = p.k_f + p.k_n + 2;
   s.dense = s.np * p.bs;
   s.dstride = (s.dense + 7) & ~7;
   const int s_cap = p.max_blocks * p.bs;
@@ -157,8 +140,6 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   s.a_pphys = o; o += align16(4 * s.np);
   const int a_l12 = o;
   s.a_keys = o;  o += align16(2 * s.seg);
-  s.a_cbits = o; o += align16(4 * s.words);
-  s.a_eqb = o;   o += align16(4 * s.words);
   s.a_dbf = o;   o += align16(4 * s.words);
   s.a_dbn = o;   o += align16(4 * s.words);
   s.a_dsel = o;  o += align16(8 * (p.k_f + p.k_n + 1));
@@ -183,8 +164,36 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   s.w_hist = w;   w += (int64_t)4 * rows * 512;
   s.w_keys = w;   w += (((int64_t)2 * rows * s.kstride) + 255) & ~(int64_t)255;
   s.w_total = w;
+}
+
+// `cus`: compute units of the device (the tile split depends on it, the
+// workspace layout does not)
+__host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
+  SelDims s;
+  const int nrows = p.batch * p.hkv;
+  s.tcap = cus / nrows > 1 ? cus / nrows : 1;
+  s.clk_tiles = (p.max_blocks + kSpanMin - 1) / kSpanMin;
+  {
+    // tile_split(kt).tiles <= k(kt) * tcap and <= ceil(kt / 64) for kt <= max_blocks
+    const int per_round = s.tcap * kSpanMax;
+    const int kmax = (p.max_blocks + per_round - 1) / per_round;
+    s.ntiles = kmax * s.tcap < s.clk_tiles ? kmax * s.tcap : s.clk_tiles;
+  }
+  const int kpad = ((p.max_blocks + TP - 1) / TP) * TP;  // keys per row
+  s.np = p.k_f + p.k_n + 2;
+  // keys staged per tail segment: as many as fit beside the debug bitmaps
+  // (one bit per page each) in 64 KiB
+  for (int seg = kpad < kSegMax ? kpad : kSegMax;; seg /= 2) {
+    s.seg = seg;
+    s.nseg = (kpad + s.seg - 1) / s.seg;
+    s.kstride = s.nseg * s.seg;
+    s.words = s.kstride / 32;
+    sel_layout(p, s);
+    if (s.lds <= 64 * 1024 || seg <= TP || seg % 16 != 0) break;
+  }
   return s;
 }
+
 
 // ---------------------------------------------------------------------------
 // per-row geometry (Appendix-A formulas of the reference, Triton integer

@@ -139,6 +139,7 @@ class GraphReadyPagedRegionCache:
         self.active_request_id = None
         self.active_req_ids = []
         self.common_dirty = True
+        self._page_cross = False  # a row's next token opens a new logical page
         self._common_active_req_ids = ()
         self._common_state_refs = ()
         self._common_layout_revision = -1
@@ -203,6 +204,9 @@ class GraphReadyPagedRegionCache:
         self._cpu_valid_req_ids_staging = torch.zeros(
             (max_query_tokens,), dtype=i64, device='cpu')
         self._cpu_planned_lengths_staging = staging((max_query_tokens,), 0, i32)
+        # rows opening a new page in a steady step: (query token index,
+        # request, logical page, physical page of every layer)
+        self._cpu_cross_staging = staging((max_query_tokens, 3 + n_layers), 0, i64)
         self._cpu_skip_far_layer_staging = staging((n_layers, max_requests), 0, i32)
         self._cpu_skip_near_layer_staging = staging((n_layers, max_requests), 0, i32)
 
@@ -524,7 +528,11 @@ class GraphReadyPagedRegionCache:
         for layer_idx in range(self.n_layers):
             table = state.block_tables[layer_idx]
             first_missing = len(table)
-            if list(table) != list(range(first_missing)):
+            if first_missing >= needed:
+                continue
+            # logical pages are only ever appended, so the table holds exactly
+            # 0 .. first_missing - 1 when its last key is first_missing - 1
+            if first_missing and next(reversed(table)) != first_missing - 1:
                 raise RuntimeError('physical block table is not append-only')
             missing = range(first_missing, needed)
             ids = self._alloc_pages(layer_idx, len(missing))
@@ -598,13 +606,12 @@ class GraphReadyPagedRegionCache:
             self._layout_state_refs = refs
         self._layout_source = active_req_ids
         page = self.geometry.page
-        full = changed
-        for state in refs:
-            if state is not None:
-                # the next token opens a new logical page: re-plan fully
-                full = full or state.logical_length % page == 0
+        # the next token of a row opens a new logical page: the steady plan
+        # appends that page; the dense-metadata planners re-plan fully
+        self._page_cross = any(state is not None and state.logical_length % page == 0
+                               for state in refs)
         self.active_req_ids = list(req_ids)
-        self.common_dirty = self.common_dirty or full
+        self.common_dirty = self.common_dirty or changed
 
     def plan_common(self, active_req_ids, query_lengths=None):
         """Plan this step's metadata; steady decode only advances lengths."""
@@ -620,12 +627,17 @@ class GraphReadyPagedRegionCache:
             self._prepare_common(active_req_ids, query_lengths)
 
     def _prepare_decode_common_fast(self, req_ids, query_lengths):
+        """Steady decode: one token per live row.  Every slot moves by one;
+        a row whose token opens a new logical page gets that page appended
+        in every layer and its slots pointed at the page's first slot."""
         if self.request_layout_revision != self._common_layout_revision:
             return False
         req_ids = self._layout_req_ids
         refs = self._layout_state_refs
         batch = len(req_ids)
         planned = []
+        crossing = []  # (batch row, query token index) of rows opening a page
+        flat = 0
         page = self.geometry.page
         for row, (rid, state) in enumerate(zip(req_ids, refs)):
             qlen = int(query_lengths[row]) if row < len(query_lengths) else 0
@@ -635,12 +647,14 @@ class GraphReadyPagedRegionCache:
                 planned.append(0)
                 continue
             length = state.logical_length + qlen
-            if qlen and state.logical_length // page != (length - 1) // page:
-                return False
             if length > state.prompt_length + self.geometry.max_new_tokens:
                 return False
+            if qlen and state.logical_length % page == 0:  # the token opens a page
+                if (length - 1) // page >= self.max_blocks:
+                    return False
+                crossing.append((row, flat))
             planned.append(length)
-        # same physical page as the previous step: valid slots move by one
+            flat += qlen
         slots = self.slot_mapping_buf[:, :batch]
         slots.add_(slots >= 0)
         self._staging_wait()
@@ -651,6 +665,19 @@ class GraphReadyPagedRegionCache:
                 self.pending_lengths[rid] = planned[row]
         self.planned_lengths_buf[:batch].copy_(
             self._cpu_planned_lengths_staging[:batch], non_blocking=True)
+        if crossing:
+            st = self._cpu_cross_staging
+            for i, (row, tok) in enumerate(crossing):
+                rid, state = req_ids[row], refs[row]
+                self._sync_block_table(state, planned[row], request_id=rid)
+                lp = (planned[row] - 1) // page
+                st[i, 0], st[i, 1], st[i, 2] = tok, rid, lp
+                for layer_idx in range(self.n_layers):
+                    st[i, 3 + layer_idx] = state.block_tables[layer_idx][lp]
+            dev = st[:len(crossing)].to(slots.device, non_blocking=True)
+            pids = dev[:, 3:].t().to(torch.int32)  # [layers, rows]
+            self.block_table_buf[:, dev[:, 1], dev[:, 2]] = pids
+            self.slot_mapping_buf[:, dev[:, 0]] = pids * page
         self._staging_mark()
         return True
 
@@ -709,6 +736,7 @@ class GraphReadyPagedRegionCache:
             self.states.get(r) if r is not None and r >= 0 else None for r in req_ids)
         self._common_layout_revision = self.request_layout_revision
         self.common_dirty = False
+        self._page_cross = False
 
     def _prepare_layer_gather(self, layer_idx, req_ids, selected_ids_by_req=None):
         """Dense (region-interval) or given selections as physical slots."""
@@ -763,7 +791,7 @@ class GraphReadyPagedRegionCache:
                          query_lengths=None, selected_ids_by_req=None):
         if current_layer_id < 0 or current_layer_id >= self.n_layers:
             raise ValueError('invalid layer id')
-        if self.common_dirty:
+        if self.common_dirty or self._page_cross:
             if query_lengths is None:
                 query_lengths = [1 if (r >= 0 and r in self.states) else 0
                                  for r in active_req_ids]
@@ -779,7 +807,7 @@ class GraphReadyPagedRegionCache:
             query_lengths = [1 if (r >= 0 and r in self.states) else 0
                              for r in active_req_ids]
         self.active_req_ids = list(active_req_ids)
-        if self.common_dirty:
+        if self.common_dirty or self._page_cross:
             self._prepare_common(active_req_ids, query_lengths)
         for layer_idx in range(self.n_layers):
             selected = None
