@@ -105,3 +105,17 @@ def test_head_dim_64_group_8(dtype):
     q = bf16_randn((2, 16, 64), gen, DEV).to(dtype)
     q2r = torch.tensor([0, 1], dtype=torch.int32, device=DEV)
     _check(cache, q, gather, lens, q2r, 64 ** -0.5, dtype)
+
+
+def test_many_rows_one_workgroup_each():
+    """512 (row, kv head) pairs: one workgroup per pair takes all its chunks
+    and writes the output without a split merge."""
+    dtype = torch.bfloat16
+    cache, gen, gather = _setup(dtype, rows=64, hkv=8, hq=32, max_vis=256, pages=200)
+    lens = torch.randint(0, 257, (64, 8), generator=torch.Generator().manual_seed(4),
+                         dtype=torch.int32).to(DEV)
+    lens[0, 0], lens[1, 1] = 256, 0
+    q = bf16_randn((64, 32, 128), gen, DEV)
+    q2r = torch.arange(64, dtype=torch.int32, device=DEV)
+    got = _check(cache, q, gather, lens, q2r, 128 ** -0.5, dtype)
+    assert np.all(got[1, 4:8] == 0)

@@ -35,7 +35,11 @@ struct AttnDims {
   int part_stride;  // floats per (row, split): G * (DV + 2)
 };
 
-__host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p) {
+// `cus`: compute units of the device.  Rows get as many split workgroups as
+// keep about two workgroups per CU busy (every split workgroup costs a
+// partial write and an arrival; a row with one split writes its output
+// directly).
+__host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p, int cus) {
   AttnDims a;
   a.rows = p.total_q * p.hkv;
   int split = p.tokens_per_split;
@@ -51,6 +55,8 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p) {
     const int lds_cap = kSplitMax * p.head_dim_v * kvb / (8 * G);
     if (lds_cap < cap) cap = lds_cap;
   }
+  const int want = a.rows > 0 ? (2 * cus + a.rows - 1) / a.rows : 1;
+  if (want < cap) cap = want;
   a.nsplit = (p.max_vis + split - 1) / split;
   if (a.nsplit > cap) a.nsplit = cap;
   if (a.nsplit < 1) a.nsplit = 1;
@@ -80,12 +86,12 @@ __device__ __forceinline__ void lds_pair(const float *v, int d, float *a,
 // without it every workgroup owns at most one and nothing is carried.
 template <typename KV, int TPR, bool LOOP>
 __global__ void __launch_bounds__(NFA_BLOCK)
-    nfa_attn_kernel(const NfaAttnParams p) {
+    nfa_attn_kernel(const NfaAttnParams p, int cus) {
   constexpr int CH = Elem<KV>::kChunk;  // dims per 16-byte chunk
   constexpr int D = TPR * CH;           // head dim (K and V)
   constexpr int RPP = NFA_BLOCK / TPR;  // rows per pass
   constexpr int PMAX = kSplitMax / RPP; // passes per split
-  const AttnDims ad = attn_dims(p);
+  const AttnDims ad = attn_dims(p, cus);
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int w = wave_id();
@@ -249,6 +255,28 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   // s_m / s_z of a head were last written before the barrier that precedes
   // the P.V step (or, with no chunk, by the same thread that reads them)
+  if (LOOP && ad.nsplit == 1) {
+    // the whole row in this workgroup: normalise and write the output
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+      const int o = tid + k * NFA_BLOCK;
+      if (o >= G * (D / 2)) break;
+      const int g = o / (D / 2);
+      const int d = 2 * (o % (D / 2));
+      const float z = s_z[g];
+      const float o0 = z == 0.0f ? 0.0f : acc0[k] / z;
+      const float o1 = z == 0.0f ? 0.0f : acc1[k] / z;
+      const int64_t oi = ((int64_t)t * p.hq + kh * G + g) * D + d;
+      if (p.q_dtype == NFA_DTYPE_BF16) {
+        ((uint16_t *)p.out)[oi] = bf16_bits(o0);
+        ((uint16_t *)p.out)[oi + 1] = bf16_bits(o1);
+      } else {
+        ((float *)p.out)[oi] = o0;
+        ((float *)p.out)[oi + 1] = o1;
+      }
+    }
+    return;
+  }
   // (a single-chunk workgroup stored its P.V above; one with no chunk
   // stores zeros here)
   const bool store_acc = LOOP || c_first >= n;
@@ -310,7 +338,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 
 extern "C" int64_t nfa_attn_workspace_bytes(const NfaAttnParams *p) {
   if (p == nullptr || p->total_q <= 0 || p->hkv <= 0) return 0;
-  return nfa::attn_dims(*p).w_total;
+  return nfa::attn_dims(*p, nfa::device_cus()).w_total;
 }
 
 extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) {
@@ -352,7 +380,8 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
     nfa_set_error("nfa_sparse_attn_decode: null device pointer");
     return NFA_EINVAL;
   }
-  const nfa::AttnDims ad = nfa::attn_dims(*p);
+  const int cus = nfa::device_cus();
+  const nfa::AttnDims ad = nfa::attn_dims(*p, cus);
   if (p->workspace == nullptr || p->workspace_bytes < ad.w_total) {
     nfa_set_error("nfa_sparse_attn_decode: workspace %lld < %lld bytes",
                   (long long)p->workspace_bytes, (long long)ad.w_total);
@@ -366,10 +395,10 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
   do {                                                                               \
     if (loop)                                                                        \
       hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, true>), grid,                \
-                         dim3(NFA_BLOCK), 0, s, *p);                                 \
+                         dim3(NFA_BLOCK), 0, s, *p, cus);                                 \
     else                                                                             \
       hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, false>), grid,               \
-                         dim3(NFA_BLOCK), 0, s, *p);                                 \
+                         dim3(NFA_BLOCK), 0, s, *p, cus);                                 \
   } while (0)
   if (tpr == 8) {
     if (bf) NFA_ATTN_LAUNCH(uint16_t, 8); else NFA_ATTN_LAUNCH(float, 8);

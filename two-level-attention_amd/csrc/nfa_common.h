@@ -22,6 +22,23 @@
 
 namespace nfa {
 
+// Compute units of the current device (cached per device; 256 when the
+// runtime cannot tell).
+inline int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) !=
+            hipSuccess ||
+        v <= 0)
+      v = 256;
+    __atomic_store_n(&cached[dev], v, __ATOMIC_RELAXED);
+  }
+  return v;
+}
+
 // ---------------------------------------------------------------------------
 // bf16 and ordering
 // ---------------------------------------------------------------------------

@@ -1964,20 +1964,6 @@ __global__ void __launch_bounds__(SB)
 using nfa::SelDims;
 
 // compute units of the current device, cached per device
-static int device_cus() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int v = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
-  if (v <= 0) {
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) !=
-            hipSuccess ||
-        v <= 0)
-      v = 256;
-    __atomic_store_n(&cached[dev], v, __ATOMIC_RELAXED);
-  }
-  return v;
-}
 
 static int select_check(const NfaSelectParams *p) {
   if (p == nullptr) {
@@ -2023,7 +2009,7 @@ static int select_check(const NfaSelectParams *p) {
     nfa_set_error("nfa_select_layer: pool_pages must be positive");
     return NFA_EINVAL;
   }
-  const SelDims sd = nfa::sel_dims(*p, device_cus());
+  const SelDims sd = nfa::sel_dims(*p, nfa::device_cus());
   if (sd.lds > 64 * 1024) {
     nfa_set_error("nfa_select_layer: geometry needs %d bytes of LDS (> 64 KiB)",
                   sd.lds);
@@ -2071,7 +2057,7 @@ extern "C" int64_t nfa_select_workspace_bytes(const NfaSelectParams *p) {
 
 template <int DSUB, typename KV>
 static hipError_t launch_select(const NfaSelectParams &p, hipStream_t stream) {
-  const SelDims sd = nfa::sel_dims(p, device_cus());
+  const SelDims sd = nfa::sel_dims(p, nfa::device_cus());
   const int rows = p.batch * p.hkv;
   hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV>), dim3(rows, sd.ntiles),
                      dim3(nfa::SB), sd.lds, stream, p, sd);
