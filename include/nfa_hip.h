@@ -216,8 +216,26 @@ typedef struct NfaRopeParams {
   void *k_out;                /* [batch, hkv, head_dim] bf16 */
 } NfaRopeParams;
 
+typedef struct NfaGateParams {
+  int32_t abi_version;
+  int32_t struct_size;
+  int32_t hq, hkv, head_dim;  /* GQA group hq/hkv divides 64; head_dim <= 128 */
+  int32_t length;             /* prompt tokens */
+  int32_t rows;               /* profiled query rows: the last `rows` */
+  int32_t sink, window, near, page;  /* RegionGeometry of the request */
+  int32_t q_dtype;            /* q and k dtype: NFA_DTYPE_BF16 */
+  float scale;
+  int32_t pad0;
+  const void *q;              /* [hq, length, head_dim] post-RoPE, strides in */
+  int64_t q_stride_h, q_stride_l;  /* elements, head_dim contiguous */
+  const void *k;              /* [hkv, length, head_dim] post-RoPE */
+  int64_t k_stride_h, k_stride_l;
+  float *out;                 /* [2, hq, rows] fp32: near mass, then far mass */
+} NfaGateParams;
+
 /* ABI / diagnostics */
 int32_t nfa_abi_version(void);
+int32_t nfa_gate_params_size(void);
 int32_t nfa_linear_params_size(void);
 int32_t nfa_rope_params_size(void);
 int32_t nfa_wall_clock_khz(void);   /* rate of the dbg_clock timestamps */
@@ -271,6 +289,12 @@ int32_t nfa_qk_norm_rope_decode(const NfaRopeParams *p, void *stream);
 int32_t nfa_rmsnorm_decode(const void *x, int64_t x_stride, const void *weight,
                            void *out, int64_t out_stride, int32_t rows,
                            int32_t dim, float eps, void *stream);
+
+/* Prefill region gate: per head and profiled row, the attention mass of
+   the far and near regions (online softmax over keys 0..qlen-1).  Replaces
+   fused_region_profile, sparse_attn/ops/frozen_gate_triton.py:84-111, behind
+   profile_regions, sparse_attn/policies/frozen_gate.py:99-111. */
+int32_t nfa_region_profile(const NfaGateParams *p, void *stream);
 
 #ifdef __cplusplus
 }

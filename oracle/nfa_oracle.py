@@ -771,3 +771,43 @@ def sparse_attention(k_pool, v_pool, q, gather, vis_lens, query_to_req, scale,
             p /= p.sum(axis=1, keepdims=True)
             out[t, kh * g:(kh + 1) * g] = p @ v
     return out
+
+
+# ---------------------------------------------------------------------------
+# prefill region gate (reference sparse_attn/policies/frozen_gate.py:45-111)
+# ---------------------------------------------------------------------------
+
+def region_bounds(length, sink, window, near, page):
+    """RegionGeometry.bounds (reference policies/region_geometry.py:18-23)
+    with Python floor division: (sink_hi, far_hi, near_hi)."""
+    sink_hi = min(sink, length)
+    near_hi = max(sink_hi, length - window)
+    aligned = ((length - window - near) // page) * page
+    far_hi = min(near_hi, max(sink_hi, aligned))
+    return sink_hi, far_hi, near_hi
+
+
+def region_profile(q, k, rows, scale, sink, window, near, page):
+    """Near and far attention mass of each head and each of the last ``rows``
+    query positions (``_stream_tail_profile``, frozen_gate.py:45-82): causal
+    softmax of ``scale * q k^T`` over keys 0..qlen-1 in float64, summed over
+    [far_hi, near_hi) and [sink_hi, far_hi) of the row's bounds.
+    ``q`` [hq, L, D], ``k`` [hkv, L, D].  Returns [2, hq, rows] (near, far)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    hq, length, _ = q.shape
+    g = hq // k.shape[0]
+    n = min(rows, length)
+    out = np.zeros((2, hq, n))
+    for h in range(hq):
+        kk = k[h // g]
+        s_all = q[h, length - n:] @ kk.T * scale
+        for r in range(n):
+            qlen = length - n + r + 1
+            s = s_all[r, :qlen]
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            sink_hi, far_hi, near_hi = region_bounds(qlen, sink, window, near, page)
+            out[0, h, r] = p[far_hi:near_hi].sum()
+            out[1, h, r] = p[sink_hi:far_hi].sum()
+    return out

@@ -111,8 +111,6 @@ def test_prefill_static_gate_and_guards():
     state = out.past_key_values.states[audit['request_id']]
     assert state.skip_far_by_layer == [True, False]
     assert state.skip_near_by_layer == [False, True]
-    with pytest.raises(ValueError, match='calibrating'):
-        prefill_frozen_request(model, ids, object(), GEO)
     with pytest.raises(ValueError, match='num_layers'):
         prefill_frozen_request(model, ids, None, GEO,
                                static_gate=SimpleNamespace(num_layers=5))

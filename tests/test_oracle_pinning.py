@@ -326,3 +326,61 @@ def test_sparse_attention_matches_torch_softmax():
             vv = vp[sl // page, 0, kv, sl % page]
             w = torch.softmax(kk @ torch.from_numpy(q[t, h]).double() * 0.25, 0)
             np.testing.assert_allclose(out[t, h], (w @ vv).numpy(), rtol=1e-9, atol=1e-12)
+
+
+# --- prefill region gate ---------------------------------------------------
+
+def test_region_bounds_match_region_geometry():
+    from sparse_attn.policies.region_geometry import RegionGeometry
+    for sink, window, near, page in ((4, 128, 4096, 16), (0, 16, 64, 64), (128, 5, 7, 3)):
+        geo = RegionGeometry(sink=sink, near=near, window=window, page=page)
+        for length in list(range(0, 300)) + [4223, 4224, 4225, 131072, 131073]:
+            assert orc.region_bounds(length, sink, window, near, page) == geo.bounds(length)
+
+
+def test_region_profile_uniform_attention_closed_form():
+    # zero queries: every visible key gets 1 / qlen
+    rng = np.random.default_rng(0)
+    length, rows = 300, 40
+    q = np.zeros((4, length, 16))
+    k = rng.standard_normal((2, length, 16))
+    out = orc.region_profile(q, k, rows, 0.25, sink=4, window=16, near=64, page=16)
+    for r in range(rows):
+        qlen = length - rows + r + 1
+        sink_hi, far_hi, near_hi = orc.region_bounds(qlen, 4, 16, 64, 16)
+        np.testing.assert_allclose(out[0, :, r], (near_hi - far_hi) / qlen, rtol=1e-12)
+        np.testing.assert_allclose(out[1, :, r], (far_hi - sink_hi) / qlen, rtol=1e-12)
+
+
+def test_region_profile_one_hot_key():
+    # one key far above the others takes all the mass of its region
+    length, rows = 400, 8
+    q = np.zeros((2, length, 8))
+    q[:, :, 0] = 1.0
+    k = np.zeros((1, length, 8))
+    for j, region in ((100, 1), (350, 0)):  # far token, near token (row 399)
+        k[:] = 0.0
+        k[0, j, 0] = 200.0
+        out = orc.region_profile(q, k, rows, 1.0, sink=4, window=16, near=64, page=16)
+        assert out[region, :, -1].min() > 1 - 1e-12
+        assert out[1 - region, :, -1].max() < 1e-12
+
+
+def test_region_profile_matches_torch_softmax():
+    rng = np.random.default_rng(1)
+    length, rows, hq, hkv, d = 90, 20, 4, 2, 8
+    q = rng.standard_normal((hq, length, d))
+    k = rng.standard_normal((hkv, length, d))
+    out = orc.region_profile(q, k, rows, 0.3, sink=2, window=8, near=16, page=4)
+    qt = torch.from_numpy(q)
+    kt = torch.from_numpy(k).repeat_interleave(hq // hkv, dim=0)
+    s = qt @ kt.transpose(1, 2) * 0.3
+    pos = torch.arange(length)
+    for r in range(rows):
+        row = length - rows + r
+        p = torch.softmax(s[:, row].masked_fill(pos > row, float('-inf')), dim=-1)
+        sink_hi, far_hi, near_hi = orc.region_bounds(row + 1, 2, 8, 16, 4)
+        np.testing.assert_allclose(out[0, :, r], p[:, far_hi:near_hi].sum(-1).numpy(),
+                                   rtol=1e-12, atol=1e-15)
+        np.testing.assert_allclose(out[1, :, r], p[:, sink_hi:far_hi].sum(-1).numpy(),
+                                   rtol=1e-12, atol=1e-15)

@@ -256,6 +256,55 @@ def test_mixed_skip_states_padding_rows_and_noncontiguous_slots():
     run_and_compare(cache, indexer, req_ids, q, decode)
 
 
+@pytest.mark.parametrize('skip', [(False, True), (True, False)])
+def test_uniform_skip_state_long_rows(skip):
+    """Every row skips the same region (region modes 1 and 2), with far and
+    near pools both long enough to matter."""
+    cache, gen, req_ids = _prod_cache([9001, 20000], skips=[skip] * 2)
+    indexer = make_indexer()
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = bf16_randn((2, cache.num_query_heads, 128), gen, DEV)
+    decode = _decode_inputs(cache, 2, gen, torch.bfloat16)
+    run_and_compare(cache, indexer, req_ids, q, decode, scaling=0.08838834764831845)
+
+
+def _hot_cache(length, hot):
+    """One request whose keys are zero except 1.0 in every L1/L2 dim for the
+    tokens of `hot` (a range); queries of ones then score those tokens (and
+    their pages) above all others, and every other score ties."""
+    from nfa_case import indexer_dims
+    cache, gen, req_ids = _prod_cache([length], zero_keys=True)
+    dims, _ = indexer_dims(make_indexer())
+    layer = cache.layers[0]
+    page = cache.geometry.page
+    table = cache.states[0].block_tables[0]
+    for t in hot:
+        layer.kv_pool_k[table[t // page], 0, :, t % page, torch.as_tensor(dims)] = 1.0
+    return cache, gen, req_ids
+
+
+@pytest.mark.parametrize('case', ['l2_quota_fills_a_bin', 'l1_budget_fills_a_bin'])
+def test_threshold_bin_taken_whole(case):
+    """The K-th largest key closes its high-byte bin exactly: exactly 892
+    tokens (the L2 quota) or exactly 96 far pages (K_F) score above all the
+    rest, all tied.  The second-level threshold pass must then take the whole
+    bin."""
+    hot = range(16, 16 + 892) if case == 'l2_quota_fills_a_bin' else range(16, 16 + 96 * 16)
+    cache, gen, req_ids = _hot_cache(9000, hot)
+    indexer = make_indexer()
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = torch.ones((1, cache.num_query_heads, 128), dtype=torch.bfloat16, device=DEV)
+    keys, values, slots = _decode_inputs(cache, 1, gen, torch.bfloat16)
+    res = run_and_compare(cache, indexer, req_ids, q, (keys * 0, values, slots))
+    r = res[0][0]
+    if case == 'l2_quota_fills_a_bin':
+        assert r.count == 892 and set(r.middle[:892]) == set(hot)
+    else:
+        assert sorted(r.i_f) == list(range(1, 97))
+
+
 def test_all_both_skip_uses_protected_path():
     cache, gen, req_ids = _prod_cache([3000, 4100], skips=[(True, True)] * 2)
     indexer = make_indexer()

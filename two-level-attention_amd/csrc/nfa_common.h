@@ -333,10 +333,13 @@ __device__ __forceinline__ void block_scan_n(int (&v)[N], int *scratch,
 // One wave: threshold bin of the top-K over a 256-bin histogram (bin = high
 // byte of a 16-bit key, higher is better).  out[0] = bin b with
 // above(b) < K <= above(b) + hist[b], or -1 when every counted entry fits
-// (total <= K, or K <= 0); out[1] = above(b); out[2] = total.  Must be
+// (total < K, or total == K unless `exact`, or K <= 0); out[1] = above(b);
+// out[2] = total.  The second-level pass over the low bytes of one
+// high-byte bin passes `exact`: there a total equal to K means the whole bin
+// is taken, and the threshold is its lowest non-empty low byte.  Must be
 // called by all 64 lanes of one wave.
 __device__ __forceinline__ void wave_threshold_bin(const int *hist, int K,
-                                                   int *out) {
+                                                   int *out, bool exact = false) {
   const int lane = lane_id();
   const int h0 = hist[4 * lane + 0], h1 = hist[4 * lane + 1];
   const int h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
@@ -344,7 +347,7 @@ __device__ __forceinline__ void wave_threshold_bin(const int *hist, int K,
   const int pre = wave_incl_sum(s);
   const int total = __builtin_amdgcn_readlane(pre, 63);
   const int x = total - pre + s;  // lanes lane..63
-  if (total <= K || K <= 0) {
+  if (total < K || (total == K && !exact) || K <= 0) {
     if (lane == 0) {
       out[0] = -1;
       out[1] = 0;

@@ -995,7 +995,7 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
       if (v != 0u && (int)(v >> 8) == hb) atomicAdd(&hist[256 + (v & 255u)], 1);
     }
     __syncthreads();
-    if (wave_id() == 0) wave_threshold_bin(hist + 256, quota - above, tmp + 12);
+    if (wave_id() == 0) wave_threshold_bin(hist + 256, quota - above, tmp + 12, true);
     __syncthreads();
     T = ((uint32_t)hb << 8) | (uint32_t)tmp[12];
     need = quota - above - tmp[13];
@@ -1543,9 +1543,9 @@ __global__ void __launch_bounds__(SB)
     __syncthreads();
     NFA_MARK(32, 26);
     if (wave_id() == 0 && hbf >= 0)
-      wave_threshold_bin(s_hist + 512, p.k_f - s_tmp[9], s_tmp + 16);
+      wave_threshold_bin(s_hist + 512, p.k_f - s_tmp[9], s_tmp + 16, true);
     if (wave_id() == 1 && hbn >= 0)
-      wave_threshold_bin(s_hist + 768, p.k_n - s_tmp[13], s_tmp + 20);
+      wave_threshold_bin(s_hist + 768, p.k_n - s_tmp[13], s_tmp + 20, true);
     __syncthreads();
   }
   const PoolThr tf = pool_threshold(p.k_f, s_tmp + 8, s_tmp + 16, s_hist + 512);

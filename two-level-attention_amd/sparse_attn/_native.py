@@ -107,12 +107,26 @@ class NfaRopeParams(ctypes.Structure):
     ]
 
 
+class NfaGateParams(ctypes.Structure):
+    _fields_ = [
+        ('abi_version', _i32), ('struct_size', _i32),
+        ('hq', _i32), ('hkv', _i32), ('head_dim', _i32),
+        ('length', _i32), ('rows', _i32),
+        ('sink', _i32), ('window', _i32), ('near', _i32), ('page', _i32),
+        ('q_dtype', _i32), ('scale', _f32), ('pad0', _i32),
+        ('q', _ptr), ('q_stride_h', _i64), ('q_stride_l', _i64),
+        ('k', _ptr), ('k_stride_h', _i64), ('k_stride_l', _i64),
+        ('out', _ptr),
+    ]
+
+
 EXPORTS = (
     'nfa_abi_version', 'nfa_wall_clock_khz', 'nfa_select_params_size', 'nfa_attn_params_size',
     'nfa_last_error', 'nfa_select_workspace_bytes', 'nfa_attn_workspace_bytes',
     'nfa_select_layer', 'nfa_sparse_attn_decode', 'nfa_paged_write_decode',
     'nfa_paged_write_prefill', 'nfa_linear_params_size', 'nfa_rope_params_size',
     'nfa_decode_linear', 'nfa_qk_norm_rope_decode', 'nfa_rmsnorm_decode',
+    'nfa_gate_params_size', 'nfa_region_profile',
 )
 
 _lib = None
@@ -165,6 +179,9 @@ def load_library(path: str = None):
         lib.nfa_rmsnorm_decode.restype = _i32
         lib.nfa_rmsnorm_decode.argtypes = [
             _ptr, _i64, _ptr, _ptr, _i64, _i32, _i32, _f32, _ptr]
+        lib.nfa_gate_params_size.restype = _i32
+        lib.nfa_region_profile.restype = _i32
+        lib.nfa_region_profile.argtypes = [ctypes.POINTER(NfaGateParams), _ptr]
         if lib.nfa_abi_version() != ABI_VERSION:
             raise NativeError('libnfa_hip ABI version mismatch')
         if lib.nfa_select_params_size() != ctypes.sizeof(NfaSelectParams):
@@ -175,6 +192,8 @@ def load_library(path: str = None):
             raise NativeError('NfaLinearParams layout mismatch')
         if lib.nfa_rope_params_size() != ctypes.sizeof(NfaRopeParams):
             raise NativeError('NfaRopeParams layout mismatch')
+        if lib.nfa_gate_params_size() != ctypes.sizeof(NfaGateParams):
+            raise NativeError('NfaGateParams layout mismatch')
         if path is None:
             _lib = lib
         return lib

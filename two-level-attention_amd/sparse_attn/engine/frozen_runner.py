@@ -6,10 +6,10 @@ Same lifecycle: dense prefill straight into the arena, per-layer far/near
 skip decisions frozen into the cache, then greedy decode steps through the
 graph runner with asynchronous token receipts.
 
-Skip decisions come from a ``StaticGateDecision`` or, without one, are all
-False (every region kept: the gate-epsilon-0 control).  The request-time
-calibrating gate (near/far attention-mass profile during prefill) is not
-built in this package; asking for it raises ``ValueError``.
+Skip decisions come from a static gate decision (``static_gate``), from the
+request-time gate (``config``, a ``GateConfig``: the near/far attention mass
+of the last prompt rows, profiled in every layer during the prefill by one
+HIP kernel), or, with neither, are all False (every region kept).
 """
 from contextlib import contextmanager
 from dataclasses import replace
@@ -17,7 +17,34 @@ from dataclasses import replace
 import torch
 
 from ..cache.paged_region_cache import GraphReadyPagedRegionCache, RequestPhase
+from ..policies.frozen_gate import decide_regions, profile_regions, region_present
 from ..scheduler.scheduler import greedy_next_tokens
+
+
+@contextmanager
+def capture_profiles(model, geometry, config):
+    """Profile each layer's prefill attention once (reference
+    engine/frozen_runner.py:15-35): the model's attention function is wrapped
+    for the duration; the wrapped call still computes the attention."""
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    impl = model.config._attn_implementation
+    original = ALL_ATTENTION_FUNCTIONS[impl]
+    profiles = {}
+
+    def profiled(module, query, key, value, *args, **kwargs):
+        layer_idx = module.layer_idx
+        if layer_idx in profiles:
+            raise ValueError('multiple prefill chunks unsupported')
+        profiles[layer_idx] = profile_regions(
+            query, key, geometry, rows=config.rows,
+            scale=kwargs.get('scaling', module.scaling))
+        return original(module, query, key, value, *args, **kwargs)
+
+    ALL_ATTENTION_FUNCTIONS[impl] = profiled
+    try:
+        yield profiles
+    finally:
+        ALL_ATTENTION_FUNCTIONS[impl] = original
 
 
 @contextmanager
@@ -68,9 +95,6 @@ def prefill_frozen_request(model, input_ids, config=None, geometry=None,
     audit)`` like the reference; ``output.past_key_values`` is the cache."""
     if geometry is None:
         raise ValueError('prefill_frozen_request needs a RegionGeometry')
-    if config is not None and static_gate is None:
-        raise ValueError('the calibrating frozen gate is not built; pass a '
-                         'static_gate or config=None (no region skipped)')
     n_layers = model.config.num_hidden_layers
     prompt_length = int(input_ids.shape[-1])
     if not isinstance(suffix_length, int) or suffix_length < 0:
@@ -84,24 +108,41 @@ def prefill_frozen_request(model, input_ids, config=None, geometry=None,
         raise ValueError('shared cache does not match model layers or geometry')
     if capacity + geometry.max_new_tokens > cache.max_blocks * geometry.page:
         raise ValueError('request exceeds shared cache sequence capacity')
-    if static_gate is not None:
-        if static_gate.num_layers != n_layers:
-            raise ValueError(f'static gate num_layers={static_gate.num_layers} does '
-                             f'not match the model ({n_layers})')
-        skip_far, skip_near = list(static_gate.skip_far), list(static_gate.skip_near)
-    else:
-        skip_far, skip_near = [False] * n_layers, [False] * n_layers
+    if static_gate is not None and static_gate.num_layers != n_layers:
+        raise ValueError(f'static gate num_layers={static_gate.num_layers} does '
+                         f'not match the model ({n_layers})')
     request_id = cache.add_request(request_id)
     cache.set_active_request(request_id)
+    profiles = None
     with _request_failure_guard(cache, request_id):
         positions = torch.arange(prompt_length, device=input_ids.device)[None]
-        output = model(input_ids=input_ids, position_ids=positions,
-                       past_key_values=cache, use_cache=True, logits_to_keep=1,
-                       attention_mask=_prefill_mask_arg(model))
+
+        def prefill():
+            return model(input_ids=input_ids, position_ids=positions,
+                         past_key_values=cache, use_cache=True, logits_to_keep=1,
+                         attention_mask=_prefill_mask_arg(model))
+
+        if static_gate is None and config is not None:
+            with capture_profiles(model, geometry, config) as profiles:
+                output = prefill()
+            if len(profiles) != n_layers:
+                raise ValueError('incomplete native layer profiling')
+            present_near, present_far = region_present(prompt_length, geometry)
+            decisions = {l: decide_regions(profiles[l], config, present_near,
+                                           present_far) for l in range(n_layers)}
+            skip_far = [decisions[l]['skip_far'] for l in range(n_layers)]
+            skip_near = [decisions[l]['skip_near'] for l in range(n_layers)]
+        else:
+            output = prefill()
+            if static_gate is not None:
+                skip_far = list(static_gate.skip_far)
+                skip_near = list(static_gate.skip_near)
+            else:
+                skip_far, skip_near = [False] * n_layers, [False] * n_layers
+            decisions = {l: {'skip_near': skip_near[l], 'skip_far': skip_far[l]}
+                         for l in range(n_layers)}
         cache.freeze(request_id, skip_far, skip_near)
-    decisions = {l: {'skip_near': skip_near[l], 'skip_far': skip_far[l]}
-                 for l in range(n_layers)}
-    return output, dict(profiles=None, decisions=decisions, request_id=request_id,
+    return output, dict(profiles=profiles, decisions=decisions, request_id=request_id,
                         material_length=prompt_length, suffix_length=suffix_length)
 
 
