@@ -49,7 +49,8 @@ constexpr int SW = SB / 64;      // waves per selector workgroup
 constexpr int TPP = 4;           // threads per page in the tile stage
 constexpr int TP = SB / TPP;     // pages scored per pass of a workgroup
 constexpr int kSpanMin = NFA_SELECT_CLOCK_PAGES;  // pages per tile, at least
-constexpr int kSpanMax = 288;    // pages per tile, at most (staged in LDS)
+constexpr int kSpanMax = 288;    // pages per pass of a tile (staged in LDS)
+constexpr int kPassMax = 16;     // passes per tile, at most
 static_assert(kSpanMin == 64 && kSpanMax >= TP, "tile geometry");
 constexpr int kStatTokens = 4;   // tokens per staging round of the stats pass
 constexpr int kSegMax = 16384;   // keys staged in LDS at once by the tail
@@ -94,7 +95,10 @@ struct TileSplit {
 
 // The kt pages of a row in tiles of `span` pages: rounds of `tcap` tiles
 // (one workgroup per CU over all rows of the launch), as few rounds as keep
-// a tile within kSpanMax pages, the pages spread evenly over the tiles.
+// a tile within kPassMax passes of kSpanMax pages, the pages spread evenly
+// over the tiles.  A pass stages, scores and publishes up to kSpanMax pages;
+// more passes per tile replace dispatch rounds of one-pass tiles (long rows,
+// many rows).
 __host__ __device__ inline TileSplit tile_split(int kt, int tcap) {
   TileSplit s;
   if (kt <= 0) {
@@ -102,7 +106,7 @@ __host__ __device__ inline TileSplit tile_split(int kt, int tcap) {
     s.tiles = 1;
     return s;
   }
-  const int per_round = tcap * kSpanMax;
+  const int per_round = tcap * kSpanMax * kPassMax;
   const int k = (kt + per_round - 1) / per_round;
   const int span = (kt + k * tcap - 1) / (k * tcap);
   s.span = span < kSpanMin ? kSpanMin : span;
@@ -175,7 +179,7 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   s.clk_tiles = (p.max_blocks + kSpanMin - 1) / kSpanMin;
   {
     // tile_split(kt).tiles <= k(kt) * tcap and <= ceil(kt / 64) for kt <= max_blocks
-    const int per_round = s.tcap * kSpanMax;
+    const int per_round = s.tcap * kSpanMax * kPassMax;
     const int kmax = (p.max_blocks + per_round - 1) / per_round;
     s.ntiles = kmax * s.tcap < s.clk_tiles ? kmax * s.tcap : s.clk_tiles;
   }
@@ -1115,7 +1119,10 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     }                                                                 \
   } while (0)
 
-template <int DSUB, typename KV>
+// MULTI: tiles may span several passes (the host picks it when a row can
+// hold more pages than one pass of every tile of a dispatch round covers);
+// without it every tile is a single pass and the extra-pass loop is absent.
+template <int DSUB, typename KV, bool MULTI>
 __global__ void __launch_bounds__(SB)
     nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
   warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
@@ -1199,7 +1206,6 @@ __global__ void __launch_bounds__(SB)
   if (tile >= split.tiles) return;
   const int t0 = tile * split.span;
   const int t1 = imin(t0 + split.span, kt_eff);
-  const int ngrp = (t1 - t0 + 63) / 64;
   const int last_blk = L > 0 ? (L - 1) / bs : -1;
   const bool owns_last = last_blk >= t0 && last_blk < t1;
   // LDS: dims, fine dims, raw query rows, histogram
@@ -1256,7 +1262,7 @@ __global__ void __launch_bounds__(SB)
   // speculative: the pools without skip flags contain the final ones
   const RowGeo g0 = row_geo(p, L, false, false);
   unsigned char *s_st = smem + sd.a_st;
-  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, t1, s_st);
+  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, imin(t0 + kSpanMax, t1), s_st);
   int32_t prev, skf, skn, ph_last;
   sload_i32x4(p.stats_len_l + req, p.skip_far_l + req, p.skip_near_l + req,
               btr + (owns_last ? imin((L - 1) / p.page, mb - 1) : 0), prev, skf,
@@ -1300,154 +1306,170 @@ __global__ void __launch_bounds__(SB)
                           : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page);
       ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)] = src[s_fdims[tid]];
     }
-  } else if (NFA_COLD(do_stats && !incremental)) {
-    float *psum_row = p.page_sum_l != nullptr
-                          ? p.page_sum_l + (req * p.hkv + kv) * DSUB
-                          : nullptr;
-    int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
-    if (tid == 0) {
-      bool vec = true;
-      for (int c = 0; vec && c < NC; ++c) {
-        const int first = s_dims[c * CH];
-        vec = (first % CH) == 0;
-        for (int e = 1; vec && e < CH; ++e) vec = s_dims[c * CH + e] == first + e;
-        s_coff[c] = first;
-      }
-      s_misc[1] = vec;
-    }
-    if (page_phys) {
-      for (int i = tid; i < t1 - t0; i += SB) {
-        const int lp = imin(((t0 + i) * bs) / p.page, mb - 1);
-        s_tphys[i] = safe_page(p, btr[lp]);
-      }
-    }
-    __syncthreads();
-    if (s_misc[1]) {
-      compute_stats_vec<DSUB, KV>(p, req, kv, L, t0, t1, s_coff,
-                                  page_phys ? s_tphys : nullptr, new_row, L - 1,
-                                  psum_row, last_blk);
-    } else {
-      __syncthreads();
-      compute_stats<DSUB, KV>(p, req, kv, L, t0, t1, s_stage, s_dims,
-                              page_phys ? s_tphys : nullptr, new_row, L - 1,
-                              psum_row, last_blk);
-    }
-    if (p.l2_keys_l != nullptr) {
-      // L2 side rows of the tile's tokens
-      const int tlo = t0 * bs;
-      const int thi = imin(t1 * bs, L);
-      const int nchv = s_misc[5];  // 16-byte runs of the L2 dims, 0: elements
-      auto src_row = [&](int tok) -> const KV * {
-        if (new_row != nullptr && tok == L - 1) return new_row;
-        const int phys = page_phys ? s_tphys[tok / bs - t0]
-                                   : safe_page(p, btr[imin(tok / p.page, mb - 1)]);
-        return kpool + kv_offset(p, phys, kv, tok % p.page);
-      };
-      if (nchv > 0) {
-        for (int e = tid; e < (thi - tlo) * nchv; e += SB) {
-          const int tok = tlo + e / nchv;
-          const int c = e % nchv;
-          *reinterpret_cast<uint4 *>((KV *)p.l2_keys_l +
-                                     l2_side_index<KV>(p, req, kv, tok, c * CH)) =
-              *reinterpret_cast<const uint4 *>(src_row(tok) + s_fdims[c * CH]);
-        }
-      } else {
-        for (int e = tid; e < (thi - tlo) * p.fine_dsub; e += SB) {
-          const int tok = tlo + e / p.fine_dsub;
-          const int d = e % p.fine_dsub;
-          ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, tok, d)] =
-              src_row(tok)[s_fdims[d]];
-        }
-      }
-    }
-    // rebuilt statistics: complete the stores, drop cached lines, read back
-    __threadfence();
-    __syncthreads();
-    __threadfence();
-    if constexpr (STG) {
-      __builtin_amdgcn_s_waitcnt(0);  // the speculative loads have landed
-      // recomputed addresses: nothing of the first issue stays live across
-      // the rebuild
-      int t0r = t0;
-      asm volatile("" : "+s"(t0r));
-      stage_stats_async(p, g0, req, kv, t0r, t1, s_st);
-    }
   }
-  if constexpr (STG) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's staged statistics
-    __syncthreads();
-  }
-  lds_barrier();
-  NFA_MARK(0, 3);
-
-  // ---- L1 scores: four waves per 64 pages, two query heads per thread -----
   const RowGeo geo = row_geo(p, L, skip_far, skip_near);
   float *s_hs = (float *)(smem + sd.a_hs);  // [head][page] bf16 head scores
   const int j0 = hp, j1 = hp + TPP;
-  if (do_stats && j0 < G) {
-    for (int grp = grp0; grp < ngrp; grp += GSTEP) {
-      const int lp = grp * 64 + lane_id();
-      const int t = t0 + lp;
-      bool fp = false, np = false;
-      if (t < t1) pools(p, geo, t, &fp, &np);
-      if (!(fp || np)) continue;
-      const bool need_mm = (fp && far_mm) || (np && near_mm);
-      const bool need_avg = !need_mm;
-      float h0 = 0.0f, h1 = 0.0f;
-      if constexpr (STG) {
-        // a missing second head scores the first one again, discarded
-        const int j1s = j1 < G ? j1 : j0;
-        l1_heads_staged(reinterpret_cast<const uint4 *>(s_st) + lp,
-                        s_qs + j0 * 2 * DSUB, s_qs + j1s * 2 * DSUB,
-                        s_qf + j0 * DSUB, s_qf + j1s * DSUB, need_mm, bs, &h0, &h1);
+  // one pass stages, scores and publishes pages [c0, c1), at most kSpanMax;
+  // the histogram accumulates in LDS over the passes of the tile
+  auto run_pass = [&](int c0, int c1) {
+    const int ngrp = (c1 - c0 + 63) / 64;
+    if (NFA_COLD(do_stats && !incremental)) {
+      float *psum_row = p.page_sum_l != nullptr
+                            ? p.page_sum_l + (req * p.hkv + kv) * DSUB
+                            : nullptr;
+      int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
+      if (tid == 0) {
+        bool vec = true;
+        for (int c = 0; vec && c < NC; ++c) {
+          const int first = s_dims[c * CH];
+          vec = (first % CH) == 0;
+          for (int e = 1; vec && e < CH; ++e) vec = s_dims[c * CH + e] == first + e;
+          s_coff[c] = first;
+        }
+        s_misc[1] = vec;
+      }
+      if (page_phys) {
+        for (int i = tid; i < c1 - c0; i += SB) {
+          const int lp = imin(((c0 + i) * bs) / p.page, mb - 1);
+          s_tphys[i] = safe_page(p, btr[lp]);
+        }
+      }
+      __syncthreads();
+      if (s_misc[1]) {
+        compute_stats_vec<DSUB, KV>(p, req, kv, L, c0, c1, s_coff,
+                                    page_phys ? s_tphys : nullptr, new_row, L - 1,
+                                    psum_row, last_blk);
       } else {
-        const bool from_lds = incremental && t == last_blk;
-        float m0 = 0.0f, a0 = 0.0f, m1 = 0.0f, a1 = 0.0f;
-        l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j0 * DSUB, need_mm, need_avg,
-                              from_lds ? s_last : nullptr, &m0, &a0);
-        if (j1 < G)
-          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j1 * DSUB, need_mm,
-                                need_avg, from_lds ? s_last : nullptr, &m1, &a1);
-        h0 = need_mm ? m0 : a0;
-        h1 = need_mm ? m1 : a1;
+        __syncthreads();
+        compute_stats<DSUB, KV>(p, req, kv, L, c0, c1, s_stage, s_dims,
+                                page_phys ? s_tphys : nullptr, new_row, L - 1,
+                                psum_row, last_blk);
       }
-      s_hs[j0 * kSpanMax + lp] = h0;
-      if (j1 < G) s_hs[j1 * kSpanMax + lp] = h1;
+      if (p.l2_keys_l != nullptr) {
+        // L2 side rows of the tile's tokens
+        const int tlo = c0 * bs;
+        const int thi = imin(c1 * bs, L);
+        const int nchv = s_misc[5];  // 16-byte runs of the L2 dims, 0: elements
+        auto src_row = [&](int tok) -> const KV * {
+          if (new_row != nullptr && tok == L - 1) return new_row;
+          const int phys = page_phys ? s_tphys[tok / bs - c0]
+                                     : safe_page(p, btr[imin(tok / p.page, mb - 1)]);
+          return kpool + kv_offset(p, phys, kv, tok % p.page);
+        };
+        if (nchv > 0) {
+          for (int e = tid; e < (thi - tlo) * nchv; e += SB) {
+            const int tok = tlo + e / nchv;
+            const int c = e % nchv;
+            *reinterpret_cast<uint4 *>((KV *)p.l2_keys_l +
+                                       l2_side_index<KV>(p, req, kv, tok, c * CH)) =
+                *reinterpret_cast<const uint4 *>(src_row(tok) + s_fdims[c * CH]);
+          }
+        } else {
+          for (int e = tid; e < (thi - tlo) * p.fine_dsub; e += SB) {
+            const int tok = tlo + e / p.fine_dsub;
+            const int d = e % p.fine_dsub;
+            ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, tok, d)] =
+                src_row(tok)[s_fdims[d]];
+          }
+        }
+      }
+      // rebuilt statistics: complete the stores, drop cached lines, read back
+      __threadfence();
+      __syncthreads();
+      __threadfence();
+      if constexpr (STG) {
+        __builtin_amdgcn_s_waitcnt(0);  // the speculative loads have landed
+        // recomputed addresses: nothing of the first issue stays live across
+        // the rebuild
+        int t0r = c0;
+        asm volatile("" : "+s"(t0r));
+        stage_stats_async(p, geo, req, kv, t0r, c1, s_st);
+      }
     }
-  }
-  lds_barrier();
+    if constexpr (STG) {
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's staged statistics
+      __syncthreads();
+    }
+    lds_barrier();
+    NFA_MARK(0, 3);
 
-  // ---- group mean, keys and high-byte histograms (the hp == 0 waves) -----
-  if (hp == 0) {
-    for (int grp = grp0; grp < ngrp; grp += GSTEP) {
-      const int lp = grp * 64 + lane_id();
-      const int t = t0 + lp;
-      if (t >= t1) continue;
-      bool fp = false, np = false;
-      if (do_stats) pools(p, geo, t, &fp, &np);
-      uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
-      if (fp || np) {
-        // bf16 head scores summed in head order
-        float acc = 0.0f;
-        for (int j = 0; j < G; ++j) acc = acc + s_hs[j * kSpanMax + lp];
-        const uint16_t mean = bf16_bits(acc / (float)G);
-        if (fp) far_bits = mean;
-        if (np) near_bits = mean;
+    // ---- L1 scores: four waves per 64 pages, two query heads per thread -----
+    if (do_stats && j0 < G) {
+      for (int grp = grp0; grp < ngrp; grp += GSTEP) {
+        const int lp = grp * 64 + lane_id();
+        const int t = c0 + lp;
+        bool fp = false, np = false;
+        if (t < c1) pools(p, geo, t, &fp, &np);
+        if (!(fp || np)) continue;
+        const bool need_mm = (fp && far_mm) || (np && near_mm);
+        const bool need_avg = !need_mm;
+        float h0 = 0.0f, h1 = 0.0f;
+        if constexpr (STG) {
+          // a missing second head scores the first one again, discarded
+          const int j1s = j1 < G ? j1 : j0;
+          l1_heads_staged(reinterpret_cast<const uint4 *>(s_st) + lp,
+                          s_qs + j0 * 2 * DSUB, s_qs + j1s * 2 * DSUB,
+                          s_qf + j0 * DSUB, s_qf + j1s * DSUB, need_mm, bs, &h0, &h1);
+        } else {
+          const bool from_lds = incremental && t == last_blk;
+          float m0 = 0.0f, a0 = 0.0f, m1 = 0.0f, a1 = 0.0f;
+          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j0 * DSUB, need_mm, need_avg,
+                                from_lds ? s_last : nullptr, &m0, &a0);
+          if (j1 < G)
+            l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j1 * DSUB, need_mm,
+                                  need_avg, from_lds ? s_last : nullptr, &m1, &a1);
+          h0 = need_mm ? m0 : a0;
+          h1 = need_mm ? m1 : a1;
+        }
+        s_hs[j0 * kSpanMax + lp] = h0;
+        if (j1 < G) s_hs[j1 * kSpanMax + lp] = h1;
       }
-      if (NFA_COLD(p.dbg_far != nullptr)) {
-        p.dbg_far[(int64_t)row * mb + t] = far_bits;
-        p.dbg_near[(int64_t)row * mb + t] = near_bits;
+    }
+    lds_barrier();
+
+    // ---- group mean, keys and high-byte histograms (the hp == 0 waves) -----
+    if (hp == 0) {
+      for (int grp = grp0; grp < ngrp; grp += GSTEP) {
+        const int lp = grp * 64 + lane_id();
+        const int t = c0 + lp;
+        if (t >= c1) continue;
+        bool fp = false, np = false;
+        if (do_stats) pools(p, geo, t, &fp, &np);
+        uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
+        if (fp || np) {
+          // bf16 head scores summed in head order
+          float acc = 0.0f;
+          for (int j = 0; j < G; ++j) acc = acc + s_hs[j * kSpanMax + lp];
+          const uint16_t mean = bf16_bits(acc / (float)G);
+          if (fp) far_bits = mean;
+          if (np) near_bits = mean;
+        }
+        if (NFA_COLD(p.dbg_far != nullptr)) {
+          p.dbg_far[(int64_t)row * mb + t] = far_bits;
+          p.dbg_near[(int64_t)row * mb + t] = near_bits;
+        }
+        // a page belongs to at most one pool: far pages lie below near_start,
+        // near pages at or above it
+        const uint32_t fk = score_key(far_bits);
+        const uint32_t nk = score_key(near_bits);
+        g_keys[t] = (uint16_t)(fk ? fk : nk);
+        if (fk) atomicAdd(&s_hist[fk >> 8], 1);
+        if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
       }
-      // a page belongs to at most one pool: far pages lie below near_start,
-      // near pages at or above it
-      const uint32_t fk = score_key(far_bits);
-      const uint32_t nk = score_key(near_bits);
-      g_keys[t] = (uint16_t)(fk ? fk : nk);
-      if (fk) atomicAdd(&s_hist[fk >> 8], 1);
-      if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
+    }
+    lds_barrier();
+  };
+  run_pass(t0, imin(t0 + kSpanMax, t1));
+  if constexpr (MULTI) {
+    // long rows and many rows: further passes instead of dispatch rounds
+    for (int c0 = t0 + kSpanMax; c0 < t1; c0 += kSpanMax) {
+      const int c1 = imin(c0 + kSpanMax, t1);
+      __syncthreads();  // the previous pass's readers of the staged statistics
+      if constexpr (STG) stage_stats_async(p, geo, req, kv, c0, c1, s_st);
+      run_pass(c0, c1);
     }
   }
-  lds_barrier();
   if (tid < 256) {
     const int hf = s_hist[tid];
     const int hn = s_hist[256 + tid];
@@ -2059,8 +2081,15 @@ template <int DSUB, typename KV>
 static hipError_t launch_select(const NfaSelectParams &p, hipStream_t stream) {
   const SelDims sd = nfa::sel_dims(p, nfa::device_cus());
   const int rows = p.batch * p.hkv;
-  hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV>), dim3(rows, sd.ntiles),
-                     dim3(nfa::SB), sd.lds, stream, p, sd);
+  // one pass per tile whenever a dispatch round of single-pass tiles covers
+  // the widest possible row
+  const bool multi = p.max_blocks > sd.tcap * nfa::kSpanMax;
+  if (multi)
+    hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, true>), dim3(rows, sd.ntiles),
+                       dim3(nfa::SB), sd.lds, stream, p, sd);
+  else
+    hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, false>), dim3(rows, sd.ntiles),
+                       dim3(nfa::SB), sd.lds, stream, p, sd);
   return hipGetLastError();
 }
 
