@@ -17,6 +17,8 @@
  *                              (select_topk_for_layer_batched; kernels :29-2028)
  *   nfa_sparse_attn_decode  <- sparse_attn/ops/paged_region_kernels.py:800-1006
  *                              (sparse_paged_attention_gather; kernel :251-363)
+ *   nfa_sparse_attn_partial <- sparse_attn/ops/paged_region_kernels.py:727-780
+ *   nfa_attn_regions_combine <- sparse_attn/ops/paged_region_kernels.py:783-797
  *   nfa_paged_write_decode  <- sparse_attn/ops/paged_region_kernels.py:665-724
  *   nfa_paged_write_prefill <- sparse_attn/ops/paged_region_kernels.py:610-662
  */
@@ -241,6 +243,8 @@ int32_t nfa_rope_params_size(void);
 int32_t nfa_wall_clock_khz(void);   /* rate of the dbg_clock timestamps */
 int32_t nfa_select_params_size(void);
 int32_t nfa_attn_params_size(void);
+int32_t nfa_attn_partial_size(void);
+int32_t nfa_attn_combine_params_size(void);
 const char *nfa_last_error(void);
 
 /* Scratch bytes a call with these parameters needs (0 on bad params). */
@@ -252,6 +256,42 @@ int32_t nfa_select_layer(const NfaSelectParams *p, void *stream);
 
 /* A10: sparse gather attention, out[t,h] = softmax(scale q k^T) v. */
 int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream);
+
+/* Per-split online-softmax state of one region's gather attention. */
+typedef struct NfaAttnPartial {
+  int32_t abi_version;
+  int32_t struct_size;
+  int32_t nsplit;             /* splits per (query row, kv head), >= 1 */
+  int32_t block_tokens;       /* split s of a row with n visible slots takes
+                                 the blocks [s*nb/nsplit, (s+1)*nb/nsplit) of
+                                 nb = ceil(n / block_tokens) blocks */
+  float *acc;                 /* [nsplit, T, hq, head_dim_v]: sum_i e_i v_i */
+  float *m;                   /* [nsplit, T, hq]: max score (-inf if none) */
+  float *z;                   /* [nsplit, T, hq]: sum_i e_i, e_i = exp(s_i - m) */
+} NfaAttnPartial;
+
+/* Disjoint-region attention (protected and middle sets attended apart, then
+   merged).  The partial replaces sparse_paged_attention_gather_partial,
+   sparse_attn/ops/paged_region_kernels.py:727-780 (kernel :367-530 with
+   WRITE_PARTIAL): p->out, p->workspace and p->workspace_bytes are unused;
+   padding rows store (0, -inf, 0).  The combine replaces
+   sparse_paged_attention_regions_combine, :783-797 (kernel :533-575): the
+   splits of region a, then those of region b, merge in split order. */
+int32_t nfa_sparse_attn_partial(const NfaAttnParams *p, const NfaAttnPartial *pt,
+                                void *stream);
+
+typedef struct NfaAttnCombineParams {
+  int32_t abi_version;
+  int32_t struct_size;
+  int32_t total_q, hq, head_dim_v;
+  int32_t out_dtype;          /* NFA_DTYPE_BF16 or NFA_DTYPE_F32 */
+  int32_t nsplit_a, nsplit_b; /* splits of each region's state (0 = absent) */
+  const float *acc_a, *m_a, *z_a;   /* NfaAttnPartial layouts */
+  const float *acc_b, *m_b, *z_b;
+  void *out;                  /* [T, hq, head_dim_v], acc / z (0 where z == 0) */
+} NfaAttnCombineParams;
+
+int32_t nfa_attn_regions_combine(const NfaAttnCombineParams *c, void *stream);
 
 /* A11: one decode token per row; slot < 0 writes nothing. */
 int32_t nfa_paged_write_decode(const void *keys, const void *values,

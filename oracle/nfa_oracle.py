@@ -773,6 +773,80 @@ def sparse_attention(k_pool, v_pool, q, gather, vis_lens, query_to_req, scale,
     return out
 
 
+def split_bounds(n, nsplit, block_tokens):
+    """Token range [lo, hi) of each split of a row with ``n`` visible slots:
+    split s takes blocks [s*nb//nsplit, (s+1)*nb//nsplit) of
+    nb = ceil(n / block_tokens) (reference ops/paged_region_kernels.py:455-461)."""
+    nb = -(-n // block_tokens)
+    out = []
+    for s in range(nsplit):
+        b0, b1 = s * nb // nsplit, (s + 1) * nb // nsplit
+        out.append((b0 * block_tokens, min(b1 * block_tokens, n)))
+    return out
+
+
+def sparse_attention_partial(k_pool, v_pool, q, gather, vis_lens, query_to_req, scale,
+                             page, nsplit, block_tokens):
+    """Split online-softmax states of one region's gather attention, float64
+    (reference ops/paged_region_kernels.py:367-530 with WRITE_PARTIAL, host
+    :727-780).  Returns acc [S, T, HQ, DV], m [S, T, HQ], z [S, T, HQ]:
+    m = the split's maximum score (-inf when it holds no valid slot),
+    z = sum exp(s_i - m), acc = sum exp(s_i - m) v_i; negative slots are
+    skipped; padding rows hold (0, -inf, 0)."""
+    q = np.asarray(q, dtype=np.float64)
+    t_total, hq, _ = q.shape
+    hk = gather.shape[1]
+    g = hq // hk
+    dv = v_pool.shape[-1]
+    max_vis = gather.shape[-1]
+    acc = np.zeros((nsplit, t_total, hq, dv))
+    m = np.full((nsplit, t_total, hq), -np.inf)
+    z = np.zeros((nsplit, t_total, hq))
+    for t in range(t_total):
+        req = int(query_to_req[t])
+        if req < 0:
+            continue
+        for kh in range(hk):
+            n = min(int(vis_lens[req, kh]), max_vis)
+            for sp, (lo, hi) in enumerate(split_bounds(n, nsplit, block_tokens)):
+                slots = np.asarray(gather[req, kh, lo:hi], dtype=np.int64)
+                slots = slots[slots >= 0]
+                if len(slots) == 0:
+                    continue
+                phys, off = slots // page, slots % page
+                k = k_pool[phys, 0, kh, off].astype(np.float64)
+                v = v_pool[phys, 0, kh, off].astype(np.float64)
+                sc = q[t, kh * g:(kh + 1) * g] @ k.T * scale
+                mx = sc.max(axis=1)
+                e = np.exp(sc - mx[:, None])
+                m[sp, t, kh * g:(kh + 1) * g] = mx
+                z[sp, t, kh * g:(kh + 1) * g] = e.sum(axis=1)
+                acc[sp, t, kh * g:(kh + 1) * g] = e @ v
+    return acc, m, z
+
+
+def regions_combine(parts_a, parts_b):
+    """Merge two regions' split states, region a's splits first, each folded
+    in with the online-softmax rescaling; acc / z, 0 where z == 0 (reference
+    ops/paged_region_kernels.py:533-575).  Float64 [T, HQ, DV]."""
+    acc_a = parts_a[0]
+    out_acc = np.zeros(acc_a.shape[1:])
+    m = np.full(acc_a.shape[1:3], -np.inf)
+    z = np.zeros(acc_a.shape[1:3])
+    with np.errstate(invalid='ignore'):
+        for acc, pm, pz in (parts_a, parts_b):
+            for sp in range(acc.shape[0]):
+                new_m = np.maximum(m, pm[sp])
+                safe = np.where(new_m == -np.inf, 0.0, new_m)
+                alpha = np.exp(m - safe)
+                beta = np.exp(pm[sp] - safe)
+                out_acc = out_acc * alpha[..., None] + acc[sp] * beta[..., None]
+                z = z * alpha + pz[sp] * beta
+                m = new_m
+    zz = np.where(z == 0.0, 1.0, z)
+    return np.where((z == 0.0)[..., None], 0.0, out_acc / zz[..., None])
+
+
 # ---------------------------------------------------------------------------
 # prefill region gate (reference sparse_attn/policies/frozen_gate.py:45-111)
 # ---------------------------------------------------------------------------

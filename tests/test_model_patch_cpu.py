@@ -116,9 +116,9 @@ def test_prefill_static_gate_and_guards():
                                static_gate=SimpleNamespace(num_layers=5))
 
 
-def test_decode_rejects_unbuilt_operator_modes():
+def test_decode_rejects_unknown_operator_modes():
     model = _tiny('qwen3')
-    register_patch(model, _args(nfa_operator_mode='serial'))
+    register_patch(model, _args(nfa_operator_mode='parallel'))
     ids = torch.randint(0, 256, (1, 100), generator=torch.Generator().manual_seed(2))
     with torch.no_grad():
         out, audit = prefill_frozen_request(model, ids, None, GEO)
@@ -126,7 +126,7 @@ def test_decode_rejects_unbuilt_operator_modes():
     rid = audit['request_id']
     cache.new_step([rid])
     cache.plan_common([rid])
-    with pytest.raises(ValueError, match='serial'), torch.no_grad():
+    with pytest.raises(ValueError, match='unknown NFA operator mode'), torch.no_grad():
         model(input_ids=ids[:, :1], position_ids=torch.tensor([[100]]),
               past_key_values=cache, use_cache=True,
               attention_mask={'full_attention': None})

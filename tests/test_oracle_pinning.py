@@ -328,6 +328,92 @@ def test_sparse_attention_matches_torch_softmax():
             np.testing.assert_allclose(out[t, h], (w @ vv).numpy(), rtol=1e-9, atol=1e-12)
 
 
+# --- disjoint-region split states and combine --------------------------------
+
+def test_split_bounds_cover_the_row_and_every_split_works():
+    # floor boundaries (not ceil-sized chunks): 10 blocks over 8 splits give
+    # every split a block, and the splits tile [0, n) in order
+    for n, nsplit, bt in ((10 * 128, 8, 128), (1000, 4, 128), (5, 4, 64), (0, 3, 64),
+                          (129, 1, 128), (4100, 7, 64)):
+        b = orc.split_bounds(n, nsplit, bt)
+        assert len(b) == nsplit
+        assert b[0][0] == 0 and b[-1][1] == n
+        assert all(b[i][1] == b[i + 1][0] for i in range(nsplit - 1))
+        nb = -(-n // bt)
+        sizes = [-(-(hi - lo) // bt) for lo, hi in b]
+        assert sum(sizes) == nb and max(sizes) - min(sizes) <= 1
+        if nb >= nsplit:
+            assert min(sizes) >= 1
+
+
+def _regions_case(seed):
+    rng = np.random.default_rng(seed)
+    hkv, hq, d, page = 2, 8, 16, 4
+    k_pool = rng.standard_normal((60, 1, hkv, page, d)).astype(F32)
+    v_pool = rng.standard_normal((60, 1, hkv, page, d)).astype(F32)
+    q = rng.standard_normal((3, hq, d)).astype(F32)
+    # distinct slots: the two regions of a (row, kv head) are disjoint
+    prot = rng.permutation(240)[:200].reshape(2, 100)
+    gather_a = np.stack([prot[:, :20], prot[:, 20:40]], axis=1)  # [2, hkv, 20]
+    gather_b = np.stack([prot[:, 40:70], prot[:, 70:100]], axis=1)  # [2, hkv, 30]
+    gather_b[1, 0, 3] = -1  # a negative slot is skipped
+    vis_a = np.array([[20, 7], [0, 13]])
+    vis_b = np.array([[30, 0], [25, 30]])
+    q2r = np.array([1, -1, 0])
+    return k_pool, v_pool, q, (gather_a, vis_a), (gather_b, vis_b), q2r, page
+
+
+@pytest.mark.parametrize('na,nb,bt', [(1, 4, 4), (2, 3, 8), (1, 1, 128), (3, 8, 2)])
+def test_regions_combine_equals_attention_over_the_union(na, nb, bt):
+    """Split states of two disjoint slot sets, merged, are softmax attention
+    over their union: pins the partition, the per-split (m, z, acc) and the
+    rescaling order together against the torch-pinned sparse_attention."""
+    k_pool, v_pool, q, (ga, va), (gb, vb), q2r, page = _regions_case(5)
+    pa = orc.sparse_attention_partial(k_pool, v_pool, q, ga, va, q2r, 0.3, page, na, bt)
+    pb = orc.sparse_attention_partial(k_pool, v_pool, q, gb, vb, q2r, 0.3, page, nb, bt)
+    got = orc.regions_combine(pa, pb)
+    width = ga.shape[-1] + gb.shape[-1]
+    union = np.full((2, 2, width), -1, dtype=np.int64)
+    vis = np.zeros((2, 2), dtype=np.int64)
+    for r in range(2):
+        for kv in range(2):
+            ids = np.concatenate([ga[r, kv, :va[r, kv]], gb[r, kv, :vb[r, kv]]])
+            union[r, kv, :len(ids)] = ids
+            vis[r, kv] = len(ids)
+    want = orc.sparse_attention(k_pool, v_pool, q, union, vis, q2r, 0.3, page)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-14)
+
+
+def test_split_state_closed_forms():
+    """One slot in a split: m is its score, z = 1, acc its value row; an
+    empty split and a padding row hold (0, -inf, 0)."""
+    k_pool, v_pool, q, (ga, va), _, q2r, page = _regions_case(9)
+    vis = np.array([[2, 0], [1, 0]])
+    acc, m, z = orc.sparse_attention_partial(k_pool, v_pool, q, ga, vis, q2r, 0.5,
+                                             page, 3, 1)
+    # row 1 (query 0), kv 0, one slot: floor boundaries 0, 0, 0, 1 put it in
+    # split 2, splits 0-1 are empty
+    assert orc.split_bounds(1, 3, 1) == [(0, 0), (0, 0), (0, 1)]
+    sl = ga[1, 0, 0]
+    k = k_pool[sl // page, 0, 0, sl % page].astype(np.float64)
+    v = v_pool[sl // page, 0, 0, sl % page].astype(np.float64)
+    for h in range(4):
+        assert m[2, 0, h] == pytest.approx(float(q[0, h].astype(np.float64) @ k) * 0.5)
+        assert z[2, 0, h] == 1.0
+        np.testing.assert_allclose(acc[2, 0, h], v)
+        assert (m[:2, 0, h] == -np.inf).all() and not z[:2, 0, h].any()
+        assert not acc[:2, 0, h].any()
+    assert (m[:, 1] == -np.inf).all() and not z[:, 1].any() and not acc[:, 1].any()
+    # row 0 (query 2), kv 0: two slots over three splits of one-token blocks
+    # -> splits 1 and 2 hold one each (floor boundaries 0, 0, 1, 2)
+    assert orc.split_bounds(2, 3, 1) == [(0, 0), (0, 1), (1, 2)]
+    assert z[0, 2, 0] == 0 and z[1, 2, 0] == 1.0 and z[2, 2, 0] == 1.0
+    # both regions empty: the combine outputs zeros, not NaN
+    empty = orc.regions_combine((acc[:, 1:2], m[:, 1:2], z[:, 1:2]),
+                                (acc[:, 1:2], m[:, 1:2], z[:, 1:2]))
+    assert np.isfinite(empty).all() and not empty.any()
+
+
 # --- prefill region gate ---------------------------------------------------
 
 def test_region_bounds_match_region_geometry():

@@ -84,9 +84,14 @@ __device__ __forceinline__ void lds_pair(const float *v, int d, float *a,
 
 // LOOP: a workgroup may own several chunks (rows wider than nsplit chunks);
 // without it every workgroup owns at most one and nothing is carried.
-template <typename KV, int TPR, bool LOOP>
+// PART (with LOOP): workgroup `split` of a row owns the caller's split --
+// blocks [split * nb / nsplit, (split + 1) * nb / nsplit) of the row's
+// nb = ceil(n / block_tokens) token blocks -- and stores its unnormalised
+// state (acc, m, z) into the caller's buffers instead of merging.
+template <typename KV, int TPR, bool LOOP, bool PART = false>
 __global__ void __launch_bounds__(NFA_BLOCK)
-    nfa_attn_kernel(const NfaAttnParams p, int cus) {
+    nfa_attn_kernel(const NfaAttnParams p, int cus, const NfaAttnPartial pt) {
+  static_assert(LOOP || !PART, "a partial split may own several chunks");
   constexpr int CH = Elem<KV>::kChunk;  // dims per 16-byte chunk
   constexpr int D = TPR * CH;           // head dim (K and V)
   constexpr int RPP = NFA_BLOCK / TPR;  // rows per pass
@@ -110,9 +115,10 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   __shared__ int s_last;
 
   unsigned char *ws = (unsigned char *)p.workspace;
-  unsigned int *cnt = (unsigned int *)(ws + ad.w_cnt);
-  float *part = (float *)(ws + ad.w_part) +
-                ((int64_t)row * ad.nsplit + split) * ad.part_stride;
+  unsigned int *cnt = PART ? nullptr : (unsigned int *)(ws + ad.w_cnt);
+  float *part = PART ? nullptr
+                     : (float *)(ws + ad.w_part) +
+                           ((int64_t)row * ad.nsplit + split) * ad.part_stride;
 
   int req = p.query_to_req[t];
   if (req >= p.gather_rows) req = -1;  // out-of-range rows act as padding
@@ -123,9 +129,19 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   // chunks split, split + nsplit, ... of ad.split slots each; the running
   // (max, denominator, P.V) of the workgroup carries from chunk to chunk
-  const int c_first = split * ad.split;
-  const int c_step = ad.nsplit * ad.split;
-  if (c_first < n) {
+  int c_first = split * ad.split;
+  int c_step = ad.nsplit * ad.split;
+  int c_end = n;
+  if constexpr (PART) {
+    // consecutive chunks over the caller's split of the row
+    const int bt = pt.block_tokens;
+    const int nb = (n + bt - 1) / bt;
+    c_first = (int)((int64_t)split * nb / pt.nsplit) * bt;
+    const int b_end = (int)((int64_t)(split + 1) * nb / pt.nsplit);
+    c_end = b_end * bt < n ? b_end * bt : n;
+    c_step = ad.split;
+  }
+  if (c_first < c_end) {
     for (int i = tid; i < G * D; i += NFA_BLOCK)
       s_q[i] = load_any(p.q, ((int64_t)t * p.hq + kh * G) * D + i, p.q_dtype);
   }
@@ -146,8 +162,8 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int rr = tid / TPR;  // row within a pass
   const KV *kpool = (const KV *)p.k_pool;
   const KV *vpool = (const KV *)p.v_pool;
-  for (int c0 = c_first; c0 < n; c0 += c_step) {
-    const int cn = n - c0 < ad.split ? n - c0 : ad.split;
+  for (int c0 = c_first; c0 < c_end; c0 += c_step) {
+    const int cn = c_end - c0 < ad.split ? c_end - c0 : ad.split;
     if (LOOP && c0 != c_first) __syncthreads();  // the previous chunk's readers are done
     for (int i = tid; i < cn; i += NFA_BLOCK) {
       const int sl = grow[c0 + i];
@@ -255,6 +271,24 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   // s_m / s_z of a head were last written before the barrier that precedes
   // the P.V step (or, with no chunk, by the same thread that reads them)
+  if constexpr (PART) {
+    // state [split][t][head]; acc rows of head_dim_v floats
+    const int64_t pb = ((int64_t)split * p.total_q + t) * p.hq + kh * G;
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+      const int o = tid + k * NFA_BLOCK;
+      if (o >= G * (D / 2)) break;
+      const int g = o / (D / 2);
+      const int d = 2 * (o % (D / 2));
+      pt.acc[(pb + g) * D + d] = acc0[k];
+      pt.acc[(pb + g) * D + d + 1] = acc1[k];
+    }
+    if (tid < G) {
+      pt.m[pb + tid] = s_m[tid];
+      pt.z[pb + tid] = s_z[tid];
+    }
+    return;
+  }
   if (LOOP && ad.nsplit == 1) {
     // the whole row in this workgroup: normalise and write the output
 #pragma unroll
@@ -334,6 +368,42 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
 }
 
+// Regions combine: one thread per output element (t, head, dim); the states
+// of region a's splits, then region b's, merge in split order with the
+// online-softmax rescaling.
+__global__ void __launch_bounds__(NFA_BLOCK)
+    nfa_regions_combine_kernel(const NfaAttnCombineParams c) {
+  const int64_t i = (int64_t)blockIdx.x * NFA_BLOCK + threadIdx.x;
+  const int64_t heads = (int64_t)c.total_q * c.hq;
+  if (i >= heads * c.head_dim_v) return;
+  const int64_t th = i / c.head_dim_v;
+  const int d = (int)(i % c.head_dim_v);
+  const float kNegInf = __uint_as_float(0xFF800000u);
+  float m = kNegInf, z = 0.0f, acc = 0.0f;
+  for (int r = 0; r < 2; ++r) {
+    const int ns = r == 0 ? c.nsplit_a : c.nsplit_b;
+    const float *pa = r == 0 ? c.acc_a : c.acc_b;
+    const float *pm = r == 0 ? c.m_a : c.m_b;
+    const float *pz = r == 0 ? c.z_a : c.z_b;
+    for (int sp = 0; sp < ns; ++sp) {
+      const int64_t e = sp * heads + th;
+      const float part_m = pm[e];
+      const float new_m = fmaxf(m, part_m);
+      const float safe_m = new_m == kNegInf ? 0.0f : new_m;
+      const float alpha = expf(m - safe_m);
+      const float beta = expf(part_m - safe_m);
+      acc = acc * alpha + pa[e * c.head_dim_v + d] * beta;
+      z = z * alpha + pz[e] * beta;
+      m = new_m;
+    }
+  }
+  const float o = z == 0.0f ? 0.0f : acc / z;
+  if (c.out_dtype == NFA_DTYPE_BF16)
+    ((uint16_t *)c.out)[i] = bf16_bits(o);
+  else
+    ((float *)c.out)[i] = o;
+}
+
 }  // namespace nfa
 
 extern "C" int64_t nfa_attn_workspace_bytes(const NfaAttnParams *p) {
@@ -341,45 +411,61 @@ extern "C" int64_t nfa_attn_workspace_bytes(const NfaAttnParams *p) {
   return nfa::attn_dims(*p, nfa::device_cus()).w_total;
 }
 
-extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) {
+// Shared argument checks of the gather attention entry points; `tpr` gets
+// the threads per K/V row.  The output pointer is checked by the caller.
+static int32_t check_attn(const NfaAttnParams *p, const char *fn, int *tpr_out) {
   if (p == nullptr || p->abi_version != NFA_ABI_VERSION ||
       p->struct_size != (int32_t)sizeof(NfaAttnParams)) {
-    nfa_set_error("nfa_sparse_attn_decode: ABI mismatch");
+    nfa_set_error("%s: ABI mismatch", fn);
     return NFA_EINVAL;
   }
-  if (p->total_q <= 0) return NFA_OK;
   if (p->hkv <= 0 || p->hq % p->hkv != 0 || p->hq / p->hkv > nfa::AGMAX) {
-    nfa_set_error("nfa_sparse_attn_decode: unsupported heads hq=%d hkv=%d",
-                  p->hq, p->hkv);
+    nfa_set_error("%s: unsupported heads hq=%d hkv=%d", fn, p->hq, p->hkv);
     return NFA_EINVAL;
   }
   const int chunk = p->kv_dtype == NFA_DTYPE_BF16 ? 8 : 4;
   const int tpr = p->head_dim / chunk;
   if (p->head_dim != p->head_dim_v || p->head_dim % chunk != 0 ||
       !(tpr == 8 || tpr == 16 || tpr == 32)) {
-    nfa_set_error("nfa_sparse_attn_decode: unsupported head dims %d/%d "
+    nfa_set_error("%s: unsupported head dims %d/%d "
                   "(K and V dims must match and span 8, 16 or 32 chunks of 16 bytes)",
-                  p->head_dim, p->head_dim_v);
+                  fn, p->head_dim, p->head_dim_v);
     return NFA_EINVAL;
   }
   if (p->kv_dtype != NFA_DTYPE_BF16 && p->kv_dtype != NFA_DTYPE_F32) {
-    nfa_set_error("nfa_sparse_attn_decode: unsupported kv dtype %d", p->kv_dtype);
+    nfa_set_error("%s: unsupported kv dtype %d", fn, p->kv_dtype);
     return NFA_EINVAL;
   }
   if (p->max_vis <= 0 || p->page <= 0 || p->pool_pages <= 0 ||
       p->gather_rows <= 0) {
-    nfa_set_error("nfa_sparse_attn_decode: bad max_vis/page/pool/rows");
+    nfa_set_error("%s: bad max_vis/page/pool/rows", fn);
     return NFA_EINVAL;
   }
   if (p->tokens_per_split < 0 || p->tokens_per_split > nfa::kSplitMax) {
-    nfa_set_error("nfa_sparse_attn_decode: tokens_per_split must be in [0,64]");
+    nfa_set_error("%s: tokens_per_split must be in [0,64]", fn);
     return NFA_EINVAL;
   }
   if (!p->q || !p->k_pool || !p->v_pool || !p->gather || !p->vis_lens ||
-      !p->query_to_req || !p->out) {
+      !p->query_to_req) {
+    nfa_set_error("%s: null device pointer", fn);
+    return NFA_EINVAL;
+  }
+  *tpr_out = tpr;
+  return NFA_OK;
+}
+
+extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) {
+  if (p != nullptr && p->abi_version == NFA_ABI_VERSION &&
+      p->struct_size == (int32_t)sizeof(NfaAttnParams) && p->total_q <= 0)
+    return NFA_OK;
+  int tpr = 0;
+  const int32_t rc = check_attn(p, "nfa_sparse_attn_decode", &tpr);
+  if (rc != NFA_OK) return rc;
+  if (!p->out) {
     nfa_set_error("nfa_sparse_attn_decode: null device pointer");
     return NFA_EINVAL;
   }
+  const NfaAttnPartial none{};
   const int cus = nfa::device_cus();
   const nfa::AttnDims ad = nfa::attn_dims(*p, cus);
   if (p->workspace == nullptr || p->workspace_bytes < ad.w_total) {
@@ -395,10 +481,10 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
   do {                                                                               \
     if (loop)                                                                        \
       hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, true>), grid,                \
-                         dim3(NFA_BLOCK), 0, s, *p, cus);                                 \
+                         dim3(NFA_BLOCK), 0, s, *p, cus, none);                          \
     else                                                                             \
       hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, false>), grid,               \
-                         dim3(NFA_BLOCK), 0, s, *p, cus);                                 \
+                         dim3(NFA_BLOCK), 0, s, *p, cus, none);                          \
   } while (0)
   if (tpr == 8) {
     if (bf) NFA_ATTN_LAUNCH(uint16_t, 8); else NFA_ATTN_LAUNCH(float, 8);
@@ -414,4 +500,89 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
     return NFA_ELAUNCH;
   }
   return NFA_OK;
+}
+
+extern "C" int32_t nfa_sparse_attn_partial(const NfaAttnParams *p,
+                                           const NfaAttnPartial *pt, void *stream) {
+  if (pt == nullptr || pt->abi_version != NFA_ABI_VERSION ||
+      pt->struct_size != (int32_t)sizeof(NfaAttnPartial)) {
+    nfa_set_error("nfa_sparse_attn_partial: ABI mismatch");
+    return NFA_EINVAL;
+  }
+  if (p != nullptr && p->abi_version == NFA_ABI_VERSION &&
+      p->struct_size == (int32_t)sizeof(NfaAttnParams) && p->total_q <= 0)
+    return NFA_OK;
+  int tpr = 0;
+  const int32_t rc = check_attn(p, "nfa_sparse_attn_partial", &tpr);
+  if (rc != NFA_OK) return rc;
+  if (pt->nsplit < 1 || pt->nsplit > 65535 || pt->block_tokens < 1) {
+    nfa_set_error("nfa_sparse_attn_partial: nsplit %d / block_tokens %d out of range",
+                  pt->nsplit, pt->block_tokens);
+    return NFA_EINVAL;
+  }
+  if (!pt->acc || !pt->m || !pt->z) {
+    nfa_set_error("nfa_sparse_attn_partial: null state pointer");
+    return NFA_EINVAL;
+  }
+  NfaAttnParams q = *p;
+  if (q.tokens_per_split == 0) q.tokens_per_split = nfa::kSplitMax;
+  const int cus = nfa::device_cus();
+  dim3 grid(pt->nsplit, p->total_q * p->hkv);
+  hipStream_t s = (hipStream_t)stream;
+  const bool bf = p->kv_dtype == NFA_DTYPE_BF16;
+#define NFA_PART_LAUNCH(KV, TPR)                                                       \
+  hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, true, true>), grid, dim3(NFA_BLOCK), \
+                     0, s, q, cus, *pt)
+  if (tpr == 8) {
+    if (bf) NFA_PART_LAUNCH(uint16_t, 8); else NFA_PART_LAUNCH(float, 8);
+  } else if (tpr == 16) {
+    if (bf) NFA_PART_LAUNCH(uint16_t, 16); else NFA_PART_LAUNCH(float, 16);
+  } else {
+    if (bf) NFA_PART_LAUNCH(uint16_t, 32); else NFA_PART_LAUNCH(float, 32);
+  }
+#undef NFA_PART_LAUNCH
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    nfa_set_error("nfa_sparse_attn_partial: launch failed: %s", hipGetErrorString(err));
+    return NFA_ELAUNCH;
+  }
+  return NFA_OK;
+}
+
+extern "C" int32_t nfa_attn_regions_combine(const NfaAttnCombineParams *c, void *stream) {
+  if (c == nullptr || c->abi_version != NFA_ABI_VERSION ||
+      c->struct_size != (int32_t)sizeof(NfaAttnCombineParams)) {
+    nfa_set_error("nfa_attn_regions_combine: ABI mismatch");
+    return NFA_EINVAL;
+  }
+  if (c->total_q <= 0) return NFA_OK;
+  if (c->hq <= 0 || c->head_dim_v <= 0 || c->nsplit_a < 0 || c->nsplit_b < 0 ||
+      (c->out_dtype != NFA_DTYPE_BF16 && c->out_dtype != NFA_DTYPE_F32)) {
+    nfa_set_error("nfa_attn_regions_combine: bad shape or dtype");
+    return NFA_EINVAL;
+  }
+  if (!c->out || (c->nsplit_a > 0 && (!c->acc_a || !c->m_a || !c->z_a)) ||
+      (c->nsplit_b > 0 && (!c->acc_b || !c->m_b || !c->z_b))) {
+    nfa_set_error("nfa_attn_regions_combine: null device pointer");
+    return NFA_EINVAL;
+  }
+  const int64_t n = (int64_t)c->total_q * c->hq * c->head_dim_v;
+  const int64_t blocks = (n + NFA_BLOCK - 1) / NFA_BLOCK;
+  if (blocks > 0x7FFFFFFF) {
+    nfa_set_error("nfa_attn_regions_combine: too many outputs");
+    return NFA_EINVAL;
+  }
+  hipLaunchKernelGGL(nfa::nfa_regions_combine_kernel, dim3((unsigned)blocks),
+                     dim3(NFA_BLOCK), 0, (hipStream_t)stream, *c);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) {
+    nfa_set_error("nfa_attn_regions_combine: launch failed: %s", hipGetErrorString(err));
+    return NFA_ELAUNCH;
+  }
+  return NFA_OK;
+}
+
+extern "C" int32_t nfa_attn_partial_size(void) { return (int32_t)sizeof(NfaAttnPartial); }
+extern "C" int32_t nfa_attn_combine_params_size(void) {
+  return (int32_t)sizeof(NfaAttnCombineParams);
 }

@@ -79,6 +79,25 @@ class NfaAttnParams(ctypes.Structure):
     ]
 
 
+class NfaAttnPartial(ctypes.Structure):
+    _fields_ = [
+        ('abi_version', _i32), ('struct_size', _i32),
+        ('nsplit', _i32), ('block_tokens', _i32),
+        ('acc', _ptr), ('m', _ptr), ('z', _ptr),
+    ]
+
+
+class NfaAttnCombineParams(ctypes.Structure):
+    _fields_ = [
+        ('abi_version', _i32), ('struct_size', _i32),
+        ('total_q', _i32), ('hq', _i32), ('head_dim_v', _i32), ('out_dtype', _i32),
+        ('nsplit_a', _i32), ('nsplit_b', _i32),
+        ('acc_a', _ptr), ('m_a', _ptr), ('z_a', _ptr),
+        ('acc_b', _ptr), ('m_b', _ptr), ('z_b', _ptr),
+        ('out', _ptr),
+    ]
+
+
 EPI_PLAIN = 0
 EPI_RESIDUAL = 1
 EPI_SILU_GATE = 2
@@ -126,7 +145,8 @@ EXPORTS = (
     'nfa_select_layer', 'nfa_sparse_attn_decode', 'nfa_paged_write_decode',
     'nfa_paged_write_prefill', 'nfa_linear_params_size', 'nfa_rope_params_size',
     'nfa_decode_linear', 'nfa_qk_norm_rope_decode', 'nfa_rmsnorm_decode',
-    'nfa_gate_params_size', 'nfa_region_profile',
+    'nfa_gate_params_size', 'nfa_region_profile', 'nfa_attn_partial_size',
+    'nfa_attn_combine_params_size', 'nfa_sparse_attn_partial', 'nfa_attn_regions_combine',
 )
 
 _lib = None
@@ -182,6 +202,13 @@ def load_library(path: str = None):
         lib.nfa_gate_params_size.restype = _i32
         lib.nfa_region_profile.restype = _i32
         lib.nfa_region_profile.argtypes = [ctypes.POINTER(NfaGateParams), _ptr]
+        lib.nfa_attn_partial_size.restype = _i32
+        lib.nfa_attn_combine_params_size.restype = _i32
+        lib.nfa_sparse_attn_partial.restype = _i32
+        lib.nfa_sparse_attn_partial.argtypes = [
+            ctypes.POINTER(NfaAttnParams), ctypes.POINTER(NfaAttnPartial), _ptr]
+        lib.nfa_attn_regions_combine.restype = _i32
+        lib.nfa_attn_regions_combine.argtypes = [ctypes.POINTER(NfaAttnCombineParams), _ptr]
         if lib.nfa_abi_version() != ABI_VERSION:
             raise NativeError('libnfa_hip ABI version mismatch')
         if lib.nfa_select_params_size() != ctypes.sizeof(NfaSelectParams):
@@ -194,6 +221,10 @@ def load_library(path: str = None):
             raise NativeError('NfaRopeParams layout mismatch')
         if lib.nfa_gate_params_size() != ctypes.sizeof(NfaGateParams):
             raise NativeError('NfaGateParams layout mismatch')
+        if lib.nfa_attn_partial_size() != ctypes.sizeof(NfaAttnPartial):
+            raise NativeError('NfaAttnPartial layout mismatch')
+        if lib.nfa_attn_combine_params_size() != ctypes.sizeof(NfaAttnCombineParams):
+            raise NativeError('NfaAttnCombineParams layout mismatch')
         if path is None:
             _lib = lib
         return lib

@@ -127,18 +127,43 @@ def sparse_paged_attention_gather(cache_layer, q, gather_indices, visible_lens,
     hk = cache_layer.num_kv_heads
     if hq % hk != 0:
         raise ValueError('GQA requires HQ % HK == 0')
-    if (gather_indices.ndim != 3 or gather_indices.shape[1] != hk
-            or visible_lens.shape != gather_indices.shape[:2]):
-        raise ValueError('gather attention expects indices [B,HK,K] and lens [B,HK]')
     page = cache_layer.geometry.page
     if page & (page - 1):
         raise ValueError('sparse gather attention requires power-of-two page size')
+    _check_gather(gather_indices, visible_lens, hk)
     nat.require_hip(q, 'sparse_paged_attention_gather')
     lib = nat.load_library()
     total_q = q.shape[0]
     out = q.new_empty((total_q, hq, cache_layer.head_dim_v))
     if total_q == 0:
         return out
+    p, keep = _attn_params(cache_layer, q, gather_indices, visible_lens,
+                           query_to_req, scale, tokens_per_split)
+    p.out = out.data_ptr()
+    need = lib.nfa_attn_workspace_bytes(ctypes.byref(p))
+    ws = _scratch(workspace, ('nfa_attn_scratch', total_q, hk, p.max_vis, hq,
+                              p.head_dim_v, p.tokens_per_split), need, q.device)
+    p.workspace = ws.data_ptr()
+    p.workspace_bytes = ws.numel()
+    nat.check(lib.nfa_sparse_attn_decode(ctypes.byref(p), nat.stream_handle()),
+              'sparse_paged_attention_gather')
+    del keep
+    return out
+
+
+def _check_gather(gather_indices, visible_lens, hk):
+    if (gather_indices.ndim != 3 or gather_indices.shape[1] != hk
+            or visible_lens.shape != gather_indices.shape[:2]):
+        raise ValueError('gather attention expects indices [B,HK,K] and lens [B,HK]')
+
+
+def _attn_params(cache_layer, q, gather_indices, visible_lens, query_to_req, scale,
+                 tokens_per_split):
+    """NfaAttnParams of a gather attention call (``out`` and the workspace
+    left unset) and the converted tensors it points into."""
+    hq = q.shape[1]
+    hk = cache_layer.num_kv_heads
+    total_q = q.shape[0]
     qc = q if q.is_contiguous() else q.contiguous()
     gather = gather_indices
     if gather.dtype != torch.int32 or not gather.is_contiguous():
@@ -156,7 +181,7 @@ def sparse_paged_attention_gather(cache_layer, q, gather_indices, visible_lens,
     p.total_q = total_q
     p.hq, p.hkv = hq, hk
     p.head_dim, p.head_dim_v = cache_layer.head_dim_k, cache_layer.head_dim_v
-    p.page = page
+    p.page = cache_layer.geometry.page
     p.gather_rows = gather.shape[0]
     p.max_vis = gather.shape[-1]
     p.kv_dtype = nat.dtype_code(cache_layer.kv_pool_k.dtype)
@@ -170,12 +195,113 @@ def sparse_paged_attention_gather(cache_layer, q, gather_indices, visible_lens,
     p.gather = gather.data_ptr()
     p.vis_lens = lens.data_ptr()
     p.query_to_req = q2r.data_ptr()
-    p.out = out.data_ptr()
-    need = lib.nfa_attn_workspace_bytes(ctypes.byref(p))
-    ws = _scratch(workspace, ('nfa_attn_scratch', total_q, hk, p.max_vis, hq,
-                              p.head_dim_v, p.tokens_per_split), need, q.device)
-    p.workspace = ws.data_ptr()
-    p.workspace_bytes = ws.numel()
-    nat.check(lib.nfa_sparse_attn_decode(ctypes.byref(p), nat.stream_handle()),
-              'sparse_paged_attention_gather')
+    return p, (qc, q2r)
+
+
+def _partial_block_tokens(cache_layer, total_q):
+    """Token block of the split partition (reference
+    ops/paged_region_kernels.py:752-757)."""
+    if cache_layer.head_dim_k >= 256 or cache_layer.head_dim_v >= 256:
+        return 64
+    return 128 if total_q <= 8 else 64
+
+
+def sparse_paged_attention_gather_partial(cache_layer, q, gather_indices, visible_lens,
+                                          query_to_req, *, scale, workspace, name, nsplit):
+    """One region's attention as fp32 split states, without normalising
+    (reference ops/paged_region_kernels.py:727-780).
+
+    Split ``s`` of a (query row, kv head) with ``n`` visible slots covers the
+    token blocks ``[s*nb//nsplit, (s+1)*nb//nsplit)`` of ``nb =
+    ceil(n / block)`` (block 128 for at most 8 query rows, else 64; 64 for
+    head dims of 256).  Returns ``(acc [nsplit, T, HQ, DV], m [nsplit, T,
+    HQ], z [nsplit, T, HQ])`` from fixed buffers of ``workspace`` keyed by
+    ``name``: ``m`` the split's maximum score (``-inf`` if it has none),
+    ``z = sum exp(s_i - m)``, ``acc = sum exp(s_i - m) v_i``."""
+    if not q.is_cuda:
+        raise RuntimeError('split regions require a HIP device')
+    if q.ndim != 3 or q.shape[-1] != cache_layer.head_dim_k:
+        raise ValueError('split regions expect flat [T,HQ,D] query')
+    hq = q.shape[1]
+    hk = cache_layer.num_kv_heads
+    if hq % hk != 0:
+        raise ValueError('GQA requires HQ % HK == 0')
+    page = cache_layer.geometry.page
+    if page & (page - 1):
+        raise ValueError('split regions require power-of-two page size')
+    if cache_layer.head_dim_k < 16 or cache_layer.head_dim_v < 16:
+        raise RuntimeError('split regions require grouped attention geometry')
+    nsplit = int(nsplit)
+    if nsplit < 1:
+        raise ValueError('nsplit must be positive')
+    _check_gather(gather_indices, visible_lens, hk)
+    nat.require_hip(q, 'sparse_paged_attention_gather_partial')
+    lib = nat.load_library()
+    total_q = q.shape[0]
+    dv = cache_layer.head_dim_v
+    part_acc = _state(workspace, f'gather_split_{name}_acc', (nsplit, total_q, hq, dv),
+                      q.device)
+    part_m = _state(workspace, f'gather_split_{name}_m', (nsplit, total_q, hq), q.device)
+    part_z = _state(workspace, f'gather_split_{name}_z', (nsplit, total_q, hq), q.device)
+    if total_q == 0:
+        return part_acc, part_m, part_z
+    p, keep = _attn_params(cache_layer, q, gather_indices, visible_lens, query_to_req,
+                           scale, 0)
+    pt = nat.NfaAttnPartial()
+    pt.abi_version = nat.ABI_VERSION
+    pt.struct_size = ctypes.sizeof(nat.NfaAttnPartial)
+    pt.nsplit = nsplit
+    pt.block_tokens = _partial_block_tokens(cache_layer, total_q)
+    pt.acc, pt.m, pt.z = part_acc.data_ptr(), part_m.data_ptr(), part_z.data_ptr()
+    nat.check(lib.nfa_sparse_attn_partial(ctypes.byref(p), ctypes.byref(pt),
+                                          nat.stream_handle()),
+              'sparse_paged_attention_gather_partial')
+    del keep
+    return part_acc, part_m, part_z
+
+
+def _state(workspace, key, shape, device):
+    """fp32 state buffer of a fixed address, cached in ``workspace``."""
+    if workspace is None:
+        return torch.empty(shape, dtype=torch.float32, device=device)
+    buf = workspace.get(key)
+    if buf is None or tuple(buf.shape) != tuple(shape):
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f'state {key!r} must be allocated before capture')
+        buf = torch.empty(shape, dtype=torch.float32, device=device)
+        workspace[key] = buf
+    return buf
+
+
+def sparse_paged_attention_regions_combine(q, protected_parts, middle_parts, *, workspace):
+    """Merge two disjoint regions' split states into the attention output
+    ``[T, HQ, DV]`` in the dtype of ``q`` (reference
+    ops/paged_region_kernels.py:783-797): protected splits first, then the
+    middle's, each folded in with the online-softmax rescaling; rows whose
+    denominator is 0 output 0."""
+    del workspace  # the combine keeps no state
+    total_q, hq = q.shape[:2]
+    dv = protected_parts[0].shape[-1]
+    for parts in (protected_parts, middle_parts):
+        acc, m, z = parts
+        if (acc.dtype != torch.float32 or acc.shape[1:] != (total_q, hq, dv)
+                or m.shape != acc.shape[:3] or z.shape != acc.shape[:3]
+                or not (acc.is_contiguous() and m.is_contiguous() and z.is_contiguous())):
+            raise ValueError('region states must be contiguous fp32 [S,T,HQ,DV] / [S,T,HQ]')
+    nat.require_hip(q, 'sparse_paged_attention_regions_combine')
+    lib = nat.load_library()
+    out = q.new_empty((total_q, hq, dv))
+    if total_q == 0:
+        return out
+    c = nat.NfaAttnCombineParams()
+    c.abi_version = nat.ABI_VERSION
+    c.struct_size = ctypes.sizeof(nat.NfaAttnCombineParams)
+    c.total_q, c.hq, c.head_dim_v = total_q, hq, dv
+    c.out_dtype = nat.dtype_code(q.dtype)
+    c.nsplit_a, c.nsplit_b = protected_parts[0].shape[0], middle_parts[0].shape[0]
+    c.acc_a, c.m_a, c.z_a = (t.data_ptr() for t in protected_parts)
+    c.acc_b, c.m_b, c.z_b = (t.data_ptr() for t in middle_parts)
+    c.out = out.data_ptr()
+    nat.check(lib.nfa_attn_regions_combine(ctypes.byref(c), nat.stream_handle()),
+              'sparse_paged_attention_regions_combine')
     return out

@@ -43,7 +43,6 @@ def _fusable(layer, hidden_states, cache):
     attn = layer.self_attn
     return (isinstance(cache, GraphReadyPagedRegionCache)
             and hasattr(attn, 'indexer')
-            and getattr(attn.indexer.args, 'nfa_operator_mode', 'off') == 'off'
             and hidden_states.dim() == 3 and hidden_states.shape[1] == 1
             and hidden_states.shape[0] <= LINEAR_MAX_ROWS
             and hidden_states.dtype == torch.bfloat16 and hidden_states.is_cuda
@@ -89,13 +88,22 @@ def nfa_decode_layer_forward(self, hidden_states, attention_mask=None,
         hq=hq, hkv=hkv, head_dim=d)
     layer_idx = attn.layer_idx
     slots = cache.slot_mapping_for_layer(layer_idx)[:b]
-    select_topk_for_layer_batched(
-        cache, layer_idx, cache.active_req_ids, q, attention=attn,
-        decode_write=(k.view(b, hkv, 1, d), v.view(b, hkv, 1, d), slots))
-    o = decode_graph_ready(
-        attn, q, cache, gather_indices=cache.gather_indices_for_layer(layer_idx),
-        visible_lens=cache.visible_lens_for_layer(layer_idx),
-        query_to_req=cache.query_to_req_buf)
+    mode = getattr(attn.indexer.args, 'nfa_operator_mode', 'off')
+    if mode == 'off':
+        select_topk_for_layer_batched(
+            cache, layer_idx, cache.active_req_ids, q, attention=attn,
+            decode_write=(k.view(b, hkv, 1, d), v.view(b, hkv, 1, d), slots))
+        o = decode_graph_ready(
+            attn, q, cache, gather_indices=cache.gather_indices_for_layer(layer_idx),
+            visible_lens=cache.visible_lens_for_layer(layer_idx),
+            query_to_req=cache.query_to_req_buf)
+    elif mode in ('serial', 'overlap'):
+        from .qwen3_attn_patch import _disjoint_regions_attention
+        o = _disjoint_regions_attention(attn, q, k.view(b, hkv, 1, d),
+                                        v.view(b, hkv, 1, d), cache, slots,
+                                        mode == 'overlap')
+    else:
+        raise ValueError(f'unknown NFA operator mode: {mode}')
     h1, = decode_linear(o.view(b, hq * d), (attn.o_proj.weight,), residual=x)
     a, = decode_linear(h1, (mlp.gate_proj.weight, mlp.up_proj.weight),
                        norm_weight=self.post_attention_layernorm.weight,

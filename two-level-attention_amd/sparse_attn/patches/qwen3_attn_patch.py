@@ -63,28 +63,98 @@ def nfa_decode_attention(module, query_states, key_states, value_states, cache,
 
     ``query_states`` ``[B, HQ, 1, D]`` and ``key_states`` / ``value_states``
     ``[B, HKV, 1, D]`` are post-RoPE.  Returns the o_proj output
-    ``[B, 1, hidden]``.
+    ``[B, 1, hidden]``.  ``--nfa_operator_mode`` (reference
+    qwen3_attn_patch.py:103-195): ``off`` selects the union and attends it
+    in one pass; ``serial`` and ``overlap`` attend the protected sink/SWA set
+    and the selected middle apart and merge the two softmax states
+    (protected first), ``overlap`` running the protected part on a side
+    stream while the selection runs.
     """
     from ..indexer.nfa_layer_batch_selector import select_topk_for_layer_batched
     from ..ops.paged_region_kernels_nfa import decode_graph_ready
 
     operator_mode = getattr(module.indexer.args, 'nfa_operator_mode', 'off')
-    if operator_mode != 'off':
-        raise ValueError(
-            f'NFA operator mode {operator_mode!r} is not built; use "off"')
     batch = input_shape[0]
     layer_idx = module.layer_idx
     slot_mapping = cache.slot_mapping_for_layer(layer_idx)[:batch]
     q_flat = query_states[:, :, 0]
-    select_topk_for_layer_batched(
-        cache, layer_idx, cache.active_req_ids, q_flat, attention=module,
-        decode_write=(key_states, value_states, slot_mapping))
-    result = decode_graph_ready(
-        module, q_flat, cache,
-        gather_indices=cache.gather_indices_for_layer(layer_idx),
-        visible_lens=cache.visible_lens_for_layer(layer_idx),
-        query_to_req=cache.query_to_req_buf)
+    if operator_mode == 'off':
+        select_topk_for_layer_batched(
+            cache, layer_idx, cache.active_req_ids, q_flat, attention=module,
+            decode_write=(key_states, value_states, slot_mapping))
+        result = decode_graph_ready(
+            module, q_flat, cache,
+            gather_indices=cache.gather_indices_for_layer(layer_idx),
+            visible_lens=cache.visible_lens_for_layer(layer_idx),
+            query_to_req=cache.query_to_req_buf)
+    elif operator_mode in ('serial', 'overlap'):
+        result = _disjoint_regions_attention(
+            module, q_flat, key_states, value_states, cache, slot_mapping,
+            operator_mode == 'overlap')
+    else:
+        raise ValueError(f'unknown NFA operator mode: {operator_mode}')
     return module.o_proj(result.reshape(*input_shape, -1).contiguous())
+
+
+def _disjoint_regions_attention(module, q_flat, key_states, value_states, cache,
+                                slot_mapping, overlap):
+    """Protected ∥ middle attention of one layer (reference
+    qwen3_attn_patch.py:123-195): the current K/V is written first, so both
+    arms read the same committed arena; serial and overlap differ only in
+    the stream of the protected arm, the merge order is the same."""
+    from ..indexer.nfa_layer_batch_selector import select_topk_for_layer_batched
+    from ..ops.paged_region_kernels import (sparse_paged_attention_gather_partial,
+                                            sparse_paged_attention_regions_combine)
+    from ..ops.paged_region_kernels_nfa import build_protected_gather, split_gather_buffers
+
+    layer_idx = module.layer_idx
+    batch = q_flat.shape[0]
+    cache.write_decode(layer_idx, key_states, value_states, slot_mapping)
+    prot_gather, prot_lens, mid_gather, mid_lens = split_gather_buffers(
+        cache, layer_idx, batch)
+    workspace = cache._nfa_selector_workspace
+    q_flat = q_flat if q_flat.is_contiguous() else q_flat.contiguous()
+    layer = cache.layers[layer_idx]
+
+    def protected_partial():
+        build_protected_gather(cache, layer_idx, module.indexer, prot_gather, prot_lens)
+        return sparse_paged_attention_gather_partial(
+            layer, q_flat, prot_gather, prot_lens, cache.query_to_req_buf,
+            scale=module.scaling, workspace=workspace, name='protected', nsplit=1)
+
+    def middle_partial():
+        select_topk_for_layer_batched(
+            cache, layer_idx, cache.active_req_ids, q_flat, attention=module,
+            middle_only=True, selection_output=(mid_gather, mid_lens))
+        return sparse_paged_attention_gather_partial(
+            layer, q_flat, mid_gather, mid_lens, cache.query_to_req_buf,
+            scale=module.scaling, workspace=workspace, name='middle', nsplit=4)
+
+    if overlap:
+        primitives = workspace.get('nfa_overlap_primitives')
+        if primitives is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError('overlap streams must be warmed before capture')
+            # default priority, like every stream of this package
+            primitives = (torch.cuda.Stream(device=q_flat.device), torch.cuda.Event(),
+                          torch.cuda.Event())
+            workspace['nfa_overlap_primitives'] = primitives
+        side, fork, join = primitives
+        main = torch.cuda.current_stream()
+        fork.record(main)
+        side.wait_event(fork)
+        with torch.cuda.stream(side):
+            prot_parts = protected_partial()
+            join.record(side)
+        mid_parts = middle_partial()
+        main.wait_event(join)
+        # the protected arm's buffers are reused by the next layer's side
+        # launches only after this join
+    else:
+        prot_parts = protected_partial()
+        mid_parts = middle_partial()
+    return sparse_paged_attention_regions_combine(
+        q_flat, prot_parts, mid_parts, workspace=workspace)
 
 
 def _rope(module, query_states, key_states, cos, sin):
