@@ -49,6 +49,9 @@ def parse():
                     help='request lengths drawn uniformly from [LO, HI] (seeded) '
                          'instead of --ctx for every request')
     ap.add_argument('--layers', type=int, default=36)
+    ap.add_argument('--operator-mode', choices=['off', 'serial', 'overlap'], default='off',
+                    help='decode attention of the timed step: one union pass (off) or '
+                         'protected and middle apart, then merged (serial / overlap)')
     ap.add_argument('--kernel-rounds', type=int, default=20)
     ap.add_argument('--cpu-seconds', type=float, default=15.0,
                     help='budget of the CPU oracle baseline sample')
@@ -135,7 +138,7 @@ def build_workload(torch, args, device):
     torch.cuda.synchronize()
     return SimpleNamespace(cache=cache, indexer=indexer, attn=attn, q=q, kn=kn,
                            vn=vn, hkv=hkv, hq=hq, d=d, page=page, req_ids=req_ids,
-                           lengths=lengths)
+                           lengths=lengths, mode=args.operator_mode)
 
 
 def run_layer(w, layer, outs):
@@ -143,6 +146,12 @@ def run_layer(w, layer, outs):
         select_topk_for_layer_batched
     from sparse_attn.ops.paged_region_kernels_nfa import decode_graph_ready
     cache = w.cache
+    if w.mode != 'off':
+        from sparse_attn.patches.qwen3_attn_patch import disjoint_regions_attention
+        outs[layer] = disjoint_regions_attention(
+            w.attn[layer], w.q[layer], w.kn[layer], w.vn[layer], cache,
+            cache.slot_mapping_for_layer(layer)[:len(w.req_ids)], w.mode == 'overlap')
+        return
     select_topk_for_layer_batched(
         cache, layer, w.req_ids, w.q[layer], attention=w.attn[layer],
         decode_write=(w.kn[layer], w.vn[layer],
@@ -632,6 +641,7 @@ def main():
                            if args.ragged else f'{args.ctx // 1024}K context')
                         + ', page 16, hipGraph',
             'layers': args.layers, 'batch': args.batch,
+            'operator_mode': args.operator_mode,
             'context': (lengths if args.ragged else args.ctx),
             **geometry,
             'nfa': 'far minmax / near avg, K1 128 (32 near), near_len 4096, '

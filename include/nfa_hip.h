@@ -86,7 +86,10 @@ typedef struct NfaSelectParams {
   int32_t protected_only;     /* sink/SWA union with an empty middle only
                                  (both regions skipped); no statistics */
   float scale;                /* attention.scaling */
-  float pad1;
+  int32_t l2_quant;           /* --nfa_l2_quant: L2 logits over 4-bit keys
+                                 (min_max_per_token_quant, tia_indexer.py:
+                                 22-31) from the packed side cache; needs
+                                 l2_keys_l, 32 L2 dims and bf16 KV */
 
   /* cache state (device pointers) */
   void *k_pool_l, *v_pool_l;          /* [P+1,1,hkv,page,D] of this layer */
@@ -112,7 +115,11 @@ typedef struct NfaSelectParams {
   /* optional L2 side copy of this layer, KV dtype: the L2 dims of every
      visible token in fine_dims order, [max_req, hkv, max_blocks * bs,
      fine_dsub]; valid with the statistics (written by the same rebuild and
-     incremental update).  NULL: the L2 logits read the K pool. */
+     incremental update).  NULL: the L2 logits read the K pool.  With
+     l2_quant: 20 bytes per (request, kv head, token) slot instead -- the 16
+     bytes of 4-bit codes of all slots (dim d in nibble d % 2 of byte d / 2),
+     then the 4 bytes of (bf16 scale, bf16 zero) of all slots, slot =
+     (req * hkv + kv) * max_blocks * bs + token. */
   void *l2_keys_l;
   /* optional fp32 running sums of each request's last (partial) L1 page,
      [max_req, hkv, dsub], valid with the statistics: with them a decode step
@@ -273,12 +280,14 @@ typedef struct NfaAttnPartial {
 /* Disjoint-region attention (protected and middle sets attended apart, then
    merged).  The partial replaces sparse_paged_attention_gather_partial,
    sparse_attn/ops/paged_region_kernels.py:727-780 (kernel :367-530 with
-   WRITE_PARTIAL): p->out, p->workspace and p->workspace_bytes are unused;
-   padding rows store (0, -inf, 0).  The combine replaces
+   WRITE_PARTIAL): p->out is unused, p->workspace holds
+   nfa_attn_partial_workspace_bytes() bytes (zero-filled once, counters left
+   at zero); padding rows store (0, -inf, 0).  The combine replaces
    sparse_paged_attention_regions_combine, :783-797 (kernel :533-575): the
    splits of region a, then those of region b, merge in split order. */
 int32_t nfa_sparse_attn_partial(const NfaAttnParams *p, const NfaAttnPartial *pt,
                                 void *stream);
+int64_t nfa_attn_partial_workspace_bytes(const NfaAttnParams *p, const NfaAttnPartial *pt);
 
 typedef struct NfaAttnCombineParams {
   int32_t abi_version;

@@ -38,7 +38,9 @@ top-quota + hole fill and the final union against brute force, and the
 attention against torch softmax.  ``tests/test_oracle_known_answers.py``
 checks the region geometry, bounds and fixed quotas against the known
 answers of the reference's own tests.  ``fake_quant4`` (the optional 4-bit
-L2 keys, read by no selector code of the reference) is parity unpinned.
+L2 keys of ``--nfa_l2_quant``, which no selector code of the reference
+reads) is pinned against torch's own bf16 evaluation of the reference
+formula (tia_indexer.py:22-31).
 L1 page indices above 65535 use exact (score, page) order; the reference
 packs the page into 16 bits (``selector:1481-1484``) and would alias there.
 """
@@ -481,10 +483,11 @@ def owned_slots(cfg: NfaConfig, token, active, pack_r, lower, upper):
 # ---------------------------------------------------------------------------
 
 def fake_quant4(x):
-    """bf16 op-by-op ``min_max_per_token_quant`` over the last axis.
-
-    Parity unpinned: no selector code of the reference reads ``l2_quant``.
-    """
+    """bf16 op-by-op ``min_max_per_token_quant`` over the last axis
+    (reference indexer/tia_indexer.py:22-31): scale = bf16(bf16(max - min)
+    clamped to 1e-9 / 15), zero = -min, code = clamp(round_half_even(
+    bf16(bf16(x + zero) / scale)), 0, 15), result bf16(bf16(code * scale) -
+    zero)."""
     x = bf16r(x)
     mx = x.max(axis=-1, keepdims=True)
     mn = x.min(axis=-1, keepdims=True)

@@ -14,7 +14,7 @@ from sparse_attn.policies.region_geometry import RegionGeometry
 def make_indexer(*, bs=16, k1=128, near_pages=32, k2=1024, sink=4, swa=128,
                  near_len=4096, subspace='tail', l2_subspace='same',
                  near_tokens='off', far_method='minmax', near_method='avg',
-                 cmp_ratio=4):
+                 cmp_ratio=4, l2_quant=False):
     args = nfa_args(subspace=subspace)
     args.tia_block_size = bs
     args.tia_level1_topk = k1
@@ -28,6 +28,7 @@ def make_indexer(*, bs=16, k1=128, near_pages=32, k2=1024, sink=4, swa=128,
     args.nfa_far_method = far_method
     args.nfa_near_method = near_method
     args.tia_level2_cmp_ratio = cmp_ratio
+    args.nfa_l2_quant = l2_quant
     return NFAIndexer(args)
 
 
@@ -75,7 +76,7 @@ def cfg_from(cache, indexer, scaling):
         scale=float(scaling), far_method=indexer.far_method,
         near_method=indexer.near_method,
         kv_dtype='bf16' if layer.kv_pool_k.dtype == torch.bfloat16 else 'fp32',
-        near_tokens=indexer.nt_near_tokens)
+        near_tokens=indexer.nt_near_tokens, l2_quant=indexer.l2_quant)
 
 
 def to_np(t):

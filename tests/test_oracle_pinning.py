@@ -328,6 +328,39 @@ def test_sparse_attention_matches_torch_softmax():
             np.testing.assert_allclose(out[t, h], (w @ vv).numpy(), rtol=1e-9, atol=1e-12)
 
 
+# --- 4-bit L2 keys ------------------------------------------------------------
+
+def _torch_min_max_quant(x):
+    """The reference's per-token 4-bit round trip (tia_indexer.py:22-31),
+    evaluated by torch in bf16: torch rounds every op's result to bf16,
+    which is what the oracle's explicit rounding points restate."""
+    max_val = x.amax(dim=-1, keepdim=True)
+    min_val = x.amin(dim=-1, keepdim=True)
+    scales = (max_val - min_val).clamp(min=1e-9) / 15
+    zeros = -min_val
+    return torch.clamp(torch.round((x + zeros) / scales), 0, 15) * scales - zeros
+
+
+def test_fake_quant4_matches_torch_bf16_ops():
+    rng = np.random.default_rng(44)
+    rows = [rng.standard_normal((4000, 32)) * s for s in (1.0, 1e-3, 37.0)]
+    grid = rng.standard_normal((200, 1)) + np.arange(32)[None, :] * 0.125  # on-grid
+    const = np.full((3, 32), 0.75)                                            # range 0
+    ties = np.tile(np.array([0.0, 15.0] + [0.5 + k for k in range(15)] * 2)[:32],
+                   (2, 1))                                                   # .5 ties
+    x = np.concatenate(rows + [grid, const, ties]).astype(F32)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    want = _torch_min_max_quant(xb).view(torch.int16).numpy().astype(np.int64) & 0xFFFF
+    got = orc.bf16_bits(orc.fake_quant4(xb.float().numpy()))
+    np.testing.assert_array_equal(got, want)
+    # closed forms: a constant row is returned as is (range clamps to 1e-9);
+    # codes round half to even (0.5 -> 0, 1.5 -> 2, ...)
+    np.testing.assert_array_equal(orc.fake_quant4(const.astype(F32)), const)
+    t = orc.fake_quant4(ties[:1].astype(F32))[0]
+    assert t[0] == 0.0 and t[1] == 15.0
+    assert list(t[2:6]) == [0.0, 2.0, 2.0, 4.0]
+
+
 # --- disjoint-region split states and combine --------------------------------
 
 def test_split_bounds_cover_the_row_and_every_split_works():

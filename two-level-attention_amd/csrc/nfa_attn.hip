@@ -39,9 +39,12 @@ struct AttnDims {
 // keep about two workgroups per CU busy (every split workgroup costs a
 // partial write and an arrival; a row with one split writes its output
 // directly).
-__host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p, int cus) {
+// `mult` caller splits per (query row, kv head), each spanning at most
+// `span` slots (1 and max_vis for the plain decode call).
+__host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p, int cus,
+                                              int mult = 1, int span = -1) {
   AttnDims a;
-  a.rows = p.total_q * p.hkv;
+  a.rows = p.total_q * p.hkv * mult;
   int split = p.tokens_per_split;
   if (split <= 0) split = 32;
   a.split = split;
@@ -57,7 +60,7 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p, int cus) {
   }
   const int want = a.rows > 0 ? (2 * cus + a.rows - 1) / a.rows : 1;
   if (want < cap) cap = want;
-  a.nsplit = (p.max_vis + split - 1) / split;
+  a.nsplit = ((span >= 0 ? span : p.max_vis) + split - 1) / split;
   if (a.nsplit > cap) a.nsplit = cap;
   if (a.nsplit < 1) a.nsplit = 1;
   a.part_stride = G * (p.head_dim_v + 2);
@@ -66,6 +69,14 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p, int cus) {
   a.w_part = w; w += (int64_t)4 * a.rows * a.nsplit * a.part_stride;
   a.w_total = w;
   return a;
+}
+
+// Most slots one caller split of a partial call can hold: ceil(nb / nsplit)
+// blocks of the nb = ceil(max_vis / block_tokens).
+__host__ __device__ inline int part_span(const NfaAttnParams &p, const NfaAttnPartial &pt) {
+  const int nb = (p.max_vis + pt.block_tokens - 1) / pt.block_tokens;
+  const int64_t span = (int64_t)((nb + pt.nsplit - 1) / pt.nsplit) * pt.block_tokens;
+  return span < p.max_vis ? (int)span : p.max_vis;
 }
 
 // Two adjacent KV elements of an LDS row as floats.
@@ -84,24 +95,27 @@ __device__ __forceinline__ void lds_pair(const float *v, int d, float *a,
 
 // LOOP: a workgroup may own several chunks (rows wider than nsplit chunks);
 // without it every workgroup owns at most one and nothing is carried.
-// PART (with LOOP): workgroup `split` of a row owns the caller's split --
-// blocks [split * nb / nsplit, (split + 1) * nb / nsplit) of the row's
-// nb = ceil(n / block_tokens) token blocks -- and stores its unnormalised
-// state (acc, m, z) into the caller's buffers instead of merging.
+// PART: grid row y is (query row, kv head, caller split cs) and covers the
+// caller's split -- blocks [cs * nb / nsplit, (cs + 1) * nb / nsplit) of the
+// row's nb = ceil(n / block_tokens) token blocks -- with its own chunks and
+// split workgroups; the merge stores the unnormalised state (acc, m, z)
+// into the caller's buffers instead of the output.
 template <typename KV, int TPR, bool LOOP, bool PART = false>
 __global__ void __launch_bounds__(NFA_BLOCK)
     nfa_attn_kernel(const NfaAttnParams p, int cus, const NfaAttnPartial pt) {
-  static_assert(LOOP || !PART, "a partial split may own several chunks");
   constexpr int CH = Elem<KV>::kChunk;  // dims per 16-byte chunk
   constexpr int D = TPR * CH;           // head dim (K and V)
   constexpr int RPP = NFA_BLOCK / TPR;  // rows per pass
   constexpr int PMAX = kSplitMax / RPP; // passes per split
-  const AttnDims ad = attn_dims(p, cus);
+  const AttnDims ad = PART ? attn_dims(p, cus, pt.nsplit, part_span(p, pt))
+                           : attn_dims(p, cus);
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int w = wave_id();
   const int split = blockIdx.x;
-  const int row = blockIdx.y;
+  const int vrow = blockIdx.y;  // arrival counter and staging row
+  const int row = PART ? vrow / pt.nsplit : vrow;
+  const int cs = PART ? vrow % pt.nsplit : 0;
   const int t = row / p.hkv;
   const int kh = row % p.hkv;
   const int G = p.hq / p.hkv;
@@ -115,10 +129,9 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   __shared__ int s_last;
 
   unsigned char *ws = (unsigned char *)p.workspace;
-  unsigned int *cnt = PART ? nullptr : (unsigned int *)(ws + ad.w_cnt);
-  float *part = PART ? nullptr
-                     : (float *)(ws + ad.w_part) +
-                           ((int64_t)row * ad.nsplit + split) * ad.part_stride;
+  unsigned int *cnt = (unsigned int *)(ws + ad.w_cnt);
+  float *part = (float *)(ws + ad.w_part) +
+                ((int64_t)vrow * ad.nsplit + split) * ad.part_stride;
 
   int req = p.query_to_req[t];
   if (req >= p.gather_rows) req = -1;  // out-of-range rows act as padding
@@ -129,18 +142,17 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   // chunks split, split + nsplit, ... of ad.split slots each; the running
   // (max, denominator, P.V) of the workgroup carries from chunk to chunk
-  int c_first = split * ad.split;
-  int c_step = ad.nsplit * ad.split;
-  int c_end = n;
+  int lo = 0, c_end = n;
   if constexpr (PART) {
-    // consecutive chunks over the caller's split of the row
+    // the caller's split of the row
     const int bt = pt.block_tokens;
     const int nb = (n + bt - 1) / bt;
-    c_first = (int)((int64_t)split * nb / pt.nsplit) * bt;
-    const int b_end = (int)((int64_t)(split + 1) * nb / pt.nsplit);
+    lo = (int)((int64_t)cs * nb / pt.nsplit) * bt;
+    const int b_end = (int)((int64_t)(cs + 1) * nb / pt.nsplit);
     c_end = b_end * bt < n ? b_end * bt : n;
-    c_step = ad.split;
   }
+  const int c_first = lo + split * ad.split;
+  const int c_step = ad.nsplit * ad.split;
   if (c_first < c_end) {
     for (int i = tid; i < G * D; i += NFA_BLOCK)
       s_q[i] = load_any(p.q, ((int64_t)t * p.hq + kh * G) * D + i, p.q_dtype);
@@ -271,9 +283,10 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   // s_m / s_z of a head were last written before the barrier that precedes
   // the P.V step (or, with no chunk, by the same thread that reads them)
-  if constexpr (PART) {
-    // state [split][t][head]; acc rows of head_dim_v floats
-    const int64_t pb = ((int64_t)split * p.total_q + t) * p.hq + kh * G;
+  // caller state [cs][t][head]; acc rows of head_dim_v floats
+  const int64_t pb = ((int64_t)cs * p.total_q + t) * p.hq + kh * G;
+  if (PART && LOOP && ad.nsplit == 1) {
+    // the whole caller split in this workgroup: its state as accumulated
 #pragma unroll
     for (int k = 0; k < OPT; ++k) {
       const int o = tid + k * NFA_BLOCK;
@@ -313,7 +326,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   // (a single-chunk workgroup stored its P.V above; one with no chunk
   // stores zeros here)
-  const bool store_acc = LOOP || c_first >= n;
+  const bool store_acc = LOOP || c_first >= c_end;
 #pragma unroll
   for (int k = 0; k < OPT; ++k) {
     const int o = tid + k * NFA_BLOCK;
@@ -329,10 +342,10 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
 
   // arrival; the last split of the (row, kv) merges
-  if (!arrive_last(&cnt[row], (unsigned int)ad.nsplit, &s_last)) return;
+  if (!arrive_last(&cnt[vrow], (unsigned int)ad.nsplit, &s_last)) return;
 
   const float *base = (const float *)(ws + ad.w_part) +
-                      (int64_t)row * ad.nsplit * ad.part_stride;
+                      (int64_t)vrow * ad.nsplit * ad.part_stride;
   // split maxima and denominators -> LDS (one round of loads)
   const int ns = ad.nsplit;
   float *s_ms = reinterpret_cast<float *>(s_v);  // [G][ns]
@@ -359,6 +372,14 @@ __global__ void __launch_bounds__(NFA_BLOCK)
         O += a * f;
       }
     }
+    if constexpr (PART) {
+      pt.acc[(pb + g) * D + d] = O;
+      if (d == 0) {
+        pt.m[pb + g] = M;
+        pt.z[pb + g] = Z;
+      }
+      continue;
+    }
     const float o = Z == 0.0f ? 0.0f : O / Z;
     const int64_t oi = ((int64_t)t * p.hq + kh * G + g) * D + d;
     if (p.q_dtype == NFA_DTYPE_BF16)
@@ -368,9 +389,14 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
 }
 
-// Regions combine: one thread per output element (t, head, dim); the states
-// of region a's splits, then region b's, merge in split order with the
-// online-softmax rescaling.
+// Regions combine: one thread per output element (t, head, dim).  The
+// states of up to kCombineRegs splits load in one round (they were written
+// by other kernels, possibly through another XCD's L2, so each dependent
+// load would cost a full memory latency); then the maximum over every split
+// of both regions, and each split's denominator and P.V scaled by
+// exp(m_s - M): the softmax over the union, as the sequential rescaling
+// region a then region b gives it.
+constexpr int kCombineRegs = 16;
 __global__ void __launch_bounds__(NFA_BLOCK)
     nfa_regions_combine_kernel(const NfaAttnCombineParams c) {
   const int64_t i = (int64_t)blockIdx.x * NFA_BLOCK + threadIdx.x;
@@ -379,23 +405,37 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int64_t th = i / c.head_dim_v;
   const int d = (int)(i % c.head_dim_v);
   const float kNegInf = __uint_as_float(0xFF800000u);
-  float m = kNegInf, z = 0.0f, acc = 0.0f;
-  for (int r = 0; r < 2; ++r) {
-    const int ns = r == 0 ? c.nsplit_a : c.nsplit_b;
-    const float *pa = r == 0 ? c.acc_a : c.acc_b;
-    const float *pm = r == 0 ? c.m_a : c.m_b;
-    const float *pz = r == 0 ? c.z_a : c.z_b;
-    for (int sp = 0; sp < ns; ++sp) {
-      const int64_t e = sp * heads + th;
-      const float part_m = pm[e];
-      const float new_m = fmaxf(m, part_m);
-      const float safe_m = new_m == kNegInf ? 0.0f : new_m;
-      const float alpha = expf(m - safe_m);
-      const float beta = expf(part_m - safe_m);
-      acc = acc * alpha + pa[e * c.head_dim_v + d] * beta;
-      z = z * alpha + pz[e] * beta;
-      m = new_m;
+  const int ns = c.nsplit_a + c.nsplit_b;
+  float M = kNegInf, z = 0.0f, acc = 0.0f;
+  for (int s0 = 0; s0 < ns; s0 += kCombineRegs) {
+    float rm[kCombineRegs], rz[kCombineRegs], ra[kCombineRegs];
+#pragma unroll
+    for (int k = 0; k < kCombineRegs; ++k) {
+      const int sp = s0 + k;
+      rm[k] = kNegInf;
+      rz[k] = ra[k] = 0.0f;
+      if (sp < ns) {
+        const bool in_a = sp < c.nsplit_a;
+        const int64_t e = (in_a ? sp : sp - c.nsplit_a) * heads + th;
+        rm[k] = (in_a ? c.m_a : c.m_b)[e];
+        rz[k] = (in_a ? c.z_a : c.z_b)[e];
+        ra[k] = (in_a ? c.acc_a : c.acc_b)[e * c.head_dim_v + d];
+      }
     }
+    float m_new = M;
+#pragma unroll
+    for (int k = 0; k < kCombineRegs; ++k) m_new = fmaxf(m_new, rm[k]);
+    if (m_new == kNegInf) continue;  // nothing valid so far
+    const float f_old = M == kNegInf ? 0.0f : __expf(M - m_new);
+    z *= f_old;
+    acc *= f_old;
+#pragma unroll
+    for (int k = 0; k < kCombineRegs; ++k) {
+      const float f = rm[k] == kNegInf ? 0.0f : __expf(rm[k] - m_new);
+      z += rz[k] * f;
+      acc += ra[k] * f;
+    }
+    M = m_new;
   }
   const float o = z == 0.0f ? 0.0f : acc / z;
   if (c.out_dtype == NFA_DTYPE_BF16)
@@ -524,15 +564,27 @@ extern "C" int32_t nfa_sparse_attn_partial(const NfaAttnParams *p,
     nfa_set_error("nfa_sparse_attn_partial: null state pointer");
     return NFA_EINVAL;
   }
-  NfaAttnParams q = *p;
-  if (q.tokens_per_split == 0) q.tokens_per_split = nfa::kSplitMax;
   const int cus = nfa::device_cus();
-  dim3 grid(pt->nsplit, p->total_q * p->hkv);
+  const int span = nfa::part_span(*p, *pt);
+  const nfa::AttnDims ad = nfa::attn_dims(*p, cus, pt->nsplit, span);
+  if (p->workspace == nullptr || p->workspace_bytes < ad.w_total) {
+    nfa_set_error("nfa_sparse_attn_partial: workspace %lld < %lld bytes",
+                  (long long)p->workspace_bytes, (long long)ad.w_total);
+    return NFA_EWORKSPACE;
+  }
+  dim3 grid(ad.nsplit, ad.rows);
   hipStream_t s = (hipStream_t)stream;
   const bool bf = p->kv_dtype == NFA_DTYPE_BF16;
+  const bool loop = (int64_t)ad.nsplit * ad.split < span;
 #define NFA_PART_LAUNCH(KV, TPR)                                                       \
-  hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, true, true>), grid, dim3(NFA_BLOCK), \
-                     0, s, q, cus, *pt)
+  do {                                                                               \
+    if (loop)                                                                        \
+      hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, true, true>), grid,          \
+                         dim3(NFA_BLOCK), 0, s, *p, cus, *pt);                         \
+    else                                                                             \
+      hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, false, true>), grid,         \
+                         dim3(NFA_BLOCK), 0, s, *p, cus, *pt);                         \
+  } while (0)
   if (tpr == 8) {
     if (bf) NFA_PART_LAUNCH(uint16_t, 8); else NFA_PART_LAUNCH(float, 8);
   } else if (tpr == 16) {
@@ -580,6 +632,14 @@ extern "C" int32_t nfa_attn_regions_combine(const NfaAttnCombineParams *c, void 
     return NFA_ELAUNCH;
   }
   return NFA_OK;
+}
+
+extern "C" int64_t nfa_attn_partial_workspace_bytes(const NfaAttnParams *p,
+                                                     const NfaAttnPartial *pt) {
+  if (p == nullptr || pt == nullptr || p->total_q <= 0 || p->hkv <= 0 ||
+      pt->nsplit < 1 || pt->block_tokens < 1 || p->max_vis <= 0)
+    return 0;
+  return nfa::attn_dims(*p, nfa::device_cus(), pt->nsplit, nfa::part_span(*p, *pt)).w_total;
 }
 
 extern "C" int32_t nfa_attn_partial_size(void) { return (int32_t)sizeof(NfaAttnPartial); }

@@ -331,6 +331,62 @@ __device__ __forceinline__ int64_t l2_side_index(const NfaSelectParams &p,
              : base + (int64_t)r * p.fine_dsub + d;
 }
 
+// 4-bit L2 side cache (--nfa_l2_quant, 32 L2 dims): per (request, kv head,
+// token) 16 bytes of codes -- dim d in nibble d % 2 of byte d / 2 -- at
+// slot * 16, and the token's bf16 scale and zero (scale in the low half) at
+// 16 * slots + 4 * slot, slot = (req * hkv + kv) * max_blocks * bs + tok.
+constexpr int kQ4Dims = 32;
+__device__ __forceinline__ int64_t q4_slot(const NfaSelectParams &p, int64_t req,
+                                           int kv, int tok) {
+  return (req * p.hkv + kv) * (int64_t)p.max_blocks * p.bs + tok;
+}
+__device__ __forceinline__ int64_t q4_slots(const NfaSelectParams &p) {
+  return (int64_t)p.max_req * p.hkv * p.max_blocks * p.bs;
+}
+
+// min_max_per_token_quant (tia_indexer.py:22-31) with torch's bf16 rounding
+// after every op: range = bf16(max - min) clamped to 1e-9, scale =
+// bf16(range / 15), zero = -min, code = clamp(round_half_even(bf16(bf16(x +
+// zero) / scale)), 0, 15).  Stores the codes and (scale, zero) of the token
+// whose K row is `row` (L2 dims at fdims); the row is read twice (range,
+// then codes) rather than held in registers.
+template <typename KV>
+__device__ __forceinline__ void q4_store(const NfaSelectParams &p, int64_t req, int kv,
+                                         int tok, const KV *row, const int *fdims) {
+  // eight dims per step: few registers live where the rebuild runs
+  float mx = Elem<KV>::load(row + fdims[0]);
+  float mn = mx;
+#pragma unroll 1
+  for (int d0 = 0; d0 < kQ4Dims; d0 += 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = Elem<KV>::load(row + fdims[d0 + e]);
+      mx = fmaxf(mx, x);
+      mn = fminf(mn, x);
+    }
+  }
+  float rng = bf16r(mx - mn);
+  if (rng < 1e-9f) rng = bf16r(1e-9f);
+  const float scale = bf16r(rng / 15.0f);
+  const float zero = -mn;
+  const int64_t slot = q4_slot(p, req, kv, tok);
+  unsigned char *base = (unsigned char *)p.l2_keys_l;
+#pragma unroll 1
+  for (int d0 = 0; d0 < kQ4Dims; d0 += 8) {
+    uint32_t w = 0u;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = Elem<KV>::load(row + fdims[d0 + e]);
+      const float t = bf16r(bf16r(x + zero) / scale);
+      const float c = fminf(fmaxf(rintf(t), 0.0f), 15.0f);
+      w |= (uint32_t)c << (4 * e);
+    }
+    *reinterpret_cast<uint32_t *>(base + slot * 16 + d0 / 2) = w;
+  }
+  *reinterpret_cast<uint32_t *>(base + q4_slots(p) * 16 + slot * 4) =
+      (uint32_t)bf16_bits(scale) | ((uint32_t)bf16_bits(zero) << 16);
+}
+
 // ---------------------------------------------------------------------------
 // page statistics of pages [pg_lo, pg_hi) for one (request, kv)
 // ---------------------------------------------------------------------------
@@ -1299,12 +1355,16 @@ __global__ void __launch_bounds__(SB)
       stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims,
                                   s_stage, new_row, s_last);
     }
-    if (p.l2_keys_l != nullptr && tid < p.fine_dsub) {
-      // the new token's L2 side row
+    if (p.l2_keys_l != nullptr && tid < (p.l2_quant ? 1 : p.fine_dsub)) {
+      // the new token's L2 side row (its 4-bit codes: one thread)
       const KV *src = new_row != nullptr
                           ? new_row
                           : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page);
-      ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)] = src[s_fdims[tid]];
+      if (p.l2_quant) {
+        q4_store<KV>(p, req, kv, L - 1, src, s_fdims);
+      } else {
+        ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)] = src[s_fdims[tid]];
+      }
     }
   }
   const RowGeo geo = row_geo(p, L, skip_far, skip_near);
@@ -1357,7 +1417,11 @@ __global__ void __launch_bounds__(SB)
                                      : safe_page(p, btr[imin(tok / p.page, mb - 1)]);
           return kpool + kv_offset(p, phys, kv, tok % p.page);
         };
-        if (nchv > 0) {
+        if (p.l2_quant) {
+          // one thread per token: gather, quantise, store
+          for (int tok = tlo + tid; tok < thi; tok += SB)
+            q4_store<KV>(p, req, kv, tok, src_row(tok), s_fdims);
+        } else if (nchv > 0) {
           for (int e = tid; e < (thi - tlo) * nchv; e += SB) {
             const int tok = tlo + e / nchv;
             const int c = e % nchv;
@@ -1779,6 +1843,71 @@ __global__ void __launch_bounds__(SB)
           safe_page(p, page_phys ? s_pphys[pi] : btr[imin(tk / p.page, mb - 1)]);
       return kpool + kv_offset(p, phys, kv, tk % p.page);
     };
+    // logit key of dense slot i (and the parity-test record)
+    auto emit = [&](int i, int tk, bool scored, float acc) {
+      uint16_t key = 0;
+      if (scored) {
+        const uint16_t bits = bf16_bits(acc);
+        key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
+        if (NFA_COLD(p.dbg_cand_tok != nullptr) && i < p.dbg_cand_cap) {
+          p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tk;
+          p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
+              bits == kNanBits ? kNegInfBits : bits;
+        }
+      } else if (NFA_COLD(p.dbg_cand_tok != nullptr) && i < p.dbg_cand_cap) {
+        p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = -1;
+      }
+      s_dk[i] = key;
+    };
+    if (p.l2_quant) {
+      // 4-bit side cache: 16 bytes of codes and 4 of (scale, zero) per
+      // slot, dequantised in registers as bf16(bf16(code * scale) - zero)
+      const unsigned char *qb = (const unsigned char *)p.l2_keys_l;
+      const int64_t poff = q4_slots(p) * 16;
+      auto q4_of = [&](int i, int &tk) -> int64_t {
+        const int pi = i / bs;
+        tk = s_pages[pi] * bs + (i - pi * bs);
+        if (tk < tok_lo || tk >= tok_hi) return -1;
+        return q4_slot(p, req, kv, tk);
+      };
+      int tk = -1;
+      int64_t sl = tid < n_dense ? q4_of(tid, tk) : -1;
+      uint4 cw = make_uint4(0u, 0u, 0u, 0u);
+      uint32_t pw = 0u;
+      if (sl >= 0) {
+        cw = *reinterpret_cast<const uint4 *>(qb + sl * 16);
+        pw = *reinterpret_cast<const uint32_t *>(qb + poff + sl * 4);
+      }
+#pragma unroll 1
+      for (int i = tid; i < n_dense; i += SB) {
+        int tkn = -1;
+        const int64_t sln = i + SB < n_dense ? q4_of(i + SB, tkn) : -1;
+        uint4 cwn = make_uint4(0u, 0u, 0u, 0u);
+        uint32_t pwn = 0u;
+        if (sln >= 0) {
+          cwn = *reinterpret_cast<const uint4 *>(qb + sln * 16);
+          pwn = *reinterpret_cast<const uint32_t *>(qb + poff + sln * 4);
+        }
+        float acc = 0.0f;
+        if (sl >= 0) {
+          const float sc = bf16_val((uint16_t)(pw & 0xFFFFu));
+          const float zr = bf16_val((uint16_t)(pw >> 16));
+          const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+          for (int d = 0; d < kQ4Dims; ++d) {
+            const float c = (float)((w4[d / 8] >> (4 * (d % 8))) & 15u);
+            const float dq = bf16r(bf16r(c * sc) - zr);
+            const float prod = dq * s_qg[d];
+            acc = acc + prod;
+          }
+        }
+        emit(i, tk, sl >= 0, acc);
+        tk = tkn;
+        sl = sln;
+        cw = cwn;
+        pw = pwn;
+      }
+    } else {
     const bool vec4 = nch > 0 && nch <= 4;  // the L2 row in at most 4 loads
     auto fetch = [&](const KV *kr, uint4 (&r)[4]) {
 #pragma unroll
@@ -1831,23 +1960,12 @@ __global__ void __launch_bounds__(SB)
           }
         }
       }
-      uint16_t key = 0;
-      if (kr != nullptr) {
-        const uint16_t bits = bf16_bits(acc);
-        key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
-        if (NFA_COLD(p.dbg_cand_tok != nullptr) && i < p.dbg_cand_cap) {
-          p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tk;
-          p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
-              bits == kNanBits ? kNegInfBits : bits;
-        }
-      } else if (NFA_COLD(p.dbg_cand_tok != nullptr) && i < p.dbg_cand_cap) {
-        p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = -1;
-      }
-      s_dk[i] = key;
+      emit(i, tk, kr != nullptr, acc);
       tk = tkn;
       kr = krn;
 #pragma unroll
       for (int c = 0; c < 4; ++c) r[c] = rn[c];
+    }
     }
   }
   __syncthreads();
@@ -2010,6 +2128,13 @@ static int select_check(const NfaSelectParams *p) {
   }
   if (p->fine_dsub <= 0 || p->fine_dsub > p->head_dim) {
     nfa_set_error("nfa_select_layer: bad L2 dim count %d", p->fine_dsub);
+    return NFA_EINVAL;
+  }
+  if (p->l2_quant && (p->l2_keys_l == nullptr || p->fine_dsub != nfa::kQ4Dims ||
+                      p->kv_dtype != NFA_DTYPE_BF16)) {
+    nfa_set_error("nfa_select_layer: 4-bit L2 keys need the L2 side cache, %d L2 "
+                  "dims and bf16 KV (got %d dims, kv dtype %d)",
+                  nfa::kQ4Dims, p->fine_dsub, p->kv_dtype);
     return NFA_EINVAL;
   }
   if (p->bs <= 0 || p->page <= 0 || p->max_blocks <= 0 || p->k2 <= 0 ||

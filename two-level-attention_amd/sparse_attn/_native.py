@@ -43,7 +43,7 @@ class NfaSelectParams(ctypes.Structure):
         ('dsub', _i32), ('fine_dsub', _i32),
         ('kv_dtype', _i32), ('q_dtype', _i32),
         ('max_vis', _i32), ('middle_only', _i32), ('pool_pages', _i32),
-        ('protected_only', _i32), ('scale', _f32), ('pad1', _f32),
+        ('protected_only', _i32), ('scale', _f32), ('l2_quant', _i32),
         ('k_pool_l', _ptr), ('v_pool_l', _ptr), ('block_table_l', _ptr),
         ('lengths', _ptr), ('active_req', _ptr), ('valid_req', _ptr),
         ('skip_far_l', _ptr), ('skip_near_l', _ptr),
@@ -147,6 +147,7 @@ EXPORTS = (
     'nfa_decode_linear', 'nfa_qk_norm_rope_decode', 'nfa_rmsnorm_decode',
     'nfa_gate_params_size', 'nfa_region_profile', 'nfa_attn_partial_size',
     'nfa_attn_combine_params_size', 'nfa_sparse_attn_partial', 'nfa_attn_regions_combine',
+    'nfa_attn_partial_workspace_bytes',
 )
 
 _lib = None
@@ -207,6 +208,9 @@ def load_library(path: str = None):
         lib.nfa_sparse_attn_partial.restype = _i32
         lib.nfa_sparse_attn_partial.argtypes = [
             ctypes.POINTER(NfaAttnParams), ctypes.POINTER(NfaAttnPartial), _ptr]
+        lib.nfa_attn_partial_workspace_bytes.restype = _i64
+        lib.nfa_attn_partial_workspace_bytes.argtypes = [
+            ctypes.POINTER(NfaAttnParams), ctypes.POINTER(NfaAttnPartial)]
         lib.nfa_attn_regions_combine.restype = _i32
         lib.nfa_attn_regions_combine.argtypes = [ctypes.POINTER(NfaAttnCombineParams), _ptr]
         if lib.nfa_abi_version() != ABI_VERSION:

@@ -70,13 +70,15 @@ def _no_capture_alloc(what):
 
 
 def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype, fine_key,
-                        head_dim, bs):
+                        head_dim, bs, quant=False):
     """Persistent per-layer page statistics [max_req, hkv, dsub, max_blocks]
     in the KV dtype, chunk-major, the fp32 running sums of each request's last
     page [max_req, hkv, dsub], and the L2 side copy [max_req, hkv,
     max_blocks * bs, fine_dsub] of every visible token's L2 dims (None for a
-    full-width L2 subspace, or when ``cache.nfa_l2_side_copy`` is False); a new
-    dims set for a layer forces rebuilds of both."""
+    full-width L2 subspace, or when ``cache.nfa_l2_side_copy`` is False) --
+    with ``quant``, 20 bytes per token slot instead (16 bytes of 4-bit codes,
+    then bf16 scale and zero); a new dims set for a layer forces rebuilds of
+    both."""
     layer0 = cache.layers[0]
     device = layer0.kv_pool_k.device
     lengths = getattr(cache, '_nfa_page_stats_lengths', None)
@@ -94,7 +96,7 @@ def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype, fine_key,
     want_side = (len(fine_key) < head_dim
                  and getattr(cache, 'nfa_l2_side_copy', True))
     key = (layer_idx, 1, int(dims.numel()), dtype, dims_key,
-           (fine_key, bs) if want_side else None)
+           (fine_key, bs, bool(quant)) if want_side else None)
     bufs = store.get(key)
     if bufs is None:
         _no_capture_alloc('page statistics')
@@ -107,10 +109,11 @@ def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype, fine_key,
                               * int(dims.numel()), dtype=torch.float32,
                               device=device),)
         side = None
-        if want_side:
-            side = torch.empty(cache.max_requests * layer0.num_kv_heads
-                               * cache.max_blocks * bs * len(fine_key),
-                               dtype=dtype, device=device)
+        slots = cache.max_requests * layer0.num_kv_heads * cache.max_blocks * bs
+        if want_side and quant:
+            side = torch.empty(slots * 20, dtype=torch.uint8, device=device)
+        elif want_side:
+            side = torch.empty(slots * len(fine_key), dtype=dtype, device=device)
         bufs = store[key] = (stats, side)
     if keys_by_layer.get(layer_idx) != key:
         _no_capture_alloc('page statistics')
@@ -224,8 +227,15 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
         raise ValueError('selection outputs must be contiguous int32')
 
     kv_dtype = layer0.kv_pool_k.dtype
+    quant = bool(getattr(indexer, 'l2_quant', False))
+    if quant and (fine_dims.numel() != 32 or kv_dtype != torch.bfloat16):
+        raise ValueError('--nfa_l2_quant needs 32 L2 dims and a bf16 KV cache '
+                         f'(got {fine_dims.numel()} dims, {kv_dtype})')
     (smin, smax, ssum, psum), l2_side, stats_len = _page_stats_buffers(
-        cache, layer_idx, l1_dims, l1_key, kv_dtype, fine_key, head_dim, bs)
+        cache, layer_idx, l1_dims, l1_key, kv_dtype, fine_key, head_dim, bs, quant)
+    if quant and l2_side is None:
+        raise ValueError('--nfa_l2_quant needs the L2 side cache (a sub-width L2 '
+                         'subspace and cache.nfa_l2_side_copy)')
     layer = cache.layers[layer_idx]
 
     p = nat.NfaSelectParams()
@@ -251,6 +261,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
     p.q_dtype = nat.dtype_code(query_states.dtype)
     p.max_vis = gather_out.shape[-1]
     p.middle_only = int(bool(middle_only))
+    p.l2_quant = int(quant)
     p.protected_only = int(region_mode == 3)
     p.scale = float(attention.scaling)
     p.pool_pages = layer.kv_pool_k.shape[0]

@@ -253,6 +253,11 @@ def sparse_paged_attention_gather_partial(cache_layer, q, gather_indices, visibl
     pt.nsplit = nsplit
     pt.block_tokens = _partial_block_tokens(cache_layer, total_q)
     pt.acc, pt.m, pt.z = part_acc.data_ptr(), part_m.data_ptr(), part_z.data_ptr()
+    need = lib.nfa_attn_partial_workspace_bytes(ctypes.byref(p), ctypes.byref(pt))
+    ws = _scratch(workspace, ('nfa_attn_partial_scratch', name, total_q, hk, p.max_vis,
+                              hq, dv, nsplit, pt.block_tokens), need, q.device)
+    p.workspace = ws.data_ptr()
+    p.workspace_bytes = ws.numel()
     nat.check(lib.nfa_sparse_attn_partial(ctypes.byref(p), ctypes.byref(pt),
                                           nat.stream_handle()),
               'sparse_paged_attention_gather_partial')

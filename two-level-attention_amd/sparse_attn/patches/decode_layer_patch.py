@@ -98,8 +98,8 @@ def nfa_decode_layer_forward(self, hidden_states, attention_mask=None,
             visible_lens=cache.visible_lens_for_layer(layer_idx),
             query_to_req=cache.query_to_req_buf)
     elif mode in ('serial', 'overlap'):
-        from .qwen3_attn_patch import _disjoint_regions_attention
-        o = _disjoint_regions_attention(attn, q, k.view(b, hkv, 1, d),
+        from .qwen3_attn_patch import disjoint_regions_attention
+        o = disjoint_regions_attention(attn, q, k.view(b, hkv, 1, d),
                                         v.view(b, hkv, 1, d), cache, slots,
                                         mode == 'overlap')
     else:

@@ -88,7 +88,7 @@ def nfa_decode_attention(module, query_states, key_states, value_states, cache,
             visible_lens=cache.visible_lens_for_layer(layer_idx),
             query_to_req=cache.query_to_req_buf)
     elif operator_mode in ('serial', 'overlap'):
-        result = _disjoint_regions_attention(
+        result = disjoint_regions_attention(
             module, q_flat, key_states, value_states, cache, slot_mapping,
             operator_mode == 'overlap')
     else:
@@ -96,7 +96,7 @@ def nfa_decode_attention(module, query_states, key_states, value_states, cache,
     return module.o_proj(result.reshape(*input_shape, -1).contiguous())
 
 
-def _disjoint_regions_attention(module, q_flat, key_states, value_states, cache,
+def disjoint_regions_attention(module, q_flat, key_states, value_states, cache,
                                 slot_mapping, overlap):
     """Protected ∥ middle attention of one layer (reference
     qwen3_attn_patch.py:123-195): the current K/V is written first, so both
