@@ -49,6 +49,8 @@ def parse():
                     help='request lengths drawn uniformly from [LO, HI] (seeded) '
                          'instead of --ctx for every request')
     ap.add_argument('--layers', type=int, default=36)
+    ap.add_argument('--l2-quant', action='store_true',
+                    help='L2 logits over the 4-bit packed tail keys (--nfa_l2_quant)')
     ap.add_argument('--operator-mode', choices=['off', 'serial', 'overlap'], default='off',
                     help='decode attention of the timed step: one union pass (off) or '
                          'protected and middle apart, then merged (serial / overlap)')
@@ -115,6 +117,7 @@ def build_workload(torch, args, device):
         dtype=torch.bfloat16, device=device)
     fargs = nfa_args('tail')
     fargs.tia_block_size = page
+    fargs.nfa_l2_quant = args.l2_quant
     indexer = NFAIndexer(fargs)
     gen = torch.Generator(device=device).manual_seed(args.seed)
     req_ids = list(range(b))
@@ -138,7 +141,8 @@ def build_workload(torch, args, device):
     torch.cuda.synchronize()
     return SimpleNamespace(cache=cache, indexer=indexer, attn=attn, q=q, kn=kn,
                            vn=vn, hkv=hkv, hq=hq, d=d, page=page, req_ids=req_ids,
-                           lengths=lengths, mode=args.operator_mode)
+                           lengths=lengths, mode=args.operator_mode,
+                           l2_quant=args.l2_quant)
 
 
 def run_layer(w, layer, outs):
@@ -165,7 +169,8 @@ def algorithmic_bytes(w, length, bs=16, window=128, near_len=4096, sink=4,
 
     Selector: L1 reads min+max (far pool, minmax score) or sum (near pool,
     avg score) of the 32 tail dims per page and KV head; L2 reads the 32 tail
-    dims (64 B) of every candidate token; plus the decode K/V write, the
+    dims (64 B) of every candidate token, or its 4-bit codes with bf16
+    scale and zero (20 B) with the 4-bit keys; plus the decode K/V write, the
     latest page's statistics update, the query and the gather row.
     Attention: K and V rows of every selected slot plus query, output and
     gather row.  Pool sizes follow the selector's region formulas.
@@ -184,7 +189,7 @@ def algorithmic_bytes(w, length, bs=16, window=128, near_len=4096, sink=4,
     # tokens and the part of the SWA boundary page before the window
     t_c = (k_far + k_near) * bs + (bs - sink % bs if sink % bs else 0) + byp % bs
     l1 = hkv * (2 * p_far * dsub * 2 + p_near * dsub * 2)
-    l2 = hkv * t_c * dsub * 2
+    l2 = hkv * t_c * (dsub // 2 + 4 if getattr(w, 'l2_quant', False) else dsub * 2)
     misc = (2 * hkv * d * 2 * 2        # decode K/V write (read + write)
             + 3 * hkv * dsub * 2       # latest page statistics
             + bs * hkv * dsub * 2      # latest page keys
@@ -641,7 +646,8 @@ def main():
                            if args.ragged else f'{args.ctx // 1024}K context')
                         + ', page 16, hipGraph',
             'layers': args.layers, 'batch': args.batch,
-            'operator_mode': args.operator_mode,
+            'operator_mode': args.operator_mode, 'l2_keys': '4-bit' if args.l2_quant
+                                                          else 'bf16',
             'context': (lengths if args.ragged else args.ctx),
             **geometry,
             'nfa': 'far minmax / near avg, K1 128 (32 near), near_len 4096, '

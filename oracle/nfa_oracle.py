@@ -228,7 +228,8 @@ def page_stats(cfg: NfaConfig, k_pool, bt_row, length, kv, n_pages=None):
         r = read[:, i, None]
         kmin = np.where(r & (v < kmin), v, kmin)
         kmax = np.where(r & (v > kmax), v, kmax)
-        ksum = np.where(r, (ksum + v).astype(F32), ksum)
+        with np.errstate(invalid='ignore'):  # inf + -inf keys sum to NaN, as on the GPU
+            ksum = np.where(r, (ksum + v).astype(F32), ksum)
     return (round_kv(kmin, cfg.kv_dtype), round_kv(kmax, cfg.kv_dtype),
             round_kv(ksum, cfg.kv_dtype))
 

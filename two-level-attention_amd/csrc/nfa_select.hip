@@ -387,6 +387,33 @@ __device__ __forceinline__ void q4_store(const NfaSelectParams &p, int64_t req, 
       (uint32_t)bf16_bits(scale) | ((uint32_t)bf16_bits(zero) << 16);
 }
 
+// q4_store by lanes 0-31 of one wave, lane d holding L2 dim d of the token:
+// the range by a shuffle tree, one code per lane, the eight nibbles of a
+// word OR-ed together across lanes.
+__device__ __forceinline__ void q4_store_lanes(const NfaSelectParams &p, int64_t req,
+                                               int kv, int tok, float x, int d) {
+  float mx = x, mn = x;
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, off, 32));
+    mn = fminf(mn, __shfl_xor(mn, off, 32));
+  }
+  float rng = bf16r(mx - mn);
+  if (rng < 1e-9f) rng = bf16r(1e-9f);
+  const float scale = bf16r(rng / 15.0f);
+  const float zero = -mn;
+  const float t = bf16r(bf16r(x + zero) / scale);
+  unsigned w = (unsigned)fminf(fmaxf(rintf(t), 0.0f), 15.0f) << (4 * (d % 8));
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1) w |= __shfl_xor(w, off, 32);
+  const int64_t slot = q4_slot(p, req, kv, tok);
+  unsigned char *base = (unsigned char *)p.l2_keys_l;
+  if (d % 8 == 0) *reinterpret_cast<uint32_t *>(base + slot * 16 + d / 2) = w;
+  if (d == 0)
+    *reinterpret_cast<uint32_t *>(base + q4_slots(p) * 16 + slot * 4) =
+        (uint32_t)bf16_bits(scale) | ((uint32_t)bf16_bits(zero) << 16);
+}
+
 // ---------------------------------------------------------------------------
 // page statistics of pages [pg_lo, pg_hi) for one (request, kv)
 // ---------------------------------------------------------------------------
@@ -1355,13 +1382,13 @@ __global__ void __launch_bounds__(SB)
       stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims,
                                   s_stage, new_row, s_last);
     }
-    if (p.l2_keys_l != nullptr && tid < (p.l2_quant ? 1 : p.fine_dsub)) {
-      // the new token's L2 side row (its 4-bit codes: one thread)
+    if (p.l2_keys_l != nullptr && tid < p.fine_dsub) {
+      // the new token's L2 side row (its 4-bit codes: lanes 0-31 of wave 0)
       const KV *src = new_row != nullptr
                           ? new_row
                           : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page);
       if (p.l2_quant) {
-        q4_store<KV>(p, req, kv, L - 1, src, s_fdims);
+        q4_store_lanes(p, req, kv, L - 1, Elem<KV>::load(src + s_fdims[tid]), tid);
       } else {
         ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)] = src[s_fdims[tid]];
       }
@@ -1896,7 +1923,8 @@ __global__ void __launch_bounds__(SB)
 #pragma unroll
           for (int d = 0; d < kQ4Dims; ++d) {
             const float c = (float)((w4[d / 8] >> (4 * (d % 8))) & 15u);
-            const float dq = bf16r(bf16r(c * sc) - zr);
+            // a NaN here (non-finite keys) still ends as a NaN logit
+            const float dq = bf16r_hw(bf16r_hw(c * sc) - zr);
             const float prod = dq * s_qg[d];
             acc = acc + prod;
           }
