@@ -1688,16 +1688,17 @@ __global__ void __launch_bounds__(SB)
     if (byp0_keep && in_cand(spl)) bp0 = spl;
     if (byp1_keep && in_cand(lb.lo / bs)) bp1 = lb.lo / bs;
   }
-  // Eight pages per thread, in page order over the threads: keys above the
+  // Sixteen pages per thread, in page order over the threads (one round of
+  // the block for up to 16384 pages): keys above the
   // threshold are selected, keys equal to it too unless only some of them
   // are (then the first `need` tied pages of the pool in page order, ranked
   // by a block scan); a second scan places the candidates, so the list is
   // sorted and free of duplicates by construction.
   int *s_pages = (int *)(smem + sd.a_pages);
-  // bit j set for pages pg0 + j in [lo, hi), j < 8
-  auto range8 = [](int pg0, int lo, int hi) -> uint32_t {
-    const int a = imin(imax(lo - pg0, 0), 8);
-    const int b = imin(imax(hi - pg0, 0), 8);
+  // bit j set for pages pg0 + j in [lo, hi), j < 16
+  auto range16 = [](int pg0, int lo, int hi) -> uint32_t {
+    const int a = imin(imax(lo - pg0, 0), 16);
+    const int b = imin(imax(hi - pg0, 0), 16);
     return ((1u << b) - 1u) & ~((1u << a) - 1u);
   };
   int np_u = 0;          // candidates so far (uniform)
@@ -1710,24 +1711,25 @@ __global__ void __launch_bounds__(SB)
       __syncthreads();
     }
     const int n = imin(sd.seg, kt_eff - seg_base);
-    const int n8 = (n + 7) / 8;
-    for (int v0 = 0; v0 < n8; v0 += SB) {  // uniform trip count
+    const int n16 = (n + 15) / 16;  // the segment holds a multiple of 16 keys
+    for (int v0 = 0; v0 < n16; v0 += SB) {  // uniform trip count
       const int v = v0 + tid;
-      const int pg0 = seg_base + v * 8;
+      const int pg0 = seg_base + v * 16;
       uint32_t cand = 0u, tief = 0u, tien = 0u;
-      if (v < n8) {
-        const uint4 w = reinterpret_cast<const uint4 *>(s_keys)[v];
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-        // masks over the eight pages: in range, near pool, candidate range
-        const uint32_t valid = range8(pg0, pg0, seg_base + n);
-        const uint32_t nearm = range8(pg0, near_start, 0x7FFFFFFF);
-        const uint32_t candm = range8(pg0, cp_lo, cp_hi);
-        auto byp8 = [&](int bp) -> uint32_t {
-          return bp >= pg0 && bp < pg0 + 8 ? 1u << (bp - pg0) : 0u;
+      if (v < n16) {
+        const uint4 wa = reinterpret_cast<const uint4 *>(s_keys)[2 * v];
+        const uint4 wb = reinterpret_cast<const uint4 *>(s_keys)[2 * v + 1];
+        const uint32_t ws[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+        // masks over the sixteen pages: in range, near pool, candidate range
+        const uint32_t valid = range16(pg0, pg0, seg_base + n);
+        const uint32_t nearm = range16(pg0, near_start, 0x7FFFFFFF);
+        const uint32_t candm = range16(pg0, cp_lo, cp_hi);
+        auto byp16 = [&](int bp) -> uint32_t {
+          return bp >= pg0 && bp < pg0 + 16 ? 1u << (bp - pg0) : 0u;
         };
         uint32_t gt = 0u, eq = 0u;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 16; ++j) {
           const uint32_t k = (ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
           const uint32_t T = ((nearm >> j) & 1u) ? (uint32_t)tn.T : (uint32_t)tf.T;
           gt |= (k > T ? 1u : 0u) << j;
@@ -1742,7 +1744,7 @@ __global__ void __launch_bounds__(SB)
         const uint32_t sel = gt | (eq & all_eq);
         tief = eq & ~all_eq & ~nearm;
         tien = eq & ~all_eq & nearm;
-        cand = (sel & candm) | byp8(bp0) | byp8(bp1);
+        cand = (sel & candm) | byp16(bp0) | byp16(bp1);
         if (NFA_COLD(dbg)) {
           for (uint32_t bits = sel; bits; bits &= bits - 1u) {
             const int j = __ffs(bits) - 1;
