@@ -1038,12 +1038,14 @@ struct RegionLists {
 // token lies in [rlo, rhi) (every candidate when !masked), ties to the lower
 // token, then hole fill with the smallest ids of [rlo, rhi) not chosen and
 // the sink filter; appended in ascending order to mid / mslot at *mid_count.
-// `hist` needs 512 ints, `tmp` 48.
+// `hist` needs 512 ints, `tmp` 48; with `hist_ready` its first 256 bins
+// already hold the high-byte histogram of the (unmasked) keys.
 __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked,
                                                 int rlo, int rhi, int quota,
                                                 int sink, const RegionLists &rl,
                                                 int *mid_count, int *hist,
-                                                int *tmp, int64_t *clk) {
+                                                int *tmp, int64_t *clk,
+                                                bool hist_ready = false) {
   if (quota <= 0) return;
   const int tid = threadIdx.x;
   // optional phase timestamps, taken right after barriers the code has anyway
@@ -1059,14 +1061,16 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     }
     return v;
   };
-  if (tid < 512) hist[tid] = 0;
-  __syncthreads();
-  mark(0);
-  for (int i = tid; i < n; i += SB) {
-    const uint32_t v = key(i);
-    if (v) atomicAdd(&hist[v >> 8], 1);
+  if (!hist_ready) {
+    if (tid < 512) hist[tid] = 0;
+    __syncthreads();
+    mark(0);
+    for (int i = tid; i < n; i += SB) {
+      const uint32_t v = key(i);
+      if (v) atomicAdd(&hist[v >> 8], 1);
+    }
+    __syncthreads();
   }
-  __syncthreads();
   mark(1);
   if (wave_id() == 0) wave_threshold_bin(hist, quota, tmp + 8);
   __syncthreads();
@@ -1089,6 +1093,12 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
   }
   mark(3);
   const int nch = total < quota ? total : quota;
+  const int nfill_req = quota - nch;
+  const int base_out = *mid_count;
+  // no hole to fill: the chosen tokens, in order, are the region's output
+  // (candidate tokens start at max(sink, lower), so the sink filter drops
+  // none of them)
+  const bool direct = nfill_req == 0;
   // ordered emission, one contiguous run of slots per thread
   const int per = (n + SB - 1) / SB;
   const int ia = tid * per;
@@ -1114,16 +1124,25 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
       }
       if (sel) {
         const int t = dv.tok(i);
-        rl.l0[pos] = t;
-        rl.l0x[pos] = dv.slot_of(i, t);
+        if (direct) {
+          rl.mid[base_out + pos] = t;
+          rl.mslot[base_out + pos] = dv.slot_of(i, t);
+        } else {
+          rl.l0[pos] = t;
+          rl.l0x[pos] = dv.slot_of(i, t);
+        }
         ++pos;
       }
     }
   }
   __syncthreads();
   mark(5);
+  if (direct) {
+    if (tid == 0) *mid_count = base_out + nch;
+    __syncthreads();
+    return;
+  }
   // hole fill: the (quota - nch) smallest ids of [rlo, rhi) not chosen
-  const int nfill_req = quota - nch;
   for (int i = tid; i < nfill_req; i += SB) {
     int lo = 0, hi = nch;
     while (lo < hi) {
@@ -1154,7 +1173,6 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
   }
   const int drop = lower_bound_i32(rl.l0, nch, sink) +
                    lower_bound_i32(rl.l1, nfill, sink);
-  const int base_out = *mid_count;
   for (int j = tid; j < nch; j += SB) {
     const int v = rl.l0[j];
     if (v >= sink) {
@@ -1845,6 +1863,10 @@ __global__ void __launch_bounds__(SB)
     }
   }
   if (tid == 0) s_misc[2] = 0;  // middle count
+  // one unmasked L2 region: its high-byte key histogram accumulates while
+  // the logits are computed (the L1 histograms are dead here)
+  const bool hist_fused = lb.quota > 0 && p.near_tokens < 0;
+  if (hist_fused && tid < 512) s_hist[tid] = 0;
   __syncthreads();  // the L1 part of the tail LDS is dead from here
   NFA_MARK(32, 6);
 
@@ -1887,6 +1909,7 @@ __global__ void __launch_bounds__(SB)
         p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = -1;
       }
       s_dk[i] = key;
+      if (hist_fused && key != 0) atomicAdd(&s_hist[key >> 8], 1);
     };
     if (p.l2_quant) {
       // 4-bit side cache: 16 bytes of codes and 4 of (scale, zero) per
@@ -2039,7 +2062,7 @@ __global__ void __launch_bounds__(SB)
     int64_t *rclk = p.dbg_clock != nullptr ? s_clk + 32 + 16 : nullptr;
     for (int r = 0; r < nreg; ++r)
       l2_region_dense(dv, masked, r_lo[r], r_hi[r], r_q[r], p.sink_tokens, rl,
-                      &s_misc[2], s_hist, s_tmp, rclk);
+                      &s_misc[2], s_hist, s_tmp, rclk, hist_fused);
   }
   __syncthreads();
   NFA_MARK(32, 12);
