@@ -1656,14 +1656,16 @@ __global__ void __launch_bounds__(SB)
         __syncthreads();
       }
       const int n = imin(sd.seg, kt_eff - seg_base);
-      // eight keys per thread from one 16-byte read
-      for (int v = tid; v < (n + 7) / 8; v += SB) {
-        const uint4 w = reinterpret_cast<const uint4 *>(s_keys)[v];
-        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+      // sixteen keys per thread from two 16-byte reads (the segment holds a
+      // multiple of 16 keys): one round of the block up to 16384 pages
+      for (int v = tid; v < (n + 15) / 16; v += SB) {
+        const uint4 wa = reinterpret_cast<const uint4 *>(s_keys)[2 * v];
+        const uint4 wb = reinterpret_cast<const uint4 *>(s_keys)[2 * v + 1];
+        const uint32_t ws[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 16; ++j) {
           const uint32_t k = (ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-          const int i = v * 8 + j;
+          const int i = v * 16 + j;
           const bool near = seg_base + i >= near_start;
           const int hb = near ? hbn : hbf;
           if (i < n && k != 0u && (int)(k >> 8) == hb)
