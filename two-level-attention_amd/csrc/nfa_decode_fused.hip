@@ -25,7 +25,6 @@ namespace nfa {
 
 constexpr int LIN_WAVES = 4;
 constexpr int LIN_CPI = 8;                     // chunks per lane per iteration
-constexpr int LIN_ITER_CHUNKS = 64 * LIN_CPI;  // chunks of a row per iteration
 constexpr int LIN_MMAX = 4;
 constexpr int LIN_LDS_BYTES = 48 * 1024;
 
@@ -144,20 +143,20 @@ __device__ __forceinline__ uint4 keep4(bool keep, const uint4 &v) {
 // each row, zeros past the row end or for a missing second row.  The loads
 // themselves are unconditional (clamped to the row's last chunk) so that all
 // of them are in flight before the first is waited for.  w0 is not null.
+template <int CPI>
 __device__ __forceinline__ void load_iter(const uint4 *w0, const uint4 *w1, int base,
-                                          int nch, uint4 (&a)[LIN_CPI],
-                                          uint4 (&b)[LIN_CPI]) {
+                                          int nch, uint4 (&a)[CPI], uint4 (&b)[CPI]) {
   const int lane = threadIdx.x & 63;
   const uint4 *p1 = w1 ? w1 : w0;
 #pragma unroll
-  for (int j = 0; j < LIN_CPI; ++j) {
+  for (int j = 0; j < CPI; ++j) {
     const int c = base + j * 64 + lane;
     const int cc = c < nch ? c : nch - 1;
     a[j] = w0[cc];
     b[j] = p1[cc];
   }
 #pragma unroll
-  for (int j = 0; j < LIN_CPI; ++j) {
+  for (int j = 0; j < CPI; ++j) {
     const bool in = base + j * 64 + lane < nch;
     a[j] = keep4(in, a[j]);
     b[j] = keep4(in && w1, b[j]);
@@ -165,14 +164,13 @@ __device__ __forceinline__ void load_iter(const uint4 *w0, const uint4 *w1, int 
 }
 
 // Multiply-add one iteration's chunks with every x row: acc[r][m] per lane.
-template <int MM>
-__device__ __forceinline__ void dot_iter(const uint4 (&a)[LIN_CPI],
-                                         const uint4 (&b)[LIN_CPI], int base, int nch,
-                                         const uint4 *s_x,
+template <int MM, int CPI>
+__device__ __forceinline__ void dot_iter(const uint4 (&a)[CPI], const uint4 (&b)[CPI],
+                                         int base, int nch, const uint4 *s_x,
                                          float (&acc)[2][LIN_MMAX]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int j = 0; j < LIN_CPI; ++j) {
+  for (int j = 0; j < CPI; ++j) {
     const int c = base + j * 64 + lane;
     if (c >= nch) break;
 #pragma unroll
@@ -188,9 +186,13 @@ __device__ __forceinline__ uint16_t ld_bf(const void *base, int64_t i) {
   return ((const uint16_t *)base)[i];
 }
 
-template <int EPI, bool NORM, int MM>
+// PRO: 0 no norm, 1 norm then the first weight loads, 2 the first weight
+// loads in flight through the norm (for grids that fit on the device at
+// once: holding those registers through the prologue costs occupancy).
+template <int EPI, int PRO, int MM>
 __global__ void __launch_bounds__(NFA_BLOCK)
     linear_kernel(const NfaLinearParams p) {
+  constexpr bool NORM = PRO != 0;
   extern __shared__ uint4 s_x[];
   __shared__ float s_red[NFA_WAVES];
   const int nch = p.k / 8;
@@ -210,24 +212,34 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     w0 = seg_row(p, unit * 2, &seg[0], &loc[0]);
     w1 = seg_row(p, unit * 2 + 1, &seg[1], &loc[1]);
   }
-  // Without a norm prologue the first weight chunks are in flight while the
-  // activations are staged; with one, the registers they would hold through
-  // the norm cost more occupancy than the overlap gains.
-  uint4 a[LIN_CPI], b[LIN_CPI];
-  if (!NORM && w0) load_iter(w0, w1, 0, nch, a, b);
+  // Two buffers of half an iteration each: the next half's loads are in
+  // flight while the current half is multiplied.  The first weight chunks
+  // are in flight while the activations are staged, unless a norm prologue
+  // would hold them at the cost of occupancy (PRO 1).
+  constexpr int HC = LIN_CPI / 2;
+  constexpr int STEP = 64 * HC;
+  uint4 a0[HC], b0[HC], a1[HC], b1[HC];
+  if (PRO != 1 && w0) {
+    load_iter<HC>(w0, w1, 0, nch, a0, b0);
+    load_iter<HC>(w0, w1, STEP, nch, a1, b1);
+  }
   stage_x<NORM>(p, nch, s_x, s_red);
   if (!w0) return;
-  if (NORM) load_iter(w0, w1, 0, nch, a, b);
+  if (PRO == 1) {
+    load_iter<HC>(w0, w1, 0, nch, a0, b0);
+    load_iter<HC>(w0, w1, STEP, nch, a1, b1);
+  }
 
   float acc[2][LIN_MMAX];
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
     for (int m = 0; m < LIN_MMAX; ++m) acc[r][m] = 0.0f;
-  dot_iter<MM>(a, b, 0, nch, s_x, acc);
-  for (int base = LIN_ITER_CHUNKS; base < nch; base += LIN_ITER_CHUNKS) {
-    load_iter(w0, w1, base, nch, a, b);
-    dot_iter<MM>(a, b, base, nch, s_x, acc);
+  for (int base = 0; base < nch; base += 2 * STEP) {
+    dot_iter<MM, HC>(a0, b0, base, nch, s_x, acc);
+    if (base + 2 * STEP < nch) load_iter<HC>(w0, w1, base + 2 * STEP, nch, a0, b0);
+    if (base + STEP < nch) dot_iter<MM, HC>(a1, b1, base + STEP, nch, s_x, acc);
+    if (base + 3 * STEP < nch) load_iter<HC>(w0, w1, base + 3 * STEP, nch, a1, b1);
   }
 
   if (EPI == NFA_EPI_SILU_GATE) {
@@ -399,6 +411,9 @@ extern "C" int32_t nfa_decode_linear(const NfaLinearParams *p, void *stream) {
   const size_t lds = (size_t)p->m * p->k * 2;
   hipStream_t s = (hipStream_t)stream;
   const bool norm = p->norm_weight != nullptr;
+  // a grid of at most four workgroups (16 waves) per CU runs in one round:
+  // its first weight loads can be in flight through the norm prologue
+  const bool early = blocks <= (int64_t)4 * nfa::device_cus();
 #define NFA_LIN(E, N, M)                                                          \
   hipLaunchKernelGGL((nfa::linear_kernel<E, N, M>), dim3((unsigned)blocks),    \
                      dim3(NFA_BLOCK), lds, s, *p)
@@ -409,13 +424,16 @@ extern "C" int32_t nfa_decode_linear(const NfaLinearParams *p, void *stream) {
     case 3: NFA_LIN(E, N, 3); break;                               \
     default: NFA_LIN(E, N, 4); break;                              \
   }
+#define NFA_LIN_P(E)                                                              \
+  if (!norm) { NFA_LIN_M(E, 0) } else if (early) { NFA_LIN_M(E, 2) } else { NFA_LIN_M(E, 1) }
   if (p->epilogue == NFA_EPI_SILU_GATE) {
-    if (norm) { NFA_LIN_M(NFA_EPI_SILU_GATE, true) } else { NFA_LIN_M(NFA_EPI_SILU_GATE, false) }
+    NFA_LIN_P(NFA_EPI_SILU_GATE)
   } else if (p->epilogue == NFA_EPI_RESIDUAL) {
-    if (norm) { NFA_LIN_M(NFA_EPI_RESIDUAL, true) } else { NFA_LIN_M(NFA_EPI_RESIDUAL, false) }
+    NFA_LIN_P(NFA_EPI_RESIDUAL)
   } else {
-    if (norm) { NFA_LIN_M(NFA_EPI_PLAIN, true) } else { NFA_LIN_M(NFA_EPI_PLAIN, false) }
+    NFA_LIN_P(NFA_EPI_PLAIN)
   }
+#undef NFA_LIN_P
 #undef NFA_LIN_M
 #undef NFA_LIN
   const hipError_t err = hipGetLastError();
