@@ -357,35 +357,55 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     s_zs[g * ns + sp] = ps[1];
   }
   __syncthreads();
-  for (int i = tid; i < G * D; i += NFA_BLOCK) {
-    const int g = i / D, d = i % D;
+  // two adjacent outputs per thread; the P.V partials of kMergeBatch splits
+  // are requested before the first is used (they come from other
+  // workgroups, through memory)
+  constexpr int kMergeBatch = 16;
+  for (int i = tid; i < G * (D / 2); i += NFA_BLOCK) {
+    const int g = i / (D / 2), d = 2 * (i % (D / 2));
     float M = kNegInf;
     for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, s_ms[g * ns + sp]);
-    float Z = 0.0f, O = 0.0f;
+    float Z = 0.0f, O0 = 0.0f, O1 = 0.0f;
     if (M != kNegInf) {
-#pragma unroll 8
-      for (int sp = 0; sp < ns; ++sp) {
-        const float ms = s_ms[g * ns + sp];
-        const float a = base[(int64_t)sp * ad.part_stride + g * (D + 2) + 2 + d];
-        const float f = ms == kNegInf ? 0.0f : __expf(ms - M);
-        Z += s_zs[g * ns + sp] * f;
-        O += a * f;
+      const float *pa = base + g * (D + 2) + 2 + d;  // 8-byte aligned: D + 2 and d even
+      for (int s0 = 0; s0 < ns; s0 += kMergeBatch) {
+        float2 av[kMergeBatch];
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) {
+          const int sp = s0 + k < ns ? s0 + k : ns - 1;  // clamped, unconditional
+          av[k] = *reinterpret_cast<const float2 *>(pa + (int64_t)sp * ad.part_stride);
+        }
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) {
+          // splits past ns (clamped loads) weigh zero
+          const int sp = s0 + k < ns ? s0 + k : ns - 1;
+          const float ms = s_ms[g * ns + sp];
+          const float f = (s0 + k < ns && ms != kNegInf) ? __expf(ms - M) : 0.0f;
+          Z += s_zs[g * ns + sp] * f;
+          O0 += av[k].x * f;
+          O1 += av[k].y * f;
+        }
       }
     }
     if constexpr (PART) {
-      pt.acc[(pb + g) * D + d] = O;
+      pt.acc[(pb + g) * D + d] = O0;
+      pt.acc[(pb + g) * D + d + 1] = O1;
       if (d == 0) {
         pt.m[pb + g] = M;
         pt.z[pb + g] = Z;
       }
       continue;
     }
-    const float o = Z == 0.0f ? 0.0f : O / Z;
+    const float o0 = Z == 0.0f ? 0.0f : O0 / Z;
+    const float o1 = Z == 0.0f ? 0.0f : O1 / Z;
     const int64_t oi = ((int64_t)t * p.hq + kh * G + g) * D + d;
-    if (p.q_dtype == NFA_DTYPE_BF16)
-      ((uint16_t *)p.out)[oi] = bf16_bits(o);
-    else
-      ((float *)p.out)[oi] = o;
+    if (p.q_dtype == NFA_DTYPE_BF16) {
+      ((uint16_t *)p.out)[oi] = bf16_bits(o0);
+      ((uint16_t *)p.out)[oi + 1] = bf16_bits(o1);
+    } else {
+      ((float *)p.out)[oi] = o0;
+      ((float *)p.out)[oi + 1] = o1;
+    }
   }
 }
 
