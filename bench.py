@@ -41,7 +41,7 @@ def parse():
     ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=200)
-    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--warmup', type=int, default=30)
     ap.add_argument('--ctx', type=int, default=131072)
     ap.add_argument('--batch', type=int, default=1,
                     help='decode rows (requests) sharing one cache per layer')
