@@ -46,7 +46,7 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p, int cus,
   AttnDims a;
   a.rows = p.total_q * p.hkv * mult;
   int split = p.tokens_per_split;
-  if (split <= 0) split = 32;
+  if (split <= 0) split = kSplitMax;  // fewer, longer splits: a cheaper merge
   a.split = split;
   const int G = p.hq / p.hkv;
   // at most kMaxSplits workgroups per row, and no more than the merge can
