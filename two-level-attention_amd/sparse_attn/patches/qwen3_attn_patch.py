@@ -10,8 +10,9 @@ attends to them with the sparse gather attention.  For bf16 decode the q/k
 RMSNorm and RoPE run as one launch (the reference's qwen3_decode_rope,
 ops/qwen3_rope_triton.py:118, plus the two norms).  Every device step is a
 HIP kernel with fixed buffers, so the decode forward can be captured into a
-hipGraph.  Operator modes other than ``'off'`` (protected-set attention beside
-the middle selection) are not built and raise ``ValueError``.
+hipGraph.  ``--nfa_operator_mode serial|overlap`` attends the protected
+sink/SWA set and the selected middle apart and merges the two softmax
+states (reference :123-195); an unknown mode raises ``ValueError``.
 """
 from typing import Optional
 
