@@ -1305,8 +1305,13 @@ __global__ void __launch_bounds__(SB)
   // neither scores nor arrival
   const TileSplit split = tile_split(kt_eff, sd.tcap);
   if (tile >= split.tiles) return;
-  const int t0 = tile * split.span;
-  const int t1 = imin(t0 + split.span, kt_eff);
+  // the pages spread evenly, the first kt % tiles tiles one page more (at
+  // 128K: one tile of 257 pages and 31 of 256, four 64-page groups per
+  // scoring round, where 257 everywhere took a second round for one page)
+  const int t_base = kt_eff / split.tiles;
+  const int t_rem = kt_eff % split.tiles;
+  const int t0 = tile * t_base + imin(tile, t_rem);
+  const int t1 = t0 + t_base + (tile < t_rem ? 1 : 0);
   const int last_blk = L > 0 ? (L - 1) / bs : -1;
   const bool owns_last = last_blk >= t0 && last_blk < t1;
   // LDS: dims, fine dims, raw query rows, histogram
