@@ -75,3 +75,34 @@ def test_workspace_size_is_host_computed(lib):
     a.struct_size = ctypes.sizeof(a)
     a.total_q, a.hq, a.hkv, a.head_dim_v, a.max_vis = 1, 32, 8, 128, 1024
     assert lib.nfa_attn_workspace_bytes(ctypes.byref(a)) > 0
+
+
+def test_partial_combine_and_quant_checks_reject_before_launch(lib):
+    from sparse_attn import _native
+    assert lib.nfa_attn_partial_size() == ctypes.sizeof(_native.NfaAttnPartial)
+    assert lib.nfa_attn_combine_params_size() == ctypes.sizeof(_native.NfaAttnCombineParams)
+    a = _native.NfaAttnParams()
+    a.abi_version, a.struct_size = _native.ABI_VERSION, ctypes.sizeof(a)
+    pt = _native.NfaAttnPartial()
+    pt.abi_version, pt.struct_size = 99, ctypes.sizeof(pt)
+    assert lib.nfa_sparse_attn_partial(ctypes.byref(a), ctypes.byref(pt), None) == -1
+    assert b'ABI mismatch' in lib.nfa_last_error()
+    pt.abi_version = _native.ABI_VERSION
+    a.total_q, a.hq, a.hkv, a.head_dim, a.head_dim_v = 1, 32, 8, 128, 128
+    a.page, a.gather_rows, a.max_vis, a.pool_pages = 16, 1, 1024, 10
+    for name in ('q', 'k_pool', 'v_pool', 'gather', 'vis_lens', 'query_to_req'):
+        setattr(a, name, 16)  # never dereferenced: rejected first
+    pt.nsplit, pt.block_tokens = 0, 128
+    assert lib.nfa_sparse_attn_partial(ctypes.byref(a), ctypes.byref(pt), None) == -1
+    assert b'nsplit' in lib.nfa_last_error()
+    c = _native.NfaAttnCombineParams()
+    c.abi_version, c.struct_size = _native.ABI_VERSION, ctypes.sizeof(c)
+    c.total_q, c.hq, c.head_dim_v, c.out_dtype = 1, 4, 8, 7
+    assert lib.nfa_attn_regions_combine(ctypes.byref(c), None) == -1
+    assert b'shape or dtype' in lib.nfa_last_error()
+    p = _native.NfaSelectParams()
+    p.abi_version, p.struct_size = _native.ABI_VERSION, ctypes.sizeof(p)
+    p.batch, p.hq, p.hkv, p.head_dim, p.dsub, p.fine_dsub = 1, 32, 8, 128, 32, 64
+    p.l2_quant = 1
+    assert lib.nfa_select_layer(ctypes.byref(p), None) == -1
+    assert b'4-bit L2 keys' in lib.nfa_last_error()
