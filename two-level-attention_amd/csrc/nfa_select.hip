@@ -1825,10 +1825,18 @@ __global__ void __launch_bounds__(SB)
     const int x = tid < (u1 - u0) ? u0 + tid : u2 + (tid - (u1 - u0));
     pre_slot = btr[imin(x / p.page, mb - 1)] * p.page + x % p.page;
   }
-  // physical pages of the candidates
+  // physical pages of the candidates: with the L2 side copy nothing reads
+  // them before the L2 top-quota, so their loads stay in flight through the
+  // logits (held in a register, stored to LDS after them)
   int *s_pphys = (int *)(smem + sd.a_pphys);
-  for (int i = tid; i < np_u; i += SB)
-    s_pphys[i] = btr[imin((s_pages[i] * bs) / p.page, mb - 1)];
+  const bool pphys_late = p.l2_keys_l != nullptr && np_u <= SB;
+  int pphys_reg = 0;
+  if (pphys_late) {
+    if (tid < np_u) pphys_reg = btr[imin((s_pages[tid] * bs) / p.page, mb - 1)];
+  } else {
+    for (int i = tid; i < np_u; i += SB)
+      s_pphys[i] = btr[imin((s_pages[i] * bs) / p.page, mb - 1)];
+  }
   if (tid == 0 && p.dbg_cand_count != nullptr)
     p.dbg_cand_count[row] = imin(np_u * bs, p.dbg_cand_cap);
   NFA_MARK(32, 4);
@@ -2028,6 +2036,7 @@ __global__ void __launch_bounds__(SB)
     }
     }
   }
+  if (pphys_late && tid < np_u) s_pphys[tid] = pphys_reg;
   __syncthreads();
   NFA_MARK(32, 9);
 
