@@ -1878,6 +1878,28 @@ __global__ void __launch_bounds__(SB)
     }
   }
   if (tid == 0) s_misc[2] = 0;  // middle count
+  // bf16/fp32 side copy in 16-byte runs: this thread's first L2 slot's row is
+  // requested now, ahead of the barrier below (the logits loop starts from it)
+  const int nchs = p.fine_dsub % CH == 0 ? p.fine_dsub / CH : 0;
+  const bool l2_pre = p.l2_keys_l != nullptr && !p.l2_quant && nchs > 0 && nchs <= 4;
+  int tk_pre = -1;
+  const KV *kr_pre = nullptr;
+  uint4 r_pre[4];
+  if (l2_pre) {
+    if (tid < np_u * bs) {
+      const int pi = tid / bs;
+      const int tk = s_pages[pi] * bs + (tid - pi * bs);
+      if (tk >= tok_lo && tk < tok_hi) {
+        tk_pre = tk;
+        kr_pre = (const KV *)p.l2_keys_l + l2_side_index<KV>(p, req, kv, tk, 0);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      r_pre[c] = kr_pre != nullptr && c < nchs
+                     ? *reinterpret_cast<const uint4 *>(kr_pre + c * bs * CH)
+                     : make_uint4(0u, 0u, 0u, 0u);
+  }
   // one unmasked L2 region: its high-byte key histogram accumulates while
   // the logits are computed (the L1 histograms are dead here)
   const bool hist_fused = lb.quota > 0 && p.near_tokens < 0;
@@ -1989,8 +2011,15 @@ __global__ void __launch_bounds__(SB)
     int tk = -1;
     const KV *kr = nullptr;
     uint4 r[4];
-    if (tid < n_dense) kr = slot_row(tid, tk);
-    if (vec4) fetch(kr, r);
+    if (l2_pre) {
+      tk = tk_pre;
+      kr = kr_pre;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) r[c] = r_pre[c];
+    } else {
+      if (tid < n_dense) kr = slot_row(tid, tk);
+      if (vec4) fetch(kr, r);
+    }
 #pragma unroll 1
     for (int i = tid; i < n_dense; i += SB) {
       int tkn = -1;
