@@ -1900,6 +1900,25 @@ __global__ void __launch_bounds__(SB)
                      ? *reinterpret_cast<const uint4 *>(kr_pre + c * bs * CH)
                      : make_uint4(0u, 0u, 0u, 0u);
   }
+  // the same for the 4-bit side cache: the first slot's codes and (scale, zero)
+  int64_t sl_pre = -1;
+  uint4 cw_pre = make_uint4(0u, 0u, 0u, 0u);
+  uint32_t pw_pre = 0u;
+  if (p.l2_quant) {
+    if (tid < np_u * bs) {
+      const int pi = tid / bs;
+      const int tk = s_pages[pi] * bs + (tid - pi * bs);
+      if (tk >= tok_lo && tk < tok_hi) {
+        tk_pre = tk;
+        sl_pre = q4_slot(p, req, kv, tk);
+      }
+    }
+    if (sl_pre >= 0) {
+      const unsigned char *qb = (const unsigned char *)p.l2_keys_l;
+      cw_pre = *reinterpret_cast<const uint4 *>(qb + sl_pre * 16);
+      pw_pre = *reinterpret_cast<const uint32_t *>(qb + q4_slots(p) * 16 + sl_pre * 4);
+    }
+  }
   // one unmasked L2 region: its high-byte key histogram accumulates while
   // the logits are computed (the L1 histograms are dead here)
   const bool hist_fused = lb.quota > 0 && p.near_tokens < 0;
@@ -1959,14 +1978,11 @@ __global__ void __launch_bounds__(SB)
         if (tk < tok_lo || tk >= tok_hi) return -1;
         return q4_slot(p, req, kv, tk);
       };
-      int tk = -1;
-      int64_t sl = tid < n_dense ? q4_of(tid, tk) : -1;
-      uint4 cw = make_uint4(0u, 0u, 0u, 0u);
-      uint32_t pw = 0u;
-      if (sl >= 0) {
-        cw = *reinterpret_cast<const uint4 *>(qb + sl * 16);
-        pw = *reinterpret_cast<const uint32_t *>(qb + poff + sl * 4);
-      }
+      // the first slot's loads were issued before the L1 LDS was released
+      int tk = tk_pre;
+      int64_t sl = sl_pre;
+      uint4 cw = cw_pre;
+      uint32_t pw = pw_pre;
 #pragma unroll 1
       for (int i = tid; i < n_dense; i += SB) {
         int tkn = -1;
