@@ -77,18 +77,23 @@ def parse():
     return ap.parse_args()
 
 
-def synthetic_keys(torch, n, hkv, d, gen, device, theta=1e6):
-    """N(0,1) x per-channel LogNormal(0,1) scale, RoPE (half-split) applied."""
-    scale = torch.exp(torch.randn(hkv, 1, d, generator=gen, device=device))
+def synthetic_keys(torch, n, hkv, d, gen, device, theta=1e6, start=0,
+                   dtype=None, scale=None):
+    """N(0,1) x per-channel LogNormal(0,1) scale, RoPE (half-split) applied
+    at positions start .. start+n-1.  Returns [1, hkv, n, d] in ``dtype``
+    (bf16 by default).  ``scale`` ([hkv, 1, d]) reuses a request's channel
+    scales, e.g. for its decode tokens."""
+    if scale is None:
+        scale = torch.exp(torch.randn(hkv, 1, d, generator=gen, device=device))
     k = torch.randn(hkv, n, d, generator=gen, device=device) * scale
     half = d // 2
     inv = theta ** (-torch.arange(0, half, device=device, dtype=torch.float32) / half)
-    pos = torch.arange(n, device=device, dtype=torch.float32)
+    pos = torch.arange(start, start + n, device=device, dtype=torch.float32)
     ang = pos[:, None] * inv[None, :]
     cos, sin = torch.cos(ang), torch.sin(ang)
     x1, x2 = k[..., :half], k[..., half:]
     out = torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1)
-    return out.to(torch.bfloat16).unsqueeze(0)
+    return out.to(dtype or torch.bfloat16).unsqueeze(0)
 
 
 def build_workload(torch, args, device):

@@ -10,8 +10,9 @@ import numpy as np
 import pytest
 import torch
 
-from nfa_case import (attention_ns, bf16_randn, cfg_from, make_cache,
-                      make_indexer, run_oracle, snapshot)
+from nfa_case import (GEO16, attention_ns, bf16_randn, cfg_from,
+                      decode_inputs, make_indexer, prefill_request, prod_cache,
+                      run_and_compare, run_oracle, snapshot, u16)
 from sparse_attn.indexer.nfa_layer_batch_selector import \
     select_topk_for_layer_batched
 from sparse_attn.policies.region_geometry import RegionGeometry
@@ -21,136 +22,10 @@ pytestmark = pytest.mark.gpu
 DEV = 'cuda'
 
 
-def _prefill(cache, req, length, gen, n_layers=1, dtype=torch.bfloat16,
-             zero_keys=False):
-    hkv = cache.num_kv_heads
-    d = cache.layers[0].head_dim_k
-    cache.add_request(req)
-    for layer in range(n_layers):
-        if zero_keys:
-            keys = torch.zeros(1, hkv, length, d, dtype=dtype, device=DEV)
-        else:
-            keys = bf16_randn((1, hkv, length, d), gen, DEV).to(dtype)
-        values = bf16_randn((1, hkv, length, d), gen, DEV).to(dtype)
-        cache.write_prefill(layer, req, keys, values)
-
-
-def _decode_inputs(cache, b, gen, dtype):
-    hkv = cache.num_kv_heads
-    d = cache.layers[0].head_dim_k
-    keys = bf16_randn((b, hkv, 1, d), gen, DEV).to(dtype)
-    values = bf16_randn((b, hkv, 1, d), gen, DEV).to(dtype)
-    slots = cache.slot_mapping_for_layer(0)[:b].clone()
-    return keys, values, slots
-
-
-def _u16(t):
-    return t.cpu().numpy().astype(np.int64) & 0xFFFF
-
-
-def run_and_compare(cache, indexer, req_ids, q, decode, *, scaling=1.0,
-                    middle_only=False, check_debug=True):
-    b = len(req_ids)
-    cfg = cfg_from(cache, indexer, scaling)
-    snap = snapshot(cache, 0, b)
-    max_vis = cache.gather_indices_for_layer(0).shape[-1]
-    dbg = {} if check_debug else None
-    sel_out = None
-    if middle_only:
-        sel_out = (torch.full((b, cache.num_kv_heads, max_vis), -7,
-                              dtype=torch.int32, device=DEV),
-                   torch.zeros((b, cache.num_kv_heads), dtype=torch.int32,
-                               device=DEV))
-    select_topk_for_layer_batched(cache, 0, req_ids, q,
-                                  attention=attention_ns(indexer, scaling),
-                                  decode_write=decode, middle_only=middle_only,
-                                  selection_output=sel_out, _debug=dbg)
-    torch.cuda.synchronize()
-    dec_np = None
-    if decode is not None:
-        dec_np = tuple(t.float().cpu().numpy() if t.is_floating_point()
-                       else t.cpu().numpy() for t in decode)
-    res, k_pool, v_pool = run_oracle(cfg, snap, q.float().cpu().numpy(), dec_np,
-                                     max_vis=max_vis, middle_only=middle_only)
-    if middle_only:
-        gather, vis = sel_out[0].cpu().numpy(), sel_out[1].cpu().numpy()
-    else:
-        gather = cache.gather_indices_for_layer(0).cpu().numpy()
-        vis = cache.visible_lens_for_layer(0).cpu().numpy()
-    region_mode = dbg.get('region_mode', 0) if dbg is not None else 0
-    for row_b in range(b):
-        for kv in range(cfg.hkv):
-            r = res[row_b][kv]
-            tag = f'row={row_b} kv={kv}'
-            assert vis[row_b, kv] == r.vis_len, tag
-            n = min(r.vis_len, max_vis)
-            np.testing.assert_array_equal(gather[row_b, kv, :n], r.gather[:n],
-                                          err_msg=tag)
-            if not check_debug or region_mode == 3 or r.far is None:
-                continue
-            kt = len(r.far)
-            np.testing.assert_array_equal(_u16(dbg['far'][row_b, kv, :kt]),
-                                          r.far.astype(np.int64), err_msg=tag)
-            np.testing.assert_array_equal(_u16(dbg['near'][row_b, kv, :kt]),
-                                          r.near.astype(np.int64), err_msg=tag)
-            np.testing.assert_array_equal(
-                dbg['i_f'][row_b, kv, :cfg.k_f].cpu().numpy(), r.i_f, err_msg=tag)
-            np.testing.assert_array_equal(
-                dbg['i_n'][row_b, kv, :cfg.k_n].cpu().numpy(), r.i_n, err_msg=tag)
-            assert tuple(dbg['bounds'][row_b].cpu().tolist()) == (
-                r.lower, r.upper, r.quota), tag
-            nc = int(dbg['cand_count'][row_b, kv])
-            tok = dbg['cand_tok'][row_b, kv, :nc].cpu().numpy()
-            logit = _u16(dbg['cand_logit'][row_b, kv, :nc])
-            # dense page-major layout: slots outside the candidate range are -1
-            scored = tok >= 0
-            tok, logit = tok[scored], logit[scored]
-            order = np.argsort(r.cand_tokens, kind='stable')
-            np.testing.assert_array_equal(tok, r.cand_tokens[order], err_msg=tag)
-            np.testing.assert_array_equal(logit, r.cand_logits[order].astype(np.int64),
-                                          err_msg=tag)
-            cnt = int(dbg['counts'][row_b, kv])
-            assert cnt == r.count, tag
-            np.testing.assert_array_equal(
-                dbg['middle'][row_b, kv, :cnt].cpu().numpy(), r.middle[:cnt],
-                err_msg=tag)
-    if decode is not None:
-        layer = cache.layers[0]
-        slots = decode[2].cpu().numpy()
-        for row_b in range(b):
-            if slots[row_b] < 0:
-                continue
-            phys, off = divmod(int(slots[row_b]), cfg.page)
-            np.testing.assert_array_equal(
-                layer.kv_pool_k[phys, 0, :, off].float().cpu().numpy(),
-                k_pool[phys, 0, :, off])
-            np.testing.assert_array_equal(
-                layer.kv_pool_v[phys, 0, :, off].float().cpu().numpy(),
-                v_pool[phys, 0, :, off])
-    return res
-
-
-GEO16 = RegionGeometry(sink=4, near=4096, window=128, page=16, max_new_tokens=64)
-
-
-def _prod_cache(lengths, *, hkv=2, hq=8, dtype=torch.bfloat16, max_req=4,
-                skips=None, req_ids=None, seed=20261201, zero_keys=False,
-                geometry=GEO16):
-    page = geometry.page
-    extra = geometry.max_new_tokens
-    max_blocks = (max(lengths) + extra + page - 1) // page + 8
-    phys = sum((n + extra + page - 1) // page for n in lengths) + 8
-    cache = make_cache(DEV, geometry=geometry, max_blocks=max_blocks,
-                       max_physical_pages=phys, max_visible_len=1024, hkv=hkv,
-                       hq=hq, dtype=dtype, max_requests=max_req,
-                       max_query_tokens=max(8, max_req))
-    gen = torch.Generator(device=DEV).manual_seed(seed)
-    req_ids = req_ids or list(range(len(lengths)))
-    skips = skips or [(False, False)] * len(lengths)
-    for rid, n, (sf, sn) in zip(req_ids, lengths, skips):
-        _prefill(cache, rid, n, gen, dtype=dtype, zero_keys=zero_keys)
-        cache.freeze(rid, [sf], [sn])
-    return cache, gen, req_ids
+_prefill = prefill_request
+_decode_inputs = decode_inputs
+_u16 = u16
+_prod_cache = prod_cache
 
 
 @pytest.mark.parametrize('lengths', [[20000], [9000, 20500], [5000, 700, 12345]])
