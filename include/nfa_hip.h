@@ -261,6 +261,22 @@ int64_t nfa_attn_workspace_bytes(const NfaAttnParams *p);
 /* A1-A9: decode write + page statistics + L1 + L2 + union for one layer. */
 int32_t nfa_select_layer(const NfaSelectParams *p, void *stream);
 
+/* No counterpart in the reference.  nfa_select_layer for callers that cannot
+   allocate device memory (code under hipGraph capture, tight serving loops,
+   harnesses that forbid hipMalloc): the same kernels and results, but the
+   scratch is a static device array of NFA_SELECT_SCRATCH_BYTES per GPU
+   (held until the process ends) instead of p->workspace, which is ignored.
+   Calls with more than NFA_SELECT_SCRATCH_ROWS rows (batch x kv heads), or
+   whose keys (2 bytes per page slot and row) do not fit beside the fixed
+   counters and histograms, fail with NFA_EWORKSPACE.  The first call on a
+   device takes the array's address and clears its counters (it synchronises
+   the stream once and must not be captured); later calls allocate, clear
+   and synchronise nothing.  All calls on one GPU share the array, so calls
+   that overlap on one GPU race: serialise them (one stream, or events). */
+#define NFA_SELECT_SCRATCH_BYTES (16 << 20)
+#define NFA_SELECT_SCRATCH_ROWS 256
+int32_t nfa_select_layer_noalloc(const NfaSelectParams *p, void *stream);
+
 /* A10: sparse gather attention, out[t,h] = softmax(scale q k^T) v. */
 int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream);
 

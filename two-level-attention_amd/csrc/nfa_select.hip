@@ -35,6 +35,7 @@
 // outputs only.
 #include "nfa_common.h"
 
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -2219,7 +2220,7 @@ using nfa::SelDims;
 
 // compute units of the current device, cached per device
 
-static int select_check(const NfaSelectParams *p) {
+static int select_check(const NfaSelectParams *p, bool need_workspace) {
   if (p == nullptr) {
     nfa_set_error("nfa_select_layer: null params");
     return NFA_EINVAL;
@@ -2285,7 +2286,7 @@ static int select_check(const NfaSelectParams *p) {
     nfa_set_error("nfa_select_layer: max_blocks %d exceeds the grid limit", p->max_blocks);
     return NFA_EINVAL;
   }
-  if (p->workspace == nullptr || p->workspace_bytes < sd.w_total) {
+  if (need_workspace && (p->workspace == nullptr || p->workspace_bytes < sd.w_total)) {
     nfa_set_error("nfa_select_layer: workspace %lld < %lld bytes",
                   (long long)p->workspace_bytes, (long long)sd.w_total);
     return NFA_EWORKSPACE;
@@ -2317,8 +2318,8 @@ extern "C" int64_t nfa_select_workspace_bytes(const NfaSelectParams *p) {
 }
 
 template <int DSUB, typename KV>
-static hipError_t launch_select(const NfaSelectParams &p, hipStream_t stream) {
-  const SelDims sd = nfa::sel_dims(p, nfa::device_cus());
+static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
+                                hipStream_t stream) {
   const int rows = p.batch * p.hkv;
   // one pass per tile whenever a dispatch round of single-pass tiles covers
   // the widest possible row
@@ -2332,41 +2333,144 @@ static hipError_t launch_select(const NfaSelectParams &p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-extern "C" int32_t nfa_select_layer(const NfaSelectParams *p, void *stream) {
-  const int rc = select_check(p);
-  if (rc != NFA_OK) return rc;
-  hipStream_t s = (hipStream_t)stream;
+// Launches the selector (or the protected-only union) of a checked call
+// with the workspace layout `sd`.
+static int32_t select_launch(const NfaSelectParams &p, const SelDims &sd,
+                             hipStream_t s, const char *who) {
   hipError_t err;
-  const bool bf = p->kv_dtype == NFA_DTYPE_BF16;
-  if (p->protected_only) {
-    dim3 grid(p->batch * p->hkv);
+  const bool bf = p.kv_dtype == NFA_DTYPE_BF16;
+  if (p.protected_only) {
+    dim3 grid(p.batch * p.hkv);
     if (bf)
       hipLaunchKernelGGL(nfa::nfa_protected_kernel<uint16_t>, grid,
-                         dim3(nfa::SB), 0, s, *p);
+                         dim3(nfa::SB), 0, s, p);
     else
       hipLaunchKernelGGL(nfa::nfa_protected_kernel<float>, grid, dim3(nfa::SB),
-                         0, s, *p);
+                         0, s, p);
     err = hipGetLastError();
-    if (err != hipSuccess) {
-      nfa_set_error("nfa_select_layer: launch failed: %s", hipGetErrorString(err));
-      return NFA_ELAUNCH;
+  } else {
+    switch (p.dsub) {
+      case 32:
+        err = bf ? launch_select<32, uint16_t>(p, sd, s)
+                 : launch_select<32, float>(p, sd, s);
+        break;
+      case 64:
+        err = bf ? launch_select<64, uint16_t>(p, sd, s)
+                 : launch_select<64, float>(p, sd, s);
+        break;
+      default:
+        err = bf ? launch_select<128, uint16_t>(p, sd, s)
+                 : launch_select<128, float>(p, sd, s);
+        break;
     }
-    return NFA_OK;
-  }
-  switch (p->dsub) {
-    case 32:
-      err = bf ? launch_select<32, uint16_t>(*p, s) : launch_select<32, float>(*p, s);
-      break;
-    case 64:
-      err = bf ? launch_select<64, uint16_t>(*p, s) : launch_select<64, float>(*p, s);
-      break;
-    default:
-      err = bf ? launch_select<128, uint16_t>(*p, s) : launch_select<128, float>(*p, s);
-      break;
   }
   if (err != hipSuccess) {
-    nfa_set_error("nfa_select_layer: launch failed: %s", hipGetErrorString(err));
+    nfa_set_error("%s: launch failed: %s", who, hipGetErrorString(err));
     return NFA_ELAUNCH;
   }
   return NFA_OK;
+}
+
+extern "C" int32_t nfa_select_layer(const NfaSelectParams *p, void *stream) {
+  const int rc = select_check(p, true);
+  if (rc != NFA_OK) return rc;
+  const SelDims sd = nfa::sel_dims(*p, nfa::device_cus());
+  return select_launch(*p, sd, (hipStream_t)stream, "nfa_select_layer");
+}
+
+// ---------------------------------------------------------------------------
+// allocation-free entry: the workspace is a static device array
+// ---------------------------------------------------------------------------
+
+// Fixed layout, so that calls of different batch shapes never place one
+// call's keys over another's counters: row arrival counters, request
+// counters, per-row histograms for the maximum row count, then the keys.
+// The kernel leaves the counters and histograms at zero when it ends, so
+// they are cleared once per device, at the first call.
+constexpr int64_t kScratchRowCnt = 0;
+constexpr int64_t kScratchReqCnt = 4 * NFA_SELECT_SCRATCH_ROWS;
+constexpr int64_t kScratchHist = kScratchReqCnt + 4 * NFA_SELECT_SCRATCH_ROWS;
+constexpr int64_t kScratchKeys = kScratchHist + (int64_t)4 * 512 * NFA_SELECT_SCRATCH_ROWS;
+static_assert(kScratchKeys % 256 == 0 && kScratchKeys < NFA_SELECT_SCRATCH_BYTES,
+              "scratch layout");
+
+static __device__ __align__(256) unsigned char scratch[NFA_SELECT_SCRATCH_BYTES];
+
+__global__ void __launch_bounds__(256) nfa_scratch_clear_kernel(uint4 *dst, int64_t n16) {
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+       i += (int64_t)gridDim.x * blockDim.x)
+    dst[i] = z;
+}
+
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[64];
+
+// This device's copy of `scratch` (its address differs per device), with the
+// counters and histograms cleared; set up at the device's first call.
+static int32_t scratch_for_device(hipStream_t s, void **out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    nfa_set_error("nfa_select_layer_noalloc: no current device");
+    return NFA_EINVAL;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] != nullptr) {
+    *out = g_scratch_ptr[dev];
+    return NFA_OK;
+  }
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+    nfa_set_error("nfa_select_layer_noalloc: the first call on a device sets up "
+                  "its scratch array and must not be captured");
+    return NFA_EINVAL;
+  }
+  void *ptr = nullptr;
+  hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (err != hipSuccess || ptr == nullptr) {
+    nfa_set_error("nfa_select_layer_noalloc: hipGetSymbolAddress failed: %s",
+                  hipGetErrorString(err));
+    return NFA_ELAUNCH;
+  }
+  hipLaunchKernelGGL(nfa_scratch_clear_kernel, dim3(256), dim3(256), 0, s,
+                     (uint4 *)ptr, kScratchKeys / 16);
+  err = hipGetLastError();
+  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  if (err != hipSuccess) {
+    nfa_set_error("nfa_select_layer_noalloc: scratch clear failed: %s",
+                  hipGetErrorString(err));
+    return NFA_ELAUNCH;
+  }
+  g_scratch_ptr[dev] = ptr;
+  *out = ptr;
+  return NFA_OK;
+}
+
+extern "C" int32_t nfa_select_layer_noalloc(const NfaSelectParams *p, void *stream) {
+  int rc = select_check(p, false);
+  if (rc != NFA_OK) return rc;
+  SelDims sd = nfa::sel_dims(*p, nfa::device_cus());
+  const int64_t rows = (int64_t)p->batch * p->hkv;
+  const int64_t keys = (((int64_t)2 * rows * sd.kstride) + 255) & ~(int64_t)255;
+  if (rows > NFA_SELECT_SCRATCH_ROWS || kScratchKeys + keys > NFA_SELECT_SCRATCH_BYTES) {
+    nfa_set_error("nfa_select_layer_noalloc: %lld rows (batch x kv heads) of %d "
+                  "pages need %lld scratch bytes; the static array holds %lld "
+                  "bytes and %d rows",
+                  (long long)rows, p->max_blocks, (long long)(kScratchKeys + keys),
+                  (long long)NFA_SELECT_SCRATCH_BYTES, NFA_SELECT_SCRATCH_ROWS);
+    return NFA_EWORKSPACE;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  void *ptr = nullptr;
+  rc = scratch_for_device(s, &ptr);
+  if (rc != NFA_OK) return rc;
+  sd.w_rowcnt = kScratchRowCnt;
+  sd.w_reqcnt = kScratchReqCnt;
+  sd.w_hist = kScratchHist;
+  sd.w_keys = kScratchKeys;
+  sd.w_total = kScratchKeys + keys;
+  NfaSelectParams q = *p;
+  q.workspace = ptr;
+  q.workspace_bytes = NFA_SELECT_SCRATCH_BYTES;
+  return select_launch(q, sd, s, "nfa_select_layer_noalloc");
 }

@@ -183,6 +183,8 @@ def load_library(path: str = None):
         lib.nfa_attn_workspace_bytes.argtypes = [ctypes.POINTER(NfaAttnParams)]
         lib.nfa_select_layer.restype = _i32
         lib.nfa_select_layer.argtypes = [ctypes.POINTER(NfaSelectParams), _ptr]
+        lib.nfa_select_layer_noalloc.restype = _i32
+        lib.nfa_select_layer_noalloc.argtypes = [ctypes.POINTER(NfaSelectParams), _ptr]
         lib.nfa_sparse_attn_decode.restype = _i32
         lib.nfa_sparse_attn_decode.argtypes = [ctypes.POINTER(NfaAttnParams), _ptr]
         lib.nfa_paged_write_decode.restype = _i32

@@ -155,19 +155,14 @@ def _alloc_debug(debug, b, hkv, max_blocks, k_f, k_n, k2, cand_cap, device):
     debug['cand_count'] = torch.zeros((b, hkv), dtype=i32, device=device)
 
 
-def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
-                                  attention=None, decode_write=None,
-                                  middle_only=False, selection_output=None,
-                                  _debug=None):
-    """Select this layer's attended tokens for every batch row.
+def select_layer_params(cache, layer_idx, req_ids, query_states,
+                        attention=None, decode_write=None, middle_only=False,
+                        selection_output=None):
+    """Validate one selector call and describe it as ``NfaSelectParams``.
 
-    ``query_states`` is the current post-RoPE query ``[B, HQ, D]``;
-    ``decode_write=(k [B,HKV,1,D], v [B,HKV,1,DV], slots [B])`` writes the
-    current token into the arena before anything reads it.  Results go to
-    ``cache.gather_indices_for_layer(layer_idx)[:B]`` (absolute physical
-    slots, ascending logical order) and ``cache.visible_lens_for_layer``;
-    with ``middle_only`` only the middle selection is written to
-    ``selection_output=(gather, lens)``.  Returns None.
+    Returns ``(params, keep)`` -- ``keep`` holds tensors the parameters
+    point into (converted decode K/V), which must outlive the launch -- or
+    None for an empty batch.  The workspace fields are left unset.
     """
     if query_states is None:
         raise ValueError('production selection requires current post-RoPE query')
@@ -181,7 +176,7 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
         raise FallbackRequired('HIP device required')
     b = len(req_ids)
     if b == 0:
-        return
+        return None
     indexer = attention.indexer
     if not hasattr(indexer, 'args') or indexer.args is None:
         raise FallbackRequired('missing indexer config')
@@ -278,12 +273,14 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
     p.q = query_states.data_ptr()
     p.q_stride_b = query_states.stride(0)
     p.q_stride_h = query_states.stride(1)
+    keep = []
     if decode_write is not None:
         # converted copies are stream-ordered allocations: safe to drop after
         # the asynchronous launch
         keys, values, slots = _check_decode_write(decode_write, b, hkv, device)
         keys = keys.to(kv_dtype)
         values = values.to(kv_dtype)
+        keep += [keys, values, slots]
         p.k_new, p.v_new, p.slots = keys.data_ptr(), values.data_ptr(), slots.data_ptr()
     p.stat_min_l, p.stat_max_l, p.stat_sum_l = (
         smin.data_ptr(), smax.data_ptr(), ssum.data_ptr())
@@ -292,6 +289,36 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
     p.page_sum_l = psum.data_ptr()
     p.gather = gather_out.data_ptr()
     p.vis_lens = vis_out.data_ptr()
+    p._region_mode = region_mode
+    keep.append(query_states)
+    return p, keep
+
+
+def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
+                                  attention=None, decode_write=None,
+                                  middle_only=False, selection_output=None,
+                                  _debug=None):
+    """Select this layer's attended tokens for every batch row.
+
+    ``query_states`` is the current post-RoPE query ``[B, HQ, D]``;
+    ``decode_write=(k [B,HKV,1,D], v [B,HKV,1,DV], slots [B])`` writes the
+    current token into the arena before anything reads it.  Results go to
+    ``cache.gather_indices_for_layer(layer_idx)[:B]`` (absolute physical
+    slots, ascending logical order) and ``cache.visible_lens_for_layer``;
+    with ``middle_only`` only the middle selection is written to
+    ``selection_output=(gather, lens)``.  Returns None.
+    """
+    built = select_layer_params(cache, layer_idx, req_ids, query_states,
+                                attention, decode_write, middle_only,
+                                selection_output)
+    if built is None:
+        return
+    p, keep = built
+    lib = nat.load_library()
+    b, hkv = p.batch, p.hkv
+    k_f, k_n, k2, bs = p.k_f, p.k_n, p.k2, p.bs
+    region_mode = p._region_mode
+    device = keep[-1].device
     need = lib.nfa_select_workspace_bytes(ctypes.byref(p))
     ws = _workspace(cache)
     scratch_key = ('nfa_select_scratch', b, hkv, cache.max_blocks, k_f, k_n)
