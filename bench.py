@@ -11,14 +11,27 @@ outlier-channel recipe: N(0,1) per channel times a per-channel
 LogNormal(0,1) scale, RoPE theta 1e6 at positions 0..L-1; values and queries
 N(0,1).
 
-One step = one decode token through the hot path of all 36 layers: the
-selector (fused decode K/V write, page statistics, L1, L2, union) and the
-sparse gather attention, captured once into a hipGraph and replayed, with
-the host-side step planning (plan_common / commit_step) in the timed loop.
-Dense projections and the MLP are outside this hot path.
+Headline (``value``, ``ms_per_step``, ``steps``, ``warmup``): whole-model
+decode of a random-init bf16 Qwen3-8B after a dense prefill of the same
+context -- ``--warmup`` untimed and ``--steps`` timed greedy steps replayed
+from a hipGraph, HIP events around each runner step, median TPOT; value =
+1000 / TPOT tok/s.
 
-Prints one JSON line (see ``_result``); ``--gpus`` above 1 is refused: this
-path runs on one GPU.
+Per layer (``config.layer_us`` and the roofline): the hot path alone -- the
+selector (fused decode K/V write, page statistics, L1, L2, union) and the
+sparse gather attention of all 36 layers -- captured into one graph, warmed
+by untimed replays, then ``--hot-steps`` replays timed with HIP events on the
+replaying stream (median), the host planning of each step (plan_common /
+commit_step) overlapping the previous replay.  The selector and the attention
+are also captured alone and timed the same way (``select_us``,
+``attention_us``, the roofline's achieved bandwidth).
+
+CPU baseline (reported, not the target): the numpy oracle on the 32K fp32
+layer, the kv heads spread over worker processes, 3 warm-up and 10 timed
+steps, split into L1 / L2 / attention.
+
+Prints one JSON line; ``--gpus`` above 1 is refused: this path runs on one
+GPU.
 """
 import argparse
 import ctypes
@@ -40,8 +53,15 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=200)
-    ap.add_argument('--warmup', type=int, default=30)
+    ap.add_argument('--steps', type=int, default=256,
+                    help='timed whole-model decode steps (the headline e2e tok/s '
+                         'is 1000 / their median TPOT)')
+    ap.add_argument('--warmup', type=int, default=3,
+                    help='untimed whole-model decode steps before them')
+    ap.add_argument('--hot-steps', type=int, default=200,
+                    help='timed replays of the 36-layer hot-path graph')
+    ap.add_argument('--hot-warmup', type=int, default=30,
+                    help='eager steps, then as many untimed graph replays, before them')
     ap.add_argument('--ctx', type=int, default=131072)
     ap.add_argument('--batch', type=int, default=1,
                     help='decode rows (requests) sharing one cache per layer')
@@ -54,17 +74,15 @@ def parse():
     ap.add_argument('--operator-mode', choices=['off', 'serial', 'overlap'], default='off',
                     help='decode attention of the timed step: one union pass (off) or '
                          'protected and middle apart, then merged (serial / overlap)')
-    ap.add_argument('--kernel-rounds', type=int, default=20)
-    ap.add_argument('--cpu-seconds', type=float, default=15.0,
-                    help='budget of the CPU oracle baseline sample')
+    ap.add_argument('--kernel-rounds', type=int, default=40,
+                    help='replays of the selector-only and attention-only graphs')
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--seed', type=int, default=20261201)
     ap.add_argument('--timeline', type=int, default=0,
                     help='print selector phase timings of N extra decode steps')
-    ap.add_argument('--e2e-steps', type=int, default=256,
-                    help='also run the whole Qwen3-8B-geometry model (random-init '
-                         'bf16): dense prefill of --ctx tokens, then this many '
-                         'greedy decode steps replayed from a hipGraph; 0 = off')
+    ap.add_argument('--no-e2e', action='store_true',
+                    help='skip the whole-model decode (the headline value is then '
+                         'the hot path\'s tok/s)')
     ap.add_argument('--e2e-unfused', action='store_true',
                     help='end-to-end decode with HF\'s own dense layers (only the '
                          'attention patched)')
@@ -104,7 +122,8 @@ def build_workload(torch, args, device):
     from sparse_attn.policies.region_geometry import RegionGeometry
 
     hkv, hq, d, page = 8, 32, 128, 16
-    new_tokens = args.warmup + args.steps + args.kernel_rounds + args.timeline + 8
+    new_tokens = (2 * args.hot_warmup + args.hot_steps + 2 * args.kernel_rounds
+                  + args.timeline + 8)
     geo = RegionGeometry(sink=4, near=4096, window=128, page=page,
                          max_new_tokens=new_tokens)
     b = args.batch
@@ -222,20 +241,6 @@ def measured_traffic(args):
     return int(m.group(1)) if m else None
 
 
-def _oracle_cfg(w):
-    """Oracle configuration of the workload (CPU baseline leg only)."""
-    from oracle import nfa_oracle as orc
-    import numpy as np
-    import torch
-    cache = w.cache
-    dims = w.indexer._subspace_indices(torch.device('cpu')).numpy()
-    return orc.NfaConfig(
-        hq=w.hq, hkv=w.hkv, head_dim=w.d, head_dim_v=w.d, bs=16, page=w.page,
-        max_blocks=cache.max_blocks, geo_sink=4, geo_near=4096, geo_window=128,
-        sink_tokens=4, swa=128, near_len=4096, k1=128, near_pages=32, k2=1024,
-        dims=np.asarray(dims), fine_dims=np.asarray(dims), scale=w.d ** -0.5)
-
-
 def time_kernels(torch, w, rounds, plan):
     """Per-launch durations of the selector entry point (kernel A + kernel B)
     and of the attention kernel.  Each is captured alone into a graph of one
@@ -274,6 +279,11 @@ def time_kernels(torch, w, rounds, plan):
     with torch.cuda.graph(g_att):
         att_all()
     cache.commit_step()
+    for _ in range(rounds):  # untimed replays: graph upload, caches
+        plan()
+        g_sel.replay()
+        g_att.replay()
+        cache.commit_step()
     torch.cuda.synchronize()
     sel, att = [], []
     lengths = []
@@ -371,7 +381,7 @@ def qwen3_8b_config(ctx, new_tokens):
 def end_to_end(torch, args, device):
     """Whole-model decode: random-init bf16 Qwen3-8B, dense prefill of
     ``args.ctx`` seeded uniform token ids into the paged cache, 3 warm-up
-    steps, then ``args.e2e_steps`` greedy steps replayed from one captured
+    steps, then ``args.steps`` greedy steps replayed from one captured
     hipGraph each; HIP events around every ``GraphRunner.step``, median
     TPOT (the steady-state time per output token)."""
     from transformers import Qwen3ForCausalLM
@@ -383,8 +393,8 @@ def end_to_end(torch, args, device):
     from sparse_attn.policies.region_geometry import RegionGeometry
     from sparse_attn.scheduler.scheduler import ContinuousBatchScheduler
 
-    warm = 3
-    new_tokens = warm + args.e2e_steps + 8
+    warm = args.warmup
+    new_tokens = warm + args.steps + 8
     cfg = qwen3_8b_config(args.ctx, new_tokens)
     t0 = time.perf_counter()
     torch.manual_seed(args.seed)
@@ -436,14 +446,14 @@ def end_to_end(torch, args, device):
         torch.cuda.synchronize()
         events = [(torch.cuda.Event(enable_timing=True),
                    torch.cuda.Event(enable_timing=True))
-                  for _ in range(args.e2e_steps)]
+                  for _ in range(args.steps)]
         t0 = time.perf_counter()
         for i, (a, b) in enumerate(events):
             a.record()
             runner.step(model, cache, generated_counts=warm + i + 1)
             b.record()
         torch.cuda.synchronize()
-        wall_ms = (time.perf_counter() - t0) * 1e3 / args.e2e_steps
+        wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     tpot = sorted(a.elapsed_time(b) for a, b in events)
     med = tpot[len(tpot) // 2]
     tokens = len(sched.flush_ready_receipts())
@@ -454,7 +464,7 @@ def end_to_end(torch, args, device):
         'dense_layers': 'fused HIP decode layers' if fused else 'HF modules',
         'params': params, 'patched_attention_layers': n_patched,
         'prompt_tokens': args.ctx, 'prefill_s': round(prefill_s, 2),
-        'decode_steps': args.e2e_steps, 'warmup_steps': warm,
+        'decode_steps': args.steps, 'warmup_steps': warm,
         'tpot_ms_median': round(med, 4),
         'tpot_ms_p10_p90': [round(tpot[len(tpot) // 10], 4),
                             round(tpot[(len(tpot) * 9) // 10], 4)],
@@ -469,56 +479,207 @@ def end_to_end(torch, args, device):
     return res
 
 
-def cpu_baseline(torch, w, seconds):
-    """The CPU oracle on a bounded sample: layer-0 decode steps at the same
-    128K context, single-threaded numpy."""
+# ---------------------------------------------------------------------------
+# CPU baseline: the numpy oracle on the single-layer 32K fp32 workload
+# ---------------------------------------------------------------------------
+
+_CPU = {}   # inherited by the forked workers: pools, query, geometry
+
+
+def _cpu_config0(seed, extra_tokens):
+    """Config-0 layer as numpy arrays: Qwen3-8B layer geometry (32 query /
+    8 KV heads, head_dim 128), 32768-token context plus ``extra_tokens``
+    decode tokens, page 16, fp32 paged K/V; outlier-channel keys (N(0,1) x
+    per-channel LogNormal(0,1) scale, RoPE theta 1e6), N(0,1) values and
+    queries."""
     import numpy as np
     from oracle import nfa_oracle as orc
-    try:
-        from threadpoolctl import threadpool_limits
-    except Exception:  # pragma: no cover
-        threadpool_limits = None
-    cache = w.cache
-    cfg = _oracle_cfg(w)
-    layer = cache.layers[0]
-    k_pool = layer.kv_pool_k.float().cpu().numpy()
-    v_pool = layer.kv_pool_v.float().cpu().numpy()
-    bt = cache.block_table_buf[0].cpu().numpy().astype(np.int64)
-    length = int(cache.states[0].logical_length) + 1
-    q = w.q[0].float().cpu().numpy()
-    q2r = np.zeros(1, dtype=np.int64)
-    ctx = threadpool_limits(1) if threadpool_limits else None
-    if ctx is not None:
-        ctx.__enter__()
-    try:
-        n = 0
-        t0 = time.perf_counter()
-        while True:
-            res = orc.select_layer(cfg, k_pool, bt, np.array([length]),
-                                   np.array([0]), np.array([True]), np.zeros(1),
-                                   np.zeros(1), q, 1024)
-            gather = np.zeros((1, w.hkv, 1024), dtype=np.int64)
-            vis = np.zeros((1, w.hkv), dtype=np.int64)
-            for kv in range(w.hkv):
-                r = res[0][kv]
-                gather[0, kv, :len(r.gather)] = r.gather
-                vis[0, kv] = r.vis_len
-            orc.sparse_attention(k_pool, v_pool, q, gather, vis, q2r,
-                                 cfg.scale, w.page)
-            n += 1
-            elapsed = time.perf_counter() - t0
-            if elapsed >= seconds or n >= 100:
-                break
-    finally:
-        if ctx is not None:
-            ctx.__exit__(None, None, None)
-    layer_s = elapsed / n
-    return dict(value=1.0 / (layer_s * len(w.q)), unit='tok/s', cores=1,
-                kind='port',
-                sample=f'{n} single-layer decode steps (selector + attention) '
-                       f'of the same 128K workload on the numpy oracle, '
-                       f'{layer_s * 1e3:.1f} ms per layer, scaled to '
-                       f'{len(w.q)} layers per token')
+    hq, hkv, d, page, ctx = 32, 8, 128, 16, 32768
+    total = ctx + extra_tokens
+    pages = (total + page - 1) // page
+    rng = np.random.default_rng(seed)
+    scale = np.exp(rng.standard_normal((hkv, 1, d), dtype=np.float32))
+    keys = rng.standard_normal((hkv, total, d), dtype=np.float32) * scale
+    half = d // 2
+    inv = 1e6 ** (-np.arange(half, dtype=np.float64) / half)
+    ang = np.arange(total, dtype=np.float64)[:, None] * inv[None, :]
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    x1, x2 = keys[..., :half], keys[..., half:]
+    keys = np.concatenate((x1 * cos - x2 * sin, x2 * cos + x1 * sin), axis=-1)
+    values = rng.standard_normal((hkv, total, d), dtype=np.float32)
+    k_pool = np.zeros((pages + 1, 1, hkv, page, d), dtype=np.float32)
+    v_pool = np.zeros_like(k_pool)
+    pad = pages * page - total
+    k_pool[:pages, 0] = np.pad(keys, ((0, 0), (0, pad), (0, 0))).reshape(
+        hkv, pages, page, d).transpose(1, 0, 2, 3)
+    v_pool[:pages, 0] = np.pad(values, ((0, 0), (0, pad), (0, 0))).reshape(
+        hkv, pages, page, d).transpose(1, 0, 2, 3)
+    dims = np.arange(96, 128)   # tail subspace at cmp_ratio 4
+    cfg = orc.NfaConfig(
+        hq=hq, hkv=hkv, head_dim=d, head_dim_v=d, bs=16, page=page,
+        max_blocks=pages + 8, geo_sink=4, geo_near=4096, geo_window=128,
+        sink_tokens=4, swa=128, near_len=4096, k1=128, near_pages=32, k2=1024,
+        dims=dims, fine_dims=dims, scale=d ** -0.5, kv_dtype='fp32')
+    bt = np.full(cfg.max_blocks, pages, dtype=np.int64)
+    bt[:pages] = np.arange(pages)
+    qs = rng.standard_normal((3 + extra_tokens, 1, hq, d), dtype=np.float32)
+    return dict(cfg=cfg, k_pool=k_pool, v_pool=v_pool, bt=bt, ctx=ctx, q=qs,
+                new_k=keys[:, ctx:], new_v=values[:, ctx:])
+
+
+def _cpu_apply_writes(kv, upto):
+    """Decode tokens 0..upto-1 of kv head ``kv`` into this process's pools
+    (a worker's pools are its own copies, so every phase-1 call replays the
+    writes it may have missed)."""
+    c = _CPU
+    page = c['cfg'].page
+    for i in range(upto):
+        pos = c['ctx'] + i
+        c['k_pool'][pos // page, 0, kv, pos % page] = c['new_k'][kv, i]
+        c['v_pool'][pos // page, 0, kv, pos % page] = c['new_v'][kv, i]
+
+
+def _cpu_l1(args):
+    from oracle import nfa_oracle as orc
+    kv, step, length = args
+    c = _CPU
+    cfg = c['cfg']
+    _cpu_apply_writes(kv, step + 1)
+    q_full = orc.prepare_q(cfg, c['q'][step, 0], cfg.dims)
+    far, near, geo = orc.l1_scores(cfg, c['k_pool'], c['bt'], length, kv, q_full,
+                                   False, False)
+    i_f = orc.l1_topk(far, 0, geo.far_end, cfg.k_f, cfg.kt_cap)
+    i_n = orc.l1_topk(near, geo.near_start, geo.near_end, cfg.k_n, cfg.kt_cap)
+    return far, near, i_f, i_n
+
+
+def _cpu_l2(args):
+    from oracle import nfa_oracle as orc
+    kv, step, length, (far, near, i_f, i_n) = args
+    c = _CPU
+    cfg = c['cfg']
+    q_fine = orc.prepare_q_grouped(cfg, c['q'][step, 0])
+    lower, upper, quota = orc.l2_bounds(cfg, length, False, False)
+    token, active, pack_r = orc.candidate_slots(cfg, i_f, i_n, far, near, length)
+    load = orc.owned_slots(cfg, token, active, pack_r, lower, upper)
+    logits = orc.l2_logits(cfg, c['k_pool'], c['bt'], token, load, q_fine[kv], kv,
+                           quota)
+    middle, count = orc.l2_middle(cfg, logits, token, length, False, False,
+                                  lower, upper, quota)
+    return orc.final_union(cfg, middle, count, length, c['bt'], 1024)
+
+
+def _cpu_attention(args):
+    import numpy as np
+    from oracle import nfa_oracle as orc
+    kv, step, (gather, vis) = args
+    c = _CPU
+    cfg = c['cfg']
+    g = cfg.group
+    q = c['q'][step][:, kv * g:(kv + 1) * g]
+    out = orc.sparse_attention(c['k_pool'][:, :, kv:kv + 1], c['v_pool'][:, :, kv:kv + 1],
+                               q, np.asarray(gather)[None, None], np.array([[vis]]),
+                               np.array([0]), cfg.scale, cfg.page)
+    return out
+
+
+def cpu_baseline(warmup=3, steps=10, seed=20261201):
+    """Single-layer decode steps of the 32K fp32 layer on the numpy oracle,
+    the 8 kv heads spread over worker processes: 3 warm-up and 10 timed
+    steps (the context grows by the decode token each step), each split
+    into L1 (decode write, page statistics, scores, top-k), L2 (candidates,
+    logits, top-quota, union) and attention, timed with perf_counter around
+    each phase; medians reported.  Runs before anything touches the GPU."""
+    import multiprocessing as mp
+    import statistics
+    _CPU.clear()
+    _CPU.update(_cpu_config0(seed, warmup + steps))
+    hkv = _CPU['cfg'].hkv
+    cores = os.cpu_count() or 1
+    workers = max(1, min(hkv, cores))
+    phases = {'l1': [], 'l2': [], 'attention': []}
+    with mp.get_context('fork').Pool(workers) as pool:
+        for step in range(warmup + steps):
+            length = _CPU['ctx'] + step + 1
+            t0 = time.perf_counter()
+            l1 = pool.map(_cpu_l1, [(kv, step, length) for kv in range(hkv)],
+                          chunksize=1)
+            t1 = time.perf_counter()
+            l2 = pool.map(_cpu_l2, [(kv, step, length, l1[kv]) for kv in range(hkv)],
+                          chunksize=1)
+            t2 = time.perf_counter()
+            pool.map(_cpu_attention, [(kv, step, l2[kv]) for kv in range(hkv)],
+                     chunksize=1)
+            t3 = time.perf_counter()
+            if step >= warmup:
+                phases['l1'].append(t1 - t0)
+                phases['l2'].append(t2 - t1)
+                phases['attention'].append(t3 - t2)
+    totals = [a + b + c for a, b, c in zip(*phases.values())]
+    med = {k: statistics.median(v) * 1e6 for k, v in phases.items()}
+    layer_us = statistics.median(totals) * 1e6
+    _CPU.clear()
+    return dict(value=round(layer_us, 1), unit='µs per decode layer (selector + attention)',
+                cores=workers, kind='port',
+                l1_us=round(med['l1'], 1), l2_us=round(med['l2'], 1),
+                attention_us=round(med['attention'], 1),
+                tok_s_36_layers=round(1e6 / (layer_us * 36), 4),
+                host_cpus=cores,
+                sample=f'{steps} timed single-layer decode steps after {warmup} '
+                       'warm-up steps of the 32768-token fp32 layer (Qwen3-8B '
+                       'layer geometry, page 16, production flags) on the numpy '
+                       f'oracle, the {hkv} kv heads in {workers} worker processes; '
+                       'median per phase')
+
+
+def hot_path_loop(torch, w, args, plan, outs):
+    """The 36-layer hot path as one captured graph: ``hot_warmup`` eager
+    steps (the first rebuilds the page statistics), capture, ``hot_warmup``
+    untimed replays, then ``hot_steps`` timed replays with HIP events on
+    the replaying stream around each.  The host planning of a step
+    (plan_common, commit_step) runs while the previous replay executes."""
+    for _ in range(args.hot_warmup):
+        plan()
+        for layer in range(args.layers):
+            run_layer(w, layer, outs)
+        w.cache.commit_step()
+    torch.cuda.synchronize()
+    plan()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for layer in range(args.layers):  # warm the capture stream
+            run_layer(w, layer, outs)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for layer in range(args.layers):
+            run_layer(w, layer, outs)
+    w.cache.commit_step()
+    for _ in range(args.hot_warmup):
+        plan()
+        graph.replay()
+        w.cache.commit_step()
+    torch.cuda.synchronize()
+    print('# hot-path graph captured and warm', file=sys.stderr, flush=True)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.hot_steps)]
+    t0 = time.perf_counter()
+    for a, b in events:
+        plan()
+        a.record()
+        graph.replay()
+        b.record()
+        w.cache.commit_step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.hot_steps
+    dev = sorted(a.elapsed_time(b) for a, b in events)
+    med = dev[len(dev) // 2]
+    print(f'# hot path: {med:.3f} ms per step (device median), {wall_ms:.3f} ms '
+          'wall', file=sys.stderr, flush=True)
+    return graph, dict(ms_per_step_median=med, wall_ms_per_step=wall_ms,
+                       ms_p10_p90=[dev[len(dev) // 10], dev[(len(dev) * 9) // 10]])
 
 
 def main():
@@ -527,6 +688,14 @@ def main():
         print(json.dumps({'error': 'this hot path runs on one GPU; '
                                    f'--gpus {args.gpus} is not supported'}))
         sys.exit(2)
+    single = args.batch == 1 and not args.ragged
+    cpu = None
+    if not args.no_cpu_baseline and single and not args.e2e_only \
+            and args.copy_calibration == 0:
+        # before torch or HIP start: the baseline forks worker processes
+        print('# cpu baseline ...', file=sys.stderr, flush=True)
+        cpu = cpu_baseline(seed=args.seed)
+        print(f'# cpu baseline: {cpu["value"]} us per layer', file=sys.stderr, flush=True)
     import torch
     from sparse_attn import _native
     if not os.path.exists(_native.LIB_PATH):
@@ -545,12 +714,10 @@ def main():
                           'launches': 3}), flush=True)
         return
     if args.e2e_only:
-        steps = args.e2e_steps or 256
-        args.e2e_steps = steps
         e2e = end_to_end(torch, args, device)
         print(json.dumps({
             'metric': 'e2e decode tok/s at 128K ctx', 'value': e2e['tok_s'],
-            'unit': 'tok/s', 'n_gpus': 1, 'steps': steps, 'warmup': 3,
+            'unit': 'tok/s', 'n_gpus': 1, 'steps': args.steps, 'warmup': args.warmup,
             'ms_per_step': e2e['tpot_ms_median'], 'higher_is_better': True,
             'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16',
             'data': 'synthetic', 'config': {'workload': 'whole-model decode', **e2e},
@@ -567,76 +734,47 @@ def main():
         cache.new_step(w.req_ids)
         cache.plan_common(w.req_ids)
 
-    # warm-up: first step rebuilds page statistics, later ones are incremental
-    for _ in range(args.warmup):
-        plan()
-        for layer in range(args.layers):
-            run_layer(w, layer, outs)
-        cache.commit_step()
-    torch.cuda.synchronize()
-
-    # capture one decode step of all layers
-    plan()
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        for layer in range(args.layers):  # warm the capture stream
-            run_layer(w, layer, outs)
-    torch.cuda.current_stream().wait_stream(stream)
-    torch.cuda.synchronize()
-    with torch.cuda.graph(graph):
-        for layer in range(args.layers):
-            run_layer(w, layer, outs)
-    cache.commit_step()
-    torch.cuda.synchronize()
-    print('# graph captured', file=sys.stderr, flush=True)
-
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        plan()
-        graph.replay()
-        cache.commit_step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
-    print(f'# timed {args.steps} steps: {ms_per_step:.3f} ms/step', file=sys.stderr,
-          flush=True)
-
+    graph, hot = hot_path_loop(torch, w, args, plan, outs)
     if args.timeline:
         selector_timeline(torch, w, args.timeline, plan)
     # per-kernel durations (events around each launch), same stream
     kt = time_kernels(torch, w, args.kernel_rounds, plan)
     per_req = [algorithmic_bytes(w, n) for n in kt['lengths']]
     nbytes = {k: sum(b[k] for b in per_req) for k in ('select', 'attention')}
-    sel_gbs = nbytes['select'] / (kt['select_us'] * 1e-6) / 1e9
-    att_gbs = nbytes['attention'] / (kt['attention_us'] * 1e-6) / 1e9
-    layer_us = ms_per_step * 1e3 / args.layers
+    sel_gbs = nbytes['select'] / (kt['select_us_median'] * 1e-6) / 1e9
+    att_gbs = nbytes['attention'] / (kt['attention_us_median'] * 1e-6) / 1e9
+    layer_us = hot['ms_per_step_median'] * 1e3 / args.layers
     layer_gbs = (nbytes['select'] + nbytes['attention']) / (layer_us * 1e-6) / 1e9
-
-    single = args.batch == 1 and not args.ragged
-    cpu = None
-    if not args.no_cpu_baseline and single:
-        print('# cpu baseline ...', file=sys.stderr, flush=True)
-        cpu = cpu_baseline(torch, w, args.cpu_seconds)
+    hot_tok_s = args.batch * 1e3 / hot['ms_per_step_median']
     geometry = {'heads': [w.hq, w.hkv], 'head_dim': w.d, 'page': w.page}
     lengths = list(w.lengths)
     e2e = None
-    if args.e2e_steps > 0 and single:
+    if not args.no_e2e and single:
         del graph, w, cache, outs
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
         e2e = end_to_end(torch, args, device)
 
+    if e2e is not None:
+        value, ms_per_step = e2e['tok_s'], e2e['tpot_ms_median']
+        steps, warmup = args.steps, args.warmup
+        headline = ('whole-model decode: random-init bf16 Qwen3-8B, dense prefill '
+                    f'of {args.ctx} tokens, median TPOT over {steps} greedy steps '
+                    'replayed from a hipGraph; hot path = selector + attention of '
+                    f'{args.layers} layers')
+    else:
+        value, ms_per_step = hot_tok_s, hot['ms_per_step_median']
+        steps, warmup = args.hot_steps, args.hot_warmup
+        headline = (f'hot path only: selector + attention of {args.layers} layers '
+                    'per decode token, median device time per graph replay')
     result = {
         'metric': 'sparse-attn decode layer µs + e2e decode tok/s at 128K '
                   'ctx; % of HBM peak',
-        'value': round(args.batch * 1e3 / ms_per_step, 2),
+        'value': round(value, 2),
         'unit': 'tok/s',
         'n_gpus': 1,
-        'steps': args.steps,
-        'warmup': args.warmup,
+        'steps': steps,
+        'warmup': warmup,
         'ms_per_step': round(ms_per_step, 4),
         'higher_is_better': True,
         'scaling': 'weak',
@@ -644,12 +782,12 @@ def main():
         'dtype': 'bf16',
         'data': 'synthetic',
         'config': {
-            'workload': f'NFA sparse-attention decode hot path (selector + '
-                        f'attention) of {args.layers} layers, Qwen3-8B attention '
-                        f'geometry, batch {args.batch}, '
+            'workload': f'NFA sparse-attention decode, Qwen3-8B attention geometry, '
+                        f'batch {args.batch}, '
                         + (f'contexts U({args.ragged[0]}, {args.ragged[1]})'
                            if args.ragged else f'{args.ctx // 1024}K context')
                         + ', page 16, hipGraph',
+            'value_is': headline,
             'layers': args.layers, 'batch': args.batch,
             'operator_mode': args.operator_mode, 'l2_keys': '4-bit' if args.l2_quant
                                                           else 'bf16',
@@ -659,8 +797,13 @@ def main():
                    'tail dims cmp 4, sink 4, SWA 128, K2 1024',
             'layer_us': round(layer_us, 3),
             'layer_hbm_frac': round(layer_gbs / HBM_PEAK_GBS, 4),
-            'select_us': round(kt['select_us'], 3),
-            'attention_us': round(kt['attention_us'], 3),
+            'hot_path_ms_per_step': round(hot['ms_per_step_median'], 4),
+            'hot_path_wall_ms_per_step': round(hot['wall_ms_per_step'], 4),
+            'hot_path_ms_p10_p90': [round(x, 4) for x in hot['ms_p10_p90']],
+            'hot_path_tok_s': round(hot_tok_s, 2),
+            'hot_path_steps': args.hot_steps,
+            'select_us': round(kt['select_us_median'], 3),
+            'attention_us': round(kt['attention_us_median'], 3),
             'select_bytes': nbytes['select'],
             'attention_bytes': nbytes['attention'],
             'attention_gbs': round(att_gbs, 1),
