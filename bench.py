@@ -287,10 +287,14 @@ def time_kernels(torch, w, rounds, plan):
     torch.cuda.synchronize()
     sel, att = [], []
     lengths = []
-    for _ in range(rounds):
+    marks = [(a, b, torch.cuda.Event(enable_timing=True))
+             for a, b in warm_events(torch, rounds)]
+    for m in marks:
+        m[2].record()
+    torch.cuda.synchronize()
+    for a, b, c in marks:
         plan()
         lengths = [int(cache.pending_lengths[r]) for r in w.req_ids]
-        a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
         a.record()
         g_sel.replay()
         b.record()
@@ -444,9 +448,7 @@ def end_to_end(torch, args, device):
         for i in range(warm):
             runner.step(model, cache, generated_counts=i + 1)
         torch.cuda.synchronize()
-        events = [(torch.cuda.Event(enable_timing=True),
-                   torch.cuda.Event(enable_timing=True))
-                  for _ in range(args.steps)]
+        events = warm_events(torch, args.steps)
         t0 = time.perf_counter()
         for i, (a, b) in enumerate(events):
             a.record()
@@ -632,6 +634,19 @@ def cpu_baseline(warmup=3, steps=10, seed=20261201):
                        'median per phase')
 
 
+def warm_events(torch, n):
+    """``n`` pairs of timing events, each recorded once already: HIP creates
+    an event at its first record, slowly for the first few hundred of a
+    process, which must not happen inside a timed loop."""
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(n)]
+    for a, b in events:
+        a.record()
+        b.record()
+    torch.cuda.synchronize()
+    return events
+
+
 def hot_path_loop(torch, w, args, plan, outs):
     """The 36-layer hot path as one captured graph: ``hot_warmup`` eager
     steps (the first rebuilds the page statistics), capture, ``hot_warmup``
@@ -663,8 +678,7 @@ def hot_path_loop(torch, w, args, plan, outs):
         w.cache.commit_step()
     torch.cuda.synchronize()
     print('# hot-path graph captured and warm', file=sys.stderr, flush=True)
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(args.hot_steps)]
+    events = warm_events(torch, args.hot_steps)
     t0 = time.perf_counter()
     for a, b in events:
         plan()

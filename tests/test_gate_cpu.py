@@ -5,7 +5,7 @@ Reference: sparse_attn/policies/frozen_gate.py:8-24 (GateConfig) and
 """
 import pytest
 
-from sparse_attn.policies.frozen_gate import (GateConfig, _profile_summary,
+from sparse_attn.policies.frozen_gate import (GateConfig, _summarise,
                                               decide_regions, region_present)
 from sparse_attn.policies.region_geometry import RegionGeometry
 
@@ -39,7 +39,7 @@ def test_decision_rule():
 def test_profile_summary_and_presence():
     import torch
     vals = torch.tensor([[0.0, 0.1, 0.2, 0.3], [1.0, 1.0, 1.0, 1.0]])
-    s = _profile_summary(vals)
+    s = _summarise(vals)
     assert s['near']['mean'] == pytest.approx(0.15)
     assert s['near']['max'] == pytest.approx(0.3)
     assert s['far'] == {'mean': 1.0, 'p95': 1.0, 'max': 1.0}

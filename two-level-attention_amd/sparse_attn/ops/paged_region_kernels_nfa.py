@@ -28,52 +28,37 @@ def nfa_args(subspace='tail'):
         '--nfa_far_skip_cache', 'retain'])
 
 
-def _protected_selection_batch(lengths, indexer, capacity):
-    """Fixed-width sink + SWA id rows and counts for ``lengths`` [B].
-
-    Width depends only on the configuration and capacity (never on live
-    lengths), so captured graphs keep their shapes.  Columns past the count
-    hold 0.
-    """
-    if lengths.ndim != 1:
-        raise ValueError('protected selection lengths must be [B]')
-    device = lengths.device
-    batch = lengths.numel()
-    length = lengths.to(torch.long)
-    width = min(int(capacity), int(indexer.sink_tokens + indexer.sliding_window_size))
-    if width == 0:
-        return (torch.zeros((batch, 0), dtype=torch.int32, device=device),
-                torch.zeros((batch,), dtype=torch.int32, device=device))
-    col = torch.arange(width, dtype=torch.long, device=device)
-    sink_count = torch.clamp(length, max=indexer.sink_tokens)
-    total = torch.clamp(length, max=indexer.sink_tokens + indexer.sliding_window_size)
-    in_sink = col[None, :] < sink_count[:, None]
-    in_swa = (col[None, :] >= sink_count[:, None]) & (col[None, :] < total[:, None])
-    swa_id = (length[:, None] - indexer.sliding_window_size
-              + col[None, :] - sink_count[:, None])
-    ids = torch.where(in_sink, col[None, :].expand(batch, -1),
-                      torch.where(in_swa, swa_id, torch.zeros_like(swa_id)))
-    return ids.to(torch.int32), total.to(torch.int32)
-
-
 def split_gather_buffers(cache, layer_idx, batch):
-    """Fixed-address protected / middle gather buffers (no capture alloc)."""
-    ws = getattr(cache, '_nfa_selector_workspace', None)
-    if ws is None:
-        ws = cache._nfa_selector_workspace = {}
-    key = ('split_gather_buffers', layer_idx, batch, cache.active_visible_bucket)
-    bufs = ws.get(key)
-    if bufs is None:
+    """Fixed-address gather rows and visible lengths of the protected and the
+    middle selection of ``layer_idx``: ``(prot_gather, prot_lens,
+    mid_gather, mid_lens)``, shaped ``[batch, HKV, W]`` / ``[batch, HKV]``
+    for the active visible bucket ``W``.
+
+    Each layer owns one int32 arena sized for the cache's largest batch and
+    visible length; every (batch, bucket) shape is a contiguous prefix view
+    of it, so the addresses a captured graph holds stay valid and no shape
+    allocates again.  The arena is created by the first (eager) call.
+    """
+    arenas = cache.__dict__.setdefault('_nfa_split_arenas', {})
+    arena = arenas.get(layer_idx)
+    layer = cache.layers[layer_idx]
+    hkv = layer.num_kv_heads
+    rows = cache.max_requests * hkv
+    if arena is None:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError('split gather buffers must be warmed before capture')
-        layer = cache.layers[layer_idx]
-        shape = (batch, layer.num_kv_heads, cache.active_visible_bucket)
-        bufs = (torch.empty((2,) + shape, dtype=torch.int32,
-                            device=layer.kv_pool_k.device),
-                torch.empty((2, batch, layer.num_kv_heads), dtype=torch.int32,
-                            device=layer.kv_pool_k.device))
-        ws[key] = bufs
-    return bufs[0][0], bufs[1][0], bufs[0][1], bufs[1][1]
+        arena = (torch.empty((2, rows * cache.max_visible_len), dtype=torch.int32,
+                             device=layer.kv_pool_k.device),
+                 torch.empty((2, rows), dtype=torch.int32,
+                             device=layer.kv_pool_k.device))
+        arenas[layer_idx] = arena
+    width = cache.active_visible_bucket
+    if batch > cache.max_requests:
+        raise ValueError('split gather batch exceeds the cache request capacity')
+    n = batch * hkv
+    slots, lens = arena
+    return (slots[0, :n * width].view(batch, hkv, width), lens[0, :n].view(batch, hkv),
+            slots[1, :n * width].view(batch, hkv, width), lens[1, :n].view(batch, hkv))
 
 
 def build_protected_gather(cache, layer_idx, indexer, gather_out, vis_out):

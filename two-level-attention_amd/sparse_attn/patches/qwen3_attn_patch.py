@@ -113,7 +113,7 @@ def disjoint_regions_attention(module, q_flat, key_states, value_states, cache,
     cache.write_decode(layer_idx, key_states, value_states, slot_mapping)
     prot_gather, prot_lens, mid_gather, mid_lens = split_gather_buffers(
         cache, layer_idx, batch)
-    workspace = cache._nfa_selector_workspace
+    workspace = cache.__dict__.setdefault('_nfa_selector_workspace', {})
     q_flat = q_flat if q_flat.is_contiguous() else q_flat.contiguous()
     layer = cache.layers[layer_idx]
 
