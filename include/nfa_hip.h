@@ -51,6 +51,9 @@ extern "C" {
 /* L1 score sources (--nfa_far_method / --nfa_near_method) */
 #define NFA_METHOD_MINMAX 0
 #define NFA_METHOD_AVG 1
+#define NFA_METHOD_AVG_TOP2 2   /* far pool only: mean of the two largest
+                                   per-head page means (needs a GQA group of
+                                   at least 2) */
 
 /*
  * One selector call over B batch rows for one layer.  Mirrors the arguments

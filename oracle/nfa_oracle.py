@@ -244,6 +244,31 @@ def prepare_q(cfg: NfaConfig, q_row, dims):
     return bf16r((q * F32(cfg.scale)).astype(F32))
 
 
+def prepare_q_unrounded(cfg: NfaConfig, q_row, dims):
+    """q_u[h, d] = f32(q[h, dims[d]]) * scale, not rounded: the query of the
+    avg_top2 far scores (``selector:2936-2938``, ``round_bf16=False``)."""
+    q = np.asarray(q_row, dtype=np.float32)[:, np.asarray(dims)]
+    return (q * F32(cfg.scale)).astype(F32)
+
+
+def top2_values(values):
+    """The two largest of ``values`` [G, n] along axis 0 in torch.topk's
+    value order (NaN above everything, +0 above -0), by the sequential
+    update of ``selector:284-331`` with the comparison of ``:162-172``."""
+    def greater(v, o):
+        vn, on = np.isnan(v), np.isnan(o)
+        pz_nz = (v == 0) & (o == 0) & ~np.signbit(v) & np.signbit(o)
+        return (vn & ~on) | (~vn & ~on & ((v > o) | pz_nz))
+    t1 = np.full(values.shape[1], -np.inf, dtype=np.float32)
+    t2 = t1.copy()
+    for v in values:
+        take = greater(v, t1)
+        second = np.where(take, t1, v)
+        t1 = np.where(take, v, t1)
+        t2 = np.where(greater(second, t2), second, t2)
+    return t1, t2
+
+
 def prepare_q_grouped(cfg: NfaConfig, q_row):
     """q_fine[kv, d] = sum_j bf16r(q[kv*G+j, fine_dims[d]] * scale)."""
     qf = prepare_q(cfg, q_row, cfg.fine_dims)
@@ -308,6 +333,23 @@ def l1_pools(cfg: NfaConfig, length, skip_far, skip_near):
     return far_pool & block_valid, near_pool & block_valid, geo
 
 
+def l1_top2_scores(cfg: NfaConfig, ksum, q_full_group, q_unrounded_group):
+    """avg_top2 far scores (``selector:2412-2427``): per head the bf16 page
+    mean against the unrounded query, the two largest heads averaged and
+    rounded to bf16 -- where the same score against the bf16-rounded query
+    (the score the reference's kernel writes first) is finite; elsewhere
+    that value stands."""
+    kavg = bf16r((ksum / F32(cfg.bs)).astype(F32))
+    with np.errstate(invalid='ignore', over='ignore'):
+        rounded = np.stack([bf16r(seq_dot(kavg, q[None, :])) for q in q_full_group])
+        exact = np.stack([bf16r(seq_dot(kavg, q[None, :])) for q in q_unrounded_group])
+        r1, r2 = top2_values(rounded)
+        u1, u2 = top2_values(exact)
+        kernel = bf16r(((r1 + r2).astype(F32) / F32(2)).astype(F32))
+        host = bf16r(((u1 + u2).astype(F32) / F32(2)).astype(F32))
+    return bf16_bits(np.where(np.isfinite(kernel), host, kernel))
+
+
 def l1_page_scores(cfg: NfaConfig, kmin, kmax, ksum, q_full_group):
     """Per-page minmax and avg scores for one kv group (bf16 values as fp32).
 
@@ -335,15 +377,17 @@ def l1_page_scores(cfg: NfaConfig, kmin, kmax, ksum, q_full_group):
 
 
 def l1_scores(cfg: NfaConfig, k_pool, bt_row, length, kv, q_full,
-              skip_far, skip_near):
+              skip_far, skip_near, q_unrounded=None):
     """far/near bf16 score bits over pages [0, kt_eff) for one (row, kv)."""
-    if cfg.far_method not in ('minmax', 'avg'):
-        raise NotImplementedError('avg_top2 far scores are not restated')
     far_pool, near_pool, geo = l1_pools(cfg, length, skip_far, skip_near)
     kmin, kmax, ksum = page_stats(cfg, k_pool, bt_row, length, kv)
     g = cfg.group
     mm, avg = l1_page_scores(cfg, kmin, kmax, ksum, q_full[kv * g:(kv + 1) * g])
-    far_val = mm if cfg.far_method == 'minmax' else avg
+    if cfg.far_method == 'avg_top2':
+        far_val = l1_top2_scores(cfg, ksum, q_full[kv * g:(kv + 1) * g],
+                                 q_unrounded[kv * g:(kv + 1) * g])
+    else:
+        far_val = mm if cfg.far_method == 'minmax' else avg
     near_val = avg if cfg.near_method == 'avg' else mm
     far = np.where(far_pool, far_val, NEG_INF_BITS).astype(np.uint16)
     near = np.where(near_pool, near_val, NEG_INF_BITS).astype(np.uint16)
@@ -700,8 +744,9 @@ def select_row(cfg: NfaConfig, k_pool, bt_row, length, q_row, kv,
         return res
     q_full = prepare_q(cfg, q_row, cfg.dims)
     q_fine = prepare_q_grouped(cfg, q_row)
+    q_unrounded = prepare_q_unrounded(cfg, q_row, cfg.dims)
     far, near, geo = l1_scores(cfg, k_pool, bt_row, length, kv, q_full,
-                               skip_far, skip_near)
+                               skip_far, skip_near, q_unrounded)
     res.far, res.near = far, near
     kt = cfg.kt_cap
     res.i_f = l1_topk(far, 0, geo.far_end, cfg.k_f, kt)

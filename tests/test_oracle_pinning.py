@@ -168,6 +168,62 @@ def test_l1_page_scores_exact_integers():
     np.testing.assert_array_equal(avg.astype(np.int64), exp_avg)
 
 
+def _torch_top2_reference(kavg, q_rows, bs_unused=None):
+    """The reference's avg_top2 formula evaluated by torch: per-head bf16
+    page means (einsum, then bf16), the top-2 values over the heads,
+    their bf16 mean."""
+    avg = torch.einsum('hd,td->ht', torch.from_numpy(q_rows), torch.from_numpy(kavg))
+    avg = avg.to(torch.bfloat16)
+    return avg.topk(2, dim=0).values.mean(dim=0)
+
+
+def test_avg_top2_far_scores_match_torch():
+    """avg_top2: the oracle's sequential restatement equals torch's own
+    evaluation of the reference formula on inputs whose dot products are
+    exact in fp32 (so the summation order cannot matter), with unrounded
+    query values that bf16 cannot hold -- the score must come from the
+    unrounded query -- plus pages whose rounded-query score is non-finite
+    (that value stands) and all-tied heads."""
+    rng = np.random.default_rng(16)
+    cfg = _cfg(bs=4, dims=np.arange(8), far_method='avg_top2')
+    g = cfg.group
+    n = 400
+    ksum = (4 * rng.integers(-15, 16, (n, 8))).astype(F32)       # kavg in [-15, 15]
+    q_u = (rng.integers(-2048, 2049, (g, 8)) / 256.0).astype(F32)  # 12-bit values
+    q_r = orc.bf16r(q_u)
+    assert not np.array_equal(q_r, q_u)
+    ksum[5] = 0.0                          # every head ties at +0
+    ksum[7, 3] = np.inf                    # rounded-query score +-inf or NaN
+    ksum[9, 0] = np.nan
+    got = orc.l1_top2_scores(cfg, ksum, q_r, q_u).astype(np.int64)
+    kavg = orc.bf16r(ksum / F32(4))
+    with np.errstate(invalid='ignore'):
+        exact = _torch_top2_reference(kavg, q_u)
+        kernel = _torch_top2_reference(kavg, q_r)
+    want = torch.where(torch.isfinite(kernel), exact, kernel)
+    want_bits = want.view(torch.int16).numpy().astype(np.int64) & 0xFFFF
+    nan = np.isnan(want.float().numpy())
+    np.testing.assert_array_equal(got[~nan], want_bits[~nan])
+    assert (got[nan] == orc.NAN_BITS).all() and nan[9]
+    # the unrounded query decides: it differs from the rounded one somewhere
+    assert not torch.equal(exact, kernel)
+    # a planted slip (the rounded query everywhere) is caught
+    slip = orc.l1_top2_scores(cfg, ksum, q_r, q_r).astype(np.int64)
+    assert (slip[~nan] != want_bits[~nan]).any()
+
+
+def test_top2_values_order_nan_and_signed_zero():
+    v = np.array([[1.0, np.nan, 0.0, -0.0, -np.inf],
+                  [3.0, 2.0, -0.0, -0.0, -np.inf],
+                  [2.0, 5.0, -1.0, 0.0, -np.inf]], dtype=F32)
+    t1, t2 = orc.top2_values(v)
+    assert t1[0] == 3.0 and t2[0] == 2.0
+    assert np.isnan(t1[1]) and t2[1] == 5.0
+    assert t1[2] == 0.0 and not np.signbit(t1[2]) and t2[2] == 0.0 and np.signbit(t2[2])
+    assert t1[3] == 0.0 and not np.signbit(t1[3])
+    assert t1[4] == -np.inf and t2[4] == -np.inf
+
+
 def test_l1_topk_brute_force():
     rng = np.random.default_rng(7)
     for trial in range(200):

@@ -307,3 +307,28 @@ def test_short_contexts_below_window():
     q = bf16_randn((4, cache.num_query_heads, 128), gen, DEV)
     decode = _decode_inputs(cache, 4, gen, torch.bfloat16)
     run_and_compare(cache, indexer, req_ids, q, decode)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+def test_avg_top2_far_scores(dtype):
+    """--nfa_far_method avg_top2 (selector:2412-2427): far scores from the two
+    largest per-head page means against the unrounded query, bit-exact with
+    the oracle in the staged bf16 path and the fp32 statistics path."""
+    cache, gen, req_ids = _prod_cache([20000, 9001], dtype=dtype)
+    indexer = make_indexer(far_method='avg_top2')
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = bf16_randn((2, cache.num_query_heads, 128), gen, DEV).to(dtype)
+    decode = _decode_inputs(cache, 2, gen, dtype)
+    run_and_compare(cache, indexer, req_ids, q, decode, scaling=0.08838834764831845)
+
+
+def test_avg_top2_needs_two_heads_per_group():
+    cache, gen, req_ids = _prod_cache([3000], hkv=2, hq=2)
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = bf16_randn((1, 2, 128), gen, DEV)
+    with pytest.raises(ValueError, match='avg_top2'):
+        select_topk_for_layer_batched(
+            cache, 0, req_ids, q,
+            attention=attention_ns(make_indexer(far_method='avg_top2'), 1.0))

@@ -72,7 +72,7 @@ struct SelDims {
   int lds;        // LDS bytes per workgroup
   // LDS: a common part, then the tile part, or the tail: its candidate pages,
   // then its L1 part or (later) its L2 part
-  int a_hist, a_tmp, a_misc, a_clk, a_qf, a_qs, a_qg, a_fdims;
+  int a_hist, a_tmp, a_misc, a_clk, a_qf, a_qs, a_qu, a_qg, a_fdims;
   int a_dims, a_last, a_tphys, a_stage, a_hs, a_st;    // tile
   int a_pages, a_pphys;                                // tail
   int a_keys, a_dbf, a_dbn, a_dsel;                    // tail, L1
@@ -129,6 +129,8 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   s.a_clk = o;   o += 8 * 64;  // debug timeline: tile marks, tail marks
   s.a_qf = o;    o += align16(4 * group * p.dsub);
   s.a_qs = o;    o += align16(4 * group * 2 * p.dsub);  // min(q,0) | max(q,0)
+  s.a_qu = o;    // unrounded scaled query rows (avg_top2 far scores)
+  if (p.far_method == NFA_METHOD_AVG_TOP2) o += align16(4 * group * p.dsub);
   s.a_qg = o;    o += align16(4 * p.fine_dsub);          // grouped L2 query
   s.a_fdims = o; o += align16(4 * p.fine_dsub);
   const int a_base = o;
@@ -744,10 +746,12 @@ static_assert(GMAX * kSpanMax * 4 <= 4 * SB * kStatTokens,
 // ascending d with separately rounded products.
 __device__ __forceinline__ void l1_heads_staged(const uint4 *st, const float *qs0,
                                                 const float *qs1, const float *qf0,
-                                                const float *qf1, bool need_mm,
-                                                int bs, float *out0, float *out1) {
+                                                const float *qf1, const float *qu0,
+                                                const float *qu1, bool need_mm,
+                                                int bs, float *out0, float *out1,
+                                                float *un0, float *un1) {
   constexpr int NC = 32 / 8;
-  float r0, r1;
+  float r0, r1, su0 = 0.0f, su1 = 0.0f;
   if (need_mm) {
     float sn0 = 0.0f, sp0 = 0.0f, sn1 = 0.0f, sp1 = 0.0f;
 #pragma unroll
@@ -799,12 +803,26 @@ __device__ __forceinline__ void l1_heads_staged(const uint4 *st, const float *qs
         sa0 = sa0 + a0;
         sa1 = sa1 + a1;
       }
+      if (qu0 != nullptr) {
+        // the same page mean against the unrounded query rows
+        load_f8(qu0 + c * 8, q0);
+        load_f8(qu1 + c * 8, q1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float a0 = k[e] * q0[e];
+          const float a1 = k[e] * q1[e];
+          su0 = su0 + a0;
+          su1 = su1 + a1;
+        }
+      }
     }
     r0 = sa0;
     r1 = sa1;
   }
   *out0 = bf16r(r0);
   *out1 = bf16r(r1);
+  *un0 = bf16r(su0);
+  *un1 = bf16r(su1);
 }
 
 // Same arithmetic with the statistics read chunk by chunk from memory (L1
@@ -812,15 +830,16 @@ __device__ __forceinline__ void l1_heads_staged(const uint4 *st, const float *qs
 template <int DSUB, typename KV>
 __device__ __forceinline__ void l1_head_mem(const NfaSelectParams &p,
                                             int64_t req, int kv, int t,
-                                            const float *q, bool need_mm,
-                                            bool need_avg, const float *s_last,
-                                            float *mm, float *avg) {
+                                            const float *q, const float *qu,
+                                            bool need_mm, bool need_avg,
+                                            const float *s_last, float *mm,
+                                            float *avg, float *avg_u) {
   constexpr int CH = Elem<KV>::kChunk;
   const KV *smin = (const KV *)p.stat_min_l;
   const KV *smax = (const KV *)p.stat_max_l;
   const KV *ssum = (const KV *)p.stat_sum_l;
   const float bsf = (float)p.bs;
-  float sn = 0.0f, sp = 0.0f, sa = 0.0f;
+  float sn = 0.0f, sp = 0.0f, sa = 0.0f, su = 0.0f;
   for (int c = 0; c < DSUB / CH; ++c) {
     float kmin[CH], kmax[CH], ks[CH];
     if (s_last != nullptr) {
@@ -850,13 +869,52 @@ __device__ __forceinline__ void l1_head_mem(const NfaSelectParams &p,
         sp = sp + b;
       }
       if (need_avg) {
-        const float a = bf16r(ks[e] / bsf) * qd;
+        const float kavg = bf16r(ks[e] / bsf);
+        const float a = kavg * qd;
         sa = sa + a;
+        if (qu != nullptr) {
+          const float b = kavg * qu[c * CH + e];
+          su = su + b;
+        }
       }
     }
   }
   if (need_mm) *mm = bf16r(sn + sp);
   if (need_avg) *avg = bf16r(sa);
+  if (need_avg && qu != nullptr) *avg_u = bf16r(su);
+}
+
+// torch.topk's value order: NaN above everything, +0 above -0.
+__device__ __forceinline__ bool score_greater(float v, float o) {
+  const bool vn = v != v, on = o != o;
+  const bool pz_over_nz = v == 0.0f && o == 0.0f && !signbit(v) && signbit(o);
+  return (vn && !on) || (!vn && !on && (v > o || pz_over_nz));
+}
+
+// avg_top2 far score of one page (selector:2412-2427, top-2 order :162-172):
+// the mean of the two largest per-head bf16 page means against the
+// unrounded scaled query, used where the same mean against the bf16-rounded
+// query is finite (elsewhere that value stands).  `hs` holds, per head at
+// a kSpanMax stride, (rounded-query bf16 << 16) | unrounded-query bf16.
+__device__ __forceinline__ uint16_t top2_far_score(const float *hs, int G) {
+  const float ninf = -__builtin_inff();
+  float r1 = ninf, r2 = ninf, u1 = ninf, u2 = ninf;
+  for (int j = 0; j < G; ++j) {
+    const uint32_t w = __float_as_uint(hs[j * kSpanMax]);
+    const float r = bf16_val((uint16_t)(w >> 16));
+    const float u = bf16_val((uint16_t)(w & 0xFFFFu));
+    const bool tr = score_greater(r, r1);
+    const float rs = tr ? r1 : r;
+    r1 = tr ? r : r1;
+    r2 = score_greater(rs, r2) ? rs : r2;
+    const bool tu = score_greater(u, u1);
+    const float us = tu ? u1 : u;
+    u1 = tu ? u : u1;
+    u2 = score_greater(us, u2) ? us : u2;
+  }
+  const float kr = bf16r((r1 + r2) / 2.0f);
+  if (!isfinite(kr)) return bf16_bits(kr);
+  return bf16_bits((u1 + u2) / 2.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1237,6 +1295,9 @@ __global__ void __launch_bounds__(SB)
   int *s_misc = (int *)(smem + sd.a_misc);
   float *s_qf = (float *)(smem + sd.a_qf);
   float *s_qs = (float *)(smem + sd.a_qs);
+  float *s_qu = (float *)(smem + sd.a_qu);
+  // avg_top2 far scores (selector:2412-2427) also need the unrounded query
+  const bool top2 = p.far_method == NFA_METHOD_AVG_TOP2;
   float *s_qg = (float *)(smem + sd.a_qg);
   int *s_fdims = (int *)(smem + sd.a_fdims);
   int *s_dims = (int *)(smem + sd.a_dims);
@@ -1340,6 +1401,7 @@ __global__ void __launch_bounds__(SB)
     s_qf[i] = qr;
     s_qs[j * 2 * DSUB + d] = qr < 0.0f ? qr : 0.0f;
     s_qs[j * 2 * DSUB + DSUB + d] = qr > 0.0f ? qr : 0.0f;
+    if (top2) s_qu[i] = s_qraw[j * hd + s_dims[d]] * p.scale;
   }
   // grouped L2 query (selector:979-1002): bf16 terms summed in head order
   for (int d = tid; d < p.fine_dsub; d += SB) {
@@ -1519,23 +1581,34 @@ __global__ void __launch_bounds__(SB)
         if (!(fp || np)) continue;
         const bool need_mm = (fp && far_mm) || (np && near_mm);
         const bool need_avg = !need_mm;
-        float h0 = 0.0f, h1 = 0.0f;
+        // avg_top2 far pages: both head means, against the rounded and the
+        // unrounded query, packed as two bf16 patterns in the head's slot
+        const bool pair = top2 && fp;
+        float h0 = 0.0f, h1 = 0.0f, u0 = 0.0f, u1 = 0.0f;
         if constexpr (STG) {
           // a missing second head scores the first one again, discarded
           const int j1s = j1 < G ? j1 : j0;
           l1_heads_staged(reinterpret_cast<const uint4 *>(s_st) + lp,
                           s_qs + j0 * 2 * DSUB, s_qs + j1s * 2 * DSUB,
-                          s_qf + j0 * DSUB, s_qf + j1s * DSUB, need_mm, bs, &h0, &h1);
+                          s_qf + j0 * DSUB, s_qf + j1s * DSUB,
+                          pair ? s_qu + j0 * DSUB : nullptr, s_qu + j1s * DSUB,
+                          need_mm, bs, &h0, &h1, &u0, &u1);
         } else {
           const bool from_lds = incremental && t == last_blk;
           float m0 = 0.0f, a0 = 0.0f, m1 = 0.0f, a1 = 0.0f;
-          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j0 * DSUB, need_mm, need_avg,
-                                from_lds ? s_last : nullptr, &m0, &a0);
+          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j0 * DSUB,
+                                pair ? s_qu + j0 * DSUB : nullptr, need_mm, need_avg,
+                                from_lds ? s_last : nullptr, &m0, &a0, &u0);
           if (j1 < G)
-            l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j1 * DSUB, need_mm,
-                                  need_avg, from_lds ? s_last : nullptr, &m1, &a1);
+            l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j1 * DSUB,
+                                  pair ? s_qu + j1 * DSUB : nullptr, need_mm,
+                                  need_avg, from_lds ? s_last : nullptr, &m1, &a1, &u1);
           h0 = need_mm ? m0 : a0;
           h1 = need_mm ? m1 : a1;
+        }
+        if (pair) {
+          h0 = __uint_as_float(((uint32_t)bf16_bits(h0) << 16) | bf16_bits(u0));
+          h1 = __uint_as_float(((uint32_t)bf16_bits(h1) << 16) | bf16_bits(u1));
         }
         s_hs[j0 * kSpanMax + lp] = h0;
         if (j1 < G) s_hs[j1 * kSpanMax + lp] = h1;
@@ -1552,7 +1625,9 @@ __global__ void __launch_bounds__(SB)
         bool fp = false, np = false;
         if (do_stats) pools(p, geo, t, &fp, &np);
         uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
-        if (fp || np) {
+        if (NFA_COLD(top2 && fp)) {
+          far_bits = top2_far_score(s_hs + lp, G);
+        } else if (fp || np) {
           // bf16 head scores summed in head order
           float acc = 0.0f;
           for (int j = 0; j < G; ++j) acc = acc + s_hs[j * kSpanMax + lp];
@@ -2235,6 +2310,14 @@ static int select_check(const NfaSelectParams *p, bool need_workspace) {
   if (p->batch <= 0 || p->hkv <= 0 || p->hq % p->hkv != 0 ||
       p->hq / p->hkv > nfa::GMAX) {
     nfa_set_error("nfa_select_layer: unsupported heads hq=%d hkv=%d", p->hq, p->hkv);
+    return NFA_EINVAL;
+  }
+  if (p->far_method < NFA_METHOD_MINMAX || p->far_method > NFA_METHOD_AVG_TOP2 ||
+      p->near_method < NFA_METHOD_MINMAX || p->near_method > NFA_METHOD_AVG ||
+      (p->far_method == NFA_METHOD_AVG_TOP2 && p->hq / p->hkv < 2)) {
+    nfa_set_error("nfa_select_layer: unsupported L1 methods far=%d near=%d "
+                  "(avg_top2 needs 2+ query heads per kv head)",
+                  p->far_method, p->near_method);
     return NFA_EINVAL;
   }
   if (!(p->dsub == 32 || p->dsub == 64 || p->dsub == 128)) {

@@ -23,6 +23,7 @@ DTYPE_BF16 = 0
 DTYPE_F32 = 1
 METHOD_MINMAX = 0
 METHOD_AVG = 1
+METHOD_AVG_TOP2 = 2
 
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64

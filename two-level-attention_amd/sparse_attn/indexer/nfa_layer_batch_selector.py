@@ -27,6 +27,8 @@ class FallbackRequired(Exception):
 
 
 _GMAX = 8
+_FAR_METHODS = {'minmax': nat.METHOD_MINMAX, 'avg': nat.METHOD_AVG,
+                'avg_top2': nat.METHOD_AVG_TOP2}
 
 
 def _dims_for(indexer, device, head_dim):
@@ -190,8 +192,12 @@ def select_layer_params(cache, layer_idx, req_ids, query_states,
                          f'layer, got {tuple(query_states.shape)}')
     if hq % hkv or hq // hkv > _GMAX:
         raise FallbackRequired(f'unsupported GQA group {hq}/{hkv}')
-    if indexer.far_method not in ('minmax', 'avg'):
+    if indexer.far_method not in _FAR_METHODS:
         raise FallbackRequired(f'far method {indexer.far_method} is not supported')
+    if indexer.far_method == 'avg_top2' and hq // hkv < 2:
+        # the reference takes torch.topk(2) over the group's heads
+        raise ValueError('nfa_far_method avg_top2 needs at least 2 query heads '
+                         f'per kv head, got {hq}/{hkv}')
     if query_states.stride(-1) != 1:
         query_states = query_states.contiguous()
     device = layer0.kv_pool_k.device
@@ -247,8 +253,7 @@ def select_layer_params(cache, layer_idx, req_ids, query_states,
     p.near_len = int(indexer.nt_near_len)
     p.k_f, p.k_n, p.k2 = k_f, k_n, k2
     p.near_tokens = -1 if indexer.nt_near_tokens is None else int(indexer.nt_near_tokens)
-    p.far_method = (nat.METHOD_MINMAX if indexer.far_method == 'minmax'
-                    else nat.METHOD_AVG)
+    p.far_method = _FAR_METHODS[indexer.far_method]
     p.near_method = (nat.METHOD_MINMAX if indexer.near_method == 'minmax'
                      else nat.METHOD_AVG)
     p.dsub, p.fine_dsub = l1_dims.numel(), fine_dims.numel()
