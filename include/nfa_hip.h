@@ -160,8 +160,9 @@ typedef struct NfaAttnParams {
   int32_t abi_version;
   int32_t struct_size;
   int32_t total_q;            /* T query rows */
-  int32_t hq, hkv, head_dim, head_dim_v, page;  /* head_dim_v == head_dim,
-                                 spanning 8, 16 or 32 chunks of 16 bytes */
+  int32_t hq, hkv, head_dim, head_dim_v, page;  /* K and V row widths, each
+                                 8, 16, 24 or 32 chunks of 16 bytes (bf16:
+                                 64/128/192/256 dims; fp32: 32 to 128) */
   int32_t gather_rows;        /* rows of gather / vis_lens */
   int32_t max_vis;
   int32_t kv_dtype, q_dtype;  /* output dtype == q dtype */

@@ -18,10 +18,10 @@ GEO = RegionGeometry(sink=4, near=4096, window=128, page=16, max_new_tokens=64)
 
 
 def _setup(dtype, hkv=8, hq=32, max_vis=1024, rows=3, pages=400, seed=7,
-           head_dim=128):
+           head_dim=128, head_dim_v=None):
     cache = make_cache(DEV, geometry=GEO, max_blocks=64, max_physical_pages=pages,
                        max_visible_len=max_vis, hkv=hkv, hq=hq, dtype=dtype,
-                       max_requests=rows, head_dim=head_dim)
+                       max_requests=rows, head_dim=head_dim, head_dim_v=head_dim_v)
     gen = torch.Generator(device=DEV).manual_seed(seed)
     layer = cache.layers[0]
     layer.kv_pool_k.copy_(bf16_randn(layer.kv_pool_k.shape, gen, DEV).to(dtype))
@@ -119,3 +119,22 @@ def test_many_rows_one_workgroup_each():
     q2r = torch.arange(64, dtype=torch.int32, device=DEV)
     got = _check(cache, q, gather, lens, q2r, 128 ** -0.5, dtype)
     assert np.all(got[1, 4:8] == 0)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('dims', [(192, 128), (64, 256), (256, 64)])
+def test_key_and_value_widths_differ(dtype, dims):
+    """K and V rows of different widths: DeepSeek-V2's expanded heads (192 /
+    128, one kv head per query head) and the other extremes the kernel
+    takes; fp32 caps rows at 128 dims (32 chunks of 16 bytes)."""
+    dk, dv = dims
+    if dtype == torch.float32 and max(dk, dv) > 128:
+        dk, dv = dk // 2, dv // 2
+    cache, gen, gather = _setup(dtype, rows=2, hkv=16, hq=16, max_vis=1024,
+                                pages=400, head_dim=dk, head_dim_v=dv)
+    lens = torch.full((2, 16), 1024, dtype=torch.int32, device=DEV)
+    lens[1, :8] = 333
+    q = bf16_randn((2, 16, dk), gen, DEV).to(dtype)
+    q2r = torch.tensor([0, 1], dtype=torch.int32, device=DEV)
+    got = _check(cache, q, gather, lens, q2r, dk ** -0.5, dtype)
+    assert got.shape == (2, 16, dv)

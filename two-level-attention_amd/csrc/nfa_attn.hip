@@ -12,10 +12,12 @@
 // the (row, kv) to arrive -- device-scope atomic counter, no waiting --
 // merges the partials and writes the output in the query dtype.
 //
-// Row layout: TPR threads share a K/V row, one 16-byte chunk each, so a pass
-// of the 256 threads covers 256 / TPR rows and every K and V chunk of the
+// Row layout: kTpr = 8 threads share a K/V row, each holding CK 16-byte
+// chunks of the K row and CV of the V row (K and V widths are independent:
+// 64 to 256 dims, e.g. 192 / 128 for DeepSeek-V2's expanded heads), so a
+// pass of the 256 threads covers 32 rows and every K and V chunk of the
 // split is requested before the first one is used.  Scores reduce over the
-// TPR threads with lane shuffles; V rows are staged in LDS and P.V runs with
+// 8 threads with lane shuffles; V rows are staged in LDS and P.V runs with
 // one thread per (head, dim pair).  All loops are rolled or short: the code
 // a workgroup executes stays a few KB, so instruction fetch does not become
 // the latency of the launch.
@@ -24,6 +26,7 @@
 namespace nfa {
 
 constexpr int AGMAX = 8;         // query heads per kv head
+constexpr int kTpr = 8;          // threads per K/V row
 constexpr int kSplitMax = 64;    // tokens per workgroup
 constexpr int kMaxSplits = 256;  // splits merged in LDS
 
@@ -100,12 +103,13 @@ __device__ __forceinline__ void lds_pair(const float *v, int d, float *a,
 // row's nb = ceil(n / block_tokens) token blocks -- with its own chunks and
 // split workgroups; the merge stores the unnormalised state (acc, m, z)
 // into the caller's buffers instead of the output.
-template <typename KV, int TPR, bool LOOP, bool PART = false>
+template <typename KV, int CK, int CV, bool LOOP, bool PART = false>
 __global__ void __launch_bounds__(NFA_BLOCK)
     nfa_attn_kernel(const NfaAttnParams p, int cus, const NfaAttnPartial pt) {
   constexpr int CH = Elem<KV>::kChunk;  // dims per 16-byte chunk
-  constexpr int D = TPR * CH;           // head dim (K and V)
-  constexpr int RPP = NFA_BLOCK / TPR;  // rows per pass
+  constexpr int DK = kTpr * CK * CH;    // K head dim
+  constexpr int D = kTpr * CV * CH;     // V head dim
+  constexpr int RPP = NFA_BLOCK / kTpr; // rows per pass
   constexpr int PMAX = kSplitMax / RPP; // passes per split
   const AttnDims ad = PART ? attn_dims(p, cus, pt.nsplit, part_span(p, pt))
                            : attn_dims(p, cus);
@@ -121,7 +125,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int G = p.hq / p.hkv;
   const float kNegInf = __uint_as_float(0xFF800000u);
 
-  __shared__ __align__(16) float s_q[AGMAX * D];
+  __shared__ __align__(16) float s_q[AGMAX * DK];
   __shared__ float s_p[AGMAX * kSplitMax];  // scores, then exp weights
   __shared__ int s_slot[kSplitMax];
   __shared__ __align__(16) KV s_v[kSplitMax * D];
@@ -154,8 +158,8 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int c_first = lo + split * ad.split;
   const int c_step = ad.nsplit * ad.split;
   if (c_first < c_end) {
-    for (int i = tid; i < G * D; i += NFA_BLOCK)
-      s_q[i] = load_any(p.q, ((int64_t)t * p.hq + kh * G) * D + i, p.q_dtype);
+    for (int i = tid; i < G * DK; i += NFA_BLOCK)
+      s_q[i] = load_any(p.q, ((int64_t)t * p.hq + kh * G) * DK + i, p.q_dtype);
   }
   if (tid < G) {
     s_m[tid] = kNegInf;
@@ -170,8 +174,8 @@ __global__ void __launch_bounds__(NFA_BLOCK)
                                  : nullptr;
   // slots outside the arena are skipped like negative ones
   const int max_slot = p.pool_pages * p.page;
-  const int sc = tid % TPR;  // chunk of the row
-  const int rr = tid / TPR;  // row within a pass
+  const int sc = tid % kTpr;  // this thread's chunks of the row: sc, sc + 8, ...
+  const int rr = tid / kTpr;  // row within a pass
   const KV *kpool = (const KV *)p.k_pool;
   const KV *vpool = (const KV *)p.v_pool;
   for (int c0 = c_first; c0 < c_end; c0 += c_step) {
@@ -184,36 +188,44 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     __syncthreads();
 
     // every K and V chunk of the split in flight at once
-    uint4 kr[PMAX], vr[PMAX];
+    uint4 kr[PMAX][CK], vr[PMAX][CV];
 #pragma unroll
     for (int pp = 0; pp < PMAX; ++pp) {
       const int j = pp * RPP + rr;
       const int slot = j < cn ? s_slot[j] : -1;
-      kr[pp] = make_uint4(0u, 0u, 0u, 0u);
-      vr[pp] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int c = 0; c < CK; ++c) kr[pp][c] = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+      for (int c = 0; c < CV; ++c) vr[pp][c] = make_uint4(0u, 0u, 0u, 0u);
       if (slot >= 0) {
-        const int64_t base =
-            (((int64_t)(slot / p.page) * p.hkv + kh) * p.page + slot % p.page) * D +
-            sc * CH;
-        kr[pp] = *reinterpret_cast<const uint4 *>(kpool + base);
-        vr[pp] = *reinterpret_cast<const uint4 *>(vpool + base);
+        const int64_t cell = ((int64_t)(slot / p.page) * p.hkv + kh) * p.page + slot % p.page;
+#pragma unroll
+        for (int c = 0; c < CK; ++c)
+          kr[pp][c] = *reinterpret_cast<const uint4 *>(kpool + cell * DK + (c * kTpr + sc) * CH);
+#pragma unroll
+        for (int c = 0; c < CV; ++c)
+          vr[pp][c] = *reinterpret_cast<const uint4 *>(vpool + cell * D + (c * kTpr + sc) * CH);
       }
     }
-    // scores: partial dot over the chunk, then a shuffle reduction over the
-    // TPR threads of the row
+    // scores: partial dot over the thread's chunks, then a shuffle
+    // reduction over the 8 threads of the row
 #pragma unroll
     for (int pp = 0; pp < PMAX; ++pp) {
       if (pp * RPP >= cn) break;
       const int j = pp * RPP + rr;
-      float x[CH];
-      unpack_chunk<KV>(kr[pp], x);
+      float x[CK][CH];
+#pragma unroll
+      for (int c = 0; c < CK; ++c) unpack_chunk<KV>(kr[pp][c], x[c]);
       for (int g = 0; g < G; ++g) {
-        const float *q = s_q + g * D + sc * CH;
         float part_s = 0.0f;
 #pragma unroll
-        for (int e = 0; e < CH; ++e) part_s = fmaf(q[e], x[e], part_s);
+        for (int c = 0; c < CK; ++c) {
+          const float *q = s_q + g * DK + (c * kTpr + sc) * CH;
 #pragma unroll
-        for (int off = 1; off < TPR; off <<= 1)
+          for (int e = 0; e < CH; ++e) part_s = fmaf(q[e], x[c][e], part_s);
+        }
+#pragma unroll
+        for (int off = 1; off < kTpr; off <<= 1)
           part_s += __shfl_xor(part_s, off, 64);
         if (sc == 0 && j < cn)
           s_p[g * kSplitMax + j] = s_slot[j] >= 0 ? part_s * p.scale : kNegInf;
@@ -223,7 +235,11 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 #pragma unroll
     for (int pp = 0; pp < PMAX; ++pp) {
       const int j = pp * RPP + rr;
-      if (j < cn) *reinterpret_cast<uint4 *>(s_v + j * D + sc * CH) = vr[pp];
+      if (j < cn) {
+#pragma unroll
+        for (int c = 0; c < CV; ++c)
+          *reinterpret_cast<uint4 *>(s_v + j * D + (c * kTpr + sc) * CH) = vr[pp][c];
+      }
     }
     __syncthreads();
 
@@ -474,6 +490,7 @@ extern "C" int64_t nfa_attn_workspace_bytes(const NfaAttnParams *p) {
 // Shared argument checks of the gather attention entry points; `tpr` gets
 // the threads per K/V row.  The output pointer is checked by the caller.
 static int32_t check_attn(const NfaAttnParams *p, const char *fn, int *tpr_out) {
+  // *tpr_out = 4 * (K chunks per thread - 1) + (V chunks per thread - 1)
   if (p == nullptr || p->abi_version != NFA_ABI_VERSION ||
       p->struct_size != (int32_t)sizeof(NfaAttnParams)) {
     nfa_set_error("%s: ABI mismatch", fn);
@@ -483,12 +500,15 @@ static int32_t check_attn(const NfaAttnParams *p, const char *fn, int *tpr_out) 
     nfa_set_error("%s: unsupported heads hq=%d hkv=%d", fn, p->hq, p->hkv);
     return NFA_EINVAL;
   }
+  // K and V rows: 8, 16, 24 or 32 chunks of 16 bytes each (64 to 256 bf16
+  // dims, 32 to 128 fp32 dims), independently
   const int chunk = p->kv_dtype == NFA_DTYPE_BF16 ? 8 : 4;
-  const int tpr = p->head_dim / chunk;
-  if (p->head_dim != p->head_dim_v || p->head_dim % chunk != 0 ||
-      !(tpr == 8 || tpr == 16 || tpr == 32)) {
+  const int ck = p->head_dim / (chunk * nfa::kTpr);
+  const int cv = p->head_dim_v / (chunk * nfa::kTpr);
+  if (p->head_dim % (chunk * nfa::kTpr) != 0 || p->head_dim_v % (chunk * nfa::kTpr) != 0 ||
+      ck < 1 || ck > 4 || cv < 1 || cv > 4) {
     nfa_set_error("%s: unsupported head dims %d/%d "
-                  "(K and V dims must match and span 8, 16 or 32 chunks of 16 bytes)",
+                  "(K and V rows must each span 8, 16, 24 or 32 chunks of 16 bytes)",
                   fn, p->head_dim, p->head_dim_v);
     return NFA_EINVAL;
   }
@@ -510,8 +530,44 @@ static int32_t check_attn(const NfaAttnParams *p, const char *fn, int *tpr_out) 
     nfa_set_error("%s: null device pointer", fn);
     return NFA_EINVAL;
   }
-  *tpr_out = tpr;
+  *tpr_out = 4 * (ck - 1) + (cv - 1);
   return NFA_OK;
+}
+
+// The kernel instance of a (K chunks, V chunks) per thread pair: `shape` =
+// 4 * (ck - 1) + (cv - 1), as check_attn reports it.
+template <typename KV, bool PART, int CK, int CV>
+static void launch_attn_cv(bool loop, dim3 grid, hipStream_t s, const NfaAttnParams &p,
+                           int cus, const NfaAttnPartial &pt) {
+  if (loop)
+    hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, CK, CV, true, PART>), grid,
+                       dim3(NFA_BLOCK), 0, s, p, cus, pt);
+  else
+    hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, CK, CV, false, PART>), grid,
+                       dim3(NFA_BLOCK), 0, s, p, cus, pt);
+}
+
+template <typename KV, bool PART, int CK>
+static void launch_attn_ck(int cv, bool loop, dim3 grid, hipStream_t s,
+                           const NfaAttnParams &p, int cus, const NfaAttnPartial &pt) {
+  switch (cv) {
+    case 1: launch_attn_cv<KV, PART, CK, 1>(loop, grid, s, p, cus, pt); break;
+    case 2: launch_attn_cv<KV, PART, CK, 2>(loop, grid, s, p, cus, pt); break;
+    case 3: launch_attn_cv<KV, PART, CK, 3>(loop, grid, s, p, cus, pt); break;
+    default: launch_attn_cv<KV, PART, CK, 4>(loop, grid, s, p, cus, pt); break;
+  }
+}
+
+template <typename KV, bool PART>
+static void launch_attn(int shape, bool loop, dim3 grid, hipStream_t s,
+                        const NfaAttnParams &p, int cus, const NfaAttnPartial &pt) {
+  const int cv = shape % 4 + 1;
+  switch (shape / 4 + 1) {
+    case 1: launch_attn_ck<KV, PART, 1>(cv, loop, grid, s, p, cus, pt); break;
+    case 2: launch_attn_ck<KV, PART, 2>(cv, loop, grid, s, p, cus, pt); break;
+    case 3: launch_attn_ck<KV, PART, 3>(cv, loop, grid, s, p, cus, pt); break;
+    default: launch_attn_ck<KV, PART, 4>(cv, loop, grid, s, p, cus, pt); break;
+  }
 }
 
 extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) {
@@ -537,23 +593,10 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
   hipStream_t s = (hipStream_t)stream;
   const bool bf = p->kv_dtype == NFA_DTYPE_BF16;
   const bool loop = (int64_t)ad.nsplit * ad.split < p->max_vis;
-#define NFA_ATTN_LAUNCH(KV, TPR)                                                       \
-  do {                                                                               \
-    if (loop)                                                                        \
-      hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, true>), grid,                \
-                         dim3(NFA_BLOCK), 0, s, *p, cus, none);                          \
-    else                                                                             \
-      hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, false>), grid,               \
-                         dim3(NFA_BLOCK), 0, s, *p, cus, none);                          \
-  } while (0)
-  if (tpr == 8) {
-    if (bf) NFA_ATTN_LAUNCH(uint16_t, 8); else NFA_ATTN_LAUNCH(float, 8);
-  } else if (tpr == 16) {
-    if (bf) NFA_ATTN_LAUNCH(uint16_t, 16); else NFA_ATTN_LAUNCH(float, 16);
-  } else {
-    if (bf) NFA_ATTN_LAUNCH(uint16_t, 32); else NFA_ATTN_LAUNCH(float, 32);
-  }
-#undef NFA_ATTN_LAUNCH
+  if (bf)
+    launch_attn<uint16_t, false>(tpr, loop, grid, s, *p, cus, none);
+  else
+    launch_attn<float, false>(tpr, loop, grid, s, *p, cus, none);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     nfa_set_error("nfa_sparse_attn_decode: launch failed: %s", hipGetErrorString(err));
@@ -596,23 +639,10 @@ extern "C" int32_t nfa_sparse_attn_partial(const NfaAttnParams *p,
   hipStream_t s = (hipStream_t)stream;
   const bool bf = p->kv_dtype == NFA_DTYPE_BF16;
   const bool loop = (int64_t)ad.nsplit * ad.split < span;
-#define NFA_PART_LAUNCH(KV, TPR)                                                       \
-  do {                                                                               \
-    if (loop)                                                                        \
-      hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, true, true>), grid,          \
-                         dim3(NFA_BLOCK), 0, s, *p, cus, *pt);                         \
-    else                                                                             \
-      hipLaunchKernelGGL((nfa::nfa_attn_kernel<KV, TPR, false, true>), grid,         \
-                         dim3(NFA_BLOCK), 0, s, *p, cus, *pt);                         \
-  } while (0)
-  if (tpr == 8) {
-    if (bf) NFA_PART_LAUNCH(uint16_t, 8); else NFA_PART_LAUNCH(float, 8);
-  } else if (tpr == 16) {
-    if (bf) NFA_PART_LAUNCH(uint16_t, 16); else NFA_PART_LAUNCH(float, 16);
-  } else {
-    if (bf) NFA_PART_LAUNCH(uint16_t, 32); else NFA_PART_LAUNCH(float, 32);
-  }
-#undef NFA_PART_LAUNCH
+  if (bf)
+    launch_attn<uint16_t, true>(tpr, loop, grid, s, *p, cus, *pt);
+  else
+    launch_attn<float, true>(tpr, loop, grid, s, *p, cus, *pt);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     nfa_set_error("nfa_sparse_attn_partial: launch failed: %s", hipGetErrorString(err));

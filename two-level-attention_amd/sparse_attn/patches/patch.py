@@ -2,7 +2,8 @@
 
 Reference: sparse_attn/patches/patch.py:28-132 (``register_patch``).  Same
 contract: every Qwen3 attention module (and, as in the reference's v1 tree,
-every Llama attention module) gets ``module.indexer`` built from ``args`` and
+every Llama and DeepSeek-V2 attention module) gets ``module.indexer`` built
+from ``args`` and
 its ``forward`` replaced on the instance (the original is kept in
 ``_nfa_original_forward``); the number of patched modules is returned, and a
 sparse method that matches no module raises instead of silently running dense
@@ -28,12 +29,23 @@ def _reject_removed_cache_args(args):
 
 def _attention_classes():
     """(class, forward) pairs of the attention modules this build patches."""
+    from transformers.models.deepseek_v2.modeling_deepseek_v2 import DeepseekV2Attention
     from transformers.models.llama.modeling_llama import LlamaAttention
     from transformers.models.qwen3.modeling_qwen3 import Qwen3Attention
+    from .deepseek_v2_attn_patch import deepseek_v2_attn_forward
     from .llama3_attn_patch import llama3_attn_forward
     from .qwen3_attn_patch import qwen3_attn_forward
     return ((Qwen3Attention, qwen3_attn_forward),
-            (LlamaAttention, llama3_attn_forward))
+            (LlamaAttention, llama3_attn_forward),
+            (DeepseekV2Attention, deepseek_v2_attn_forward))
+
+
+def _key_dim(module):
+    """Per-head key width the selector sees (DeepSeek-V2: the expanded
+    nope + rope key)."""
+    if hasattr(module, 'qk_head_dim'):
+        return module.qk_head_dim
+    return module.head_dim
 
 
 def register_patch(model: nn.Module, args, snapshot=None,
@@ -65,7 +77,7 @@ def register_patch(model: nn.Module, args, snapshot=None,
                 module.indexer = indexer_type(args, snapshot=snapshot)
             else:
                 module.indexer = indexer_type(args)
-            module.indexer.head_dim = module.head_dim
+            module.indexer.head_dim = _key_dim(module)
             if hasattr(module, 'layer_idx'):
                 module.indexer.layer_idx = module.layer_idx
             if not hasattr(module, '_nfa_original_forward'):
@@ -90,9 +102,10 @@ def register_patch(model: nn.Module, args, snapshot=None,
     if args.method != 'none' and n_patched == 0:
         kinds = sorted({type(m).__name__ for _, m in model.named_modules()})
         raise RuntimeError(
-            f'method={args.method!r} but the model has no Qwen3Attention or '
-            f'LlamaAttention module to patch (patched=0); running on would '
-            f'label dense output as sparse. Module types: {kinds[:8]}')
+            f'method={args.method!r} but the model has no Qwen3Attention, '
+            f'LlamaAttention or DeepseekV2Attention module to patch (patched=0); '
+            f'running on would label dense output as sparse. Module types: '
+            f'{kinds[:8]}')
     return n_patched
 
 
