@@ -1282,7 +1282,9 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
 // MULTI: tiles may span several passes (the host picks it when a row can
 // hold more pages than one pass of every tile of a dispatch round covers);
 // without it every tile is a single pass and the extra-pass loop is absent.
-template <int DSUB, typename KV, bool MULTI>
+// TOP2: the avg_top2 far method, a separate instance so the extra query
+// rows and head scores cost the default instances no registers.
+template <int DSUB, typename KV, bool MULTI, bool TOP2>
 __global__ void __launch_bounds__(SB)
     nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
   warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
@@ -1297,7 +1299,7 @@ __global__ void __launch_bounds__(SB)
   float *s_qs = (float *)(smem + sd.a_qs);
   float *s_qu = (float *)(smem + sd.a_qu);
   // avg_top2 far scores (selector:2412-2427) also need the unrounded query
-  const bool top2 = p.far_method == NFA_METHOD_AVG_TOP2;
+  constexpr bool top2 = TOP2;
   float *s_qg = (float *)(smem + sd.a_qg);
   int *s_fdims = (int *)(smem + sd.a_fdims);
   int *s_dims = (int *)(smem + sd.a_dims);
@@ -2407,12 +2409,21 @@ static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
   // one pass per tile whenever a dispatch round of single-pass tiles covers
   // the widest possible row
   const bool multi = p.max_blocks > sd.tcap * nfa::kSpanMax;
-  if (multi)
-    hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, true>), dim3(rows, sd.ntiles),
+  const dim3 grid(rows, sd.ntiles);
+  if (p.far_method == NFA_METHOD_AVG_TOP2) {
+    if (multi)
+      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, true, true>), grid,
+                         dim3(nfa::SB), sd.lds, stream, p, sd);
+    else
+      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, false, true>), grid,
+                         dim3(nfa::SB), sd.lds, stream, p, sd);
+  } else if (multi) {
+    hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, true, false>), grid,
                        dim3(nfa::SB), sd.lds, stream, p, sd);
-  else
-    hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, false>), dim3(rows, sd.ntiles),
+  } else {
+    hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, false, false>), grid,
                        dim3(nfa::SB), sd.lds, stream, p, sd);
+  }
   return hipGetLastError();
 }
 
