@@ -3,7 +3,8 @@
 // Reference: sparse_paged_attention_gather / _gather_attend_grouped_kernel,
 // sparse_attn/ops/paged_region_kernels.py:251-363 and :800-1006.
 //
-// Grid (nsplit, T * hkv), 256 threads.  Each workgroup owns one (query row,
+// Grid nsplit x T * hkv (rows padded to a multiple of 8, one dimension, in
+// an XCD-aware order), 256 threads.  Each workgroup owns one (query row,
 // kv head) and the chunks split, split + nsplit, ... of at most 64 selected
 // slots (one chunk per workgroup at decode widths; any visible width is
 // covered with at most 256 workgroups per row), handles the G query heads of
@@ -27,6 +28,7 @@ namespace nfa {
 
 constexpr int AGMAX = 8;         // query heads per kv head
 constexpr int kTpr = 8;          // threads per K/V row
+constexpr int kXcds = 8;         // XCDs of the device (MI355X), for the block order
 constexpr int kSplitMax = 64;    // tokens per workgroup
 constexpr int kMaxSplits = 256;  // splits merged in LDS
 
@@ -52,15 +54,9 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p, int cus,
   if (split <= 0) split = kSplitMax;  // fewer, longer splits: a cheaper merge
   a.split = split;
   const int G = p.hq / p.hkv;
-  // at most kMaxSplits workgroups per row, and no more than the merge can
-  // stage in the V tile's LDS (a maximum and a denominator per head and
-  // split); a workgroup takes every nsplit-th chunk of the row
+  // at most kMaxSplits workgroups per row; a workgroup takes every
+  // nsplit-th chunk of the row
   int cap = kMaxSplits;
-  if (G > 0) {
-    const int kvb = p.kv_dtype == NFA_DTYPE_BF16 ? 2 : 4;
-    const int lds_cap = kSplitMax * p.head_dim_v * kvb / (8 * G);
-    if (lds_cap < cap) cap = lds_cap;
-  }
   const int want = a.rows > 0 ? (2 * cus + a.rows - 1) / a.rows : 1;
   if (want < cap) cap = want;
   a.nsplit = ((span >= 0 ? span : p.max_vis) + split - 1) / split;
@@ -80,6 +76,47 @@ __host__ __device__ inline int part_span(const NfaAttnParams &p, const NfaAttnPa
   const int nb = (p.max_vis + pt.block_tokens - 1) / pt.block_tokens;
   const int64_t span = (int64_t)((nb + pt.nsplit - 1) / pt.nsplit) * pt.block_tokens;
   return span < p.max_vis ? (int)span : p.max_vis;
+}
+
+// DPP lane moves (VALU, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dppf(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each group of 8 consecutive lanes, in every lane of the group:
+// quad_perm xor 1, quad_perm xor 2, then row_half_mirror (lane i <-> 7 - i).
+__device__ __forceinline__ float sum8(float x) {
+  x += dppf<0xB1>(x);
+  x += dppf<0x4E>(x);
+  x += dppf<0x141>(x);
+  return x;
+}
+
+// Wave-wide maximum / sum: the three 8-lane steps and row_mirror (lane
+// i <-> 15 - i) give every lane its row's result; the four rows combine in
+// scalar registers.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dppf<0xB1>(x));
+  x = fmaxf(x, dppf<0x4E>(x));
+  x = fmaxf(x, dppf<0x141>(x));
+  x = fmaxf(x, dppf<0x140>(x));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dppf<0xB1>(x);
+  x += dppf<0x4E>(x);
+  x += dppf<0x141>(x);
+  x += dppf<0x140>(x);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // Two adjacent KV elements of an LDS row as floats.
@@ -116,8 +153,18 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int w = wave_id();
-  const int split = blockIdx.x;
-  const int vrow = blockIdx.y;  // arrival counter and staging row
+  // XCD-aware order: workgroups are dispatched round-robin over the XCDs
+  // in linear id order, so ids congruent mod kXcds share an XCD (and its
+  // L2).  Rows go in groups of kXcds, row r of a group taking the ids
+  // congruent to r: all splits of a row run on one XCD, and the merge reads
+  // their partials from that XCD's L2.  Rows past the last one (the padding
+  // of the final group) exit at once.
+  const int linear = blockIdx.x;
+  const int group = linear / (kXcds * ad.nsplit);
+  const int within = linear % (kXcds * ad.nsplit);
+  const int vrow = group * kXcds + within % kXcds;  // arrival counter and staging row
+  const int split = within / kXcds;
+  if (vrow >= ad.rows) return;
   const int row = PART ? vrow / pt.nsplit : vrow;
   const int cs = PART ? vrow % pt.nsplit : 0;
   const int t = row / p.hkv;
@@ -126,7 +173,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const float kNegInf = __uint_as_float(0xFF800000u);
 
   __shared__ __align__(16) float s_q[AGMAX * DK];
-  __shared__ float s_p[AGMAX * kSplitMax];  // scores, then exp weights
+  __shared__ __align__(16) float s_p[AGMAX * kSplitMax];  // scores, then exp weights
   __shared__ int s_slot[kSplitMax];
   __shared__ __align__(16) KV s_v[kSplitMax * D];
   __shared__ float s_m[AGMAX], s_z[AGMAX], s_f[AGMAX];
@@ -224,9 +271,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 #pragma unroll
           for (int e = 0; e < CH; ++e) part_s = fmaf(q[e], x[c][e], part_s);
         }
-#pragma unroll
-        for (int off = 1; off < kTpr; off <<= 1)
-          part_s += __shfl_xor(part_s, off, 64);
+        part_s = sum8(part_s);  // the 8 threads of the row (kTpr == 8)
         if (sc == 0 && j < cn)
           s_p[g * kSplitMax + j] = s_slot[j] >= 0 ? part_s * p.scale : kNegInf;
       }
@@ -246,21 +291,14 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     // online softmax per head (one wave per head): new running max, the
     // factor for what was accumulated so far, weights of this chunk
     for (int g = w; g < G; g += NFA_WAVES) {
-      float m = kNegInf;
-      for (int i = lane; i < cn; i += 64) m = fmaxf(m, s_p[g * kSplitMax + i]);
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+      // one score per lane (a chunk holds at most 64 = kSplitMax slots)
+      const float sl = lane < cn ? s_p[g * kSplitMax + lane] : kNegInf;
+      const float m = wave_max(sl);
       const float m_old = s_m[g];
       const float m_new = fmaxf(m_old, m);
-      float z = 0.0f;
-      for (int i = lane; i < cn; i += 64) {
-        const float sc2 = s_p[g * kSplitMax + i];
-        const float e = (m_new == kNegInf) ? 0.0f : __expf(sc2 - m_new);
-        s_p[g * kSplitMax + i] = e;
-        z += e;
-      }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) z += __shfl_xor(z, off, 64);
+      const float e = (m_new == kNegInf || lane >= cn) ? 0.0f : __expf(sl - m_new);
+      if (lane < cn) s_p[g * kSplitMax + lane] = e;
+      const float z = wave_sum(e);
       if (lane == 0) {
         const float f = m_old == kNegInf ? 0.0f : __expf(m_old - m_new);
         s_f[g] = f;
@@ -278,15 +316,34 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       const int g = o / (D / 2);
       const int d = 2 * (o % (D / 2));
       const float f = LOOP ? s_f[g] : 0.0f;
-      float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll 4
-      for (int j = 0; j < cn; ++j) {
-        const float pr = s_p[g * kSplitMax + j];
-        float v0, v1;
+      // four weights per 16-byte LDS read, two independent chains per output
+      // (weights past cn are 0 and their V rows are never staged: skipped)
+      float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+      const float4 *pw = reinterpret_cast<const float4 *>(s_p + g * kSplitMax);
+      for (int j = 0; j < cn; j += 4) {
+        const float4 w4 = pw[j / 4];
+        float v0, v1, u0, u1;
         lds_pair(s_v + j * D, d, &v0, &v1);
-        a0 = fmaf(pr, v0, a0);
-        a1 = fmaf(pr, v1, a1);
+        a0 = fmaf(w4.x, v0, a0);
+        a1 = fmaf(w4.x, v1, a1);
+        if (j + 1 < cn) {
+          lds_pair(s_v + (j + 1) * D, d, &u0, &u1);
+          b0 = fmaf(w4.y, u0, b0);
+          b1 = fmaf(w4.y, u1, b1);
+        }
+        if (j + 2 < cn) {
+          lds_pair(s_v + (j + 2) * D, d, &v0, &v1);
+          a0 = fmaf(w4.z, v0, a0);
+          a1 = fmaf(w4.z, v1, a1);
+        }
+        if (j + 3 < cn) {
+          lds_pair(s_v + (j + 3) * D, d, &u0, &u1);
+          b0 = fmaf(w4.w, u0, b0);
+          b1 = fmaf(w4.w, u1, b1);
+        }
       }
+      a0 = a0 + b0;
+      a1 = a1 + b1;
       if (LOOP) {
         acc0[k] = acc0[k] * f + a0;
         acc1[k] = acc1[k] * f + a1;
@@ -362,46 +419,43 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 
   const float *base = (const float *)(ws + ad.w_part) +
                       (int64_t)vrow * ad.nsplit * ad.part_stride;
-  // split maxima and denominators -> LDS (one round of loads)
+  // two adjacent outputs per thread; each split's (max, denominator, P.V
+  // pair) for them requested in one round (they come from the other split
+  // workgroups of this row, through this XCD's L2), merged as a stream:
+  // rescale what is held to the new maximum, add the batch
   const int ns = ad.nsplit;
-  float *s_ms = reinterpret_cast<float *>(s_v);  // [G][ns]
-  float *s_zs = s_ms + G * ns;                    // [G][ns]
-  for (int i = tid; i < G * ns; i += NFA_BLOCK) {
-    const int g = i / ns, sp = i % ns;
-    const float *ps = base + (int64_t)sp * ad.part_stride + g * (D + 2);
-    s_ms[g * ns + sp] = ps[0];
-    s_zs[g * ns + sp] = ps[1];
-  }
-  __syncthreads();
-  // two adjacent outputs per thread; the P.V partials of kMergeBatch splits
-  // are requested before the first is used (they come from other
-  // workgroups, through memory)
   constexpr int kMergeBatch = 16;
   for (int i = tid; i < G * (D / 2); i += NFA_BLOCK) {
     const int g = i / (D / 2), d = 2 * (i % (D / 2));
-    float M = kNegInf;
-    for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, s_ms[g * ns + sp]);
-    float Z = 0.0f, O0 = 0.0f, O1 = 0.0f;
-    if (M != kNegInf) {
-      const float *pa = base + g * (D + 2) + 2 + d;  // 8-byte aligned: D + 2 and d even
-      for (int s0 = 0; s0 < ns; s0 += kMergeBatch) {
-        float2 av[kMergeBatch];
+    const float *pg = base + g * (D + 2);
+    float M = kNegInf, Z = 0.0f, O0 = 0.0f, O1 = 0.0f;
+    for (int s0 = 0; s0 < ns; s0 += kMergeBatch) {
+      float2 mz[kMergeBatch], av[kMergeBatch];
 #pragma unroll
-        for (int k = 0; k < kMergeBatch; ++k) {
-          const int sp = s0 + k < ns ? s0 + k : ns - 1;  // clamped, unconditional
-          av[k] = *reinterpret_cast<const float2 *>(pa + (int64_t)sp * ad.part_stride);
-        }
-#pragma unroll
-        for (int k = 0; k < kMergeBatch; ++k) {
-          // splits past ns (clamped loads) weigh zero
-          const int sp = s0 + k < ns ? s0 + k : ns - 1;
-          const float ms = s_ms[g * ns + sp];
-          const float f = (s0 + k < ns && ms != kNegInf) ? __expf(ms - M) : 0.0f;
-          Z += s_zs[g * ns + sp] * f;
-          O0 += av[k].x * f;
-          O1 += av[k].y * f;
-        }
+      for (int k = 0; k < kMergeBatch; ++k) {
+        const int sp = s0 + k < ns ? s0 + k : ns - 1;  // clamped, unconditional
+        const float *ps = pg + (int64_t)sp * ad.part_stride;
+        mz[k] = *reinterpret_cast<const float2 *>(ps);          // 8-byte aligned:
+        av[k] = *reinterpret_cast<const float2 *>(ps + 2 + d);  // D + 2, d even
       }
+      float mb = M;
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k)
+        if (s0 + k < ns) mb = fmaxf(mb, mz[k].x);
+      if (mb == kNegInf) continue;  // nothing valid yet
+      const float fo = M == kNegInf ? 0.0f : __expf(M - mb);
+      Z *= fo;
+      O0 *= fo;
+      O1 *= fo;
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        // splits past ns (clamped loads) and empty splits weigh zero
+        const float f = (s0 + k < ns && mz[k].x != kNegInf) ? __expf(mz[k].x - mb) : 0.0f;
+        Z += mz[k].y * f;
+        O0 += av[k].x * f;
+        O1 += av[k].y * f;
+      }
+      M = mb;
     }
     if constexpr (PART) {
       pt.acc[(pb + g) * D + d] = O0;
@@ -589,7 +643,7 @@ extern "C" int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream) 
                   (long long)p->workspace_bytes, (long long)ad.w_total);
     return NFA_EWORKSPACE;
   }
-  dim3 grid(ad.nsplit, ad.rows);
+  dim3 grid((unsigned)(((ad.rows + nfa::kXcds - 1) / nfa::kXcds) * nfa::kXcds * ad.nsplit));
   hipStream_t s = (hipStream_t)stream;
   const bool bf = p->kv_dtype == NFA_DTYPE_BF16;
   const bool loop = (int64_t)ad.nsplit * ad.split < p->max_vis;
@@ -635,7 +689,7 @@ extern "C" int32_t nfa_sparse_attn_partial(const NfaAttnParams *p,
                   (long long)p->workspace_bytes, (long long)ad.w_total);
     return NFA_EWORKSPACE;
   }
-  dim3 grid(ad.nsplit, ad.rows);
+  dim3 grid((unsigned)(((ad.rows + nfa::kXcds - 1) / nfa::kXcds) * nfa::kXcds * ad.nsplit));
   hipStream_t s = (hipStream_t)stream;
   const bool bf = p->kv_dtype == NFA_DTYPE_BF16;
   const bool loop = (int64_t)ad.nsplit * ad.split < span;
