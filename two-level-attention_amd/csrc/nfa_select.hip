@@ -35,6 +35,7 @@
 // outputs only.
 #include "nfa_common.h"
 
+#include <atomic>
 #include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
@@ -53,9 +54,13 @@ constexpr int kSpanMin = NFA_SELECT_CLOCK_PAGES;  // pages per tile, at least
 constexpr int kSpanMax = 288;    // pages per pass of a tile (staged in LDS)
 constexpr int kPassMax = 16;     // passes per tile, at most
 static_assert(kSpanMin == 64 && kSpanMax >= TP, "tile geometry");
+// pages per tile, at most: kPassMax - 1 passes of TP pages and a last one of
+// up to kSpanMax
+constexpr int kTileMax = TP * (kPassMax - 1) + kSpanMax;
 constexpr int kStatTokens = 4;   // tokens per staging round of the stats pass
 constexpr int kSegMax = 16384;   // keys staged in LDS at once by the tail
 constexpr int kQRawPerThread = 4;  // G * head_dim <= 4 * SB query elements
+constexpr int kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
 
 struct SelDims {
   int ntiles;     // L1 tiles per row at most (kernel A grid.y)
@@ -70,10 +75,12 @@ struct SelDims {
   int dstride;    // dense keys in LDS (multiple of 8)
   int prot;       // protected width = min(s_cap, sink + swa)
   int lds;        // LDS bytes per workgroup
+  int lds_tail;   // LDS bytes of the tail alone (at most 64 KiB)
+  int multi;      // tiles may take several passes (second staging buffer)
   // LDS: a common part, then the tile part, or the tail: its candidate pages,
   // then its L1 part or (later) its L2 part
   int a_hist, a_tmp, a_misc, a_clk, a_qf, a_qs, a_qu, a_qg, a_fdims;
-  int a_dims, a_last, a_tphys, a_stage, a_hs, a_st;    // tile
+  int a_dims, a_last, a_tphys, a_stage, a_hs, a_st, a_st2;  // tile
   int a_pages, a_pphys;                                // tail
   int a_keys, a_dbf, a_dbn, a_dsel;                    // tail, L1
   int a_dk, a_l0, a_l0x, a_l1, a_l1x, a_mid, a_mslot;  // tail, L2
@@ -94,12 +101,20 @@ struct TileSplit {
   int span, tiles;  // pages per tile, tiles of the row
 };
 
+// End of the pass of a tile ending at t1 that starts at page c0: the rest of
+// the tile when it fits one pass (kSpanMax pages), else one scoring round of
+// TP pages.  A tile of w > kSpanMax pages takes 1 + ceil((w - kSpanMax) / TP)
+// passes, all but the last of exactly TP pages.
+__host__ __device__ inline int pass_end(int c0, int t1) {
+  return t1 - c0 <= kSpanMax ? t1 : c0 + TP;
+}
+
 // The kt pages of a row in tiles of `span` pages: rounds of `tcap` tiles
 // (one workgroup per CU over all rows of the launch), as few rounds as keep
-// a tile within kPassMax passes of kSpanMax pages, the pages spread evenly
-// over the tiles.  A pass stages, scores and publishes up to kSpanMax pages;
-// more passes per tile replace dispatch rounds of one-pass tiles (long rows,
-// many rows).
+// a tile within kTileMax pages (kPassMax passes), the pages spread evenly
+// over the tiles.  A pass stages, scores and publishes the pages of one
+// pass_end step; more passes per tile replace dispatch rounds of one-pass
+// tiles (long rows, many rows).
 __host__ __device__ inline TileSplit tile_split(int kt, int tcap) {
   TileSplit s;
   if (kt <= 0) {
@@ -107,7 +122,7 @@ __host__ __device__ inline TileSplit tile_split(int kt, int tcap) {
     s.tiles = 1;
     return s;
   }
-  const int per_round = tcap * kSpanMax * kPassMax;
+  const int per_round = tcap * kTileMax;
   const int k = (kt + per_round - 1) / per_round;
   const int span = (kt + k * tcap - 1) / (k * tcap);
   s.span = span < kSpanMin ? kSpanMin : span;
@@ -141,6 +156,8 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   s.a_hs = s.a_stage;  // per-head page scores, after the statistics phase
   s.a_st = o;          // bf16 32-dim statistics of the tile, staged
   if (stats_staged(p)) o += 2 * (32 / 8) * kSpanMax * 16;
+  s.a_st2 = o;         // the next pass's, staged while this one is scored
+  if (stats_staged(p) && s.multi) o += 2 * (32 / 8) * kSpanMax * 16;
   const int a_tile = o;
   o = a_base;
   s.a_pages = o; o += align16(4 * s.np);
@@ -160,9 +177,8 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   s.a_mid = o;   o += align16(4 * p.k2);
   s.a_mslot = o; o += align16(4 * p.k2);
   const int a_l2 = o;
-  s.lds = a_tile;
-  if (a_l1 > s.lds) s.lds = a_l1;
-  if (a_l2 > s.lds) s.lds = a_l2;
+  s.lds_tail = a_l1 > a_l2 ? a_l1 : a_l2;
+  s.lds = a_tile > s.lds_tail ? a_tile : s.lds_tail;
   // workspace
   const int rows = p.batch * p.hkv;
   int64_t w = 0;
@@ -182,12 +198,15 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   s.clk_tiles = (p.max_blocks + kSpanMin - 1) / kSpanMin;
   {
     // tile_split(kt).tiles <= k(kt) * tcap and <= ceil(kt / 64) for kt <= max_blocks
-    const int per_round = s.tcap * kSpanMax * kPassMax;
+    const int per_round = s.tcap * kTileMax;
     const int kmax = (p.max_blocks + per_round - 1) / per_round;
     s.ntiles = kmax * s.tcap < s.clk_tiles ? kmax * s.tcap : s.clk_tiles;
   }
   const int kpad = ((p.max_blocks + TP - 1) / TP) * TP;  // keys per row
   s.np = p.k_f + p.k_n + 2;
+  // a tile spans more than one pass only when a dispatch round of one-pass
+  // tiles cannot cover the widest row
+  s.multi = p.max_blocks > s.tcap * kSpanMax;
   // keys staged per tail segment: as many as fit beside the debug bitmaps
   // (one bit per page each) in 64 KiB
   for (int seg = kpad < kSegMax ? kpad : kSegMax;; seg /= 2) {
@@ -196,7 +215,7 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
     s.kstride = s.nseg * s.seg;
     s.words = s.kstride / 32;
     sel_layout(p, s);
-    if (s.lds <= 64 * 1024 || seg <= TP || seg % 16 != 0) break;
+    if (s.lds_tail <= 64 * 1024 || seg <= TP || seg % 16 != 0) break;
   }
   return s;
 }
@@ -689,21 +708,47 @@ __device__ __forceinline__ void stats_append_token(const NfaSelectParams &p,
   psum[d] = sm;
 }
 
-// Asynchronous global-to-LDS loads (gfx950 global_load_lds_dwordx4) of the
-// bf16 statistics of pages [t0, t1), 32 L1 dims:
-// s_st[slot][chunk][kSpanMax] 16-byte chunks, slot 0 the min (minmax pools)
-// or the sum (avg pools), slot 1 the max.  Lane i of a wave writes
-// base + 16 i, so a wave fills 64 consecutive pages of one (slot, chunk) row
-// per instruction; pages outside both pools are not loaded.  Completes at
-// the issuing wave's next vmcnt wait.
+// LDS byte address of a pointer into the workgroup's LDS.
+__device__ __forceinline__ uint32_t lds_addr(const void *ptr) {
+  typedef __attribute__((address_space(3))) const void lds_cvoid;
+  return (uint32_t)(uintptr_t)(lds_cvoid *)ptr;
+}
+
+// One gfx950 global_load_lds_dwordx4: lane i of the wave copies the 16 bytes
+// at its src to LDS byte lds + 16 i (inactive lanes copy nothing); M0 holds
+// the wave-uniform LDS base and is read one wait state after it is written.
+// Written as assembly, the copy is invisible to the compiler, which
+// therefore inserts no wait for it before later LDS reads of unrelated data:
+// the destination may be read only after the issuing wave's vmcnt(0) wait
+// followed by a workgroup barrier.
+__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
+// Asynchronous global-to-LDS copies of the bf16 statistics of pages
+// [t0, t1), 32 L1 dims: s_st[slot][chunk][kSpanMax] 16-byte chunks, slot 0
+// the min (minmax pools) or the sum (avg pools), slot 1 the max.  A wave
+// fills 64 consecutive pages of one (slot, chunk) row per copy; pages outside
+// both pools are not copied.  Complete at the issuing wave's next vmcnt(0)
+// wait (see lds_dma16).
 __device__ __forceinline__ void stage_stats_async(const NfaSelectParams &p,
                                                   const RowGeo &g, int64_t req,
                                                   int kv, int t0, int t1,
                                                   unsigned char *s_st) {
   constexpr int NC = 32 / 8;
-  typedef __attribute__((address_space(3))) void lds_void;
   const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
   const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
+  // the statistic bases held in scalar registers: the per-lane choice of
+  // base is then a register select, not a load of the kernel argument at a
+  // per-lane offset (whose wait would also wait for every earlier copy)
+  const uint16_t *smin = (const uint16_t *)p.stat_min_l;
+  const uint16_t *ssum = (const uint16_t *)p.stat_sum_l;
+  const uint16_t *smax = (const uint16_t *)p.stat_max_l;
+  asm volatile("" : "+s"(smin), "+s"(ssum), "+s"(smax));
+  const uint32_t lds0 = lds_addr(s_st);
   const int nblk = (t1 - t0 + 63) / 64;
   // units (chunk, 64-page block), both slots per unit
   for (int u = wave_id(); u < NC * nblk; u += SW) {
@@ -715,18 +760,9 @@ __device__ __forceinline__ void stage_stats_async(const NfaSelectParams &p,
     const bool mm = (fp && far_mm) || (np && near_mm);
     const bool avg = (fp && !far_mm) || (np && !near_mm);
     const int64_t base = stat_index<uint16_t>(p, req, kv, c * 8, t, 32);
-    unsigned char *row0 = s_st + (c * kSpanMax + blk * 64) * 16;
-    if (mm || avg) {
-      const uint16_t *src = (const uint16_t *)(mm ? p.stat_min_l : p.stat_sum_l);
-      __builtin_amdgcn_global_load_lds((const void *)(src + base),
-                                       (lds_void *)row0, 16, 0, 0);
-    }
-    if (mm) {
-      const uint16_t *src = (const uint16_t *)p.stat_max_l;
-      __builtin_amdgcn_global_load_lds((const void *)(src + base),
-                                       (lds_void *)(row0 + NC * kSpanMax * 16),
-                                       16, 0, 0);
-    }
+    const uint32_t row0 = lds0 + (uint32_t)(c * kSpanMax + blk * 64) * 16;
+    if (mm || avg) lds_dma16((mm ? smin : ssum) + base, row0);
+    if (mm) lds_dma16(smax + base, row0 + NC * kSpanMax * 16);
   }
 }
 
@@ -738,53 +774,44 @@ constexpr int GMAX = 8;
 static_assert(GMAX * kSpanMax * 4 <= 4 * SB * kStatTokens,
               "head scores fit the stage");
 
-// Two query heads of one page from the staged statistics st (chunk c at
+// One query head of one page from the staged statistics st (chunk c at
 // st[c * kSpanMax], the max slot at st[4 * kSpanMax]):
 // bf16(Σ_d kmin_d·min(q_d,0) + Σ_d kmax_d·max(q_d,0)) for minmax pools, from
-// the split queries qs = [min(q,0) | max(q,0)], and bf16(Σ_d bf16(ksum_d /
-// bs)·q_d) for avg pools, from the queries qf; every sum sequential in
-// ascending d with separately rounded products.
-__device__ __forceinline__ void l1_heads_staged(const uint4 *st, const float *qs0,
-                                                const float *qs1, const float *qf0,
-                                                const float *qf1, const float *qu0,
-                                                const float *qu1, bool need_mm,
-                                                int bs, float *out0, float *out1,
-                                                float *un0, float *un1) {
+// the split query qs = [min(q,0) | max(q,0)], and bf16(Σ_d bf16(ksum_d /
+// bs)·q_d) for avg pools, from the query qf (and, with qu, the same mean
+// against the unrounded query into *un); every sum sequential in ascending
+// d with separately rounded products.
+__device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs,
+                                                const float *qf, const float *qu,
+                                                bool need_mm, int bs, float *un) {
   constexpr int NC = 32 / 8;
-  float r0, r1, su0 = 0.0f, su1 = 0.0f;
+  float r, su = 0.0f;
   if (need_mm) {
-    float sn0 = 0.0f, sp0 = 0.0f, sn1 = 0.0f, sp1 = 0.0f;
+    float sn = 0.0f, sp = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      float lo[8], hi[8], ln0[8], hp0[8], ln1[8], hp1[8];
+      float lo[8], hi[8], ln[8], hp[8];
       unpack_chunk<uint16_t>(st[c * kSpanMax], lo);
       unpack_chunk<uint16_t>(st[(NC + c) * kSpanMax], hi);
-      load_f8(qs0 + c * 8, ln0);
-      load_f8(qs0 + 32 + c * 8, hp0);
-      load_f8(qs1 + c * 8, ln1);
-      load_f8(qs1 + 32 + c * 8, hp1);
+      load_f8(qs + c * 8, ln);
+      load_f8(qs + 32 + c * 8, hp);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float a0 = lo[e] * ln0[e];
-        const float b0 = hi[e] * hp0[e];
-        const float a1 = lo[e] * ln1[e];
-        const float b1 = hi[e] * hp1[e];
-        sn0 = sn0 + a0;
-        sp0 = sp0 + b0;
-        sn1 = sn1 + a1;
-        sp1 = sp1 + b1;
+        const float a = lo[e] * ln[e];
+        const float b = hi[e] * hp[e];
+        sn = sn + a;
+        sp = sp + b;
       }
     }
-    r0 = sn0 + sp0;
-    r1 = sn1 + sp1;
+    r = sn + sp;
   } else {
     const float bsf = (float)bs;
     const bool pow2 = (bs & (bs - 1)) == 0;
     const float inv = 1.0f / bsf;
-    float sa0 = 0.0f, sa1 = 0.0f;
+    float sa = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      float k[8], q0[8], q1[8];
+      float k[8], q[8];
       unpack_chunk<uint16_t>(st[c * kSpanMax], k);
       // x / bs == x * (1 / bs) exactly when bs is a power of two
       if (pow2) {
@@ -794,35 +821,25 @@ __device__ __forceinline__ void l1_heads_staged(const uint4 *st, const float *qs
 #pragma unroll
         for (int e = 0; e < 8; ++e) k[e] = bf16r(k[e] / bsf);
       }
-      load_f8(qf0 + c * 8, q0);
-      load_f8(qf1 + c * 8, q1);
+      load_f8(qf + c * 8, q);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float a0 = k[e] * q0[e];
-        const float a1 = k[e] * q1[e];
-        sa0 = sa0 + a0;
-        sa1 = sa1 + a1;
+        const float a = k[e] * q[e];
+        sa = sa + a;
       }
-      if (qu0 != nullptr) {
-        // the same page mean against the unrounded query rows
-        load_f8(qu0 + c * 8, q0);
-        load_f8(qu1 + c * 8, q1);
+      if (qu != nullptr) {
+        load_f8(qu + c * 8, q);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float a0 = k[e] * q0[e];
-          const float a1 = k[e] * q1[e];
-          su0 = su0 + a0;
-          su1 = su1 + a1;
+          const float a = k[e] * q[e];
+          su = su + a;
         }
       }
     }
-    r0 = sa0;
-    r1 = sa1;
+    r = sa;
   }
-  *out0 = bf16r(r0);
-  *out1 = bf16r(r1);
-  *un0 = bf16r(su0);
-  *un1 = bf16r(su1);
+  *un = bf16r(su);
+  return bf16r(r);
 }
 
 // Same arithmetic with the statistics read chunk by chunk from memory (L1
@@ -1433,7 +1450,7 @@ __global__ void __launch_bounds__(SB)
   // speculative: the pools without skip flags contain the final ones
   const RowGeo g0 = row_geo(p, L, false, false);
   unsigned char *s_st = smem + sd.a_st;
-  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, imin(t0 + kSpanMax, t1), s_st);
+  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, pass_end(t0, t1), s_st);
   int32_t prev, skf, skn, ph_last;
   sload_i32x4(p.stats_len_l + req, p.skip_far_l + req, p.skip_near_l + req,
               btr + (owns_last ? imin((L - 1) / p.page, mb - 1) : 0), prev, skf,
@@ -1485,9 +1502,13 @@ __global__ void __launch_bounds__(SB)
   const RowGeo geo = row_geo(p, L, skip_far, skip_near);
   float *s_hs = (float *)(smem + sd.a_hs);  // [head][page] bf16 head scores
   const int j0 = hp, j1 = hp + TPP;
-  // one pass stages, scores and publishes pages [c0, c1), at most kSpanMax;
-  // the histogram accumulates in LDS over the passes of the tile
-  auto run_pass = [&](int c0, int c1) {
+  // one pass scores and publishes pages [c0, c1) from the statistics staged
+  // in st; the histogram accumulates in LDS over the passes of the tile.
+  // The next pass's statistics, pages [n0, n1), are copied into nst while
+  // this pass is scored (not on a rebuild, which restages each pass after
+  // recomputing it)
+  auto run_pass = [&](int c0, int c1, unsigned char *st, int n0, int n1,
+                      unsigned char *nst) {
     const int ngrp = (c1 - c0 + 63) / 64;
     if (NFA_COLD(do_stats && !incremental)) {
       float *psum_row = p.page_sum_l != nullptr
@@ -1563,7 +1584,7 @@ __global__ void __launch_bounds__(SB)
         // the rebuild
         int t0r = c0;
         asm volatile("" : "+s"(t0r));
-        stage_stats_async(p, geo, req, kv, t0r, c1, s_st);
+        stage_stats_async(p, geo, req, kv, t0r, c1, st);
       }
     }
     if constexpr (STG) {
@@ -1572,6 +1593,11 @@ __global__ void __launch_bounds__(SB)
     }
     lds_barrier();
     NFA_MARK(0, 3);
+    if constexpr (STG && MULTI) {
+      // every wave has finished the previous pass, which read nst
+      if (n0 < n1 && !(do_stats && !incremental))
+        stage_stats_async(p, geo, req, kv, n0, n1, nst);
+    }
 
     // ---- L1 scores: four waves per 64 pages, two query heads per thread -----
     if (do_stats && j0 < G) {
@@ -1588,13 +1614,13 @@ __global__ void __launch_bounds__(SB)
         const bool pair = top2 && fp;
         float h0 = 0.0f, h1 = 0.0f, u0 = 0.0f, u1 = 0.0f;
         if constexpr (STG) {
-          // a missing second head scores the first one again, discarded
-          const int j1s = j1 < G ? j1 : j0;
-          l1_heads_staged(reinterpret_cast<const uint4 *>(s_st) + lp,
-                          s_qs + j0 * 2 * DSUB, s_qs + j1s * 2 * DSUB,
-                          s_qf + j0 * DSUB, s_qf + j1s * DSUB,
-                          pair ? s_qu + j0 * DSUB : nullptr, s_qu + j1s * DSUB,
-                          need_mm, bs, &h0, &h1, &u0, &u1);
+          // the second head only for groups above TPP heads (uniform per wave)
+          const uint4 *su = reinterpret_cast<const uint4 *>(st) + lp;
+          h0 = l1_head_staged(su, s_qs + j0 * 2 * DSUB, s_qf + j0 * DSUB,
+                              pair ? s_qu + j0 * DSUB : nullptr, need_mm, bs, &u0);
+          if (j1 < G)
+            h1 = l1_head_staged(su, s_qs + j1 * 2 * DSUB, s_qf + j1 * DSUB,
+                                pair ? s_qu + j1 * DSUB : nullptr, need_mm, bs, &u1);
         } else {
           const bool from_lds = incremental && t == last_blk;
           float m0 = 0.0f, a0 = 0.0f, m1 = 0.0f, a1 = 0.0f;
@@ -1652,14 +1678,21 @@ __global__ void __launch_bounds__(SB)
     }
     lds_barrier();
   };
-  run_pass(t0, imin(t0 + kSpanMax, t1));
-  if constexpr (MULTI) {
-    // long rows and many rows: further passes instead of dispatch rounds
-    for (int c0 = t0 + kSpanMax; c0 < t1; c0 += kSpanMax) {
-      const int c1 = imin(c0 + kSpanMax, t1);
-      __syncthreads();  // the previous pass's readers of the staged statistics
-      if constexpr (STG) stage_stats_async(p, geo, req, kv, c0, c1, s_st);
-      run_pass(c0, c1);
+  {
+    unsigned char *st = s_st;
+    unsigned char *nst = smem + sd.a_st2;
+    int c1 = pass_end(t0, t1);
+    run_pass(t0, c1, st, c1, c1 < t1 ? pass_end(c1, t1) : c1, nst);
+    if constexpr (MULTI) {
+      // long rows and many rows: further passes instead of dispatch rounds,
+      // the staging buffers alternating
+      for (int c0 = c1; c0 < t1; c0 = c1) {
+        c1 = pass_end(c0, t1);
+        unsigned char *tmp = st;
+        st = nst;
+        nst = tmp;
+        run_pass(c0, c1, st, c1, c1 < t1 ? pass_end(c1, t1) : c1, nst);
+      }
     }
   }
   if (tid < 256) {
@@ -2357,9 +2390,9 @@ static int select_check(const NfaSelectParams *p, bool need_workspace) {
     return NFA_EINVAL;
   }
   const SelDims sd = nfa::sel_dims(*p, nfa::device_cus());
-  if (sd.lds > 64 * 1024) {
-    nfa_set_error("nfa_select_layer: geometry needs %d bytes of LDS (> 64 KiB)",
-                  sd.lds);
+  if (sd.lds > nfa::kLdsMax || sd.lds_tail > 64 * 1024) {
+    nfa_set_error("nfa_select_layer: geometry needs %d bytes of LDS (tail %d)",
+                  sd.lds, sd.lds_tail);
     return NFA_EINVAL;
   }
   if ((p->hq / p->hkv) * p->head_dim > nfa::kQRawPerThread * nfa::SB) {
@@ -2402,14 +2435,42 @@ extern "C" int64_t nfa_select_workspace_bytes(const NfaSelectParams *p) {
   return nfa::sel_dims(*p, 256).w_total;  // independent of the CU count
 }
 
+// Lets `kernel` take up to kLdsMax bytes of dynamic LDS on the current
+// device (the default cap is 64 KiB); `done` remembers the devices already
+// set, one bit each.
+static hipError_t lds_optin(const void *kernel, std::atomic<uint64_t> &done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          nfa::kLdsMax);
+  if (e == hipSuccess) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
+
 template <int DSUB, typename KV>
 static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
                                 hipStream_t stream) {
   const int rows = p.batch * p.hkv;
   // one pass per tile whenever a dispatch round of single-pass tiles covers
-  // the widest possible row
-  const bool multi = p.max_blocks > sd.tcap * nfa::kSpanMax;
+  // the widest possible row; several passes stage the next pass's statistics
+  // in a second LDS buffer (beyond 64 KiB)
+  const bool multi = sd.multi != 0;
   const dim3 grid(rows, sd.ntiles);
+  if (sd.lds > 64 * 1024) {
+    static std::atomic<uint64_t> optin[4];
+    const bool top2 = p.far_method == NFA_METHOD_AVG_TOP2;
+    const void *k[4] = {
+        reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, false, false>),
+        reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, false, true>),
+        reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, true, false>),
+        reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, true, true>)};
+    const int i = 2 * (int)multi + (int)top2;
+    const hipError_t e = lds_optin(k[i], optin[i]);
+    if (e != hipSuccess) return e;
+  }
   if (p.far_method == NFA_METHOD_AVG_TOP2) {
     if (multi)
       hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, true, true>), grid,
