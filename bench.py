@@ -347,6 +347,15 @@ def selector_timeline(torch, w, steps, plan):
         for k, name in enumerate(names):
             d = (tile[:, :, k + 1] - tile[:, :, k]) * us
             acc.setdefault(f'A tile {name} (max)', []).append(d.max())
+        # summed over a tile's passes: staging wait, scores, keys + histogram;
+        # then the histogram flush after the last pass
+        for k, name in ((8, 'passes: staging wait'), (9, 'passes: scores'),
+                        (10, 'passes: keys+hist')):
+            acc.setdefault(f'A tile {name} (max)', []).append(tile[:, :, k].max() * us)
+        acc.setdefault('A tile hist flush (max)', []).append(
+            ((tile[:, :, 4] - tile[:, :, 6]) * us).max())
+        acc.setdefault('A tile slowest scoring tile', []).append(
+            float(np.unravel_index(tile[:, :, 9].argmax(), tile.shape[:2])[1]))
         spans = [('tail L1 threshold', 0, 1),
                  ('  L1 thr: hist+keys load', 0, 24), ('  L1 thr: coarse bins', 24, 25),
                  ('  L1 thr: refine pass', 25, 26), ('  L1 thr: fine bins', 26, 1),

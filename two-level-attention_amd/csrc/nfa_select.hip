@@ -48,8 +48,8 @@ namespace nfa {
 
 constexpr int SB = 1024;         // threads per selector workgroup
 constexpr int SW = SB / 64;      // waves per selector workgroup
-constexpr int TPP = 4;           // threads per page in the tile stage
-constexpr int TP = SB / TPP;     // pages scored per pass of a workgroup
+constexpr int TPP = 4;           // lanes per page when scoring groups of 4 heads
+constexpr int TP = SB / TPP;     // pages of a scoring round (and of a pass)
 constexpr int kSpanMin = NFA_SELECT_CLOCK_PAGES;  // pages per tile, at least
 constexpr int kSpanMax = 288;    // pages per pass of a tile (staged in LDS)
 constexpr int kPassMax = 16;     // passes per tile, at most
@@ -58,7 +58,7 @@ static_assert(kSpanMin == 64 && kSpanMax >= TP, "tile geometry");
 // up to kSpanMax
 constexpr int kTileMax = TP * (kPassMax - 1) + kSpanMax;
 constexpr int kStatTokens = 4;   // tokens per staging round of the stats pass
-constexpr int kSegMax = 16384;   // keys staged in LDS at once by the tail
+constexpr int kSegMax = 1 << 17;  // keys staged in LDS at once by the tail, at most
 constexpr int kQRawPerThread = 4;  // G * head_dim <= 4 * SB query elements
 constexpr int kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
 
@@ -75,7 +75,6 @@ struct SelDims {
   int dstride;    // dense keys in LDS (multiple of 8)
   int prot;       // protected width = min(s_cap, sink + swa)
   int lds;        // LDS bytes per workgroup
-  int lds_tail;   // LDS bytes of the tail alone (at most 64 KiB)
   int multi;      // tiles may take several passes (second staging buffer)
   // LDS: a common part, then the tile part, or the tail: its candidate pages,
   // then its L1 part or (later) its L2 part
@@ -142,10 +141,11 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   s.a_tmp = o;   o += align16(4 * 128);
   s.a_misc = o;  o += align16(4 * 32);
   s.a_clk = o;   o += 8 * 64;  // debug timeline: tile marks, tail marks
-  s.a_qf = o;    o += align16(4 * group * p.dsub);
-  s.a_qs = o;    o += align16(4 * group * 2 * p.dsub);  // min(q,0) | max(q,0)
+  // query rows padded by 4 floats each
+  s.a_qf = o;    o += align16(4 * group * (p.dsub + 4));
+  s.a_qs = o;    o += align16(4 * group * (2 * p.dsub + 4));  // min(q,0) | max(q,0)
   s.a_qu = o;    // unrounded scaled query rows (avg_top2 far scores)
-  if (p.far_method == NFA_METHOD_AVG_TOP2) o += align16(4 * group * p.dsub);
+  if (p.far_method == NFA_METHOD_AVG_TOP2) o += align16(4 * group * (p.dsub + 4));
   s.a_qg = o;    o += align16(4 * p.fine_dsub);          // grouped L2 query
   s.a_fdims = o; o += align16(4 * p.fine_dsub);
   const int a_base = o;
@@ -177,8 +177,8 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   s.a_mid = o;   o += align16(4 * p.k2);
   s.a_mslot = o; o += align16(4 * p.k2);
   const int a_l2 = o;
-  s.lds_tail = a_l1 > a_l2 ? a_l1 : a_l2;
-  s.lds = a_tile > s.lds_tail ? a_tile : s.lds_tail;
+  const int a_tail = a_l1 > a_l2 ? a_l1 : a_l2;
+  s.lds = a_tile > a_tail ? a_tile : a_tail;
   // workspace
   const int rows = p.batch * p.hkv;
   int64_t w = 0;
@@ -208,14 +208,14 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   // tiles cannot cover the widest row
   s.multi = p.max_blocks > s.tcap * kSpanMax;
   // keys staged per tail segment: as many as fit beside the debug bitmaps
-  // (one bit per page each) in 64 KiB
+  // (one bit per page each) in the LDS of a workgroup
   for (int seg = kpad < kSegMax ? kpad : kSegMax;; seg /= 2) {
     s.seg = seg;
     s.nseg = (kpad + s.seg - 1) / s.seg;
     s.kstride = s.nseg * s.seg;
     s.words = s.kstride / 32;
     sel_layout(p, s);
-    if (s.lds_tail <= 64 * 1024 || seg <= TP || seg % 16 != 0) break;
+    if (s.lds <= kLdsMax || seg <= TP || seg % 16 != 0) break;
   }
   return s;
 }
@@ -780,7 +780,9 @@ static_assert(GMAX * kSpanMax * 4 <= 4 * SB * kStatTokens,
 // the split query qs = [min(q,0) | max(q,0)], and bf16(Σ_d bf16(ksum_d /
 // bs)·q_d) for avg pools, from the query qf (and, with qu, the same mean
 // against the unrounded query into *un); every sum sequential in ascending
-// d with separately rounded products.
+// d with separately rounded products.  x / bs is computed as x * (1 / bs),
+// exact when bs is a power of two (POW2), else as a division.
+template <bool POW2>
 __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs,
                                                 const float *qf, const float *qu,
                                                 bool need_mm, int bs, float *un) {
@@ -806,21 +808,14 @@ __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs
     r = sn + sp;
   } else {
     const float bsf = (float)bs;
-    const bool pow2 = (bs & (bs - 1)) == 0;
     const float inv = 1.0f / bsf;
     float sa = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       float k[8], q[8];
       unpack_chunk<uint16_t>(st[c * kSpanMax], k);
-      // x / bs == x * (1 / bs) exactly when bs is a power of two
-      if (pow2) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) k[e] = bf16r(k[e] * inv);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) k[e] = bf16r(k[e] / bsf);
-      }
+      for (int e = 0; e < 8; ++e) k[e] = bf16r(POW2 ? k[e] * inv : k[e] / bsf);
       load_f8(qf + c * 8, q);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -970,25 +965,23 @@ __device__ __forceinline__ bool tie_cut(const PoolThr &t) {
   return t.need < (1 << 30) && t.T > 0 && t.T < 0x10000;
 }
 
-// Stage keys [seg_base, seg_base + seg) of a row into LDS with 16-byte
-// loads, every load of the segment in flight at once (seg <= kSegMax).
+// Stage keys [seg_base, seg_base + seg) of a row into LDS by asynchronous
+// 16-byte copies (seg a multiple of 8 keys): readable after dma_barrier().
 __device__ __forceinline__ void stage_keys(const uint16_t *g_keys, int seg_base,
                                            int seg, uint16_t *s_keys) {
-  constexpr int R = kSegMax / 8 / SB;
   const int n16 = seg / 8;
   const uint4 *src = reinterpret_cast<const uint4 *>(g_keys + seg_base);
-  uint4 *dst = reinterpret_cast<uint4 *>(s_keys);
-  uint4 r[R];
-#pragma unroll
-  for (int k = 0; k < R; ++k) {
-    const int u = threadIdx.x + k * SB;
-    r[k] = u < n16 ? src[u] : make_uint4(0u, 0u, 0u, 0u);
+  const uint32_t lds0 = lds_addr(s_keys);
+  for (int u0 = wave_id() * 64; u0 < n16; u0 += SB) {
+    const int u = u0 + lane_id();
+    if (u < n16) lds_dma16(src + u, lds0 + (uint32_t)u0 * 16);
   }
-#pragma unroll
-  for (int k = 0; k < R; ++k) {
-    const int u = threadIdx.x + k * SB;
-    if (u < n16) dst[u] = r[k];
-  }
+}
+
+// Completes this wave's asynchronous copies, then the workgroup's.
+__device__ __forceinline__ void dma_barrier() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
 }
 
 // Protected sink/SWA ids as up to two disjoint intervals [u0,u1) [u2,u3),
@@ -1312,6 +1305,10 @@ __global__ void __launch_bounds__(SB)
   int *s_hist = (int *)(smem + sd.a_hist);  // far hi | near hi | far lo | near lo
   int *s_tmp = (int *)(smem + sd.a_tmp);
   int *s_misc = (int *)(smem + sd.a_misc);
+  // query rows of the group's heads, each row padded by 16 bytes so that the
+  // rows of the heads scored side by side start in different LDS banks
+  constexpr int QF = DSUB + 4;      // s_qf, s_qu row stride (floats)
+  constexpr int QS = 2 * DSUB + 4;  // s_qs row stride
   float *s_qf = (float *)(smem + sd.a_qf);
   float *s_qs = (float *)(smem + sd.a_qs);
   float *s_qu = (float *)(smem + sd.a_qu);
@@ -1334,12 +1331,6 @@ __global__ void __launch_bounds__(SB)
   const int G = p.hq / p.hkv;
   const int bs = p.bs;
   const int mb = p.max_blocks;
-  // wave w scores query heads hp = w % TPP and hp + TPP of the pages of the
-  // 64-page groups w / TPP, w / TPP + SW / TPP, ...: query reads are uniform
-  // over the wave
-  const int hp = wave_id() % TPP;
-  const int grp0 = wave_id() / TPP;
-  constexpr int GSTEP = SW / TPP;
 
   const int64_t clk_tile = ((int64_t)row * (sd.clk_tiles + 1) + tile) * 32;
   const int64_t clk_tail = ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32;
@@ -1408,6 +1399,13 @@ __global__ void __launch_bounds__(SB)
     }
   }
   if (tid < 512) s_hist[tid] = 0;
+  // the tile's first statistics are requested as soon as the query words
+  // are consumed (a later wait of the compiler's for a load of the wave
+  // also waits for these copies): speculative, the pools without skip flags
+  // contain the final ones
+  const RowGeo g0 = row_geo(p, L, false, false);
+  unsigned char *s_st = smem + sd.a_st;
+  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, pass_end(t0, t1), s_st);
   lds_barrier();
   NFA_MARK(0, 1);
 
@@ -1417,10 +1415,10 @@ __global__ void __launch_bounds__(SB)
     const int j = i / DSUB;
     const int d = i % DSUB;
     const float qr = bf16r(s_qraw[j * hd + s_dims[d]] * p.scale);
-    s_qf[i] = qr;
-    s_qs[j * 2 * DSUB + d] = qr < 0.0f ? qr : 0.0f;
-    s_qs[j * 2 * DSUB + DSUB + d] = qr > 0.0f ? qr : 0.0f;
-    if (top2) s_qu[i] = s_qraw[j * hd + s_dims[d]] * p.scale;
+    s_qf[j * QF + d] = qr;
+    s_qs[j * QS + d] = qr < 0.0f ? qr : 0.0f;
+    s_qs[j * QS + DSUB + d] = qr > 0.0f ? qr : 0.0f;
+    if (top2) s_qu[j * QF + d] = s_qraw[j * hd + s_dims[d]] * p.scale;
   }
   // grouped L2 query (selector:979-1002): bf16 terms summed in head order
   for (int d = tid; d < p.fine_dsub; d += SB) {
@@ -1442,15 +1440,9 @@ __global__ void __launch_bounds__(SB)
   lds_barrier();  // the query rows; the raw rows' LDS is free again
   NFA_MARK(0, 2);
 
-  // ---- second round trip: statistics (asynchronous), request state -------
-  // (after every LDS read of the prologue: a read behind an asynchronous
-  // global-to-LDS load waits for it)
+  // ---- second round trip: request state --------------------------------
   const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
   const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
-  // speculative: the pools without skip flags contain the final ones
-  const RowGeo g0 = row_geo(p, L, false, false);
-  unsigned char *s_st = smem + sd.a_st;
-  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, pass_end(t0, t1), s_st);
   int32_t prev, skf, skn, ph_last;
   sload_i32x4(p.stats_len_l + req, p.skip_far_l + req, p.skip_near_l + req,
               btr + (owns_last ? imin((L - 1) / p.page, mb - 1) : 0), prev, skf,
@@ -1501,7 +1493,10 @@ __global__ void __launch_bounds__(SB)
   }
   const RowGeo geo = row_geo(p, L, skip_far, skip_near);
   float *s_hs = (float *)(smem + sd.a_hs);  // [head][page] bf16 head scores
-  const int j0 = hp, j1 = hp + TPP;
+  const int lpp_log = G <= 1 ? 0 : G <= 2 ? 1 : G <= 4 ? 2 : 3;
+  const int lpp = 1 << lpp_log;  // lanes per page
+  const int ppw = 64 >> lpp_log;  // pages per wave and round
+  const bool bs_pow2 = (bs & (bs - 1)) == 0;
   // one pass scores and publishes pages [c0, c1) from the statistics staged
   // in st; the histogram accumulates in LDS over the passes of the tile.
   // The next pass's statistics, pages [n0, n1), are copied into nst while
@@ -1509,7 +1504,7 @@ __global__ void __launch_bounds__(SB)
   // recomputing it)
   auto run_pass = [&](int c0, int c1, unsigned char *st, int n0, int n1,
                       unsigned char *nst) {
-    const int ngrp = (c1 - c0 + 63) / 64;
+    NFA_MARK(0, 7);
     if (NFA_COLD(do_stats && !incremental)) {
       float *psum_row = p.page_sum_l != nullptr
                             ? p.page_sum_l + (req * p.hkv + kv) * DSUB
@@ -1599,66 +1594,51 @@ __global__ void __launch_bounds__(SB)
         stage_stats_async(p, geo, req, kv, n0, n1, nst);
     }
 
-    // ---- L1 scores: four waves per 64 pages, two query heads per thread -----
-    if (do_stats && j0 < G) {
-      for (int grp = grp0; grp < ngrp; grp += GSTEP) {
-        const int lp = grp * 64 + lane_id();
-        const int t = c0 + lp;
-        bool fp = false, np = false;
-        if (t < c1) pools(p, geo, t, &fp, &np);
-        if (!(fp || np)) continue;
-        const bool need_mm = (fp && far_mm) || (np && near_mm);
+    // ---- L1 scores, group means, keys and high-byte histograms -----------
+    // lpp lanes per page (one per query head of the group, padded to a
+    // power of two), 64 / lpp pages per wave and round: each lane scores one
+    // head of its page into s_hs, then the page's first lane combines the
+    // page's head scores (written by lanes of the same wave, so in order
+    // without a barrier), publishes the key and counts it in the histogram.
+    // Every page of the pass gets a key (0 for pages in no pool).
+    for (int base = wave_id() * ppw; base < c1 - c0; base += SW * ppw) {
+      const int lp = base + (lane_id() >> lpp_log);
+      const int j = lane_id() & (lpp - 1);
+      const int t = c0 + lp;
+      bool fp = false, np = false;
+      if (do_stats && t < c1) pools(p, geo, t, &fp, &np);
+      const bool need_mm = (fp && far_mm) || (np && near_mm);
+      if ((fp || np) && j < G) {
         const bool need_avg = !need_mm;
-        // avg_top2 far pages: both head means, against the rounded and the
+        // avg_top2 far pages: the head mean against the rounded and the
         // unrounded query, packed as two bf16 patterns in the head's slot
         const bool pair = top2 && fp;
-        float h0 = 0.0f, h1 = 0.0f, u0 = 0.0f, u1 = 0.0f;
+        const float *qu = pair ? s_qu + j * QF : nullptr;
+        float h, u = 0.0f;
         if constexpr (STG) {
-          // the second head only for groups above TPP heads (uniform per wave)
           const uint4 *su = reinterpret_cast<const uint4 *>(st) + lp;
-          h0 = l1_head_staged(su, s_qs + j0 * 2 * DSUB, s_qf + j0 * DSUB,
-                              pair ? s_qu + j0 * DSUB : nullptr, need_mm, bs, &u0);
-          if (j1 < G)
-            h1 = l1_head_staged(su, s_qs + j1 * 2 * DSUB, s_qf + j1 * DSUB,
-                                pair ? s_qu + j1 * DSUB : nullptr, need_mm, bs, &u1);
+          h = bs_pow2 ? l1_head_staged<true>(su, s_qs + j * QS, s_qf + j * QF, qu,
+                                             need_mm, bs, &u)
+                      : l1_head_staged<false>(su, s_qs + j * QS, s_qf + j * QF, qu,
+                                              need_mm, bs, &u);
         } else {
           const bool from_lds = incremental && t == last_blk;
-          float m0 = 0.0f, a0 = 0.0f, m1 = 0.0f, a1 = 0.0f;
-          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j0 * DSUB,
-                                pair ? s_qu + j0 * DSUB : nullptr, need_mm, need_avg,
-                                from_lds ? s_last : nullptr, &m0, &a0, &u0);
-          if (j1 < G)
-            l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j1 * DSUB,
-                                  pair ? s_qu + j1 * DSUB : nullptr, need_mm,
-                                  need_avg, from_lds ? s_last : nullptr, &m1, &a1, &u1);
-          h0 = need_mm ? m0 : a0;
-          h1 = need_mm ? m1 : a1;
+          float m = 0.0f, a = 0.0f;
+          l1_head_mem<DSUB, KV>(p, req, kv, t, s_qf + j * QF, qu, need_mm, need_avg,
+                                from_lds ? s_last : nullptr, &m, &a, &u);
+          h = need_mm ? m : a;
         }
-        if (pair) {
-          h0 = __uint_as_float(((uint32_t)bf16_bits(h0) << 16) | bf16_bits(u0));
-          h1 = __uint_as_float(((uint32_t)bf16_bits(h1) << 16) | bf16_bits(u1));
-        }
-        s_hs[j0 * kSpanMax + lp] = h0;
-        if (j1 < G) s_hs[j1 * kSpanMax + lp] = h1;
+        if (pair) h = __uint_as_float(((uint32_t)bf16_bits(h) << 16) | bf16_bits(u));
+        s_hs[j * kSpanMax + lp] = h;
       }
-    }
-    lds_barrier();
-
-    // ---- group mean, keys and high-byte histograms (the hp == 0 waves) -----
-    if (hp == 0) {
-      for (int grp = grp0; grp < ngrp; grp += GSTEP) {
-        const int lp = grp * 64 + lane_id();
-        const int t = c0 + lp;
-        if (t >= c1) continue;
-        bool fp = false, np = false;
-        if (do_stats) pools(p, geo, t, &fp, &np);
+      if (j == 0 && t < c1) {
         uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
         if (NFA_COLD(top2 && fp)) {
           far_bits = top2_far_score(s_hs + lp, G);
         } else if (fp || np) {
           // bf16 head scores summed in head order
           float acc = 0.0f;
-          for (int j = 0; j < G; ++j) acc = acc + s_hs[j * kSpanMax + lp];
+          for (int jj = 0; jj < G; ++jj) acc = acc + s_hs[jj * kSpanMax + lp];
           const uint16_t mean = bf16_bits(acc / (float)G);
           if (fp) far_bits = mean;
           if (np) near_bits = mean;
@@ -1677,6 +1657,14 @@ __global__ void __launch_bounds__(SB)
       }
     }
     lds_barrier();
+    NFA_MARK(0, 5);
+    NFA_MARK(0, 6);
+    if (NFA_COLD(p.dbg_clock != nullptr) && tid == 0) {
+      // per-pass durations summed over the passes: staging wait, scores, keys
+      s_clk[8] += s_clk[3] - s_clk[7];
+      s_clk[9] += s_clk[5] - s_clk[3];
+      s_clk[10] += s_clk[6] - s_clk[5];
+    }
   };
   {
     unsigned char *st = s_st;
@@ -1754,7 +1742,7 @@ __global__ void __launch_bounds__(SB)
     s_misc[4] = 0;
   }
   if (sd.nseg == 1) stage_keys(g_keys, 0, sd.seg, s_keys);
-  __syncthreads();
+  dma_barrier();
   NFA_MARK(32, 24);
   // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
   if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 8);
@@ -1769,7 +1757,7 @@ __global__ void __launch_bounds__(SB)
       if (NFA_COLD(sd.nseg > 1)) {
         __syncthreads();
         stage_keys(g_keys, seg_base, sd.seg, s_keys);
-        __syncthreads();
+        dma_barrier();
       }
       const int n = imin(sd.seg, kt_eff - seg_base);
       // sixteen keys per thread from two 16-byte reads (the segment holds a
@@ -1844,7 +1832,7 @@ __global__ void __launch_bounds__(SB)
     if (NFA_COLD(sd.nseg > 1)) {
       __syncthreads();
       stage_keys(g_keys, seg_base, sd.seg, s_keys);
-      __syncthreads();
+      dma_barrier();
     }
     const int n = imin(sd.seg, kt_eff - seg_base);
     const int n16 = (n + 15) / 16;  // the segment holds a multiple of 16 keys
@@ -2390,9 +2378,9 @@ static int select_check(const NfaSelectParams *p, bool need_workspace) {
     return NFA_EINVAL;
   }
   const SelDims sd = nfa::sel_dims(*p, nfa::device_cus());
-  if (sd.lds > nfa::kLdsMax || sd.lds_tail > 64 * 1024) {
-    nfa_set_error("nfa_select_layer: geometry needs %d bytes of LDS (tail %d)",
-                  sd.lds, sd.lds_tail);
+  if (sd.lds > nfa::kLdsMax) {
+    nfa_set_error("nfa_select_layer: geometry needs %d bytes of LDS (> %d)", sd.lds,
+                  nfa::kLdsMax);
     return NFA_EINVAL;
   }
   if ((p->hq / p->hkv) * p->head_dim > nfa::kQRawPerThread * nfa::SB) {
