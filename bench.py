@@ -225,13 +225,23 @@ def algorithmic_bytes(w, length, bs=16, window=128, near_len=4096, sink=4,
                 p_near=p_near, t_c=t_c)
 
 
+# profiled workloads: (ctx, batch, ragged) -> rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+_TRAFFIC_PROFILES = {
+    (131072, 1, None): 'nfa_select_layer_128k_hbm_traffic.md',
+    (1048576, 1, None): 'nfa_select_layer_1m_kernel_trace_hbm_traffic.md',
+    (131072, 16, (32768, 131072)): 'nfa_select_layer_16x_ragged_kernel_trace_hbm_traffic.md',
+}
+
+
 def measured_traffic(args):
     """HBM bytes per selector launch at this workload, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (None when absent or when the
-    workload differs from the profiled one)."""
-    if args.ctx != 131072 or args.batch != 1 or args.ragged:
+    workload differs from the profiled ones)."""
+    ragged = tuple(args.ragged) if args.ragged else None
+    name = _TRAFFIC_PROFILES.get((args.ctx, args.batch, ragged))
+    if name is None or args.l2_quant or args.operator_mode != 'off':
         return None
-    path = os.path.join(ROOT, 'profiles', 'nfa_select_layer_128k_hbm_traffic.md')
+    path = os.path.join(ROOT, 'profiles', name)
     try:
         with open(path) as f:
             text = f.read()
