@@ -401,6 +401,124 @@ def qwen3_8b_config(ctx, new_tokens):
     return cfg
 
 
+def llama31_8b_config(ctx, new_tokens):
+    """Llama-3.1-8B architecture (32 layers, hidden 4096, MLP 14336, 32/8
+    heads, head_dim 128, vocab 128256, RoPE theta 5e5 with llama3 scaling)."""
+    from transformers import LlamaConfig
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336,
+                      num_hidden_layers=32, num_attention_heads=32,
+                      num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-5,
+                      rope_theta=500000.0, tie_word_embeddings=False,
+                      rope_scaling={'rope_type': 'llama3', 'factor': 8.0,
+                                    'low_freq_factor': 1.0, 'high_freq_factor': 4.0,
+                                    'original_max_position_embeddings': 8192},
+                      max_position_embeddings=max(131072, ctx + new_tokens + 64))
+    cfg._attn_implementation = 'sdpa'
+    return cfg
+
+
+def end_to_end_batch(torch, args, device, lengths):
+    """Whole-model decode of a ragged batch: random-init bf16 Llama-3.1-8B,
+    one dense prefill per prompt (seeded uniform token ids of the given
+    lengths) into one paged cache sized for their pages, then the batch
+    decoded together: 3 warm-up steps and ``args.steps`` greedy steps
+    replayed from one captured hipGraph; HIP events around every
+    ``GraphRunner.step``, median step time; tok/s = batch / step."""
+    from transformers import LlamaForCausalLM
+    from sparse_attn.engine.frozen_runner import (build_frozen_cache,
+                                                  prefill_frozen_request)
+    from sparse_attn.engine.graph_runner import GraphRunner
+    from sparse_attn.ops.decode_fused import LINEAR_MAX_ROWS
+    from sparse_attn.ops.paged_region_kernels_nfa import nfa_args
+    from sparse_attn.patches.patch import register_patch
+    from sparse_attn.policies.region_geometry import RegionGeometry
+    from sparse_attn.scheduler.scheduler import ContinuousBatchScheduler
+
+    warm = args.warmup
+    b = len(lengths)
+    new_tokens = warm + args.steps + 8
+    cfg = llama31_8b_config(max(lengths), new_tokens)
+    t0 = time.perf_counter()
+    torch.manual_seed(args.seed)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            model = LlamaForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    fargs = nfa_args('tail')
+    fargs.tia_block_size = 16
+    n_patched = register_patch(model, fargs, rmsnorm_decode=True, decode_layers=True)
+    params = sum(p.numel() for p in model.parameters())
+    torch.cuda.synchronize()
+    print(f'# e2e batch model ready ({params / 1e9:.2f} B params) in '
+          f'{time.perf_counter() - t0:.1f}s', file=sys.stderr, flush=True)
+
+    page = 16
+    geo = RegionGeometry(sink=4, near=4096, window=128, page=page,
+                         max_new_tokens=new_tokens)
+    pages = sum((n + new_tokens + page - 1) // page for n in lengths)
+    cache = build_frozen_cache(model, geo, max(lengths), max_requests=b,
+                               max_visible_len=1024, physical_pages=pages + 8)
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    rids, firsts = [], []
+    t0 = time.perf_counter()
+    with torch.no_grad(), sdpa_kernel([SDPBackend.FLASH_ATTENTION,
+                                       SDPBackend.EFFICIENT_ATTENTION]):
+        for i, n in enumerate(lengths):
+            ids = torch.randint(0, cfg.vocab_size, (1, n), generator=gen, device=device)
+            out, audit = prefill_frozen_request(model, ids, None, geo, cache=cache)
+            rids.append(audit['request_id'])
+            firsts.append(int(out.logits[0, -1].argmax()))
+            del out, ids
+            print(f'# e2e batch prefill {i + 1}/{b}: {n} tokens', file=sys.stderr,
+                  flush=True)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    sched = ContinuousBatchScheduler(cache=cache, max_batch=b, eos_ids=(), pad_token_id=0)
+    for rid, tok in zip(rids, firsts):
+        sched.add_request(rid)
+        sched.next_tokens[rid] = tok
+    runner = GraphRunner(scheduler=sched, buckets=(b,), visible_buckets=(), device=device)
+    with torch.no_grad():
+        runner.capture_all(model, cache)
+        for i in range(warm):
+            runner.step(model, cache, generated_counts=i + 1)
+        torch.cuda.synchronize()
+        events = warm_events(torch, args.steps)
+        t0 = time.perf_counter()
+        for i, (a, e) in enumerate(events):
+            a.record()
+            runner.step(model, cache, generated_counts=warm + i + 1)
+            e.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    step = sorted(a.elapsed_time(e) for a, e in events)
+    med = step[len(step) // 2]
+    tokens = len(sched.flush_ready_receipts())
+    print(f'# e2e batch decode: median step {med:.3f} ms for {b} requests, '
+          f'wall {wall_ms:.3f} ms/step', file=sys.stderr, flush=True)
+    return {
+        'model': 'Llama-3.1-8B architecture, random-init bf16 weights',
+        'dense_layers': ('fused HIP decode layers' if b <= LINEAR_MAX_ROWS else
+                         f'HF modules (the fused HIP decode layers take up to '
+                         f'{LINEAR_MAX_ROWS} rows)'),
+        'params': params, 'patched_attention_layers': n_patched,
+        'prompt_tokens': list(lengths), 'prefill_s': round(prefill_s, 2),
+        'decode_steps': args.steps, 'warmup_steps': warm,
+        'step_ms_median': round(med, 4),
+        'step_ms_p10_p90': [round(step[len(step) // 10], 4),
+                            round(step[(len(step) * 9) // 10], 4)],
+        'wall_ms_per_step': round(wall_ms, 4),
+        'tok_s': round(b * 1e3 / med, 2),
+        'graph_replays': runner.replay_count,
+        'graph_eager_fallbacks': runner.eager_fallback_count,
+        'receipts': tokens,
+    }
+
+
 def end_to_end(torch, args, device):
     """Whole-model decode: random-init bf16 Qwen3-8B, dense prefill of
     ``args.ctx`` seeded uniform token ids into the paged cache, 3 warm-up
@@ -782,19 +900,28 @@ def main():
     geometry = {'heads': [w.hq, w.hkv], 'head_dim': w.d, 'page': w.page}
     lengths = list(w.lengths)
     e2e = None
-    if not args.no_e2e and single:
+    if not args.no_e2e:
         del graph, w, cache, outs
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
-        e2e = end_to_end(torch, args, device)
+        e2e = (end_to_end(torch, args, device) if single
+               else end_to_end_batch(torch, args, device, lengths))
 
-    if e2e is not None:
+    if e2e is not None and single:
         value, ms_per_step = e2e['tok_s'], e2e['tpot_ms_median']
         steps, warmup = args.steps, args.warmup
         headline = ('whole-model decode: random-init bf16 Qwen3-8B, dense prefill '
                     f'of {args.ctx} tokens, median TPOT over {steps} greedy steps '
                     'replayed from a hipGraph; hot path = selector + attention of '
                     f'{args.layers} layers')
+    elif e2e is not None:
+        value, ms_per_step = e2e['tok_s'], e2e['step_ms_median']
+        steps, warmup = args.steps, args.warmup
+        headline = (f'whole-model decode of {args.batch} ragged requests: random-init '
+                    'bf16 Llama-3.1-8B, one dense prefill per prompt, median step '
+                    f'time over {steps} greedy steps of the whole batch replayed from '
+                    f'a hipGraph, tok/s = {args.batch} / step; hot path = selector + '
+                    f'attention of {args.layers} layers')
     else:
         value, ms_per_step = hot_tok_s, hot['ms_per_step_median']
         steps, warmup = args.hot_steps, args.hot_warmup
@@ -815,7 +942,8 @@ def main():
         'dtype': 'bf16',
         'data': 'synthetic',
         'config': {
-            'workload': f'NFA sparse-attention decode, Qwen3-8B attention geometry, '
+            'workload': f'NFA sparse-attention decode, 32/8 heads, head_dim 128 '
+                        f'(Qwen3-8B and Llama-3.1-8B attention geometry), '
                         f'batch {args.batch}, '
                         + (f'contexts U({args.ragged[0]}, {args.ragged[1]})'
                            if args.ragged else f'{args.ctx // 1024}K context')

@@ -71,17 +71,21 @@ def _model_dims(model):
 
 
 def build_frozen_cache(model, geometry, sequence_capacity, *, max_requests=1,
-                       max_visible_len=None):
+                       max_visible_len=None, physical_pages=None):
     """Fixed-address cache for ``max_requests`` requests of up to
-    ``sequence_capacity`` prompt tokens plus ``geometry.max_new_tokens``."""
+    ``sequence_capacity`` prompt tokens plus ``geometry.max_new_tokens``.
+    ``physical_pages`` sizes the K/V arena when the requests together need
+    fewer pages than ``max_requests`` full-length ones (ragged batches)."""
     page = geometry.page
     max_blocks = (sequence_capacity + geometry.max_new_tokens + page - 1) // page + 8
     if max_visible_len is None:
         max_visible_len = sequence_capacity + geometry.max_new_tokens + 16
+    if physical_pages is None:
+        physical_pages = max_requests * max_blocks + 8
     cfg, hkv, head_dim, head_dim_v = _model_dims(model)
     return GraphReadyPagedRegionCache(
         cfg.num_hidden_layers, geometry, max_requests=max_requests,
-        max_physical_pages=max_requests * max_blocks + 8, max_blocks=max_blocks,
+        max_physical_pages=physical_pages, max_blocks=max_blocks,
         max_visible_len=max_visible_len, max_query_tokens=max_requests,
         num_kv_heads=hkv, num_query_heads=cfg.num_attention_heads,
         head_dim_k=head_dim, head_dim_v=head_dim_v, dtype=model.dtype,
