@@ -366,6 +366,26 @@ def selector_timeline(torch, w, steps, plan):
             ((tile[:, :, 4] - tile[:, :, 6]) * us).max())
         acc.setdefault('A tile slowest scoring tile', []).append(
             float(np.unravel_index(tile[:, :, 9].argmax(), tile.shape[:2])[1]))
+        # the tile that arrives last in each row, and the median tile: their
+        # start (from the kernel's first mark) and phase durations
+        live = tile[:, :, 4] > 0
+        arr = np.where(live, tile[:, :, 4], 0)
+        last_t = arr.argmax(axis=1)
+        rows_i = np.arange(tile.shape[0])
+        acc.setdefault('A last-arriving tile index (median row)', []).append(
+            float(np.median(last_t)))
+        for nm, sel in (('last tile', tile[rows_i, last_t]),):
+            acc.setdefault(f'A {nm}: start', []).append(
+                float(np.median((sel[:, 0] - start) * us)))
+            for k, name in enumerate(names):
+                acc.setdefault(f'A {nm}: {name}', []).append(
+                    float(np.median((sel[:, k + 1] - sel[:, k]) * us)))
+        dur = np.where(live, (tile[:, :, 4] - tile[:, :, 0]) * us, np.nan)
+        acc.setdefault('A tile duration (median tile)', []).append(
+            float(np.nanmedian(dur)))
+        st0 = np.where(live, (tile[:, :, 0] - start) * us, np.nan)
+        acc.setdefault('A tile start (median tile)', []).append(float(np.nanmedian(st0)))
+        acc.setdefault('A tile start (max)', []).append(float(np.nanmax(st0)))
         spans = [('tail L1 threshold', 0, 1),
                  ('  L1 thr: hist+keys load', 0, 24), ('  L1 thr: coarse bins', 24, 25),
                  ('  L1 thr: refine pass', 25, 26), ('  L1 thr: fine bins', 26, 1),

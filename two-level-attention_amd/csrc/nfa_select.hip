@@ -36,6 +36,7 @@
 #include "nfa_common.h"
 
 #include <atomic>
+#include <type_traits>
 #include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
@@ -76,8 +77,11 @@ struct SelDims {
   int prot;       // protected width = min(s_cap, sink + swa)
   int lds;        // LDS bytes per workgroup
   int multi;      // tiles may take several passes (second staging buffer)
+  int group;      // query heads per kv head
+  int hd_sh, bs_sh, page_sh;  // log2 of head_dim, bs, page, or -1
   // LDS: a common part, then the tile part, or the tail: its candidate pages,
   // then its L1 part or (later) its L2 part
+  int a_ctx;  // the row state wave 0 hands to the other waves
   int a_hist, a_tmp, a_misc, a_clk, a_qf, a_qs, a_qu, a_qg, a_fdims;
   int a_dims, a_last, a_tphys, a_stage, a_hs, a_st, a_st2;  // tile
   int a_pages, a_pphys;                                // tail
@@ -137,6 +141,7 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   const int s_cap = p.max_blocks * p.bs;
   s.prot = p.sink_tokens + p.swa < s_cap ? p.sink_tokens + p.swa : s_cap;
   int o = 0;
+  s.a_ctx = o;   o += align16(4 * 20);
   s.a_hist = o;  o += align16(4 * 4 * 256);
   s.a_tmp = o;   o += align16(4 * 128);
   s.a_misc = o;  o += align16(4 * 32);
@@ -194,6 +199,15 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
 __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   SelDims s;
   const int nrows = p.batch * p.hkv;
+  auto log2_or = [](int v) {
+    int sh = 0;
+    while ((1 << sh) < v) ++sh;
+    return v > 0 && (1 << sh) == v ? sh : -1;
+  };
+  s.group = p.hq / p.hkv;
+  s.hd_sh = log2_or(p.head_dim);
+  s.bs_sh = log2_or(p.bs);
+  s.page_sh = log2_or(p.page);
   s.tcap = cus / nrows > 1 ? cus / nrows : 1;
   s.clk_tiles = (p.max_blocks + kSpanMin - 1) / kSpanMin;
   {
@@ -235,29 +249,64 @@ struct RowGeo {
 __device__ __forceinline__ int imin(int a, int b) { return a < b ? a : b; }
 __device__ __forceinline__ int imax(int a, int b) { return a > b ? a : b; }
 
-__device__ __forceinline__ RowGeo row_geo(const NfaSelectParams &p, int L,
-                                          bool skip_far, bool skip_near) {
+// x / d with C's truncation toward zero; sh = log2(d) when d is a power of
+// two (a shift instead of the division sequence), else -1
+__device__ __forceinline__ int div_p2(int x, int d, int sh) {
+  if (sh < 0) return x / d;
+  return x >= 0 ? (x >> sh) : -((-x) >> sh);
+}
+
+__device__ __forceinline__ RowGeo row_geo(const NfaSelectParams &p, const SelDims &sd,
+                                          int L, bool skip_far, bool skip_near) {
   RowGeo g;
   const int bs = p.bs;
+  auto dbs = [&](int x) { return div_p2(x, bs, sd.bs_sh); };
   const int pool_near_len = imax(bs, p.near_len);
   g.L = L;
-  g.kt_eff = L > 0 ? (L + bs - 1) / bs : 0;
-  g.spl = p.sink_tokens / bs;
-  g.near_start = imax((L - p.geo_window - pool_near_len) / bs, g.spl);
-  g.swa_lo_blk = imax(g.near_start, g.kt_eff - imax(1, p.geo_window / bs));
+  g.kt_eff = L > 0 ? dbs(L + bs - 1) : 0;
+  g.spl = dbs(p.sink_tokens);
+  g.near_start = imax(dbs(L - p.geo_window - pool_near_len), g.spl);
+  g.swa_lo_blk = imax(g.near_start, g.kt_eff - imax(1, dbs(p.geo_window)));
   g.far_end = imin(g.kt_eff, g.near_start);
   g.near_end = g.swa_lo_blk;
   g.far_on = !skip_far;
   g.near_on = !skip_near;
   g.sink_hi = imin(p.geo_sink, L);
   g.swa_hi = imax(g.sink_hi, L - p.geo_window);
-  const int far_blk = (L - p.geo_window - p.geo_near) / p.page;
+  const int far_blk = div_p2(L - p.geo_window - p.geo_near, p.page, sd.page_sh);
   g.orig_far_hi = imin(g.swa_hi, imax(g.sink_hi, far_blk * p.page));
   const int swa_lo_tok = imax(L - p.geo_window, 0);
-  g.byp_blk = swa_lo_tok / bs;
-  g.sink_unaligned = (p.geo_sink % bs) != 0;
-  g.byp_cond = (swa_lo_tok % bs != 0) && (g.byp_blk >= g.spl);
+  g.byp_blk = dbs(swa_lo_tok);
+  g.sink_unaligned = (p.geo_sink - dbs(p.geo_sink) * bs) != 0;
+  g.byp_cond = (swa_lo_tok - g.byp_blk * bs != 0) && (g.byp_blk >= g.spl);
   if (g.sink_unaligned) g.byp_cond = g.byp_cond && (g.byp_blk != g.spl);
+  return g;
+}
+
+// The row geometry wave 0 stored at s_ctx[8..20) (int4 words 2..4), as
+// wave-uniform values, with the given pool switches.
+__device__ __forceinline__ RowGeo ctx_geo(const int *s_ctx, int L, bool far_on,
+                                          bool near_on) {
+  const int4 *c4 = reinterpret_cast<const int4 *>(s_ctx);
+  const int4 e = c4[2], f = c4[3], h = c4[4];
+  auto u = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+  RowGeo g;
+  g.L = L;
+  g.kt_eff = u(e.x);
+  g.near_start = u(e.y);
+  g.swa_lo_blk = u(e.z);
+  g.far_end = u(e.w);
+  g.near_end = u(f.x);
+  g.sink_hi = u(f.y);
+  g.swa_hi = u(f.z);
+  g.orig_far_hi = u(f.w);
+  g.spl = u(h.x);
+  g.byp_blk = u(h.y);
+  const int fl = u(h.z);
+  g.byp_cond = (fl & 1) != 0;
+  g.sink_unaligned = (fl & 2) != 0;
+  g.far_on = far_on;
+  g.near_on = near_on;
   return g;
 }
 
@@ -671,41 +720,6 @@ __device__ __forceinline__ void stats_latest_page(
     s_last[DSUB + d] = Elem<KV>::load(&c);
     s_last[2 * DSUB + d] = Elem<KV>::load(&s);
   }
-}
-
-// Statistics of the latest page after appending token L-1, thread d < DSUB:
-// the sequential min / max / sum continue from the stored min and max (exact
-// KV values) and the fp32 running sum of the page (the stored sum is
-// rounded), or start over when the token opens a new page.  `row` is the
-// token's key row.
-template <int DSUB, typename KV>
-__device__ __forceinline__ void stats_append_token(const NfaSelectParams &p,
-                                                   int64_t req, int kv, int L,
-                                                   int pg, const KV *row,
-                                                   const int *s_dims) {
-  const int d = threadIdx.x;
-  const int64_t si = stat_index<KV>(p, req, kv, d, pg, DSUB);
-  float *psum = p.page_sum_l + (req * p.hkv + kv) * DSUB;
-  KV *smin = (KV *)p.stat_min_l;
-  KV *smax = (KV *)p.stat_max_l;
-  KV *ssum = (KV *)p.stat_sum_l;
-  const bool first = (L - 1) % p.bs == 0;
-  float mn = __uint_as_float(0x7F800000u);
-  float mx = __uint_as_float(0xFF800000u);
-  float sm = 0.0f;
-  if (!first) {
-    mn = Elem<KV>::load(smin + si);
-    mx = Elem<KV>::load(smax + si);
-    sm = psum[d];
-  }
-  const float x = Elem<KV>::load(row + s_dims[d]);
-  mn = (x < mn) ? x : mn;
-  mx = (x > mx) ? x : mx;
-  sm = sm + x;
-  smin[si] = (KV)Elem<KV>::from_f32(mn);
-  smax[si] = (KV)Elem<KV>::from_f32(mx);
-  ssum[si] = (KV)Elem<KV>::from_f32(sm);
-  psum[d] = sm;
 }
 
 // LDS byte address of a pointer into the workgroup's LDS.
@@ -1322,13 +1336,15 @@ __global__ void __launch_bounds__(SB)
   float *s_stage = (float *)(smem + sd.a_stage);
 
   const int tid = threadIdx.x;
-  // tile-major grid: the first dispatch round holds the low tiles of every
-  // row, and a row's tiles share an XCD (workgroups go round-robin over XCDs)
-  const int row = blockIdx.x;
-  const int tile = blockIdx.y;
-  const int b = row / p.hkv;
-  const int kv = row % p.hkv;
-  const int G = p.hq / p.hkv;
+  // grid (kv, batch row, tile): workgroup kv + hkv * (b + batch * tile) is
+  // number row + rows * tile (row = b * hkv + kv), so the first dispatch
+  // round holds the low tiles of every row and a row's tiles share an XCD
+  // (workgroups go round-robin over the XCDs)
+  const int kv = blockIdx.x;
+  const int b = blockIdx.y;
+  const int tile = blockIdx.z;
+  const int row = b * p.hkv + kv;
+  const int G = sd.group;
   const int bs = p.bs;
   const int mb = p.max_blocks;
 
@@ -1343,9 +1359,12 @@ __global__ void __launch_bounds__(SB)
   int *g_hist = (int *)(ws + sd.w_hist) + (int64_t)row * 512;
   uint16_t *g_keys = (uint16_t *)(ws + sd.w_keys) + (int64_t)row * sd.kstride;
 
-  // ---- first round trip: every load that depends on no other ------------
-  // vector loads first (unconditional, clamped indices), then the row state
-  // through the scalar cache
+  // ---- first round trip ---------------------------------------------------
+  // Wave 0 alone reads the row state through the scalar cache and derives
+  // the row's uniform geometry (tile split, pool boundaries), which it hands
+  // to the other waves through LDS: uniform integer work executed by every
+  // wave would cost each SIMD four times its issue slots.  Meanwhile every
+  // wave loads its share of the query rows.
   const int dim_v = p.dims[imin(tid, DSUB - 1)];
   const int fdim_v = p.fine_dims[imin(tid, p.fine_dsub - 1)];
   // the kv group's query rows, whole (the L1 dims are gathered from LDS):
@@ -1360,32 +1379,45 @@ __global__ void __launch_bounds__(SB)
 #pragma unroll
   for (int k = 0; k < kQRawPerThread; ++k) {
     const int i = imin(tid + k * SB, nq - 1);
-    const int64_t byte = (qrow + (int64_t)(i / hd) * p.q_stride_h + i % hd) << qsh;
+    const int j = div_p2(i, hd, sd.hd_sh);
+    const int64_t byte = (qrow + (int64_t)j * p.q_stride_h + (i - j * hd)) << qsh;
     qodd[k] = (int)(byte & 2);
     qbits[k] = *(const uint32_t *)((const unsigned char *)p.q + (byte & ~(int64_t)3));
   }
-  int32_t L, slot_b;
-  int64_t act64, req;
-  sload_row(p.lengths + b, p.active_req + b, p.valid_req + b,
-            p.k_new != nullptr ? p.slots + b : p.lengths + b, L, act64, req, slot_b);
-  const bool active = act64 >= 0;
-  if (p.k_new == nullptr) slot_b = -1;
-  const int32_t *btr = p.block_table_l + req * mb;
-  // pages past the block-table width are never scored (selector:205-206)
-  const int kt_eff = imin(L > 0 ? (L + bs - 1) / bs : 0, mb);
-  // this tile's pages [t0, t1); tiles past the row's pages take no part,
-  // neither scores nor arrival
-  const TileSplit split = tile_split(kt_eff, sd.tcap);
-  if (tile >= split.tiles) return;
-  // the pages spread evenly, the first kt % tiles tiles one page more (at
-  // 128K: one tile of 257 pages and 31 of 256, four 64-page groups per
-  // scoring round, where 257 everywhere took a second round for one page)
-  const int t_base = kt_eff / split.tiles;
-  const int t_rem = kt_eff % split.tiles;
-  const int t0 = tile * t_base + imin(tile, t_rem);
-  const int t1 = t0 + t_base + (tile < t_rem ? 1 : 0);
-  const int last_blk = L > 0 ? (L - 1) / bs : -1;
-  const bool owns_last = last_blk >= t0 && last_blk < t1;
+  int *s_ctx = (int *)(smem + sd.a_ctx);
+  if (wave_id() == 0) {
+    int32_t L0, slot0;
+    int64_t act0, req0;
+    sload_row(p.lengths + b, p.active_req + b, p.valid_req + b,
+              p.k_new != nullptr ? p.slots + b : p.lengths + b, L0, act0, req0, slot0);
+    if (p.k_new == nullptr) slot0 = -1;
+    // pages past the block-table width are never scored (selector:205-206)
+    const int kt0 = imin(L0 > 0 ? div_p2(L0 + bs - 1, bs, sd.bs_sh) : 0, mb);
+    const TileSplit sp = tile_split(kt0, sd.tcap);
+    // this tile's pages [t0, t1): the pages spread evenly, the first
+    // kt % tiles tiles one page more (at 128K: one tile of 257 pages and 31
+    // of 256, four 64-page groups per scoring round, where 257 everywhere
+    // took a second round for one page)
+    int t0v = 0, t1v = 0;
+    if (tile < sp.tiles) {
+      const int t_base = kt0 / sp.tiles;
+      const int t_rem = kt0 - t_base * sp.tiles;
+      t0v = tile * t_base + imin(tile, t_rem);
+      t1v = t0v + t_base + (tile < t_rem ? 1 : 0);
+    }
+    // the pools without skip flags (a superset of the final ones): the
+    // first statistics are staged from them before the flags arrive
+    const RowGeo g = row_geo(p, sd, L0, false, false);
+    if (lane_id() == 0) {
+      int4 *c4 = reinterpret_cast<int4 *>(s_ctx);
+      c4[0] = make_int4(L0, act0 >= 0 ? 1 : 0, (int)req0, (int)(req0 >> 32));
+      c4[1] = make_int4(slot0, sp.tiles, t0v, t1v);
+      c4[2] = make_int4(g.kt_eff, g.near_start, g.swa_lo_blk, g.far_end);
+      c4[3] = make_int4(g.near_end, g.sink_hi, g.swa_hi, g.orig_far_hi);
+      c4[4] = make_int4(g.spl, g.byp_blk,
+                        (g.byp_cond ? 1 : 0) | (g.sink_unaligned ? 2 : 0), 0);
+    }
+  }
   // LDS: dims, fine dims, raw query rows, histogram
   float *s_qraw = s_stage;  // until the statistics phase
   if (tid < DSUB) s_dims[tid] = dim_v;
@@ -1399,15 +1431,48 @@ __global__ void __launch_bounds__(SB)
     }
   }
   if (tid < 512) s_hist[tid] = 0;
-  // the tile's first statistics are requested as soon as the query words
-  // are consumed (a later wait of the compiler's for a load of the wave
-  // also waits for these copies): speculative, the pools without skip flags
-  // contain the final ones
-  const RowGeo g0 = row_geo(p, L, false, false);
-  unsigned char *s_st = smem + sd.a_st;
-  if constexpr (STG) stage_stats_async(p, g0, req, kv, t0, pass_end(t0, t1), s_st);
   lds_barrier();
   NFA_MARK(0, 1);
+  int32_t L, slot_b, t0, t1, kt_eff;
+  int64_t req;
+  bool active;
+  TileSplit split;
+  {
+    const int4 *c4 = reinterpret_cast<const int4 *>(s_ctx);
+    const int4 a = c4[0], c = c4[1];
+    auto u = [](int v) { return __builtin_amdgcn_readfirstlane(v); };
+    L = u(a.x);
+    active = u(a.y) != 0;
+    req = (int64_t)(((uint64_t)(uint32_t)u(a.w) << 32) | (uint32_t)u(a.z));
+    slot_b = u(c.x);
+    split.tiles = u(c.y);
+    t0 = u(c.z);
+    t1 = u(c.w);
+    kt_eff = u(c4[2].x);
+  }
+  // tiles past the row's pages take no part, neither scores nor arrival
+  if (tile >= split.tiles) return;
+  const int32_t *btr = p.block_table_l + req * mb;
+  const int last_blk = L > 0 ? div_p2(L - 1, bs, sd.bs_sh) : -1;
+  const bool owns_last = last_blk >= t0 && last_blk < t1;
+
+  // ---- second round trip, issued now and waited for with the first staged
+  //      statistics: previous statistics length, skip flags and the physical
+  //      page of the decode token.  Vector loads (a lane offset the compiler
+  //      cannot prove uniform), so that the LDS accesses below wait for none
+  //      of them.
+  int vz = 0;
+  asm volatile("" : "+v"(vz));
+  const int lp_last = owns_last ? imin(div_p2(L - 1, p.page, sd.page_sh), mb - 1) : 0;
+  const int prev_v = p.stats_len_l[req + vz];
+  const int skf_v = p.skip_far_l[req + vz];
+  const int skn_v = p.skip_near_l[req + vz];
+  const int phl_v = btr[lp_last + vz];
+
+  // the tile's first statistics, staged by asynchronous copies into LDS
+  unsigned char *s_st = smem + sd.a_st;
+  if constexpr (STG)
+    stage_stats_async(p, ctx_geo(s_ctx, L, true, true), req, kv, t0, pass_end(t0, t1), s_st);
 
   // scaled, bf16-rounded query rows of this kv group (selector:943-963), and
   // their negative and positive parts
@@ -1437,19 +1502,17 @@ __global__ void __launch_bounds__(SB)
     const bool all = __ballot(!ok) == 0;
     if (lane_id() == 0) s_misc[5] = all ? p.fine_dsub / CH : 0;
   }
-  lds_barrier();  // the query rows; the raw rows' LDS is free again
+  // (the first pass's barrier orders these LDS writes before their reads;
+  // the query rows' LDS is reused only after it)
   NFA_MARK(0, 2);
 
-  // ---- second round trip: request state --------------------------------
+  // ---- request state ------------------------------------------------------
   const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
   const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
-  int32_t prev, skf, skn, ph_last;
-  sload_i32x4(p.stats_len_l + req, p.skip_far_l + req, p.skip_near_l + req,
-              btr + (owns_last ? imin((L - 1) / p.page, mb - 1) : 0), prev, skf,
-              skn, ph_last);
-  const bool skip_far = skf != 0;
-  const bool skip_near = skn != 0;
-  if (!(owns_last && active)) ph_last = 0;
+  const int32_t prev = __builtin_amdgcn_readfirstlane(prev_v);
+  const bool skip_far = __builtin_amdgcn_readfirstlane(skf_v) != 0;
+  const bool skip_near = __builtin_amdgcn_readfirstlane(skn_v) != 0;
+  const int32_t ph_last = owns_last && active ? __builtin_amdgcn_readfirstlane(phl_v) : 0;
   // the decode token's key row is read from k_new for the statistics when
   // the fused write targets the slot of token L-1
   const KV *new_row = nullptr;
@@ -1459,39 +1522,86 @@ __global__ void __launch_bounds__(SB)
         slot_b == ph_last * p.page + (L - 1) % p.page)
       new_row = (const KV *)p.k_new + ((int64_t)b * p.hkv + kv) * p.head_dim;
   }
-  // decode write of the current token (selector:1030-1061), fire and forget
-  if (p.k_new != nullptr && active && owns_last) decode_write<KV>(p, b, kv);
 
   // ---- page statistics: latest page, or the whole tile on a rebuild -----
   const bool do_stats = active && L > 0 && !(skip_far && skip_near);
   const bool incremental = prev > 0 && L == prev + 1;
   const bool page_phys = (p.page % bs) == 0;
   const KV *kpool = (const KV *)p.k_pool_l;
-  if (do_stats && incremental && owns_last) {
-    if (__builtin_expect(p.page_sum_l != nullptr, 1)) {
-      if (tid < DSUB)
-        stats_append_token<DSUB, KV>(
-            p, req, kv, L, last_blk,
-            new_row != nullptr ? new_row
-                               : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page),
-            s_dims);
-    } else {
-      stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims,
-                                  s_stage, new_row, s_last);
+  // The latest page is never in a pool (it lies in the window:
+  // swa_lo_blk <= kt_eff - 1), so the decode token's statistics append, its
+  // L2 side row and the decode K/V write complete after the scores, their
+  // loads in flight meanwhile; only the recompute path without the fp32
+  // running sums stays in front.
+  const bool owner_late = do_stats && incremental && owns_last && p.page_sum_l != nullptr;
+  if (do_stats && incremental && owns_last && NFA_COLD(p.page_sum_l == nullptr)) {
+    __syncthreads();  // the query preparation has read the raw rows in s_stage
+    stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims, s_stage,
+                                new_row, s_last);
+  }
+  // The owner's decode K/V write, statistics append and L2 side row: loads
+  // issued once the first pass's statistics have landed (no staging wait
+  // waits for them), stores after that pass's scores.
+  const bool dw = p.k_new != nullptr && active && owns_last;
+  const bool side_late = do_stats && incremental && owns_last && p.l2_keys_l != nullptr;
+  const bool owner_any = dw || owner_late || side_late;
+  KV dw_k = 0, dw_v = 0, side_raw = 0;
+  float ap_mn = __uint_as_float(0x7F800000u);  // a new page starts from +inf,
+  float ap_mx = __uint_as_float(0xFF800000u);  // -inf and 0
+  float ap_sm = 0.0f, ap_x = 0.0f;
+  auto owner_finish = [&]() {
+    if (dw && slot_b >= 0 && slot_b / p.page < p.pool_pages) {
+      // decode write of the current token (selector:1030-1061)
+      const int phys = slot_b / p.page;
+      const int off = slot_b % p.page;
+      if (tid < p.head_dim) ((KV *)p.k_pool_l)[kv_offset(p, phys, kv, off) + tid] = dw_k;
+      if (tid < p.head_dim_v)
+        ((KV *)p.v_pool_l)[(((int64_t)phys * p.hkv + kv) * p.page + off) * p.head_dim_v +
+                           tid] = dw_v;
     }
-    if (p.l2_keys_l != nullptr && tid < p.fine_dsub) {
+    if (owner_late && tid < DSUB) {
+      // the token's dims continue the page's min / max exactly and the fp32
+      // running sum sequentially (selector:32-131)
+      const int64_t si = stat_index<KV>(p, req, kv, tid, last_blk, DSUB);
+      const float x = ap_x;
+      const float mn = (x < ap_mn) ? x : ap_mn;
+      const float mx = (x > ap_mx) ? x : ap_mx;
+      const float sm = ap_sm + x;
+      ((KV *)p.stat_min_l)[si] = (KV)Elem<KV>::from_f32(mn);
+      ((KV *)p.stat_max_l)[si] = (KV)Elem<KV>::from_f32(mx);
+      ((KV *)p.stat_sum_l)[si] = (KV)Elem<KV>::from_f32(sm);
+      p.page_sum_l[(req * p.hkv + kv) * DSUB + tid] = sm;
+    }
+    if (side_late && tid < p.fine_dsub) {
       // the new token's L2 side row (its 4-bit codes: lanes 0-31 of wave 0)
-      const KV *src = new_row != nullptr
-                          ? new_row
-                          : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page);
       if (p.l2_quant) {
-        q4_store_lanes(p, req, kv, L - 1, Elem<KV>::load(src + s_fdims[tid]), tid);
+        q4_store_lanes(p, req, kv, L - 1, Elem<KV>::load(&side_raw), tid);
       } else {
-        ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)] = src[s_fdims[tid]];
+        ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)] = side_raw;
       }
     }
-  }
-  const RowGeo geo = row_geo(p, L, skip_far, skip_near);
+  };
+  auto owner_prefetch = [&]() {
+    if (dw) {
+      const int64_t nb = (int64_t)b * p.hkv + kv;
+      if (tid < p.head_dim) dw_k = ((const KV *)p.k_new)[nb * p.head_dim + tid];
+      if (tid < p.head_dim_v) dw_v = ((const KV *)p.v_new)[nb * p.head_dim_v + tid];
+    }
+    const KV *trow = new_row != nullptr
+                         ? new_row
+                         : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page);
+    if (owner_late && tid < DSUB) {
+      if ((L - 1) % bs != 0) {
+        const int64_t si = stat_index<KV>(p, req, kv, tid, last_blk, DSUB);
+        ap_mn = Elem<KV>::load((const KV *)p.stat_min_l + si);
+        ap_mx = Elem<KV>::load((const KV *)p.stat_max_l + si);
+        ap_sm = p.page_sum_l[(req * p.hkv + kv) * DSUB + tid];
+      }
+      ap_x = Elem<KV>::load(trow + s_dims[tid]);
+    }
+    if (side_late && tid < p.fine_dsub) side_raw = trow[s_fdims[tid]];
+  };
+  const RowGeo geo = ctx_geo(s_ctx, L, !skip_far, !skip_near);
   float *s_hs = (float *)(smem + sd.a_hs);  // [head][page] bf16 head scores
   const int lpp_log = G <= 1 ? 0 : G <= 2 ? 1 : G <= 4 ? 2 : 3;
   const int lpp = 1 << lpp_log;  // lanes per page
@@ -1502,10 +1612,14 @@ __global__ void __launch_bounds__(SB)
   // The next pass's statistics, pages [n0, n1), are copied into nst while
   // this pass is scored (not on a rebuild, which restages each pass after
   // recomputing it)
-  auto run_pass = [&](int c0, int c1, unsigned char *st, int n0, int n1,
+  // `first` (std::true_type for the tile's first pass only) compiles the
+  // owner's work into that pass alone
+  auto run_pass = [&](auto first, int c0, int c1, unsigned char *st, int n0, int n1,
                       unsigned char *nst) {
+    constexpr bool kFirst = decltype(first)::value;
     NFA_MARK(0, 7);
     if (NFA_COLD(do_stats && !incremental)) {
+      __syncthreads();  // the query preparation has read the raw rows in s_stage
       float *psum_row = p.page_sum_l != nullptr
                             ? p.page_sum_l + (req * p.hkv + kv) * DSUB
                             : nullptr;
@@ -1588,6 +1702,7 @@ __global__ void __launch_bounds__(SB)
     }
     lds_barrier();
     NFA_MARK(0, 3);
+    if (kFirst && owner_any) owner_prefetch();
     if constexpr (STG && MULTI) {
       // every wave has finished the previous pass, which read nst
       if (n0 < n1 && !(do_stats && !incremental))
@@ -1656,6 +1771,9 @@ __global__ void __launch_bounds__(SB)
         if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
       }
     }
+    // the owner's decode write, statistics append and L2 side row, once:
+    // the loaded values are dead before any further pass
+    if (kFirst && owner_any) owner_finish();
     lds_barrier();
     NFA_MARK(0, 5);
     NFA_MARK(0, 6);
@@ -1670,7 +1788,7 @@ __global__ void __launch_bounds__(SB)
     unsigned char *st = s_st;
     unsigned char *nst = smem + sd.a_st2;
     int c1 = pass_end(t0, t1);
-    run_pass(t0, c1, st, c1, c1 < t1 ? pass_end(c1, t1) : c1, nst);
+    run_pass(std::true_type{}, t0, c1, st, c1, c1 < t1 ? pass_end(c1, t1) : c1, nst);
     if constexpr (MULTI) {
       // long rows and many rows: further passes instead of dispatch rounds,
       // the staging buffers alternating
@@ -1679,7 +1797,7 @@ __global__ void __launch_bounds__(SB)
         unsigned char *tmp = st;
         st = nst;
         nst = tmp;
-        run_pass(c0, c1, st, c1, c1 < t1 ? pass_end(c1, t1) : c1, nst);
+        run_pass(std::false_type{}, c0, c1, st, c1, c1 < t1 ? pass_end(c1, t1) : c1, nst);
       }
     }
   }
@@ -2441,12 +2559,11 @@ static hipError_t lds_optin(const void *kernel, std::atomic<uint64_t> &done) {
 template <int DSUB, typename KV>
 static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
                                 hipStream_t stream) {
-  const int rows = p.batch * p.hkv;
   // one pass per tile whenever a dispatch round of single-pass tiles covers
   // the widest possible row; several passes stage the next pass's statistics
   // in a second LDS buffer (beyond 64 KiB)
   const bool multi = sd.multi != 0;
-  const dim3 grid(rows, sd.ntiles);
+  const dim3 grid(p.hkv, p.batch, sd.ntiles);
   if (sd.lds > 64 * 1024) {
     static std::atomic<uint64_t> optin[4];
     const bool top2 = p.far_method == NFA_METHOD_AVG_TOP2;
