@@ -184,11 +184,24 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   float *part = (float *)(ws + ad.w_part) +
                 ((int64_t)vrow * ad.nsplit + split) * ad.part_stride;
 
+  // Query row t usually reads gather row t (query_to_req is the identity at
+  // decode): that row's visible length and this thread's slot of the first
+  // chunk are loaded together with query_to_req, and used when it agrees,
+  // instead of three dependent round trips.
+  const int spec = !PART && t < p.gather_rows ? t : -1;
+  const int spec_i = split * ad.split + tid;  // first chunk's slot of this thread
+  int spec_n = 0, spec_slot = -1;
+  if (spec >= 0) {
+    spec_n = p.vis_lens[spec * p.hkv + kh];
+    if (tid < ad.split && spec_i < p.max_vis)
+      spec_slot = p.gather[((int64_t)spec * p.hkv + kh) * p.max_vis + spec_i];
+  }
   int req = p.query_to_req[t];
   if (req >= p.gather_rows) req = -1;  // out-of-range rows act as padding
+  const bool spec_ok = spec >= 0 && req == spec;
   int n = 0;
   if (req >= 0) {
-    n = p.vis_lens[req * p.hkv + kh];
+    n = spec_ok ? spec_n : p.vis_lens[req * p.hkv + kh];
     if (n > p.max_vis) n = p.max_vis;
   }
   // chunks split, split + nsplit, ... of ad.split slots each; the running
@@ -229,7 +242,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     const int cn = c_end - c0 < ad.split ? c_end - c0 : ad.split;
     if (LOOP && c0 != c_first) __syncthreads();  // the previous chunk's readers are done
     for (int i = tid; i < cn; i += NFA_BLOCK) {
-      const int sl = grow[c0 + i];
+      const int sl = spec_ok && c0 == c_first ? spec_slot : grow[c0 + i];
       s_slot[i] = sl < max_slot ? sl : -1;
     }
     __syncthreads();
@@ -320,6 +333,31 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       // (weights past cn are 0 and their V rows are never staged: skipped)
       float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
       const float4 *pw = reinterpret_cast<const float4 *>(s_p + g * kSplitMax);
+      if (cn == kSplitMax) {
+        // a full chunk: sixteen slots' weights and V pairs requested before
+        // their multiply-adds (one LDS round trip per sixteen slots, not per
+        // four), the same two chains in the same order as below
+#pragma unroll
+        for (int j0 = 0; j0 < kSplitMax; j0 += 16) {
+          float4 w4[4];
+          float va[16], vb[16];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) w4[u] = pw[j0 / 4 + u];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) lds_pair(s_v + (j0 + u) * D, d, &va[u], &vb[u]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            a0 = fmaf(w4[u].x, va[4 * u], a0);
+            a1 = fmaf(w4[u].x, vb[4 * u], a1);
+            b0 = fmaf(w4[u].y, va[4 * u + 1], b0);
+            b1 = fmaf(w4[u].y, vb[4 * u + 1], b1);
+            a0 = fmaf(w4[u].z, va[4 * u + 2], a0);
+            a1 = fmaf(w4[u].z, vb[4 * u + 2], a1);
+            b0 = fmaf(w4[u].w, va[4 * u + 3], b0);
+            b1 = fmaf(w4[u].w, vb[4 * u + 3], b1);
+          }
+        }
+      } else
       for (int j = 0; j < cn; j += 4) {
         const float4 w4 = pw[j / 4];
         float v0, v1, u0, u1;
