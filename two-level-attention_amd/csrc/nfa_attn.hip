@@ -184,6 +184,16 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   float *part = (float *)(ws + ad.w_part) +
                 ((int64_t)vrow * ad.nsplit + split) * ad.part_stride;
 
+  // the query rows of the group, requested first (they depend on nothing;
+  // stored to LDS once the row's metadata is in)
+  constexpr int QPT = (AGMAX * DK + NFA_BLOCK - 1) / NFA_BLOCK;
+  float qv[QPT];
+#pragma unroll
+  for (int k = 0; k < QPT; ++k) {
+    const int i = tid + k * NFA_BLOCK;
+    qv[k] = i < G * DK ? load_any(p.q, ((int64_t)t * p.hq + kh * G) * DK + i, p.q_dtype)
+                       : 0.0f;
+  }
   // Query row t usually reads gather row t (query_to_req is the identity at
   // decode): that row's visible length and this thread's slot of the first
   // chunk are loaded together with query_to_req, and used when it agrees,
@@ -218,8 +228,11 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const int c_first = lo + split * ad.split;
   const int c_step = ad.nsplit * ad.split;
   if (c_first < c_end) {
-    for (int i = tid; i < G * DK; i += NFA_BLOCK)
-      s_q[i] = load_any(p.q, ((int64_t)t * p.hq + kh * G) * DK + i, p.q_dtype);
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+      const int i = tid + k * NFA_BLOCK;
+      if (i < G * DK) s_q[i] = qv[k];
+    }
   }
   if (tid < G) {
     s_m[tid] = kNegInf;
