@@ -141,7 +141,7 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   const int s_cap = p.max_blocks * p.bs;
   s.prot = p.sink_tokens + p.swa < s_cap ? p.sink_tokens + p.swa : s_cap;
   int o = 0;
-  s.a_ctx = o;   o += align16(4 * 20);
+  s.a_ctx = o;   o += align16(4 * 24);
   s.a_hist = o;  o += align16(4 * 4 * 256);
   s.a_tmp = o;   o += align16(4 * 128);
   s.a_misc = o;  o += align16(4 * 32);
@@ -1512,6 +1512,7 @@ __global__ void __launch_bounds__(SB)
   const int32_t prev = __builtin_amdgcn_readfirstlane(prev_v);
   const bool skip_far = __builtin_amdgcn_readfirstlane(skf_v) != 0;
   const bool skip_near = __builtin_amdgcn_readfirstlane(skn_v) != 0;
+  if (tid == 0) s_ctx[23] = (skip_far ? 1 : 0) | (skip_near ? 2 : 0);  // for the tail
   const int32_t ph_last = owns_last && active ? __builtin_amdgcn_readfirstlane(phl_v) : 0;
   // the decode token's key row is read from k_new for the statistics when
   // the fused write targets the slot of token L-1
@@ -1824,6 +1825,51 @@ __global__ void __launch_bounds__(SB)
   if (!arrive_last(&row_cnt[row], (unsigned int)split.tiles, &s_misc[0])) return;
 
   // =========================== tail ======================================
+  // The tail re-derives its state: the kernel arguments read again through
+  // a pointer the compiler cannot fold into the tile stage's copies, the row
+  // state from what wave 0 left in LDS.  Nothing of the tile stage stays live
+  // across the arrival (scalar registers are the scarce resource of this
+  // kernel: every value held across it is spilled and reloaded in the tail).
+  {
+  typedef __attribute__((address_space(4))) const NfaSelectParams ParamsK;
+  typedef __attribute__((address_space(4))) const SelDims DimsK;
+  ParamsK *pk = (ParamsK *)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(pk));
+  constexpr size_t kSdOff =
+      (sizeof(NfaSelectParams) + alignof(SelDims) - 1) / alignof(SelDims) * alignof(SelDims);
+  DimsK *dk = (DimsK *)((__attribute__((address_space(4))) const char *)pk + kSdOff);
+  // generic pointers cast from the hidden constant-space ones: after
+  // inlining, the loads are scalar loads from the kernel argument segment
+  const NfaSelectParams &p = *(const NfaSelectParams *)pk;
+  const SelDims &sd = *(const SelDims *)dk;
+  const int tid = threadIdx.x;
+  const int kv = blockIdx.x;
+  const int b = blockIdx.y;
+  const int row = b * p.hkv + kv;
+  const int bs = p.bs;
+  const int mb = p.max_blocks;
+  const int *s_ctx = (const int *)(smem + sd.a_ctx);
+  const int L = __builtin_amdgcn_readfirstlane(s_ctx[0]);
+  const int64_t req = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(s_ctx[3]) << 32) |
+                                (uint32_t)__builtin_amdgcn_readfirstlane(s_ctx[2]));
+  const int kt_eff = __builtin_amdgcn_readfirstlane(s_ctx[8]);
+  const int skf = __builtin_amdgcn_readfirstlane(s_ctx[23]);
+  const bool skip_far = (skf & 1) != 0;
+  const bool skip_near = (skf & 2) != 0;
+  const RowGeo geo = ctx_geo(s_ctx, L, !skip_far, !skip_near);
+  const int32_t *btr = p.block_table_l + req * mb;
+  const bool page_phys = (p.page % bs) == 0;
+  const KV *kpool = (const KV *)p.k_pool_l;
+  unsigned char *ws = (unsigned char *)p.workspace;
+  int *g_hist = (int *)(ws + sd.w_hist) + (int64_t)row * 512;
+  uint16_t *g_keys = (uint16_t *)(ws + sd.w_keys) + (int64_t)row * sd.kstride;
+  int *s_hist = (int *)(smem + sd.a_hist);
+  int *s_tmp = (int *)(smem + sd.a_tmp);
+  int *s_misc = (int *)(smem + sd.a_misc);
+  float *s_qg = (float *)(smem + sd.a_qg);
+  int *s_fdims = (int *)(smem + sd.a_fdims);
+  int64_t *s_clk = (int64_t *)(smem + sd.a_clk);
+  const int64_t clk_tail = ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32;
   // (its LDS overlaps the tile stage's private part, no longer used)
   uint16_t *s_keys = (uint16_t *)(smem + sd.a_keys);
   const bool dbg = p.dbg_i_f != nullptr;
@@ -2422,6 +2468,7 @@ __global__ void __launch_bounds__(SB)
   if (tid == 0) p.vis_lens[b * p.hkv + kv] = nkeep + nu;
   NFA_MARK(32, 13);
   NFA_FLUSH(32, clk_tail);
+  }  // tail
 }
 
 
