@@ -271,8 +271,10 @@ int32_t nfa_select_layer(const NfaSelectParams *p, void *stream);
    scratch is a static device array of NFA_SELECT_SCRATCH_BYTES per GPU
    (held until the process ends) instead of p->workspace, which is ignored.
    Calls with more than NFA_SELECT_SCRATCH_ROWS rows (batch x kv heads), or
-   whose keys (2 bytes per page slot and row) do not fit beside the fixed
-   counters and histograms, fail with NFA_EWORKSPACE.  The first call on a
+   whose page keys (2 bytes per page slot and row; 10 bytes plus 4 per tile
+   when the block table can hold rows of more than 16384 pages, whose tiles
+   then list their pages for the tail) do not fit beside the fixed counters
+   and histograms, fail with NFA_EWORKSPACE.  The first call on a
    device takes the array's address and clears its counters (it synchronises
    the stream once and must not be captured); later calls allocate, clear
    and synchronise nothing.  All calls on one GPU share the array, so calls

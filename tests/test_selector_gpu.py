@@ -70,6 +70,25 @@ def test_one_million_token_context():
     assert int(res[0][0].i_n.min()) > 65535  # near pages past 16-bit ids
 
 
+@pytest.mark.parametrize('zero_keys', [False, True])
+def test_long_and_short_rows_in_one_launch(zero_keys):
+    """A row of 19375 pages (past 16384: its tiles list their own top-K
+    pages for the tail) beside a short row that leaves the tail every key,
+    in the multi-pass instance; with all-zero keys (ties everywhere) every
+    page of the long row survives its tile and the tail reads every key."""
+    cache, gen, req_ids = _prod_cache([310000, 20000], hkv=2, hq=8, max_req=2,
+                                      zero_keys=zero_keys)
+    indexer = make_indexer()
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = bf16_randn((2, 8, 128), gen, DEV)
+    decode = _decode_inputs(cache, 2, gen, torch.bfloat16)
+    print(f'# long and short rows (zero keys {zero_keys}): selector + oracle', flush=True)
+    res = run_and_compare(cache, indexer, req_ids, q, decode,
+                          scaling=0.08838834764831845)
+    assert res[0][0].vis_len == 1024 and res[1][0].vis_len == 1024
+
+
 @pytest.mark.parametrize('side_copy', [True, False])
 def test_l2_from_side_copy_or_k_pool(side_copy):
     # the L2 logits read the L2 side copy, or the K pool when it is off

@@ -62,6 +62,10 @@ constexpr int kStatTokens = 4;   // tokens per staging round of the stats pass
 constexpr int kSegMax = 1 << 17;  // keys staged in LDS at once by the tail, at most
 constexpr int kQRawPerThread = 4;  // G * head_dim <= 4 * SB query elements
 constexpr int kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
+// Rows of more pages than this list their survivors (the tiles' own top-K
+// keys) for the tail; shorter rows leave the tail every key, which costs it
+// less than the listing costs the tiles.
+constexpr int kSurvPages = 16384;
 
 struct SelDims {
   int ntiles;     // L1 tiles per row at most (kernel A grid.y)
@@ -77,6 +81,7 @@ struct SelDims {
   int prot;       // protected width = min(s_cap, sink + swa)
   int lds;        // LDS bytes per workgroup
   int multi;      // tiles may take several passes (second staging buffer)
+  int surv;       // rows may be long enough to list survivors (multi only)
   int group;      // query heads per kv head
   int hd_sh, bs_sh, page_sh;  // log2 of head_dim, bs, page, or -1
   // LDS: a common part, then the tile part, or the tail: its candidate pages,
@@ -84,12 +89,14 @@ struct SelDims {
   int a_ctx;  // the row state wave 0 hands to the other waves
   int a_hist, a_tmp, a_misc, a_clk, a_qf, a_qs, a_qu, a_qg, a_fdims;
   int a_dims, a_last, a_tphys, a_stage, a_hs, a_st, a_st2;  // tile
+  int a_tkeys;    // the tile's page keys (its survivors are listed from them)
   int a_pages, a_pphys;                                // tail
+  int sc;         // survivors the tail holds in LDS (more: every key is read)
   int a_keys, a_dbf, a_dbn, a_dsel;                    // tail, L1
   int a_dk, a_l0, a_l0x, a_l1, a_l1x, a_mid, a_mslot;  // tail, L2
   // global workspace byte offsets; counters and histograms first (they must
   // start at zero and are reset by the kernel itself)
-  int64_t w_rowcnt, w_reqcnt, w_hist, w_keys, w_total;
+  int64_t w_rowcnt, w_reqcnt, w_hist, w_keys, w_surv, w_scount, w_total;
 };
 
 __host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
@@ -163,12 +170,17 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   if (stats_staged(p)) o += 2 * (32 / 8) * kSpanMax * 16;
   s.a_st2 = o;         // the next pass's, staged while this one is scored
   if (stats_staged(p) && s.multi) o += 2 * (32 / 8) * kSpanMax * 16;
+  s.a_tkeys = o; if (s.surv) o += align16(2 * kTileMax);
   const int a_tile = o;
   o = a_base;
   s.a_pages = o; o += align16(4 * s.np);
   s.a_pphys = o; o += align16(4 * s.np);
   const int a_l12 = o;
-  s.a_keys = o;  o += align16(2 * s.seg);
+  // the row's keys, or (instead) its survivors: pages (4 bytes) then keys
+  s.sc = ((2 * s.seg) / 8) & ~15;
+  if (s.sc < 8192) s.sc = 8192;
+  if (s.sc > 32 * SB) s.sc = 32 * SB;  // at most 32 per thread in the selection
+  s.a_keys = o;  o += align16(s.surv && 8 * s.sc > 2 * s.seg ? 8 * s.sc : 2 * s.seg);
   s.a_dbf = o;   o += align16(4 * s.words);
   s.a_dbn = o;   o += align16(4 * s.words);
   s.a_dsel = o;  o += align16(8 * (p.k_f + p.k_n + 1));
@@ -191,6 +203,9 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   s.w_reqcnt = w; w += ((int64_t)4 * p.batch + 255) & ~(int64_t)255;
   s.w_hist = w;   w += (int64_t)4 * rows * 512;
   s.w_keys = w;   w += (((int64_t)2 * rows * s.kstride) + 255) & ~(int64_t)255;
+  // survivors' pages, then keys, and the tiles' survivor counts
+  s.w_surv = w;   if (s.surv) w += (int64_t)8 * rows * s.kstride;
+  s.w_scount = w; if (s.surv) w += (((int64_t)4 * rows * s.ntiles) + 255) & ~(int64_t)255;
   s.w_total = w;
 }
 
@@ -221,6 +236,7 @@ __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   // a tile spans more than one pass only when a dispatch round of one-pass
   // tiles cannot cover the widest row
   s.multi = p.max_blocks > s.tcap * kSpanMax;
+  s.surv = s.multi && p.max_blocks > kSurvPages && p.far_method != NFA_METHOD_AVG_TOP2;
   // keys staged per tail segment: as many as fit beside the debug bitmaps
   // (one bit per page each) in the LDS of a workgroup
   for (int seg = kpad < kSegMax ? kpad : kSegMax;; seg /= 2) {
@@ -737,6 +753,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void *ptr) {
 // followed by a workgroup barrier.
 __device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds)
+               : "memory", "m0");
+}
+
+// One global_load_lds_dword: lane i copies the 4 bytes at its src to LDS
+// byte lds + 4 i (inactive lanes copy nothing); the same rules as lds_dma16.
+__device__ __forceinline__ void lds_dma4(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                :
                : "v"(src), "s"(lds)
                : "memory", "m0");
@@ -1303,14 +1328,18 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     }                                                                 \
   } while (0)
 
-// MULTI: tiles may span several passes (the host picks it when a row can
-// hold more pages than one pass of every tile of a dispatch round covers);
-// without it every tile is a single pass and the extra-pass loop is absent.
+// MODE 1 and 2 (MULTI): tiles may span several passes (the host picks it
+// when a row can hold more pages than one pass of every tile of a dispatch
+// round covers); without it every tile is a single pass and the extra-pass
+// loop is absent.  MODE 2 (SURV) adds the survivor lists of rows longer than
+// kSurvPages (the host picks it when the block table can hold such rows).
 // TOP2: the avg_top2 far method, a separate instance so the extra query
 // rows and head scores cost the default instances no registers.
-template <int DSUB, typename KV, bool MULTI, bool TOP2>
+template <int DSUB, typename KV, int MODE, bool TOP2>
 __global__ void __launch_bounds__(SB)
     nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
+  constexpr bool MULTI = MODE >= 1;
+  constexpr bool SURV = MODE == 2;
   warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int CH = Elem<KV>::kChunk;
@@ -1604,6 +1633,7 @@ __global__ void __launch_bounds__(SB)
   };
   const RowGeo geo = ctx_geo(s_ctx, L, !skip_far, !skip_near);
   float *s_hs = (float *)(smem + sd.a_hs);  // [head][page] bf16 head scores
+  uint16_t *s_tkeys = (uint16_t *)(smem + sd.a_tkeys);  // the tile's keys
   const int lpp_log = G <= 1 ? 0 : G <= 2 ? 1 : G <= 4 ? 2 : 3;
   const int lpp = 1 << lpp_log;  // lanes per page
   const int ppw = 64 >> lpp_log;  // pages per wave and round
@@ -1768,6 +1798,7 @@ __global__ void __launch_bounds__(SB)
         const uint32_t fk = score_key(far_bits);
         const uint32_t nk = score_key(near_bits);
         g_keys[t] = (uint16_t)(fk ? fk : nk);
+        if constexpr (SURV) s_tkeys[t - t0] = (uint16_t)(fk ? fk : nk);
         if (fk) atomicAdd(&s_hist[fk >> 8], 1);
         if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
       }
@@ -1801,6 +1832,62 @@ __global__ void __launch_bounds__(SB)
         run_pass(std::false_type{}, c0, c1, st, c1, c1 < t1 ? pass_end(c1, t1) : c1, nst);
       }
     }
+  }
+  // ---- survivors: a key below the tile's own K-th largest key (of its
+  //      pool) has K keys of the tile above it, so it is not among the row's
+  //      top K; the tile lists its other pages and keys, in page order, from
+  //      its first page on, for the tail to read instead of every key of the
+  //      row.  The tile's K-th key: the coarse bin from the tile histogram,
+  //      then the low bytes of the tile's keys in that bin.
+  if (SURV && kt_eff > kSurvPages) {
+    if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 40);
+    if (wave_id() == 1) wave_threshold_bin(s_hist + 256, p.k_n, s_tmp + 44);
+    int *s_lo = (int *)(smem + sd.a_stage);  // low-byte histograms (far | near)
+    if (tid < 512) s_lo[tid] = 0;
+    lds_barrier();
+    const int hb_f = s_tmp[40], hb_n = s_tmp[44];
+    const int npg = t1 - t0;
+    const int ppt = (npg + SB - 1) / SB;
+    const int pa = imin(tid * ppt, npg);
+    const int pb = imin(pa + ppt, npg);
+    // keys >= thr survive: every valid key when the pool's keys all fit K
+    int thr_f = 1, thr_n = 1;
+    if (hb_f >= 0 || hb_n >= 0) {
+      for (int i = pa; i < pb; ++i) {
+        const uint32_t key = s_tkeys[i];
+        const bool near = t0 + i >= geo.near_start;
+        if (key != 0u && (int)(key >> 8) == (near ? hb_n : hb_f))
+          atomicAdd(&s_lo[(near ? 256 : 0) + (key & 255u)], 1);
+      }
+      lds_barrier();
+      if (wave_id() == 0 && hb_f >= 0)
+        wave_threshold_bin(s_lo, p.k_f - s_tmp[41], s_tmp + 48, true);
+      if (wave_id() == 1 && hb_n >= 0)
+        wave_threshold_bin(s_lo + 256, p.k_n - s_tmp[45], s_tmp + 52, true);
+      lds_barrier();
+      // (a fine bin of -1: the whole coarse bin is taken, down to its
+      // lowest key)
+      if (hb_f >= 0) thr_f = (hb_f << 8) | imax(s_tmp[48], 0);
+      if (hb_n >= 0) thr_n = (hb_n << 8) | imax(s_tmp[52], 0);
+    }
+    auto survives = [&](int i, uint32_t key) {
+      return key != 0u && (int)key >= (t0 + i >= geo.near_start ? thr_n : thr_f);
+    };
+    int c = 0;
+    for (int i = pa; i < pb; ++i) c += survives(i, s_tkeys[i]) ? 1 : 0;
+    int total;
+    int pos = block_scan_exclusive<SW>(c, s_tmp, &total);
+    int *sv_page = (int *)(ws + sd.w_surv) + (int64_t)row * 2 * sd.kstride + t0;
+    uint32_t *sv_key = (uint32_t *)(sv_page + sd.kstride);
+    for (int i = pa; i < pb; ++i) {
+      const uint32_t key = s_tkeys[i];
+      if (survives(i, key)) {
+        sv_page[pos] = t0 + i;
+        sv_key[pos] = key;
+        ++pos;
+      }
+    }
+    if (tid == 0) ((int *)(ws + sd.w_scount))[(int64_t)row * sd.ntiles + tile] = total;
   }
   if (tid < 256) {
     const int hf = s_hist[tid];
@@ -1905,7 +1992,46 @@ __global__ void __launch_bounds__(SB)
     s_misc[3] = 0;  // debug selection list lengths (far, near)
     s_misc[4] = 0;
   }
-  if (sd.nseg == 1) stage_keys(g_keys, 0, sd.seg, s_keys);
+  // The row's survivors (every tile listed them at its first page, in page
+  // order) are read instead of every key when the row has at most 64 tiles
+  // and they fit the LDS; their counts come first.
+  const int ntile = __builtin_amdgcn_readfirstlane(s_ctx[5]);
+  int *s_spre = s_tmp + 64;  // survivors of the tiles before tile t
+  const bool surv_on = SURV && kt_eff > kSurvPages;
+  if (surv_on && wave_id() == 0) {
+    const int lane = lane_id();
+    const int cnt = lane < ntile && ntile <= 64
+                        ? ((const int *)(ws + sd.w_scount))[(int64_t)row * sd.ntiles + lane]
+                        : 0;
+    const int inc = wave_incl_sum(cnt);
+    s_spre[lane] = inc - cnt;
+    if (lane == 63) s_misc[8] = inc;
+  }
+  if (surv_on) lds_barrier();
+  const int n_surv = surv_on ? __builtin_amdgcn_readfirstlane(s_misc[8]) : 0;
+  const bool surv_path = surv_on && ntile <= 64 && n_surv <= sd.sc;
+  int *s_spage = (int *)(smem + sd.a_keys);               // survivors' pages
+  uint32_t *s_skey = (uint32_t *)(s_spage + sd.sc);       // and keys
+  if (surv_path) {
+    // each tile's list in runs of 64 entries, copied straight into LDS
+    const int t_base = kt_eff / ntile;
+    const int t_rem = kt_eff - t_base * ntile;
+    const int *sv_page = (const int *)(ws + sd.w_surv) + (int64_t)row * 2 * sd.kstride;
+    const uint32_t *sv_key = (const uint32_t *)(sv_page + sd.kstride);
+    for (int t = wave_id(); t < ntile; t += SW) {
+      const int tt0 = t * t_base + imin(t, t_rem);
+      const int pre = s_spre[t];
+      const int cnt = (t + 1 < ntile ? s_spre[t + 1] : n_surv) - pre;
+      for (int e0 = 0; e0 < cnt; e0 += 64) {
+        if (e0 + lane_id() < cnt) {
+          lds_dma4(sv_page + tt0 + e0 + lane_id(), lds_addr(s_spage + pre + e0));
+          lds_dma4(sv_key + tt0 + e0 + lane_id(), lds_addr(s_skey + pre + e0));
+        }
+      }
+    }
+  } else if (sd.nseg == 1) {
+    stage_keys(g_keys, 0, sd.seg, s_keys);
+  }
   dma_barrier();
   NFA_MARK(32, 24);
   // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
@@ -1914,7 +2040,16 @@ __global__ void __launch_bounds__(SB)
   __syncthreads();
   NFA_MARK(32, 25);
   const int hbf = s_tmp[8], hbn = s_tmp[12];
-  if (hbf >= 0 || hbn >= 0) {
+  if ((hbf >= 0 || hbn >= 0) && surv_path) {
+    // refinement over the survivors (every key of a threshold bin is one)
+    for (int i = tid; i < n_surv; i += SB) {
+      const uint32_t k = s_skey[i];
+      const bool near = s_spage[i] >= near_start;
+      if ((int)(k >> 8) == (near ? hbn : hbf))
+        atomicAdd(&s_hist[(near ? 768 : 512) + (k & 255u)], 1);
+    }
+  }
+  if ((hbf >= 0 || hbn >= 0) && !surv_path) {
     // refinement: low-byte histograms of the keys in the threshold bins
     for (int sg = 0; sg < sd.nseg; ++sg) {
       const int seg_base = sg * sd.seg;
@@ -1941,6 +2076,8 @@ __global__ void __launch_bounds__(SB)
         }
       }
     }
+  }
+  if (hbf >= 0 || hbn >= 0) {
     __syncthreads();
     NFA_MARK(32, 26);
     if (wave_id() == 0 && hbf >= 0)
@@ -1991,7 +2128,71 @@ __global__ void __launch_bounds__(SB)
   };
   int np_u = 0;          // candidates so far (uniform)
   int tfb = 0, tnb = 0;  // tied far / near pages so far (uniform)
-  for (int sg = 0; sg < sd.nseg; ++sg) {
+  if (surv_path) {
+    // The survivors in page order, a contiguous run per thread: the tied
+    // keys ranked by a first scan, candidate positions by a second, the
+    // bypass pages (in no pool, so never survivors unless the two
+    // geometries disagree) placed among them.
+    const int per = (n_surv + SB - 1) / SB;  // <= 32
+    const int ia = imin(tid * per, n_surv);
+    const int ib = imin(ia + per, n_surv);
+    const bool all_f = tf.need == (1 << 30);
+    const bool all_n = tn.need == (1 << 30);
+    int rf = 0, rn = 0;
+    if (tie_cut(tf) || tie_cut(tn)) {
+      int c2[2] = {0, 0}, tot2[2];
+      for (int i = ia; i < ib; ++i) {
+        const bool near = s_spage[i] >= near_start;
+        if (s_skey[i] == (uint32_t)(near ? tn.T : tf.T) && !(near ? all_n : all_f))
+          ++c2[near ? 1 : 0];
+      }
+      block_scan_n<2, SW>(c2, s_tmp + 32, tot2);
+      rf = c2[0];
+      rn = c2[1];
+    }
+    int c5[5] = {0, 0, 0, 0, 0}, tot5[5];
+    uint32_t candm = 0u;
+    for (int i = ia; i < ib; ++i) {
+      const int page = s_spage[i];
+      const uint32_t k = s_skey[i];
+      const bool near = page >= near_start;
+      const uint32_t T = (uint32_t)(near ? tn.T : tf.T);
+      bool sel = k > T;
+      if (k == T) sel = (near ? all_n : all_f) || (near ? rn++ < tn.need : rf++ < tf.need);
+      if (!sel) continue;
+      if (NFA_COLD(dbg)) dbg_select(page, k, near);
+      if (page >= cp_lo && page < cp_hi) {
+        candm |= 1u << (i - ia);
+        ++c5[0];
+        c5[1] += page < bp0 ? 1 : 0;
+        c5[2] += page < bp1 ? 1 : 0;
+        c5[3] += page == bp0 ? 1 : 0;
+        c5[4] += page == bp1 ? 1 : 0;
+      }
+    }
+    block_scan_n<5, SW>(c5, s_tmp + 32, tot5);
+    const bool ins0 = bp0 >= 0 && tot5[3] == 0;
+    const bool ins1 = bp1 >= 0 && bp1 != bp0 && tot5[4] == 0;
+    int pos = c5[0];
+    for (uint32_t bits = candm; bits; bits &= bits - 1u) {
+      const int page = s_spage[ia + __ffs(bits) - 1];
+      const int dest = pos + (ins0 && page > bp0 ? 1 : 0) + (ins1 && page > bp1 ? 1 : 0);
+      if (dest < sd.np) s_pages[dest] = page;
+      ++pos;
+    }
+    if (tid == 0) {
+      if (ins0) {
+        const int r0 = tot5[1] + (ins1 && bp1 < bp0 ? 1 : 0);
+        if (r0 < sd.np) s_pages[r0] = bp0;
+      }
+      if (ins1) {
+        const int r1 = tot5[2] + (ins0 && bp0 < bp1 ? 1 : 0);
+        if (r1 < sd.np) s_pages[r1] = bp1;
+      }
+    }
+    np_u = tot5[0] + (ins0 ? 1 : 0) + (ins1 ? 1 : 0);
+  }
+  for (int sg = 0; sg < (surv_path ? 0 : sd.nseg); ++sg) {
     const int seg_base = sg * sd.seg;
     if (NFA_COLD(sd.nseg > 1)) {
       __syncthreads();
@@ -2608,34 +2809,44 @@ static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
                                 hipStream_t stream) {
   // one pass per tile whenever a dispatch round of single-pass tiles covers
   // the widest possible row; several passes stage the next pass's statistics
-  // in a second LDS buffer (beyond 64 KiB)
-  const bool multi = sd.multi != 0;
+  // in a second LDS buffer (beyond 64 KiB); rows that may be long list their
+  // survivors
+  const int mode = sd.multi ? (sd.surv ? 2 : 1) : 0;
+  const bool top2 = p.far_method == NFA_METHOD_AVG_TOP2;
   const dim3 grid(p.hkv, p.batch, sd.ntiles);
+  const void *k[5] = {
+      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, false>),
+      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, true>),
+      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 1, false>),
+      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 1, true>),
+      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 2, false>)};
+  const int i = mode == 2 ? 4 : 2 * mode + (int)top2;
   if (sd.lds > 64 * 1024) {
-    static std::atomic<uint64_t> optin[4];
-    const bool top2 = p.far_method == NFA_METHOD_AVG_TOP2;
-    const void *k[4] = {
-        reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, false, false>),
-        reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, false, true>),
-        reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, true, false>),
-        reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, true, true>)};
-    const int i = 2 * (int)multi + (int)top2;
+    static std::atomic<uint64_t> optin[5];
     const hipError_t e = lds_optin(k[i], optin[i]);
     if (e != hipSuccess) return e;
   }
-  if (p.far_method == NFA_METHOD_AVG_TOP2) {
-    if (multi)
-      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, true, true>), grid,
+  switch (i) {
+    case 0:
+      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 0, false>), grid,
                          dim3(nfa::SB), sd.lds, stream, p, sd);
-    else
-      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, false, true>), grid,
+      break;
+    case 1:
+      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 0, true>), grid,
                          dim3(nfa::SB), sd.lds, stream, p, sd);
-  } else if (multi) {
-    hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, true, false>), grid,
-                       dim3(nfa::SB), sd.lds, stream, p, sd);
-  } else {
-    hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, false, false>), grid,
-                       dim3(nfa::SB), sd.lds, stream, p, sd);
+      break;
+    case 2:
+      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 1, false>), grid,
+                         dim3(nfa::SB), sd.lds, stream, p, sd);
+      break;
+    case 3:
+      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 1, true>), grid,
+                         dim3(nfa::SB), sd.lds, stream, p, sd);
+      break;
+    default:
+      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 2, false>), grid,
+                         dim3(nfa::SB), sd.lds, stream, p, sd);
+      break;
   }
   return hipGetLastError();
 }
@@ -2758,12 +2969,16 @@ extern "C" int32_t nfa_select_layer_noalloc(const NfaSelectParams *p, void *stre
   if (rc != NFA_OK) return rc;
   SelDims sd = nfa::sel_dims(*p, nfa::device_cus());
   const int64_t rows = (int64_t)p->batch * p->hkv;
+  // per row: keys (2 bytes a page), survivors (8 bytes a page), tile counts
   const int64_t keys = (((int64_t)2 * rows * sd.kstride) + 255) & ~(int64_t)255;
-  if (rows > NFA_SELECT_SCRATCH_ROWS || kScratchKeys + keys > NFA_SELECT_SCRATCH_BYTES) {
+  const int64_t surv = sd.surv ? (int64_t)8 * rows * sd.kstride : 0;
+  const int64_t scnt = sd.surv ? (((int64_t)4 * rows * sd.ntiles) + 255) & ~(int64_t)255 : 0;
+  const int64_t need = kScratchKeys + keys + surv + scnt;
+  if (rows > NFA_SELECT_SCRATCH_ROWS || need > NFA_SELECT_SCRATCH_BYTES) {
     nfa_set_error("nfa_select_layer_noalloc: %lld rows (batch x kv heads) of %d "
                   "pages need %lld scratch bytes; the static array holds %lld "
                   "bytes and %d rows",
-                  (long long)rows, p->max_blocks, (long long)(kScratchKeys + keys),
+                  (long long)rows, p->max_blocks, (long long)need,
                   (long long)NFA_SELECT_SCRATCH_BYTES, NFA_SELECT_SCRATCH_ROWS);
     return NFA_EWORKSPACE;
   }
@@ -2775,7 +2990,9 @@ extern "C" int32_t nfa_select_layer_noalloc(const NfaSelectParams *p, void *stre
   sd.w_reqcnt = kScratchReqCnt;
   sd.w_hist = kScratchHist;
   sd.w_keys = kScratchKeys;
-  sd.w_total = kScratchKeys + keys;
+  sd.w_surv = kScratchKeys + keys;
+  sd.w_scount = sd.w_surv + surv;
+  sd.w_total = need;
   NfaSelectParams q = *p;
   q.workspace = ptr;
   q.workspace_bytes = NFA_SELECT_SCRATCH_BYTES;
