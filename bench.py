@@ -364,6 +364,14 @@ def selector_timeline(torch, w, steps, plan):
             acc.setdefault(f'A tile {name} (max)', []).append(tile[:, :, k].max() * us)
         acc.setdefault('A tile hist flush (max)', []).append(
             ((tile[:, :, 4] - tile[:, :, 6]) * us).max())
+        # survivor lists of long rows (marks 11-15 when present)
+        if (tile[:, :, 15] > 0).any():
+            ok = tile[:, :, 15] > 0
+            for a, bb, name in ((6, 11, 'coarse bins'), (11, 12, 'refine'),
+                                (12, 13, 'fine bins+count'), (13, 14, 'scan'),
+                                (14, 15, 'write'), (15, 4, 'hist flush')):
+                acc.setdefault(f'A tile survivors: {name} (max)', []).append(
+                    float(((tile[:, :, bb] - tile[:, :, a]) * us)[ok].max()))
         acc.setdefault('A tile slowest scoring tile', []).append(
             float(np.unravel_index(tile[:, :, 9].argmax(), tile.shape[:2])[1]))
         # the tile that arrives last in each row, and the median tile: their

@@ -1845,6 +1845,7 @@ __global__ void __launch_bounds__(SB)
     int *s_lo = (int *)(smem + sd.a_stage);  // low-byte histograms (far | near)
     if (tid < 512) s_lo[tid] = 0;
     lds_barrier();
+    NFA_MARK(0, 11);
     const int hb_f = s_tmp[40], hb_n = s_tmp[44];
     const int npg = t1 - t0;
     const int ppt = (npg + SB - 1) / SB;
@@ -1860,6 +1861,7 @@ __global__ void __launch_bounds__(SB)
           atomicAdd(&s_lo[(near ? 256 : 0) + (key & 255u)], 1);
       }
       lds_barrier();
+      NFA_MARK(0, 12);
       if (wave_id() == 0 && hb_f >= 0)
         wave_threshold_bin(s_lo, p.k_f - s_tmp[41], s_tmp + 48, true);
       if (wave_id() == 1 && hb_n >= 0)
@@ -1875,8 +1877,10 @@ __global__ void __launch_bounds__(SB)
     };
     int c = 0;
     for (int i = pa; i < pb; ++i) c += survives(i, s_tkeys[i]) ? 1 : 0;
+    NFA_MARK(0, 13);
     int total;
     int pos = block_scan_exclusive<SW>(c, s_tmp, &total);
+    NFA_MARK(0, 14);
     int *sv_page = (int *)(ws + sd.w_surv) + (int64_t)row * 2 * sd.kstride + t0;
     uint32_t *sv_key = (uint32_t *)(sv_page + sd.kstride);
     for (int i = pa; i < pb; ++i) {
@@ -1888,6 +1892,7 @@ __global__ void __launch_bounds__(SB)
       }
     }
     if (tid == 0) ((int *)(ws + sd.w_scount))[(int64_t)row * sd.ntiles + tile] = total;
+    NFA_MARK(0, 15);
   }
   if (tid < 256) {
     const int hf = s_hist[tid];
