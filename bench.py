@@ -382,12 +382,20 @@ def selector_timeline(torch, w, steps, plan):
         rows_i = np.arange(tile.shape[0])
         acc.setdefault('A last-arriving tile index (median row)', []).append(
             float(np.median(last_t)))
-        for nm, sel in (('last tile', tile[rows_i, last_t]),):
+        # the tile of median duration in each row
+        dur_rt = np.where(live, tile[:, :, 4] - tile[:, :, 0], -1)
+        med_t = np.array([np.argsort(r)[len(r) - 1 - int(np.sum(r >= 0)) // 2]
+                          for r in dur_rt])
+        for nm, sel in (('last tile', tile[rows_i, last_t]),
+                        ('median tile', tile[rows_i, med_t])):
             acc.setdefault(f'A {nm}: start', []).append(
                 float(np.median((sel[:, 0] - start) * us)))
             for k, name in enumerate(names):
                 acc.setdefault(f'A {nm}: {name}', []).append(
                     float(np.median((sel[:, k + 1] - sel[:, k]) * us)))
+            for k, name in ((8, 'staging wait'), (9, 'scores'), (10, 'keys+hist')):
+                acc.setdefault(f'A {nm}: passes {name}', []).append(
+                    float(np.median(sel[:, k] * us)))
         dur = np.where(live, (tile[:, :, 4] - tile[:, :, 0]) * us, np.nan)
         acc.setdefault('A tile duration (median tile)', []).append(
             float(np.nanmedian(dur)))
