@@ -353,6 +353,18 @@ def selector_timeline(torch, w, steps, plan):
         acc.setdefault('kernel span', []).append((tail[:, 13].max() - start) * us)
         acc.setdefault('last tile arrives', []).append(
             (tile[:, :, 4].max() - start) * us)
+        # per row: its tail's first mark after its last tile's arrival mark
+        # (the counters, the release and acquire, the tail's own set-up)
+        gap = (tail[:, 0] - tile[:, :, 4].max(axis=1)) * us
+        acc.setdefault('arrival to tail start (max row)', []).append(float(gap.max()))
+        acc.setdefault('tail start (max)', []).append(float((tail[:, 0].max() - start) * us))
+        if (tail[:, 27] > 0).all():
+            g1 = (tail[:, 27] - tile[:, :, 4].max(axis=1)) * us
+            g2 = (tail[:, 0] - tail[:, 27]) * us
+            acc.setdefault('  arrival: marks flush + request counter (max row)', []).append(
+                float(g1.max()))
+            acc.setdefault('  arrival: row counter + tail set-up (max row)', []).append(
+                float(g2.max()))
         names = ['row scalars', 'q prep', 'page stats', 'L1 scores+publish']
         for k, name in enumerate(names):
             d = (tile[:, :, k + 1] - tile[:, :, k]) * us

@@ -112,7 +112,9 @@ typedef struct NfaSelectParams {
   const int32_t *slots;               /* [batch] physical slot or -1 */
 
   /* persistent page statistics of this layer, KV dtype,
-     [max_req, hkv, dsub/chunk, max_blocks, chunk] with chunk = 16B/elem */
+     [max_req, hkv, dsub/chunk, max_blocks, chunk] with chunk = 16B/elem:
+     per page dim the min, the max and the mean bf16(KV(sum) / bs) (the avg
+     pools' key; the fp32 running sum of the newest page is page_sum_l) */
   void *stat_min_l, *stat_max_l, *stat_sum_l;
   int32_t *stats_len_l;               /* [max_req] */
   /* optional L2 side copy of this layer, KV dtype: the L2 dims of every

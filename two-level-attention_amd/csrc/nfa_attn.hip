@@ -399,8 +399,8 @@ __global__ void __launch_bounds__(NFA_BLOCK)
         acc0[k] = acc0[k] * f + a0;
         acc1[k] = acc1[k] * f + a1;
       } else {
-        part[g * (D + 2) + 2 + d] = a0;
-        part[g * (D + 2) + 3 + d] = a1;
+        store_coherent(&part[g * (D + 2) + 2 + d], a0);
+        store_coherent(&part[g * (D + 2) + 3 + d], a1);
       }
     }
     if (!LOOP) break;
@@ -457,16 +457,17 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     if (!store_acc || o >= G * (D / 2)) break;
     const int g = o / (D / 2);
     const int d = 2 * (o % (D / 2));
-    part[g * (D + 2) + 2 + d] = acc0[k];
-    part[g * (D + 2) + 3 + d] = acc1[k];
+    store_coherent(&part[g * (D + 2) + 2 + d], acc0[k]);
+    store_coherent(&part[g * (D + 2) + 3 + d], acc1[k]);
   }
   if (tid < G) {
-    part[tid * (D + 2) + 0] = s_m[tid];
-    part[tid * (D + 2) + 1] = s_z[tid];
+    store_coherent(&part[tid * (D + 2) + 0], s_m[tid]);
+    store_coherent(&part[tid * (D + 2) + 1], s_z[tid]);
   }
 
-  // arrival; the last split of the (row, kv) merges
-  if (!arrive_last(&cnt[vrow], (unsigned int)ad.nsplit, &s_last)) return;
+  // arrival; the last split of the (row, kv) merges (the partials went out
+  // through coherent stores: no L2 writeback)
+  if (!arrive_last(&cnt[vrow], (unsigned int)ad.nsplit, &s_last, false)) return;
 
   const float *base = (const float *)(ws + ad.w_part) +
                       (int64_t)vrow * ad.nsplit * ad.part_stride;

@@ -233,19 +233,47 @@ __device__ __forceinline__ uint4 pack_chunk(const float *x) {
 // cross-workgroup publication ("last arriving workgroup" pattern)
 // ---------------------------------------------------------------------------
 
+// A store that is coherent device-wide by itself: the relaxed agent-scope
+// atomic store (`global_store ... sc1`) is written through this XCD's L2 to
+// where every XCD reads it, and its completion (vmcnt) waits for that.  Data
+// handed to another workgroup only through such stores and through atomics
+// needs no L2 writeback before the hand-over (arrive_last with writeback
+// false).  A plain store may stay dirty in this XCD's L2: on 252 workgroups
+// in rows of 7 (each row over several XCDs), 3000 hand-overs of plain stores
+// without the writeback left 2.6 % of the words stale for the last
+// workgroup, these stores none.
+template <typename T>
+__device__ __forceinline__ void store_coherent(T *p, T v) {
+  static_assert(sizeof(T) == 2 || sizeof(T) == 4, "16- or 32-bit elements");
+  if constexpr (sizeof(T) == 2) {
+    uint16_t u;
+    __builtin_memcpy(&u, &v, 2);
+    __hip_atomic_store(reinterpret_cast<uint16_t *>(p), u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    uint32_t u;
+    __builtin_memcpy(&u, &v, 4);
+    __hip_atomic_store(reinterpret_cast<uint32_t *>(p), u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // Every wave completes its own global stores, the workgroup meets at a
-// barrier, then one wave makes them visible device-wide (one agent-scope
-// release for the whole workgroup, not one per wave) and takes a ticket from
-// the device-scope counter.  Returns true in every thread of the workgroup
-// that arrives last of `n`; that workgroup has acquired (one agent-scope
-// acquire, then a barrier) and resets the counter, so no memset is needed
-// between launches.  `s_flag` is one int of LDS.
+// barrier, then one wave makes them visible device-wide (with `writeback`,
+// one agent-scope release -- an L2 writeback, 1-2 us -- for the whole
+// workgroup, not one per wave; without it the data must have been written
+// with store_coherent or atomics, whose completion the wait already covers)
+// and takes a ticket from the device-scope counter.  Returns true in every
+// thread of the workgroup that arrives last of `n`; that workgroup has
+// acquired (one agent-scope acquire, then a barrier) and resets the counter,
+// so no memset is needed between launches.  `s_flag` is one int of LDS.
 __device__ __forceinline__ bool arrive_last(unsigned int *counter,
-                                            unsigned int n, int *s_flag) {
+                                            unsigned int n, int *s_flag,
+                                            bool writeback = true) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    if (writeback) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     const unsigned int before =
         __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);

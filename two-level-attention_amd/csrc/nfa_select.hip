@@ -495,10 +495,10 @@ __device__ __forceinline__ void q4_store_lanes(const NfaSelectParams &p, int64_t
   for (int off = 1; off < 8; off <<= 1) w |= __shfl_xor(w, off, 32);
   const int64_t slot = q4_slot(p, req, kv, tok);
   unsigned char *base = (unsigned char *)p.l2_keys_l;
-  if (d % 8 == 0) *reinterpret_cast<uint32_t *>(base + slot * 16 + d / 2) = w;
+  if (d % 8 == 0) store_coherent(reinterpret_cast<uint32_t *>(base + slot * 16 + d / 2), w);
   if (d == 0)
-    *reinterpret_cast<uint32_t *>(base + q4_slots(p) * 16 + slot * 4) =
-        (uint32_t)bf16_bits(scale) | ((uint32_t)bf16_bits(zero) << 16);
+    store_coherent(reinterpret_cast<uint32_t *>(base + q4_slots(p) * 16 + slot * 4),
+                   (uint32_t)bf16_bits(scale) | ((uint32_t)bf16_bits(zero) << 16));
 }
 
 // ---------------------------------------------------------------------------
@@ -517,6 +517,16 @@ __device__ __forceinline__ bool is_new(int tok, int new_tok, const void *row) {
 // code: this is the path of the incremental (latest page) update.  ``s_tphys``
 // (or NULL) holds the physical page of every page of the range when a page
 // never straddles two physical pages.
+// The stored avg statistic of one page dim: the page sum rounded to the KV
+// dtype, divided by bs and rounded to bf16 -- the key the avg pools score
+// with (selector:311-354), computed once when the page's statistics are
+// written instead of by every query head at every decode step.
+template <typename KV>
+__device__ __forceinline__ KV page_mean(float sum, int bs) {
+  const KV s = (KV)Elem<KV>::from_f32(sum);
+  return (KV)Elem<KV>::from_f32(bf16r(Elem<KV>::load(&s) / (float)bs));
+}
+
 template <int DSUB, typename KV>
 __device__ __forceinline__ void compute_stats(const NfaSelectParams &p, int64_t req, int kv,
                               int L, int pg_lo, int pg_hi, float *s_stage,
@@ -577,7 +587,7 @@ __device__ __forceinline__ void compute_stats(const NfaSelectParams &p, int64_t 
       const int64_t si = stat_index<KV>(p, req, kv, d, pg, DSUB);
       const KV a = (KV)Elem<KV>::from_f32(mn);
       const KV c = (KV)Elem<KV>::from_f32(mx);
-      const KV s = (KV)Elem<KV>::from_f32(sm);
+      const KV s = page_mean<KV>(sm, p.bs);
       smin[si] = a;
       smax[si] = c;
       ssum[si] = s;
@@ -658,7 +668,7 @@ __device__ __forceinline__ void compute_stats_vec(const NfaSelectParams &p, int6
     for (int e = 0; e < CH; ++e) {
       const KV a = (KV)Elem<KV>::from_f32(mn[e]);
       const KV b = (KV)Elem<KV>::from_f32(mx[e]);
-      const KV s = (KV)Elem<KV>::from_f32(sm[e]);
+      const KV s = page_mean<KV>(sm[e], p.bs);
       smin[si + e] = a;
       smax[si + e] = b;
       ssum[si + e] = s;
@@ -728,7 +738,7 @@ __device__ __forceinline__ void stats_latest_page(
     const int64_t si = stat_index<KV>(p, req, kv, d, pg, DSUB);
     const KV a = (KV)Elem<KV>::from_f32(mn);
     const KV c = (KV)Elem<KV>::from_f32(mx);
-    const KV s = (KV)Elem<KV>::from_f32(sm);
+    const KV s = page_mean<KV>(sm, p.bs);
     ((KV *)p.stat_min_l)[si] = a;
     ((KV *)p.stat_max_l)[si] = c;
     ((KV *)p.stat_sum_l)[si] = s;
@@ -816,15 +826,14 @@ static_assert(GMAX * kSpanMax * 4 <= 4 * SB * kStatTokens,
 // One query head of one page from the staged statistics st (chunk c at
 // st[c * kSpanMax], the max slot at st[4 * kSpanMax]):
 // bf16(Σ_d kmin_d·min(q_d,0) + Σ_d kmax_d·max(q_d,0)) for minmax pools, from
-// the split query qs = [min(q,0) | max(q,0)], and bf16(Σ_d bf16(ksum_d /
-// bs)·q_d) for avg pools, from the query qf (and, with qu, the same mean
-// against the unrounded query into *un); every sum sequential in ascending
-// d with separately rounded products.  x / bs is computed as x * (1 / bs),
-// exact when bs is a power of two (POW2), else as a division.
-template <bool POW2>
+// the split query qs = [min(q,0) | max(q,0)], and bf16(Σ_d kmean_d·q_d)
+// for avg pools (kmean_d = bf16(ksum_d / bs), the stored statistic), from
+// the query qf (and, with qu, the same mean against the unrounded query into
+// *un); every sum sequential in ascending d with separately rounded
+// products.
 __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs,
                                                 const float *qf, const float *qu,
-                                                bool need_mm, int bs, float *un) {
+                                                bool need_mm, float *un) {
   constexpr int NC = 32 / 8;
   float r, su = 0.0f;
   if (need_mm) {
@@ -846,15 +855,11 @@ __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs
     }
     r = sn + sp;
   } else {
-    const float bsf = (float)bs;
-    const float inv = 1.0f / bsf;
     float sa = 0.0f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       float k[8], q[8];
       unpack_chunk<uint16_t>(st[c * kSpanMax], k);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) k[e] = bf16r(POW2 ? k[e] * inv : k[e] / bsf);
       load_f8(qf + c * 8, q);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -889,7 +894,6 @@ __device__ __forceinline__ void l1_head_mem(const NfaSelectParams &p,
   const KV *smin = (const KV *)p.stat_min_l;
   const KV *smax = (const KV *)p.stat_max_l;
   const KV *ssum = (const KV *)p.stat_sum_l;
-  const float bsf = (float)p.bs;
   float sn = 0.0f, sp = 0.0f, sa = 0.0f, su = 0.0f;
   for (int c = 0; c < DSUB / CH; ++c) {
     float kmin[CH], kmax[CH], ks[CH];
@@ -920,7 +924,7 @@ __device__ __forceinline__ void l1_head_mem(const NfaSelectParams &p,
         sp = sp + b;
       }
       if (need_avg) {
-        const float kavg = bf16r(ks[e] / bsf);
+        const float kavg = ks[e];
         const float a = kavg * qd;
         sa = sa + a;
         if (qu != nullptr) {
@@ -1384,7 +1388,6 @@ __global__ void __launch_bounds__(SB)
   NFA_MARK(0, 0);
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
-  unsigned int *req_cnt = (unsigned int *)(ws + sd.w_reqcnt);
   int *g_hist = (int *)(ws + sd.w_hist) + (int64_t)row * 512;
   uint16_t *g_keys = (uint16_t *)(ws + sd.w_keys) + (int64_t)row * sd.kstride;
 
@@ -1584,7 +1587,7 @@ __global__ void __launch_bounds__(SB)
       // decode write of the current token (selector:1030-1061)
       const int phys = slot_b / p.page;
       const int off = slot_b % p.page;
-      if (tid < p.head_dim) ((KV *)p.k_pool_l)[kv_offset(p, phys, kv, off) + tid] = dw_k;
+      if (tid < p.head_dim) store_coherent(&((KV *)p.k_pool_l)[kv_offset(p, phys, kv, off) + tid], dw_k);
       if (tid < p.head_dim_v)
         ((KV *)p.v_pool_l)[(((int64_t)phys * p.hkv + kv) * p.page + off) * p.head_dim_v +
                            tid] = dw_v;
@@ -1599,7 +1602,7 @@ __global__ void __launch_bounds__(SB)
       const float sm = ap_sm + x;
       ((KV *)p.stat_min_l)[si] = (KV)Elem<KV>::from_f32(mn);
       ((KV *)p.stat_max_l)[si] = (KV)Elem<KV>::from_f32(mx);
-      ((KV *)p.stat_sum_l)[si] = (KV)Elem<KV>::from_f32(sm);
+      ((KV *)p.stat_sum_l)[si] = page_mean<KV>(sm, p.bs);
       p.page_sum_l[(req * p.hkv + kv) * DSUB + tid] = sm;
     }
     if (side_late && tid < p.fine_dsub) {
@@ -1607,7 +1610,7 @@ __global__ void __launch_bounds__(SB)
       if (p.l2_quant) {
         q4_store_lanes(p, req, kv, L - 1, Elem<KV>::load(&side_raw), tid);
       } else {
-        ((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)] = side_raw;
+        store_coherent(&((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)], side_raw);
       }
     }
   };
@@ -1637,7 +1640,6 @@ __global__ void __launch_bounds__(SB)
   const int lpp_log = G <= 1 ? 0 : G <= 2 ? 1 : G <= 4 ? 2 : 3;
   const int lpp = 1 << lpp_log;  // lanes per page
   const int ppw = 64 >> lpp_log;  // pages per wave and round
-  const bool bs_pow2 = (bs & (bs - 1)) == 0;
   // one pass scores and publishes pages [c0, c1) from the statistics staged
   // in st; the histogram accumulates in LDS over the passes of the tile.
   // The next pass's statistics, pages [n0, n1), are copied into nst while
@@ -1763,10 +1765,7 @@ __global__ void __launch_bounds__(SB)
         float h, u = 0.0f;
         if constexpr (STG) {
           const uint4 *su = reinterpret_cast<const uint4 *>(st) + lp;
-          h = bs_pow2 ? l1_head_staged<true>(su, s_qs + j * QS, s_qf + j * QF, qu,
-                                             need_mm, bs, &u)
-                      : l1_head_staged<false>(su, s_qs + j * QS, s_qf + j * QF, qu,
-                                              need_mm, bs, &u);
+          h = l1_head_staged(su, s_qs + j * QS, s_qf + j * QF, qu, need_mm, &u);
         } else {
           const bool from_lds = incremental && t == last_blk;
           float m = 0.0f, a = 0.0f;
@@ -1797,7 +1796,7 @@ __global__ void __launch_bounds__(SB)
         // near pages at or above it
         const uint32_t fk = score_key(far_bits);
         const uint32_t nk = score_key(near_bits);
-        g_keys[t] = (uint16_t)(fk ? fk : nk);
+        store_coherent(&g_keys[t], (uint16_t)(fk ? fk : nk));
         if constexpr (SURV) s_tkeys[t - t0] = (uint16_t)(fk ? fk : nk);
         if (fk) atomicAdd(&s_hist[fk >> 8], 1);
         if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
@@ -1886,12 +1885,12 @@ __global__ void __launch_bounds__(SB)
     for (int i = pa; i < pb; ++i) {
       const uint32_t key = s_tkeys[i];
       if (survives(i, key)) {
-        sv_page[pos] = t0 + i;
-        sv_key[pos] = key;
+        store_coherent(&sv_page[pos], t0 + i);
+        store_coherent(&sv_key[pos], key);
         ++pos;
       }
     }
-    if (tid == 0) ((int *)(ws + sd.w_scount))[(int64_t)row * sd.ntiles + tile] = total;
+    if (tid == 0) store_coherent(&((int *)(ws + sd.w_scount))[(int64_t)row * sd.ntiles + tile], total);
     NFA_MARK(0, 15);
   }
   if (tid < 256) {
@@ -1904,17 +1903,14 @@ __global__ void __launch_bounds__(SB)
   NFA_FLUSH(0, clk_tile);
 
   // ---- arrival; the last workgroup of the row runs the tail --------------
-  if (tid == 0) {
-    // every workgroup of the request has read stats_len once all arrived
-    const unsigned int rb = __hip_atomic_fetch_add(
-        &req_cnt[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (rb == (unsigned int)(split.tiles * p.hkv - 1)) {
-      if (do_stats) p.stats_len_l[req] = L;
-      __hip_atomic_store(&req_cnt[b], 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  if (!arrive_last(&row_cnt[row], (unsigned int)split.tiles, &s_misc[0])) return;
+  // What the tail reads of this workgroup's writes -- keys, page lists, the
+  // decode token's K row and L2 side row -- went out through coherent
+  // stores and the histogram through atomics; only a rebuild's side rows
+  // and statistics are plain stores that need the L2 writeback.
+  NFA_MARK(32, 27);
+  if (!arrive_last(&row_cnt[row], (unsigned int)split.tiles, &s_misc[0],
+                   do_stats && !incremental))
+    return;
 
   // =========================== tail ======================================
   // The tail re-derives its state: the kernel arguments read again through
@@ -1953,6 +1949,15 @@ __global__ void __launch_bounds__(SB)
   const bool page_phys = (p.page % bs) == 0;
   const KV *kpool = (const KV *)p.k_pool_l;
   unsigned char *ws = (unsigned char *)p.workspace;
+  // Every workgroup of the request has read its statistics length once the
+  // tails of all its kv rows have started; the last of them records the new
+  // length (the counter's answer is read after the key staging below waited
+  // for every load anyway).
+  unsigned int *req_cnt = (unsigned int *)(ws + sd.w_reqcnt);
+  unsigned int req_rank = 0u;
+  if (tid == 0)
+    req_rank = __hip_atomic_fetch_add(&req_cnt[b], 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
   int *g_hist = (int *)(ws + sd.w_hist) + (int64_t)row * 512;
   uint16_t *g_keys = (uint16_t *)(ws + sd.w_keys) + (int64_t)row * sd.kstride;
   int *s_hist = (int *)(smem + sd.a_hist);
@@ -2038,6 +2043,11 @@ __global__ void __launch_bounds__(SB)
     stage_keys(g_keys, 0, sd.seg, s_keys);
   }
   dma_barrier();
+  if (tid == 0 && req_rank == (unsigned int)(p.hkv - 1)) {
+    const bool active = __builtin_amdgcn_readfirstlane(s_ctx[1]) != 0;
+    if (active && L > 0 && !(skip_far && skip_near)) p.stats_len_l[req] = L;
+    __hip_atomic_store(&req_cnt[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   NFA_MARK(32, 24);
   // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
   if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 8);
