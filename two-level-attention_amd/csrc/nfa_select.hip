@@ -271,6 +271,10 @@ __device__ __forceinline__ int div_p2(int x, int d, int sh) {
   if (sh < 0) return x / d;
   return x >= 0 ? (x >> sh) : -((-x) >> sh);
 }
+// the same for x >= 0
+__device__ __forceinline__ int udiv_p2(int x, int d, int sh) {
+  return sh >= 0 ? (x >> sh) : x / d;
+}
 
 __device__ __forceinline__ RowGeo row_geo(const NfaSelectParams &p, const SelDims &sd,
                                           int L, bool skip_far, bool skip_near) {
@@ -1129,16 +1133,19 @@ struct DenseView {
   const int32_t *bt;
   int n, bs, page, mb;
   bool page_phys;
+  int bs_sh, page_sh;  // log2 of bs and page, or -1
   __device__ __forceinline__ int tok(int i) const {
-    const int pi = i / bs;
+    const int pi = udiv_p2(i, bs, bs_sh);
     return pages[pi] * bs + (i - pi * bs);
   }
   __device__ __forceinline__ int slot_of(int i, int t) const {
-    const int ph = page_phys ? pphys[i / bs] : bt[imin(t / page, mb - 1)];
-    return ph * page + t % page;
+    const int tp = udiv_p2(t, page, page_sh);
+    const int ph = page_phys ? pphys[udiv_p2(i, bs, bs_sh)] : bt[imin(tp, mb - 1)];
+    return ph * page + (t - tp * page);
   }
   __device__ __forceinline__ int slot_of_token(int t) const {
-    return bt[imin(t / page, mb - 1)] * page + t % page;
+    const int tp = udiv_p2(t, page, page_sh);
+    return bt[imin(tp, mb - 1)] * page + (t - tp * page);
   }
 };
 
@@ -2302,7 +2309,8 @@ __global__ void __launch_bounds__(SB)
   int pre_slot = 0;
   if (!p.middle_only && tid < nu) {
     const int x = tid < (u1 - u0) ? u0 + tid : u2 + (tid - (u1 - u0));
-    pre_slot = btr[imin(x / p.page, mb - 1)] * p.page + x % p.page;
+    const int xp = udiv_p2(x, p.page, sd.page_sh);
+    pre_slot = btr[imin(xp, mb - 1)] * p.page + (x - xp * p.page);
   }
   // physical pages of the candidates: with the L2 side copy nothing reads
   // them before the L2 top-quota, so their loads stay in flight through the
@@ -2311,10 +2319,11 @@ __global__ void __launch_bounds__(SB)
   const bool pphys_late = p.l2_keys_l != nullptr && np_u <= SB;
   int pphys_reg = 0;
   if (pphys_late) {
-    if (tid < np_u) pphys_reg = btr[imin((s_pages[tid] * bs) / p.page, mb - 1)];
+    if (tid < np_u)
+      pphys_reg = btr[imin(udiv_p2(s_pages[tid] * bs, p.page, sd.page_sh), mb - 1)];
   } else {
     for (int i = tid; i < np_u; i += SB)
-      s_pphys[i] = btr[imin((s_pages[i] * bs) / p.page, mb - 1)];
+      s_pphys[i] = btr[imin(udiv_p2(s_pages[i] * bs, p.page, sd.page_sh), mb - 1)];
   }
   if (tid == 0 && p.dbg_cand_count != nullptr)
     p.dbg_cand_count[row] = imin(np_u * bs, p.dbg_cand_cap);
@@ -2366,7 +2375,7 @@ __global__ void __launch_bounds__(SB)
   uint4 r_pre[4];
   if (l2_pre) {
     if (tid < np_u * bs) {
-      const int pi = tid / bs;
+      const int pi = udiv_p2(tid, bs, sd.bs_sh);
       const int tk = s_pages[pi] * bs + (tid - pi * bs);
       if (tk >= tok_lo && tk < tok_hi) {
         tk_pre = tk;
@@ -2385,7 +2394,7 @@ __global__ void __launch_bounds__(SB)
   uint32_t pw_pre = 0u;
   if (p.l2_quant) {
     if (tid < np_u * bs) {
-      const int pi = tid / bs;
+      const int pi = udiv_p2(tid, bs, sd.bs_sh);
       const int tk = s_pages[pi] * bs + (tid - pi * bs);
       if (tk >= tok_lo && tk < tok_hi) {
         tk_pre = tk;
@@ -2419,28 +2428,38 @@ __global__ void __launch_bounds__(SB)
     // major) or element d at d (token-major); K pool: the L2 dims' offsets
     auto choff = [&](int c) { return side ? c * bs * CH : s_fdims[c * CH]; };
     auto eoff = [&](int d) { return side ? d : s_fdims[d]; };
+    // the side copy of this (request, kv head): page pg's token r starts at
+    // side0 + pg * bs * fine_dsub + r * (CH, chunk-major, or fine_dsub)
+    const KV *side0 = side ? (const KV *)p.l2_keys_l +
+                                 l2_side_index<KV>(p, req, kv, 0, 0)
+                           : nullptr;
+    const int side_pg = bs * p.fine_dsub;
+    const int side_tk = p.fine_dsub % CH == 0 ? CH : p.fine_dsub;
     // slot i: its token and L2 row (null outside the candidate range)
     auto slot_row = [&](int i, int &tk) -> const KV * {
-      const int pi = i / bs;
-      tk = s_pages[pi] * bs + (i - pi * bs);
+      const int pi = div_p2(i, bs, sd.bs_sh);
+      const int r = i - pi * bs;
+      const int pg = s_pages[pi];
+      tk = pg * bs + r;
       if (tk < tok_lo || tk >= tok_hi) return nullptr;
-      if (side) return (const KV *)p.l2_keys_l + l2_side_index<KV>(p, req, kv, tk, 0);
+      if (side) return side0 + (int64_t)pg * side_pg + r * side_tk;
       const int phys =
           safe_page(p, page_phys ? s_pphys[pi] : btr[imin(tk / p.page, mb - 1)]);
       return kpool + kv_offset(p, phys, kv, tk % p.page);
     };
     // logit key of dense slot i (and the parity-test record)
+    const bool dbg_cand = NFA_COLD(p.dbg_cand_tok != nullptr);
     auto emit = [&](int i, int tk, bool scored, float acc) {
       uint16_t key = 0;
       if (scored) {
         const uint16_t bits = bf16_bits(acc);
         key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
-        if (NFA_COLD(p.dbg_cand_tok != nullptr) && i < p.dbg_cand_cap) {
+        if (NFA_COLD(dbg_cand) && i < p.dbg_cand_cap) {
           p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tk;
           p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
               bits == kNanBits ? kNegInfBits : bits;
         }
-      } else if (NFA_COLD(p.dbg_cand_tok != nullptr) && i < p.dbg_cand_cap) {
+      } else if (NFA_COLD(dbg_cand) && i < p.dbg_cand_cap) {
         p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = -1;
       }
       s_dk[i] = key;
@@ -2452,7 +2471,7 @@ __global__ void __launch_bounds__(SB)
       const unsigned char *qb = (const unsigned char *)p.l2_keys_l;
       const int64_t poff = q4_slots(p) * 16;
       auto q4_of = [&](int i, int &tk) -> int64_t {
-        const int pi = i / bs;
+        const int pi = udiv_p2(i, bs, sd.bs_sh);
         tk = s_pages[pi] * bs + (i - pi * bs);
         if (tk < tok_lo || tk >= tok_hi) return -1;
         return q4_slot(p, req, kv, tk);
@@ -2503,6 +2522,11 @@ __global__ void __launch_bounds__(SB)
     };
     // slots tid, tid + SB, ...: the next slot's loads are in flight while
     // the current slot's dot product runs (rolled: compact code)
+    // the grouped L2 query in registers (the loop's LDS stores would keep
+    // the compiler from hoisting its reads)
+    float qv[4 * CH];
+#pragma unroll
+    for (int e = 0; e < 4 * CH; ++e) qv[e] = vec4 && e < nch * CH ? s_qg[e] : 0.0f;
     int tk = -1;
     const KV *kr = nullptr;
     uint4 r[4];
@@ -2532,7 +2556,7 @@ __global__ void __launch_bounds__(SB)
             unpack_chunk<KV>(r[c], x);
 #pragma unroll
             for (int e = 0; e < CH; ++e) {
-              const float prod = x[e] * s_qg[c * CH + e];
+              const float prod = x[e] * qv[c * CH + e];
               acc = acc + prod;
             }
           }
@@ -2570,7 +2594,7 @@ __global__ void __launch_bounds__(SB)
                        (int *)(smem + sd.a_l1), (int *)(smem + sd.a_l1x),
                        (int *)(smem + sd.a_mid), (int *)(smem + sd.a_mslot)};
   const DenseView dv{s_dk, s_pages, s_pphys, btr, n_dense, bs, p.page, mb,
-                     page_phys};
+                     page_phys, sd.bs_sh, sd.page_sh};
   if (lb.quota > 0) {
     int nreg = 1;
     bool masked = false;
