@@ -365,6 +365,14 @@ def selector_timeline(torch, w, steps, plan):
                 float(g1.max()))
             acc.setdefault('  arrival: row counter + tail set-up (max row)', []).append(
                 float(g2.max()))
+        # arrival steps of the last workgroup when the kernel records them
+        # (marks 28-31: completion wait, group ticket, row ticket, acquire)
+        if (tail[:, 31] > 0).all():
+            for a, bb, name in ((27, 28, 'completion wait + barrier'),
+                                (28, 29, 'group ticket'), (29, 30, 'row ticket'),
+                                (30, 31, 'acquire + barrier'), (31, 0, 'tail set-up')):
+                d = (tail[:, bb] - tail[:, a]) * us
+                acc.setdefault(f'    {name} (max row)', []).append(float(d.max()))
         names = ['row scalars', 'q prep', 'page stats', 'L1 scores+publish']
         for k, name in enumerate(names):
             d = (tile[:, :, k + 1] - tile[:, :, k]) * us

@@ -2370,16 +2370,23 @@ __global__ void __launch_bounds__(SB)
   // requested now, ahead of the barrier below (the logits loop starts from it)
   const int nchs = p.fine_dsub % CH == 0 ? p.fine_dsub / CH : 0;
   const bool l2_pre = p.l2_keys_l != nullptr && !p.l2_quant && nchs > 0 && nchs <= 4;
+  // the side copy of this (request, kv head): page pg's token r starts at
+  // side0 + pg * bs * fine_dsub + r * (CH, chunk-major, or fine_dsub)
+  const KV *side0 = p.l2_keys_l != nullptr
+                        ? (const KV *)p.l2_keys_l + l2_side_index<KV>(p, req, kv, 0, 0)
+                        : nullptr;
   int tk_pre = -1;
   const KV *kr_pre = nullptr;
   uint4 r_pre[4];
   if (l2_pre) {
     if (tid < np_u * bs) {
       const int pi = udiv_p2(tid, bs, sd.bs_sh);
-      const int tk = s_pages[pi] * bs + (tid - pi * bs);
+      const int r = tid - pi * bs;
+      const int pg = s_pages[pi];
+      const int tk = pg * bs + r;
       if (tk >= tok_lo && tk < tok_hi) {
         tk_pre = tk;
-        kr_pre = (const KV *)p.l2_keys_l + l2_side_index<KV>(p, req, kv, tk, 0);
+        kr_pre = side0 + (int64_t)pg * (bs * p.fine_dsub) + r * CH;
       }
     }
 #pragma unroll
@@ -2428,11 +2435,6 @@ __global__ void __launch_bounds__(SB)
     // major) or element d at d (token-major); K pool: the L2 dims' offsets
     auto choff = [&](int c) { return side ? c * bs * CH : s_fdims[c * CH]; };
     auto eoff = [&](int d) { return side ? d : s_fdims[d]; };
-    // the side copy of this (request, kv head): page pg's token r starts at
-    // side0 + pg * bs * fine_dsub + r * (CH, chunk-major, or fine_dsub)
-    const KV *side0 = side ? (const KV *)p.l2_keys_l +
-                                 l2_side_index<KV>(p, req, kv, 0, 0)
-                           : nullptr;
     const int side_pg = bs * p.fine_dsub;
     const int side_tk = p.fine_dsub % CH == 0 ? CH : p.fine_dsub;
     // slot i: its token and L2 row (null outside the candidate range)
