@@ -1584,7 +1584,12 @@ __global__ void __launch_bounds__(SB)
   // waits for them), stores after that pass's scores.
   const bool dw = p.k_new != nullptr && active && owns_last;
   const bool side_late = do_stats && incremental && owns_last && p.l2_keys_l != nullptr;
-  const bool owner_any = dw || owner_late || side_late;
+  // (only the waves holding a written element take part: the index
+  // arithmetic is uniform, and run by every wave it would cost each SIMD
+  // four times its scalar issue slots)
+  const bool owner_any =
+      (dw || owner_late || side_late) &&
+      wave_id() * 64 < imax(imax(p.head_dim, p.head_dim_v), imax(DSUB, p.fine_dsub));
   KV dw_k = 0, dw_v = 0, side_raw = 0;
   float ap_mn = __uint_as_float(0x7F800000u);  // a new page starts from +inf,
   float ap_mx = __uint_as_float(0xFF800000u);  // -inf and 0
@@ -1961,9 +1966,14 @@ __global__ void __launch_bounds__(SB)
   // length (the counter's answer is read after the key staging below waited
   // for every load anyway).
   unsigned int *req_cnt = (unsigned int *)(ws + sd.w_reqcnt);
+  // (through a lane offset the compiler cannot prove uniform: a uniform
+  // address lets the atomic optimizer rewrite the ticket into a wave
+  // reduction that waits for the answer on the spot)
   unsigned int req_rank = 0u;
+  int t_vz = 0;
+  asm volatile("" : "+v"(t_vz));
   if (tid == 0)
-    req_rank = __hip_atomic_fetch_add(&req_cnt[b], 1u, __ATOMIC_RELAXED,
+    req_rank = __hip_atomic_fetch_add(&req_cnt[b + t_vz], 1u, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
   int *g_hist = (int *)(ws + sd.w_hist) + (int64_t)row * 512;
   uint16_t *g_keys = (uint16_t *)(ws + sd.w_keys) + (int64_t)row * sd.kstride;
