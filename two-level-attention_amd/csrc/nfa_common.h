@@ -339,8 +339,10 @@ __device__ __forceinline__ int block_scan_exclusive(int v, int *scratch,
 
 // Exclusive prefix sums of N ints at once over a block of WAVES waves (one
 // pair of barriers for all N); v is replaced by its exclusive prefix, total
-// receives the block totals.  `scratch` needs WAVES * N ints.
-template <int N, int WAVES = NFA_WAVES>
+// receives the block totals.  `scratch` needs WAVES * N ints.  Without
+// `kTrailing` the second barrier is left out: the caller guarantees that
+// another barrier comes before anything writes `scratch` again.
+template <int N, int WAVES = NFA_WAVES, bool kTrailing = true>
 __device__ __forceinline__ void block_scan_n(int (&v)[N], int *scratch,
                                              int (&total)[N]) {
   const int lane = lane_id();
@@ -361,7 +363,7 @@ __device__ __forceinline__ void block_scan_n(int (&v)[N], int *scratch,
     total[k] = __builtin_amdgcn_readlane(t, WAVES - 1);
     v[k] = before + x[k] - v[k];
   }
-  __syncthreads();
+  if constexpr (kTrailing) __syncthreads();
 }
 
 // One wave: threshold bin of the top-K over a 256-bin histogram (bin = high

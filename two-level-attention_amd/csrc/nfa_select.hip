@@ -1229,7 +1229,8 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
     c[1] += (v == T && v != 0u);
   }
   int tot2[2];
-  block_scan_n<2, SW>(c, tmp + 32, tot2);
+  // (its scratch is next written after the barrier that ends the emission)
+  block_scan_n<2, SW, false>(c, tmp + 32, tot2);
   mark(4);
   {
     int eq = c[1];
@@ -2276,7 +2277,9 @@ __global__ void __launch_bounds__(SB)
       }
       if (tie_cut(tf) || tie_cut(tn)) {
         int c2[2] = {(int)__popc(tief), (int)__popc(tien)}, tot2[2];
-        block_scan_n<2, SW>(c2, s_tmp + 32, tot2);
+        // (the position scan below, on other scratch, holds the barriers
+        // before this scratch is written again)
+        block_scan_n<2, SW, false>(c2, s_tmp + 32, tot2);
         int rf = tfb + c2[0], rn = tnb + c2[1];
         for (uint32_t bits = tief; bits; bits &= bits - 1u) {
           const int j = __ffs(bits) - 1;
