@@ -1015,11 +1015,13 @@ __device__ __forceinline__ bool tie_cut(const PoolThr &t) {
 // Stage keys [seg_base, seg_base + seg) of a row into LDS by asynchronous
 // 16-byte copies (seg a multiple of 8 keys): readable after dma_barrier().
 __device__ __forceinline__ void stage_keys(const uint16_t *g_keys, int seg_base,
-                                           int seg, uint16_t *s_keys) {
+                                           int seg, uint16_t *s_keys,
+                                           int first_wave = 0) {
   const int n16 = seg / 8;
   const uint4 *src = reinterpret_cast<const uint4 *>(g_keys + seg_base);
   const uint32_t lds0 = lds_addr(s_keys);
-  for (int u0 = wave_id() * 64; u0 < n16; u0 += SB) {
+  if (wave_id() < first_wave) return;
+  for (int u0 = (wave_id() - first_wave) * 64; u0 < n16; u0 += (SW - first_wave) * 64) {
     const int u = u0 + lane_id();
     if (u < n16) lds_dma16(src + u, lds0 + (uint32_t)u0 * 16);
   }
@@ -2005,10 +2007,19 @@ __global__ void __launch_bounds__(SB)
   const bool any_cand = lb.quota > 0 && tok_hi > tok_lo;
   const int near_start = geo.near_start;
 
-  // row histograms into LDS, reset for the next launch
-  if (tid < 512) {
-    s_hist[tid] = atomicExch(&g_hist[tid], 0);
-    s_hist[512 + tid] = 0;
+  // row histograms into LDS, reset for the next launch: wave 0 takes the
+  // far pool's 256 bins and wave 1 the near pool's (four a lane, as their
+  // threshold scans read them), so each can find its coarse threshold bin
+  // while the other waves copy the keys
+  if (wave_id() < 2) {
+    const int base = wave_id() * 256 + 4 * lane_id();
+    int h[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) h[k] = atomicExch(&g_hist[base + k], 0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s_hist[base + k] = h[k];
+  } else if (tid < 128 + 512) {
+    s_hist[512 + (tid - 128)] = 0;
   }
   if (NFA_COLD(dbg)) {
     for (int w = tid; w < sd.words; w += SB) {
@@ -2058,8 +2069,11 @@ __global__ void __launch_bounds__(SB)
       }
     }
   } else if (sd.nseg == 1) {
-    stage_keys(g_keys, 0, sd.seg, s_keys);
+    stage_keys(g_keys, 0, sd.seg, s_keys, 2);
   }
+  // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
+  if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 8);
+  if (wave_id() == 1) wave_threshold_bin(s_hist + 256, p.k_n, s_tmp + 12);
   dma_barrier();
   if (tid == 0 && req_rank == (unsigned int)(p.hkv - 1)) {
     const bool active = __builtin_amdgcn_readfirstlane(s_ctx[1]) != 0;
@@ -2067,10 +2081,6 @@ __global__ void __launch_bounds__(SB)
     __hip_atomic_store(&req_cnt[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   NFA_MARK(32, 24);
-  // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
-  if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 8);
-  if (wave_id() == 1) wave_threshold_bin(s_hist + 256, p.k_n, s_tmp + 12);
-  __syncthreads();
   NFA_MARK(32, 25);
   const int hbf = s_tmp[8], hbn = s_tmp[12];
   if ((hbf >= 0 || hbn >= 0) && surv_path) {
