@@ -709,7 +709,7 @@ def _cpu_config0(seed, extra_tokens):
         hkv, pages, page, d).transpose(1, 0, 2, 3)
     v_pool[:pages, 0] = np.pad(values, ((0, 0), (0, pad), (0, 0))).reshape(
         hkv, pages, page, d).transpose(1, 0, 2, 3)
-    dims = np.arange(96, 128)   # tail subspace at cmp_ratio 4
+    dims = cpu_tail_dims(d, 4)
     cfg = orc.NfaConfig(
         hq=hq, hkv=hkv, head_dim=d, head_dim_v=d, bs=16, page=page,
         max_blocks=pages + 8, geo_sink=4, geo_near=4096, geo_window=128,
@@ -720,6 +720,19 @@ def _cpu_config0(seed, extra_tokens):
     qs = rng.standard_normal((3 + extra_tokens, 1, hq, d), dtype=np.float32)
     return dict(cfg=cfg, k_pool=k_pool, v_pool=v_pool, bt=bt, ctx=ctx, q=qs,
                 new_k=keys[:, ctx:], new_v=values[:, ctx:])
+
+
+def cpu_tail_dims(head_dim, cmp_ratio):
+    """The production L1/L2 dims (``--nfa_subspace tail``, L2 subspace
+    ``same``): the last head_dim / 2 / cmp_ratio dims of each rotary half
+    (reference sparse_attn/indexer/nfa_indexer.py:112-121), [48..63] and
+    [112..127] for head_dim 128 at cmp_ratio 4.  Computed here without torch:
+    the baseline runs before torch starts."""
+    import numpy as np
+    half = head_dim // 2
+    delta = half // cmp_ratio
+    return np.concatenate((np.arange(half - delta, half),
+                           np.arange(head_dim - delta, head_dim)))
 
 
 def _cpu_apply_writes(kv, upto):
@@ -734,25 +747,47 @@ def _cpu_apply_writes(kv, upto):
         c['v_pool'][pos // page, 0, kv, pos % page] = c['new_v'][kv, i]
 
 
+def cpu_l1_part(cfg, k_pool, bt, length, kv, q_full, p0, p1):
+    """far / near bf16 score bits of pages [p0, p1) of one (row, kv head),
+    no region skipped: the oracle's l1_scores restricted to a page range
+    (page statistics and scores are per page; the pool masks are the
+    row's).  Needs page == bs, so page p0 starts block-table entry p0."""
+    import numpy as np
+    from oracle import nfa_oracle as orc
+    far_pool, near_pool, _ = orc.l1_pools(cfg, length, False, False)
+    kmin, kmax, ksum = orc.page_stats(cfg, k_pool, bt[p0:], length - p0 * cfg.bs,
+                                      kv, n_pages=p1 - p0)
+    g = cfg.group
+    mm, avg = orc.l1_page_scores(cfg, kmin, kmax, ksum, q_full[kv * g:(kv + 1) * g])
+    far_val = mm if cfg.far_method == 'minmax' else avg
+    near_val = avg if cfg.near_method == 'avg' else mm
+    far = np.where(far_pool[p0:p1], far_val, orc.NEG_INF_BITS).astype(np.uint16)
+    near = np.where(near_pool[p0:p1], near_val, orc.NEG_INF_BITS).astype(np.uint16)
+    return far, near
+
+
 def _cpu_l1(args):
     from oracle import nfa_oracle as orc
-    kv, step, length = args
+    kv, step, length, p0, p1 = args
     c = _CPU
     cfg = c['cfg']
     _cpu_apply_writes(kv, step + 1)
     q_full = orc.prepare_q(cfg, c['q'][step, 0], cfg.dims)
-    far, near, geo = orc.l1_scores(cfg, c['k_pool'], c['bt'], length, kv, q_full,
-                                   False, False)
-    i_f = orc.l1_topk(far, 0, geo.far_end, cfg.k_f, cfg.kt_cap)
-    i_n = orc.l1_topk(near, geo.near_start, geo.near_end, cfg.k_n, cfg.kt_cap)
-    return far, near, i_f, i_n
+    return cpu_l1_part(cfg, c['k_pool'], c['bt'], length, kv, q_full, p0, p1)
 
 
 def _cpu_l2(args):
+    import numpy as np
     from oracle import nfa_oracle as orc
-    kv, step, length, (far, near, i_f, i_n) = args
+    kv, step, length, parts = args
     c = _CPU
     cfg = c['cfg']
+    _cpu_apply_writes(kv, step + 1)
+    far = np.concatenate([f for f, _ in parts])
+    near = np.concatenate([n for _, n in parts])
+    geo = orc.l1_geometry(cfg, length)
+    i_f = orc.l1_topk(far, 0, geo.far_end, cfg.k_f, cfg.kt_cap)
+    i_n = orc.l1_topk(near, geo.near_start, geo.near_end, cfg.k_n, cfg.kt_cap)
     q_fine = orc.prepare_q_grouped(cfg, c['q'][step, 0])
     lower, upper, quota = orc.l2_bounds(cfg, length, False, False)
     token, active, pack_r = orc.candidate_slots(cfg, i_f, i_n, far, near, length)
@@ -770,6 +805,7 @@ def _cpu_attention(args):
     kv, step, (gather, vis) = args
     c = _CPU
     cfg = c['cfg']
+    _cpu_apply_writes(kv, step + 1)   # the window holds the decode tokens
     g = cfg.group
     q = c['q'][step][:, kv * g:(kv + 1) * g]
     out = orc.sparse_attention(c['k_pool'][:, :, kv:kv + 1], c['v_pool'][:, :, kv:kv + 1],
@@ -779,29 +815,37 @@ def _cpu_attention(args):
 
 
 def cpu_baseline(warmup=3, steps=10, seed=20261201):
-    """Single-layer decode steps of the 32K fp32 layer on the numpy oracle,
-    the 8 kv heads spread over worker processes: 3 warm-up and 10 timed
-    steps (the context grows by the decode token each step), each split
-    into L1 (decode write, page statistics, scores, top-k), L2 (candidates,
-    logits, top-quota, union) and attention, timed with perf_counter around
-    each phase; medians reported.  Runs before anything touches the GPU."""
+    """Single-layer decode steps of the 32K fp32 layer on the numpy oracle
+    over every host CPU: 3 warm-up and 10 timed steps (the context grows by
+    the decode token each step), each split into L1 (decode write, page
+    statistics and scores; each kv head's pages in ``cores // 8`` ranges,
+    one worker task each), L2 (L1 top-k, candidates, logits, top-quota,
+    union; one task per kv head) and attention (one task per kv head), timed
+    with perf_counter around each phase; medians reported.  Runs before
+    anything touches the GPU."""
     import multiprocessing as mp
     import statistics
     _CPU.clear()
     _CPU.update(_cpu_config0(seed, warmup + steps))
     hkv = _CPU['cfg'].hkv
     cores = os.cpu_count() or 1
-    workers = max(1, min(hkv, cores))
+    workers = max(1, cores)
+    # page ranges per kv head in the L1 phase: every CPU busy
+    nparts = max(1, min(4, cores // hkv))
     phases = {'l1': [], 'l2': [], 'attention': []}
     with mp.get_context('fork').Pool(workers) as pool:
         for step in range(warmup + steps):
             length = _CPU['ctx'] + step + 1
+            kt = -(-length // _CPU['cfg'].bs)
+            cuts = [kt * i // nparts for i in range(nparts + 1)]
             t0 = time.perf_counter()
-            l1 = pool.map(_cpu_l1, [(kv, step, length) for kv in range(hkv)],
+            l1 = pool.map(_cpu_l1, [(kv, step, length, cuts[i], cuts[i + 1])
+                                    for kv in range(hkv) for i in range(nparts)],
                           chunksize=1)
             t1 = time.perf_counter()
-            l2 = pool.map(_cpu_l2, [(kv, step, length, l1[kv]) for kv in range(hkv)],
-                          chunksize=1)
+            l2 = pool.map(_cpu_l2, [(kv, step, length,
+                                     l1[kv * nparts:(kv + 1) * nparts])
+                                    for kv in range(hkv)], chunksize=1)
             t2 = time.perf_counter()
             pool.map(_cpu_attention, [(kv, step, l2[kv]) for kv in range(hkv)],
                      chunksize=1)
@@ -822,9 +866,13 @@ def cpu_baseline(warmup=3, steps=10, seed=20261201):
                 host_cpus=cores,
                 sample=f'{steps} timed single-layer decode steps after {warmup} '
                        'warm-up steps of the 32768-token fp32 layer (Qwen3-8B '
-                       'layer geometry, page 16, production flags) on the numpy '
-                       f'oracle, the {hkv} kv heads in {workers} worker processes; '
-                       'median per phase')
+                       'layer geometry, page 16, production flags: minmax far / '
+                       'avg near pools, L1 and L2 dims [48..63] + [112..127] '
+                       '(tail subspace at cmp_ratio 4), 96 + 32 pages, 1024 '
+                       'tokens, sink 4, window 128) on the numpy oracle in '
+                       f'{workers} worker processes (L1: {hkv} kv heads x '
+                       f'{nparts} page ranges; L2 and attention: one task per kv '
+                       'head); median per phase')
 
 
 def warm_events(torch, n):

@@ -267,6 +267,17 @@ int64_t nfa_attn_workspace_bytes(const NfaAttnParams *p);
 /* A1-A9: decode write + page statistics + L1 + L2 + union for one layer. */
 int32_t nfa_select_layer(const NfaSelectParams *p, void *stream);
 
+/* No counterpart in the reference (its Triton launches have no instances to
+   choose): diagnostics of the launch plan of nfa_select_layer for these
+   parameters, for tests and benchmarks.  Writes up to n of: [0] kernel
+   instance (0 single-pass tiles, 1 multi-pass tiles, 2 multi-pass tiles that
+   list their top-K pages for the tail, -1 protected-only union), [1] tiles
+   per row in one dispatch round, [2] grid tiles, [3] tiles of a row of
+   max_blocks pages, [4] their passes, [5] LDS bytes per workgroup, [6] key
+   segments of the tail, [7] workspace bytes (clamped to int32).  Launches
+   nothing. */
+int32_t nfa_select_plan(const NfaSelectParams *p, int32_t *out, int32_t n);
+
 /* No counterpart in the reference.  nfa_select_layer for callers that cannot
    allocate device memory (code under hipGraph capture, tight serving loops,
    harnesses that forbid hipMalloc): the same kernels and results, but the

@@ -723,13 +723,15 @@ class RowResult:
 
 
 def apply_decode_write(k_pool, v_pool, keys, values, slots, page):
-    """K/V write of one token per row at its slot (paged_region_kernels.py:15-61)."""
+    """K/V write of one token per row at its slot (paged_region_kernels.py:15-61).
+    ``v_pool`` None writes the keys only (selection never reads V)."""
     for b, slot in enumerate(np.asarray(slots).tolist()):
         if slot < 0:
             continue
         phys, off = divmod(int(slot), page)
         k_pool[phys, 0, :, off, :] = keys[b, :, 0, :]
-        v_pool[phys, 0, :, off, :] = values[b, :, 0, :]
+        if v_pool is not None:
+            v_pool[phys, 0, :, off, :] = values[b, :, 0, :]
 
 
 def select_row(cfg: NfaConfig, k_pool, bt_row, length, q_row, kv,

@@ -84,11 +84,13 @@ def to_np(t):
         t.detach().cpu().numpy()
 
 
-def snapshot(cache, layer_idx, batch):
-    """Numpy copy of everything the selector reads for ``layer_idx``."""
+def snapshot(cache, layer_idx, batch, with_v=True):
+    """Numpy copy of everything the selector reads for ``layer_idx`` (the V
+    pool too unless ``with_v`` is False: selection never reads it)."""
     layer = cache.layers[layer_idx]
     return dict(
-        k_pool=to_np(layer.kv_pool_k), v_pool=to_np(layer.kv_pool_v),
+        k_pool=to_np(layer.kv_pool_k),
+        v_pool=to_np(layer.kv_pool_v) if with_v else None,
         block_table=to_np(cache.block_table_buf[layer_idx]).astype(np.int64),
         lengths=to_np(cache.planned_lengths_buf[:batch]).astype(np.int64),
         req_ids=to_np(cache.valid_req_ids_buf[:batch]).astype(np.int64),
@@ -97,10 +99,14 @@ def snapshot(cache, layer_idx, batch):
         skip_near=to_np(cache.skip_near_layer_buf[layer_idx]))
 
 
-def run_oracle(cfg, snap, q, decode=None, max_vis=1024, middle_only=False):
-    """Oracle selection on a snapshot; ``decode`` = (keys, values, slots)."""
-    k_pool = snap['k_pool'].copy()
-    v_pool = snap['v_pool'].copy()
+def run_oracle(cfg, snap, q, decode=None, max_vis=1024, middle_only=False,
+               copy=True):
+    """Oracle selection on a snapshot; ``decode`` = (keys, values, slots).
+    ``copy`` False applies the decode write to the snapshot's own pools."""
+    k_pool = snap['k_pool'].copy() if copy else snap['k_pool']
+    v_pool = snap['v_pool']
+    if copy and v_pool is not None:
+        v_pool = v_pool.copy()
     if decode is not None:
         keys, values, slots = decode
         active = snap['active']
@@ -203,17 +209,29 @@ def prod_cache(lengths, *, hkv=2, hq=8, dtype=torch.bfloat16, max_req=4,
 
 
 def run_and_compare(cache, indexer, req_ids, q, decode, *, scaling=1.0,
-                    middle_only=False, check_debug=True, return_pools=False):
+                    middle_only=False, check_debug=True, return_pools=False,
+                    with_v=True, plan=None):
     """Run the HIP selector on layer 0 and the oracle on a snapshot of the
     same cache; compare every intermediate bit for bit.  Returns the oracle's
-    per-row results (and the post-decode-write pools with ``return_pools``)."""
+    per-row results (and the post-decode-write pools with ``return_pools``).
+
+    ``check_debug`` False runs the production launch (no debug buffers, the
+    launch the benchmarks and the model time) and compares its gather rows,
+    visible lengths and decode-written rows.  ``with_v`` False leaves the V
+    pool out of the snapshot (large contexts; the returned V pool is None).
+    ``plan``, a dict, receives the launch plan (kernel instance, tiles,
+    passes)."""
     from sparse_attn.indexer.nfa_layer_batch_selector import \
         select_topk_for_layer_batched
     b = len(req_ids)
     cfg = cfg_from(cache, indexer, scaling)
-    snap = snapshot(cache, 0, b)
+    snap = snapshot(cache, 0, b, with_v=with_v)
     max_vis = cache.gather_indices_for_layer(0).shape[-1]
     dbg = {} if check_debug else None
+    if plan is not None:
+        plan.clear()
+        plan.update(launch_plan(cache, indexer, req_ids, q, decode, scaling,
+                                middle_only))
     sel_out = None
     if middle_only:
         sel_out = (torch.full((b, cache.num_kv_heads, max_vis), -7,
@@ -230,7 +248,8 @@ def run_and_compare(cache, indexer, req_ids, q, decode, *, scaling=1.0,
         dec_np = tuple(t.float().cpu().numpy() if t.is_floating_point()
                        else t.cpu().numpy() for t in decode)
     res, k_pool, v_pool = run_oracle(cfg, snap, q.float().cpu().numpy(), dec_np,
-                                     max_vis=max_vis, middle_only=middle_only)
+                                     max_vis=max_vis, middle_only=middle_only,
+                                     copy=False)
     del snap
     if middle_only:
         gather, vis = sel_out[0].cpu().numpy(), sel_out[1].cpu().numpy()
@@ -248,11 +267,13 @@ def run_and_compare(cache, indexer, req_ids, q, decode, *, scaling=1.0,
                                           err_msg=tag)
             if not check_debug or region_mode == 3 or r.far is None:
                 continue
-            kt = len(r.far)
+            # pages past the block-table width are never scored (the
+            # oracle's scores there are outside every top-k)
+            kt = min(len(r.far), cfg.max_blocks)
             np.testing.assert_array_equal(u16(dbg['far'][row_b, kv, :kt]),
-                                          r.far.astype(np.int64), err_msg=tag)
+                                          r.far[:kt].astype(np.int64), err_msg=tag)
             np.testing.assert_array_equal(u16(dbg['near'][row_b, kv, :kt]),
-                                          r.near.astype(np.int64), err_msg=tag)
+                                          r.near[:kt].astype(np.int64), err_msg=tag)
             np.testing.assert_array_equal(
                 dbg['i_f'][row_b, kv, :cfg.k_f].cpu().numpy(), r.i_f, err_msg=tag)
             np.testing.assert_array_equal(
@@ -284,9 +305,34 @@ def run_and_compare(cache, indexer, req_ids, q, decode, *, scaling=1.0,
             np.testing.assert_array_equal(
                 layer.kv_pool_k[phys, 0, :, off].float().cpu().numpy(),
                 k_pool[phys, 0, :, off])
-            np.testing.assert_array_equal(
-                layer.kv_pool_v[phys, 0, :, off].float().cpu().numpy(),
-                v_pool[phys, 0, :, off])
+            if v_pool is not None:
+                np.testing.assert_array_equal(
+                    layer.kv_pool_v[phys, 0, :, off].float().cpu().numpy(),
+                    v_pool[phys, 0, :, off])
     if return_pools:
         return res, k_pool, v_pool
     return res
+
+
+def launch_plan(cache, indexer, req_ids, q, decode=None, scaling=1.0,
+                middle_only=False):
+    """The selector's launch plan for this call (kernel instance, tiles per
+    row, passes of a max_blocks row), queried without launching."""
+    import ctypes
+
+    from sparse_attn import _native as nat
+    from sparse_attn.indexer.nfa_layer_batch_selector import \
+        select_layer_params
+    b = len(req_ids)
+    sel_out = None
+    if middle_only:
+        sel_out = (cache.gather_indices_for_layer(0)[:b],
+                   cache.visible_lens_for_layer(0)[:b])
+    p, _keep = select_layer_params(cache, 0, req_ids, q,
+                                   attention_ns(indexer, scaling), decode,
+                                   middle_only, sel_out)
+    out = (ctypes.c_int32 * 8)()
+    lib = nat.load_library()
+    nat.check(lib.nfa_select_plan(ctypes.byref(p), out, 8), 'nfa_select_plan')
+    return dict(zip(('instance', 'round_tiles', 'grid_tiles', 'row_tiles',
+                     'passes', 'lds', 'segments', 'workspace'), list(out)))

@@ -13,9 +13,16 @@ at the token positions), and compares the HIP path with the oracle:
   rtol 1e-4 / atol 1e-5 (fp32 KV) against the float64 oracle.
 
 Workloads: 131072-token context at batch 1 with 20 incremental decode steps
-(compared at the rebuild step and two incremental steps), a 32768-token
-context with fp32 KV and fp32 queries, and 16 requests of lengths drawn
-uniformly from [32768, 131072] in one shared cache.
+(compared at the rebuild step and three incremental steps), a 32768-token
+context with fp32 KV and fp32 queries, 16 requests of lengths drawn
+uniformly from [32768, 131072] in one shared cache, and a 1M-token context
+with the 32/8 heads (the multi-pass selector instance whose tiles list their
+own top-K pages for the tail).
+
+Every workload also runs the production launch -- no debug buffers, the
+launch the benchmarks and the model patches time -- for at least one step,
+whose gather rows, visible lengths and decode-written rows are compared with
+the oracle.
 """
 from types import SimpleNamespace
 
@@ -84,7 +91,16 @@ def test_128k_context_batch1_incremental_steps():
         cache.plan_common(req_ids)
         q = bf16_randn((1, HQ, D), gen, GPU)
         decode = _decode_token(cache, 1, gen, torch.bfloat16, [length + step])
-        if step in (0, 9, 19):
+        if step == 14:
+            # the production launch (no debug buffers), incremental statistics
+            plan = {}
+            res = run_and_compare(cache, indexer, req_ids, q, decode,
+                                  scaling=SCALE, check_debug=False, plan=plan)
+            assert plan['instance'] == 0 and plan['passes'] == 1, plan
+            assert all(res[0][kv].vis_len == 1024 for kv in range(HKV))
+            print('# 128K step 15 (production launch): selections bit-exact',
+                  flush=True)
+        elif step in (0, 9, 19):
             res, k_pool, v_pool = run_and_compare(
                 cache, indexer, req_ids, q, decode, scaling=SCALE,
                 return_pools=True)
@@ -118,18 +134,65 @@ def test_32k_context_fp32_kv():
 
 
 def test_16_ragged_requests_32k_to_128k():
-    """16 requests with lengths U(32768, 131072) in one shared cache."""
+    """16 requests with lengths U(32768, 131072) in one shared cache: the
+    rebuild step through the production launch, the next (incremental) step
+    with every debug output and attention."""
     lengths = torch.randint(32768, 131073, (16,),
                             generator=torch.Generator().manual_seed(20261201)).tolist()
     cache, gen, req_ids = prod_cache(lengths, hkv=HKV, hq=HQ, max_req=16,
                                      key_fn=_outlier_keys)
     indexer = make_indexer()
-    cache.new_step(req_ids)
-    cache.plan_common(req_ids)
-    q = bf16_randn((16, HQ, D), gen, GPU)
-    decode = _decode_token(cache, 16, gen, torch.bfloat16, lengths)
     print(f'# 16 ragged requests, {sum(lengths)} tokens', flush=True)
-    res, k_pool, v_pool = run_and_compare(cache, indexer, req_ids, q, decode,
-                                          scaling=SCALE, return_pools=True)
-    assert all(res[r][kv].vis_len == 1024 for r in range(16) for kv in range(HKV))
-    _check_attention(cache, q, k_pool, v_pool, 16, torch.bfloat16)
+    for step in range(2):
+        cache.new_step(req_ids)
+        cache.plan_common(req_ids)
+        q = bf16_randn((16, HQ, D), gen, GPU)
+        decode = _decode_token(cache, 16, gen, torch.bfloat16,
+                               [n + step for n in lengths])
+        plan = {}
+        res, k_pool, v_pool = run_and_compare(cache, indexer, req_ids, q, decode,
+                                              scaling=SCALE, return_pools=True,
+                                              check_debug=step == 1, plan=plan)
+        assert plan['instance'] == 1, plan  # multi-pass tiles, no page lists
+        assert all(res[r][kv].vis_len == 1024 for r in range(16) for kv in range(HKV))
+        print(f'# 16 ragged step {step + 1} (debug {step == 1}): selections '
+              'bit-exact', flush=True)
+        if step == 1:
+            _check_attention(cache, q, k_pool, v_pool, 16, torch.bfloat16)
+        del k_pool, v_pool
+        cache.commit_step()
+
+
+def test_1m_context_8_kv_heads_page_lists():
+    """1M-token context (plus 8192 tokens, so that every near-pool page id
+    passes 16 bits) with the benchmark's 32/8 heads: 32 tiles per row of 8
+    passes each, whose tiles list their own top-K pages for the tail (the
+    instance the 1M benchmark times).  The rebuild step is compared with
+    every debug output, the next (incremental) step through the production
+    launch."""
+    length = (1 << 20) + 8192
+    geo = RegionGeometry(sink=4, near=4096, window=128, page=16, max_new_tokens=32)
+    cache, gen, req_ids = prod_cache([length], hkv=HKV, hq=HQ, max_req=1,
+                                     geometry=geo, key_fn=_outlier_keys)
+    indexer = make_indexer()
+    print('# 1M workload (8 kv heads) ready', flush=True)
+    for step in range(2):
+        cache.new_step(req_ids)
+        cache.plan_common(req_ids)
+        q = bf16_randn((1, HQ, D), gen, GPU)
+        decode = _decode_token(cache, 1, gen, torch.bfloat16, [length + step])
+        plan = {}
+        res = run_and_compare(cache, indexer, req_ids, q, decode, scaling=SCALE,
+                              check_debug=step == 0, with_v=False, plan=plan)
+        assert plan['instance'] == 2 and plan['round_tiles'] == 32, plan
+        assert plan['passes'] == 8, plan
+        for kv in range(HKV):
+            r = res[0][kv]
+            assert r.vis_len == 1024
+            # the near pool's pages (and its page-list entries) lie past
+            # 16-bit ids; far pages reach 65783 at this length
+            assert int(r.i_n.min()) > 65535
+        print(f'# 1M step {step + 1} (debug {step == 0}): selections bit-exact',
+              flush=True)
+        del res
+        cache.commit_step()

@@ -351,3 +351,64 @@ def test_avg_top2_needs_two_heads_per_group():
         select_topk_for_layer_batched(
             cache, 0, req_ids, q,
             attention=attention_ns(make_indexer(far_method='avg_top2'), 1.0))
+
+
+@pytest.mark.parametrize('lengths,hkv,hq,instance', [
+    ([20000], 2, 8, 0),         # single-pass tiles
+    ([540000], 8, 32, 2),       # multi-pass tiles listing their top-K pages
+])
+def test_block_smaller_than_page_scores_block_table_width(lengths, hkv, hq, instance):
+    """--tia_block_size 16 over 32-token pages: ceil(L / 16) exceeds the
+    block-table width, and only its first max_blocks L1 blocks are scored
+    (selector:205-206).  The tiles split those pages; the tail's key scans
+    and the page lists of long rows (second case, 16886 pages per row) must
+    cover exactly them."""
+    geo = RegionGeometry(sink=4, near=4096, window=128, page=32, max_new_tokens=64)
+    cache, gen, req_ids = _prod_cache(lengths, hkv=hkv, hq=hq, max_req=1,
+                                      geometry=geo)
+    assert -(-lengths[0] // 16) > cache.max_blocks
+    indexer = make_indexer()
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = bf16_randn((1, hq, 128), gen, DEV)
+    decode = _decode_inputs(cache, 1, gen, torch.bfloat16)
+    plan = {}
+    print(f'# block 16 / page 32, {lengths[0]} tokens: selector + oracle', flush=True)
+    run_and_compare(cache, indexer, req_ids, q, decode,
+                    scaling=0.08838834764831845, plan=plan, with_v=False)
+    assert plan['instance'] == instance, plan
+
+
+def test_handover_over_incremental_production_steps():
+    """Regression test of the cross-workgroup hand-over without the L2
+    writeback: 30 incremental decode steps through the production launch
+    (the tiles hand keys, page lists and histograms to the tail through
+    device-scope stores and atomics), on 6 rows whose tiles spread over
+    several XCDs (workgroup row + 6 * tile), every step compared with the
+    oracle."""
+    cache, gen, req_ids = _prod_cache([9000, 20500, 14000], max_req=3)
+    indexer = make_indexer()
+    for step in range(30):
+        cache.new_step(req_ids)
+        cache.plan_common(req_ids)
+        q = bf16_randn((3, cache.num_query_heads, 128), gen, DEV)
+        decode = _decode_inputs(cache, 3, gen, torch.bfloat16)
+        run_and_compare(cache, indexer, req_ids, q, decode,
+                        scaling=0.08838834764831845, check_debug=False)
+        cache.commit_step()
+
+
+def test_batch_wider_than_the_output_rows_is_rejected():
+    """A batch of more rows than the cache's gather rows (request slots) is
+    rejected before any launch instead of writing past them."""
+    cache, gen, req_ids = _prod_cache([3000, 3100], max_req=2)
+    rows = req_ids + [-1]   # within max_query_tokens, beyond max_requests
+    cache.new_step(rows)
+    cache.plan_common(rows)
+    q = bf16_randn((3, cache.num_query_heads, 128), gen, DEV)
+    before = cache.gather_indices_buf.clone()
+    with pytest.raises(ValueError, match='selection outputs hold 2 rows'):
+        select_topk_for_layer_batched(cache, 0, rows, q,
+                                      attention=attention_ns(make_indexer(), 1.0))
+    torch.cuda.synchronize()
+    assert torch.equal(cache.gather_indices_buf, before)

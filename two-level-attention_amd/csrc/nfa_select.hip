@@ -209,8 +209,8 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   s.w_total = w;
 }
 
-// `cus`: compute units of the device (the tile split depends on it, the
-// workspace layout does not)
+// `cus`: compute units of the device; the tile split and with it the
+// workspace layout (tile counts, survivor lists) depend on it
 __host__ __device__ inline SelDims sel_dims(const NfaSelectParams &p, int cus) {
   SelDims s;
   const int nrows = p.batch * p.hkv;
@@ -1456,8 +1456,10 @@ __global__ void __launch_bounds__(SB)
       c4[1] = make_int4(slot0, sp.tiles, t0v, t1v);
       c4[2] = make_int4(g.kt_eff, g.near_start, g.swa_lo_blk, g.far_end);
       c4[3] = make_int4(g.near_end, g.sink_hi, g.swa_hi, g.orig_far_hi);
+      // (word 19: the pages the tiles split, clamped to the block-table
+      // width; kt_eff at word 8 stays unclamped for the pool geometry)
       c4[4] = make_int4(g.spl, g.byp_blk,
-                        (g.byp_cond ? 1 : 0) | (g.sink_unaligned ? 2 : 0), 0);
+                        (g.byp_cond ? 1 : 0) | (g.sink_unaligned ? 2 : 0), kt0);
     }
   }
   // LDS: dims, fine dims, raw query rows, histogram
@@ -1475,7 +1477,7 @@ __global__ void __launch_bounds__(SB)
   if (tid < 512) s_hist[tid] = 0;
   lds_barrier();
   NFA_MARK(0, 1);
-  int32_t L, slot_b, t0, t1, kt_eff;
+  int32_t L, slot_b, t0, t1, kt_tiles;
   int64_t req;
   bool active;
   TileSplit split;
@@ -1490,7 +1492,7 @@ __global__ void __launch_bounds__(SB)
     split.tiles = u(c.y);
     t0 = u(c.z);
     t1 = u(c.w);
-    kt_eff = u(c4[2].x);
+    kt_tiles = u(c4[4].w);
   }
   // tiles past the row's pages take no part, neither scores nor arrival
   if (tile >= split.tiles) return;
@@ -1585,7 +1587,12 @@ __global__ void __launch_bounds__(SB)
   // The owner's decode K/V write, statistics append and L2 side row: loads
   // issued once the first pass's statistics have landed (no staging wait
   // waits for them), stores after that pass's scores.
-  const bool dw = p.k_new != nullptr && active && owns_last;
+  // (the decode write falls to the row's last tile when the last page lies
+  // past the pages the tiles split: a block-table row of max_blocks pages
+  // of `page` tokens can hold more than max_blocks blocks of bs < page
+  // tokens, and those have no statistics to append to)
+  const bool dw = p.k_new != nullptr && active && last_blk >= t0 &&
+                  (last_blk < t1 || t1 >= kt_tiles);
   const bool side_late = do_stats && incremental && owns_last && p.l2_keys_l != nullptr;
   // (only the waves holding a written element take part: the index
   // arithmetic is uniform, and run by every wave it would cost each SIMD
@@ -1853,7 +1860,7 @@ __global__ void __launch_bounds__(SB)
   //      its first page on, for the tail to read instead of every key of the
   //      row.  The tile's K-th key: the coarse bin from the tile histogram,
   //      then the low bytes of the tile's keys in that bin.
-  if (SURV && kt_eff > kSurvPages) {
+  if (SURV && kt_tiles > kSurvPages) {
     if (wave_id() == 0) wave_threshold_bin(s_hist, p.k_f, s_tmp + 40);
     if (wave_id() == 1) wave_threshold_bin(s_hist + 256, p.k_n, s_tmp + 44);
     int *s_lo = (int *)(smem + sd.a_stage);  // low-byte histograms (far | near)
@@ -1955,7 +1962,10 @@ __global__ void __launch_bounds__(SB)
   const int L = __builtin_amdgcn_readfirstlane(s_ctx[0]);
   const int64_t req = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(s_ctx[3]) << 32) |
                                 (uint32_t)__builtin_amdgcn_readfirstlane(s_ctx[2]));
-  const int kt_eff = __builtin_amdgcn_readfirstlane(s_ctx[8]);
+  // the pages the tiles split and keyed: ceil(L / bs) clamped to the
+  // block-table width (pages past it are never scored, selector:205-206);
+  // the survivor offsets and the key scans cover exactly these
+  const int kt_tiles = __builtin_amdgcn_readfirstlane(s_ctx[19]);
   const int skf = __builtin_amdgcn_readfirstlane(s_ctx[23]);
   const bool skip_far = (skf & 1) != 0;
   const bool skip_near = (skf & 2) != 0;
@@ -2001,9 +2011,12 @@ __global__ void __launch_bounds__(SB)
     p.dbg_bounds[b * 3 + 1] = lb.upper;
     p.dbg_bounds[b * 3 + 2] = lb.quota;
   }
-  // candidate tokens lie in [tok_lo, tok_hi) and exist only when quota > 0
+  // candidate tokens lie in [tok_lo, tok_hi) and exist only when quota > 0;
+  // below S_cap = max_blocks * bs too (selector:1167-1184): a bypass page
+  // past it (a block-table row of bs < page holds more blocks than that)
+  // is no candidate
   const int tok_lo = imax(p.sink_tokens, lb.lower);
-  const int tok_hi = imin(imin(lb.lo, L), lb.upper);
+  const int tok_hi = imin(imin(imin(lb.lo, L), lb.upper), mb * bs);
   const bool any_cand = lb.quota > 0 && tok_hi > tok_lo;
   const int near_start = geo.near_start;
 
@@ -2036,7 +2049,7 @@ __global__ void __launch_bounds__(SB)
   // and they fit the LDS; their counts come first.
   const int ntile = __builtin_amdgcn_readfirstlane(s_ctx[5]);
   int *s_spre = s_tmp + 64;  // survivors of the tiles before tile t
-  const bool surv_on = SURV && kt_eff > kSurvPages;
+  const bool surv_on = SURV && kt_tiles > kSurvPages;
   if (surv_on && wave_id() == 0) {
     const int lane = lane_id();
     const int cnt = lane < ntile && ntile <= 64
@@ -2053,8 +2066,8 @@ __global__ void __launch_bounds__(SB)
   uint32_t *s_skey = (uint32_t *)(s_spage + sd.sc);       // and keys
   if (surv_path) {
     // each tile's list in runs of 64 entries, copied straight into LDS
-    const int t_base = kt_eff / ntile;
-    const int t_rem = kt_eff - t_base * ntile;
+    const int t_base = kt_tiles / ntile;
+    const int t_rem = kt_tiles - t_base * ntile;
     const int *sv_page = (const int *)(ws + sd.w_surv) + (int64_t)row * 2 * sd.kstride;
     const uint32_t *sv_key = (const uint32_t *)(sv_page + sd.kstride);
     for (int t = wave_id(); t < ntile; t += SW) {
@@ -2101,7 +2114,7 @@ __global__ void __launch_bounds__(SB)
         stage_keys(g_keys, seg_base, sd.seg, s_keys);
         dma_barrier();
       }
-      const int n = imin(sd.seg, kt_eff - seg_base);
+      const int n = imin(sd.seg, kt_tiles - seg_base);
       // sixteen keys per thread from two 16-byte reads (the segment holds a
       // multiple of 16 keys): one round of the block up to 16384 pages
       for (int v = tid; v < (n + 15) / 16; v += SB) {
@@ -2242,7 +2255,7 @@ __global__ void __launch_bounds__(SB)
       stage_keys(g_keys, seg_base, sd.seg, s_keys);
       dma_barrier();
     }
-    const int n = imin(sd.seg, kt_eff - seg_base);
+    const int n = imin(sd.seg, kt_tiles - seg_base);
     const int n16 = (n + 15) / 16;  // the segment holds a multiple of 16 keys
     for (int v0 = 0; v0 < n16; v0 += SB) {  // uniform trip count
       const int v = v0 + tid;
@@ -2850,7 +2863,29 @@ static int select_check(const NfaSelectParams *p, bool need_workspace) {
 
 extern "C" int64_t nfa_select_workspace_bytes(const NfaSelectParams *p) {
   if (p == nullptr || p->batch <= 0 || p->hkv <= 0) return 0;
-  return nfa::sel_dims(*p, 256).w_total;  // independent of the CU count
+  // the same CU count as the launch: the tile split (tiles per row, passes,
+  // page lists) and so the workspace layout depend on it
+  return nfa::sel_dims(*p, nfa::device_cus()).w_total;
+}
+
+// The launch plan of a checked call: which kernel instance runs and how a
+// row of max_blocks pages is tiled (parity tests assert the instance).
+extern "C" int32_t nfa_select_plan(const NfaSelectParams *p, int32_t *out, int32_t n) {
+  const int rc = select_check(p, false);
+  if (rc != NFA_OK) return rc;
+  if (out == nullptr || n < 0) {
+    nfa_set_error("nfa_select_plan: null output");
+    return NFA_EINVAL;
+  }
+  const SelDims sd = nfa::sel_dims(*p, nfa::device_cus());
+  const nfa::TileSplit sp = nfa::tile_split(p->max_blocks, sd.tcap);
+  const int passes =
+      sp.span <= nfa::kSpanMax ? 1 : 1 + (sp.span - nfa::kSpanMax + nfa::TP - 1) / nfa::TP;
+  const int32_t v[8] = {p->protected_only ? -1 : (sd.multi ? (sd.surv ? 2 : 1) : 0),
+                        sd.tcap, sd.ntiles, sp.tiles, passes, sd.lds, sd.nseg,
+                        (int32_t)(sd.w_total < INT32_MAX ? sd.w_total : INT32_MAX)};
+  for (int i = 0; i < n && i < 8; ++i) out[i] = v[i];
+  return NFA_OK;
 }
 
 // Lets `kernel` take up to kLdsMax bytes of dynamic LDS on the current

@@ -143,7 +143,7 @@ class NfaGateParams(ctypes.Structure):
 EXPORTS = (
     'nfa_abi_version', 'nfa_wall_clock_khz', 'nfa_select_params_size', 'nfa_attn_params_size',
     'nfa_last_error', 'nfa_select_workspace_bytes', 'nfa_attn_workspace_bytes',
-    'nfa_select_layer', 'nfa_sparse_attn_decode', 'nfa_paged_write_decode',
+    'nfa_select_layer', 'nfa_select_plan', 'nfa_sparse_attn_decode', 'nfa_paged_write_decode',
     'nfa_paged_write_prefill', 'nfa_linear_params_size', 'nfa_rope_params_size',
     'nfa_decode_linear', 'nfa_qk_norm_rope_decode', 'nfa_rmsnorm_decode',
     'nfa_gate_params_size', 'nfa_region_profile', 'nfa_attn_partial_size',
@@ -184,6 +184,9 @@ def load_library(path: str = None):
         lib.nfa_attn_workspace_bytes.argtypes = [ctypes.POINTER(NfaAttnParams)]
         lib.nfa_select_layer.restype = _i32
         lib.nfa_select_layer.argtypes = [ctypes.POINTER(NfaSelectParams), _ptr]
+        lib.nfa_select_plan.restype = _i32
+        lib.nfa_select_plan.argtypes = [ctypes.POINTER(NfaSelectParams),
+                                        ctypes.POINTER(_i32), _i32]
         lib.nfa_select_layer_noalloc.restype = _i32
         lib.nfa_select_layer_noalloc.argtypes = [ctypes.POINTER(NfaSelectParams), _ptr]
         lib.nfa_sparse_attn_decode.restype = _i32

@@ -182,6 +182,10 @@ class GraphRunner:
         padded = list(req_ids) + [-1] * (bucket - rows)
         width = self.visible_bucket_for(cache, padded)
         cache.plan_common(padded)
+        # a runner that never captured (eager only) has not prepared the
+        # narrower visible buckets: the step prepares the one it uses (never
+        # under capture; capture_all prepares them all up front)
+        cache.ensure_visible_buckets((width,))
         cache.set_active_visible_bucket(width)
         ids, pos = self._bucket_inputs(bucket)
         n = input_ids.shape[0]

@@ -226,6 +226,12 @@ def select_layer_params(cache, layer_idx, req_ids, query_states,
     if (gather_out.dtype != torch.int32 or not gather_out.is_contiguous()
             or vis_out.dtype != torch.int32 or not vis_out.is_contiguous()):
         raise ValueError('selection outputs must be contiguous int32')
+    if (gather_out.ndim != 3 or vis_out.ndim != 2 or gather_out.shape[0] < b
+            or vis_out.shape[0] < b or gather_out.shape[1] != hkv
+            or vis_out.shape[1] != hkv):
+        # the kernel writes one gather row per (batch row, kv head)
+        raise ValueError(f'selection outputs hold {gather_out.shape[0]} rows of '
+                         f'{gather_out.shape[1]} kv heads; the call needs {b} of {hkv}')
 
     kv_dtype = layer0.kv_pool_k.dtype
     quant = bool(getattr(indexer, 'l2_quant', False))
@@ -364,6 +370,14 @@ def select_topk_for_layer_batched(cache, layer_idx, req_ids, query_states,
             _debug['clock'] = torch.zeros((b * hkv, ntiles + 1, 32),
                                           dtype=torch.int64, device=device)
             p.dbg_clock = _debug['clock'].data_ptr()
+    if _debug is not None:
+        # the launch plan: kernel instance, tiles per row, passes of a row of
+        # max_blocks pages (tests assert which instance a shape runs)
+        plan = (ctypes.c_int32 * 8)()
+        nat.check(lib.nfa_select_plan(ctypes.byref(p), plan, 8), 'nfa_select_plan')
+        _debug['plan'] = dict(zip(('instance', 'round_tiles', 'grid_tiles',
+                                   'row_tiles', 'passes', 'lds', 'segments',
+                                   'workspace'), list(plan)))
     rc = lib.nfa_select_layer(ctypes.byref(p), nat.stream_handle())
     if rc == -1 and 'LDS' in lib.nfa_last_error().decode():
         raise FallbackRequired(lib.nfa_last_error().decode())
