@@ -815,23 +815,25 @@ def _cpu_attention(args):
 
 
 def cpu_baseline(warmup=3, steps=10, seed=20261201):
-    """Single-layer decode steps of the 32K fp32 layer on the numpy oracle
-    over every host CPU: 3 warm-up and 10 timed steps (the context grows by
-    the decode token each step), each split into L1 (decode write, page
-    statistics and scores; each kv head's pages in ``cores // 8`` ranges,
-    one worker task each), L2 (L1 top-k, candidates, logits, top-quota,
-    union; one task per kv head) and attention (one task per kv head), timed
-    with perf_counter around each phase; medians reported.  Runs before
-    anything touches the GPU."""
+    """Single-layer decode steps of the 32K fp32 layer on the numpy oracle:
+    3 warm-up and 10 timed steps (the context grows by the decode token each
+    step), each split into L1 (decode write, page
+    statistics and scores), L2 (L1 top-k, candidates, logits, top-quota,
+    union) and attention, one task per kv head and phase, timed with
+    perf_counter around each phase; medians reported.  Runs before anything
+    touches the GPU."""
     import multiprocessing as mp
     import statistics
     _CPU.clear()
     _CPU.update(_cpu_config0(seed, warmup + steps))
     hkv = _CPU['cfg'].hkv
     cores = os.cpu_count() or 1
-    workers = max(1, cores)
-    # page ranges per kv head in the L1 phase: every CPU busy
-    nparts = max(1, min(4, cores // hkv))
+    # one worker per kv head: the phases are bound by the host's memory
+    # bandwidth (numpy gathers of the K pool), so more concurrent workers
+    # slow each other down -- on the 16-CPU GPU host, 16 workers over 2
+    # page ranges per kv head took the L1 phase from 23.7 ms to 92.5 ms
+    workers = max(1, min(hkv, cores))
+    nparts = 1
     phases = {'l1': [], 'l2': [], 'attention': []}
     with mp.get_context('fork').Pool(workers) as pool:
         for step in range(warmup + steps):
@@ -870,9 +872,9 @@ def cpu_baseline(warmup=3, steps=10, seed=20261201):
                        'avg near pools, L1 and L2 dims [48..63] + [112..127] '
                        '(tail subspace at cmp_ratio 4), 96 + 32 pages, 1024 '
                        'tokens, sink 4, window 128) on the numpy oracle in '
-                       f'{workers} worker processes (L1: {hkv} kv heads x '
-                       f'{nparts} page ranges; L2 and attention: one task per kv '
-                       'head); median per phase')
+                       f'{workers} worker processes, one per kv head (memory-'
+                       'bandwidth bound: 16 workers were 4x slower on a 16-CPU '
+                       'host); median per phase')
 
 
 def warm_events(torch, n):
