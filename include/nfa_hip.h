@@ -92,10 +92,19 @@ typedef struct NfaSelectParams {
   int32_t l2_quant;           /* --nfa_l2_quant: L2 logits over 4-bit keys
                                  (min_max_per_token_quant, tia_indexer.py:
                                  22-31) from the packed side cache; needs
-                                 l2_keys_l, 32 L2 dims and bf16 KV */
+                                 l2_keys_l, 32 or 64 L2 dims and bf16 KV */
+  int32_t kv_heads_mem;       /* kv heads of the KV arena, the statistics,
+                                 the side cache, k_new and v_new: hkv (or 0,
+                                 read as hkv), or 1
+                                 when every selection row reads one shared
+                                 arena head (an absorbed-MLA latent cache:
+                                 hkv = hq selection rows of one query head
+                                 each; only selection row 0 writes the
+                                 shared state, and v_new may then be NULL:
+                                 the values are part of the key rows) */
 
   /* cache state (device pointers) */
-  void *k_pool_l, *v_pool_l;          /* [P+1,1,hkv,page,D] of this layer */
+  void *k_pool_l, *v_pool_l;          /* [P+1,1,kv_heads_mem,page,D] of this layer */
   const int32_t *block_table_l;       /* [max_req, max_blocks] */
   const int32_t *lengths;             /* [batch] planned lengths */
   const int64_t *active_req;          /* [batch] request id or -1 */
@@ -108,11 +117,11 @@ typedef struct NfaSelectParams {
   int64_t q_stride_b, q_stride_h;     /* element strides */
 
   /* decode write fused into the selector; k_new == NULL disables it */
-  const void *k_new, *v_new;          /* [batch, hkv, 1, D] contiguous */
+  const void *k_new, *v_new;          /* [batch, kv_heads_mem, 1, D] contiguous */
   const int32_t *slots;               /* [batch] physical slot or -1 */
 
   /* persistent page statistics of this layer, KV dtype,
-     [max_req, hkv, dsub/chunk, max_blocks, chunk] with chunk = 16B/elem:
+     [max_req, kv_heads_mem, dsub/chunk, max_blocks, chunk], chunk = 16B/elem:
      per page dim the min, the max and the mean bf16(KV(sum) / bs) (the avg
      pools' key; the fp32 running sum of the newest page is page_sum_l) */
   void *stat_min_l, *stat_max_l, *stat_sum_l;
@@ -121,10 +130,10 @@ typedef struct NfaSelectParams {
      visible token in fine_dims order, [max_req, hkv, max_blocks * bs,
      fine_dsub]; valid with the statistics (written by the same rebuild and
      incremental update).  NULL: the L2 logits read the K pool.  With
-     l2_quant: 20 bytes per (request, kv head, token) slot instead -- the 16
-     bytes of 4-bit codes of all slots (dim d in nibble d % 2 of byte d / 2),
-     then the 4 bytes of (bf16 scale, bf16 zero) of all slots, slot =
-     (req * hkv + kv) * max_blocks * bs + token. */
+     l2_quant: fine_dsub / 2 + 4 bytes per (request, kv head, token) slot
+     instead -- the fine_dsub / 2 bytes of 4-bit codes of all slots (dim d in
+     nibble d % 2 of byte d / 2), then the 4 bytes of (bf16 scale, bf16
+     zero) of all slots, slot = (req * hkv + kv) * max_blocks * bs + token. */
   void *l2_keys_l;
   /* optional fp32 running sums of each request's last (partial) L1 page,
      [max_req, hkv, dsub], valid with the statistics: with them a decode step
@@ -184,6 +193,40 @@ typedef struct NfaAttnParams {
   void *workspace;
   int64_t workspace_bytes;
 } NfaAttnParams;
+
+/*
+ * Absorbed multi-head latent attention decode (DeepSeek-V2 MLA): one latent
+ * row per token, [kv_a_layernorm(c) (value_dim) | RoPE'd k_pe (latent_dim -
+ * value_dim)], shared by every head (a KV arena of one kv head); each query
+ * head attends over its own gather row (its selection, from nfa_select_layer
+ * with kv_heads_mem 1 and one selection row per head).
+ */
+typedef struct NfaMlaAttnParams {
+  int32_t abi_version;
+  int32_t struct_size;
+  int32_t total_q;            /* T query rows */
+  int32_t heads;              /* query heads = gather rows per query row */
+  int32_t latent_dim;         /* latent row width = value_dim + 64 */
+  int32_t value_dim;          /* 64, 128, 256 or 512: the row's first dims */
+  int32_t page;
+  int32_t gather_rows;        /* rows of gather / vis_lens */
+  int32_t max_vis;
+  int32_t kv_dtype;           /* NFA_DTYPE_BF16 */
+  int32_t q_dtype, out_dtype; /* NFA_DTYPE_BF16 or NFA_DTYPE_F32 */
+  int32_t pool_pages;         /* pages in the arena; slots beyond are skipped */
+  float scale;
+  const void *q;              /* [T, heads, latent_dim]: per head
+                                 [W_uk,h^T q_nope,h | q_pe,h] */
+  const void *kv_pool;        /* [P+1, 1, 1, page, latent_dim] */
+  const int32_t *gather;      /* [gather_rows, heads, max_vis] physical slots */
+  const int32_t *vis_lens;    /* [gather_rows, heads] */
+  const int32_t *query_to_req;/* [T] */
+  void *out;                  /* [T, heads, value_dim]: sum_i p_i c_i per head,
+                                 before the value up-projection */
+  void *workspace;            /* nfa_mla_attn_workspace_bytes(), zero-filled
+                                 once; counters are left at zero */
+  int64_t workspace_bytes;
+} NfaMlaAttnParams;
 
 /* Decode-step dense layers around the sparse attention (bf16 only). */
 #define NFA_EPI_PLAIN 0      /* y_s = x W_s^T for each segment s */
@@ -299,6 +342,17 @@ int32_t nfa_select_layer_noalloc(const NfaSelectParams *p, void *stream);
 /* A10: sparse gather attention, out[t,h] = softmax(scale q k^T) v. */
 int32_t nfa_sparse_attn_decode(const NfaAttnParams *p, void *stream);
 
+/* No counterpart in the reference, whose DeepSeek-V2 and GLM patches expand
+   the latent per head first (v1 tree sparse_attn/patches/
+   deepseek_v2_attn_patch.py; sparse_attn/patches/glm4_moe_lite_attn_patch.py:
+   36-59) and run sparse_paged_attention_gather on the expanded heads: the
+   absorbed form of that attention over a latent arena, per head
+   out_h = softmax(scale q_h K^T) K[:, :value_dim] over the head's gather
+   row (equal to the expanded attention up to rounding). */
+int32_t nfa_mla_attn_decode(const NfaMlaAttnParams *p, void *stream);
+int64_t nfa_mla_attn_workspace_bytes(const NfaMlaAttnParams *p);
+int32_t nfa_mla_attn_params_size(void);
+
 /* Per-split online-softmax state of one region's gather attention. */
 typedef struct NfaAttnPartial {
   int32_t abi_version;
@@ -337,7 +391,9 @@ typedef struct NfaAttnCombineParams {
 
 int32_t nfa_attn_regions_combine(const NfaAttnCombineParams *c, void *stream);
 
-/* A11: one decode token per row; slot < 0 writes nothing. */
+/* A11: one decode token per row; slot < 0 writes nothing.  head_dim_v 0
+   writes the keys only (values and v_pool may be NULL), for a latent arena
+   whose values are part of the key rows; the same holds for the prefill. */
 int32_t nfa_paged_write_decode(const void *keys, const void *values,
                                const int32_t *slots, int32_t batch,
                                int32_t hkv, int32_t head_dim,

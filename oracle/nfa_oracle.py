@@ -824,6 +824,40 @@ def sparse_attention(k_pool, v_pool, q, gather, vis_lens, query_to_req, scale,
     return out
 
 
+def mla_sparse_attention(latent_pool, q_lat, gather, vis_lens, query_to_req, scale,
+                         page, value_dim):
+    """Absorbed latent attention over per-head selections, in float64.
+
+    ``latent_pool`` [P+1, 1, 1, page, D] holds one row per token, [c
+    (value_dim) | k_pe]; ``q_lat`` [T, H, D] per head [W_uk,h^T q_nope,h |
+    q_pe,h]; ``gather`` [rows, H, W] / ``vis_lens`` [rows, H] are each head's
+    selection.  Returns [T, H, value_dim]: sum_i softmax(scale q_h . K_i)
+    K_i[:value_dim] per head, before the value up-projection (0 for padding
+    rows).  No reference counterpart: the algebraic form of
+    ``sparse_attention`` over the expanded heads K_h = [W_uk,h c | k_pe],
+    V_h = W_uv,h c, against which tests/test_oracle_pinning.py pins it."""
+    q = np.asarray(q_lat, dtype=np.float64)
+    t_total, heads, _ = q.shape
+    max_vis = gather.shape[-1]
+    out = np.zeros((t_total, heads, value_dim), dtype=np.float64)
+    for t in range(t_total):
+        req = int(query_to_req[t])
+        if req < 0:
+            continue
+        for h in range(heads):
+            n = min(int(vis_lens[req, h]), max_vis)
+            slots = np.asarray(gather[req, h, :n], dtype=np.int64)
+            slots = slots[slots >= 0]
+            if len(slots) == 0:
+                continue
+            rows = latent_pool[slots // page, 0, 0, slots % page].astype(np.float64)
+            s = rows @ q[t, h] * scale
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            out[t, h] = p @ rows[:, :value_dim]
+    return out
+
+
 def split_bounds(n, nsplit, block_tokens):
     """Token range [lo, hi) of each split of a row with ``n`` visible slots:
     split s takes blocks [s*nb//nsplit, (s+1)*nb//nsplit) of

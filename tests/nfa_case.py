@@ -45,7 +45,13 @@ def make_cache(device, *, geometry, n_layers=1, max_requests=4, max_blocks,
         dtype=dtype, device=device)
 
 
-def indexer_dims(indexer, head_dim=128):
+def indexer_dims(indexer, head_dim=128, latent_value_dim=None):
+    """(L1 dims, L2 dims) the selector reads; of a latent arena row
+    [c (latent_value_dim) | k_pe]: the k_pe dims (the expanded heads'
+    mla_rope dims)."""
+    if latent_value_dim is not None:
+        dims = np.arange(latent_value_dim, head_dim)
+        return dims, dims
     cpu = torch.device('cpu')
     full = np.arange(head_dim)
     l1 = (indexer._subspace_indices(cpu).numpy() if indexer.enable_subspace
@@ -60,11 +66,16 @@ def indexer_dims(indexer, head_dim=128):
 
 
 def cfg_from(cache, indexer, scaling):
+    """Oracle configuration of the cache's layer 0 and the indexer; a latent
+    arena is seen as its expanded heads (one selection row per query head)."""
     layer = cache.layers[0]
-    l1, fine = indexer_dims(indexer, layer.head_dim_k)
+    latent = getattr(cache, 'latent', False)
+    l1, fine = indexer_dims(indexer, layer.head_dim_k,
+                            layer.head_dim_v if latent else None)
     nb_near = max(0, int(indexer.nt_near_pages))
     return orc.NfaConfig(
-        hq=cache.num_query_heads, hkv=layer.num_kv_heads,
+        hq=cache.num_query_heads,
+        hkv=cache.selection_heads if latent else layer.num_kv_heads,
         head_dim=layer.head_dim_k, head_dim_v=layer.head_dim_v,
         bs=int(indexer.args.tia_block_size), page=cache.geometry.page,
         max_blocks=cache.max_blocks, geo_sink=cache.geometry.sink,
@@ -88,9 +99,11 @@ def snapshot(cache, layer_idx, batch, with_v=True):
     """Numpy copy of everything the selector reads for ``layer_idx`` (the V
     pool too unless ``with_v`` is False: selection never reads it)."""
     layer = cache.layers[layer_idx]
+    latent = getattr(cache, 'latent', False)
     return dict(
         k_pool=to_np(layer.kv_pool_k),
-        v_pool=to_np(layer.kv_pool_v) if with_v else None,
+        v_pool=to_np(layer.kv_pool_v) if with_v and not latent else None,
+        latent_heads=cache.selection_heads if latent else None,
         block_table=to_np(cache.block_table_buf[layer_idx]).astype(np.int64),
         lengths=to_np(cache.planned_lengths_buf[:batch]).astype(np.int64),
         req_ids=to_np(cache.valid_req_ids_buf[:batch]).astype(np.int64),
@@ -112,7 +125,14 @@ def run_oracle(cfg, snap, q, decode=None, max_vis=1024, middle_only=False,
         active = snap['active']
         slots = np.where(active, np.asarray(slots), -1)
         orc.apply_decode_write(k_pool, v_pool, np.asarray(keys, np.float32),
-                               np.asarray(values, np.float32), slots, cfg.page)
+                               None if values is None else np.asarray(values, np.float32),
+                               slots, cfg.page)
+    if snap.get('latent_heads'):
+        # a latent arena as its expanded heads: every head reads the shared
+        # rows (expand_kv copies k_pe into every head)
+        shape = list(k_pool.shape)
+        shape[2] = snap['latent_heads']
+        k_pool = np.broadcast_to(k_pool, tuple(shape))
     res = orc.select_layer(cfg, k_pool, snap['block_table'], snap['lengths'],
                            snap['req_ids'], snap['active'], snap['skip_far'],
                            snap['skip_near'], np.asarray(q, np.float32),
@@ -245,7 +265,8 @@ def run_and_compare(cache, indexer, req_ids, q, decode, *, scaling=1.0,
     torch.cuda.synchronize()
     dec_np = None
     if decode is not None:
-        dec_np = tuple(t.float().cpu().numpy() if t.is_floating_point()
+        dec_np = tuple(None if t is None else
+                       t.float().cpu().numpy() if t.is_floating_point()
                        else t.cpu().numpy() for t in decode)
     res, k_pool, v_pool = run_oracle(cfg, snap, q.float().cpu().numpy(), dec_np,
                                      max_vis=max_vis, middle_only=middle_only,
@@ -302,9 +323,10 @@ def run_and_compare(cache, indexer, req_ids, q, decode, *, scaling=1.0,
             if slots[row_b] < 0:
                 continue
             phys, off = divmod(int(slots[row_b]), cfg.page)
+            arena = layer.num_kv_heads
             np.testing.assert_array_equal(
                 layer.kv_pool_k[phys, 0, :, off].float().cpu().numpy(),
-                k_pool[phys, 0, :, off])
+                k_pool[phys, 0, :arena, off])
             if v_pool is not None:
                 np.testing.assert_array_equal(
                     layer.kv_pool_v[phys, 0, :, off].float().cpu().numpy(),

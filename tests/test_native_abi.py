@@ -102,7 +102,12 @@ def test_partial_combine_and_quant_checks_reject_before_launch(lib):
     assert b'shape or dtype' in lib.nfa_last_error()
     p = _native.NfaSelectParams()
     p.abi_version, p.struct_size = _native.ABI_VERSION, ctypes.sizeof(p)
-    p.batch, p.hq, p.hkv, p.head_dim, p.dsub, p.fine_dsub = 1, 32, 8, 128, 32, 64
+    p.batch, p.hq, p.hkv, p.head_dim, p.dsub, p.fine_dsub = 1, 32, 8, 128, 32, 48
     p.l2_quant = 1
     assert lib.nfa_select_layer(ctypes.byref(p), None) == -1
     assert b'4-bit L2 keys' in lib.nfa_last_error()
+    assert b'32 or 64' in lib.nfa_last_error()
+    # arena heads shared by the selection rows: hkv, 0 (= hkv) or 1 only
+    p.l2_quant, p.fine_dsub, p.kv_heads_mem = 0, 32, 4
+    assert lib.nfa_select_layer(ctypes.byref(p), None) == -1
+    assert b'kv_heads_mem' in lib.nfa_last_error()

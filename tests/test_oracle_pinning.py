@@ -384,6 +384,37 @@ def test_sparse_attention_matches_torch_softmax():
             np.testing.assert_allclose(out[t, h], (w @ vv).numpy(), rtol=1e-9, atol=1e-12)
 
 
+def test_mla_attention_equals_expanded_attention():
+    """The absorbed latent attention against the torch-pinned attention
+    over expanded heads (DeepseekV2Attention.expand_kv): K_h = [W_uk,h c |
+    k_pe], V_h = W_uv,h c, q_h = [q_nope,h | q_pe,h]; the latent form takes
+    q_lat,h = [W_uk,h^T q_nope,h | q_pe,h] and out_h = W_uv,h o_lat,h.  Equal
+    in float64 up to rounding; a transposed projection, a wrong value slice
+    or a dropped RoPE term fails it."""
+    rng = np.random.default_rng(31)
+    heads, rank, rope, nope, dv, page = 4, 16, 8, 12, 10, 4
+    latent = rng.standard_normal((9, 1, 1, page, rank + rope))
+    w_uk = rng.standard_normal((heads, nope, rank))
+    w_uv = rng.standard_normal((heads, dv, rank))
+    q_nope = rng.standard_normal((2, heads, nope))
+    q_pe = rng.standard_normal((2, heads, rope))
+    gather = rng.integers(0, 36, (3, heads, 10)).astype(np.int64)
+    vis = rng.integers(0, 11, (3, heads))
+    q2r = np.array([2, -1])
+    c, k_pe = latent[..., :rank], latent[..., rank:]
+    k_exp = np.concatenate([np.einsum('pabtr,hnr->pahtn', c, w_uk),
+                            np.broadcast_to(k_pe, c.shape[:2] + (heads, page, rope))],
+                           axis=-1)
+    v_exp = np.einsum('pabtr,hvr->pahtv', c, w_uv)
+    q_exp = np.concatenate([q_nope, q_pe], axis=-1)
+    want = orc.sparse_attention(k_exp, v_exp, q_exp, gather, vis, q2r, 0.3, page)
+    q_lat = np.concatenate([np.einsum('thn,hnr->thr', q_nope, w_uk), q_pe], axis=-1)
+    o_lat = orc.mla_sparse_attention(latent, q_lat, gather, vis, q2r, 0.3, page, rank)
+    got = np.einsum('thr,hvr->thv', o_lat, w_uv)
+    np.testing.assert_allclose(got, want, rtol=1e-9, atol=1e-12)
+    assert (got[1] == 0).all()  # the padding row
+
+
 # --- 4-bit L2 keys ------------------------------------------------------------
 
 def _torch_min_max_quant(x):

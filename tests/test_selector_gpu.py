@@ -123,13 +123,15 @@ def test_incremental_side_rows_become_candidates():
         cache.commit_step()
 
 
-@pytest.mark.parametrize('lengths', [[20000], [5000, 700, 12345]])
-def test_l2_quant_4bit_keys_bit_exact(lengths):
+@pytest.mark.parametrize('lengths,subspace', [([20000], 'tail'), ([5000, 700, 12345], 'tail'),
+                                              ([20000], 'rope'), ([5000, 700, 12345], 'rope')])
+def test_l2_quant_4bit_keys_bit_exact(lengths, subspace):
     """--nfa_l2_quant: L2 logits over the packed 4-bit side cache (written by
     the statistics rebuild) against the oracle's min_max_per_token_quant
-    semantics: every candidate's logit bits, the middle and the gather."""
+    semantics: every candidate's logit bits, the middle and the gather; 32
+    L2 dims (tail subspace) and 64 (rope subspace)."""
     cache, gen, req_ids = _prod_cache(lengths)
-    indexer = make_indexer(l2_quant=True)
+    indexer = make_indexer(l2_quant=True, subspace=subspace)
     b = len(req_ids)
     cache.new_step(req_ids)
     cache.plan_common(req_ids)
@@ -138,16 +140,17 @@ def test_l2_quant_4bit_keys_bit_exact(lengths):
     run_and_compare(cache, indexer, req_ids, q, decode, scaling=0.08838834764831845)
 
 
-def test_l2_quant_incremental_rows_and_raw_differ():
-    """4-bit rows written by decode steps become candidates and score as the
-    oracle's quantised keys; the 4-bit and raw modes pick different tokens
-    (so the flag is live)."""
+@pytest.mark.parametrize('subspace', ['tail', 'rope'])
+def test_l2_quant_incremental_rows_and_raw_differ(subspace):
+    """4-bit rows written by decode steps (32 or 64 lanes quantising the new
+    token) become candidates and score as the oracle's quantised keys; the
+    4-bit and raw modes pick different tokens (so the flag is live)."""
     geo = RegionGeometry(sink=4, near=4096, window=128, page=16,
                          max_new_tokens=256)
     # long enough that the L2 quota (892) is below the candidate count, so
     # the logits decide
     cache, gen, req_ids = _prod_cache([12000], geometry=geo)
-    indexer = make_indexer(l2_quant=True)
+    indexer = make_indexer(l2_quant=True, subspace=subspace)
     for step in range(150):
         cache.new_step(req_ids)
         cache.plan_common(req_ids)
@@ -160,7 +163,8 @@ def test_l2_quant_incremental_rows_and_raw_differ():
             cache.commit_step()
         else:
             res = run_and_compare(cache, indexer, req_ids, q, decode)
-    raw, _, _ = run_oracle(cfg_from(cache, make_indexer(), 1.0), snapshot(cache, 0, 1),
+    raw, _, _ = run_oracle(cfg_from(cache, make_indexer(subspace=subspace), 1.0),
+                           snapshot(cache, 0, 1),
                            q.float().cpu().numpy(), None, max_vis=1024)
     assert any(not np.array_equal(res[0][kv].middle, raw[0][kv].middle)
                for kv in range(cache.num_kv_heads))
@@ -171,7 +175,7 @@ def test_l2_quant_rejects_unsupported_geometry():
     cache.new_step(req_ids)
     cache.plan_common(req_ids)
     q = bf16_randn((1, cache.num_query_heads, 128), gen, DEV)
-    wide = make_indexer(l2_quant=True, subspace='rope')  # 64 L2 dims
+    wide = make_indexer(l2_quant=True, l2_subspace='full')  # 128 L2 dims
     with pytest.raises(ValueError, match='l2_quant'):
         select_topk_for_layer_batched(cache, 0, req_ids, q,
                                       attention=attention_ns(wide, 1.0))

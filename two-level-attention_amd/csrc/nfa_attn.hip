@@ -78,47 +78,6 @@ __host__ __device__ inline int part_span(const NfaAttnParams &p, const NfaAttnPa
   return span < p.max_vis ? (int)span : p.max_vis;
 }
 
-// DPP lane moves (VALU, no LDS round trip).
-template <int CTRL>
-__device__ __forceinline__ float dppf(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over each group of 8 consecutive lanes, in every lane of the group:
-// quad_perm xor 1, quad_perm xor 2, then row_half_mirror (lane i <-> 7 - i).
-__device__ __forceinline__ float sum8(float x) {
-  x += dppf<0xB1>(x);
-  x += dppf<0x4E>(x);
-  x += dppf<0x141>(x);
-  return x;
-}
-
-// Wave-wide maximum / sum: the three 8-lane steps and row_mirror (lane
-// i <-> 15 - i) give every lane its row's result; the four rows combine in
-// scalar registers.
-__device__ __forceinline__ float wave_max(float x) {
-  x = fmaxf(x, dppf<0xB1>(x));
-  x = fmaxf(x, dppf<0x4E>(x));
-  x = fmaxf(x, dppf<0x141>(x));
-  x = fmaxf(x, dppf<0x140>(x));
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
-  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-__device__ __forceinline__ float wave_sum(float x) {
-  x += dppf<0xB1>(x);
-  x += dppf<0x4E>(x);
-  x += dppf<0x141>(x);
-  x += dppf<0x140>(x);
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
-  return (r0 + r1) + (r2 + r3);
-}
-
 // Two adjacent KV elements of an LDS row as floats.
 __device__ __forceinline__ void lds_pair(const uint16_t *v, int d, float *a,
                                          float *b) {
@@ -319,12 +278,12 @@ __global__ void __launch_bounds__(NFA_BLOCK)
     for (int g = w; g < G; g += NFA_WAVES) {
       // one score per lane (a chunk holds at most 64 = kSplitMax slots)
       const float sl = lane < cn ? s_p[g * kSplitMax + lane] : kNegInf;
-      const float m = wave_max(sl);
+      const float m = wave_max_dpp(sl);
       const float m_old = s_m[g];
       const float m_new = fmaxf(m_old, m);
       const float e = (m_new == kNegInf || lane >= cn) ? 0.0f : __expf(sl - m_new);
       if (lane < cn) s_p[g * kSplitMax + lane] = e;
-      const float z = wave_sum(e);
+      const float z = wave_sum_dpp(e);
       if (lane == 0) {
         const float f = m_old == kNegInf ? 0.0f : __expf(m_old - m_new);
         s_f[g] = f;

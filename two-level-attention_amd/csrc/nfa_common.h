@@ -289,6 +289,51 @@ __device__ __forceinline__ bool arrive_last(unsigned int *counter,
 }
 
 // ---------------------------------------------------------------------------
+// DPP reductions of the attention kernels
+// ---------------------------------------------------------------------------
+
+// DPP lane moves (VALU, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dppf(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each group of 8 consecutive lanes, in every lane of the group:
+// quad_perm xor 1, quad_perm xor 2, then row_half_mirror (lane i <-> 7 - i).
+__device__ __forceinline__ float sum8(float x) {
+  x += dppf<0xB1>(x);
+  x += dppf<0x4E>(x);
+  x += dppf<0x141>(x);
+  return x;
+}
+
+// Wave-wide maximum / sum: the three 8-lane steps and row_mirror (lane
+// i <-> 15 - i) give every lane its row's result; the four rows combine in
+// scalar registers.
+__device__ __forceinline__ float wave_max_dpp(float x) {
+  x = fmaxf(x, dppf<0xB1>(x));
+  x = fmaxf(x, dppf<0x4E>(x));
+  x = fmaxf(x, dppf<0x141>(x));
+  x = fmaxf(x, dppf<0x140>(x));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ float wave_sum_dpp(float x) {
+  x += dppf<0xB1>(x);
+  x += dppf<0x4E>(x);
+  x += dppf<0x141>(x);
+  x += dppf<0x140>(x);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// ---------------------------------------------------------------------------
 // block-level (256 threads) scans and reductions
 // ---------------------------------------------------------------------------
 

@@ -389,7 +389,7 @@ __device__ __forceinline__ int64_t stat_index(const NfaSelectParams &p,
                                               int64_t req, int kv, int d,
                                               int page_t, int dsub) {
   constexpr int CH = Elem<KV>::kChunk;
-  return ((((req * p.hkv + kv) * (dsub / CH) + d / CH) * (int64_t)p.max_blocks +
+  return ((((req * p.kv_heads_mem + kv) * (dsub / CH) + d / CH) * (int64_t)p.max_blocks +
            page_t) *
           CH) +
          (d % CH);
@@ -402,7 +402,7 @@ __device__ __forceinline__ int safe_page(const NfaSelectParams &p, int phys) {
 
 __device__ __forceinline__ int64_t kv_offset(const NfaSelectParams &p,
                                              int phys, int kv, int off) {
-  return (((int64_t)phys * p.hkv + kv) * p.page + off) * p.head_dim;
+  return (((int64_t)phys * p.kv_heads_mem + kv) * p.page + off) * p.head_dim;
 }
 
 // L2 side copy of one (request, kv head): per L1 page of bs tokens, when the
@@ -414,7 +414,7 @@ __device__ __forceinline__ int64_t l2_side_index(const NfaSelectParams &p,
                                                  int64_t req, int kv, int tok,
                                                  int d) {
   constexpr int CH = Elem<KV>::kChunk;
-  const int64_t page = (req * p.hkv + kv) * (int64_t)p.max_blocks + tok / p.bs;
+  const int64_t page = (req * p.kv_heads_mem + kv) * (int64_t)p.max_blocks + tok / p.bs;
   const int r = tok % p.bs;
   const int64_t base = page * p.bs * p.fine_dsub;
   return p.fine_dsub % CH == 0
@@ -422,17 +422,20 @@ __device__ __forceinline__ int64_t l2_side_index(const NfaSelectParams &p,
              : base + (int64_t)r * p.fine_dsub + d;
 }
 
-// 4-bit L2 side cache (--nfa_l2_quant, 32 L2 dims): per (request, kv head,
-// token) 16 bytes of codes -- dim d in nibble d % 2 of byte d / 2 -- at
-// slot * 16, and the token's bf16 scale and zero (scale in the low half) at
-// 16 * slots + 4 * slot, slot = (req * hkv + kv) * max_blocks * bs + tok.
-constexpr int kQ4Dims = 32;
+// 4-bit L2 side cache (--nfa_l2_quant, 32 or 64 L2 dims): per (request, kv
+// head, token) fine_dsub / 2 bytes of codes -- dim d in nibble d % 2 of
+// byte d / 2 -- at slot * fine_dsub / 2, and the token's bf16 scale and zero
+// (scale in the low half) after every slot's codes, at slots * fine_dsub / 2
+// + 4 * slot; slot = (req * hkv + kv) * max_blocks * bs + tok.
+__host__ __device__ __forceinline__ bool q4_dims_ok(int fine_dsub) {
+  return fine_dsub == 32 || fine_dsub == 64;
+}
 __device__ __forceinline__ int64_t q4_slot(const NfaSelectParams &p, int64_t req,
                                            int kv, int tok) {
-  return (req * p.hkv + kv) * (int64_t)p.max_blocks * p.bs + tok;
+  return (req * p.kv_heads_mem + kv) * (int64_t)p.max_blocks * p.bs + tok;
 }
 __device__ __forceinline__ int64_t q4_slots(const NfaSelectParams &p) {
-  return (int64_t)p.max_req * p.hkv * p.max_blocks * p.bs;
+  return (int64_t)p.max_req * p.kv_heads_mem * p.max_blocks * p.bs;
 }
 
 // min_max_per_token_quant (tia_indexer.py:22-31) with torch's bf16 rounding
@@ -445,10 +448,12 @@ template <typename KV>
 __device__ __forceinline__ void q4_store(const NfaSelectParams &p, int64_t req, int kv,
                                          int tok, const KV *row, const int *fdims) {
   // eight dims per step: few registers live where the rebuild runs
+  const int nd = p.fine_dsub;
+  const int cb = nd / 2;  // code bytes per slot
   float mx = Elem<KV>::load(row + fdims[0]);
   float mn = mx;
 #pragma unroll 1
-  for (int d0 = 0; d0 < kQ4Dims; d0 += 8) {
+  for (int d0 = 0; d0 < nd; d0 += 8) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float x = Elem<KV>::load(row + fdims[d0 + e]);
@@ -463,7 +468,7 @@ __device__ __forceinline__ void q4_store(const NfaSelectParams &p, int64_t req, 
   const int64_t slot = q4_slot(p, req, kv, tok);
   unsigned char *base = (unsigned char *)p.l2_keys_l;
 #pragma unroll 1
-  for (int d0 = 0; d0 < kQ4Dims; d0 += 8) {
+  for (int d0 = 0; d0 < nd; d0 += 8) {
     uint32_t w = 0u;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -472,22 +477,25 @@ __device__ __forceinline__ void q4_store(const NfaSelectParams &p, int64_t req, 
       const float c = fminf(fmaxf(rintf(t), 0.0f), 15.0f);
       w |= (uint32_t)c << (4 * e);
     }
-    *reinterpret_cast<uint32_t *>(base + slot * 16 + d0 / 2) = w;
+    *reinterpret_cast<uint32_t *>(base + slot * cb + d0 / 2) = w;
   }
-  *reinterpret_cast<uint32_t *>(base + q4_slots(p) * 16 + slot * 4) =
+  *reinterpret_cast<uint32_t *>(base + q4_slots(p) * cb + slot * 4) =
       (uint32_t)bf16_bits(scale) | ((uint32_t)bf16_bits(zero) << 16);
 }
 
-// q4_store by lanes 0-31 of one wave, lane d holding L2 dim d of the token:
-// the range by a shuffle tree, one code per lane, the eight nibbles of a
-// word OR-ed together across lanes.
+// q4_store by lanes 0 .. fine_dsub - 1 of one wave, lane d holding L2 dim d
+// of the token: the range by a shuffle tree over those lanes, one code per
+// lane, the eight nibbles of a word OR-ed together across lanes.
 __device__ __forceinline__ void q4_store_lanes(const NfaSelectParams &p, int64_t req,
                                                int kv, int tok, float x, int d) {
+  const int nd = p.fine_dsub;  // 32 or 64 lanes
   float mx = x, mn = x;
 #pragma unroll
-  for (int off = 16; off > 0; off >>= 1) {
-    mx = fmaxf(mx, __shfl_xor(mx, off, 32));
-    mn = fminf(mn, __shfl_xor(mn, off, 32));
+  for (int off = 32; off > 0; off >>= 1) {
+    if (off < nd) {
+      mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      mn = fminf(mn, __shfl_xor(mn, off, 64));
+    }
   }
   float rng = bf16r(mx - mn);
   if (rng < 1e-9f) rng = bf16r(1e-9f);
@@ -496,12 +504,13 @@ __device__ __forceinline__ void q4_store_lanes(const NfaSelectParams &p, int64_t
   const float t = bf16r(bf16r(x + zero) / scale);
   unsigned w = (unsigned)fminf(fmaxf(rintf(t), 0.0f), 15.0f) << (4 * (d % 8));
 #pragma unroll
-  for (int off = 1; off < 8; off <<= 1) w |= __shfl_xor(w, off, 32);
+  for (int off = 1; off < 8; off <<= 1) w |= __shfl_xor(w, off, 64);
   const int64_t slot = q4_slot(p, req, kv, tok);
+  const int cb = nd / 2;
   unsigned char *base = (unsigned char *)p.l2_keys_l;
-  if (d % 8 == 0) store_coherent(reinterpret_cast<uint32_t *>(base + slot * 16 + d / 2), w);
+  if (d % 8 == 0) store_coherent(reinterpret_cast<uint32_t *>(base + slot * cb + d / 2), w);
   if (d == 0)
-    store_coherent(reinterpret_cast<uint32_t *>(base + q4_slots(p) * 16 + slot * 4),
+    store_coherent(reinterpret_cast<uint32_t *>(base + q4_slots(p) * cb + slot * 4),
                    (uint32_t)bf16_bits(scale) | ((uint32_t)bf16_bits(zero) << 16));
 }
 
@@ -1071,6 +1080,8 @@ __device__ __forceinline__ void protected_intervals(const NfaSelectParams &p,
   }
 }
 
+// (kv: the arena's kv head; no V rows when v_new is NULL, a shared latent
+// arena whose values are part of the key rows)
 template <typename KV>
 __device__ __forceinline__ void decode_write(const NfaSelectParams &p, int b,
                                              int kv) {
@@ -1082,12 +1093,14 @@ __device__ __forceinline__ void decode_write(const NfaSelectParams &p, int b,
   KV *vp = (KV *)p.v_pool_l;
   const KV *kn = (const KV *)p.k_new;
   const KV *vn = (const KV *)p.v_new;
+  const int hm = p.kv_heads_mem;
   for (int d = threadIdx.x; d < p.head_dim; d += SB)
     kp[kv_offset(p, phys, kv, off) + d] =
-        kn[((int64_t)b * p.hkv + kv) * p.head_dim + d];
+        kn[((int64_t)b * hm + kv) * p.head_dim + d];
+  if (vn == nullptr) return;
   for (int d = threadIdx.x; d < p.head_dim_v; d += SB)
-    vp[(((int64_t)phys * p.hkv + kv) * p.page + off) * p.head_dim_v + d] =
-        vn[((int64_t)b * p.hkv + kv) * p.head_dim_v + d];
+    vp[(((int64_t)phys * hm + kv) * p.page + off) * p.head_dim_v + d] =
+        vn[((int64_t)b * hm + kv) * p.head_dim_v + d];
 }
 
 // Both regions skipped (region mode 3 / disjoint protected gather): decode
@@ -1097,11 +1110,13 @@ __global__ void __launch_bounds__(SB)
     nfa_protected_kernel(const NfaSelectParams p) {
   const int row = blockIdx.x;
   const int b = row / p.hkv;
-  const int kv = row % p.hkv;
+  const int kv = row % p.hkv;  // selection row of the batch row
   const int L = p.lengths[b];
   const bool active = p.active_req[b] >= 0;
   const int64_t req = p.valid_req[b];
-  if (p.k_new != nullptr && active) decode_write<KV>(p, b, kv);
+  // a shared arena (kv_heads_mem 1) is written by selection row 0 only
+  if (p.k_new != nullptr && active && kv < p.kv_heads_mem)
+    decode_write<KV>(p, b, p.kv_heads_mem > 1 ? kv : 0);
   if (p.middle_only) {
     if (threadIdx.x == 0) p.vis_lens[b * p.hkv + kv] = 0;
     return;
@@ -1383,10 +1398,15 @@ __global__ void __launch_bounds__(SB)
   // number row + rows * tile (row = b * hkv + kv), so the first dispatch
   // round holds the low tiles of every row and a row's tiles share an XCD
   // (workgroups go round-robin over the XCDs)
-  const int kv = blockIdx.x;
+  // kvq: the selection row's kv head (its query rows, gather row and
+  // workspace row); kv: the arena's kv head it reads and writes, 0 for
+  // every row when the rows share one arena head (kv_heads_mem 1: the
+  // latent rows of an absorbed-MLA cache, one selection row per query head)
+  const int kvq = blockIdx.x;
+  const int kv = p.kv_heads_mem > 1 ? kvq : 0;
   const int b = blockIdx.y;
   const int tile = blockIdx.z;
-  const int row = b * p.hkv + kv;
+  const int row = b * p.hkv + kvq;
   const int G = sd.group;
   const int bs = p.bs;
   const int mb = p.max_blocks;
@@ -1415,7 +1435,7 @@ __global__ void __launch_bounds__(SB)
   const int hd = p.head_dim;
   const int nq = G * hd;
   const int qsh = p.q_dtype == NFA_DTYPE_BF16 ? 1 : 2;  // log2 element bytes
-  const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kv * G * p.q_stride_h;
+  const int64_t qrow = (int64_t)b * p.q_stride_b + (int64_t)kvq * G * p.q_stride_h;
   uint32_t qbits[kQRawPerThread];
   int qodd[kQRawPerThread];
 #pragma unroll
@@ -1565,7 +1585,7 @@ __global__ void __launch_bounds__(SB)
   if (owns_last && active && p.k_new != nullptr) {
     if (slot_b >= 0 && slot_b / p.page < p.pool_pages &&
         slot_b == ph_last * p.page + (L - 1) % p.page)
-      new_row = (const KV *)p.k_new + ((int64_t)b * p.hkv + kv) * p.head_dim;
+      new_row = (const KV *)p.k_new + ((int64_t)b * p.kv_heads_mem + kv) * p.head_dim;
   }
 
   // ---- page statistics: latest page, or the whole tile on a rebuild -----
@@ -1578,8 +1598,12 @@ __global__ void __launch_bounds__(SB)
   // L2 side row and the decode K/V write complete after the scores, their
   // loads in flight meanwhile; only the recompute path without the fp32
   // running sums stays in front.
-  const bool owner_late = do_stats && incremental && owns_last && p.page_sum_l != nullptr;
-  if (do_stats && incremental && owns_last && NFA_COLD(p.page_sum_l == nullptr)) {
+  // (rows sharing one arena head leave its writes to selection row 0: the
+  // running sums must be continued once, and the rest are the same values)
+  const bool writer = kvq < p.kv_heads_mem;
+  const bool owner_late =
+      do_stats && incremental && owns_last && writer && p.page_sum_l != nullptr;
+  if (do_stats && incremental && owns_last && writer && NFA_COLD(p.page_sum_l == nullptr)) {
     __syncthreads();  // the query preparation has read the raw rows in s_stage
     stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims, s_stage,
                                 new_row, s_last);
@@ -1591,9 +1615,10 @@ __global__ void __launch_bounds__(SB)
   // past the pages the tiles split: a block-table row of max_blocks pages
   // of `page` tokens can hold more than max_blocks blocks of bs < page
   // tokens, and those have no statistics to append to)
-  const bool dw = p.k_new != nullptr && active && last_blk >= t0 &&
+  const bool dw = p.k_new != nullptr && active && writer && last_blk >= t0 &&
                   (last_blk < t1 || t1 >= kt_tiles);
-  const bool side_late = do_stats && incremental && owns_last && p.l2_keys_l != nullptr;
+  const bool side_late =
+      do_stats && incremental && owns_last && writer && p.l2_keys_l != nullptr;
   // (only the waves holding a written element take part: the index
   // arithmetic is uniform, and run by every wave it would cost each SIMD
   // four times its scalar issue slots)
@@ -1610,9 +1635,9 @@ __global__ void __launch_bounds__(SB)
       const int phys = slot_b / p.page;
       const int off = slot_b % p.page;
       if (tid < p.head_dim) store_coherent(&((KV *)p.k_pool_l)[kv_offset(p, phys, kv, off) + tid], dw_k);
-      if (tid < p.head_dim_v)
-        ((KV *)p.v_pool_l)[(((int64_t)phys * p.hkv + kv) * p.page + off) * p.head_dim_v +
-                           tid] = dw_v;
+      if (tid < p.head_dim_v && p.v_new != nullptr)
+        ((KV *)p.v_pool_l)[(((int64_t)phys * p.kv_heads_mem + kv) * p.page + off) *
+                               p.head_dim_v + tid] = dw_v;
     }
     if (owner_late && tid < DSUB) {
       // the token's dims continue the page's min / max exactly and the fp32
@@ -1625,7 +1650,7 @@ __global__ void __launch_bounds__(SB)
       ((KV *)p.stat_min_l)[si] = (KV)Elem<KV>::from_f32(mn);
       ((KV *)p.stat_max_l)[si] = (KV)Elem<KV>::from_f32(mx);
       ((KV *)p.stat_sum_l)[si] = page_mean<KV>(sm, p.bs);
-      p.page_sum_l[(req * p.hkv + kv) * DSUB + tid] = sm;
+      p.page_sum_l[(req * p.kv_heads_mem + kv) * DSUB + tid] = sm;
     }
     if (side_late && tid < p.fine_dsub) {
       // the new token's L2 side row (its 4-bit codes: lanes 0-31 of wave 0)
@@ -1638,9 +1663,10 @@ __global__ void __launch_bounds__(SB)
   };
   auto owner_prefetch = [&]() {
     if (dw) {
-      const int64_t nb = (int64_t)b * p.hkv + kv;
+      const int64_t nb = (int64_t)b * p.kv_heads_mem + kv;
       if (tid < p.head_dim) dw_k = ((const KV *)p.k_new)[nb * p.head_dim + tid];
-      if (tid < p.head_dim_v) dw_v = ((const KV *)p.v_new)[nb * p.head_dim_v + tid];
+      if (tid < p.head_dim_v && p.v_new != nullptr)
+        dw_v = ((const KV *)p.v_new)[nb * p.head_dim_v + tid];
     }
     const KV *trow = new_row != nullptr
                          ? new_row
@@ -1650,7 +1676,7 @@ __global__ void __launch_bounds__(SB)
         const int64_t si = stat_index<KV>(p, req, kv, tid, last_blk, DSUB);
         ap_mn = Elem<KV>::load((const KV *)p.stat_min_l + si);
         ap_mx = Elem<KV>::load((const KV *)p.stat_max_l + si);
-        ap_sm = p.page_sum_l[(req * p.hkv + kv) * DSUB + tid];
+        ap_sm = p.page_sum_l[(req * p.kv_heads_mem + kv) * DSUB + tid];
       }
       ap_x = Elem<KV>::load(trow + s_dims[tid]);
     }
@@ -1676,7 +1702,7 @@ __global__ void __launch_bounds__(SB)
     if (NFA_COLD(do_stats && !incremental)) {
       __syncthreads();  // the query preparation has read the raw rows in s_stage
       float *psum_row = p.page_sum_l != nullptr
-                            ? p.page_sum_l + (req * p.hkv + kv) * DSUB
+                            ? p.page_sum_l + (req * p.kv_heads_mem + kv) * DSUB
                             : nullptr;
       int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
       if (tid == 0) {
@@ -1953,9 +1979,10 @@ __global__ void __launch_bounds__(SB)
   const NfaSelectParams &p = *(const NfaSelectParams *)pk;
   const SelDims &sd = *(const SelDims *)dk;
   const int tid = threadIdx.x;
-  const int kv = blockIdx.x;
+  const int kvq = blockIdx.x;  // selection row, as in the tile stage
+  const int kv = p.kv_heads_mem > 1 ? kvq : 0;  // the arena's kv head
   const int b = blockIdx.y;
-  const int row = b * p.hkv + kv;
+  const int row = b * p.hkv + kvq;
   const int bs = p.bs;
   const int mb = p.max_blocks;
   const int *s_ctx = (const int *)(smem + sd.a_ctx);
@@ -2006,7 +2033,7 @@ __global__ void __launch_bounds__(SB)
   NFA_MARK(32, 0);
 
   const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
-  if (NFA_COLD(p.dbg_bounds != nullptr) && kv == 0 && tid == 0) {
+  if (NFA_COLD(p.dbg_bounds != nullptr) && kvq == 0 && tid == 0) {
     p.dbg_bounds[b * 3 + 0] = lb.lower;
     p.dbg_bounds[b * 3 + 1] = lb.upper;
     p.dbg_bounds[b * 3 + 2] = lb.quota;
@@ -2431,9 +2458,10 @@ __global__ void __launch_bounds__(SB)
                      ? *reinterpret_cast<const uint4 *>(kr_pre + c * bs * CH)
                      : make_uint4(0u, 0u, 0u, 0u);
   }
-  // the same for the 4-bit side cache: the first slot's codes and (scale, zero)
+  // the same for the 4-bit side cache: the first slot's codes (one or two
+  // 16-byte runs for 32 or 64 L2 dims) and (scale, zero)
   int64_t sl_pre = -1;
-  uint4 cw_pre = make_uint4(0u, 0u, 0u, 0u);
+  uint4 cw_pre = make_uint4(0u, 0u, 0u, 0u), cw2_pre = make_uint4(0u, 0u, 0u, 0u);
   uint32_t pw_pre = 0u;
   if (p.l2_quant) {
     if (tid < np_u * bs) {
@@ -2446,8 +2474,10 @@ __global__ void __launch_bounds__(SB)
     }
     if (sl_pre >= 0) {
       const unsigned char *qb = (const unsigned char *)p.l2_keys_l;
-      cw_pre = *reinterpret_cast<const uint4 *>(qb + sl_pre * 16);
-      pw_pre = *reinterpret_cast<const uint32_t *>(qb + q4_slots(p) * 16 + sl_pre * 4);
+      const int cb = p.fine_dsub / 2;
+      cw_pre = *reinterpret_cast<const uint4 *>(qb + sl_pre * cb);
+      if (cb > 16) cw2_pre = *reinterpret_cast<const uint4 *>(qb + sl_pre * cb + 16);
+      pw_pre = *reinterpret_cast<const uint32_t *>(qb + q4_slots(p) * cb + sl_pre * 4);
     }
   }
   // one unmasked L2 region: its high-byte key histogram accumulates while
@@ -2507,46 +2537,57 @@ __global__ void __launch_bounds__(SB)
       // 4-bit side cache: 16 bytes of codes and 4 of (scale, zero) per
       // slot, dequantised in registers as bf16(bf16(code * scale) - zero)
       const unsigned char *qb = (const unsigned char *)p.l2_keys_l;
-      const int64_t poff = q4_slots(p) * 16;
+      const int cb = p.fine_dsub / 2;  // 16 or 32 code bytes per slot
+      const bool two = cb > 16;
+      const int64_t poff = q4_slots(p) * cb;
       auto q4_of = [&](int i, int &tk) -> int64_t {
         const int pi = udiv_p2(i, bs, sd.bs_sh);
         tk = s_pages[pi] * bs + (i - pi * bs);
         if (tk < tok_lo || tk >= tok_hi) return -1;
         return q4_slot(p, req, kv, tk);
       };
+      // 32 dims of dequantised keys from one 16-byte run of codes, dotted
+      // with the grouped query from dim d0 on, in dim order
+      auto dot32 = [&](const uint4 &cw, float sc, float zr, int d0, float acc) {
+        const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+        for (int d = 0; d < 32; ++d) {
+          const float c = (float)((w4[d / 8] >> (4 * (d % 8))) & 15u);
+          // a NaN here (non-finite keys) still ends as a NaN logit
+          const float dq = bf16r_hw(bf16r_hw(c * sc) - zr);
+          const float prod = dq * s_qg[d0 + d];
+          acc = acc + prod;
+        }
+        return acc;
+      };
       // the first slot's loads were issued before the L1 LDS was released
       int tk = tk_pre;
       int64_t sl = sl_pre;
-      uint4 cw = cw_pre;
+      uint4 cw = cw_pre, cw2 = cw2_pre;
       uint32_t pw = pw_pre;
 #pragma unroll 1
       for (int i = tid; i < n_dense; i += SB) {
         int tkn = -1;
         const int64_t sln = i + SB < n_dense ? q4_of(i + SB, tkn) : -1;
-        uint4 cwn = make_uint4(0u, 0u, 0u, 0u);
+        uint4 cwn = make_uint4(0u, 0u, 0u, 0u), cwn2 = make_uint4(0u, 0u, 0u, 0u);
         uint32_t pwn = 0u;
         if (sln >= 0) {
-          cwn = *reinterpret_cast<const uint4 *>(qb + sln * 16);
+          cwn = *reinterpret_cast<const uint4 *>(qb + sln * cb);
+          if (two) cwn2 = *reinterpret_cast<const uint4 *>(qb + sln * cb + 16);
           pwn = *reinterpret_cast<const uint32_t *>(qb + poff + sln * 4);
         }
         float acc = 0.0f;
         if (sl >= 0) {
           const float sc = bf16_val((uint16_t)(pw & 0xFFFFu));
           const float zr = bf16_val((uint16_t)(pw >> 16));
-          const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
-#pragma unroll
-          for (int d = 0; d < kQ4Dims; ++d) {
-            const float c = (float)((w4[d / 8] >> (4 * (d % 8))) & 15u);
-            // a NaN here (non-finite keys) still ends as a NaN logit
-            const float dq = bf16r_hw(bf16r_hw(c * sc) - zr);
-            const float prod = dq * s_qg[d];
-            acc = acc + prod;
-          }
+          acc = dot32(cw, sc, zr, 0, acc);
+          if (two) acc = dot32(cw2, sc, zr, 32, acc);
         }
         emit(i, tk, sl >= 0, acc);
         tk = tkn;
         sl = sln;
         cw = cwn;
+        cw2 = cwn2;
         pw = pwn;
       }
     } else {
@@ -2679,11 +2720,11 @@ __global__ void __launch_bounds__(SB)
   }
 
   // ---- final union with the protected sink/SWA ids (selector:1337-1437) --
-  int32_t *grow = p.gather + ((int64_t)b * p.hkv + kv) * p.max_vis;
+  int32_t *grow = p.gather + (int64_t)row * p.max_vis;
   if (NFA_COLD(p.middle_only)) {
     const int n = imin(mcount, p.max_vis);
     for (int k = tid; k < n; k += SB) grow[k] = s_mslot[k];
-    if (tid == 0) p.vis_lens[b * p.hkv + kv] = n;
+    if (tid == 0) p.vis_lens[row] = n;
     NFA_MARK(32, 13);
     NFA_FLUSH(32, clk_tail);
     return;
@@ -2701,7 +2742,7 @@ __global__ void __launch_bounds__(SB)
                                 : btr[imin(x / p.page, mb - 1)] * p.page + x % p.page;
       if (dest < p.max_vis) grow[dest] = slot;
     }
-    if (tid == 0) p.vis_lens[b * p.hkv + kv] = mcount + nu;
+    if (tid == 0) p.vis_lens[row] = mcount + nu;
     NFA_MARK(32, 13);
     NFA_FLUSH(32, clk_tail);
     return;
@@ -2743,7 +2784,7 @@ __global__ void __launch_bounds__(SB)
                               : btr[imin(x / p.page, mb - 1)] * p.page + x % p.page;
     if (dest < p.max_vis) grow[dest] = slot;
   }
-  if (tid == 0) p.vis_lens[b * p.hkv + kv] = nkeep + nu;
+  if (tid == 0) p.vis_lens[row] = nkeep + nu;
   NFA_MARK(32, 13);
   NFA_FLUSH(32, clk_tail);
   }  // tail
@@ -2760,6 +2801,13 @@ __global__ void __launch_bounds__(SB)
 using nfa::SelDims;
 
 // compute units of the current device, cached per device
+
+// The parameters with defaults filled in (kv_heads_mem 0 = hkv).
+static NfaSelectParams select_normalized(const NfaSelectParams &p) {
+  NfaSelectParams q = p;
+  if (q.kv_heads_mem == 0) q.kv_heads_mem = q.hkv;
+  return q;
+}
 
 static int select_check(const NfaSelectParams *p, bool need_workspace) {
   if (p == nullptr) {
@@ -2778,6 +2826,11 @@ static int select_check(const NfaSelectParams *p, bool need_workspace) {
     nfa_set_error("nfa_select_layer: unsupported heads hq=%d hkv=%d", p->hq, p->hkv);
     return NFA_EINVAL;
   }
+  if (p->kv_heads_mem != 0 && p->kv_heads_mem != p->hkv && p->kv_heads_mem != 1) {
+    nfa_set_error("nfa_select_layer: kv_heads_mem %d must be hkv (%d) or 1",
+                  p->kv_heads_mem, p->hkv);
+    return NFA_EINVAL;
+  }
   if (p->far_method < NFA_METHOD_MINMAX || p->far_method > NFA_METHOD_AVG_TOP2 ||
       p->near_method < NFA_METHOD_MINMAX || p->near_method > NFA_METHOD_AVG ||
       (p->far_method == NFA_METHOD_AVG_TOP2 && p->hq / p->hkv < 2)) {
@@ -2794,11 +2847,11 @@ static int select_check(const NfaSelectParams *p, bool need_workspace) {
     nfa_set_error("nfa_select_layer: bad L2 dim count %d", p->fine_dsub);
     return NFA_EINVAL;
   }
-  if (p->l2_quant && (p->l2_keys_l == nullptr || p->fine_dsub != nfa::kQ4Dims ||
+  if (p->l2_quant && (p->l2_keys_l == nullptr || !nfa::q4_dims_ok(p->fine_dsub) ||
                       p->kv_dtype != NFA_DTYPE_BF16)) {
-    nfa_set_error("nfa_select_layer: 4-bit L2 keys need the L2 side cache, %d L2 "
-                  "dims and bf16 KV (got %d dims, kv dtype %d)",
-                  nfa::kQ4Dims, p->fine_dsub, p->kv_dtype);
+    nfa_set_error("nfa_select_layer: 4-bit L2 keys need the L2 side cache, 32 or 64 "
+                  "L2 dims and bf16 KV (got %d dims, kv dtype %d)",
+                  p->fine_dsub, p->kv_dtype);
     return NFA_EINVAL;
   }
   if (p->bs <= 0 || p->page <= 0 || p->max_blocks <= 0 || p->k2 <= 0 ||
@@ -2847,8 +2900,11 @@ static int select_check(const NfaSelectParams *p, bool need_workspace) {
     nfa_set_error("nfa_select_layer: null device pointer");
     return NFA_EINVAL;
   }
-  if (p->k_new != nullptr && (p->v_new == nullptr || p->slots == nullptr ||
-                              p->v_pool_l == nullptr)) {
+  // (a shared arena head may take keys only: its values are part of them)
+  const bool shared = p->kv_heads_mem != 0 && p->kv_heads_mem < p->hkv;
+  if (p->k_new != nullptr &&
+      ((p->v_new == nullptr && !shared) || p->slots == nullptr ||
+       (p->v_new != nullptr && p->v_pool_l == nullptr))) {
     nfa_set_error("nfa_select_layer: decode write needs k, v, slots and v pool");
     return NFA_EINVAL;
   }
@@ -2991,8 +3047,9 @@ static int32_t select_launch(const NfaSelectParams &p, const SelDims &sd,
 extern "C" int32_t nfa_select_layer(const NfaSelectParams *p, void *stream) {
   const int rc = select_check(p, true);
   if (rc != NFA_OK) return rc;
-  const SelDims sd = nfa::sel_dims(*p, nfa::device_cus());
-  return select_launch(*p, sd, (hipStream_t)stream, "nfa_select_layer");
+  const NfaSelectParams q = select_normalized(*p);
+  const SelDims sd = nfa::sel_dims(q, nfa::device_cus());
+  return select_launch(q, sd, (hipStream_t)stream, "nfa_select_layer");
 }
 
 // ---------------------------------------------------------------------------
@@ -3092,7 +3149,7 @@ extern "C" int32_t nfa_select_layer_noalloc(const NfaSelectParams *p, void *stre
   sd.w_surv = kScratchKeys + keys;
   sd.w_scount = sd.w_surv + surv;
   sd.w_total = need;
-  NfaSelectParams q = *p;
+  NfaSelectParams q = select_normalized(*p);
   q.workspace = ptr;
   q.workspace_bytes = NFA_SELECT_SCRATCH_BYTES;
   return select_launch(q, sd, s, "nfa_select_layer_noalloc");

@@ -92,10 +92,12 @@ extern "C" int32_t nfa_attn_params_size(void) {
   return (int32_t)sizeof(NfaAttnParams);
 }
 
+// DV == 0 writes keys only (values and the V pool may then be NULL): a
+// latent arena whose values are part of the key rows.
 static int check_write(int batch, int hkv, int D, int DV, int page, int dtype,
                        const void *k, const void *v, const void *kp,
                        const void *vp, const char *who) {
-  if (hkv <= 0 || D <= 0 || DV <= 0 || page <= 0 || batch < 0) {
+  if (hkv <= 0 || D <= 0 || DV < 0 || page <= 0 || batch < 0) {
     nfa_set_error("%s: bad geometry", who);
     return NFA_EINVAL;
   }
@@ -103,7 +105,7 @@ static int check_write(int batch, int hkv, int D, int DV, int page, int dtype,
     nfa_set_error("%s: unsupported dtype %d", who, dtype);
     return NFA_EINVAL;
   }
-  if (!k || !v || !kp || !vp) {
+  if (!k || !kp || (DV > 0 && (!v || !vp))) {
     nfa_set_error("%s: null device pointer", who);
     return NFA_EINVAL;
   }

@@ -16,7 +16,8 @@ PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(PKG_ROOT, 'csrc')
 LIB_DIR = os.path.join(PKG_ROOT, 'lib')
 OBJ_DIR = os.path.join(PKG_ROOT, 'lib', 'obj')
-SOURCES = ('nfa_select.hip', 'nfa_attn.hip', 'nfa_write.hip', 'nfa_decode_fused.hip', 'nfa_gate.hip')
+SOURCES = ('nfa_select.hip', 'nfa_attn.hip', 'nfa_mla_attn.hip', 'nfa_write.hip',
+           'nfa_decode_fused.hip', 'nfa_gate.hip')
 ARCH = 'gfx950'
 
 # Bit-exactness of the selector depends on these: no FMA contraction, IEEE

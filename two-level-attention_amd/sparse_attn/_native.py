@@ -45,6 +45,7 @@ class NfaSelectParams(ctypes.Structure):
         ('kv_dtype', _i32), ('q_dtype', _i32),
         ('max_vis', _i32), ('middle_only', _i32), ('pool_pages', _i32),
         ('protected_only', _i32), ('scale', _f32), ('l2_quant', _i32),
+        ('kv_heads_mem', _i32),
         ('k_pool_l', _ptr), ('v_pool_l', _ptr), ('block_table_l', _ptr),
         ('lengths', _ptr), ('active_req', _ptr), ('valid_req', _ptr),
         ('skip_far_l', _ptr), ('skip_near_l', _ptr),
@@ -77,6 +78,19 @@ class NfaAttnParams(ctypes.Structure):
         ('q', _ptr), ('k_pool', _ptr), ('v_pool', _ptr),
         ('gather', _ptr), ('vis_lens', _ptr), ('query_to_req', _ptr),
         ('out', _ptr), ('workspace', _ptr), ('workspace_bytes', _i64),
+    ]
+
+
+class NfaMlaAttnParams(ctypes.Structure):
+    _fields_ = [
+        ('abi_version', _i32), ('struct_size', _i32),
+        ('total_q', _i32), ('heads', _i32), ('latent_dim', _i32),
+        ('value_dim', _i32), ('page', _i32), ('gather_rows', _i32),
+        ('max_vis', _i32), ('kv_dtype', _i32), ('q_dtype', _i32),
+        ('out_dtype', _i32), ('pool_pages', _i32), ('scale', _f32),
+        ('q', _ptr), ('kv_pool', _ptr), ('gather', _ptr), ('vis_lens', _ptr),
+        ('query_to_req', _ptr), ('out', _ptr), ('workspace', _ptr),
+        ('workspace_bytes', _i64),
     ]
 
 
@@ -148,7 +162,8 @@ EXPORTS = (
     'nfa_decode_linear', 'nfa_qk_norm_rope_decode', 'nfa_rmsnorm_decode',
     'nfa_gate_params_size', 'nfa_region_profile', 'nfa_attn_partial_size',
     'nfa_attn_combine_params_size', 'nfa_sparse_attn_partial', 'nfa_attn_regions_combine',
-    'nfa_attn_partial_workspace_bytes',
+    'nfa_attn_partial_workspace_bytes', 'nfa_mla_attn_decode',
+    'nfa_mla_attn_workspace_bytes', 'nfa_mla_attn_params_size',
 )
 
 _lib = None
@@ -219,6 +234,11 @@ def load_library(path: str = None):
             ctypes.POINTER(NfaAttnParams), ctypes.POINTER(NfaAttnPartial)]
         lib.nfa_attn_regions_combine.restype = _i32
         lib.nfa_attn_regions_combine.argtypes = [ctypes.POINTER(NfaAttnCombineParams), _ptr]
+        lib.nfa_mla_attn_params_size.restype = _i32
+        lib.nfa_mla_attn_decode.restype = _i32
+        lib.nfa_mla_attn_decode.argtypes = [ctypes.POINTER(NfaMlaAttnParams), _ptr]
+        lib.nfa_mla_attn_workspace_bytes.restype = _i64
+        lib.nfa_mla_attn_workspace_bytes.argtypes = [ctypes.POINTER(NfaMlaAttnParams)]
         if lib.nfa_abi_version() != ABI_VERSION:
             raise NativeError('libnfa_hip ABI version mismatch')
         if lib.nfa_select_params_size() != ctypes.sizeof(NfaSelectParams):
@@ -235,6 +255,8 @@ def load_library(path: str = None):
             raise NativeError('NfaAttnPartial layout mismatch')
         if lib.nfa_attn_combine_params_size() != ctypes.sizeof(NfaAttnCombineParams):
             raise NativeError('NfaAttnCombineParams layout mismatch')
+        if lib.nfa_mla_attn_params_size() != ctypes.sizeof(NfaMlaAttnParams):
+            raise NativeError('NfaMlaAttnParams layout mismatch')
         if path is None:
             _lib = lib
         return lib

@@ -131,21 +131,31 @@ class RequestState:
 
 class GraphReadyPagedRegionLayer:
     """One layer's physical KV arena ``[P + 1, 1, HKV, page, D]`` and its page
-    allocator (the PAD page ``P`` is never handed out)."""
+    allocator (the PAD page ``P`` is never handed out).  A ``latent`` arena
+    (absorbed multi-head latent attention) holds one row per token and kv
+    head, ``[c | k_pe]``, whose first ``head_dim_v`` dims are the values:
+    ``kv_pool_v`` is then a view of ``kv_pool_k``, not a second pool."""
 
     def __init__(self, *, geometry, max_physical_pages, num_kv_heads,
-                 num_query_heads=None, head_dim_k, head_dim_v, dtype, device):
+                 num_query_heads=None, head_dim_k, head_dim_v, dtype, device,
+                 latent=False):
         self.geometry = geometry
         self.max_physical_pages = max_physical_pages
         self.PAD_PAGE_ID = max_physical_pages
         self.num_kv_heads = num_kv_heads
         self.head_dim_k = head_dim_k
         self.head_dim_v = head_dim_v
+        self.latent = bool(latent)
         self.dtype = dtype
         self.device = device
         shape = (max_physical_pages + 1, 1, num_kv_heads, geometry.page)
         self.kv_pool_k = torch.empty(shape + (head_dim_k,), dtype=dtype, device=device)
-        self.kv_pool_v = torch.empty(shape + (head_dim_v,), dtype=dtype, device=device)
+        if self.latent:
+            if head_dim_v > head_dim_k:
+                raise ValueError('latent values are the first dims of the key rows')
+            self.kv_pool_v = self.kv_pool_k[..., :head_dim_v]
+        else:
+            self.kv_pool_v = torch.empty(shape + (head_dim_v,), dtype=dtype, device=device)
         self.kv_pool_k[-1].zero_()
         self.kv_pool_v[-1].zero_()
         self._fresh = 0          # pages [_fresh, P) were never handed out
@@ -213,7 +223,7 @@ class GraphReadyPagedRegionCache:
     def __init__(self, n_layers, geometry, *, max_requests, max_physical_pages,
                  max_blocks, max_visible_len, max_query_tokens, num_kv_heads,
                  num_query_heads=None, head_dim_k, head_dim_v, dtype, device,
-                 visible_buckets=None):
+                 visible_buckets=None, latent=False):
         device = torch.device(device)
         self.geometry = geometry
         self.n_layers = n_layers
@@ -223,11 +233,18 @@ class GraphReadyPagedRegionCache:
         self.max_query_tokens = max_query_tokens
         self.num_kv_heads = num_kv_heads
         self.num_query_heads = num_query_heads or num_kv_heads
+        # a latent arena (absorbed MLA: one shared row per token) selects per
+        # query head, so its gather rows are per query head
+        self.latent = bool(latent)
+        if self.latent and num_kv_heads != 1:
+            raise ValueError('a latent arena holds one kv head')
+        self.selection_heads = self.num_query_heads if self.latent else num_kv_heads
         self.layers = [
             GraphReadyPagedRegionLayer(
                 geometry=geometry, max_physical_pages=max_physical_pages,
                 num_kv_heads=num_kv_heads, head_dim_k=head_dim_k,
-                head_dim_v=head_dim_v, dtype=dtype, device=device)
+                head_dim_v=head_dim_v, dtype=dtype, device=device,
+                latent=self.latent)
             for _ in range(n_layers)]
         self.layer_kv_ptrs_buf = torch.tensor(
             [layer.kv_pool_k.data_ptr() for layer in self.layers],
@@ -266,10 +283,10 @@ class GraphReadyPagedRegionCache:
         self.query_req_ids_buf = torch.arange(q, dtype=i64, device=device)
         self.block_table_buf = torch.full((nl, r, max_blocks), pad, dtype=i32,
                                           device=device)
-        self.gather_indices_buf = torch.full((nl, r, num_kv_heads, max_visible_len),
+        sh = self.selection_heads
+        self.gather_indices_buf = torch.full((nl, r, sh, max_visible_len),
                                              INVALID_GATHER_IDX, dtype=i32, device=device)
-        self.visible_lens_buf = torch.zeros((nl, r, num_kv_heads), dtype=i32,
-                                            device=device)
+        self.visible_lens_buf = torch.zeros((nl, r, sh), dtype=i32, device=device)
         self.skip_far_layer_buf = torch.zeros((nl, r), dtype=i32, device=device)
         self.skip_near_layer_buf = torch.zeros((nl, r), dtype=i32, device=device)
 
@@ -297,7 +314,7 @@ class GraphReadyPagedRegionCache:
                 raise ValueError(
                     f'visible bucket {width} outside (0, {self.max_visible_len}]')
             if width < self.max_visible_len and width not in self._gather_indices_by_vis:
-                shape = (self.n_layers, self.max_requests, self.num_kv_heads)
+                shape = (self.n_layers, self.max_requests, self.selection_heads)
                 dev = self.gather_indices_buf.device
                 self._gather_indices_by_vis[width] = torch.full(
                     shape + (width,), INVALID_GATHER_IDX, dtype=torch.int32, device=dev)
@@ -431,7 +448,10 @@ class GraphReadyPagedRegionCache:
             raise ValueError('graph-ready prefill expects unpadded B1 KV')
         if keys.shape[1] != layer.num_kv_heads:
             raise ValueError('KV head count does not match arena')
-        if keys.device != values.device or keys.dtype != values.dtype:
+        if values is None:
+            if not layer.latent:
+                raise ValueError('prefill values are required (not a latent arena)')
+        elif keys.device != values.device or keys.dtype != values.dtype:
             raise ValueError('KV dtype/device mismatch')
         n = keys.shape[-2]
         pages = -(-n // page)

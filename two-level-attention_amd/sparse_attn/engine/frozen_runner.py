@@ -58,16 +58,21 @@ def _request_failure_guard(cache, request_id):
 
 
 def _model_dims(model):
-    """(config, kv heads, key dim, value dim) of the paged arena: a
+    """(config, kv heads, key dim, value dim, latent) of the paged arena: a
     DeepSeek-V2 model stores its latent attention expanded per head (key =
-    nope + rope dims, one kv head per query head)."""
+    nope + rope dims, one kv head per query head), or -- patched with
+    ``mla='absorbed'`` -- as latent rows (one kv head of kv_lora_rank + rope
+    dims, the values their first kv_lora_rank dims)."""
     cfg = model.config
     if getattr(cfg, 'model_type', None) == 'deepseek_v2':
+        if getattr(model, '_nfa_mla', 'expanded') == 'absorbed':
+            return (cfg, 1, cfg.kv_lora_rank + cfg.qk_rope_head_dim, cfg.kv_lora_rank,
+                    True)
         return (cfg, cfg.num_attention_heads, cfg.qk_nope_head_dim + cfg.qk_rope_head_dim,
-                cfg.v_head_dim)
+                cfg.v_head_dim, False)
     head_dim = getattr(cfg, 'head_dim', None) or cfg.hidden_size // cfg.num_attention_heads
     return (cfg, cfg.num_key_value_heads, head_dim,
-            int(getattr(cfg, 'v_head_dim', None) or head_dim))
+            int(getattr(cfg, 'v_head_dim', None) or head_dim), False)
 
 
 def build_frozen_cache(model, geometry, sequence_capacity, *, max_requests=1,
@@ -82,14 +87,14 @@ def build_frozen_cache(model, geometry, sequence_capacity, *, max_requests=1,
         max_visible_len = sequence_capacity + geometry.max_new_tokens + 16
     if physical_pages is None:
         physical_pages = max_requests * max_blocks + 8
-    cfg, hkv, head_dim, head_dim_v = _model_dims(model)
+    cfg, hkv, head_dim, head_dim_v, latent = _model_dims(model)
     return GraphReadyPagedRegionCache(
         cfg.num_hidden_layers, geometry, max_requests=max_requests,
         max_physical_pages=physical_pages, max_blocks=max_blocks,
         max_visible_len=max_visible_len, max_query_tokens=max_requests,
         num_kv_heads=hkv, num_query_heads=cfg.num_attention_heads,
         head_dim_k=head_dim, head_dim_v=head_dim_v, dtype=model.dtype,
-        device=next(model.parameters()).device)
+        device=next(model.parameters()).device, latent=latent)
 
 
 def _prefill_mask_arg(model):

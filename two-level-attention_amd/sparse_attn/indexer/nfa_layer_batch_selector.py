@@ -58,6 +58,26 @@ def _dims_for(indexer, device, head_dim):
     return l1, fine, l1_key, fine_key
 
 
+def _latent_dims(indexer, device, layer0):
+    """L1 / L2 dims of a latent arena row ``[c (head_dim_v) | k_pe]``: the
+    RoPE part, where the expanded heads' ``mla_rope`` dims (128..191 of
+    ``[k_nope | k_pe]``, ``nfa_indexer.py:133-134``) come from -- every
+    expanded head holds the same k_pe, so selections agree bit for bit."""
+    if (not indexer.enable_subspace or indexer.subspace != 'mla_rope'
+            or indexer.l2_subspace != 'same'):
+        raise ValueError('a latent (absorbed MLA) cache selects on the mla_rope '
+                         'subspace with the same L2 dims')
+    cache = getattr(indexer, '_nfa_hip_latent_dims', None)
+    key = (str(device), layer0.head_dim_k, layer0.head_dim_v)
+    if cache is not None and cache[0] == key:
+        return cache[1], cache[1], cache[2], cache[2]
+    dims = torch.arange(layer0.head_dim_v, layer0.head_dim_k, dtype=torch.int64)
+    dims_key = tuple(dims.tolist())
+    dims = dims.to(device=device, dtype=torch.int32).contiguous()
+    indexer._nfa_hip_latent_dims = (key, dims, dims_key)
+    return dims, dims, dims_key, dims_key
+
+
 def _workspace(cache):
     ws = getattr(cache, '_nfa_selector_workspace', None)
     if ws is None:
@@ -78,9 +98,9 @@ def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype, fine_key,
     page [max_req, hkv, dsub], and the L2 side copy [max_req, hkv,
     max_blocks * bs, fine_dsub] of every visible token's L2 dims (None for a
     full-width L2 subspace, or when ``cache.nfa_l2_side_copy`` is False) --
-    with ``quant``, 20 bytes per token slot instead (16 bytes of 4-bit codes,
-    then bf16 scale and zero); a new dims set for a layer forces rebuilds of
-    both."""
+    with ``quant``, fine_dsub / 2 + 4 bytes per token slot instead (4-bit
+    codes, then bf16 scale and zero); a new dims set for a layer forces
+    rebuilds of both."""
     layer0 = cache.layers[0]
     device = layer0.kv_pool_k.device
     lengths = getattr(cache, '_nfa_page_stats_lengths', None)
@@ -113,7 +133,9 @@ def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype, fine_key,
         side = None
         slots = cache.max_requests * layer0.num_kv_heads * cache.max_blocks * bs
         if want_side and quant:
-            side = torch.empty(slots * 20, dtype=torch.uint8, device=device)
+            # fine_dsub / 2 bytes of codes, then bf16 scale and zero, per slot
+            side = torch.empty(slots * (len(fine_key) // 2 + 4), dtype=torch.uint8,
+                               device=device)
         elif want_side:
             side = torch.empty(slots * len(fine_key), dtype=dtype, device=device)
         bufs = store[key] = (stats, side)
@@ -124,11 +146,15 @@ def _page_stats_buffers(cache, layer_idx, dims, dims_key, dtype, fine_key,
     return bufs[0], bufs[1], lengths[layer_idx]
 
 
-def _check_decode_write(decode_write, b, hkv, device):
+def _check_decode_write(decode_write, b, hkv, device, latent=False):
     keys, values, slots = decode_write
     if keys.ndim != 4 or keys.shape[-2] != 1:
         raise ValueError('graph-ready decode KV must be one token per row')
-    if values.ndim != 4 or values.shape[-2] != 1:
+    if values is None:
+        # a latent arena's values are the key rows' first dims
+        if not latent:
+            raise ValueError('paged write decode expects [B,HK,1,DV] values')
+    elif values.ndim != 4 or values.shape[-2] != 1:
         raise ValueError('paged write decode expects [B,HK,1,DV] values')
     if keys.shape[0] != b or keys.shape[0] != slots.shape[0]:
         raise ValueError('request batch must match KV batch')
@@ -138,7 +164,8 @@ def _check_decode_write(decode_write, b, hkv, device):
         slots = slots.to(device)
     if slots.dtype != torch.int32:
         slots = slots.to(torch.int32)
-    return (keys.contiguous(), values.contiguous(), slots.contiguous())
+    return (keys.contiguous(), None if values is None else values.contiguous(),
+            slots.contiguous())
 
 
 def _alloc_debug(debug, b, hkv, max_blocks, k_f, k_n, k2, cand_cap, device):
@@ -185,7 +212,11 @@ def select_layer_params(cache, layer_idx, req_ids, query_states,
     if b > cache.planned_lengths_buf.numel():
         raise ValueError('selector batch exceeds fixed query metadata capacity')
     hq = cache.num_query_heads
-    hkv = layer0.num_kv_heads
+    latent = bool(getattr(cache, 'latent', False))
+    arena_heads = layer0.num_kv_heads
+    # selection rows per batch row: the kv heads, or every query head of a
+    # latent arena (one shared row per token, selected per query head)
+    hkv = cache.selection_heads if latent else arena_heads
     head_dim = layer0.head_dim_k
     if query_states.shape != (b, hq, head_dim):
         raise ValueError(f'current query must be [{b},{hq},{head_dim}] for one '
@@ -205,7 +236,10 @@ def select_layer_params(cache, layer_idx, req_ids, query_states,
 
     bs = int(indexer.args.tia_block_size)
     geo = cache.geometry
-    l1_dims, fine_dims, l1_key, fine_key = _dims_for(indexer, device, head_dim)
+    if latent:
+        l1_dims, fine_dims, l1_key, fine_key = _latent_dims(indexer, device, layer0)
+    else:
+        l1_dims, fine_dims, l1_key, fine_key = _dims_for(indexer, device, head_dim)
     if l1_dims.numel() not in (32, 64, 128):
         raise FallbackRequired(f'{l1_dims.numel()} L1 dims are not supported')
     nb_near = max(0, int(indexer.nt_near_pages))
@@ -235,8 +269,8 @@ def select_layer_params(cache, layer_idx, req_ids, query_states,
 
     kv_dtype = layer0.kv_pool_k.dtype
     quant = bool(getattr(indexer, 'l2_quant', False))
-    if quant and (fine_dims.numel() != 32 or kv_dtype != torch.bfloat16):
-        raise ValueError('--nfa_l2_quant needs 32 L2 dims and a bf16 KV cache '
+    if quant and (fine_dims.numel() not in (32, 64) or kv_dtype != torch.bfloat16):
+        raise ValueError('--nfa_l2_quant needs 32 or 64 L2 dims and a bf16 KV cache '
                          f'(got {fine_dims.numel()} dims, {kv_dtype})')
     (smin, smax, ssum, psum), l2_side, stats_len = _page_stats_buffers(
         cache, layer_idx, l1_dims, l1_key, kv_dtype, fine_key, head_dim, bs, quant)
@@ -250,6 +284,7 @@ def select_layer_params(cache, layer_idx, req_ids, query_states,
     p.struct_size = ctypes.sizeof(nat.NfaSelectParams)
     p.batch = b
     p.hq, p.hkv = hq, hkv
+    p.kv_heads_mem = arena_heads if not latent else 1
     p.head_dim, p.head_dim_v = head_dim, layer0.head_dim_v
     p.bs, p.page = bs, geo.page
     p.max_blocks, p.max_req = cache.max_blocks, cache.max_requests
@@ -288,11 +323,15 @@ def select_layer_params(cache, layer_idx, req_ids, query_states,
     if decode_write is not None:
         # converted copies are stream-ordered allocations: safe to drop after
         # the asynchronous launch
-        keys, values, slots = _check_decode_write(decode_write, b, hkv, device)
+        keys, values, slots = _check_decode_write(decode_write, b, arena_heads, device,
+                                                  latent)
         keys = keys.to(kv_dtype)
-        values = values.to(kv_dtype)
-        keep += [keys, values, slots]
-        p.k_new, p.v_new, p.slots = keys.data_ptr(), values.data_ptr(), slots.data_ptr()
+        keep += [keys, slots]
+        p.k_new, p.slots = keys.data_ptr(), slots.data_ptr()
+        if values is not None and not latent:
+            values = values.to(kv_dtype)
+            keep.append(values)
+            p.v_new = values.data_ptr()
     p.stat_min_l, p.stat_max_l, p.stat_sum_l = (
         smin.data_ptr(), smax.data_ptr(), ssum.data_ptr())
     p.stats_len_l = stats_len.data_ptr()

@@ -19,9 +19,16 @@ def _kv_contiguous(x):
 
 def paged_write_prefill(cache_layer, key_states, value_states, block_table, *,
                         workspace=None):
-    """Scatter an unpadded ``[1, HK, N, D]`` prefill through ``block_table``."""
+    """Scatter an unpadded ``[1, HK, N, D]`` prefill through ``block_table``.
+    A latent arena takes ``value_states`` None (its values are the key rows'
+    first dims)."""
     if key_states.ndim != 4 or key_states.shape[0] != 1 or key_states.shape[2] < 1:
         raise ValueError('paged write prefill expects [1,HK,N,D] keys')
+    keys_only = value_states is None
+    if keys_only and not getattr(cache_layer, 'latent', False):
+        raise ValueError('paged write prefill expects [1,HK,N,DV] values')
+    if keys_only:
+        value_states = key_states[..., :cache_layer.head_dim_v]
     if value_states.ndim != 4 or value_states.shape[:3] != key_states.shape[:3]:
         raise ValueError('paged write prefill expects [1,HK,N,DV] values')
     if key_states.shape[1] != cache_layer.num_kv_heads:
@@ -43,18 +50,21 @@ def paged_write_prefill(cache_layer, key_states, value_states, block_table, *,
             pid = int(block_table[lp])
             lo, hi = lp * page, min(lp * page + page, n)
             cache_layer.kv_pool_k[pid, 0, :, :hi - lo].copy_(key_states[0, :, lo:hi])
-            cache_layer.kv_pool_v[pid, 0, :, :hi - lo].copy_(value_states[0, :, lo:hi])
+            if not keys_only:
+                cache_layer.kv_pool_v[pid, 0, :, :hi - lo].copy_(value_states[0, :, lo:hi])
         return key_states, value_states
     lib = nat.load_library()
     keys = _kv_contiguous(key_states)
-    values = _kv_contiguous(value_states)
+    values = None if keys_only else _kv_contiguous(value_states)
     table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
     table = _kv_contiguous(table)
+    # keys only: value width 0, no value pointers
     rc = lib.nfa_paged_write_prefill(
-        keys.data_ptr(), values.data_ptr(), n, table.data_ptr(),
-        cache_layer.num_kv_heads, cache_layer.head_dim_k, cache_layer.head_dim_v,
+        keys.data_ptr(), None if keys_only else values.data_ptr(), n, table.data_ptr(),
+        cache_layer.num_kv_heads, cache_layer.head_dim_k,
+        0 if keys_only else cache_layer.head_dim_v,
         page, nat.dtype_code(keys.dtype), cache_layer.kv_pool_k.data_ptr(),
-        cache_layer.kv_pool_v.data_ptr(), nat.stream_handle())
+        None if keys_only else cache_layer.kv_pool_v.data_ptr(), nat.stream_handle())
     nat.check(rc, 'paged_write_prefill')
     return key_states, value_states
 
@@ -148,6 +158,72 @@ def sparse_paged_attention_gather(cache_layer, q, gather_indices, visible_lens,
     nat.check(lib.nfa_sparse_attn_decode(ctypes.byref(p), nat.stream_handle()),
               'sparse_paged_attention_gather')
     del keep
+    return out
+
+
+def sparse_mla_attention_gather(cache_layer, q, gather_indices, visible_lens,
+                                query_to_req, *, scale, workspace=None,
+                                out_dtype=None):
+    """Absorbed latent attention of each query head over its own selection.
+
+    ``cache_layer`` is a latent arena (one kv head, rows of ``head_dim_k`` =
+    value dims + 64 RoPE dims, the values the rows' first ``head_dim_v``
+    dims); ``q`` ``[T, H, head_dim_k]`` holds per head ``[W_uk^T q_nope |
+    q_pe]``; ``gather_indices`` ``[B, H, W]`` / ``visible_lens`` ``[B, H]``
+    are the per-head selections.  Returns ``[T, H, head_dim_v]`` -- each
+    head's softmax-weighted latent rows, before the value up-projection --
+    in ``out_dtype`` (default: the dtype of ``q``).  No reference
+    counterpart: the reference attends over expanded heads
+    (``sparse_paged_attention_gather``), which this equals up to rounding.
+    """
+    if q.ndim != 3 or q.shape[-1] != cache_layer.head_dim_k:
+        raise ValueError('latent attention expects flat [T,H,latent] query')
+    if cache_layer.num_kv_heads != 1:
+        raise ValueError('latent attention expects a single-head latent arena')
+    heads = q.shape[1]
+    _check_gather(gather_indices, visible_lens, heads)
+    if (gather_indices.dtype != torch.int32 or not gather_indices.is_contiguous()
+            or visible_lens.dtype != torch.int32 or not visible_lens.is_contiguous()):
+        raise ValueError('gather indices and lens must be contiguous int32')
+    nat.require_hip(q, 'sparse_mla_attention_gather')
+    lib = nat.load_library()
+    total_q = q.shape[0]
+    out = q.new_empty((total_q, heads, cache_layer.head_dim_v),
+                      dtype=out_dtype or q.dtype)
+    if total_q == 0:
+        return out
+    qc = q if q.is_contiguous() else q.contiguous()
+    q2r = query_to_req
+    if q2r.dtype != torch.int32:
+        q2r = q2r.to(torch.int32)
+    q2r = q2r.contiguous()
+    p = nat.NfaMlaAttnParams()
+    p.abi_version = nat.ABI_VERSION
+    p.struct_size = ctypes.sizeof(nat.NfaMlaAttnParams)
+    p.total_q, p.heads = total_q, heads
+    p.latent_dim, p.value_dim = cache_layer.head_dim_k, cache_layer.head_dim_v
+    p.page = cache_layer.geometry.page
+    p.gather_rows = gather_indices.shape[0]
+    p.max_vis = gather_indices.shape[-1]
+    p.kv_dtype = nat.dtype_code(cache_layer.kv_pool_k.dtype)
+    p.q_dtype = nat.dtype_code(qc.dtype)
+    p.out_dtype = nat.dtype_code(out.dtype)
+    p.pool_pages = cache_layer.kv_pool_k.shape[0]
+    p.scale = float(scale)
+    p.q = qc.data_ptr()
+    p.kv_pool = cache_layer.kv_pool_k.data_ptr()
+    p.gather = gather_indices.data_ptr()
+    p.vis_lens = visible_lens.data_ptr()
+    p.query_to_req = q2r.data_ptr()
+    p.out = out.data_ptr()
+    need = lib.nfa_mla_attn_workspace_bytes(ctypes.byref(p))
+    ws = _scratch(workspace, ('nfa_mla_attn_scratch', total_q, heads, p.max_vis,
+                              p.value_dim), need, q.device)
+    p.workspace = ws.data_ptr()
+    p.workspace_bytes = ws.numel()
+    nat.check(lib.nfa_mla_attn_decode(ctypes.byref(p), nat.stream_handle()),
+              'sparse_mla_attention_gather')
+    del qc, q2r
     return out
 
 

@@ -51,14 +51,21 @@ def _key_dim(module):
 def register_patch(model: nn.Module, args, snapshot=None,
                    rmsnorm_decode: bool = False,
                    mlp_silu_decode: bool = False,
-                   decode_layers: bool = False) -> int:
+                   decode_layers: bool = False,
+                   mla: str = 'expanded') -> int:
     """Patch the model's attention modules; returns how many were patched.
 
     ``rmsnorm_decode`` / ``mlp_silu_decode`` also move the decode-step
     RMSNorm and MLP onto fused HIP kernels; ``decode_layers`` runs the whole
-    decoder layer's decode step as seven fused launches.
+    decoder layer's decode step as seven fused launches.  ``mla`` chooses how
+    a DeepSeek-V2 model's caches hold its latent attention: ``expanded``
+    (per-head keys and values, as the reference's patch) or ``absorbed``
+    (one latent row per token, selection and attention in the latent space;
+    no reference counterpart).
     """
     _reject_removed_cache_args(args)
+    if mla not in ('expanded', 'absorbed'):
+        raise ValueError(f'unknown MLA layout {mla!r} (expanded or absorbed)')
     indexer_type = indexer_type_dict.get(args.method, None)
     if args.method != 'none' and indexer_type is None:
         raise ValueError(f'not support {args.method}')
@@ -85,6 +92,14 @@ def register_patch(model: nn.Module, args, snapshot=None,
             module.forward = MethodType(forward, module)
             n_patched += 1
     model_type = getattr(getattr(model, 'config', None), 'model_type', None)
+    if mla == 'absorbed':
+        if model_type != 'deepseek_v2':
+            raise ValueError('the absorbed MLA layout needs a DeepSeek-V2 model')
+        if getattr(args, 'nfa_subspace', None) != 'mla_rope':
+            raise ValueError('the absorbed MLA layout selects on --nfa_subspace mla_rope')
+    if model_type == 'deepseek_v2':
+        # read by build_frozen_cache: the arena layout of the model's caches
+        model._nfa_mla = mla
     if (rmsnorm_decode or mlp_silu_decode or decode_layers) and n_patched:
         if model_type not in ('qwen3', 'llama'):
             raise ValueError('fused decode patches cover Qwen3 and Llama models')
