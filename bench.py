@@ -88,6 +88,11 @@ def parse():
                          'attention patched)')
     ap.add_argument('--e2e-only', action='store_true',
                     help='run only the end-to-end model decode')
+    ap.add_argument('--mla', choices=['expanded', 'absorbed'],
+                    help='only the DeepSeek-V2-Lite MLA decode layer (16 heads, '
+                         'latent 512 + 64, batch 4 x 64K, 4-bit L2 keys on the 64 '
+                         'RoPE dims, --layers layers): expanded heads or the '
+                         'absorbed latent arena')
     ap.add_argument('--copy-calibration', type=int, default=0, metavar='MIB',
                     help='only copy a MIB-MiB device buffer three times (the '
                          'known-size kernel that scales rocprofv3 FETCH_SIZE '
@@ -877,6 +882,271 @@ def cpu_baseline(warmup=3, steps=10, seed=20261201):
                        'host); median per phase')
 
 
+# ---------------------------------------------------------------------------
+# DeepSeek-V2-Lite MLA decode layer (expanded heads or absorbed latent arena)
+# ---------------------------------------------------------------------------
+
+MLA_HEADS, MLA_RANK, MLA_ROPE, MLA_NOPE, MLA_V = 16, 512, 64, 128, 128
+
+
+def mla_algorithmic_bytes(mode, lengths, k2=1024, bs=16, window=128, near_len=4096,
+                          sink=4, k_far=96, k_near=32):
+    """Bytes one selector launch and one attention launch must move for the
+    DeepSeek-V2-Lite layer.  Selector: page statistics of the 64 RoPE dims
+    (min + max of far pages, the mean of near pages) -- once per request in
+    the latent arena, where every head shares them, once per head expanded
+    -- plus each head's candidate tokens' 4-bit L2 rows (32 B of codes, bf16
+    scale and zero), the decode row and each head's gather row.  Attention:
+    each head's selected rows (latent: the 576-dim row, 1152 B; expanded:
+    192 + 128 dims, 640 B), query, output and gather row."""
+    dsub, h = MLA_ROPE, MLA_HEADS
+    sel = att = 0
+    for n in lengths:
+        kt = (n + bs - 1) // bs
+        spl = sink // bs
+        near_start = max((n - window - near_len) // bs, spl)
+        swa_lo = max(near_start, kt - max(1, window // bs))
+        p_far = max(0, near_start - spl) - (1 if sink % bs and near_start > spl else 0)
+        p_near = max(0, swa_lo - near_start)
+        byp = max(n - window, 0)
+        t_c = (k_far + k_near) * bs + (bs - sink % bs if sink % bs else 0) + byp % bs
+        stat_heads = 1 if mode == 'absorbed' else h
+        l1 = stat_heads * (2 * p_far + p_near) * dsub * 2
+        l2 = h * t_c * (dsub // 2 + 4)
+        if mode == 'absorbed':
+            row = (MLA_RANK + MLA_ROPE) * 2
+            misc = row + h * (MLA_RANK + MLA_ROPE) * 2 + h * k2 * 4
+            att += h * k2 * row + h * (MLA_RANK + MLA_ROPE) * 2 + h * MLA_RANK * 4 + h * k2 * 4
+        else:
+            row = (MLA_NOPE + MLA_ROPE + MLA_V) * 2
+            misc = h * row + h * (MLA_NOPE + MLA_ROPE) * 2 + h * k2 * 4
+            att += h * k2 * row + h * (MLA_NOPE + MLA_ROPE) * 2 + h * MLA_V * 2 + h * k2 * 4
+        sel += l1 + l2 + misc
+    return dict(select=sel, attention=att)
+
+
+def mla_layer_bench(torch, args, device):
+    """Selector and attention of the DeepSeek-V2-Lite decode layer, batch 4 x
+    65536 tokens, ``--layers`` layers each with its own arena: selector-only
+    and attention-only graphs of one launch per layer, timed like the
+    Qwen3-8B layer (HIP events around each replay, lengths advancing)."""
+    from types import SimpleNamespace
+    from sparse_attn.cache import GraphReadyPagedRegionCache
+    from sparse_attn.indexer.nfa_indexer import NFAIndexer
+    from sparse_attn.indexer.nfa_layer_batch_selector import \
+        select_topk_for_layer_batched
+    from sparse_attn.ops.paged_region_kernels import (sparse_mla_attention_gather,
+                                                      sparse_paged_attention_gather)
+    from sparse_attn.ops.paged_region_kernels_nfa import nfa_args
+    from sparse_attn.policies.region_geometry import RegionGeometry
+
+    mode, layers, b, ctx = args.mla, args.layers, 4, 65536
+    h, rank, rope, nope, dv = MLA_HEADS, MLA_RANK, MLA_ROPE, MLA_NOPE, MLA_V
+    page = 16
+    new_tokens = 2 * args.kernel_rounds + 8
+    geo = RegionGeometry(sink=4, near=4096, window=128, page=page,
+                         max_new_tokens=new_tokens)
+    pages = (ctx + new_tokens + page - 1) // page
+    latent = mode == 'absorbed'
+    cache = GraphReadyPagedRegionCache(
+        layers, geo, max_requests=b, max_physical_pages=b * pages + 1,
+        max_blocks=pages + 8, max_visible_len=1024, max_query_tokens=b,
+        num_kv_heads=1 if latent else h, num_query_heads=h,
+        head_dim_k=rank + rope if latent else nope + rope,
+        head_dim_v=rank if latent else dv, dtype=torch.bfloat16, device=device,
+        latent=latent)
+    fargs = nfa_args('mla_rope')
+    fargs.tia_block_size = page
+    fargs.nfa_l2_quant = True
+    indexer = NFAIndexer(fargs)
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    scale = (nope + rope) ** -0.5
+    w_uk, w_uv, w_exp = [], [], []
+    for layer in range(layers):
+        w = (torch.randn(h * (nope + dv), rank, generator=gen, device=device)
+             * rank ** -0.5).to(torch.bfloat16).view(h, nope + dv, rank)
+        w_uk.append(w[:, :nope].contiguous())
+        w_uv.append(w[:, nope:].contiguous())
+        # kv_b_proj^T as a contiguous [rank, H * (nope + v)] operand (the
+        # expanded arena is c @ kv_b_proj^T, a plain 2-D product)
+        w_exp.append(w.reshape(h * (nope + dv), rank).t().contiguous())
+    for rid in range(b):
+        cache.add_request(rid)
+        for layer in range(layers):
+            c = torch.randn(ctx, rank, generator=gen, device=device).to(torch.bfloat16)
+            k_pe = synthetic_keys(torch, ctx, 1, rope, gen, device)[0, 0]
+            if latent:
+                cache.write_prefill(layer, rid, torch.cat([c, k_pe], -1)[None, None], None)
+            else:
+                kv = torch.matmul(c, w_exp[layer]).view(ctx, h, nope + dv).transpose(0, 1)
+                k = torch.cat([kv[..., :nope], k_pe[None].expand(h, -1, -1)], dim=-1)
+                v = kv[..., nope:]
+                cache.write_prefill(layer, rid, k[None].contiguous(), v[None].contiguous())
+                del kv, k, v
+            del c, k_pe
+        cache.freeze(rid, [False] * layers, [False] * layers)
+    attn = [SimpleNamespace(indexer=indexer, scaling=scale, layer_idx=l)
+            for l in range(layers)]
+    q_nope = [torch.randn(b, h, nope, generator=gen, device=device).to(torch.bfloat16)
+              for _ in range(layers)]
+    q_pe = [torch.randn(b, h, rope, generator=gen, device=device).to(torch.bfloat16)
+            for _ in range(layers)]
+    row = [torch.randn(b, 1, 1, rank + rope if latent else nope + rope, generator=gen,
+                       device=device).to(torch.bfloat16) for _ in range(layers)]
+    if latent:
+        q = [torch.cat([torch.bmm(qn.transpose(0, 1).contiguous(), wk).transpose(0, 1), qp],
+                       -1).contiguous() for qn, qp, wk in zip(q_nope, q_pe, w_uk)]
+        keys = row
+        vals = [None] * layers
+    else:
+        q = [torch.cat([qn, qp], -1).contiguous() for qn, qp in zip(q_nope, q_pe)]
+        keys = [torch.randn(b, h, 1, nope + rope, generator=gen, device=device).to(
+            torch.bfloat16) for _ in range(layers)]
+        vals = [torch.randn(b, h, 1, dv, generator=gen, device=device).to(torch.bfloat16)
+                for _ in range(layers)]
+    w_uv_t = [w.transpose(1, 2).contiguous() for w in w_uv]
+    ws = cache.__dict__.setdefault('_nfa_selector_workspace', {})
+    req_ids = list(range(b))
+    outs = [None] * layers
+
+    def sel_all():
+        for layer in range(layers):
+            select_topk_for_layer_batched(
+                cache, layer, req_ids, q[layer], attention=attn[layer],
+                decode_write=(keys[layer], vals[layer],
+                              cache.slot_mapping_for_layer(layer)[:b]))
+
+    def att_all():
+        for layer in range(layers):
+            if latent:
+                o = sparse_mla_attention_gather(
+                    cache.layers[layer], q[layer], cache.gather_indices_for_layer(layer),
+                    cache.visible_lens_for_layer(layer), cache.query_to_req_buf,
+                    scale=scale, workspace=ws)
+                # each head's value up-projection: [H, B, rank] x [H, rank, v]
+                outs[layer] = torch.bmm(o.transpose(0, 1).contiguous(), w_uv_t[layer])
+            else:
+                outs[layer] = sparse_paged_attention_gather(
+                    cache.layers[layer], q[layer], cache.gather_indices_for_layer(layer),
+                    cache.visible_lens_for_layer(layer), cache.query_to_req_buf,
+                    scale=scale, workspace=ws)
+
+    def plan():
+        cache.new_step(req_ids)
+        cache.plan_common(req_ids)
+
+    w = SimpleNamespace(q=q)
+    print(f'# MLA ({mode}) workload ready: {layers} layers, {b} x {ctx} tokens',
+          file=sys.stderr, flush=True)
+    kt = _time_graphs(torch, sel_all, att_all, layers, args.kernel_rounds, plan, cache,
+                      req_ids)
+    nbytes = mla_algorithmic_bytes(mode, kt['lengths'])
+    arena = cache.layers[0].kv_pool_k.numel() * 2 + (
+        0 if latent else cache.layers[0].kv_pool_v.numel() * 2)
+    stats, side = stats_side_bytes(cache)
+    sel_gbs = nbytes['select'] / (kt['select_us_median'] * 1e-6) / 1e9
+    att_gbs = nbytes['attention'] / (kt['attention_us_median'] * 1e-6) / 1e9
+    layer_us = kt['select_us_median'] + kt['attention_us_median']
+    tokens = cache.layers[0].max_physical_pages * page
+    result = {
+        'metric': 'MLA sparse-attn decode layer µs (DeepSeek-V2-Lite, batch 4 x 64K)',
+        'value': round(layer_us, 3), 'unit': 'µs per layer (selector + attention)',
+        'n_gpus': 1, 'steps': args.kernel_rounds, 'warmup': args.kernel_rounds,
+        'ms_per_step': round(layer_us * layers / 1000.0, 4),
+        'higher_is_better': False, 'scaling': 'weak', 'vs_baseline': None,
+        'dtype': 'bf16', 'data': 'synthetic',
+        'config': {
+            'workload': f'DeepSeek-V2-Lite MLA decode layer ({mode}): 16 heads, '
+                        f'latent {rank} + {rope}, nope {nope}, v {dv}, batch {b} x '
+                        f'{ctx} tokens, page 16, 4-bit L2 keys on the {rope} RoPE dims, '
+                        f'{layers} layers with their own arenas, hipGraph',
+            'mla': mode, 'layers': layers, 'batch': b, 'context': ctx,
+            'select_us': round(kt['select_us_median'], 3),
+            'attention_us': round(kt['attention_us_median'], 3),
+            'select_bytes': nbytes['select'], 'attention_bytes': nbytes['attention'],
+            'attention_gbs': round(att_gbs, 1),
+            'layer_hbm_frac': round((nbytes['select'] + nbytes['attention'])
+                                    / (layer_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            'arena_bytes_per_token': arena // tokens,
+            'arena_bytes_per_layer': arena,
+            'page_stats_bytes_per_layer': stats,
+            'l2_side_bytes_per_layer': side,
+            'attention_includes': ('the latent kernel and the W_uv up-projection'
+                                   if latent else 'the gather attention kernel'),
+        },
+        'roofline': {
+            'bound': 'hbm', 'kernel': 'nfa_select_layer (nfa_select_kernel)',
+            'achieved': round(sel_gbs, 1), 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
+            'frac': round(sel_gbs / HBM_PEAK_GBS, 4), 'traffic': None,
+        },
+        'cpu_baseline': None,
+    }
+    print(json.dumps(result), flush=True)
+    del w
+
+
+def stats_side_bytes(cache, layer=0):
+    """Bytes of one layer's persistent page statistics (min, max, mean and
+    the fp32 running sums) and of its L2 side cache (raw L2 dims, or 4-bit
+    codes with scale and zero)."""
+    stats = side = 0
+    for key, (st, sd) in getattr(cache, '_nfa_page_stats_persistent', {}).items():
+        if key[0] != layer:
+            continue
+        stats += sum(t.numel() * t.element_size() for t in st)
+        if sd is not None:
+            side += sd.numel() * sd.element_size()
+    return stats, side
+
+
+def _time_graphs(torch, sel_all, att_all, layers, rounds, plan, cache, req_ids):
+    """Median per-launch µs of a selector-only and an attention-only graph of
+    one launch per layer (HIP events on the replaying stream, lengths
+    advancing between replays as in decode)."""
+    plan()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        sel_all()
+        att_all()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g_sel, g_att = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_sel):
+        sel_all()
+    with torch.cuda.graph(g_att):
+        att_all()
+    cache.commit_step()
+    for _ in range(rounds):
+        plan()
+        g_sel.replay()
+        g_att.replay()
+        cache.commit_step()
+    torch.cuda.synchronize()
+    sel, att, lengths = [], [], []
+    marks = [(a, b, torch.cuda.Event(enable_timing=True))
+             for a, b in warm_events(torch, rounds)]
+    for m in marks:
+        m[2].record()
+    torch.cuda.synchronize()
+    for a, b, c in marks:
+        plan()
+        lengths = [int(cache.pending_lengths[r]) for r in req_ids]
+        a.record()
+        g_sel.replay()
+        b.record()
+        g_att.replay()
+        c.record()
+        cache.commit_step()
+        c.synchronize()
+        sel.append(a.elapsed_time(b) * 1000.0 / layers)
+        att.append(b.elapsed_time(c) * 1000.0 / layers)
+    sel.sort()
+    att.sort()
+    return dict(select_us_median=sel[len(sel) // 2],
+                attention_us_median=att[len(att) // 2], lengths=lengths)
+
+
 def warm_events(torch, n):
     """``n`` pairs of timing events, each recorded once already: HIP creates
     an event at its first record, slowly for the first few hundred of a
@@ -948,7 +1218,7 @@ def main():
     single = args.batch == 1 and not args.ragged
     cpu = None
     if not args.no_cpu_baseline and single and not args.e2e_only \
-            and args.copy_calibration == 0:
+            and args.copy_calibration == 0 and not args.mla:
         # before torch or HIP start: the baseline forks worker processes
         print('# cpu baseline ...', file=sys.stderr, flush=True)
         cpu = cpu_baseline(seed=args.seed)
@@ -969,6 +1239,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({'copy_bytes_read': n, 'copy_bytes_written': n,
                           'launches': 3}), flush=True)
+        return
+    if args.mla:
+        mla_layer_bench(torch, args, device)
         return
     if args.e2e_only:
         e2e = end_to_end(torch, args, device)
@@ -1005,6 +1278,7 @@ def main():
     hot_tok_s = args.batch * 1e3 / hot['ms_per_step_median']
     geometry = {'heads': [w.hq, w.hkv], 'head_dim': w.d, 'page': w.page}
     lengths = list(w.lengths)
+    stats_bytes, side_bytes = stats_side_bytes(cache)
     e2e = None
     if not args.no_e2e:
         del graph, w, cache, outs
@@ -1074,6 +1348,10 @@ def main():
             'select_bytes': nbytes['select'],
             'attention_bytes': nbytes['attention'],
             'attention_gbs': round(att_gbs, 1),
+            # persistent per-layer memory besides the KV arena (all request
+            # slots): page statistics and the L2 side cache (--l2-quant: 4-bit)
+            'page_stats_bytes_per_layer': stats_bytes,
+            'l2_side_bytes_per_layer': side_bytes,
             'parallelism': 'single GPU',
         },
         'roofline': {
