@@ -1004,7 +1004,6 @@ def mla_layer_bench(torch, args, device):
             torch.bfloat16) for _ in range(layers)]
         vals = [torch.randn(b, h, 1, dv, generator=gen, device=device).to(torch.bfloat16)
                 for _ in range(layers)]
-    w_uv_t = [w.transpose(1, 2).contiguous() for w in w_uv]
     ws = cache.__dict__.setdefault('_nfa_selector_workspace', {})
     req_ids = list(range(b))
     outs = [None] * layers
@@ -1019,12 +1018,11 @@ def mla_layer_bench(torch, args, device):
     def att_all():
         for layer in range(layers):
             if latent:
-                o = sparse_mla_attention_gather(
+                # each head's value up-projection fused into the kernel
+                outs[layer] = sparse_mla_attention_gather(
                     cache.layers[layer], q[layer], cache.gather_indices_for_layer(layer),
                     cache.visible_lens_for_layer(layer), cache.query_to_req_buf,
-                    scale=scale, workspace=ws)
-                # each head's value up-projection: [H, B, rank] x [H, rank, v]
-                outs[layer] = torch.bmm(o.transpose(0, 1).contiguous(), w_uv_t[layer])
+                    scale=scale, workspace=ws, w_uv=w_uv[layer])
             else:
                 outs[layer] = sparse_paged_attention_gather(
                     cache.layers[layer], q[layer], cache.gather_indices_for_layer(layer),
@@ -1071,7 +1069,7 @@ def mla_layer_bench(torch, args, device):
             'arena_bytes_per_layer': arena,
             'page_stats_bytes_per_layer': stats,
             'l2_side_bytes_per_layer': side,
-            'attention_includes': ('the latent kernel and the W_uv up-projection'
+            'attention_includes': ('the latent kernel with the W_uv up-projection fused'
                                    if latent else 'the gather attention kernel'),
         },
         'roofline': {

@@ -221,8 +221,13 @@ typedef struct NfaMlaAttnParams {
   const int32_t *gather;      /* [gather_rows, heads, max_vis] physical slots */
   const int32_t *vis_lens;    /* [gather_rows, heads] */
   const int32_t *query_to_req;/* [T] */
-  void *out;                  /* [T, heads, value_dim]: sum_i p_i c_i per head,
-                                 before the value up-projection */
+  const void *w_uv;           /* optional [heads, out_dim, value_dim] bf16: each
+                                 head's value up-projection (kv_b_proj's value
+                                 rows), applied to the head's result */
+  int32_t out_dim;            /* rows of each head's w_uv (e.g. v_head_dim) */
+  int32_t pad0;
+  void *out;                  /* [T, heads, out_dim] = W_uv,h (sum_i p_i c_i)
+                                 with w_uv, else [T, heads, value_dim] */
   void *workspace;            /* nfa_mla_attn_workspace_bytes(), zero-filled
                                  once; counters are left at zero */
   int64_t workspace_bytes;

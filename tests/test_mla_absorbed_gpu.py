@@ -79,9 +79,14 @@ def _decode_rows(cache, b, gen):
 # the attention kernel
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize('rank,out_dtype', [(512, torch.bfloat16), (512, torch.float32),
-                                            (64, torch.float32)])
-def test_mla_attention_kernel_matches_oracle(rank, out_dtype):
+@pytest.mark.parametrize('rank,out_dtype,project', [
+    (512, torch.bfloat16, False), (512, torch.float32, False), (64, torch.float32, False),
+    (512, torch.float32, True), (512, torch.bfloat16, True), (64, torch.float32, True)])
+def test_mla_attention_kernel_matches_oracle(rank, out_dtype, project):
+    """The latent kernel against the float64 latent oracle; with ``project``
+    the head-wise value up-projection (128 rows of ``rank`` dims per head)
+    fused into its last step, against the oracle's result projected in
+    float64."""
     gen = torch.Generator(device=GPU).manual_seed(rank)
     page, pages, heads, rows, width = 16, 300, HEADS, 3, 1024
     cache = GraphReadyPagedRegionCache(
@@ -102,14 +107,20 @@ def test_mla_attention_kernel_matches_oracle(rank, out_dtype):
     vis = vis.to(torch.int32).contiguous()
     q2r = torch.tensor([2, -1, 0, 1], dtype=torch.int32, device=GPU)  # a padding row
     q = (torch.randn(4, heads, rank + 64, generator=gen, device=GPU) * 0.05).to(torch.bfloat16)
-    print(f'# mla attention rank={rank} out={out_dtype}', flush=True)
+    w_uv = None
+    if project:
+        w_uv = (torch.randn(heads, VDIM, rank, generator=gen, device=GPU)
+                * rank ** -0.5).to(torch.bfloat16)
+    print(f'# mla attention rank={rank} out={out_dtype} project={project}', flush=True)
     out = sparse_mla_attention_gather(layer, q, gather.contiguous(), vis, q2r,
-                                      scale=SCALE, out_dtype=out_dtype)
+                                      scale=SCALE, out_dtype=out_dtype, w_uv=w_uv)
     torch.cuda.synchronize()
     want = orc.mla_sparse_attention(layer.kv_pool_k.float().cpu().numpy(),
                                     q.float().cpu().numpy(), gather.cpu().numpy(),
                                     vis.cpu().numpy(), q2r.cpu().numpy(), SCALE, page,
                                     rank)
+    if project:
+        want = np.einsum('thr,hvr->thv', want, w_uv.double().cpu().numpy())
     got = out.float().cpu().numpy()
     assert (got[1] == 0).all()
     if out_dtype == torch.bfloat16:
@@ -229,12 +240,11 @@ def test_dsv2_lite_layer_4_requests_64k_latent_and_expanded():
             np.testing.assert_array_equal(lat_g[r, h, :n], exp_g[r, h, :n])
     print('# DSV2-Lite expanded selections equal the latent ones', flush=True)
     # attention: both against float64 attention over the expanded heads
-    o_lat = sparse_mla_attention_gather(
+    # (the head-wise W_uv up-projection fused into the latent kernel)
+    out_lat = sparse_mla_attention_gather(
         lat.layers[0], q_lat, lat.gather_indices_for_layer(0),
         lat.visible_lens_for_layer(0), lat.query_to_req_buf, scale=SCALE,
-        out_dtype=torch.float32)
-    out_lat = torch.bmm(o_lat.transpose(0, 1).contiguous(),
-                        w_uv.float().transpose(1, 2).contiguous()).transpose(0, 1)
+        out_dtype=torch.float32, w_uv=w_uv)
     out_exp = sparse_paged_attention_gather(
         exp.layers[0], q_exp, exp.gather_indices_for_layer(0),
         exp.visible_lens_for_layer(0), exp.query_to_req_buf, scale=SCALE)

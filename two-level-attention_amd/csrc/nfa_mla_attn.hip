@@ -7,14 +7,18 @@
 // selection):
 //   s_i = scale * (q_h . K_i),  q_h = [W_uk,h^T q_nope,h | q_pe,h]
 //   o_h = sum_i softmax(s)_i * K_i[0 : value_dim]
-// and the caller applies the head's value up-projection W_uv,h to o_h.  The
+// and, given w_uv, the head's value up-projection W_uv,h o_h is written
+// instead of o_h (fused into the merge: no second launch).  The
 // same attention as DeepseekV2Attention over its expanded heads (reference
 // v1 tree sparse_attn/patches/deepseek_v2_attn_patch.py, transformers'
 // expand_kv): q_nope . (W_uk c) = (W_uk^T q_nope) . c and
 // sum_i p_i (W_uv c_i) = W_uv (sum_i p_i c_i), up to rounding.
 //
-// Grid nsplit x rows (rows = T * heads, one gather row per head), in the
-// XCD-aware order of the gather attention: a row's splits run on one XCD.
+// Grid nsplit x rows (rows = T * heads, one gather row per head).  Workgroups
+// go round-robin over the XCDs in linear id order; each XCD takes a
+// contiguous block of rows (query-row major), so a row's splits, and the
+// heads of one query row, which share their sink / window rows and part of
+// their middles, run on one XCD and share its L2.
 // A workgroup takes the chunks split, split + nsplit, ... of 32 selected
 // slots; 8 threads share a latent row, each holding CK 16-byte chunks of it
 // (its first CV chunks are value dims), so one read of the row serves the
@@ -35,12 +39,13 @@ struct MlaDims {
   int64_t w_cnt, w_part, w_total;
 };
 
-// Rows get as many split workgroups as keep about two workgroups per CU busy.
+// Rows get as many split workgroups as keep about four workgroups per CU
+// busy (35 KB of LDS each at 576-dim rows).
 __host__ __device__ inline MlaDims mla_dims(const NfaMlaAttnParams &p, int cus) {
   MlaDims a;
   a.rows = p.total_q * p.heads;
   int cap = kMlaMaxSplits;
-  const int want = a.rows > 0 ? (2 * cus + a.rows - 1) / a.rows : 1;
+  const int want = a.rows > 0 ? (4 * cus + a.rows - 1) / a.rows : 1;
   if (want < cap) cap = want;
   a.nsplit = (p.max_vis + kMlaSplit - 1) / kMlaSplit;
   if (a.nsplit > cap) a.nsplit = cap;
@@ -60,6 +65,65 @@ __device__ __forceinline__ void store_out(const NfaMlaAttnParams &p, int64_t i, 
     ((float *)p.out)[i] = v;
 }
 
+// The head's output from its DV-dim result in LDS: W_uv,h s_o (out_dim
+// values) with the up-projection, else s_o itself.  8 lanes share a weight
+// row (lane sc takes the row's 16-byte chunks sc, sc + 8, ..., so one load
+// of the 8 lanes is one whole 128-byte line), U rows in flight per lane;
+// the 8 partial sums meet in sum8.
+template <int DV>
+__device__ __forceinline__ void mla_write_out(const NfaMlaAttnParams &p, int t, int h,
+                                              const float *s_o) {
+  if (p.w_uv == nullptr) {
+    for (int d = threadIdx.x; d < DV; d += NFA_BLOCK)
+      store_out(p, ((int64_t)t * p.heads + h) * DV + d, s_o[d]);
+    return;
+  }
+  constexpr int CH = 8;                          // bf16 per 16-byte chunk
+  constexpr int CV = DV / (CH * kMlaTpr);        // chunks per lane and row
+  constexpr int U = CV >= 8 ? 1 : 4;             // rows in flight per lane
+  constexpr int RPP = NFA_BLOCK / kMlaTpr;       // rows per pass of the block
+  const int sc = threadIdx.x % kMlaTpr;
+  const int rr = threadIdx.x / kMlaTpr;
+  const int od = p.out_dim;
+  const uint16_t *w = (const uint16_t *)p.w_uv + (int64_t)h * od * DV;
+  const int64_t ob = ((int64_t)t * p.heads + h) * od;
+  // (rr is uniform over the 8 lanes of a group, so sum8 sees whole groups)
+  for (int o0 = rr; o0 < od; o0 += U * RPP) {
+    uint4 wr[U][CV];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int o = o0 + u * RPP;
+#pragma unroll
+      for (int c = 0; c < CV; ++c)
+        wr[u][c] = o < od ? *reinterpret_cast<const uint4 *>(w + (int64_t)o * DV +
+                                                             (c * kMlaTpr + sc) * CH)
+                          : make_uint4(0u, 0u, 0u, 0u);
+    }
+    float acc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CV; ++c) {
+      const float4 x0 = *reinterpret_cast<const float4 *>(s_o + (c * kMlaTpr + sc) * CH);
+      const float4 x1 = *reinterpret_cast<const float4 *>(s_o + (c * kMlaTpr + sc) * CH + 4);
+      const float x[CH] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float w8[CH];
+        unpack_chunk<uint16_t>(wr[u][c], w8);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) acc[u] = fmaf(w8[e], x[e], acc[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float v = sum8(acc[u]);
+      const int o = o0 + u * RPP;
+      if (sc == 0 && o < od) store_out(p, ob + o, v);
+    }
+  }
+}
+
 // LOOP: a workgroup may own several chunks (rows wider than nsplit chunks).
 template <int CK, int CV, bool LOOP>
 __global__ void __launch_bounds__(NFA_BLOCK)
@@ -71,12 +135,13 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   const MlaDims ad = mla_dims(p, cus);
   const int tid = threadIdx.x;
   const int lane = lane_id();
+  // XCD x = linear % 8 takes rows [x * r8, (x + 1) * r8)
   const int linear = blockIdx.x;
-  const int group = linear / (kMlaXcds * ad.nsplit);
-  const int within = linear % (kMlaXcds * ad.nsplit);
-  const int row = group * kMlaXcds + within % kMlaXcds;
-  const int split = within / kMlaXcds;
-  if (row >= ad.rows) return;
+  const int r8 = (ad.rows + kMlaXcds - 1) / kMlaXcds;
+  const int j = linear / kMlaXcds;
+  const int row = (linear % kMlaXcds) * r8 + j / ad.nsplit;
+  const int split = j % ad.nsplit;
+  if (j / ad.nsplit >= r8 || row >= ad.rows) return;
   const int t = row / p.heads;
   const int h = row % p.heads;
   const float kNegInf = __uint_as_float(0xFF800000u);
@@ -202,18 +267,21 @@ __global__ void __launch_bounds__(NFA_BLOCK)
   }
   // (s_m / s_z were last written before the barrier ahead of P.V, or with
   // no chunk by thread 0 before the first barrier)
+  float *s_o = reinterpret_cast<float *>(s_v);  // the head's result (P.V is done)
   if (LOOP && ad.nsplit == 1) {
     // the whole row in this workgroup: normalise and write the output
+    __syncthreads();  // every thread's P.V reads of s_v are done
 #pragma unroll
     for (int k = 0; k < OPT; ++k) {
       const int o = tid + k * NFA_BLOCK;
       if (o >= DV / 2) break;
       const int d = 2 * o;
       const float z = s_z;
-      const int64_t oi = ((int64_t)t * p.heads + h) * DV + d;
-      store_out(p, oi, z == 0.0f ? 0.0f : acc0[k] / z);
-      store_out(p, oi + 1, z == 0.0f ? 0.0f : acc1[k] / z);
+      s_o[d] = z == 0.0f ? 0.0f : acc0[k] / z;
+      s_o[d + 1] = z == 0.0f ? 0.0f : acc1[k] / z;
     }
+    __syncthreads();
+    mla_write_out<DV>(p, t, h, s_o);
     return;
   }
   // (a single-chunk workgroup stored its P.V above; one with no chunk
@@ -266,10 +334,11 @@ __global__ void __launch_bounds__(NFA_BLOCK)
       }
       M = mb;
     }
-    const int64_t oi = ((int64_t)t * p.heads + h) * DV + d;
-    store_out(p, oi, Z == 0.0f ? 0.0f : O0 / Z);
-    store_out(p, oi + 1, Z == 0.0f ? 0.0f : O1 / Z);
+    s_o[d] = Z == 0.0f ? 0.0f : O0 / Z;
+    s_o[d + 1] = Z == 0.0f ? 0.0f : O1 / Z;
   }
+  __syncthreads();
+  mla_write_out<DV>(p, t, h, s_o);
 }
 
 }  // namespace nfa
@@ -306,6 +375,10 @@ static int32_t check_mla(const NfaMlaAttnParams *p, int *cv_out) {
   }
   if (!p->q || !p->kv_pool || !p->gather || !p->vis_lens || !p->query_to_req || !p->out) {
     nfa_set_error("nfa_mla_attn_decode: null device pointer");
+    return NFA_EINVAL;
+  }
+  if (p->w_uv != nullptr && (p->out_dim <= 0 || p->out_dim > 4096)) {
+    nfa_set_error("nfa_mla_attn_decode: out_dim %d out of range", p->out_dim);
     return NFA_EINVAL;
   }
   *cv_out = cv;

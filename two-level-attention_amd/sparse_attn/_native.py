@@ -89,8 +89,8 @@ class NfaMlaAttnParams(ctypes.Structure):
         ('max_vis', _i32), ('kv_dtype', _i32), ('q_dtype', _i32),
         ('out_dtype', _i32), ('pool_pages', _i32), ('scale', _f32),
         ('q', _ptr), ('kv_pool', _ptr), ('gather', _ptr), ('vis_lens', _ptr),
-        ('query_to_req', _ptr), ('out', _ptr), ('workspace', _ptr),
-        ('workspace_bytes', _i64),
+        ('query_to_req', _ptr), ('w_uv', _ptr), ('out_dim', _i32), ('pad0', _i32),
+        ('out', _ptr), ('workspace', _ptr), ('workspace_bytes', _i64),
     ]
 
 

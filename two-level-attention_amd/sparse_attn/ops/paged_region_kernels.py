@@ -163,7 +163,7 @@ def sparse_paged_attention_gather(cache_layer, q, gather_indices, visible_lens,
 
 def sparse_mla_attention_gather(cache_layer, q, gather_indices, visible_lens,
                                 query_to_req, *, scale, workspace=None,
-                                out_dtype=None):
+                                out_dtype=None, w_uv=None):
     """Absorbed latent attention of each query head over its own selection.
 
     ``cache_layer`` is a latent arena (one kv head, rows of ``head_dim_k`` =
@@ -171,8 +171,10 @@ def sparse_mla_attention_gather(cache_layer, q, gather_indices, visible_lens,
     dims); ``q`` ``[T, H, head_dim_k]`` holds per head ``[W_uk^T q_nope |
     q_pe]``; ``gather_indices`` ``[B, H, W]`` / ``visible_lens`` ``[B, H]``
     are the per-head selections.  Returns ``[T, H, head_dim_v]`` -- each
-    head's softmax-weighted latent rows, before the value up-projection --
-    in ``out_dtype`` (default: the dtype of ``q``).  No reference
+    head's softmax-weighted latent rows -- or, with ``w_uv`` ``[H, V,
+    head_dim_v]`` (bf16, each head's value up-projection), ``[T, H, V]`` =
+    ``W_uv,h`` applied to them, in ``out_dtype`` (default: the dtype of
+    ``q``).  No reference
     counterpart: the reference attends over expanded heads
     (``sparse_paged_attention_gather``), which this equals up to rounding.
     """
@@ -188,8 +190,12 @@ def sparse_mla_attention_gather(cache_layer, q, gather_indices, visible_lens,
     nat.require_hip(q, 'sparse_mla_attention_gather')
     lib = nat.load_library()
     total_q = q.shape[0]
-    out = q.new_empty((total_q, heads, cache_layer.head_dim_v),
-                      dtype=out_dtype or q.dtype)
+    if w_uv is not None:
+        if (w_uv.dtype != torch.bfloat16 or w_uv.ndim != 3 or w_uv.shape[0] != heads
+                or w_uv.shape[2] != cache_layer.head_dim_v or not w_uv.is_contiguous()):
+            raise ValueError('w_uv must be a contiguous bf16 [H, V, head_dim_v] tensor')
+    width = cache_layer.head_dim_v if w_uv is None else w_uv.shape[1]
+    out = q.new_empty((total_q, heads, width), dtype=out_dtype or q.dtype)
     if total_q == 0:
         return out
     qc = q if q.is_contiguous() else q.contiguous()
@@ -215,6 +221,9 @@ def sparse_mla_attention_gather(cache_layer, q, gather_indices, visible_lens,
     p.gather = gather_indices.data_ptr()
     p.vis_lens = visible_lens.data_ptr()
     p.query_to_req = q2r.data_ptr()
+    if w_uv is not None:
+        p.w_uv = w_uv.data_ptr()
+        p.out_dim = w_uv.shape[1]
     p.out = out.data_ptr()
     need = lib.nfa_mla_attn_workspace_bytes(ctypes.byref(p))
     ws = _scratch(workspace, ('nfa_mla_attn_scratch', total_q, heads, p.max_vis,

@@ -89,8 +89,8 @@ def _latent_parts(module, hidden_states, position_embeddings):
 
 
 def absorbed_weights(module):
-    """The head-wise halves of kv_b_proj: W_uk [H, nope, rank] and W_uv^T
-    [H, rank, v], contiguous (cached until the weight changes)."""
+    """The head-wise halves of kv_b_proj: W_uk [H, nope, rank] and W_uv
+    [H, v, rank], contiguous (cached until the weight changes)."""
     w = module.kv_b_proj.weight
     held = module.__dict__.get('_nfa_absorbed')
     if held is not None and held[0] is w and held[1] == w._version:
@@ -99,9 +99,9 @@ def absorbed_weights(module):
     wv = w.detach().view(heads, module.qk_nope_head_dim + module.v_head_dim,
                          module.kv_lora_rank)
     w_uk = wv[:, :module.qk_nope_head_dim, :].contiguous()
-    w_uv_t = wv[:, module.qk_nope_head_dim:, :].transpose(1, 2).contiguous()
-    module._nfa_absorbed = (w, w._version, w_uk, w_uv_t)
-    return w_uk, w_uv_t
+    w_uv = wv[:, module.qk_nope_head_dim:, :].contiguous()
+    module._nfa_absorbed = (w, w._version, w_uk, w_uv)
+    return w_uk, w_uv
 
 
 def absorbed_decode_attention(module, q_nope, q_pe, rows, cache, batch):
@@ -112,7 +112,7 @@ def absorbed_decode_attention(module, q_nope, q_pe, rows, cache, batch):
     from ..ops.paged_region_kernels import sparse_mla_attention_gather
 
     layer_idx = module.layer_idx
-    w_uk, w_uv_t = absorbed_weights(module)
+    w_uk, w_uv = absorbed_weights(module)
     heads = module.num_heads
     # q_abs = W_uk^T q_nope per head: [H, B, nope] x [H, nope, rank] (both
     # operands contiguous)
@@ -123,15 +123,13 @@ def absorbed_decode_attention(module, q_nope, q_pe, rows, cache, batch):
     select_topk_for_layer_batched(
         cache, layer_idx, cache.active_req_ids, q_lat, attention=module,
         decode_write=(keys, None, slot_mapping))
-    o_lat = sparse_mla_attention_gather(
+    # out_h = W_uv,h (sum_i p_i c_i), the up-projection fused into the kernel
+    out = sparse_mla_attention_gather(
         cache.layers[layer_idx], q_lat, cache.gather_indices_for_layer(layer_idx),
         cache.visible_lens_for_layer(layer_idx), cache.query_to_req_buf,
-        scale=module.scaling,
+        scale=module.scaling, w_uv=w_uv,
         workspace=cache.__dict__.setdefault('_nfa_selector_workspace', {}))
-    # out_h = W_uv,h (sum_i p_i c_i): [H, B, rank] x [H, rank, v]
-    out = torch.bmm(o_lat.transpose(0, 1).contiguous(), w_uv_t)
-    out = out.transpose(0, 1).reshape(batch, 1, heads * module.v_head_dim)
-    return module.o_proj(out)
+    return module.o_proj(out.reshape(batch, 1, heads * module.v_head_dim))
 
 
 def deepseek_v2_attn_forward(
