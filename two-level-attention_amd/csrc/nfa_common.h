@@ -242,6 +242,17 @@ __device__ __forceinline__ uint4 pack_chunk(const float *x) {
 // in rows of 7 (each row over several XCDs), 3000 hand-overs of plain stores
 // without the writeback left 2.6 % of the words stale for the last
 // workgroup, these stores none.
+//
+// Why this is the release without its writeback: in LLVM's AMDGPU memory
+// model for GFX942 (gfx950 follows it), an agent-scope release fence is
+// `buffer_wbl2 sc1` (write back the lines this XCD's L2 holds dirty) then
+// `s_waitcnt vmcnt(0)`, and an agent-scope monotonic store is
+// `global_store ... sc1`, which the L2 does not hold dirty.  For data
+// written only through such stores and through atomics the writeback has
+// nothing to write, and the wait is the `s_waitcnt(0)` that arrive_last
+// issues itself; the last arrival still runs the agent-scope acquire
+// (`buffer_inv sc1`) before it reads.  A plain store among the handed-over
+// data breaks this: its writer must arrive with writeback true.
 template <typename T>
 __device__ __forceinline__ void store_coherent(T *p, T v) {
   static_assert(sizeof(T) == 2 || sizeof(T) == 4, "16- or 32-bit elements");
@@ -267,6 +278,13 @@ __device__ __forceinline__ void store_coherent(T *p, T v) {
 // thread of the workgroup that arrives last of `n`; that workgroup has
 // acquired (one agent-scope acquire, then a barrier) and resets the counter,
 // so no memset is needed between launches.  `s_flag` is one int of LDS.
+// Callers without the writeback, and what their last arrival reads:
+//   selector tile -> row tail: the page keys, the per-tile page lists and
+//     their counts, the decode token's K row and L2 side row (all
+//     store_coherent), the row histograms (atomics); a statistics rebuild
+//     writes plain stores and arrives with the writeback;
+//   attention and latent attention splits -> merge: each split's (m, z, acc)
+//     partial (store_coherent).
 __device__ __forceinline__ bool arrive_last(unsigned int *counter,
                                             unsigned int n, int *s_flag,
                                             bool writeback = true) {
