@@ -17,8 +17,10 @@ algorithms; parity tests compare the two bit for bit.
 Declared arithmetic (the reference leaves fp32 reduction order to Triton, so
 the order is declared here and the HIP kernels follow it exactly):
 
-* every fp32 reduction is sequential, index ascending, starting from +0.0,
-  with separately rounded multiply and add (no FMA);
+* every fp32 reduction is sequential, index ascending, starting from +0.0;
+  the selector's dot products (L1 page scores, L2 logits) add each exact
+  product with one rounding (``exact_dot``: a fused multiply-add per term;
+  ``seq_dot``, the rounded-product order, is kept to show the difference);
 * ``bf16r`` is fp32 -> bf16 round-to-nearest-even; any NaN becomes the
   canonical positive quiet NaN 0x7FC0 (NaN then ranks first, as on the
   reference GPU);
@@ -109,6 +111,64 @@ def seq_dot(a, b) -> np.ndarray:
     with np.errstate(invalid='ignore', over='ignore'):
         for d in range(a.shape[-1]):
             acc = (acc + (a[..., d] * b[..., d]).astype(F32)).astype(F32)
+    return acc
+
+
+_F32_OVER = float(2.0 ** 128 - 2.0 ** 103)   # fp32 overflow threshold (max + ulp/2)
+_F32_MAX = float(np.finfo(np.float32).max)
+
+
+def add_exact_f32(acc, p) -> np.ndarray:
+    """fl32(acc + p) with one rounding: ``acc`` fp32, ``p`` an exact value
+    held in float64 (the product of two fp32 values always is).  This is
+    what a fused multiply-add fma(a, b, acc) computes for p = a * b.
+
+    TwoSum gives s + e == acc + p exactly (s, e float64); fp32 rounding of
+    s is the fp32 rounding of s + e unless s lies exactly on a midpoint
+    between two fp32 values (midpoints are float64 numbers, and |e| is
+    below half a float64 ulp of s), where the sign of e breaks the tie."""
+    a = np.asarray(acc, dtype=np.float32).astype(np.float64)
+    p = np.asarray(p, dtype=np.float64)
+    with np.errstate(invalid='ignore', over='ignore'):
+        s = a + p
+        bb = s - a
+        e = (a - (s - bb)) + (p - bb)
+        r = s.astype(np.float32)
+        fin = np.isfinite(s) & (e != 0)
+        if fin.any():
+            r64 = r.astype(np.float64)
+            d = s - r64
+            toward = np.where(d > 0, np.float32(np.inf), np.float32(-np.inf))
+            n = np.nextafter(r, toward.astype(np.float32))
+            mid = fin & np.isfinite(r) & (d != 0) & (2.0 * s == r64 + n.astype(np.float64))
+            r = np.where(mid & (np.sign(e) == np.sign(d)), n, r)
+            # s exactly on the overflow threshold: a negative e keeps the
+            # result finite
+            edge = fin & np.isinf(r) & (np.abs(s) == _F32_OVER) & (np.sign(e) == -np.sign(s))
+            r = np.where(edge, np.sign(s).astype(np.float32) * np.float32(_F32_MAX), r)
+    return np.asarray(r, dtype=np.float32)
+
+
+def exact_dot(a, b) -> np.ndarray:
+    """sum_d a[..., d] * b[..., d] in fp32, d ascending, from +0.0, each
+    exact product added with one rounding: the fused multiply-add chain
+    acc = fma(a_d, b_d, acc) of the selector's dot products.  Where the fp32
+    product is already exact (always for two bf16 values in the normal
+    range) this is the plain fp32 add of that product."""
+    a, b = np.broadcast_arrays(np.asarray(a, dtype=np.float32),
+                               np.asarray(b, dtype=np.float32))
+    acc = np.zeros(a.shape[:-1], dtype=np.float32)
+    with np.errstate(invalid='ignore', over='ignore'):
+        for d in range(a.shape[-1]):
+            x, y = a[..., d], b[..., d]
+            p32 = (x * y).astype(F32)
+            p64 = x.astype(np.float64) * y.astype(np.float64)
+            fast = (acc + p32).astype(F32)
+            ok = p32.astype(np.float64) == p64          # NaN takes the slow path
+            if ok.all():
+                acc = fast
+            else:
+                acc = np.where(ok, fast, add_exact_f32(acc, p64)).astype(F32)
     return acc
 
 
@@ -341,8 +401,8 @@ def l1_top2_scores(cfg: NfaConfig, ksum, q_full_group, q_unrounded_group):
     that value stands."""
     kavg = bf16r((ksum / F32(cfg.bs)).astype(F32))
     with np.errstate(invalid='ignore', over='ignore'):
-        rounded = np.stack([bf16r(seq_dot(kavg, q[None, :])) for q in q_full_group])
-        exact = np.stack([bf16r(seq_dot(kavg, q[None, :])) for q in q_unrounded_group])
+        rounded = np.stack([bf16r(exact_dot(kavg, q[None, :])) for q in q_full_group])
+        exact = np.stack([bf16r(exact_dot(kavg, q[None, :])) for q in q_unrounded_group])
         r1, r2 = top2_values(rounded)
         u1, u2 = top2_values(exact)
         kernel = bf16r(((r1 + r2).astype(F32) / F32(2)).astype(F32))
@@ -365,11 +425,11 @@ def l1_page_scores(cfg: NfaConfig, kmin, kmax, ksum, q_full_group):
     mm_acc = np.zeros(kmin.shape[0], dtype=np.float32)
     avg_acc = np.zeros(kmin.shape[0], dtype=np.float32)
     for j in range(g):
-        s_neg = seq_dot(kmin, qlow[j][None, :])
-        s_pos = seq_dot(kmax, qhigh[j][None, :])
+        s_neg = exact_dot(kmin, qlow[j][None, :])
+        s_pos = exact_dot(kmax, qhigh[j][None, :])
         mm_j = bf16r((s_neg + s_pos).astype(F32))
         mm_acc = (mm_acc + mm_j).astype(F32)
-        avg_j = bf16r(seq_dot(kavg, q_full_group[j][None, :]))
+        avg_j = bf16r(exact_dot(kavg, q_full_group[j][None, :]))
         avg_acc = (avg_acc + avg_j).astype(F32)
     mm = bf16_bits((mm_acc / F32(g)).astype(F32))
     avg = bf16_bits((avg_acc / F32(g)).astype(F32))
@@ -556,7 +616,7 @@ def l2_logits(cfg: NfaConfig, k_pool, bt_row, token, load, q_fine_kv, kv, quota)
                           cfg.page, cfg.max_blocks)
     if cfg.l2_quant:
         vals = fake_quant4(vals)
-    logit = bf16_bits(seq_dot(vals, q_fine_kv[None, :]))
+    logit = bf16_bits(exact_dot(vals, q_fine_kv[None, :]))
     logit = np.where(logit == NAN_BITS, NEG_INF_BITS, logit)
     out[idx] = logit
     return out

@@ -86,6 +86,94 @@ def test_seq_dot_is_ascending_fp32_without_fma():
     np.testing.assert_array_equal(orc.seq_sum(ints), ints.astype(np.int64).sum(0).astype(F32))
 
 
+def _round_f32_exact(x):
+    """Round a Fraction to fp32, round-to-nearest-even, with denormals and
+    overflow to inf, by integer arithmetic alone (no float rounding)."""
+    from fractions import Fraction
+    if x == 0:
+        return F32(0.0)
+    sign = -1 if x < 0 else 1
+    a = abs(x)
+    # exponent E with 2^E <= a < 2^(E+1)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    q = max(e, -126) - 23                 # the fp32 grid spacing at a
+    m = a / Fraction(2) ** q              # a in units of the spacing
+    n, r = divmod(m.numerator, m.denominator)
+    twice = 2 * r
+    if twice > m.denominator or (twice == m.denominator and n % 2 == 1):
+        n += 1
+    val = Fraction(n) * Fraction(2) ** q
+    if val >= Fraction(2) ** 128:
+        return F32(sign * np.inf)
+    return F32(sign * float(val))
+
+
+def test_exact_dot_is_the_fused_multiply_add_chain():
+    """exact_dot equals the sequential chain acc = round(acc + a*b) computed
+    in exact rational arithmetic, on random fp32 vectors with exponents
+    spread over the whole range (products that fp32 cannot hold, denormals,
+    cancellations), against rounding done by integers alone."""
+    from fractions import Fraction
+    rng = np.random.default_rng(41)
+    n, d = 300, 12
+    mant = rng.uniform(1.0, 2.0, (2, n, d))
+    ex = rng.integers(-75, 60, (2, n, d))
+    sgn = rng.choice([-1.0, 1.0], (2, n, d))
+    vals = (sgn * mant * np.exp2(ex)).astype(F32)
+    vals[0, :40] = orc.bf16r(vals[0, :40])          # bf16 operands too
+    vals[1, :40] = orc.bf16r(vals[1, :40])
+    vals[0, 40:60, 3] = -vals[0, 40:60, 2]          # cancellations
+    vals[1, 40:60, 3] = vals[1, 40:60, 2]
+    a, b = vals
+    got = orc.exact_dot(a, b)
+    for i in range(n):
+        acc = F32(0.0)
+        for k in range(d):
+            exact = Fraction(float(acc)) + Fraction(float(a[i, k])) * Fraction(float(b[i, k]))
+            acc = _round_f32_exact(exact)
+        assert got[i].tobytes() == acc.tobytes(), (i, got[i], acc)
+
+
+def test_exact_dot_ties_overflow_and_specials():
+    """The single rounding where a float64 sum would round twice: acc + p on
+    an fp32 midpoint in float64 but off it exactly (both directions), the
+    overflow threshold, the fused closed form, and inf / NaN / zero terms."""
+    one = F32(1.0)
+    # true value just above the midpoint 1 + 2^-24: rounds up (ties-to-even
+    # of the float64 sum would give 1)
+    assert orc.add_exact_f32(one, 2.0 ** -24 + 2.0 ** -70) == F32(1 + 2.0 ** -23)
+    assert F32(1.0 + (2.0 ** -24 + 2.0 ** -70)) == one
+    # just below the midpoint between 1 + 2^-23 and 1 + 2^-22: rounds down
+    lo = F32(1 + 2.0 ** -23)
+    assert orc.add_exact_f32(lo, 2.0 ** -24 - 2.0 ** -70) == lo
+    assert F32(np.float64(lo) + (2.0 ** -24 - 2.0 ** -70)) == F32(1 + 2.0 ** -22)
+    # exactly on the overflow threshold in float64, below it exactly
+    fmax = F32(np.finfo(F32).max)
+    assert orc.add_exact_f32(fmax, 2.0 ** 103 - 2.0 ** 50) == fmax
+    with np.errstate(over='ignore'):
+        assert np.isinf(F32(np.float64(fmax) + (2.0 ** 103 - 2.0 ** 50)))
+    assert np.isinf(orc.add_exact_f32(fmax, 2.0 ** 103))
+    # fused: (1 + 2^-12)^2 - (1 + 2^-11) keeps the 2^-24 a rounded product loses
+    a = F32(1 + 2.0 ** -12)
+    got = orc.exact_dot(np.array([-(1 + 2.0 ** -11), a], dtype=F32),
+                        np.array([1, a], dtype=F32))
+    assert got == F32(2.0 ** -24)
+    assert orc.seq_dot(np.array([-(1 + 2.0 ** -11), a], dtype=F32),
+                       np.array([1, a], dtype=F32)) == F32(0)
+    # inf * 0 is NaN, inf survives, zeros keep +0
+    assert np.isnan(orc.exact_dot(np.array([np.inf, 1], dtype=F32), np.array([0, 1], dtype=F32)))
+    assert orc.exact_dot(np.array([np.inf, 1], dtype=F32), np.array([2, 1], dtype=F32)) == np.inf
+    z = orc.exact_dot(np.array([-1, 0], dtype=F32), np.array([0, 5], dtype=F32))
+    assert z == 0 and not np.signbit(z)
+    # integers: exact whatever the order of rounding
+    ints = np.random.default_rng(4).integers(-50, 50, (7, 33)).astype(F32)
+    w = np.random.default_rng(5).integers(-5, 5, (33,)).astype(F32)
+    np.testing.assert_array_equal(orc.exact_dot(ints, w),
+                                  (ints.astype(np.int64) @ w.astype(np.int64)).astype(F32))
+
+
 # ---------------------------------------------------------------------------
 # page statistics and query preparation
 # ---------------------------------------------------------------------------

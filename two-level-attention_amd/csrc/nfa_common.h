@@ -1,9 +1,12 @@
 // Device helpers shared by the NFA selector and attention kernels (gfx950).
 //
 // Arithmetic contract (shared with the CPU oracle): fp32 reductions are
-// sequential, index ascending, from +0.0, with separately rounded multiply and
-// add.  This file is compiled with -ffp-contract=off and additionally turns
-// contraction off with a pragma so no FMA is formed behind our back.
+// sequential, index ascending, from +0.0.  The selector's dot products (L1
+// page scores, L2 logits) add each exact product with one rounding, an
+// explicit fused multiply-add per term; every other product is rounded
+// before its add.  This file is compiled with -ffp-contract=off and
+// additionally turns contraction off with a pragma, so the only FMAs are the
+// explicit ones.
 #pragma once
 #pragma clang fp contract(off)
 

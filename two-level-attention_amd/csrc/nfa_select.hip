@@ -89,7 +89,7 @@ struct SelDims {
   int a_ctx;  // the row state wave 0 hands to the other waves
   int a_hist, a_tmp, a_misc, a_clk, a_qf, a_qs, a_qu, a_qg, a_fdims;
   int a_dims, a_last, a_tphys, a_stage, a_hs, a_st, a_st2;  // tile
-  int a_tkeys;    // the tile's page keys (its survivors are listed from them)
+  int a_tkeys;    // the tile's page keys over its passes (multi-pass tiles)
   int a_pages, a_pphys;                                // tail
   int sc;         // survivors the tail holds in LDS (more: every key is read)
   int a_keys, a_dbf, a_dbn, a_dsel;                    // tail, L1
@@ -170,7 +170,7 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   if (stats_staged(p)) o += 2 * (32 / 8) * kSpanMax * 16;
   s.a_st2 = o;         // the next pass's, staged while this one is scored
   if (stats_staged(p) && s.multi) o += 2 * (32 / 8) * kSpanMax * 16;
-  s.a_tkeys = o; if (s.surv) o += align16(2 * kTileMax);
+  s.a_tkeys = o; if (s.multi) o += align16(2 * kTileMax);
   const int a_tile = o;
   o = a_base;
   s.a_pages = o; o += align16(4 * s.np);
@@ -796,10 +796,12 @@ __device__ __forceinline__ void lds_dma4(const void *src, uint32_t lds) {
 // fills 64 consecutive pages of one (slot, chunk) row per copy; pages outside
 // both pools are not copied.  Complete at the issuing wave's next vmcnt(0)
 // wait (see lds_dma16).
+// Waves w0, w0 + 1, ... (nw of them) issue the copies.
 __device__ __forceinline__ void stage_stats_async(const NfaSelectParams &p,
                                                   const RowGeo &g, int64_t req,
                                                   int kv, int t0, int t1,
-                                                  unsigned char *s_st) {
+                                                  unsigned char *s_st, int w0 = 0,
+                                                  int nw = SW) {
   constexpr int NC = 32 / 8;
   const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
   const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
@@ -813,7 +815,8 @@ __device__ __forceinline__ void stage_stats_async(const NfaSelectParams &p,
   const uint32_t lds0 = lds_addr(s_st);
   const int nblk = (t1 - t0 + 63) / 64;
   // units (chunk, 64-page block), both slots per unit
-  for (int u = wave_id(); u < NC * nblk; u += SW) {
+  if (wave_id() < w0) return;
+  for (int u = wave_id() - w0; u < NC * nblk; u += nw) {
     const int c = u / nblk;
     const int blk = u % nblk;
     const int t = t0 + blk * 64 + lane_id();
@@ -842,8 +845,8 @@ static_assert(GMAX * kSpanMax * 4 <= 4 * SB * kStatTokens,
 // the split query qs = [min(q,0) | max(q,0)], and bf16(Σ_d kmean_d·q_d)
 // for avg pools (kmean_d = bf16(ksum_d / bs), the stored statistic), from
 // the query qf (and, with qu, the same mean against the unrounded query into
-// *un); every sum sequential in ascending d with separately rounded
-// products.
+// *un); every sum sequential in ascending d, each exact product added with
+// one rounding (a fused multiply-add per term).
 __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs,
                                                 const float *qf, const float *qu,
                                                 bool need_mm, float *un) {
@@ -860,10 +863,8 @@ __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs
       load_f8(qs + 32 + c * 8, hp);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float a = lo[e] * ln[e];
-        const float b = hi[e] * hp[e];
-        sn = sn + a;
-        sp = sp + b;
+        sn = __builtin_fmaf(lo[e], ln[e], sn);
+        sp = __builtin_fmaf(hi[e], hp[e], sp);
       }
     }
     r = sn + sp;
@@ -875,23 +876,82 @@ __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs
       unpack_chunk<uint16_t>(st[c * kSpanMax], k);
       load_f8(qf + c * 8, q);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float a = k[e] * q[e];
-        sa = sa + a;
-      }
+      for (int e = 0; e < 8; ++e) sa = __builtin_fmaf(k[e], q[e], sa);
       if (qu != nullptr) {
         load_f8(qu + c * 8, q);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float a = k[e] * q[e];
-          su = su + a;
-        }
+        for (int e = 0; e < 8; ++e) su = __builtin_fmaf(k[e], q[e], su);
       }
     }
     r = sa;
   }
   *un = bf16r(su);
   return bf16r(r);
+}
+
+// The page's G head scores in head order, summed from +0 (the group's
+// score before the division by G): the same per-head arithmetic as
+// l1_head_staged, for one page per lane.  qs / qf are the first head's rows
+// (strides QS / QF floats); every lane reads the same query address, so
+// those reads are LDS broadcasts.
+template <int QF, int QS>
+__device__ __forceinline__ float l1_group_staged(const uint4 *st, const float *qs,
+                                                 const float *qf, int G, bool need_mm) {
+  constexpr int NC = 32 / 8;
+  float acc = 0.0f;
+  // heads in pairs: four (minmax) or two (avg) independent sums in flight,
+  // a chunk of statistics unpacked per pair (few registers live)
+  if (need_mm) {
+#pragma unroll 1
+    for (int j = 0; j < G; j += 2) {
+      const bool two = j + 1 < G;  // uniform
+      const float *q0 = qs + j * QS;
+      const float *q1 = two ? q0 + QS : q0;
+      float sn0 = 0.0f, sp0 = 0.0f, sn1 = 0.0f, sp1 = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        float lo[8], hi[8], n0[8], p0[8], n1[8], p1[8];
+        unpack_chunk<uint16_t>(st[c * kSpanMax], lo);
+        unpack_chunk<uint16_t>(st[(NC + c) * kSpanMax], hi);
+        load_f8(q0 + c * 8, n0);
+        load_f8(q0 + 32 + c * 8, p0);
+        load_f8(q1 + c * 8, n1);
+        load_f8(q1 + 32 + c * 8, p1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          sn0 = __builtin_fmaf(lo[e], n0[e], sn0);
+          sp0 = __builtin_fmaf(hi[e], p0[e], sp0);
+          sn1 = __builtin_fmaf(lo[e], n1[e], sn1);
+          sp1 = __builtin_fmaf(hi[e], p1[e], sp1);
+        }
+      }
+      acc = acc + bf16r(sn0 + sp0);
+      if (two) acc = acc + bf16r(sn1 + sp1);
+    }
+  } else {
+#pragma unroll 1
+    for (int j = 0; j < G; j += 2) {
+      const bool two = j + 1 < G;
+      const float *q0 = qf + j * QF;
+      const float *q1 = two ? q0 + QF : q0;
+      float sa0 = 0.0f, sa1 = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        float k[8], v0[8], v1[8];
+        unpack_chunk<uint16_t>(st[c * kSpanMax], k);
+        load_f8(q0 + c * 8, v0);
+        load_f8(q1 + c * 8, v1);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          sa0 = __builtin_fmaf(k[e], v0[e], sa0);
+          sa1 = __builtin_fmaf(k[e], v1[e], sa1);
+        }
+      }
+      acc = acc + bf16r(sa0);
+      if (two) acc = acc + bf16r(sa1);
+    }
+  }
+  return acc;
 }
 
 // Same arithmetic with the statistics read chunk by chunk from memory (L1
@@ -931,19 +991,13 @@ __device__ __forceinline__ void l1_head_mem(const NfaSelectParams &p,
       if (need_mm) {
         const float ql = qd < 0.0f ? qd : 0.0f;
         const float qh = qd > 0.0f ? qd : 0.0f;
-        const float a = kmin[e] * ql;
-        const float b = kmax[e] * qh;
-        sn = sn + a;
-        sp = sp + b;
+        sn = __builtin_fmaf(kmin[e], ql, sn);
+        sp = __builtin_fmaf(kmax[e], qh, sp);
       }
       if (need_avg) {
         const float kavg = ks[e];
-        const float a = kavg * qd;
-        sa = sa + a;
-        if (qu != nullptr) {
-          const float b = kavg * qu[c * CH + e];
-          su = su + b;
-        }
+        sa = __builtin_fmaf(kavg, qd, sa);
+        if (qu != nullptr) su = __builtin_fmaf(kavg, qu[c * CH + e], su);
       }
     }
   }
@@ -1621,10 +1675,14 @@ __global__ void __launch_bounds__(SB)
       do_stats && incremental && owns_last && writer && p.l2_keys_l != nullptr;
   // (only the waves holding a written element take part: the index
   // arithmetic is uniform, and run by every wave it would cost each SIMD
-  // four times its scalar issue slots)
+  // four times its scalar issue slots.  With one lane per page the scores
+  // of a pass take the first four or five waves, so the owner's elements go
+  // to waves 8 and up, otherwise idle; owner lane o = tid - 64 * kOwnerWave)
+  constexpr int kOwnerWave = STG && !TOP2 ? 8 : 0;
+  const int otid = tid - 64 * kOwnerWave;
   const bool owner_any =
-      (dw || owner_late || side_late) &&
-      wave_id() * 64 < imax(imax(p.head_dim, p.head_dim_v), imax(DSUB, p.fine_dsub));
+      (dw || owner_late || side_late) && wave_id() >= kOwnerWave &&
+      (wave_id() - kOwnerWave) * 64 < imax(imax(p.head_dim, p.head_dim_v), imax(DSUB, p.fine_dsub));
   KV dw_k = 0, dw_v = 0, side_raw = 0;
   float ap_mn = __uint_as_float(0x7F800000u);  // a new page starts from +inf,
   float ap_mx = __uint_as_float(0xFF800000u);  // -inf and 0
@@ -1634,15 +1692,15 @@ __global__ void __launch_bounds__(SB)
       // decode write of the current token (selector:1030-1061)
       const int phys = slot_b / p.page;
       const int off = slot_b % p.page;
-      if (tid < p.head_dim) store_coherent(&((KV *)p.k_pool_l)[kv_offset(p, phys, kv, off) + tid], dw_k);
-      if (tid < p.head_dim_v && p.v_new != nullptr)
+      if (otid < p.head_dim) store_coherent(&((KV *)p.k_pool_l)[kv_offset(p, phys, kv, off) + otid], dw_k);
+      if (otid < p.head_dim_v && p.v_new != nullptr)
         ((KV *)p.v_pool_l)[(((int64_t)phys * p.kv_heads_mem + kv) * p.page + off) *
-                               p.head_dim_v + tid] = dw_v;
+                               p.head_dim_v + otid] = dw_v;
     }
-    if (owner_late && tid < DSUB) {
+    if (owner_late && otid < DSUB) {
       // the token's dims continue the page's min / max exactly and the fp32
       // running sum sequentially (selector:32-131)
-      const int64_t si = stat_index<KV>(p, req, kv, tid, last_blk, DSUB);
+      const int64_t si = stat_index<KV>(p, req, kv, otid, last_blk, DSUB);
       const float x = ap_x;
       const float mn = (x < ap_mn) ? x : ap_mn;
       const float mx = (x > ap_mx) ? x : ap_mx;
@@ -1650,37 +1708,37 @@ __global__ void __launch_bounds__(SB)
       ((KV *)p.stat_min_l)[si] = (KV)Elem<KV>::from_f32(mn);
       ((KV *)p.stat_max_l)[si] = (KV)Elem<KV>::from_f32(mx);
       ((KV *)p.stat_sum_l)[si] = page_mean<KV>(sm, p.bs);
-      p.page_sum_l[(req * p.kv_heads_mem + kv) * DSUB + tid] = sm;
+      p.page_sum_l[(req * p.kv_heads_mem + kv) * DSUB + otid] = sm;
     }
-    if (side_late && tid < p.fine_dsub) {
+    if (side_late && otid < p.fine_dsub) {
       // the new token's L2 side row (its 4-bit codes: lanes 0-31 of wave 0)
       if (p.l2_quant) {
-        q4_store_lanes(p, req, kv, L - 1, Elem<KV>::load(&side_raw), tid);
+        q4_store_lanes(p, req, kv, L - 1, Elem<KV>::load(&side_raw), otid);
       } else {
-        store_coherent(&((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, tid)], side_raw);
+        store_coherent(&((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, otid)], side_raw);
       }
     }
   };
   auto owner_prefetch = [&]() {
     if (dw) {
       const int64_t nb = (int64_t)b * p.kv_heads_mem + kv;
-      if (tid < p.head_dim) dw_k = ((const KV *)p.k_new)[nb * p.head_dim + tid];
-      if (tid < p.head_dim_v && p.v_new != nullptr)
-        dw_v = ((const KV *)p.v_new)[nb * p.head_dim_v + tid];
+      if (otid < p.head_dim) dw_k = ((const KV *)p.k_new)[nb * p.head_dim + otid];
+      if (otid < p.head_dim_v && p.v_new != nullptr)
+        dw_v = ((const KV *)p.v_new)[nb * p.head_dim_v + otid];
     }
     const KV *trow = new_row != nullptr
                          ? new_row
                          : kpool + kv_offset(p, last_phys, kv, (L - 1) % p.page);
-    if (owner_late && tid < DSUB) {
+    if (owner_late && otid < DSUB) {
       if ((L - 1) % bs != 0) {
-        const int64_t si = stat_index<KV>(p, req, kv, tid, last_blk, DSUB);
+        const int64_t si = stat_index<KV>(p, req, kv, otid, last_blk, DSUB);
         ap_mn = Elem<KV>::load((const KV *)p.stat_min_l + si);
         ap_mx = Elem<KV>::load((const KV *)p.stat_max_l + si);
-        ap_sm = p.page_sum_l[(req * p.kv_heads_mem + kv) * DSUB + tid];
+        ap_sm = p.page_sum_l[(req * p.kv_heads_mem + kv) * DSUB + otid];
       }
-      ap_x = Elem<KV>::load(trow + s_dims[tid]);
+      ap_x = Elem<KV>::load(trow + s_dims[otid]);
     }
-    if (side_late && tid < p.fine_dsub) side_raw = trow[s_fdims[tid]];
+    if (side_late && otid < p.fine_dsub) side_raw = trow[s_fdims[otid]];
   };
   const RowGeo geo = ctx_geo(s_ctx, L, !skip_far, !skip_near);
   float *s_hs = (float *)(smem + sd.a_hs);  // [head][page] bf16 head scores
@@ -1785,12 +1843,58 @@ __global__ void __launch_bounds__(SB)
     NFA_MARK(0, 3);
     if (kFirst && owner_any) owner_prefetch();
     if constexpr (STG && MULTI) {
-      // every wave has finished the previous pass, which read nst
+      // every wave has finished the previous pass, which read nst; with one
+      // lane per page the copies come from waves 8-15, which score nothing
+      constexpr int w0 = TOP2 ? 0 : 8;
       if (n0 < n1 && !(do_stats && !incremental))
-        stage_stats_async(p, geo, req, kv, n0, n1, nst);
+        stage_stats_async(p, geo, req, kv, n0, n1, nst, w0, SW - w0);
     }
 
     // ---- L1 scores, group means, keys and high-byte histograms -----------
+    // a page's group key: published, counted in the tile's histograms (a
+    // page belongs to at most one pool: far pages lie below near_start,
+    // near pages at or above it).  Multi-pass tiles keep their keys in LDS
+    // and write them out after the last pass: a store issued in a pass
+    // would be waited for by the next pass's staging wait (vmcnt counts
+    // stores), its full write-through latency on every pass.
+    auto publish = [&](int t, uint16_t far_bits, uint16_t near_bits) {
+      if (NFA_COLD(p.dbg_far != nullptr)) {
+        p.dbg_far[(int64_t)row * mb + t] = far_bits;
+        p.dbg_near[(int64_t)row * mb + t] = near_bits;
+      }
+      const uint32_t fk = score_key(far_bits);
+      const uint32_t nk = score_key(near_bits);
+      if constexpr (MULTI)
+        s_tkeys[t - t0] = (uint16_t)(fk ? fk : nk);
+      else
+        store_coherent(&g_keys[t], (uint16_t)(fk ? fk : nk));
+      if (fk) atomicAdd(&s_hist[fk >> 8], 1);
+      if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
+    };
+    if constexpr (STG && !TOP2) {
+      // One lane per page, 64 pages per wave and round: the lane reads and
+      // unpacks its page's statistics once and scores the G heads in order
+      // against query rows read as LDS broadcasts, so a page costs one
+      // unpack, one pool test and one key instead of one per head lane; the
+      // 256 pages of a pass take four waves, one per SIMD.
+      for (int base = wave_id() * 64; base < c1 - c0; base += SW * 64) {
+        const int lp = base + lane_id();
+        const int t = c0 + lp;
+        bool fp = false, np = false;
+        if (do_stats && t < c1) pools(p, geo, t, &fp, &np);
+        uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
+        if (fp || np) {
+          const bool need_mm = (fp && far_mm) || (np && near_mm);
+          const uint4 *su = reinterpret_cast<const uint4 *>(st) + lp;
+          const float acc = l1_group_staged<QF, QS>(su, s_qs, s_qf, G, need_mm);
+          // bf16 head scores summed in head order, then the group mean
+          const uint16_t mean = bf16_bits(acc / (float)G);
+          if (fp) far_bits = mean;
+          if (np) near_bits = mean;
+        }
+        if (t < c1) publish(t, far_bits, near_bits);
+      }
+    } else {
     // lpp lanes per page (one per query head of the group, padded to a
     // power of two), 64 / lpp pages per wave and round: each lane scores one
     // head of its page into s_hs, then the page's first lane combines the
@@ -1836,19 +1940,9 @@ __global__ void __launch_bounds__(SB)
           if (fp) far_bits = mean;
           if (np) near_bits = mean;
         }
-        if (NFA_COLD(p.dbg_far != nullptr)) {
-          p.dbg_far[(int64_t)row * mb + t] = far_bits;
-          p.dbg_near[(int64_t)row * mb + t] = near_bits;
-        }
-        // a page belongs to at most one pool: far pages lie below near_start,
-        // near pages at or above it
-        const uint32_t fk = score_key(far_bits);
-        const uint32_t nk = score_key(near_bits);
-        store_coherent(&g_keys[t], (uint16_t)(fk ? fk : nk));
-        if constexpr (SURV) s_tkeys[t - t0] = (uint16_t)(fk ? fk : nk);
-        if (fk) atomicAdd(&s_hist[fk >> 8], 1);
-        if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
+        publish(t, far_bits, near_bits);
       }
+    }
     }
     // the owner's decode write, statistics append and L2 side row, once:
     // the loaded values are dead before any further pass
@@ -1878,6 +1972,9 @@ __global__ void __launch_bounds__(SB)
         nst = tmp;
         run_pass(std::false_type{}, c0, c1, st, c1, c1 < t1 ? pass_end(c1, t1) : c1, nst);
       }
+      // the tile's keys out to the workspace for the row's tail (the last
+      // pass's barrier ordered every key's LDS write before these reads)
+      for (int i = tid; i < t1 - t0; i += SB) store_coherent(&g_keys[t0 + i], s_tkeys[i]);
     }
   }
   // ---- survivors: a key below the tile's own K-th largest key (of its
@@ -2487,8 +2584,9 @@ __global__ void __launch_bounds__(SB)
   __syncthreads();  // the L1 part of the tail LDS is dead from here
   NFA_MARK(32, 6);
 
-  // ---- L2 logits (selector:423-516): fp32 dot over the L2 dims in order, --
-  //      the dense slots of the candidate pages, SPT per thread in flight
+  // ---- L2 logits (selector:423-516): fp32 dot over the L2 dims in order --
+  //      (a fused multiply-add per dim), the dense slots of the candidate
+  //      pages, SPT per thread in flight
   uint16_t *s_dk = (uint16_t *)(smem + sd.a_dk);
   const int n_dense = np_u * bs;
   {
@@ -2555,8 +2653,7 @@ __global__ void __launch_bounds__(SB)
           const float c = (float)((w4[d / 8] >> (4 * (d % 8))) & 15u);
           // a NaN here (non-finite keys) still ends as a NaN logit
           const float dq = bf16r_hw(bf16r_hw(c * sc) - zr);
-          const float prod = dq * s_qg[d0 + d];
-          acc = acc + prod;
+          acc = __builtin_fmaf(dq, s_qg[d0 + d], acc);
         }
         return acc;
       };
@@ -2635,8 +2732,7 @@ __global__ void __launch_bounds__(SB)
             unpack_chunk<KV>(r[c], x);
 #pragma unroll
             for (int e = 0; e < CH; ++e) {
-              const float prod = x[e] * qv[c * CH + e];
-              acc = acc + prod;
+              acc = __builtin_fmaf(x[e], qv[c * CH + e], acc);
             }
           }
         } else if (nch > 0) {
@@ -2644,14 +2740,12 @@ __global__ void __launch_bounds__(SB)
             float x[CH];
             load_chunk<KV>(kr + choff(c), x);
             for (int e = 0; e < CH; ++e) {
-              const float prod = x[e] * s_qg[c * CH + e];
-              acc = acc + prod;
+              acc = __builtin_fmaf(x[e], s_qg[c * CH + e], acc);
             }
           }
         } else {
           for (int d = 0; d < p.fine_dsub; ++d) {
-            const float prod = Elem<KV>::load(kr + eoff(d)) * s_qg[d];
-            acc = acc + prod;
+            acc = __builtin_fmaf(Elem<KV>::load(kr + eoff(d)), s_qg[d], acc);
           }
         }
       }
