@@ -943,7 +943,7 @@ def mla_layer_bench(torch, args, device):
     mode, layers, b, ctx = args.mla, args.layers, 4, 65536
     h, rank, rope, nope, dv = MLA_HEADS, MLA_RANK, MLA_ROPE, MLA_NOPE, MLA_V
     page = 16
-    new_tokens = 2 * args.kernel_rounds + 8
+    new_tokens = 2 * args.kernel_rounds + args.timeline + 8
     geo = RegionGeometry(sink=4, near=4096, window=128, page=page,
                          max_new_tokens=new_tokens)
     pages = (ctx + new_tokens + page - 1) // page
@@ -1038,6 +1038,10 @@ def mla_layer_bench(torch, args, device):
           file=sys.stderr, flush=True)
     kt = _time_graphs(torch, sel_all, att_all, layers, args.kernel_rounds, plan, cache,
                       req_ids)
+    if args.timeline:
+        selector_timeline(torch, SimpleNamespace(cache=cache, q=q, req_ids=req_ids,
+                                                 attn=attn, kn=keys, vn=vals),
+                          args.timeline, plan)
     nbytes = mla_algorithmic_bytes(mode, kt['lengths'])
     arena = cache.layers[0].kv_pool_k.numel() * 2 + (
         0 if latent else cache.layers[0].kv_pool_v.numel() * 2)

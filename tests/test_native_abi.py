@@ -111,3 +111,17 @@ def test_partial_combine_and_quant_checks_reject_before_launch(lib):
     p.l2_quant, p.fine_dsub, p.kv_heads_mem = 0, 32, 4
     assert lib.nfa_select_layer(ctypes.byref(p), None) == -1
     assert b'kv_heads_mem' in lib.nfa_last_error()
+    # the fused decode write puts one element of the row on each of the
+    # workgroup's 1024 threads: wider rows are refused
+    w = _native.NfaSelectParams()
+    w.abi_version, w.struct_size = _native.ABI_VERSION, ctypes.sizeof(w)
+    w.batch, w.hq, w.hkv, w.head_dim, w.head_dim_v = 1, 1, 1, 1100, 1024
+    w.dsub, w.fine_dsub, w.bs, w.page, w.max_blocks = 32, 32, 16, 16, 512
+    w.k_f, w.k_n, w.k2, w.pool_pages, w.max_vis, w.max_req = 96, 32, 1024, 10, 1024, 1
+    for name in ('q', 'k_pool_l', 'v_pool_l', 'block_table_l', 'lengths', 'active_req',
+                 'valid_req', 'slots', 'k_new', 'v_new', 'stat_min_l', 'stat_max_l',
+                 'stat_sum_l', 'stats_len_l', 'skip_far_l', 'skip_near_l', 'gather',
+                 'vis_lens', 'dims', 'fine_dims'):
+        setattr(w, name, 16)  # never dereferenced: rejected first
+    assert lib.nfa_select_layer(ctypes.byref(w), None) == -1
+    assert b'fused decode write' in lib.nfa_last_error()

@@ -101,10 +101,11 @@ struct SelDims {
 
 __host__ __device__ inline int align16(int x) { return (x + 15) & ~15; }
 
-// bf16 statistics over 32 L1 dims are staged in LDS by asynchronous
-// global-to-LDS loads; other geometries are read from memory while scoring
+// bf16 statistics over 32 or 64 L1 dims are staged in LDS by asynchronous
+// global-to-LDS loads (32 dims double-buffered over the passes of a tile);
+// other geometries are read from memory while scoring
 __host__ __device__ inline bool stats_staged(const NfaSelectParams &p) {
-  return p.dsub == 32 && p.kv_dtype == NFA_DTYPE_BF16;
+  return (p.dsub == 32 || p.dsub == 64) && p.kv_dtype == NFA_DTYPE_BF16;
 }
 
 struct TileSplit {
@@ -167,9 +168,9 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   s.a_stage = o; o += align16(4 * SB * kStatTokens);
   s.a_hs = s.a_stage;  // per-head page scores, after the statistics phase
   s.a_st = o;          // bf16 32-dim statistics of the tile, staged
-  if (stats_staged(p)) o += 2 * (32 / 8) * kSpanMax * 16;
+  if (stats_staged(p)) o += 2 * (p.dsub / 8) * kSpanMax * 16;
   s.a_st2 = o;         // the next pass's, staged while this one is scored
-  if (stats_staged(p) && s.multi) o += 2 * (32 / 8) * kSpanMax * 16;
+  if (stats_staged(p) && s.multi && p.dsub == 32) o += 2 * (32 / 8) * kSpanMax * 16;
   s.a_tkeys = o; if (s.multi) o += align16(2 * kTileMax);
   const int a_tile = o;
   o = a_base;
@@ -797,12 +798,13 @@ __device__ __forceinline__ void lds_dma4(const void *src, uint32_t lds) {
 // both pools are not copied.  Complete at the issuing wave's next vmcnt(0)
 // wait (see lds_dma16).
 // Waves w0, w0 + 1, ... (nw of them) issue the copies.
+template <int DSUB>
 __device__ __forceinline__ void stage_stats_async(const NfaSelectParams &p,
                                                   const RowGeo &g, int64_t req,
                                                   int kv, int t0, int t1,
                                                   unsigned char *s_st, int w0 = 0,
                                                   int nw = SW) {
-  constexpr int NC = 32 / 8;
+  constexpr int NC = DSUB / 8;
   const bool far_mm = p.far_method == NFA_METHOD_MINMAX;
   const bool near_mm = p.near_method == NFA_METHOD_MINMAX;
   // the statistic bases held in scalar registers: the per-lane choice of
@@ -824,7 +826,7 @@ __device__ __forceinline__ void stage_stats_async(const NfaSelectParams &p,
     if (t < t1) pools(p, g, t, &fp, &np);
     const bool mm = (fp && far_mm) || (np && near_mm);
     const bool avg = (fp && !far_mm) || (np && !near_mm);
-    const int64_t base = stat_index<uint16_t>(p, req, kv, c * 8, t, 32);
+    const int64_t base = stat_index<uint16_t>(p, req, kv, c * 8, t, DSUB);
     const uint32_t row0 = lds0 + (uint32_t)(c * kSpanMax + blk * 64) * 16;
     if (mm || avg) lds_dma16((mm ? smin : ssum) + base, row0);
     if (mm) lds_dma16(smax + base, row0 + NC * kSpanMax * 16);
@@ -847,20 +849,21 @@ static_assert(GMAX * kSpanMax * 4 <= 4 * SB * kStatTokens,
 // the query qf (and, with qu, the same mean against the unrounded query into
 // *un); every sum sequential in ascending d, each exact product added with
 // one rounding (a fused multiply-add per term).
+template <int DSUB>
 __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs,
                                                 const float *qf, const float *qu,
                                                 bool need_mm, float *un) {
-  constexpr int NC = 32 / 8;
+  constexpr int NC = DSUB / 8;
   float r, su = 0.0f;
   if (need_mm) {
     float sn = 0.0f, sp = 0.0f;
-#pragma unroll
+#pragma unroll (NC > 4 ? 2 : NC)
     for (int c = 0; c < NC; ++c) {
       float lo[8], hi[8], ln[8], hp[8];
       unpack_chunk<uint16_t>(st[c * kSpanMax], lo);
       unpack_chunk<uint16_t>(st[(NC + c) * kSpanMax], hi);
       load_f8(qs + c * 8, ln);
-      load_f8(qs + 32 + c * 8, hp);
+      load_f8(qs + DSUB + c * 8, hp);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         sn = __builtin_fmaf(lo[e], ln[e], sn);
@@ -870,7 +873,7 @@ __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs
     r = sn + sp;
   } else {
     float sa = 0.0f;
-#pragma unroll
+#pragma unroll (NC > 4 ? 2 : NC)
     for (int c = 0; c < NC; ++c) {
       float k[8], q[8];
       unpack_chunk<uint16_t>(st[c * kSpanMax], k);
@@ -894,10 +897,10 @@ __device__ __forceinline__ float l1_head_staged(const uint4 *st, const float *qs
 // l1_head_staged, for one page per lane.  qs / qf are the first head's rows
 // (strides QS / QF floats); every lane reads the same query address, so
 // those reads are LDS broadcasts.
-template <int QF, int QS>
+template <int QF, int QS, int DSUB>
 __device__ __forceinline__ float l1_group_staged(const uint4 *st, const float *qs,
                                                  const float *qf, int G, bool need_mm) {
-  constexpr int NC = 32 / 8;
+  constexpr int NC = DSUB / 8;
   float acc = 0.0f;
   // heads in pairs: four (minmax) or two (avg) independent sums in flight,
   // a chunk of statistics unpacked per pair (few registers live)
@@ -908,15 +911,15 @@ __device__ __forceinline__ float l1_group_staged(const uint4 *st, const float *q
       const float *q0 = qs + j * QS;
       const float *q1 = two ? q0 + QS : q0;
       float sn0 = 0.0f, sp0 = 0.0f, sn1 = 0.0f, sp1 = 0.0f;
-#pragma unroll
+#pragma unroll (NC > 4 ? 2 : NC)
       for (int c = 0; c < NC; ++c) {
         float lo[8], hi[8], n0[8], p0[8], n1[8], p1[8];
         unpack_chunk<uint16_t>(st[c * kSpanMax], lo);
         unpack_chunk<uint16_t>(st[(NC + c) * kSpanMax], hi);
         load_f8(q0 + c * 8, n0);
-        load_f8(q0 + 32 + c * 8, p0);
+        load_f8(q0 + DSUB + c * 8, p0);
         load_f8(q1 + c * 8, n1);
-        load_f8(q1 + 32 + c * 8, p1);
+        load_f8(q1 + DSUB + c * 8, p1);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           sn0 = __builtin_fmaf(lo[e], n0[e], sn0);
@@ -935,7 +938,7 @@ __device__ __forceinline__ float l1_group_staged(const uint4 *st, const float *q
       const float *q0 = qf + j * QF;
       const float *q1 = two ? q0 + QF : q0;
       float sa0 = 0.0f, sa1 = 0.0f;
-#pragma unroll
+#pragma unroll (NC > 4 ? 2 : NC)
       for (int c = 0; c < NC; ++c) {
         float k[8], v0[8], v1[8];
         unpack_chunk<uint16_t>(st[c * kSpanMax], k);
@@ -1427,7 +1430,8 @@ __global__ void __launch_bounds__(SB)
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int CH = Elem<KV>::kChunk;
   constexpr int NC = DSUB / CH;
-  constexpr bool STG = DSUB == 32 && sizeof(KV) == 2;  // stats staged in LDS
+  constexpr bool STG = (DSUB == 32 || DSUB == 64) && sizeof(KV) == 2;  // stats staged in LDS
+  constexpr bool STG2 = STG && DSUB == 32;  // double-buffered over a tile's passes
   int *s_hist = (int *)(smem + sd.a_hist);  // far hi | near hi | far lo | near lo
   int *s_tmp = (int *)(smem + sd.a_tmp);
   int *s_misc = (int *)(smem + sd.a_misc);
@@ -1590,7 +1594,8 @@ __global__ void __launch_bounds__(SB)
   // the tile's first statistics, staged by asynchronous copies into LDS
   unsigned char *s_st = smem + sd.a_st;
   if constexpr (STG)
-    stage_stats_async(p, ctx_geo(s_ctx, L, true, true), req, kv, t0, pass_end(t0, t1), s_st);
+    stage_stats_async<DSUB>(p, ctx_geo(s_ctx, L, true, true), req, kv, t0, pass_end(t0, t1),
+                            s_st);
 
   // scaled, bf16-rounded query rows of this kv group (selector:943-963), and
   // their negative and positive parts
@@ -1677,12 +1682,14 @@ __global__ void __launch_bounds__(SB)
   // arithmetic is uniform, and run by every wave it would cost each SIMD
   // four times its scalar issue slots.  With one lane per page the scores
   // of a pass take the first four or five waves, so the owner's elements go
-  // to waves 8 and up, otherwise idle; owner lane o = tid - 64 * kOwnerWave)
-  constexpr int kOwnerWave = STG && !TOP2 ? 8 : 0;
-  const int otid = tid - 64 * kOwnerWave;
-  const bool owner_any =
-      (dw || owner_late || side_late) && wave_id() >= kOwnerWave &&
-      (wave_id() - kOwnerWave) * 64 < imax(imax(p.head_dim, p.head_dim_v), imax(DSUB, p.fine_dsub));
+  // to the last waves, otherwise idle; owner lane o = tid - 64 * own_w0;
+  // the widest row written (a 576-dim latent row takes nine waves) decides
+  // how many: the last ones)
+  const int own_elems = imax(imax(p.head_dim, p.head_dim_v), imax(DSUB, p.fine_dsub));
+  const int own_w0 = STG && !TOP2 ? imax(SW - (own_elems + 63) / 64, 0) : 0;
+  const int otid = tid - 64 * own_w0;
+  const bool owner_any = (dw || owner_late || side_late) && wave_id() >= own_w0 &&
+                         (wave_id() - own_w0) * 64 < own_elems;
   KV dw_k = 0, dw_v = 0, side_raw = 0;
   float ap_mn = __uint_as_float(0x7F800000u);  // a new page starts from +inf,
   float ap_mx = __uint_as_float(0xFF800000u);  // -inf and 0
@@ -1832,8 +1839,14 @@ __global__ void __launch_bounds__(SB)
         // the rebuild
         int t0r = c0;
         asm volatile("" : "+s"(t0r));
-        stage_stats_async(p, geo, req, kv, t0r, c1, st);
+        stage_stats_async<DSUB>(p, geo, req, kv, t0r, c1, st);
       }
+    }
+    if constexpr (STG && MULTI && !STG2) {
+      // one buffer: a later pass stages its own statistics now (the pass
+      // before has finished reading them)
+      if (!kFirst && !(do_stats && !incremental))
+        stage_stats_async<DSUB>(p, geo, req, kv, c0, c1, st);
     }
     if constexpr (STG) {
       __builtin_amdgcn_s_waitcnt(0);  // this wave's staged statistics
@@ -1842,12 +1855,12 @@ __global__ void __launch_bounds__(SB)
     lds_barrier();
     NFA_MARK(0, 3);
     if (kFirst && owner_any) owner_prefetch();
-    if constexpr (STG && MULTI) {
+    if constexpr (STG2 && MULTI) {
       // every wave has finished the previous pass, which read nst; with one
       // lane per page the copies come from waves 8-15, which score nothing
       constexpr int w0 = TOP2 ? 0 : 8;
       if (n0 < n1 && !(do_stats && !incremental))
-        stage_stats_async(p, geo, req, kv, n0, n1, nst, w0, SW - w0);
+        stage_stats_async<DSUB>(p, geo, req, kv, n0, n1, nst, w0, SW - w0);
     }
 
     // ---- L1 scores, group means, keys and high-byte histograms -----------
@@ -1872,6 +1885,8 @@ __global__ void __launch_bounds__(SB)
       if (nk) atomicAdd(&s_hist[256 + (nk >> 8)], 1);
     };
     if constexpr (STG && !TOP2) {
+      const bool g_pow2 = (G & (G - 1)) == 0;
+      const float g_inv = 1.0f / (float)G;
       // One lane per page, 64 pages per wave and round: the lane reads and
       // unpacks its page's statistics once and scores the G heads in order
       // against query rows read as LDS broadcasts, so a page costs one
@@ -1886,9 +1901,12 @@ __global__ void __launch_bounds__(SB)
         if (fp || np) {
           const bool need_mm = (fp && far_mm) || (np && near_mm);
           const uint4 *su = reinterpret_cast<const uint4 *>(st) + lp;
-          const float acc = l1_group_staged<QF, QS>(su, s_qs, s_qf, G, need_mm);
-          // bf16 head scores summed in head order, then the group mean
-          const uint16_t mean = bf16_bits(acc / (float)G);
+          const float acc = l1_group_staged<QF, QS, DSUB>(su, s_qs, s_qf, G, need_mm);
+          // bf16 head scores summed in head order, then the group mean (a
+          // power-of-two group: the multiply by 1 / G is the same correctly
+          // rounded quotient)
+          const float m = g_pow2 ? acc * g_inv : acc / (float)G;
+          const uint16_t mean = bf16_bits(m);
           if (fp) far_bits = mean;
           if (np) near_bits = mean;
         }
@@ -1917,7 +1935,7 @@ __global__ void __launch_bounds__(SB)
         float h, u = 0.0f;
         if constexpr (STG) {
           const uint4 *su = reinterpret_cast<const uint4 *>(st) + lp;
-          h = l1_head_staged(su, s_qs + j * QS, s_qf + j * QF, qu, need_mm, &u);
+          h = l1_head_staged<DSUB>(su, s_qs + j * QS, s_qf + j * QF, qu, need_mm, &u);
         } else {
           const bool from_lds = incremental && t == last_blk;
           float m = 0.0f, a = 0.0f;
@@ -1959,7 +1977,7 @@ __global__ void __launch_bounds__(SB)
   };
   {
     unsigned char *st = s_st;
-    unsigned char *nst = smem + sd.a_st2;
+    unsigned char *nst = STG2 ? smem + sd.a_st2 : s_st;
     int c1 = pass_end(t0, t1);
     run_pass(std::true_type{}, t0, c1, st, c1, c1 < t1 ? pass_end(c1, t1) : c1, nst);
     if constexpr (MULTI) {
@@ -2976,6 +2994,12 @@ static int select_check(const NfaSelectParams *p, bool need_workspace) {
   if ((p->hq / p->hkv) * p->head_dim > nfa::kQRawPerThread * nfa::SB) {
     nfa_set_error("nfa_select_layer: query group of %d x %d elements is too wide",
                   p->hq / p->hkv, p->head_dim);
+    return NFA_EINVAL;
+  }
+  if (p->k_new != nullptr && (p->head_dim > nfa::SB || p->head_dim_v > nfa::SB)) {
+    // one element per thread of the workgroup in the fused decode write
+    nfa_set_error("nfa_select_layer: the fused decode write takes rows of at most %d "
+                  "elements (K %d, V %d)", nfa::SB, p->head_dim, p->head_dim_v);
     return NFA_EINVAL;
   }
   if (sd.ntiles > 65535) {
