@@ -97,6 +97,13 @@ def parse():
                     help='only copy a MIB-MiB device buffer three times (the '
                          'known-size kernel that scales rocprofv3 FETCH_SIZE '
                          'and WRITE_SIZE readings) and exit')
+    ap.add_argument('--gather-calibration', type=int, default=0, metavar='MIB',
+                    help='only gather a quarter of a MIB-MiB device buffer in '
+                         'random order, three times as 1 KiB rows and three '
+                         'times as 64-byte rows (the access sizes of the '
+                         'selector\'s staged statistics and of one L2 side '
+                         'row), and exit: FETCH_SIZE per known byte on '
+                         'scattered reads')
     return ap.parse_args()
 
 
@@ -1220,7 +1227,8 @@ def main():
     single = args.batch == 1 and not args.ragged
     cpu = None
     if not args.no_cpu_baseline and single and not args.e2e_only \
-            and args.copy_calibration == 0 and not args.mla:
+            and args.copy_calibration == 0 and args.gather_calibration == 0 \
+            and not args.mla:
         # before torch or HIP start: the baseline forks worker processes
         print('# cpu baseline ...', file=sys.stderr, flush=True)
         cpu = cpu_baseline(seed=args.seed)
@@ -1241,6 +1249,26 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({'copy_bytes_read': n, 'copy_bytes_written': n,
                           'launches': 3}), flush=True)
+        return
+    if args.gather_calibration > 0:
+        n = args.gather_calibration << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=device)
+        gen = torch.Generator(device=device).manual_seed(args.seed)
+        out = {}
+        for name, row_bytes in (('gather_1k', 1024), ('gather_64b', 64)):
+            rows = src.view(-1, row_bytes // 4)
+            idx = torch.randperm(rows.shape[0], generator=gen, device=device)[
+                :rows.shape[0] // 4].contiguous()
+            torch.cuda.synchronize()
+            for _ in range(3):
+                got = rows.index_select(0, idx)
+            torch.cuda.synchronize()
+            out[name] = {'rows': int(idx.numel()), 'row_bytes': row_bytes,
+                         'bytes_read': int(idx.numel()) * row_bytes,
+                         'bytes_written': int(got.numel()) * 4,
+                         'index_bytes': int(idx.numel()) * 8, 'launches': 3}
+            del got, idx
+        print(json.dumps(out), flush=True)
         return
     if args.mla:
         mla_layer_bench(torch, args, device)

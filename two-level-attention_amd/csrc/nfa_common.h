@@ -66,6 +66,16 @@ __device__ __forceinline__ float bf16r(float x) { return bf16_val(bf16_bits(x));
 // -- in two instructions; a NaN input gives a NaN of another payload.
 __device__ __forceinline__ float bf16r_hw(float x) { return (float)(__bf16)x; }
 
+// Two roundings in one conversion (the same round-to-nearest-even per value).
+typedef __bf16 nfa_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float nfa_f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void bf16r_hw2(float a, float b, float &ra, float &rb) {
+  const nfa_f32x2 v = {a, b};
+  const nfa_bf16x2 h = __builtin_convertvector(v, nfa_bf16x2);
+  ra = (float)h.x;
+  rb = (float)h.y;
+}
+
 // Order-preserving 16-bit key of bf16 bits: +0 > -0, +NaN highest.
 __device__ __forceinline__ uint32_t ord16u(uint32_t b) {
   return (b & 0x8000u) ? ((~b) & 0xFFFFu) : (b | 0x8000u);

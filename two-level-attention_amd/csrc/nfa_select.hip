@@ -2664,14 +2664,25 @@ __global__ void __launch_bounds__(SB)
       };
       // 32 dims of dequantised keys from one 16-byte run of codes, dotted
       // with the grouped query from dim d0 on, in dim order
+      // (two dims per conversion; a code's byte from the nibbles spread
+      // into bytes, even and odd nibbles apart)
       auto dot32 = [&](const uint4 &cw, float sc, float zr, int d0, float acc) {
         const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
 #pragma unroll
-        for (int d = 0; d < 32; ++d) {
-          const float c = (float)((w4[d / 8] >> (4 * (d % 8))) & 15u);
-          // a NaN here (non-finite keys) still ends as a NaN logit
-          const float dq = bf16r_hw(bf16r_hw(c * sc) - zr);
-          acc = __builtin_fmaf(dq, s_qg[d0 + d], acc);
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t ev = w4[k] & 0x0F0F0F0Fu;         // dims 0, 2, 4, 6
+          const uint32_t od = (w4[k] >> 4) & 0x0F0F0F0Fu;  // dims 1, 3, 5, 7
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float c0 = (float)((ev >> (8 * j)) & 0xFFu);
+            const float c1 = (float)((od >> (8 * j)) & 0xFFu);
+            float a, b;
+            bf16r_hw2(c0 * sc, c1 * sc, a, b);
+            // a NaN here (non-finite keys) still ends as a NaN logit
+            bf16r_hw2(a - zr, b - zr, a, b);
+            acc = __builtin_fmaf(a, s_qg[d0 + 8 * k + 2 * j], acc);
+            acc = __builtin_fmaf(b, s_qg[d0 + 8 * k + 2 * j + 1], acc);
+          }
         }
         return acc;
       };
