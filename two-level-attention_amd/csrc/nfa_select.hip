@@ -819,8 +819,8 @@ __device__ __forceinline__ void stage_stats_async(const NfaSelectParams &p,
   // units (chunk, 64-page block), both slots per unit
   if (wave_id() < w0) return;
   for (int u = wave_id() - w0; u < NC * nblk; u += nw) {
-    const int c = u / nblk;
-    const int blk = u % nblk;
+    const int c = u % NC;   // NC a power of two: no division
+    const int blk = u / NC;
     const int t = t0 + blk * 64 + lane_id();
     bool fp = false, np = false;
     if (t < t1) pools(p, g, t, &fp, &np);
@@ -902,56 +902,42 @@ __device__ __forceinline__ float l1_group_staged(const uint4 *st, const float *q
                                                  const float *qf, int G, bool need_mm) {
   constexpr int NC = DSUB / 8;
   float acc = 0.0f;
-  // heads in pairs: four (minmax) or two (avg) independent sums in flight,
-  // a chunk of statistics unpacked per pair (few registers live)
+  // one head at a time, a chunk of statistics unpacked per head (few
+  // registers live: the kernel sits at its register budget)
   if (need_mm) {
 #pragma unroll 1
-    for (int j = 0; j < G; j += 2) {
-      const bool two = j + 1 < G;  // uniform
+    for (int j = 0; j < G; ++j) {
       const float *q0 = qs + j * QS;
-      const float *q1 = two ? q0 + QS : q0;
-      float sn0 = 0.0f, sp0 = 0.0f, sn1 = 0.0f, sp1 = 0.0f;
+      float sn = 0.0f, sp = 0.0f;
 #pragma unroll (NC > 4 ? 2 : NC)
       for (int c = 0; c < NC; ++c) {
-        float lo[8], hi[8], n0[8], p0[8], n1[8], p1[8];
+        float lo[8], hi[8], n0[8], p0[8];
         unpack_chunk<uint16_t>(st[c * kSpanMax], lo);
         unpack_chunk<uint16_t>(st[(NC + c) * kSpanMax], hi);
         load_f8(q0 + c * 8, n0);
         load_f8(q0 + DSUB + c * 8, p0);
-        load_f8(q1 + c * 8, n1);
-        load_f8(q1 + DSUB + c * 8, p1);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          sn0 = __builtin_fmaf(lo[e], n0[e], sn0);
-          sp0 = __builtin_fmaf(hi[e], p0[e], sp0);
-          sn1 = __builtin_fmaf(lo[e], n1[e], sn1);
-          sp1 = __builtin_fmaf(hi[e], p1[e], sp1);
+          sn = __builtin_fmaf(lo[e], n0[e], sn);
+          sp = __builtin_fmaf(hi[e], p0[e], sp);
         }
       }
-      acc = acc + bf16r(sn0 + sp0);
-      if (two) acc = acc + bf16r(sn1 + sp1);
+      acc = acc + bf16r(sn + sp);
     }
   } else {
 #pragma unroll 1
-    for (int j = 0; j < G; j += 2) {
-      const bool two = j + 1 < G;
+    for (int j = 0; j < G; ++j) {
       const float *q0 = qf + j * QF;
-      const float *q1 = two ? q0 + QF : q0;
-      float sa0 = 0.0f, sa1 = 0.0f;
+      float sa = 0.0f;
 #pragma unroll (NC > 4 ? 2 : NC)
       for (int c = 0; c < NC; ++c) {
-        float k[8], v0[8], v1[8];
+        float k[8], v0[8];
         unpack_chunk<uint16_t>(st[c * kSpanMax], k);
         load_f8(q0 + c * 8, v0);
-        load_f8(q1 + c * 8, v1);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          sa0 = __builtin_fmaf(k[e], v0[e], sa0);
-          sa1 = __builtin_fmaf(k[e], v1[e], sa1);
-        }
+        for (int e = 0; e < 8; ++e) sa = __builtin_fmaf(k[e], v0[e], sa);
       }
-      acc = acc + bf16r(sa0);
-      if (two) acc = acc + bf16r(sa1);
+      acc = acc + bf16r(sa);
     }
   }
   return acc;
