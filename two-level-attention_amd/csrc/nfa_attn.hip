@@ -64,7 +64,7 @@ __host__ __device__ inline AttnDims attn_dims(const NfaAttnParams &p, int cus,
   if (a.nsplit < 1) a.nsplit = 1;
   a.part_stride = G * (p.head_dim_v + 2);
   int64_t w = 0;
-  a.w_cnt = w;  w += ((int64_t)4 * a.rows + 255) & ~(int64_t)255;
+  a.w_cnt = w;  w += ((int64_t)4 * kArriveStride * a.rows + 255) & ~(int64_t)255;
   a.w_part = w; w += (int64_t)4 * a.rows * a.nsplit * a.part_stride;
   a.w_total = w;
   return a;
@@ -426,7 +426,7 @@ __global__ void __launch_bounds__(NFA_BLOCK)
 
   // arrival; the last split of the (row, kv) merges (the partials went out
   // through coherent stores: no L2 writeback)
-  if (!arrive_last(&cnt[vrow], (unsigned int)ad.nsplit, &s_last, false)) return;
+  if (!arrive_last(&cnt[vrow * kArriveStride], (unsigned int)ad.nsplit, &s_last, false)) return;
 
   const float *base = (const float *)(ws + ad.w_part) +
                       (int64_t)vrow * ad.nsplit * ad.part_stride;

@@ -200,7 +200,7 @@ __host__ __device__ inline void sel_layout(const NfaSelectParams &p, SelDims &s)
   // workspace
   const int rows = p.batch * p.hkv;
   int64_t w = 0;
-  s.w_rowcnt = w; w += ((int64_t)4 * rows + 255) & ~(int64_t)255;
+  s.w_rowcnt = w; w += ((int64_t)4 * kArriveStride * rows + 255) & ~(int64_t)255;
   s.w_reqcnt = w; w += ((int64_t)4 * p.batch + 255) & ~(int64_t)255;
   s.w_hist = w;   w += (int64_t)4 * rows * 512;
   s.w_keys = w;   w += (((int64_t)2 * rows * s.kstride) + 255) & ~(int64_t)255;
@@ -2057,7 +2057,7 @@ __global__ void __launch_bounds__(SB)
   // stores and the histogram through atomics; only a rebuild's side rows
   // and statistics are plain stores that need the L2 writeback.
   NFA_MARK(32, 27);
-  if (!arrive_last(&row_cnt[row], (unsigned int)split.tiles, &s_misc[0],
+  if (!arrive_last(&row_cnt[row * kArriveStride], (unsigned int)split.tiles, &s_misc[0],
                    do_stats && !incremental))
     return;
 
@@ -3177,7 +3177,7 @@ extern "C" int32_t nfa_select_layer(const NfaSelectParams *p, void *stream) {
 // The kernel leaves the counters and histograms at zero when it ends, so
 // they are cleared once per device, at the first call.
 constexpr int64_t kScratchRowCnt = 0;
-constexpr int64_t kScratchReqCnt = 4 * NFA_SELECT_SCRATCH_ROWS;
+constexpr int64_t kScratchReqCnt = (int64_t)4 * nfa::kArriveStride * NFA_SELECT_SCRATCH_ROWS;
 constexpr int64_t kScratchHist = kScratchReqCnt + 4 * NFA_SELECT_SCRATCH_ROWS;
 constexpr int64_t kScratchKeys = kScratchHist + (int64_t)4 * 512 * NFA_SELECT_SCRATCH_ROWS;
 static_assert(kScratchKeys % 256 == 0 && kScratchKeys < NFA_SELECT_SCRATCH_BYTES,
