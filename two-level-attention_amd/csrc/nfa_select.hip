@@ -49,10 +49,13 @@ namespace nfa {
 
 constexpr int SB = 1024;         // threads per selector workgroup
 constexpr int SW = SB / 64;      // waves per selector workgroup
-constexpr int TPP = 4;           // lanes per page when scoring groups of 4 heads
-constexpr int TP = SB / TPP;     // pages of a scoring round (and of a pass)
+// Pages of a pass of a multi-pass tile.  Staged scores take one lane per
+// page, and a pass costs the dependent chain of one page's sums whatever its
+// width, so a pass is as wide as two staging buffers of 32-dim statistics
+// fit in LDS beside the rest of the tile (seven waves score it).
+constexpr int TP = 448;
 constexpr int kSpanMin = NFA_SELECT_CLOCK_PAGES;  // pages per tile, at least
-constexpr int kSpanMax = 288;    // pages per pass of a tile (staged in LDS)
+constexpr int kSpanMax = 448;    // pages per pass of a tile (staged in LDS)
 constexpr int kPassMax = 16;     // passes per tile, at most
 static_assert(kSpanMin == 64 && kSpanMax >= TP, "tile geometry");
 // pages per tile, at most: kPassMax - 1 passes of TP pages and a last one of
@@ -1877,7 +1880,7 @@ __global__ void __launch_bounds__(SB)
       // unpacks its page's statistics once and scores the G heads in order
       // against query rows read as LDS broadcasts, so a page costs one
       // unpack, one pool test and one key instead of one per head lane; the
-      // 256 pages of a pass take four waves, one per SIMD.
+      // up to 448 pages of a pass take seven waves.
       for (int base = wave_id() * 64; base < c1 - c0; base += SW * 64) {
         const int lp = base + lane_id();
         const int t = c0 + lp;
