@@ -165,7 +165,7 @@ def test_16_ragged_requests_32k_to_128k():
 
 def test_1m_context_8_kv_heads_page_lists():
     """1M-token context (plus 8192 tokens, so that every near-pool page id
-    passes 16 bits) with the benchmark's 32/8 heads: 32 tiles per row of 8
+    passes 16 bits) with the benchmark's 32/8 heads: 32 tiles per row of 5
     passes each, whose tiles list their own top-K pages for the tail (the
     instance the 1M benchmark times).  The rebuild step is compared with
     every debug output, the next (incremental) step through the production
