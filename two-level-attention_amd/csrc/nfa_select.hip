@@ -1879,13 +1879,20 @@ __global__ void __launch_bounds__(SB)
       // One lane per page, 64 pages per wave and round: the lane reads and
       // unpacks its page's statistics once and scores the G heads in order
       // against query rows read as LDS broadcasts, so a page costs one
-      // unpack, one pool test and one key instead of one per head lane; the
-      // up to 448 pages of a pass take seven waves.
-      for (int base = wave_id() * 64; base < c1 - c0; base += SW * 64) {
-        const int lp = base + lane_id();
-        const int t = c0 + lp;
+      // unpack, one pool test and one key instead of one per head lane.
+      // The 64-page groups never straddle near_start ([c0, ns) grouped from
+      // c0, [ns, c1) from ns), so no wave runs both pools' arithmetic one
+      // after the other; the up to 448 pages of a pass take seven or eight
+      // waves.
+      const int ns = imin(imax(geo.near_start, c0), c1);
+      const int nfg = (ns - c0 + 63) >> 6;
+      const int ngr = nfg + ((c1 - ns + 63) >> 6);
+      for (int gi = wave_id(); gi < ngr; gi += SW) {
+        const int ce = gi < nfg ? ns : c1;
+        const int t = (gi < nfg ? c0 + gi * 64 : ns + (gi - nfg) * 64) + lane_id();
+        const int lp = t - c0;
         bool fp = false, np = false;
-        if (do_stats && t < c1) pools(p, geo, t, &fp, &np);
+        if (do_stats && t < ce) pools(p, geo, t, &fp, &np);
         uint16_t far_bits = kNegInfBits, near_bits = kNegInfBits;
         if (fp || np) {
           const bool need_mm = (fp && far_mm) || (np && near_mm);
@@ -1899,7 +1906,7 @@ __global__ void __launch_bounds__(SB)
           if (fp) far_bits = mean;
           if (np) near_bits = mean;
         }
-        if (t < c1) publish(t, far_bits, near_bits);
+        if (t < ce) publish(t, far_bits, near_bits);
       }
     } else {
     // lpp lanes per page (one per query head of the group, padded to a
