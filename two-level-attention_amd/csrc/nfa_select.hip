@@ -1670,10 +1670,11 @@ __global__ void __launch_bounds__(SB)
   // (only the waves holding a written element take part: the index
   // arithmetic is uniform, and run by every wave it would cost each SIMD
   // four times its scalar issue slots.  With one lane per page the scores
-  // of a pass take the first four or five waves, so the owner's elements go
-  // to the last waves, otherwise idle; owner lane o = tid - 64 * own_w0;
-  // the widest row written (a 576-dim latent row takes nine waves) decides
-  // how many: the last ones)
+  // of a pass take the first four to eight waves (64-page groups of up to
+  // 448 pages), so the owner's elements go to the last waves, which score
+  // nothing; owner lane o = tid - 64 * own_w0; the widest row written
+  // decides how many: the last ones (a 576-dim latent row takes nine, from
+  // wave 7, which also scores the eighth group of a pass that has one)
   const int own_elems = imax(imax(p.head_dim, p.head_dim_v), imax(DSUB, p.fine_dsub));
   const int own_w0 = STG && !TOP2 ? imax(SW - (own_elems + 63) / 64, 0) : 0;
   const int otid = tid - 64 * own_w0;
