@@ -50,9 +50,11 @@ namespace nfa {
 constexpr int SB = 1024;         // threads per selector workgroup
 constexpr int SW = SB / 64;      // waves per selector workgroup
 // Pages of a pass of a multi-pass tile.  Staged scores take one lane per
-// page, and a pass costs the dependent chain of one page's sums whatever its
-// width, so a pass is as wide as two staging buffers of 32-dim statistics
-// fit in LDS beside the rest of the tile (seven waves score it).
+// page, and a pass's time grows far slower than its width (the dependent
+// chain of one page's sums, then the scoring waves that share a SIMD:
+// 2.4 us at 256 pages, 3.2 us at 448), so a pass is as wide as two staging
+// buffers of 32-dim statistics fit in LDS beside the rest of the tile
+// (seven waves score it).
 constexpr int TP = 448;
 constexpr int kSpanMin = NFA_SELECT_CLOCK_PAGES;  // pages per tile, at least
 constexpr int kSpanMax = 448;    // pages per pass of a tile (staged in LDS)
