@@ -322,6 +322,29 @@ def test_fp32_kv_and_query():
     run_and_compare(cache, indexer, req_ids, q, decode, scaling=0.0883883)
 
 
+@pytest.mark.parametrize('far,near', [('avg', 'minmax'), ('minmax', 'minmax'),
+                                      ('avg', 'avg')])
+def test_pool_methods_with_staged_bf16_statistics(far, near):
+    """Each pool's method swapped on bf16 statistics, which are staged in LDS
+    and scored one lane per page in 64-page groups that never hold pages of
+    both pools (at these lengths the near pool's first page lies inside a
+    64-page stretch of its tile), and the 60000-token row's tiles take two
+    passes (32 rows share the launch: 8 tiles per row, at most 448 pages a
+    pass)."""
+    lengths = [60000, 9000, 33000, 700]
+    cache, gen, req_ids = _prod_cache(lengths, hkv=8, hq=32, max_req=4)
+    indexer = make_indexer(far_method=far, near_method=near)
+    cache.new_step(req_ids)
+    cache.plan_common(req_ids)
+    q = bf16_randn((4, 32, 128), gen, DEV)
+    decode = _decode_inputs(cache, 4, gen, torch.bfloat16)
+    plan = {}
+    print(f'# pool methods far {far} / near {near}: selector + oracle', flush=True)
+    run_and_compare(cache, indexer, req_ids, q, decode,
+                    scaling=0.08838834764831845, plan=plan)
+    assert plan['instance'] == 1 and plan['passes'] > 1, plan
+
+
 def test_short_contexts_below_window():
     cache, gen, req_ids = _prod_cache([40, 100, 140, 300])
     indexer = make_indexer()
