@@ -1627,20 +1627,28 @@ __global__ void __launch_bounds__(SB)
   const bool skip_far = __builtin_amdgcn_readfirstlane(skf_v) != 0;
   const bool skip_near = __builtin_amdgcn_readfirstlane(skn_v) != 0;
   if (tid == 0) s_ctx[23] = (skip_far ? 1 : 0) | (skip_near ? 2 : 0);  // for the tail
-  const int32_t ph_last = owns_last && active ? __builtin_amdgcn_readfirstlane(phl_v) : 0;
-  // the decode token's key row is read from k_new for the statistics when
-  // the fused write targets the slot of token L-1
-  const KV *new_row = nullptr;
-  const int last_phys = safe_page(p, ph_last);
-  if (owns_last && active && p.k_new != nullptr) {
-    if (slot_b >= 0 && slot_b / p.page < p.pool_pages &&
-        slot_b == ph_last * p.page + (L - 1) % p.page)
-      new_row = (const KV *)p.k_new + ((int64_t)b * p.kv_heads_mem + kv) * p.head_dim;
-  }
-
   // ---- page statistics: latest page, or the whole tile on a rebuild -----
   const bool do_stats = active && L > 0 && !(skip_far && skip_near);
   const bool incremental = prev > 0 && L == prev + 1;
+  // The decode token's physical page, and its key row, read from k_new for
+  // the statistics when the fused write targets the slot of token L-1.  On
+  // an incremental step with running sums only the owner's loads after the
+  // first staging wait need them, so the block-table load is waited for
+  // there, with the staged statistics, instead of here (the owner tile is
+  // its row's last to arrive; its latest block-table entry is often a cache
+  // miss)
+  int32_t ph_last = 0;
+  int last_phys = 0;
+  const KV *new_row = nullptr;
+  auto resolve_last = [&]() {
+    ph_last = owns_last && active ? __builtin_amdgcn_readfirstlane(phl_v) : 0;
+    last_phys = safe_page(p, ph_last);
+    if (owns_last && active && p.k_new != nullptr && slot_b >= 0 &&
+        slot_b / p.page < p.pool_pages && slot_b == ph_last * p.page + (L - 1) % p.page)
+      new_row = (const KV *)p.k_new + ((int64_t)b * p.kv_heads_mem + kv) * p.head_dim;
+  };
+  const bool last_late = do_stats && incremental && p.page_sum_l != nullptr;
+  if (!last_late) resolve_last();
   const bool page_phys = (p.page % bs) == 0;
   const KV *kpool = (const KV *)p.k_pool_l;
   // The latest page is never in a pool (it lies in the window:
@@ -1719,6 +1727,7 @@ __global__ void __launch_bounds__(SB)
     }
   };
   auto owner_prefetch = [&]() {
+    if (last_late) resolve_last();
     if (dw) {
       const int64_t nb = (int64_t)b * p.kv_heads_mem + kv;
       if (otid < p.head_dim) dw_k = ((const KV *)p.k_new)[nb * p.head_dim + otid];
