@@ -1384,25 +1384,33 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
 // the selector kernel: L1 tiles, then the tail (candidate pages, L2)
 // ---------------------------------------------------------------------------
 
+// A debug output of the parity tests (or the timeline), compiled into the
+// DBG instances only: the production instances carry none of the debug
+// stores, lists and bitmaps, whose code would otherwise sit between the hot
+// blocks (the 128K instance is 77 KB with them, 68 KB without: the
+// instruction cache missed on it in every workgroup; 25.4 -> 23.8 us).
+#define NFA_DBGP(ptr) (DBG ? (ptr) : nullptr)
+
 // Phase timestamp (debug timeline): every wave of the workgroup has reached
 // it (memory accesses in flight stay in flight), then thread 0 keeps the
 // wall clock in LDS slot k of the tile (0) or tail (32) marks; NFA_FLUSH
 // copies them out at the end of the stage, so no global store of the
 // timeline sits inside a measured phase.  Uniform conditions.
-#define NFA_MARK(part, k)                                             \
-  do {                                                                \
-    if (NFA_COLD(p.dbg_clock != nullptr)) {                           \
-      lds_barrier();                                                  \
-      if (threadIdx.x == 0) s_clk[(part) + (k)] = wall_clock64();     \
-    }                                                                 \
+#define NFA_MARK(part, k)                                                 \
+  do {                                                                    \
+    if (NFA_COLD(NFA_DBGP(p.dbg_clock) != nullptr)) {                     \
+      lds_barrier();                                                      \
+      if (threadIdx.x == 0) s_clk[(part) + (k)] = wall_clock64();         \
+    }                                                                     \
   } while (0)
-#define NFA_FLUSH(part, slot_base)                                    \
-  do {                                                                \
-    if (NFA_COLD(p.dbg_clock != nullptr)) {                           \
-      lds_barrier();                                                  \
-      if (threadIdx.x < 32 && s_clk[(part) + threadIdx.x] != 0)       \
-        p.dbg_clock[(slot_base) + threadIdx.x] = s_clk[(part) + threadIdx.x]; \
-    }                                                                 \
+#define NFA_FLUSH(part, slot_base)                                        \
+  do {                                                                    \
+    if (NFA_COLD(NFA_DBGP(p.dbg_clock) != nullptr)) {                     \
+      lds_barrier();                                                      \
+      if (threadIdx.x < 32 && s_clk[(part) + threadIdx.x] != 0)           \
+        NFA_DBGP(p.dbg_clock)[(slot_base) + threadIdx.x] =                \
+            s_clk[(part) + threadIdx.x];                                  \
+    }                                                                     \
   } while (0)
 
 // MODE 1 and 2 (MULTI): tiles may span several passes (the host picks it
@@ -1411,8 +1419,9 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
 // loop is absent.  MODE 2 (SURV) adds the survivor lists of rows longer than
 // kSurvPages (the host picks it when the block table can hold such rows).
 // TOP2: the avg_top2 far method, a separate instance so the extra query
-// rows and head scores cost the default instances no registers.
-template <int DSUB, typename KV, int MODE, bool TOP2>
+// rows and head scores cost the default instances no registers.  DBG: the
+// debug outputs compiled in (the host picks it when any is requested).
+template <int DSUB, typename KV, int MODE, bool TOP2, bool DBG>
 __global__ void __launch_bounds__(SB)
     nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
   constexpr bool MULTI = MODE >= 1;
@@ -1463,7 +1472,7 @@ __global__ void __launch_bounds__(SB)
   const int64_t clk_tile = ((int64_t)row * (sd.clk_tiles + 1) + tile) * 32;
   const int64_t clk_tail = ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32;
   int64_t *s_clk = (int64_t *)(smem + sd.a_clk);
-  if (NFA_COLD(p.dbg_clock != nullptr) && tid < 64) s_clk[tid] = 0;
+  if (NFA_COLD(NFA_DBGP(p.dbg_clock) != nullptr) && tid < 64) s_clk[tid] = 0;
   NFA_MARK(0, 0);
   unsigned char *ws = (unsigned char *)p.workspace;
   unsigned int *row_cnt = (unsigned int *)(ws + sd.w_rowcnt);
@@ -1872,9 +1881,9 @@ __global__ void __launch_bounds__(SB)
     // would be waited for by the next pass's staging wait (vmcnt counts
     // stores), its full write-through latency on every pass.
     auto publish = [&](int t, uint16_t far_bits, uint16_t near_bits) {
-      if (NFA_COLD(p.dbg_far != nullptr)) {
-        p.dbg_far[(int64_t)row * mb + t] = far_bits;
-        p.dbg_near[(int64_t)row * mb + t] = near_bits;
+      if (NFA_COLD(NFA_DBGP(p.dbg_far) != nullptr)) {
+        NFA_DBGP(p.dbg_far)[(int64_t)row * mb + t] = far_bits;
+        NFA_DBGP(p.dbg_near)[(int64_t)row * mb + t] = near_bits;
       }
       const uint32_t fk = score_key(far_bits);
       const uint32_t nk = score_key(near_bits);
@@ -1976,7 +1985,7 @@ __global__ void __launch_bounds__(SB)
     lds_barrier();
     NFA_MARK(0, 5);
     NFA_MARK(0, 6);
-    if (NFA_COLD(p.dbg_clock != nullptr) && tid == 0) {
+    if (NFA_COLD(NFA_DBGP(p.dbg_clock) != nullptr) && tid == 0) {
       // per-pass durations summed over the passes: staging wait, scores, keys
       s_clk[8] += s_clk[3] - s_clk[7];
       s_clk[9] += s_clk[5] - s_clk[3];
@@ -2149,17 +2158,17 @@ __global__ void __launch_bounds__(SB)
   const int64_t clk_tail = ((int64_t)row * (sd.clk_tiles + 1) + sd.clk_tiles) * 32;
   // (its LDS overlaps the tile stage's private part, no longer used)
   uint16_t *s_keys = (uint16_t *)(smem + sd.a_keys);
-  const bool dbg = p.dbg_i_f != nullptr;
+  const bool dbg = NFA_DBGP(p.dbg_i_f) != nullptr;
   uint32_t *s_dbf = (uint32_t *)(smem + sd.a_dbf);
   uint32_t *s_dbn = (uint32_t *)(smem + sd.a_dbn);
   uint64_t *s_dsel = (uint64_t *)(smem + sd.a_dsel);
   NFA_MARK(32, 0);
 
   const L2Bounds lb = l2_bounds(p, L, skip_far, skip_near, p.geo_near);
-  if (NFA_COLD(p.dbg_bounds != nullptr) && kvq == 0 && tid == 0) {
-    p.dbg_bounds[b * 3 + 0] = lb.lower;
-    p.dbg_bounds[b * 3 + 1] = lb.upper;
-    p.dbg_bounds[b * 3 + 2] = lb.quota;
+  if (NFA_COLD(NFA_DBGP(p.dbg_bounds) != nullptr) && kvq == 0 && tid == 0) {
+    NFA_DBGP(p.dbg_bounds)[b * 3 + 0] = lb.lower;
+    NFA_DBGP(p.dbg_bounds)[b * 3 + 1] = lb.upper;
+    NFA_DBGP(p.dbg_bounds)[b * 3 + 2] = lb.quota;
   }
   // candidate tokens lie in [tok_lo, tok_hi) and exist only when quota > 0;
   // below S_cap = max_blocks * bs too (selector:1167-1184): a bypass page
@@ -2511,8 +2520,8 @@ __global__ void __launch_bounds__(SB)
     for (int i = tid; i < np_u; i += SB)
       s_pphys[i] = btr[imin(udiv_p2(s_pages[i] * bs, p.page, sd.page_sh), mb - 1)];
   }
-  if (tid == 0 && p.dbg_cand_count != nullptr)
-    p.dbg_cand_count[row] = imin(np_u * bs, p.dbg_cand_cap);
+  if (tid == 0 && NFA_DBGP(p.dbg_cand_count) != nullptr)
+    NFA_DBGP(p.dbg_cand_count)[row] = imin(np_u * bs, p.dbg_cand_cap);
   NFA_MARK(32, 4);
   // L1 debug outputs: I_F / I_N (selector:1766-1803 order: valid pages by
   // (score desc, page asc), then -inf fillers by ascending page)
@@ -2522,8 +2531,8 @@ __global__ void __launch_bounds__(SB)
       const int nsel = pool == 0 ? tf.nsel : tn.nsel;
       const uint64_t *sel = s_dsel + (pool == 0 ? 0 : p.k_f);
       const uint32_t *bm = pool == 0 ? s_dbf : s_dbn;
-      int32_t *out = (pool == 0 ? p.dbg_i_f + (int64_t)row * p.k_f
-                                : p.dbg_i_n + (int64_t)row * p.k_n);
+      int32_t *out = (pool == 0 ? NFA_DBGP(p.dbg_i_f) + (int64_t)row * p.k_f
+                                : NFA_DBGP(p.dbg_i_n) + (int64_t)row * p.k_n);
       for (int i = tid; i < nsel; i += SB) {
         const uint64_t ki = sel[i];
         const uint32_t vi = (uint32_t)(ki >> 32), ti = (uint32_t)ki;
@@ -2640,19 +2649,19 @@ __global__ void __launch_bounds__(SB)
       return kpool + kv_offset(p, phys, kv, tk % p.page);
     };
     // logit key of dense slot i (and the parity-test record)
-    const bool dbg_cand = NFA_COLD(p.dbg_cand_tok != nullptr);
+    const bool dbg_cand = NFA_COLD(NFA_DBGP(p.dbg_cand_tok) != nullptr);
     auto emit = [&](int i, int tk, bool scored, float acc) {
       uint16_t key = 0;
       if (scored) {
         const uint16_t bits = bf16_bits(acc);
         key = bits == kNanBits ? 0 : (uint16_t)score_key(bits);
         if (NFA_COLD(dbg_cand) && i < p.dbg_cand_cap) {
-          p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = tk;
-          p.dbg_cand_logit[(int64_t)row * p.dbg_cand_cap + i] =
+          NFA_DBGP(p.dbg_cand_tok)[(int64_t)row * p.dbg_cand_cap + i] = tk;
+          NFA_DBGP(p.dbg_cand_logit)[(int64_t)row * p.dbg_cand_cap + i] =
               bits == kNanBits ? kNegInfBits : bits;
         }
       } else if (NFA_COLD(dbg_cand) && i < p.dbg_cand_cap) {
-        p.dbg_cand_tok[(int64_t)row * p.dbg_cand_cap + i] = -1;
+        NFA_DBGP(p.dbg_cand_tok)[(int64_t)row * p.dbg_cand_cap + i] = -1;
       }
       s_dk[i] = key;
       if (hist_fused && key != 0) atomicAdd(&s_hist[key >> 8], 1);
@@ -2833,7 +2842,7 @@ __global__ void __launch_bounds__(SB)
       r_hi[1] = imax(near_low, near_high);
       r_q[1] = near_quota;
     }
-    int64_t *rclk = p.dbg_clock != nullptr ? s_clk + 32 + 16 : nullptr;
+    int64_t *rclk = NFA_DBGP(p.dbg_clock) != nullptr ? s_clk + 32 + 16 : nullptr;
     for (int r = 0; r < nreg; ++r)
       l2_region_dense(dv, masked, r_lo[r], r_hi[r], r_q[r], p.sink_tokens, rl,
                       &s_misc[2], s_hist, s_tmp, rclk, hist_fused);
@@ -2844,10 +2853,10 @@ __global__ void __launch_bounds__(SB)
   if (mcount > p.k2) mcount = p.k2;
   const int *s_mid = rl.mid;
   const int *s_mslot = rl.mslot;
-  if (NFA_COLD(p.dbg_middle != nullptr)) {
+  if (NFA_COLD(NFA_DBGP(p.dbg_middle) != nullptr)) {
     for (int k = tid; k < p.k2; k += SB)
-      p.dbg_middle[(int64_t)row * p.k2 + k] = k < mcount ? s_mid[k] : 0;
-    if (tid == 0) p.dbg_counts[row] = mcount;
+      NFA_DBGP(p.dbg_middle)[(int64_t)row * p.k2 + k] = k < mcount ? s_mid[k] : 0;
+    if (tid == 0) NFA_DBGP(p.dbg_counts)[row] = mcount;
   }
 
   // ---- final union with the protected sink/SWA ids (selector:1337-1437) --
@@ -3105,41 +3114,31 @@ static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
   // survivors
   const int mode = sd.multi ? (sd.surv ? 2 : 1) : 0;
   const bool top2 = p.far_method == NFA_METHOD_AVG_TOP2;
+  const bool dbg = p.dbg_far != nullptr || p.dbg_i_f != nullptr ||
+                   p.dbg_counts != nullptr || p.dbg_bounds != nullptr ||
+                   p.dbg_cand_tok != nullptr || p.dbg_clock != nullptr;
   const dim3 grid(p.hkv, p.batch, sd.ntiles);
-  const void *k[5] = {
-      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, false>),
-      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, true>),
-      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 1, false>),
-      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 1, true>),
-      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 2, false>)};
-  const int i = mode == 2 ? 4 : 2 * mode + (int)top2;
+  // instances in the order (mode, top2) 0/false, 0/true, 1/false, 1/true,
+  // 2/false, without debug outputs then with them
+#define NFA_SEL_K(m, t, d) reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, m, t, d>)
+  const void *k[10] = {NFA_SEL_K(0, false, false), NFA_SEL_K(0, true, false),
+                       NFA_SEL_K(1, false, false), NFA_SEL_K(1, true, false),
+                       NFA_SEL_K(2, false, false), NFA_SEL_K(0, false, true),
+                       NFA_SEL_K(0, true, true),   NFA_SEL_K(1, false, true),
+                       NFA_SEL_K(1, true, true),   NFA_SEL_K(2, false, true)};
+#undef NFA_SEL_K
+  const int i = (mode == 2 ? 4 : 2 * mode + (int)top2) + (dbg ? 5 : 0);
   if (sd.lds > 64 * 1024) {
-    static std::atomic<uint64_t> optin[5];
+    static std::atomic<uint64_t> optin[10];
     const hipError_t e = lds_optin(k[i], optin[i]);
     if (e != hipSuccess) return e;
   }
-  switch (i) {
-    case 0:
-      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 0, false>), grid,
-                         dim3(nfa::SB), sd.lds, stream, p, sd);
-      break;
-    case 1:
-      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 0, true>), grid,
-                         dim3(nfa::SB), sd.lds, stream, p, sd);
-      break;
-    case 2:
-      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 1, false>), grid,
-                         dim3(nfa::SB), sd.lds, stream, p, sd);
-      break;
-    case 3:
-      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 1, true>), grid,
-                         dim3(nfa::SB), sd.lds, stream, p, sd);
-      break;
-    default:
-      hipLaunchKernelGGL((nfa::nfa_select_kernel<DSUB, KV, 2, false>), grid,
-                         dim3(nfa::SB), sd.lds, stream, p, sd);
-      break;
-  }
+  // the kernel's arguments as the launch API takes them
+  NfaSelectParams pa = p;
+  SelDims sa = sd;
+  void *args[] = {&pa, &sa};
+  const hipError_t le = hipLaunchKernel(k[i], grid, dim3(nfa::SB), args, sd.lds, stream);
+  if (le != hipSuccess) return le;
   return hipGetLastError();
 }
 
