@@ -1420,10 +1420,17 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
 // kSurvPages (the host picks it when the block table can hold such rows).
 // TOP2: the avg_top2 far method, a separate instance so the extra query
 // rows and head scores cost the default instances no registers.  DBG: the
-// debug outputs compiled in (the host picks it when any is requested).
-template <int DSUB, typename KV, int MODE, bool TOP2, bool DBG>
+// debug outputs compiled in (the host picks it when any is requested).  Q4:
+// the L2 keys' format fixed per production instance, so the bf16 instances
+// carry none of the 4-bit code and its registers (at 1M the page-list
+// instance spilled two values with both: 45.5 -> 43.3 us without); the
+// debug instances keep the choice at run time.
+template <int DSUB, typename KV, int MODE, bool TOP2, bool DBG, int Q4>
 __global__ void __launch_bounds__(SB)
     nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
+  // 4-bit L2 keys: fixed by the instance (0 bf16 / fp32 keys, 1 packed 4-bit
+  // codes), or read from the call (2)
+  const bool l2_quant = Q4 == 2 ? p.l2_quant != 0 : Q4 == 1;
   constexpr bool MULTI = MODE >= 1;
   constexpr bool SURV = MODE == 2;
   warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
@@ -1728,7 +1735,7 @@ __global__ void __launch_bounds__(SB)
     }
     if (side_late && otid < p.fine_dsub) {
       // the new token's L2 side row (its 4-bit codes: lanes 0-31 of wave 0)
-      if (p.l2_quant) {
+      if (l2_quant) {
         q4_store_lanes(p, req, kv, L - 1, Elem<KV>::load(&side_raw), otid);
       } else {
         store_coherent(&((KV *)p.l2_keys_l)[l2_side_index<KV>(p, req, kv, L - 1, otid)], side_raw);
@@ -1818,7 +1825,7 @@ __global__ void __launch_bounds__(SB)
                                      : safe_page(p, btr[imin(tok / p.page, mb - 1)]);
           return kpool + kv_offset(p, phys, kv, tok % p.page);
         };
-        if (p.l2_quant) {
+        if (l2_quant) {
           // one thread per token: gather, quantise, store
           for (int tok = tlo + tid; tok < thi; tok += SB)
             q4_store<KV>(p, req, kv, tok, src_row(tok), s_fdims);
@@ -2564,7 +2571,7 @@ __global__ void __launch_bounds__(SB)
   // bf16/fp32 side copy in 16-byte runs: this thread's first L2 slot's row is
   // requested now, ahead of the barrier below (the logits loop starts from it)
   const int nchs = p.fine_dsub % CH == 0 ? p.fine_dsub / CH : 0;
-  const bool l2_pre = p.l2_keys_l != nullptr && !p.l2_quant && nchs > 0 && nchs <= 4;
+  const bool l2_pre = p.l2_keys_l != nullptr && !l2_quant && nchs > 0 && nchs <= 4;
   // the side copy of this (request, kv head): page pg's token r starts at
   // side0 + pg * bs * fine_dsub + r * (CH, chunk-major, or fine_dsub)
   const KV *side0 = p.l2_keys_l != nullptr
@@ -2595,7 +2602,7 @@ __global__ void __launch_bounds__(SB)
   int64_t sl_pre = -1;
   uint4 cw_pre = make_uint4(0u, 0u, 0u, 0u), cw2_pre = make_uint4(0u, 0u, 0u, 0u);
   uint32_t pw_pre = 0u;
-  if (p.l2_quant) {
+  if (l2_quant) {
     if (tid < np_u * bs) {
       const int pi = udiv_p2(tid, bs, sd.bs_sh);
       const int tk = s_pages[pi] * bs + (tid - pi * bs);
@@ -2666,7 +2673,7 @@ __global__ void __launch_bounds__(SB)
       s_dk[i] = key;
       if (hist_fused && key != 0) atomicAdd(&s_hist[key >> 8], 1);
     };
-    if (p.l2_quant) {
+    if (l2_quant) {
       // 4-bit side cache: 16 bytes of codes and 4 of (scale, zero) per
       // slot, dequantised in registers as bf16(bf16(code * scale) - zero)
       const unsigned char *qb = (const unsigned char *)p.l2_keys_l;
@@ -3118,18 +3125,21 @@ static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
                    p.dbg_counts != nullptr || p.dbg_bounds != nullptr ||
                    p.dbg_cand_tok != nullptr || p.dbg_clock != nullptr;
   const dim3 grid(p.hkv, p.batch, sd.ntiles);
-  // instances in the order (mode, top2) 0/false, 0/true, 1/false, 1/true,
-  // 2/false, without debug outputs then with them
-#define NFA_SEL_K(m, t, d) reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, m, t, d>)
-  const void *k[10] = {NFA_SEL_K(0, false, false), NFA_SEL_K(0, true, false),
-                       NFA_SEL_K(1, false, false), NFA_SEL_K(1, true, false),
-                       NFA_SEL_K(2, false, false), NFA_SEL_K(0, false, true),
-                       NFA_SEL_K(0, true, true),   NFA_SEL_K(1, false, true),
-                       NFA_SEL_K(1, true, true),   NFA_SEL_K(2, false, true)};
-#undef NFA_SEL_K
-  const int i = (mode == 2 ? 4 : 2 * mode + (int)top2) + (dbg ? 5 : 0);
+  // instances by (mode, top2): 0/false, 0/true, 1/false, 1/true, 2/false;
+  // production ones with bf16 L2 keys, then with 4-bit keys, then the debug
+  // ones (the key format read at run time)
+#define NFA_SEL_K5(d, q)                                                          \
+  reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, false, d, q>), \
+      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, true, d, q>), \
+      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 1, false, d, q>), \
+      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 1, true, d, q>), \
+      reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 2, false, d, q>)
+  const void *k[15] = {NFA_SEL_K5(false, 0), NFA_SEL_K5(false, 1), NFA_SEL_K5(true, 2)};
+#undef NFA_SEL_K5
+  const int i = (mode == 2 ? 4 : 2 * mode + (int)top2) +
+                (dbg ? 10 : p.l2_quant ? 5 : 0);
   if (sd.lds > 64 * 1024) {
-    static std::atomic<uint64_t> optin[10];
+    static std::atomic<uint64_t> optin[15];
     const hipError_t e = lds_optin(k[i], optin[i]);
     if (e != hipSuccess) return e;
   }
