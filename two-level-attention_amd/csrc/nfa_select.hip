@@ -1423,14 +1423,17 @@ __device__ __forceinline__ void l2_region_dense(const DenseView &dv, bool masked
 // debug outputs compiled in (the host picks it when any is requested).  Q4:
 // the L2 keys' format fixed per production instance, so the bf16 instances
 // carry none of the 4-bit code and its registers (at 1M the page-list
-// instance spilled two values with both: 45.5 -> 43.3 us without); the
-// debug instances keep the choice at run time.
+// instance spilled two values with both: 45.5 -> 43.3 us without), and the
+// L2 side copy assumed (16 ragged 51.9 -> 51.3 us); the debug instances, and
+// calls without the side copy, keep both choices at run time.
 template <int DSUB, typename KV, int MODE, bool TOP2, bool DBG, int Q4>
 __global__ void __launch_bounds__(SB)
     nfa_select_kernel(const NfaSelectParams p, const SelDims sd) {
   // 4-bit L2 keys: fixed by the instance (0 bf16 / fp32 keys, 1 packed 4-bit
-  // codes), or read from the call (2)
+  // codes, both read from the L2 side copy), or read from the call (2: the
+  // side copy may be off, the L2 dims then read from the K pool)
   const bool l2_quant = Q4 == 2 ? p.l2_quant != 0 : Q4 == 1;
+  const bool l2_side = Q4 == 2 ? p.l2_keys_l != nullptr : true;
   constexpr bool MULTI = MODE >= 1;
   constexpr bool SURV = MODE == 2;
   warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
@@ -1692,7 +1695,7 @@ __global__ void __launch_bounds__(SB)
   const bool dw = p.k_new != nullptr && active && writer && last_blk >= t0 &&
                   (last_blk < t1 || t1 >= kt_tiles);
   const bool side_late =
-      do_stats && incremental && owns_last && writer && p.l2_keys_l != nullptr;
+      do_stats && incremental && owns_last && writer && l2_side;
   // (only the waves holding a written element take part: the index
   // arithmetic is uniform, and run by every wave it would cost each SIMD
   // four times its scalar issue slots.  With one lane per page the scores
@@ -1814,7 +1817,7 @@ __global__ void __launch_bounds__(SB)
                                 page_phys ? s_tphys : nullptr, new_row, L - 1,
                                 psum_row, last_blk);
       }
-      if (p.l2_keys_l != nullptr) {
+      if (l2_side) {
         // L2 side rows of the tile's tokens
         const int tlo = c0 * bs;
         const int thi = imin(c1 * bs, L);
@@ -2518,7 +2521,7 @@ __global__ void __launch_bounds__(SB)
   // them before the L2 top-quota, so their loads stay in flight through the
   // logits (held in a register, stored to LDS after them)
   int *s_pphys = (int *)(smem + sd.a_pphys);
-  const bool pphys_late = p.l2_keys_l != nullptr && np_u <= SB;
+  const bool pphys_late = l2_side && np_u <= SB;
   int pphys_reg = 0;
   if (pphys_late) {
     if (tid < np_u)
@@ -2571,10 +2574,10 @@ __global__ void __launch_bounds__(SB)
   // bf16/fp32 side copy in 16-byte runs: this thread's first L2 slot's row is
   // requested now, ahead of the barrier below (the logits loop starts from it)
   const int nchs = p.fine_dsub % CH == 0 ? p.fine_dsub / CH : 0;
-  const bool l2_pre = p.l2_keys_l != nullptr && !l2_quant && nchs > 0 && nchs <= 4;
+  const bool l2_pre = l2_side && !l2_quant && nchs > 0 && nchs <= 4;
   // the side copy of this (request, kv head): page pg's token r starts at
   // side0 + pg * bs * fine_dsub + r * (CH, chunk-major, or fine_dsub)
-  const KV *side0 = p.l2_keys_l != nullptr
+  const KV *side0 = l2_side
                         ? (const KV *)p.l2_keys_l + l2_side_index<KV>(p, req, kv, 0, 0)
                         : nullptr;
   int tk_pre = -1;
@@ -2634,7 +2637,7 @@ __global__ void __launch_bounds__(SB)
   {
     const float *s_qg = (const float *)(smem + sd.a_qg);
     // the L2 dims of a slot: its side row (dense, in order) or its K row
-    const bool side = p.l2_keys_l != nullptr;
+    const bool side = l2_side;
     const int nch = side ? (p.fine_dsub % CH == 0 ? p.fine_dsub / CH : 0)
                          : s_misc[5];  // 16-byte runs, 0: element loads
     // side copy: kr = element 0 of the token, chunk c at c * bs * CH (chunk-
@@ -3126,8 +3129,9 @@ static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
                    p.dbg_cand_tok != nullptr || p.dbg_clock != nullptr;
   const dim3 grid(p.hkv, p.batch, sd.ntiles);
   // instances by (mode, top2): 0/false, 0/true, 1/false, 1/true, 2/false;
-  // production ones with bf16 L2 keys, then with 4-bit keys, then the debug
-  // ones (the key format read at run time)
+  // production ones with bf16 L2 keys, then with 4-bit keys (both from the
+  // L2 side copy), then the debug ones (the key format and the side copy read
+  // at run time; they also serve calls without the side copy)
 #define NFA_SEL_K5(d, q)                                                          \
   reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, false, d, q>), \
       reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, true, d, q>), \
@@ -3137,7 +3141,7 @@ static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
   const void *k[15] = {NFA_SEL_K5(false, 0), NFA_SEL_K5(false, 1), NFA_SEL_K5(true, 2)};
 #undef NFA_SEL_K5
   const int i = (mode == 2 ? 4 : 2 * mode + (int)top2) +
-                (dbg ? 10 : p.l2_quant ? 5 : 0);
+                (dbg || p.l2_keys_l == nullptr ? 10 : p.l2_quant ? 5 : 0);
   if (sd.lds > 64 * 1024) {
     static std::atomic<uint64_t> optin[15];
     const hipError_t e = lds_optin(k[i], optin[i]);
