@@ -1434,6 +1434,13 @@ __global__ void __launch_bounds__(SB)
   // side copy may be off, the L2 dims then read from the K pool)
   const bool l2_quant = Q4 == 2 ? p.l2_quant != 0 : Q4 == 1;
   const bool l2_side = Q4 == 2 ? p.l2_keys_l != nullptr : true;
+  // and the production instances (Q4 0, 1) hold only what production calls
+  // take: the fp32 running sums of the latest page present, the row's keys
+  // in one LDS segment, no fixed near-token quota; the host sends any other
+  // call to the instances that read these from the call (Q4 2)
+  const bool has_psum = Q4 == 2 ? p.page_sum_l != nullptr : true;
+  const bool multi_seg = Q4 == 2 ? sd.nseg > 1 : false;
+  const bool near_quota = Q4 == 2 ? p.near_tokens >= 0 : false;
   constexpr bool MULTI = MODE >= 1;
   constexpr bool SURV = MODE == 2;
   warm_kernargs<sizeof(NfaSelectParams) + sizeof(SelDims)>();
@@ -1666,7 +1673,7 @@ __global__ void __launch_bounds__(SB)
         slot_b / p.page < p.pool_pages && slot_b == ph_last * p.page + (L - 1) % p.page)
       new_row = (const KV *)p.k_new + ((int64_t)b * p.kv_heads_mem + kv) * p.head_dim;
   };
-  const bool last_late = do_stats && incremental && p.page_sum_l != nullptr;
+  const bool last_late = do_stats && incremental && has_psum;
   if (!last_late) resolve_last();
   const bool page_phys = (p.page % bs) == 0;
   const KV *kpool = (const KV *)p.k_pool_l;
@@ -1679,8 +1686,8 @@ __global__ void __launch_bounds__(SB)
   // running sums must be continued once, and the rest are the same values)
   const bool writer = kvq < p.kv_heads_mem;
   const bool owner_late =
-      do_stats && incremental && owns_last && writer && p.page_sum_l != nullptr;
-  if (do_stats && incremental && owns_last && writer && NFA_COLD(p.page_sum_l == nullptr)) {
+      do_stats && incremental && owns_last && writer && has_psum;
+  if (do_stats && incremental && owns_last && writer && NFA_COLD(!has_psum)) {
     __syncthreads();  // the query preparation has read the raw rows in s_stage
     stats_latest_page<DSUB, KV>(p, req, kv, L, last_blk, last_phys, s_dims, s_stage,
                                 new_row, s_last);
@@ -1786,7 +1793,7 @@ __global__ void __launch_bounds__(SB)
     NFA_MARK(0, 7);
     if (NFA_COLD(do_stats && !incremental)) {
       __syncthreads();  // the query preparation has read the raw rows in s_stage
-      float *psum_row = p.page_sum_l != nullptr
+      float *psum_row = has_psum
                             ? p.page_sum_l + (req * p.kv_heads_mem + kv) * DSUB
                             : nullptr;
       int *s_coff = (int *)s_stage;  // DSUB / CH chunk offsets
@@ -2250,7 +2257,7 @@ __global__ void __launch_bounds__(SB)
         }
       }
     }
-  } else if (sd.nseg == 1) {
+  } else if (!multi_seg) {
     stage_keys(g_keys, 0, sd.seg, s_keys, 2);
   }
   // coarse threshold bins: wave 0 the far pool, wave 1 the near pool
@@ -2278,7 +2285,7 @@ __global__ void __launch_bounds__(SB)
     // refinement: low-byte histograms of the keys in the threshold bins
     for (int sg = 0; sg < sd.nseg; ++sg) {
       const int seg_base = sg * sd.seg;
-      if (NFA_COLD(sd.nseg > 1)) {
+      if (NFA_COLD(multi_seg)) {
         __syncthreads();
         stage_keys(g_keys, seg_base, sd.seg, s_keys);
         dma_barrier();
@@ -2419,7 +2426,7 @@ __global__ void __launch_bounds__(SB)
   }
   for (int sg = 0; sg < (surv_path ? 0 : sd.nseg); ++sg) {
     const int seg_base = sg * sd.seg;
-    if (NFA_COLD(sd.nseg > 1)) {
+    if (NFA_COLD(multi_seg)) {
       __syncthreads();
       stage_keys(g_keys, seg_base, sd.seg, s_keys);
       dma_barrier();
@@ -2624,7 +2631,7 @@ __global__ void __launch_bounds__(SB)
   }
   // one unmasked L2 region: its high-byte key histogram accumulates while
   // the logits are computed (the L1 histograms are dead here)
-  const bool hist_fused = lb.quota > 0 && p.near_tokens < 0;
+  const bool hist_fused = lb.quota > 0 && !near_quota;
   if (hist_fused && tid < 512) s_hist[tid] = 0;
   __syncthreads();  // the L1 part of the tail LDS is dead from here
   NFA_MARK(32, 6);
@@ -2828,7 +2835,7 @@ __global__ void __launch_bounds__(SB)
     int nreg = 1;
     bool masked = false;
     int r_lo[2] = {lb.lower, 0}, r_hi[2] = {lb.upper, 0}, r_q[2] = {lb.quota, 0};
-    if (NFA_COLD(p.near_tokens >= 0)) {
+    if (NFA_COLD(near_quota)) {
       // far quota first, the remainder goes to near (selector:873-920)
       const L2Bounds fb = l2_bounds(p, L, false, false, p.near_len);
       const int base = imax(imin(L, p.k2) - p.sink_tokens - (L - fb.lo), 0);
@@ -3130,8 +3137,9 @@ static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
   const dim3 grid(p.hkv, p.batch, sd.ntiles);
   // instances by (mode, top2): 0/false, 0/true, 1/false, 1/true, 2/false;
   // production ones with bf16 L2 keys, then with 4-bit keys (both from the
-  // L2 side copy), then the debug ones (the key format and the side copy read
-  // at run time; they also serve calls without the side copy)
+  // L2 side copy), then the debug ones (the key format, the side copy and the
+  // other options read at run time; they also serve production calls that
+  // take one of those options)
 #define NFA_SEL_K5(d, q)                                                          \
   reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, false, d, q>), \
       reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 0, true, d, q>), \
@@ -3140,8 +3148,10 @@ static hipError_t launch_select(const NfaSelectParams &p, const SelDims &sd,
       reinterpret_cast<const void *>(&nfa::nfa_select_kernel<DSUB, KV, 2, false, d, q>)
   const void *k[15] = {NFA_SEL_K5(false, 0), NFA_SEL_K5(false, 1), NFA_SEL_K5(true, 2)};
 #undef NFA_SEL_K5
-  const int i = (mode == 2 ? 4 : 2 * mode + (int)top2) +
-                (dbg || p.l2_keys_l == nullptr ? 10 : p.l2_quant ? 5 : 0);
+  // what only the run-time instances hold
+  const bool rt = dbg || p.l2_keys_l == nullptr || p.page_sum_l == nullptr ||
+                  sd.nseg > 1 || p.near_tokens >= 0;
+  const int i = (mode == 2 ? 4 : 2 * mode + (int)top2) + (rt ? 10 : p.l2_quant ? 5 : 0);
   if (sd.lds > 64 * 1024) {
     static std::atomic<uint64_t> optin[15];
     const hipError_t e = lds_optin(k[i], optin[i]);
